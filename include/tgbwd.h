@@ -1,0 +1,166 @@
+/*
+ * tgbwd.h — C-ABI of libtgbwd.so, the gfx950 backward-pass engine behind the
+ * tensor_gpu_v2 API (DragonShadows1978/Project-Tensor).
+ *
+ * Conventions
+ *  - Every function returns int: 0 on success, negative on error
+ *    (-1 invalid argument, -2 HIP error, -3 unsupported, -4 workspace too small);
+ *    tg_last_error() returns the thread's last message.
+ *  - Pointers are device pointers unless stated; the caller owns every buffer,
+ *    the library keeps no reference after return.
+ *  - `stream` is a hipStream_t (NULL = default stream).  Work is asynchronous
+ *    on that stream; only tg_stream_sync waits.
+ *  - dtype codes: 0 = fp32, 1 = fp16, 2 = bf16.
+ *  - `accumulate` != 0 means out += result (the reference's `grad += local`
+ *    closures); 0 means out = result (out is not read).
+ *  - Tensors are contiguous row-major unless leading dimensions are passed.
+ *
+ * Each entry cites the reference code it replaces (paths are relative to the
+ * reference repository root).
+ */
+#ifndef TGBWD_H
+#define TGBWD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- runtime ---------------------------------------------------------- */
+/* Select `device` and check that it is gfx950.  Replaces the implicit CuPy
+ * device context (tensor_gpu_v2/_core.py:16, :116-125). */
+int tg_init(int device);
+const char* tg_last_error(void);
+int tg_version(void);
+int tg_stream_sync(void* stream);
+
+/* ---- elementwise activations ------------------------------------------ */
+/* dx (+)= dy * gelu'(x), tanh approximation.
+ * Replaces RawKernel gelu_backward(x, grad_out, grad_in, n) and the
+ * `self.grad += grad_in` that follows it (_core.py:493-507, :1185-1190),
+ * and the xp fallback (_core.py:1199-1206). */
+int tg_gelu_bwd(int dtype, const void* x, const void* dy, void* dx, int64_t n, int accumulate,
+                void* stream);
+/* dx (+)= dy * silu'(x).  Replaces silu_backward (_core.py:522-533, :1225-1230)
+ * and the xp path (_core.py:1237-1243). */
+int tg_silu_bwd(int dtype, const void* x, const void* dy, void* dx, int64_t n, int accumulate,
+                void* stream);
+/* Forward kernels feeding the above: gelu_forward (_core.py:479-491),
+ * silu_forward (_core.py:510-520). */
+int tg_gelu_fwd(int dtype, const void* x, void* y, int64_t n, void* stream);
+int tg_silu_fwd(int dtype, const void* x, void* y, int64_t n, void* stream);
+/* y = alpha*x + beta*y (beta == 0: y not read), x/y dtypes may differ.
+ * The generic `parent.grad += g` accumulation of the closures (_core.py:945-966). */
+int tg_axpby(int dtype_x, const void* x, int dtype_y, void* y, int64_t n, float alpha,
+             float beta, void* stream);
+/* Fill with a constant by a kernel (grad zeroing; graph-capture safe). */
+int tg_fill(int dtype, void* y, int64_t n, float value, void* stream);
+
+/* ---- row-wise ----------------------------------------------------------- */
+/* Softmax over the last axis of a [rows, cols] matrix (_core.py:1286-1292). */
+int tg_softmax_fwd(int dtype, const void* x, void* y, int64_t rows, int64_t cols, void* stream);
+/* dx (+)= y * (dy - rowsum(dy*y))  (_core.py:1294-1297). */
+int tg_softmax_bwd(int dtype, const void* y, const void* dy, void* dx, int64_t rows,
+                   int64_t cols, int accumulate, void* stream);
+/* LayerNorm forward over the last axis; saves mean and rstd = 1/sqrt(var+eps)
+ * per row (fp32).  gamma/beta fp32.  (_nn.py:900-919) */
+int tg_layernorm_fwd(int dtype, const void* x, const float* gamma, const float* beta, void* y,
+                     float* mean, float* rstd, int64_t rows, int64_t cols, float eps,
+                     void* stream);
+/* LayerNorm backward (_nn.py:921-942): dx (+)= rstd*(g - mean(g) - xhat*mean(g*xhat)),
+ * g = dy*gamma, xhat = (x-mean)*rstd; dgamma (+)= sum dy*xhat, dbeta (+)= sum dy
+ * (either may be NULL).  Workspace from tg_layernorm_bwd_workspace. */
+size_t tg_layernorm_bwd_workspace(int dtype, int64_t rows, int64_t cols);
+int tg_layernorm_bwd(int dtype, const void* x, const float* mean, const float* rstd,
+                     const float* gamma, const void* dy, void* dx, float* dgamma, float* dbeta,
+                     int64_t rows, int64_t cols, int accumulate_dx, int accumulate_params,
+                     void* workspace, size_t workspace_bytes, void* stream);
+/* out[c] (+)= sum_r in[r][c]: Tensor._unbroadcast's leading-dimension sums
+ * (_core.py:1380-1424), e.g. the Linear bias gradient. */
+size_t tg_reduce_rows_workspace(int64_t rows, int64_t cols);
+int tg_reduce_rows(int dtype_in, const void* in, int dtype_out, void* out, int64_t rows,
+                   int64_t cols, int accumulate, void* workspace, size_t workspace_bytes,
+                   void* stream);
+
+/* ---- batch norm (+ReLU), fp32 ----------------------------------------- */
+/* layout: 0 = NHWC ([N*H*W, C]), 1 = NCHW.  HW = H*W. */
+size_t tg_batchnorm_workspace(int layout, int64_t N, int64_t C, int64_t HW);
+/* Training forward of FusedBatchNormReLU / BatchNorm2D (_nn.py:794-810, :701-714):
+ * batch mean/var (population), rstd, running-stat EMA (either running pointer
+ * may be NULL), y = [relu](gamma*xhat + beta).  var may be NULL. */
+int tg_batchnorm_fwd_train(int layout, const float* x, const float* gamma, const float* beta,
+                           float* y, float* mean, float* rstd, float* var, float* running_mean,
+                           float* running_var, float momentum, int64_t N, int64_t C, int64_t HW,
+                           float eps, int relu, void* workspace, size_t workspace_bytes,
+                           void* stream);
+/* Training backward (_nn.py:812-833; BatchNorm2D _nn.py:720-736 with relu = 0):
+ * dx (+)= gamma*rstd*(dy_m - mean(dy_m) - xhat*mean(dy_m*xhat)), dy_m = dy*[out>0],
+ * dgamma (+)= sum dy_m*xhat, dbeta (+)= sum dy_m (either may be NULL). */
+int tg_batchnorm_bwd(int layout, const float* x, const float* mean, const float* rstd,
+                     const float* gamma, const float* beta, const float* dy, float* dx,
+                     float* dgamma, float* dbeta, int64_t N, int64_t C, int64_t HW, int relu,
+                     int accumulate_dx, int accumulate_params, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
+/* ---- optimizers and gradient hygiene (multi-tensor, host pointer lists) --- */
+/* Adam / AdamW step over `ntensors` fp32 tensors (_nn.py:1413-1442, FusedAdam
+ * fused_adam_step _training.py:2198-2220, launch _training.py:2250-2268):
+ * decoupled decay p -= lr*wd*p first, then the moment updates and
+ * p -= lr*(m/bc1)/(sqrt(v/bc2)+eps).  max_exp_avg_sq != NULL selects AMSGrad
+ * (_nn.py:1436-1438). */
+int tg_adam_step(int ntensors, float* const* params, const float* const* grads,
+                 float* const* exp_avg, float* const* exp_avg_sq, float* const* max_exp_avg_sq,
+                 const int64_t* numel, float lr, float beta1, float beta2, float eps,
+                 float weight_decay, float bias_correction1, float bias_correction2,
+                 void* stream);
+/* GradScaler.unscale_ (_nn.py:1795-1833): g *= mul (if write); flags[i] (device,
+ * cleared first) |= 1 if tensor i had a non-finite value, |= 2 if the scaled
+ * tensor has one. */
+int tg_unscale_check(int ntensors, int dtype, void* const* grads, const int64_t* numel, float mul,
+                     int write, int* flags, void* stream);
+/* clip_grad_norm_ (_nn.py:1563-1626) reduction: out[0] (device double) =
+ * sum g^2 (kind 0), max|g| (kind 1) or sum |g|^p (kind 2) over finite entries;
+ * flags[i] |= 1 when tensor i has non-finite entries. */
+size_t tg_grad_norm_workspace(int ntensors, const int64_t* numel);
+int tg_grad_norm(int ntensors, int dtype, void* const* grads, const int64_t* numel, int norm_kind,
+                 float p, double* out, int* flags, void* workspace, size_t workspace_bytes,
+                 void* stream);
+/* xp.where(isfinite(g), g, 0) per tensor (_nn.py:1596). */
+int tg_zero_nonfinite(int ntensors, int dtype, void* const* grads, const int64_t* numel,
+                      void* stream);
+
+/* ---- dense contractions (MFMA) ------------------------------------------ */
+/* Batched row-major GEMM: C[b] = alpha * op(A[b]) @ op(B[b]) + beta * C[b],
+ * op(A) is [M,K] (trans_a = 0: A[m*lda+k]; 1: A[k*lda+m]), op(B) is [K,N]
+ * (trans_b = 0: B[k*ldb+n]; 1: B[n*ldb+k]); stride 0 broadcasts an operand.
+ * dtype_ab in {fp32, fp16, bf16}; dtype_c is fp32 or dtype_ab.  Serves the
+ * matmul forward and its backward dA = dC @ B^T, dB = A^T @ dC
+ * (_core.py:999-1068). */
+int tg_gemm(int dtype_ab, int dtype_c, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
+            float alpha, const void* A, int64_t lda, int64_t stride_a, const void* B,
+            int64_t ldb, int64_t stride_b, float beta, void* C, int64_t ldc, int64_t stride_c,
+            int64_t batch, void* stream);
+
+/* ---- attention ------------------------------------------------------------ */
+/* FlashAttention forward on contiguous (B,H,S,D) tensors, saving the row
+ * log-sum-exp lse[B,H,Sq] (fp32) for the backward.  causal masks col > row
+ * (_core.py:1686-1786).  dtype fp16 or bf16, D in {64, 128}. */
+int tg_flash_attn_fwd(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
+                      int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D, float scale,
+                      int causal, void* stream);
+/* FlashAttention backward (_core.py:1799-1867): recomputes P from lse,
+ * dV = P^T dO, dP = dO V^T, dS = P*(dP - rowsum(dO*O))*scale, dQ = dS K,
+ * dK = dS^T Q.  Workspace from tg_flash_attn_bwd_workspace. */
+size_t tg_flash_attn_bwd_workspace(int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D);
+int tg_flash_attn_bwd(int dtype, const void* q, const void* k, const void* v, const void* o,
+                      const void* dout, const float* lse, void* dq, void* dk, void* dv, int64_t B,
+                      int64_t H, int64_t Sq, int64_t Sk, int64_t D, float scale, int causal,
+                      int accumulate, void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TGBWD_H */

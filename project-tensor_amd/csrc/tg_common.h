@@ -1,0 +1,138 @@
+// Shared device helpers and host-side error plumbing for libtgbwd (gfx950 only).
+//
+// Every exported entry point returns an int status (TG_OK = 0, negative on error)
+// and records a message retrievable with tg_last_error().  Kernels are launched
+// asynchronously on the caller's stream; the library never synchronises except
+// where an entry point documents a device->host result.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "tgbwd.h"
+
+#define TG_EXPORT extern "C" __attribute__((visibility("default")))
+
+enum tg_status {
+  TG_OK = 0,
+  TG_ERR_INVALID = -1,   // bad argument (shape, pointer, dtype)
+  TG_ERR_HIP = -2,       // HIP runtime / launch error
+  TG_ERR_UNSUPPORTED = -3,
+  TG_ERR_WORKSPACE = -4, // workspace missing or too small
+};
+
+enum tg_dtype { TG_F32 = 0, TG_F16 = 1, TG_BF16 = 2, TG_F64 = 3 };
+
+typedef _Float16 tg_half;
+typedef __bf16 tg_bf16;
+
+// ---- host-side error handling (defined in tg_runtime.hip) ----
+void tg_set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+int tg_check_launch(const char* what);
+
+#define TG_REQUIRE(cond, ...)            \
+  do {                                   \
+    if (!(cond)) {                       \
+      tg_set_error(__VA_ARGS__);         \
+      return TG_ERR_INVALID;             \
+    }                                    \
+  } while (0)
+
+static inline hipStream_t tg_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+static inline bool tg_aligned16(const void* p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+static inline int tg_dtype_size(int dt) {
+  switch (dt) {
+    case TG_F32: return 4;
+    case TG_F16: return 2;
+    case TG_BF16: return 2;
+    case TG_F64: return 8;
+    default: return 0;
+  }
+}
+
+// ---- device helpers ----
+__device__ __forceinline__ float tg_to_float(float v) { return v; }
+__device__ __forceinline__ float tg_to_float(tg_half v) { return (float)v; }
+__device__ __forceinline__ float tg_to_float(tg_bf16 v) { return (float)v; }
+
+template <typename T> __device__ __forceinline__ T tg_from_float(float v);
+template <> __device__ __forceinline__ float tg_from_float<float>(float v) { return v; }
+template <> __device__ __forceinline__ tg_half tg_from_float<tg_half>(float v) { return (tg_half)v; }
+template <> __device__ __forceinline__ tg_bf16 tg_from_float<tg_bf16>(float v) { return (tg_bf16)v; }
+
+// Sum across the 64 lanes of a wavefront (butterfly, every lane gets the total).
+__device__ __forceinline__ float tg_wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+__device__ __forceinline__ double tg_wave_sum_d(double v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+__device__ __forceinline__ float tg_wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// Block-wide sum of NV values for a block of NW wavefronts, through LDS.
+// `red` must hold NW*NV floats.  All threads receive the totals.
+template <int NW, int NV>
+__device__ __forceinline__ void tg_block_sum(float (&v)[NV], float* red) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) v[i] = tg_wave_sum(v[i]);
+  if (NW == 1) return;
+  if (lane == 0) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) red[wave * NV + i] = v[i];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) s += red[w * NV + i];
+    v[i] = s;
+  }
+  __syncthreads();
+}
+
+// 16-byte vector of T used for coalesced dwordx4 traffic.
+template <typename T> struct tg_vec16 {
+  static constexpr int N = 16 / sizeof(T);
+  T v[N];
+};
+
+template <typename T>
+__device__ __forceinline__ tg_vec16<T> tg_load16(const T* p) {
+  tg_vec16<T> r;
+  *reinterpret_cast<uint4*>(&r) = *reinterpret_cast<const uint4*>(p);
+  return r;
+}
+template <typename T>
+__device__ __forceinline__ tg_vec16<T> tg_load16_nt(const T* p) {
+  tg_vec16<T> r;
+  uint4 u;
+  u.x = __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(p) + 0);
+  u.y = __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(p) + 1);
+  u.z = __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(p) + 2);
+  u.w = __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(p) + 3);
+  *reinterpret_cast<uint4*>(&r) = u;
+  return r;
+}
+template <typename T>
+__device__ __forceinline__ void tg_store16(T* p, const tg_vec16<T>& r) {
+  *reinterpret_cast<uint4*>(p) = *reinterpret_cast<const uint4*>(&r);
+}
+
+// Number of CUs on the current device, cached per device by tg_runtime.
+int tg_num_cus();

@@ -1,0 +1,284 @@
+// Elementwise activation forward/backward (GELU tanh-approx, SiLU) and the
+// generic grad-accumulate kernel (y = a*x + b*y with dtype conversion).
+//
+// Layout: flat contiguous arrays of n elements.  Traffic is issued as 16-byte
+// (dwordx4) vectors, UNROLL vectors in flight per thread, one pass over the
+// array; a 16-byte misaligned operand switches to the scalar variant.
+#include "tg_common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 4;
+
+enum { OP_GELU = 0, OP_SILU = 1 };
+
+// tanh-approx GELU derivative, reference formula (_core.py:493-507):
+//   u = c0*(x + c1*x^3), t = tanh(u)
+//   g = 0.5*(1+t) + 0.5*x*(1-t^2)*c0*(1+3*c1*x^2)
+// tanh is evaluated from e = exp(-2|u|) in (0,1] so that neither (1+t) nor
+// (1-t^2) = sech^2(u) loses precision to cancellation.
+__device__ __forceinline__ float gelu_grad(float x) {
+  const float c0 = 0.7978845608028654f, c1 = 0.044715f;
+  const float x2 = x * x;
+  const float u = c0 * (x + c1 * x2 * x);
+  const float e = __expf(-2.0f * fabsf(u));
+  const float r = 1.0f / (1.0f + e);
+  const float onept = (u >= 0.f) ? 1.0f + (1.0f - e) * r : 2.0f * e * r;  // 1 + tanh(u)
+  const float sech2 = 4.0f * e * r * r;                                   // 1 - tanh(u)^2
+  const float du = c0 * (1.0f + 3.0f * c1 * x2);
+  return 0.5f * onept + 0.5f * x * sech2 * du;
+}
+
+__device__ __forceinline__ float gelu_fwd(float x) {
+  const float c0 = 0.7978845608028654f, c1 = 0.044715f;
+  const float u = c0 * (x + c1 * x * x * x);
+  const float e = __expf(-2.0f * fabsf(u));
+  const float r = 1.0f / (1.0f + e);
+  const float onept = (u >= 0.f) ? 1.0f + (1.0f - e) * r : 2.0f * e * r;
+  return 0.5f * x * onept;
+}
+
+// SiLU derivative, reference formula (_core.py:522-533): s*(1 + x*(1-s)),
+// s = sigmoid(x).  1-s is formed as e*s with e = exp(-x) (no cancellation).
+__device__ __forceinline__ float silu_grad(float x) {
+  const float e = __expf(-x);
+  const float s = 1.0f / (1.0f + e);
+  const float oms = (x >= 0.f) ? e * s : 1.0f - s;
+  return s * (1.0f + x * oms);
+}
+__device__ __forceinline__ float silu_fwd(float x) {
+  const float e = __expf(-x);
+  return x / (1.0f + e);
+}
+
+template <int OP> __device__ __forceinline__ float act_grad(float x) {
+  return OP == OP_GELU ? gelu_grad(x) : silu_grad(x);
+}
+template <int OP> __device__ __forceinline__ float act_fwd(float x) {
+  return OP == OP_GELU ? gelu_fwd(x) : silu_fwd(x);
+}
+
+// dx (+)= dy * act'(x)
+template <typename T, int OP, bool ACC>
+__global__ __launch_bounds__(kThreads) void k_act_bwd(const T* __restrict__ x,
+                                                      const T* __restrict__ dy,
+                                                      T* __restrict__ dx, int64_t nvec,
+                                                      int64_t n) {
+  constexpr int V = tg_vec16<T>::N;
+  const int64_t base = (int64_t)blockIdx.x * kThreads * kUnroll + threadIdx.x;
+  tg_vec16<T> xv[kUnroll], gv[kUnroll], ov[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t i = base + (int64_t)u * kThreads;
+    if (i < nvec) {
+      xv[u] = tg_load16(x + i * V);
+      gv[u] = tg_load16(dy + i * V);
+      if (ACC) ov[u] = tg_load16(dx + i * V);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t i = base + (int64_t)u * kThreads;
+    if (i < nvec) {
+      tg_vec16<T> r;
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        float g = tg_to_float(gv[u].v[j]) * act_grad<OP>(tg_to_float(xv[u].v[j]));
+        if (ACC) g += tg_to_float(ov[u].v[j]);
+        r.v[j] = tg_from_float<T>(g);
+      }
+      tg_store16(dx + i * V, r);
+    }
+  }
+  // scalar tail (fewer than V elements), handled by the first block
+  if (blockIdx.x == 0) {
+    for (int64_t i = nvec * V + threadIdx.x; i < n; i += kThreads) {
+      float g = tg_to_float(dy[i]) * act_grad<OP>(tg_to_float(x[i]));
+      if (ACC) g += tg_to_float(dx[i]);
+      dx[i] = tg_from_float<T>(g);
+    }
+  }
+}
+
+template <typename T, int OP>
+__global__ __launch_bounds__(kThreads) void k_act_fwd(const T* __restrict__ x,
+                                                      T* __restrict__ y, int64_t nvec,
+                                                      int64_t n) {
+  constexpr int V = tg_vec16<T>::N;
+  const int64_t base = (int64_t)blockIdx.x * kThreads * kUnroll + threadIdx.x;
+  tg_vec16<T> xv[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t i = base + (int64_t)u * kThreads;
+    if (i < nvec) xv[u] = tg_load16(x + i * V);
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t i = base + (int64_t)u * kThreads;
+    if (i < nvec) {
+      tg_vec16<T> r;
+#pragma unroll
+      for (int j = 0; j < V; ++j) r.v[j] = tg_from_float<T>(act_fwd<OP>(tg_to_float(xv[u].v[j])));
+      tg_store16(y + i * V, r);
+    }
+  }
+  if (blockIdx.x == 0) {
+    for (int64_t i = nvec * V + threadIdx.x; i < n; i += kThreads)
+      y[i] = tg_from_float<T>(act_fwd<OP>(tg_to_float(x[i])));
+  }
+}
+
+template <typename T, int OP>
+int launch_act_bwd(const void* x, const void* dy, void* dx, int64_t n, int acc, hipStream_t s) {
+  constexpr int V = tg_vec16<T>::N;
+  const bool vec = tg_aligned16(x) && tg_aligned16(dy) && tg_aligned16(dx);
+  const int64_t nvec = vec ? n / V : 0;
+  int64_t blocks = (nvec + kThreads * kUnroll - 1) / (kThreads * kUnroll);
+  if (blocks < 1) blocks = 1;
+  if (blocks > 0x7fffffff) {
+    tg_set_error("activation backward: n=%lld too large", (long long)n);
+    return TG_ERR_INVALID;
+  }
+  if (acc)
+    k_act_bwd<T, OP, true><<<(unsigned)blocks, kThreads, 0, s>>>(
+        (const T*)x, (const T*)dy, (T*)dx, nvec, n);
+  else
+    k_act_bwd<T, OP, false><<<(unsigned)blocks, kThreads, 0, s>>>(
+        (const T*)x, (const T*)dy, (T*)dx, nvec, n);
+  return tg_check_launch(OP == OP_GELU ? "tg_gelu_bwd" : "tg_silu_bwd");
+}
+
+template <typename T, int OP>
+int launch_act_fwd(const void* x, void* y, int64_t n, hipStream_t s) {
+  constexpr int V = tg_vec16<T>::N;
+  const bool vec = tg_aligned16(x) && tg_aligned16(y);
+  const int64_t nvec = vec ? n / V : 0;
+  int64_t blocks = (nvec + kThreads * kUnroll - 1) / (kThreads * kUnroll);
+  if (blocks < 1) blocks = 1;
+  k_act_fwd<T, OP><<<(unsigned)blocks, kThreads, 0, s>>>((const T*)x, (T*)y, nvec, n);
+  return tg_check_launch(OP == OP_GELU ? "tg_gelu_fwd" : "tg_silu_fwd");
+}
+
+template <int OP>
+int dispatch_bwd(int dtype, const void* x, const void* dy, void* dx, int64_t n, int acc,
+                 void* stream) {
+  TG_REQUIRE(n >= 0, "activation backward: negative n");
+  if (n == 0) return TG_OK;
+  TG_REQUIRE(x && dy && dx, "activation backward: null pointer");
+  hipStream_t s = tg_stream(stream);
+  switch (dtype) {
+    case TG_F32: return launch_act_bwd<float, OP>(x, dy, dx, n, acc, s);
+    case TG_F16: return launch_act_bwd<tg_half, OP>(x, dy, dx, n, acc, s);
+    case TG_BF16: return launch_act_bwd<tg_bf16, OP>(x, dy, dx, n, acc, s);
+  }
+  tg_set_error("activation backward: unsupported dtype %d", dtype);
+  return TG_ERR_UNSUPPORTED;
+}
+
+template <int OP>
+int dispatch_fwd(int dtype, const void* x, void* y, int64_t n, void* stream) {
+  TG_REQUIRE(n >= 0, "activation forward: negative n");
+  if (n == 0) return TG_OK;
+  TG_REQUIRE(x && y, "activation forward: null pointer");
+  hipStream_t s = tg_stream(stream);
+  switch (dtype) {
+    case TG_F32: return launch_act_fwd<float, OP>(x, y, n, s);
+    case TG_F16: return launch_act_fwd<tg_half, OP>(x, y, n, s);
+    case TG_BF16: return launch_act_fwd<tg_bf16, OP>(x, y, n, s);
+  }
+  tg_set_error("activation forward: unsupported dtype %d", dtype);
+  return TG_ERR_UNSUPPORTED;
+}
+
+// ---------------------------------------------------------------------------
+// y = alpha*x + beta*y   (beta == 0: y is not read).  x and y may differ in dtype;
+// arithmetic is fp32.  Used for `grad += g` with a dtype cast and for scaling.
+template <typename TX, typename TY>
+__global__ __launch_bounds__(kThreads) void k_axpby(const TX* __restrict__ x, TY* __restrict__ y,
+                                                    float alpha, float beta, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
+    float v = alpha * tg_to_float(x[i]);
+    if (beta != 0.f) v += beta * tg_to_float(y[i]);
+    y[i] = tg_from_float<TY>(v);
+  }
+}
+
+template <typename TX, typename TY>
+int launch_axpby(const void* x, void* y, float a, float b, int64_t n, hipStream_t s) {
+  int64_t blocks = (n + kThreads * 4 - 1) / (kThreads * 4);
+  const int64_t cap = (int64_t)tg_num_cus() * 32;
+  if (blocks > cap) blocks = cap;
+  if (blocks < 1) blocks = 1;
+  k_axpby<TX, TY><<<(unsigned)blocks, kThreads, 0, s>>>((const TX*)x, (TY*)y, a, b, n);
+  return tg_check_launch("tg_axpby");
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void k_fill(T* __restrict__ y, float v, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  const T tv = tg_from_float<T>(v);
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) y[i] = tv;
+}
+
+}  // namespace
+
+// ---- exported C-ABI ----
+
+TG_EXPORT int tg_gelu_bwd(int dtype, const void* x, const void* dy, void* dx, int64_t n,
+                          int accumulate, void* stream) {
+  return dispatch_bwd<OP_GELU>(dtype, x, dy, dx, n, accumulate, stream);
+}
+TG_EXPORT int tg_silu_bwd(int dtype, const void* x, const void* dy, void* dx, int64_t n,
+                          int accumulate, void* stream) {
+  return dispatch_bwd<OP_SILU>(dtype, x, dy, dx, n, accumulate, stream);
+}
+TG_EXPORT int tg_gelu_fwd(int dtype, const void* x, void* y, int64_t n, void* stream) {
+  return dispatch_fwd<OP_GELU>(dtype, x, y, n, stream);
+}
+TG_EXPORT int tg_silu_fwd(int dtype, const void* x, void* y, int64_t n, void* stream) {
+  return dispatch_fwd<OP_SILU>(dtype, x, y, n, stream);
+}
+
+TG_EXPORT int tg_axpby(int dtype_x, const void* x, int dtype_y, void* y, int64_t n, float alpha,
+                       float beta, void* stream) {
+  TG_REQUIRE(n >= 0, "tg_axpby: negative n");
+  if (n == 0) return TG_OK;
+  TG_REQUIRE(x && y, "tg_axpby: null pointer");
+  hipStream_t s = tg_stream(stream);
+#define TG_AXPBY_CASE(DX, TX, DY, TY) \
+  if (dtype_x == DX && dtype_y == DY) return launch_axpby<TX, TY>(x, y, alpha, beta, n, s);
+  TG_AXPBY_CASE(TG_F32, float, TG_F32, float)
+  TG_AXPBY_CASE(TG_F32, float, TG_F16, tg_half)
+  TG_AXPBY_CASE(TG_F32, float, TG_BF16, tg_bf16)
+  TG_AXPBY_CASE(TG_F16, tg_half, TG_F32, float)
+  TG_AXPBY_CASE(TG_F16, tg_half, TG_F16, tg_half)
+  TG_AXPBY_CASE(TG_BF16, tg_bf16, TG_F32, float)
+  TG_AXPBY_CASE(TG_BF16, tg_bf16, TG_BF16, tg_bf16)
+#undef TG_AXPBY_CASE
+  tg_set_error("tg_axpby: unsupported dtype pair (%d,%d)", dtype_x, dtype_y);
+  return TG_ERR_UNSUPPORTED;
+}
+
+// Fill n elements with `value` (a kernel, not a memset node, so it is safe to
+// record into a captured graph).
+TG_EXPORT int tg_fill(int dtype, void* y, int64_t n, float value, void* stream) {
+  TG_REQUIRE(n >= 0, "tg_fill: negative n");
+  if (n == 0) return TG_OK;
+  TG_REQUIRE(y, "tg_fill: null pointer");
+  hipStream_t s = tg_stream(stream);
+  int64_t blocks = (n + kThreads * 4 - 1) / (kThreads * 4);
+  const int64_t cap = (int64_t)tg_num_cus() * 32;
+  if (blocks > cap) blocks = cap;
+  if (blocks < 1) blocks = 1;
+  switch (dtype) {
+    case TG_F32: k_fill<float><<<(unsigned)blocks, kThreads, 0, s>>>((float*)y, value, n); break;
+    case TG_F16: k_fill<tg_half><<<(unsigned)blocks, kThreads, 0, s>>>((tg_half*)y, value, n); break;
+    case TG_BF16: k_fill<tg_bf16><<<(unsigned)blocks, kThreads, 0, s>>>((tg_bf16*)y, value, n); break;
+    default:
+      tg_set_error("tg_fill: unsupported dtype %d", dtype);
+      return TG_ERR_UNSUPPORTED;
+  }
+  return tg_check_launch("tg_fill");
+}

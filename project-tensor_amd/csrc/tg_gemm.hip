@@ -1,0 +1,306 @@
+// Batched row-major GEMM on CDNA4 matrix cores:
+//   C[b] = alpha * op(A[b]) @ op(B[b]) + beta * C[b]
+// serving the matmul forward and its backward dA = dC @ B^T, dB = A^T @ dC
+// (reference: Tensor.__matmul__ and its closure, _core.py:999-1068).
+//
+// Block tile 128x128xBK, 256 threads = 4 wavefronts in a 2x2 grid, each wave a
+// 64x64 sub-tile = 2x2 MFMA 32x32 tiles:
+//   fp16 / bf16: v_mfma_f32_32x32x16_{f16,bf16}, BK = 32
+//   fp32:        v_mfma_f32_32x32x2_f32,        BK = 16
+// Both operands are staged through LDS in k-contiguous layout (As[m][k], Bs[n][k]);
+// an operand whose global layout is contiguous along m/n is transposed while it is
+// written to LDS.  The next k-tile is fetched into registers while the current one
+// is multiplied.  Accumulation is fp32; the epilogue applies alpha/beta and converts.
+#include "tg_common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int BM = 128, BN = 128;
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+template <typename T> struct Mfma;
+template <> struct Mfma<tg_half> {
+  static constexpr int BK = 32;   // k per tile
+  static constexpr int EPL = 8;   // elements a lane feeds one instruction
+  __device__ static void run(const tg_half* a, const tg_half* b, f32x16& c) {
+    f16x8 av, bv;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) { av[e] = a[e]; bv[e] = b[e]; }
+    c = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, c, 0, 0, 0);
+  }
+};
+template <> struct Mfma<tg_bf16> {
+  static constexpr int BK = 32;
+  static constexpr int EPL = 8;
+  __device__ static void run(const tg_bf16* a, const tg_bf16* b, f32x16& c) {
+    bf16x8 av, bv;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) { av[e] = a[e]; bv[e] = b[e]; }
+    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, c, 0, 0, 0);
+  }
+};
+template <> struct Mfma<float> {
+  static constexpr int BK = 16;
+  static constexpr int EPL = 1;
+  __device__ static void run(const float* a, const float* b, f32x16& c) {
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[0], b[0], c, 0, 0, 0);
+  }
+};
+
+// Global -> register -> LDS staging of one operand tile (ROWS x BK), where "rows"
+// are m (for A) or n (for B).  KC: the operand is contiguous along k in memory.
+template <typename T, bool KC, bool VEC>
+struct TileLoader {
+  static constexpr int BK = Mfma<T>::BK;
+  static constexpr int VE = 16 / sizeof(T);                 // elements per 16B vector
+  static constexpr int NV = (128 * BK) / (VE * kThreads);   // vectors per thread (2)
+  static constexpr int NS = (128 * BK) / kThreads;          // scalars per thread
+  static constexpr int LDK = BK + 16 / (int)sizeof(T);      // padded LDS row (k) stride
+  T reg[VEC ? NV * VE : NS];
+
+  // rows_total: M or N extent; ld: leading dimension of the stored matrix.
+  __device__ void load(const T* __restrict__ base, int64_t ld, int64_t rows_total, int64_t K,
+                       int64_t row0, int64_t k0) {
+    const int t = threadIdx.x;
+    if (VEC) {
+#pragma unroll
+      for (int r = 0; r < NV; ++r) {
+        const int v = t + r * kThreads;
+        int64_t row, k;
+        if (KC) {
+          row = row0 + v / (BK / VE);
+          k = k0 + (v % (BK / VE)) * VE;
+        } else {
+          k = k0 + v / (128 / VE);
+          row = row0 + (v % (128 / VE)) * VE;
+        }
+        uint4 u = make_uint4(0, 0, 0, 0);
+        if (KC) {
+          if (row < rows_total && k + VE <= K)
+            u = *reinterpret_cast<const uint4*>(base + row * ld + k);
+          else if (row < rows_total && k < K) {
+            T tmp[VE];
+#pragma unroll
+            for (int e = 0; e < VE; ++e) tmp[e] = (k + e < K) ? base[row * ld + k + e] : T(0);
+            u = *reinterpret_cast<uint4*>(tmp);
+          }
+        } else {
+          if (k < K && row + VE <= rows_total)
+            u = *reinterpret_cast<const uint4*>(base + k * ld + row);
+          else if (k < K && row < rows_total) {
+            T tmp[VE];
+#pragma unroll
+            for (int e = 0; e < VE; ++e)
+              tmp[e] = (row + e < rows_total) ? base[k * ld + row + e] : T(0);
+            u = *reinterpret_cast<uint4*>(tmp);
+          }
+        }
+        *reinterpret_cast<uint4*>(&reg[r * VE]) = u;
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const int e = t + s * kThreads;
+        int64_t row, k;
+        if (KC) {
+          row = row0 + e / BK;
+          k = k0 + e % BK;
+        } else {
+          k = k0 + e / 128;
+          row = row0 + e % 128;
+        }
+        reg[s] = (row < rows_total && k < K) ? (KC ? base[row * ld + k] : base[k * ld + row]) : T(0);
+      }
+    }
+  }
+
+  __device__ void store(T* __restrict__ lds) const {
+    const int t = threadIdx.x;
+    if (VEC) {
+#pragma unroll
+      for (int r = 0; r < NV; ++r) {
+        const int v = t + r * kThreads;
+        if (KC) {
+          const int row = v / (BK / VE), k = (v % (BK / VE)) * VE;
+          *reinterpret_cast<uint4*>(lds + row * LDK + k) =
+              *reinterpret_cast<const uint4*>(&reg[r * VE]);
+        } else {
+          const int k = v / (128 / VE), row = (v % (128 / VE)) * VE;
+#pragma unroll
+          for (int e = 0; e < VE; ++e) lds[(row + e) * LDK + k] = reg[r * VE + e];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const int e = t + s * kThreads;
+        int row, k;
+        if (KC) {
+          row = e / BK;
+          k = e % BK;
+        } else {
+          k = e / 128;
+          row = e % 128;
+        }
+        lds[row * LDK + k] = reg[s];
+      }
+    }
+  }
+};
+
+template <typename T, typename TC, bool TA, bool TB, bool VEC>
+__global__ __launch_bounds__(kThreads) void k_gemm(int64_t M, int64_t N, int64_t K, float alpha,
+                                                   const T* __restrict__ A, int64_t lda,
+                                                   int64_t sa, const T* __restrict__ B,
+                                                   int64_t ldb, int64_t sb, float beta,
+                                                   TC* __restrict__ C, int64_t ldc, int64_t sc) {
+  constexpr int BK = Mfma<T>::BK;
+  constexpr int EPL = Mfma<T>::EPL;
+  constexpr int KPL = BK / 2;  // k elements per lane per tile (lane half h owns k in [h*KPL, h*KPL+KPL))
+  using LA = TileLoader<T, !TA, VEC>;
+  using LB = TileLoader<T, TB, VEC>;
+  constexpr int LDK = LA::LDK;
+  __shared__ __attribute__((aligned(16))) T As[BM * LDK];
+  __shared__ __attribute__((aligned(16))) T Bs[BN * LDK];
+
+  const int64_t bz = blockIdx.z;
+  A += bz * sa;
+  B += bz * sb;
+  C += bz * sc;
+  const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+  const int lr = lane & 31, lh = lane >> 5;
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  LA la;
+  LB lb;
+  la.load(A, lda, M, K, m0, 0);
+  lb.load(B, ldb, N, K, n0, 0);
+  for (int64_t k0 = 0; k0 < K; k0 += BK) {
+    __syncthreads();
+    la.store(As);
+    lb.store(Bs);
+    __syncthreads();
+    if (k0 + BK < K) {
+      la.load(A, lda, M, K, m0, k0 + BK);
+      lb.load(B, ldb, N, K, n0, k0 + BK);
+    }
+    T af[2][KPL], bf[2][KPL];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const T* pa = As + (wm + i * 32 + lr) * LDK + lh * KPL;
+      const T* pb = Bs + (wn + i * 32 + lr) * LDK + lh * KPL;
+#pragma unroll
+      for (int e = 0; e < KPL; e += 16 / (int)sizeof(T)) {
+        *reinterpret_cast<uint4*>(&af[i][e]) = *reinterpret_cast<const uint4*>(pa + e);
+        *reinterpret_cast<uint4*>(&bf[i][e]) = *reinterpret_cast<const uint4*>(pb + e);
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < KPL / EPL; ++s)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) Mfma<T>::run(&af[i][s * EPL], &bf[j][s * EPL], acc[i][j]);
+  }
+
+  // Epilogue: acc[i][j][r], r = g*4 + q  ->  row = 8g + 4*lh + q, col = lr (32x32 tile).
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t col = n0 + wn + j * 32 + lr;
+      if (col >= N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + wm + i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
+        if (row < M) {
+          float v = alpha * acc[i][j][r];
+          TC* pc = C + row * ldc + col;
+          if (beta != 0.f) v += beta * tg_to_float(*pc);
+          *pc = tg_from_float<TC>(v);
+        }
+      }
+    }
+}
+
+template <typename T, typename TC>
+int launch(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const void* A,
+           int64_t lda, int64_t sa, const void* B, int64_t ldb, int64_t sb, float beta, void* C,
+           int64_t ldc, int64_t sc, int64_t batch, hipStream_t s) {
+  constexpr int VE = 16 / sizeof(T);
+  const bool vec = tg_aligned16(A) && tg_aligned16(B) && lda % VE == 0 && ldb % VE == 0 &&
+                   sa % VE == 0 && sb % VE == 0;
+  dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM), (unsigned)batch);
+  const T* a = (const T*)A;
+  const T* b = (const T*)B;
+  TC* c = (TC*)C;
+#define TG_G(TA_, TB_, V_) \
+  k_gemm<T, TC, TA_, TB_, V_><<<grid, kThreads, 0, s>>>(M, N, K, alpha, a, lda, sa, b, ldb, sb, beta, c, ldc, sc)
+  if (vec) {
+    if (!ta && !tb) TG_G(false, false, true);
+    else if (!ta && tb) TG_G(false, true, true);
+    else if (ta && !tb) TG_G(true, false, true);
+    else TG_G(true, true, true);
+  } else {
+    if (!ta && !tb) TG_G(false, false, false);
+    else if (!ta && tb) TG_G(false, true, false);
+    else if (ta && !tb) TG_G(true, false, false);
+    else TG_G(true, true, false);
+  }
+#undef TG_G
+  return tg_check_launch("tg_gemm");
+}
+
+}  // namespace
+
+TG_EXPORT int tg_gemm(int dtype_ab, int dtype_c, int trans_a, int trans_b, int64_t M, int64_t N,
+                      int64_t K, float alpha, const void* A, int64_t lda, int64_t stride_a,
+                      const void* B, int64_t ldb, int64_t stride_b, float beta, void* C,
+                      int64_t ldc, int64_t stride_c, int64_t batch, void* stream) {
+  TG_REQUIRE(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "tg_gemm: negative extent");
+  if (M == 0 || N == 0 || batch == 0) return TG_OK;
+  TG_REQUIRE(C, "tg_gemm: null C");
+  TG_REQUIRE(ldc >= N, "tg_gemm: ldc %lld < N %lld", (long long)ldc, (long long)N);
+  TG_REQUIRE(batch <= 65535, "tg_gemm: batch %lld exceeds 65535", (long long)batch);
+  TG_REQUIRE((M + BM - 1) / BM <= 65535, "tg_gemm: M too large");
+  hipStream_t s = tg_stream(stream);
+  if (K == 0) {
+    // C = beta*C: no product term; reuse the kernel with K = 0 (acc stays zero).
+  } else {
+    TG_REQUIRE(A && B, "tg_gemm: null operand");
+    TG_REQUIRE(lda >= (trans_a ? M : K) && ldb >= (trans_b ? K : N), "tg_gemm: bad leading dim");
+  }
+  if (dtype_ab == TG_F16) {
+    if (dtype_c == TG_F32)
+      return launch<tg_half, float>(trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb,
+                                    stride_b, beta, C, ldc, stride_c, batch, s);
+    if (dtype_c == TG_F16)
+      return launch<tg_half, tg_half>(trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb,
+                                      stride_b, beta, C, ldc, stride_c, batch, s);
+  } else if (dtype_ab == TG_BF16) {
+    if (dtype_c == TG_F32)
+      return launch<tg_bf16, float>(trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb,
+                                    stride_b, beta, C, ldc, stride_c, batch, s);
+    if (dtype_c == TG_BF16)
+      return launch<tg_bf16, tg_bf16>(trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb,
+                                      stride_b, beta, C, ldc, stride_c, batch, s);
+  } else if (dtype_ab == TG_F32 && dtype_c == TG_F32) {
+    return launch<float, float>(trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb,
+                                stride_b, beta, C, ldc, stride_c, batch, s);
+  }
+  tg_set_error("tg_gemm: unsupported dtype combination ab=%d c=%d", dtype_ab, dtype_c);
+  return TG_ERR_UNSUPPORTED;
+}

@@ -1,0 +1,842 @@
+// Row-wise kernels over a row-major [rows, cols] matrix:
+//   softmax forward/backward along the last axis,
+//   LayerNorm forward (saves mean, rstd) and backward (dx, dgamma, dbeta),
+//   column sums (the unbroadcast reduction of a bias gradient).
+//
+// Register path: a row is split across TPR threads (a wavefront when TPR=64,
+// the whole 256-thread block when TPR=256), each thread holding VPT 16-byte
+// vectors, so every element of x/y/dy is read from HBM exactly once.  Row sums
+// use wavefront butterflies plus one LDS exchange when TPR=256.  Shapes that do
+// not fit (cols not a multiple of the vector width, misaligned, or very wide)
+// take the looping wavefront-per-row path, which re-reads the row from cache.
+#include "tg_common.h"
+
+namespace {
+
+constexpr int kBlock = 256;
+
+// ---------------------------------------------------------------------------
+// Partial sums across the TPR threads of a row group.  For TPR == 256 the block
+// is one group; `red` holds 4*NV floats.
+template <int TPR, int NV>
+__device__ __forceinline__ void group_sum(float (&v)[NV], float* red) {
+  if (TPR == 64) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) v[i] = tg_wave_sum(v[i]);
+  } else {
+    tg_block_sum<4, NV>(v, red);
+  }
+}
+template <int TPR>
+__device__ __forceinline__ float group_max(float v, float* red) {
+  v = tg_wave_max(v);
+  if (TPR == 64) return v;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  v = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  return v;
+}
+
+// ============================ softmax ======================================
+// Forward: y = exp(x - max) / sum(exp(x - max))   (_core.py:1286-1292)
+template <typename T, int TPR, int VPT>
+__global__ __launch_bounds__(kBlock) void k_softmax_fwd_reg(const T* __restrict__ x,
+                                                            T* __restrict__ y, int64_t rows,
+                                                            int cols) {
+  constexpr int V = tg_vec16<T>::N;
+  constexpr int G = kBlock / TPR;
+  __shared__ float red[8];
+  const int t = threadIdx.x % TPR;
+  const int64_t row = (int64_t)blockIdx.x * G + threadIdx.x / TPR;
+  const bool live = row < rows;
+  const int nv = cols / V;
+  const T* xr = x + (live ? row : 0) * (int64_t)cols;
+  float xv[VPT][V];
+  float m = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    const int vi = t + k * TPR;
+    if (live && vi < nv) {
+      tg_vec16<T> a = tg_load16(xr + vi * V);
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        xv[k][j] = tg_to_float(a.v[j]);
+        m = fmaxf(m, xv[k][j]);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < V; ++j) xv[k][j] = -INFINITY;
+    }
+  }
+  m = group_max<TPR>(m, red);
+  float s[1] = {0.f};
+#pragma unroll
+  for (int k = 0; k < VPT; ++k)
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      const float e = (xv[k][j] == -INFINITY) ? 0.f : __expf(xv[k][j] - m);
+      xv[k][j] = e;
+      s[0] += e;
+    }
+  group_sum<TPR, 1>(s, red);
+  const float inv = 1.0f / s[0];
+  if (!live) return;
+  T* yr = y + row * (int64_t)cols;
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    const int vi = t + k * TPR;
+    if (vi < nv) {
+      tg_vec16<T> o;
+#pragma unroll
+      for (int j = 0; j < V; ++j) o.v[j] = tg_from_float<T>(xv[k][j] * inv);
+      tg_store16(yr + vi * V, o);
+    }
+  }
+}
+
+// Backward: dx (+)= y * (dy - sum(dy * y))   (_core.py:1294-1297)
+template <typename T, int TPR, int VPT, bool ACC>
+__global__ __launch_bounds__(kBlock) void k_softmax_bwd_reg(const T* __restrict__ y,
+                                                            const T* __restrict__ dy,
+                                                            T* __restrict__ dx, int64_t rows,
+                                                            int cols) {
+  constexpr int V = tg_vec16<T>::N;
+  constexpr int G = kBlock / TPR;
+  __shared__ float red[8];
+  const int t = threadIdx.x % TPR;
+  const int64_t row = (int64_t)blockIdx.x * G + threadIdx.x / TPR;
+  const bool live = row < rows;
+  const int nv = cols / V;
+  const int64_t off = (live ? row : 0) * (int64_t)cols;
+  tg_vec16<T> yv[VPT], gv[VPT];
+  float s[1] = {0.f};
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    const int vi = t + k * TPR;
+    if (live && vi < nv) {
+      yv[k] = tg_load16(y + off + vi * V);
+      gv[k] = tg_load16(dy + off + vi * V);
+#pragma unroll
+      for (int j = 0; j < V; ++j) s[0] += tg_to_float(yv[k].v[j]) * tg_to_float(gv[k].v[j]);
+    }
+  }
+  group_sum<TPR, 1>(s, red);
+  if (!live) return;
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    const int vi = t + k * TPR;
+    if (vi < nv) {
+      tg_vec16<T> o;
+      if (ACC) o = tg_load16(dx + off + vi * V);
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        float r = tg_to_float(yv[k].v[j]) * (tg_to_float(gv[k].v[j]) - s[0]);
+        if (ACC) r += tg_to_float(o.v[j]);
+        o.v[j] = tg_from_float<T>(r);
+      }
+      tg_store16(dx + off + vi * V, o);
+    }
+  }
+}
+
+// Looping wavefront-per-row variants for arbitrary cols.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_softmax_fwd_loop(const T* __restrict__ x,
+                                                             T* __restrict__ y, int64_t rows,
+                                                             int64_t cols) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + row * cols;
+  T* yr = y + row * cols;
+  float m = -INFINITY;
+  for (int64_t c = lane; c < cols; c += 64) m = fmaxf(m, tg_to_float(xr[c]));
+  m = tg_wave_max(m);
+  float s = 0.f;
+  for (int64_t c = lane; c < cols; c += 64) {
+    const float v = tg_to_float(xr[c]);
+    s += (v == -INFINITY) ? 0.f : __expf(v - m);
+  }
+  s = tg_wave_sum(s);
+  const float inv = 1.0f / s;
+  for (int64_t c = lane; c < cols; c += 64) {
+    const float v = tg_to_float(xr[c]);
+    yr[c] = tg_from_float<T>(((v == -INFINITY) ? 0.f : __expf(v - m)) * inv);
+  }
+}
+
+template <typename T, bool ACC>
+__global__ __launch_bounds__(kBlock) void k_softmax_bwd_loop(const T* __restrict__ y,
+                                                             const T* __restrict__ dy,
+                                                             T* __restrict__ dx, int64_t rows,
+                                                             int64_t cols) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t off = row * cols;
+  float s = 0.f;
+  for (int64_t c = lane; c < cols; c += 64) s += tg_to_float(y[off + c]) * tg_to_float(dy[off + c]);
+  s = tg_wave_sum(s);
+  for (int64_t c = lane; c < cols; c += 64) {
+    float r = tg_to_float(y[off + c]) * (tg_to_float(dy[off + c]) - s);
+    if (ACC) r += tg_to_float(dx[off + c]);
+    dx[off + c] = tg_from_float<T>(r);
+  }
+}
+
+// Choose threads-per-row and vectors-per-thread for the register path.
+// Returns false if the row does not fit the register path.
+template <typename T>
+bool pick_reg_shape(int64_t cols, bool aligned, int* tpr, int* vpt) {
+  constexpr int V = tg_vec16<T>::N;
+  if (!aligned || cols % V != 0 || cols <= 0) return false;
+  const int64_t nv = cols / V;
+  if (nv <= 64 * 4) {
+    *tpr = 64;
+    *vpt = nv <= 64 ? 1 : nv <= 128 ? 2 : 4;
+    return true;
+  }
+  if (nv <= 256 * 8) {
+    *tpr = 256;
+    *vpt = nv <= 256 ? 1 : nv <= 512 ? 2 : nv <= 1024 ? 4 : 8;
+    return true;
+  }
+  return false;
+}
+
+#define TG_REG_DISPATCH(KERNEL_LAUNCH)                   \
+  switch (tpr * 16 + vpt) {                              \
+    case 64 * 16 + 1: KERNEL_LAUNCH(64, 1); break;       \
+    case 64 * 16 + 2: KERNEL_LAUNCH(64, 2); break;       \
+    case 64 * 16 + 4: KERNEL_LAUNCH(64, 4); break;       \
+    case 256 * 16 + 1: KERNEL_LAUNCH(256, 1); break;     \
+    case 256 * 16 + 2: KERNEL_LAUNCH(256, 2); break;     \
+    case 256 * 16 + 4: KERNEL_LAUNCH(256, 4); break;     \
+    case 256 * 16 + 8: KERNEL_LAUNCH(256, 8); break;     \
+  }
+
+template <typename T>
+int softmax_fwd_t(const void* x, void* y, int64_t rows, int64_t cols, hipStream_t s) {
+  int tpr = 0, vpt = 0;
+  if (pick_reg_shape<T>(cols, tg_aligned16(x) && tg_aligned16(y), &tpr, &vpt)) {
+    const int64_t g = kBlock / tpr;
+    const unsigned blocks = (unsigned)((rows + g - 1) / g);
+#define L(TPR, VPT) \
+  k_softmax_fwd_reg<T, TPR, VPT><<<blocks, kBlock, 0, s>>>((const T*)x, (T*)y, rows, (int)cols)
+    TG_REG_DISPATCH(L)
+#undef L
+  } else {
+    k_softmax_fwd_loop<T><<<(unsigned)((rows + 3) / 4), kBlock, 0, s>>>((const T*)x, (T*)y, rows,
+                                                                        cols);
+  }
+  return tg_check_launch("tg_softmax_fwd");
+}
+
+template <typename T>
+int softmax_bwd_t(const void* y, const void* dy, void* dx, int64_t rows, int64_t cols, int acc,
+                  hipStream_t s) {
+  int tpr = 0, vpt = 0;
+  const bool al = tg_aligned16(y) && tg_aligned16(dy) && tg_aligned16(dx);
+  if (pick_reg_shape<T>(cols, al, &tpr, &vpt)) {
+    const int64_t g = kBlock / tpr;
+    const unsigned blocks = (unsigned)((rows + g - 1) / g);
+    if (acc) {
+#define L(TPR, VPT)                                                                            \
+  k_softmax_bwd_reg<T, TPR, VPT, true><<<blocks, kBlock, 0, s>>>((const T*)y, (const T*)dy, \
+                                                                 (T*)dx, rows, (int)cols)
+      TG_REG_DISPATCH(L)
+#undef L
+    } else {
+#define L(TPR, VPT)                                                                             \
+  k_softmax_bwd_reg<T, TPR, VPT, false><<<blocks, kBlock, 0, s>>>((const T*)y, (const T*)dy, \
+                                                                  (T*)dx, rows, (int)cols)
+      TG_REG_DISPATCH(L)
+#undef L
+    }
+  } else {
+    const unsigned blocks = (unsigned)((rows + 3) / 4);
+    if (acc)
+      k_softmax_bwd_loop<T, true><<<blocks, kBlock, 0, s>>>((const T*)y, (const T*)dy, (T*)dx,
+                                                            rows, cols);
+    else
+      k_softmax_bwd_loop<T, false><<<blocks, kBlock, 0, s>>>((const T*)y, (const T*)dy, (T*)dx,
+                                                             rows, cols);
+  }
+  return tg_check_launch("tg_softmax_bwd");
+}
+
+// ============================ LayerNorm ====================================
+// Forward (_nn.py:900-917): mean, population variance over the row,
+// xhat = (x-mean)/sqrt(var+eps), y = gamma*xhat + beta.  Saves mean and
+// rstd = 1/sqrt(var+eps) per row (fp32).
+template <typename T, int TPR, int VPT>
+__global__ __launch_bounds__(kBlock) void k_ln_fwd_reg(const T* __restrict__ x,
+                                                       const float* __restrict__ gamma,
+                                                       const float* __restrict__ beta,
+                                                       T* __restrict__ y, float* __restrict__ mean,
+                                                       float* __restrict__ rstd, int64_t rows,
+                                                       int cols, float eps) {
+  constexpr int V = tg_vec16<T>::N;
+  constexpr int G = kBlock / TPR;
+  __shared__ float red[8];
+  const int t = threadIdx.x % TPR;
+  const int64_t row = (int64_t)blockIdx.x * G + threadIdx.x / TPR;
+  const bool live = row < rows;
+  const int nv = cols / V;
+  const int64_t off = (live ? row : 0) * (int64_t)cols;
+  float xv[VPT][V];
+  float s[1] = {0.f};
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    const int vi = t + k * TPR;
+    if (live && vi < nv) {
+      tg_vec16<T> a = tg_load16(x + off + vi * V);
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        xv[k][j] = tg_to_float(a.v[j]);
+        s[0] += xv[k][j];
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < V; ++j) xv[k][j] = 0.f;
+    }
+  }
+  group_sum<TPR, 1>(s, red);
+  const float mu = s[0] / (float)cols;
+  float q[1] = {0.f};
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    const int vi = t + k * TPR;
+    if (live && vi < nv) {
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const float d = xv[k][j] - mu;
+        q[0] += d * d;
+      }
+    }
+  }
+  group_sum<TPR, 1>(q, red);
+  const float rs = 1.0f / sqrtf(q[0] / (float)cols + eps);
+  if (!live) return;
+  if (t == 0) {
+    mean[row] = mu;
+    rstd[row] = rs;
+  }
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    const int vi = t + k * TPR;
+    if (vi < nv) {
+      tg_vec16<T> o;
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const int c = vi * V + j;
+        o.v[j] = tg_from_float<T>(gamma[c] * ((xv[k][j] - mu) * rs) + beta[c]);
+      }
+      tg_store16(y + off + vi * V, o);
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_ln_fwd_loop(const T* __restrict__ x,
+                                                        const float* __restrict__ gamma,
+                                                        const float* __restrict__ beta,
+                                                        T* __restrict__ y, float* __restrict__ mean,
+                                                        float* __restrict__ rstd, int64_t rows,
+                                                        int64_t cols, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t off = row * cols;
+  float s = 0.f;
+  for (int64_t c = lane; c < cols; c += 64) s += tg_to_float(x[off + c]);
+  const float mu = tg_wave_sum(s) / (float)cols;
+  float q = 0.f;
+  for (int64_t c = lane; c < cols; c += 64) {
+    const float d = tg_to_float(x[off + c]) - mu;
+    q += d * d;
+  }
+  const float rs = 1.0f / sqrtf(tg_wave_sum(q) / (float)cols + eps);
+  if (lane == 0) {
+    mean[row] = mu;
+    rstd[row] = rs;
+  }
+  for (int64_t c = lane; c < cols; c += 64)
+    y[off + c] = tg_from_float<T>(gamma[c] * ((tg_to_float(x[off + c]) - mu) * rs) + beta[c]);
+}
+
+// Backward (_nn.py:921-942), with g = dy*gamma and xhat = (x-mean)*rstd:
+//   dx (+)= rstd * (g - mean(g) - xhat * mean(g*xhat))
+//   dgamma partial = sum_rows dy*xhat, dbeta partial = sum_rows dy
+// Block b walks rows b, b+nblocks, ...; its threads own fixed columns, so the
+// dgamma/dbeta partials stay in registers and are written once per block to
+// part[b][0:cols] and part[nblocks + b][0:cols].
+template <typename T, int TPR, int VPT, bool ACC>
+__global__ __launch_bounds__(kBlock) void k_ln_bwd_reg(
+    const T* __restrict__ x, const float* __restrict__ mean, const float* __restrict__ rstd,
+    const float* __restrict__ gamma, const T* __restrict__ dy, T* __restrict__ dx,
+    float* __restrict__ part, int64_t rows, int cols) {
+  constexpr int V = tg_vec16<T>::N;
+  constexpr int G = kBlock / TPR;
+  __shared__ float red[8];
+  const int t = threadIdx.x % TPR;
+  const int grp = threadIdx.x / TPR;
+  const int nv = cols / V;
+  float gam[VPT][V], pg[VPT][V], pb[VPT][V];
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    const int vi = t + k * TPR;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      gam[k][j] = (vi < nv) ? gamma[vi * V + j] : 0.f;
+      pg[k][j] = 0.f;
+      pb[k][j] = 0.f;
+    }
+  }
+  const float inv_n = 1.0f / (float)cols;
+  // Every group iterates the same number of times so block barriers stay uniform.
+  const int64_t stride = (int64_t)gridDim.x * G;
+  const int64_t iters = (rows + stride - 1) / stride;
+  for (int64_t it = 0; it < iters; ++it) {
+    const int64_t row = it * stride + (int64_t)blockIdx.x * G + grp;
+    const bool live = row < rows;
+    const int64_t off = (live ? row : 0) * (int64_t)cols;
+    const float mu = live ? mean[row] : 0.f;
+    const float rs = live ? rstd[row] : 0.f;
+    float xh[VPT][V], dyv[VPT][V];
+    float sums[2] = {0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+      const int vi = t + k * TPR;
+      if (live && vi < nv) {
+        tg_vec16<T> a = tg_load16(x + off + vi * V);
+        tg_vec16<T> b = tg_load16(dy + off + vi * V);
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          xh[k][j] = (tg_to_float(a.v[j]) - mu) * rs;
+          dyv[k][j] = tg_to_float(b.v[j]);
+          const float g = dyv[k][j] * gam[k][j];
+          sums[0] += g;
+          sums[1] += g * xh[k][j];
+          pg[k][j] += dyv[k][j] * xh[k][j];
+          pb[k][j] += dyv[k][j];
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+          xh[k][j] = 0.f;
+          dyv[k][j] = 0.f;
+        }
+      }
+    }
+    group_sum<TPR, 2>(sums, red);
+    if (live) {
+      const float mg = sums[0] * inv_n, mgx = sums[1] * inv_n;
+#pragma unroll
+      for (int k = 0; k < VPT; ++k) {
+        const int vi = t + k * TPR;
+        if (vi < nv) {
+          tg_vec16<T> o;
+          if (ACC) o = tg_load16(dx + off + vi * V);
+#pragma unroll
+          for (int j = 0; j < V; ++j) {
+            float r = rs * (dyv[k][j] * gam[k][j] - mg - xh[k][j] * mgx);
+            if (ACC) r += tg_to_float(o.v[j]);
+            o.v[j] = tg_from_float<T>(r);
+          }
+          tg_store16(dx + off + vi * V, o);
+        }
+      }
+    }
+  }
+  // Combine the G row groups of this block, then write the block partial.
+  // (G > 1 only when TPR == 64; LDS holds G-1 groups' partials one vector at a time.)
+  __shared__ float xch[2][kBlock / 64 - 1][64 * 8];
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    const int vi = t + k * TPR;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      if (G > 1) {
+        if (grp > 0) {
+          xch[0][grp - 1][t * V + j] = pg[k][j];
+          xch[1][grp - 1][t * V + j] = pb[k][j];
+        }
+      }
+    }
+    if (G > 1) {
+      __syncthreads();
+      if (grp == 0) {
+#pragma unroll
+        for (int j = 0; j < V; ++j)
+#pragma unroll
+          for (int q = 0; q < G - 1; ++q) {
+            pg[k][j] += xch[0][q][t * V + j];
+            pb[k][j] += xch[1][q][t * V + j];
+          }
+      }
+      __syncthreads();
+    }
+    if (grp == 0 && vi < nv) {
+      float* pgo = part + (int64_t)blockIdx.x * cols + vi * V;
+      float* pbo = part + ((int64_t)gridDim.x + blockIdx.x) * cols + vi * V;
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        pgo[j] = pg[k][j];
+        pbo[j] = pb[k][j];
+      }
+    }
+  }
+}
+
+// Generic LayerNorm backward: wavefront per row for dx; dgamma/dbeta partials
+// go through a per-block LDS-free scheme: each block owns a row range and
+// accumulates per-column sums with a column loop after its rows (re-reading them).
+template <typename T, bool ACC>
+__global__ __launch_bounds__(kBlock) void k_ln_bwd_dx_loop(
+    const T* __restrict__ x, const float* __restrict__ mean, const float* __restrict__ rstd,
+    const float* __restrict__ gamma, const T* __restrict__ dy, T* __restrict__ dx, int64_t rows,
+    int64_t cols) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t off = row * cols;
+  const float mu = mean[row], rs = rstd[row];
+  float a = 0.f, b = 0.f;
+  for (int64_t c = lane; c < cols; c += 64) {
+    const float xh = (tg_to_float(x[off + c]) - mu) * rs;
+    const float g = tg_to_float(dy[off + c]) * gamma[c];
+    a += g;
+    b += g * xh;
+  }
+  const float mg = tg_wave_sum(a) / (float)cols, mgx = tg_wave_sum(b) / (float)cols;
+  for (int64_t c = lane; c < cols; c += 64) {
+    const float xh = (tg_to_float(x[off + c]) - mu) * rs;
+    float r = rs * (tg_to_float(dy[off + c]) * gamma[c] - mg - xh * mgx);
+    if (ACC) r += tg_to_float(dx[off + c]);
+    dx[off + c] = tg_from_float<T>(r);
+  }
+}
+
+// dgamma/dbeta partials for the generic path: grid (ceil(cols/256), nsplit);
+// part[split][c] = sum over the split's rows of dy*xhat, part[nsplit+split][c] of dy.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_ln_bwd_param_loop(
+    const T* __restrict__ x, const float* __restrict__ mean, const float* __restrict__ rstd,
+    const T* __restrict__ dy, float* __restrict__ part, int64_t rows, int64_t cols) {
+  const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (c >= cols) return;
+  const int64_t nsplit = gridDim.y;
+  const int64_t per = (rows + nsplit - 1) / nsplit;
+  const int64_t r0 = blockIdx.y * per;
+  const int64_t r1 = r0 + per < rows ? r0 + per : rows;
+  float sg = 0.f, sb = 0.f;
+  for (int64_t r = r0; r < r1; ++r) {
+    const float d = tg_to_float(dy[r * cols + c]);
+    sg += d * (tg_to_float(x[r * cols + c]) - mean[r]) * rstd[r];
+    sb += d;
+  }
+  part[(int64_t)blockIdx.y * cols + c] = sg;
+  part[(nsplit + blockIdx.y) * cols + c] = sb;
+}
+
+// ============================ column sums ==================================
+// Stage 1: part[split][c] = sum over rows in split of in[r][c]   (grid: ctiles x nsplit)
+template <typename TI>
+__global__ __launch_bounds__(kBlock) void k_colsum_partial(const TI* __restrict__ in,
+                                                           float* __restrict__ part, int64_t rows,
+                                                           int64_t cols) {
+  const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (c >= cols) return;
+  const int64_t nsplit = gridDim.y;
+  const int64_t per = (rows + nsplit - 1) / nsplit;
+  const int64_t r0 = blockIdx.y * per;
+  const int64_t r1 = r0 + per < rows ? r0 + per : rows;
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  int64_t r = r0;
+  for (; r + 4 <= r1; r += 4) {
+    s0 += tg_to_float(in[(r + 0) * cols + c]);
+    s1 += tg_to_float(in[(r + 1) * cols + c]);
+    s2 += tg_to_float(in[(r + 2) * cols + c]);
+    s3 += tg_to_float(in[(r + 3) * cols + c]);
+  }
+  for (; r < r1; ++r) s0 += tg_to_float(in[r * cols + c]);
+  part[(int64_t)blockIdx.y * cols + c] = (s0 + s1) + (s2 + s3);
+}
+
+// Stage 2: out[c] (+)= sum_{s < nsplit} part[s][c]   (fixed order: deterministic)
+template <typename TO, bool ACC>
+__global__ __launch_bounds__(kBlock) void k_colsum_final(const float* __restrict__ part,
+                                                         TO* __restrict__ out, int64_t nsplit,
+                                                         int64_t cols) {
+  const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (c >= cols) return;
+  float s = 0.f;
+  for (int64_t k = 0; k < nsplit; ++k) s += part[k * cols + c];
+  if (ACC) s += tg_to_float(out[c]);
+  out[c] = tg_from_float<TO>(s);
+}
+
+template <typename TO>
+int colsum_final(const float* part, void* out, int64_t nsplit, int64_t cols, int acc,
+                 hipStream_t s) {
+  const unsigned blocks = (unsigned)((cols + kBlock - 1) / kBlock);
+  if (acc)
+    k_colsum_final<TO, true><<<blocks, kBlock, 0, s>>>(part, (TO*)out, nsplit, cols);
+  else
+    k_colsum_final<TO, false><<<blocks, kBlock, 0, s>>>(part, (TO*)out, nsplit, cols);
+  return tg_check_launch("column-sum final");
+}
+
+int colsum_final_dt(int dtype, const float* part, void* out, int64_t nsplit, int64_t cols,
+                    int acc, hipStream_t s) {
+  switch (dtype) {
+    case TG_F32: return colsum_final<float>(part, out, nsplit, cols, acc, s);
+    case TG_F16: return colsum_final<tg_half>(part, out, nsplit, cols, acc, s);
+    case TG_BF16: return colsum_final<tg_bf16>(part, out, nsplit, cols, acc, s);
+  }
+  tg_set_error("column-sum: unsupported output dtype %d", dtype);
+  return TG_ERR_UNSUPPORTED;
+}
+
+int64_t colsum_splits(int64_t rows, int64_t cols) {
+  const int64_t ctiles = (cols + kBlock - 1) / kBlock;
+  int64_t want = (4 * (int64_t)tg_num_cus() + ctiles - 1) / ctiles;
+  int64_t maxs = rows / 16;
+  if (want > maxs) want = maxs;
+  if (want > 1024) want = 1024;
+  if (want < 1) want = 1;
+  return want;
+}
+
+// Row-groups per LayerNorm-backward launch (the number of dgamma/dbeta partials).
+int64_t ln_bwd_blocks(int64_t rows, int tpr) {
+  const int64_t g = kBlock / tpr;
+  int64_t want = 2 * (int64_t)tg_num_cus();
+  const int64_t maxb = (rows + g - 1) / g;
+  if (want > maxb) want = maxb;
+  if (want < 1) want = 1;
+  return want;
+}
+
+template <typename T>
+int ln_fwd_t(const void* x, const float* gamma, const float* beta, void* y, float* mean,
+             float* rstd, int64_t rows, int64_t cols, float eps, hipStream_t s) {
+  int tpr = 0, vpt = 0;
+  if (pick_reg_shape<T>(cols, tg_aligned16(x) && tg_aligned16(y), &tpr, &vpt)) {
+    const int64_t g = kBlock / tpr;
+    const unsigned blocks = (unsigned)((rows + g - 1) / g);
+#define L(TPR, VPT)                                                                     \
+  k_ln_fwd_reg<T, TPR, VPT><<<blocks, kBlock, 0, s>>>((const T*)x, gamma, beta, (T*)y, mean, \
+                                                      rstd, rows, (int)cols, eps)
+    TG_REG_DISPATCH(L)
+#undef L
+  } else {
+    k_ln_fwd_loop<T><<<(unsigned)((rows + 3) / 4), kBlock, 0, s>>>(
+        (const T*)x, gamma, beta, (T*)y, mean, rstd, rows, cols, eps);
+  }
+  return tg_check_launch("tg_layernorm_fwd");
+}
+
+struct LnBwdPlan {
+  bool reg;
+  int tpr, vpt;
+  int64_t nparts;  // number of dgamma (and dbeta) partial rows in the workspace
+};
+
+template <typename T>
+LnBwdPlan ln_bwd_plan(int64_t rows, int64_t cols, bool aligned) {
+  LnBwdPlan p{};
+  p.reg = pick_reg_shape<T>(cols, aligned, &p.tpr, &p.vpt);
+  p.nparts = p.reg ? ln_bwd_blocks(rows, p.tpr) : colsum_splits(rows, cols);
+  return p;
+}
+
+LnBwdPlan ln_bwd_plan_dt(int dtype, int64_t rows, int64_t cols, bool aligned) {
+  switch (dtype) {
+    case TG_F16: return ln_bwd_plan<tg_half>(rows, cols, aligned);
+    case TG_BF16: return ln_bwd_plan<tg_bf16>(rows, cols, aligned);
+    default: return ln_bwd_plan<float>(rows, cols, aligned);
+  }
+}
+
+template <typename T>
+int ln_bwd_t(const void* x, const float* mean, const float* rstd, const float* gamma,
+             const void* dy, void* dx, float* dgamma, float* dbeta, int64_t rows, int64_t cols,
+             int acc_dx, int acc_params, float* part, const LnBwdPlan& p, hipStream_t s) {
+  if (p.reg) {
+    const unsigned blocks = (unsigned)p.nparts;
+    const int tpr = p.tpr, vpt = p.vpt;
+    if (acc_dx) {
+#define L(TPR, VPT)                                                                           \
+  k_ln_bwd_reg<T, TPR, VPT, true><<<blocks, kBlock, 0, s>>>((const T*)x, mean, rstd, gamma, \
+                                                            (const T*)dy, (T*)dx, part, rows, \
+                                                            (int)cols)
+      TG_REG_DISPATCH(L)
+#undef L
+    } else {
+#define L(TPR, VPT)                                                                            \
+  k_ln_bwd_reg<T, TPR, VPT, false><<<blocks, kBlock, 0, s>>>((const T*)x, mean, rstd, gamma, \
+                                                             (const T*)dy, (T*)dx, part, rows, \
+                                                             (int)cols)
+      TG_REG_DISPATCH(L)
+#undef L
+    }
+  } else {
+    const unsigned blocks = (unsigned)((rows + 3) / 4);
+    if (acc_dx)
+      k_ln_bwd_dx_loop<T, true><<<blocks, kBlock, 0, s>>>((const T*)x, mean, rstd, gamma,
+                                                          (const T*)dy, (T*)dx, rows, cols);
+    else
+      k_ln_bwd_dx_loop<T, false><<<blocks, kBlock, 0, s>>>((const T*)x, mean, rstd, gamma,
+                                                           (const T*)dy, (T*)dx, rows, cols);
+    dim3 grid((unsigned)((cols + kBlock - 1) / kBlock), (unsigned)p.nparts);
+    k_ln_bwd_param_loop<T><<<grid, kBlock, 0, s>>>((const T*)x, mean, rstd, (const T*)dy, part,
+                                                   rows, cols);
+  }
+  int st = tg_check_launch("tg_layernorm_bwd");
+  if (st) return st;
+  if (dgamma) {
+    st = colsum_final<float>(part, dgamma, p.nparts, cols, acc_params, s);
+    if (st) return st;
+  }
+  if (dbeta) st = colsum_final<float>(part + p.nparts * cols, dbeta, p.nparts, cols, acc_params, s);
+  return st;
+}
+
+}  // namespace
+
+// ============================ exported C-ABI ===============================
+
+TG_EXPORT int tg_softmax_fwd(int dtype, const void* x, void* y, int64_t rows, int64_t cols,
+                             void* stream) {
+  TG_REQUIRE(rows >= 0 && cols >= 0, "tg_softmax_fwd: negative shape");
+  if (rows == 0 || cols == 0) return TG_OK;
+  TG_REQUIRE(x && y, "tg_softmax_fwd: null pointer");
+  hipStream_t s = tg_stream(stream);
+  switch (dtype) {
+    case TG_F32: return softmax_fwd_t<float>(x, y, rows, cols, s);
+    case TG_F16: return softmax_fwd_t<tg_half>(x, y, rows, cols, s);
+    case TG_BF16: return softmax_fwd_t<tg_bf16>(x, y, rows, cols, s);
+  }
+  tg_set_error("tg_softmax_fwd: unsupported dtype %d", dtype);
+  return TG_ERR_UNSUPPORTED;
+}
+
+TG_EXPORT int tg_softmax_bwd(int dtype, const void* y, const void* dy, void* dx, int64_t rows,
+                             int64_t cols, int accumulate, void* stream) {
+  TG_REQUIRE(rows >= 0 && cols >= 0, "tg_softmax_bwd: negative shape");
+  if (rows == 0 || cols == 0) return TG_OK;
+  TG_REQUIRE(y && dy && dx, "tg_softmax_bwd: null pointer");
+  hipStream_t s = tg_stream(stream);
+  switch (dtype) {
+    case TG_F32: return softmax_bwd_t<float>(y, dy, dx, rows, cols, accumulate, s);
+    case TG_F16: return softmax_bwd_t<tg_half>(y, dy, dx, rows, cols, accumulate, s);
+    case TG_BF16: return softmax_bwd_t<tg_bf16>(y, dy, dx, rows, cols, accumulate, s);
+  }
+  tg_set_error("tg_softmax_bwd: unsupported dtype %d", dtype);
+  return TG_ERR_UNSUPPORTED;
+}
+
+TG_EXPORT int tg_layernorm_fwd(int dtype, const void* x, const float* gamma, const float* beta,
+                               void* y, float* mean, float* rstd, int64_t rows, int64_t cols,
+                               float eps, void* stream) {
+  TG_REQUIRE(rows >= 0 && cols > 0, "tg_layernorm_fwd: bad shape");
+  if (rows == 0) return TG_OK;
+  TG_REQUIRE(x && gamma && beta && y && mean && rstd, "tg_layernorm_fwd: null pointer");
+  hipStream_t s = tg_stream(stream);
+  switch (dtype) {
+    case TG_F32: return ln_fwd_t<float>(x, gamma, beta, y, mean, rstd, rows, cols, eps, s);
+    case TG_F16: return ln_fwd_t<tg_half>(x, gamma, beta, y, mean, rstd, rows, cols, eps, s);
+    case TG_BF16: return ln_fwd_t<tg_bf16>(x, gamma, beta, y, mean, rstd, rows, cols, eps, s);
+  }
+  tg_set_error("tg_layernorm_fwd: unsupported dtype %d", dtype);
+  return TG_ERR_UNSUPPORTED;
+}
+
+TG_EXPORT size_t tg_layernorm_bwd_workspace(int dtype, int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  // Alignment unknown at query time: size for the larger of the two plans.
+  LnBwdPlan a = ln_bwd_plan_dt(dtype, rows, cols, true);
+  LnBwdPlan b = ln_bwd_plan_dt(dtype, rows, cols, false);
+  const int64_t np = a.nparts > b.nparts ? a.nparts : b.nparts;
+  return (size_t)(2 * np * cols) * sizeof(float);
+}
+
+TG_EXPORT int tg_layernorm_bwd(int dtype, const void* x, const float* mean, const float* rstd,
+                               const float* gamma, const void* dy, void* dx, float* dgamma,
+                               float* dbeta, int64_t rows, int64_t cols, int accumulate_dx,
+                               int accumulate_params, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  TG_REQUIRE(rows >= 0 && cols > 0, "tg_layernorm_bwd: bad shape");
+  if (rows == 0) return TG_OK;
+  TG_REQUIRE(x && mean && rstd && gamma && dy && dx, "tg_layernorm_bwd: null pointer");
+  const bool al = tg_aligned16(x) && tg_aligned16(dy) && tg_aligned16(dx);
+  LnBwdPlan p = ln_bwd_plan_dt(dtype, rows, cols, al);
+  const size_t need = (size_t)(2 * p.nparts * cols) * sizeof(float);
+  if (!workspace || workspace_bytes < need) {
+    tg_set_error("tg_layernorm_bwd: workspace of %zu bytes needed, got %zu", need,
+                 workspace ? workspace_bytes : (size_t)0);
+    return TG_ERR_WORKSPACE;
+  }
+  hipStream_t s = tg_stream(stream);
+  float* part = (float*)workspace;
+  switch (dtype) {
+    case TG_F32:
+      return ln_bwd_t<float>(x, mean, rstd, gamma, dy, dx, dgamma, dbeta, rows, cols,
+                             accumulate_dx, accumulate_params, part, p, s);
+    case TG_F16:
+      return ln_bwd_t<tg_half>(x, mean, rstd, gamma, dy, dx, dgamma, dbeta, rows, cols,
+                               accumulate_dx, accumulate_params, part, p, s);
+    case TG_BF16:
+      return ln_bwd_t<tg_bf16>(x, mean, rstd, gamma, dy, dx, dgamma, dbeta, rows, cols,
+                               accumulate_dx, accumulate_params, part, p, s);
+  }
+  tg_set_error("tg_layernorm_bwd: unsupported dtype %d", dtype);
+  return TG_ERR_UNSUPPORTED;
+}
+
+TG_EXPORT size_t tg_reduce_rows_workspace(int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  return (size_t)(colsum_splits(rows, cols) * cols) * sizeof(float);
+}
+
+// out[c] (+)= sum_r in[r][c] for a row-major [rows, cols] input: the reduction that
+// unbroadcasts a [.., cols] gradient onto a [cols] parameter (_core.py:1380-1424).
+TG_EXPORT int tg_reduce_rows(int dtype_in, const void* in, int dtype_out, void* out,
+                             int64_t rows, int64_t cols, int accumulate, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  TG_REQUIRE(rows >= 0 && cols >= 0, "tg_reduce_rows: negative shape");
+  if (cols == 0) return TG_OK;
+  TG_REQUIRE(out, "tg_reduce_rows: null output");
+  hipStream_t s = tg_stream(stream);
+  if (rows == 0) {
+    if (accumulate) return TG_OK;
+    // sum over zero rows is zero
+    const int64_t ns = 0;
+    return colsum_final_dt(dtype_out, (const float*)workspace, out, ns, cols, 0, s);
+  }
+  TG_REQUIRE(in, "tg_reduce_rows: null input");
+  const int64_t ns = colsum_splits(rows, cols);
+  const size_t need = (size_t)(ns * cols) * sizeof(float);
+  if (!workspace || workspace_bytes < need) {
+    tg_set_error("tg_reduce_rows: workspace of %zu bytes needed, got %zu", need,
+                 workspace ? workspace_bytes : (size_t)0);
+    return TG_ERR_WORKSPACE;
+  }
+  float* part = (float*)workspace;
+  dim3 grid((unsigned)((cols + kBlock - 1) / kBlock), (unsigned)ns);
+  switch (dtype_in) {
+    case TG_F32: k_colsum_partial<float><<<grid, kBlock, 0, s>>>((const float*)in, part, rows, cols); break;
+    case TG_F16: k_colsum_partial<tg_half><<<grid, kBlock, 0, s>>>((const tg_half*)in, part, rows, cols); break;
+    case TG_BF16: k_colsum_partial<tg_bf16><<<grid, kBlock, 0, s>>>((const tg_bf16*)in, part, rows, cols); break;
+    default:
+      tg_set_error("tg_reduce_rows: unsupported input dtype %d", dtype_in);
+      return TG_ERR_UNSUPPORTED;
+  }
+  int st = tg_check_launch("tg_reduce_rows");
+  if (st) return st;
+  return colsum_final_dt(dtype_out, part, out, ns, cols, accumulate, s);
+}

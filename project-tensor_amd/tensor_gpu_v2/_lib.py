@@ -1,0 +1,519 @@
+"""ctypes binding of libtgbwd.so (the gfx950 kernels) and thin typed wrappers.
+
+Every wrapper takes torch device tensors (torch is used only as the device
+allocator and stream provider), checks shapes/dtypes on the host, passes raw
+pointers and sizes across the C-ABI declared in include/tgbwd.h, and raises
+RuntimeError with the library's message on a non-zero status.
+
+There is no fallback: if the shared library is missing or cannot be loaded,
+every wrapper raises.  Build it with ``python project-tensor_amd/build_lib.py``.
+"""
+import ctypes
+import os
+import threading
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.environ.get("TG_HIP_LIB", os.path.join(_HERE, "libtgbwd.so"))
+
+F32, F16, BF16 = 0, 1, 2
+NHWC, NCHW = 0, 1
+
+_TORCH_TO_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+_f32 = ctypes.c_float
+_sz = ctypes.c_size_t
+
+# name -> (restype, argtypes).  Mirrors include/tgbwd.h one to one.
+SIGNATURES = {
+    "tg_init": (_i32, [_i32]),
+    "tg_last_error": (ctypes.c_char_p, []),
+    "tg_version": (_i32, []),
+    "tg_stream_sync": (_i32, [_vp]),
+    "tg_gelu_bwd": (_i32, [_i32, _vp, _vp, _vp, _i64, _i32, _vp]),
+    "tg_silu_bwd": (_i32, [_i32, _vp, _vp, _vp, _i64, _i32, _vp]),
+    "tg_gelu_fwd": (_i32, [_i32, _vp, _vp, _i64, _vp]),
+    "tg_silu_fwd": (_i32, [_i32, _vp, _vp, _i64, _vp]),
+    "tg_axpby": (_i32, [_i32, _vp, _i32, _vp, _i64, _f32, _f32, _vp]),
+    "tg_fill": (_i32, [_i32, _vp, _i64, _f32, _vp]),
+    "tg_softmax_fwd": (_i32, [_i32, _vp, _vp, _i64, _i64, _vp]),
+    "tg_softmax_bwd": (_i32, [_i32, _vp, _vp, _vp, _i64, _i64, _i32, _vp]),
+    "tg_layernorm_fwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _vp]),
+    "tg_layernorm_bwd_workspace": (_sz, [_i32, _i64, _i64]),
+    "tg_layernorm_bwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
+                                _i32, _i32, _vp, _sz, _vp]),
+    "tg_reduce_rows_workspace": (_sz, [_i64, _i64]),
+    "tg_reduce_rows": (_i32, [_i32, _vp, _i32, _vp, _i64, _i64, _i32, _vp, _sz, _vp]),
+    "tg_batchnorm_workspace": (_sz, [_i32, _i64, _i64, _i64]),
+    "tg_batchnorm_fwd_train": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f32,
+                                      _i64, _i64, _i64, _f32, _i32, _vp, _sz, _vp]),
+    "tg_batchnorm_bwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
+                                _i64, _i32, _i32, _i32, _vp, _sz, _vp]),
+    "tg_adam_step": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _f32, _f32, _f32, _f32, _f32,
+                            _f32, _f32, _vp]),
+    "tg_unscale_check": (_i32, [_i32, _i32, _vp, _vp, _f32, _i32, _vp, _vp]),
+    "tg_grad_norm_workspace": (_sz, [_i32, _vp]),
+    "tg_grad_norm": (_i32, [_i32, _i32, _vp, _vp, _i32, _f32, _vp, _vp, _vp, _sz, _vp]),
+    "tg_zero_nonfinite": (_i32, [_i32, _i32, _vp, _vp, _vp]),
+    "tg_gemm": (_i32, [_i32, _i32, _i32, _i32, _i64, _i64, _i64, _f32, _vp, _i64, _i64, _vp,
+                       _i64, _i64, _f32, _vp, _i64, _i64, _i64, _vp]),
+    "tg_flash_attn_fwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                                 _f32, _i32, _vp]),
+    "tg_flash_attn_bwd_workspace": (_sz, [_i64, _i64, _i64, _i64, _i64]),
+    "tg_flash_attn_bwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
+                                 _i64, _i64, _i64, _f32, _i32, _i32, _vp, _sz, _vp]),
+}
+
+_lib = None
+_lib_lock = threading.Lock()
+_inited = set()
+
+
+def load():
+    """Load libtgbwd.so and bind every exported function (no GPU needed)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lib_lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"libtgbwd.so not found at {LIB_PATH}; build it with "
+                "`python project-tensor_amd/build_lib.py` (no fallback path exists)")
+        lib = ctypes.CDLL(LIB_PATH)
+        missing = []
+        for name, (res, args) in SIGNATURES.items():
+            try:
+                fn = getattr(lib, name)
+            except AttributeError:
+                missing.append(name)
+                continue
+            fn.restype = res
+            fn.argtypes = args
+        if missing:
+            raise RuntimeError(f"{LIB_PATH} lacks exported symbols {missing}; rebuild it")
+        _lib = lib
+    return _lib
+
+
+def last_error():
+    return load().tg_last_error().decode(errors="replace")
+
+
+def _check(name, status):
+    if status != 0:
+        raise RuntimeError(f"{name} failed (status {status}): {last_error()}")
+
+
+def ensure_device(device_index=None):
+    """tg_init once per device (checks the part is gfx950)."""
+    if device_index is None:
+        device_index = torch.cuda.current_device()
+    if device_index not in _inited:
+        _check("tg_init", load().tg_init(int(device_index)))
+        _inited.add(device_index)
+
+
+def stream_handle():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def dtype_code(t):
+    try:
+        return _TORCH_TO_CODE[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype} for the HIP kernels "
+                        "(float32, float16, bfloat16 are supported)") from None
+
+
+def ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _dev(t, name):
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise TypeError(f"{name} must be a torch device tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return t
+
+
+def workspace(nbytes, device):
+    """Caller-owned scratch from torch's caching allocator."""
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def _same(name, *ts):
+    shape, dt = ts[0].shape, ts[0].dtype
+    for t in ts[1:]:
+        if t.shape != shape or t.dtype != dt:
+            raise ValueError(f"{name}: operands must share shape and dtype, got "
+                             f"{[tuple(x.shape) for x in ts]} / {[x.dtype for x in ts]}")
+
+
+# ---------------------------------------------------------------- elementwise
+def act_bwd(kind, x, dy, dx, accumulate):
+    """dx (+)= dy * act'(x) for kind in {'gelu', 'silu'}."""
+    for n, t in (("x", x), ("dy", dy), ("dx", dx)):
+        _dev(t, n)
+    _same(f"{kind}_bwd", x, dy, dx)
+    ensure_device(x.device.index)
+    fn = load().tg_gelu_bwd if kind == "gelu" else load().tg_silu_bwd
+    _check(f"tg_{kind}_bwd", fn(dtype_code(x), ptr(x), ptr(dy), ptr(dx), x.numel(),
+                                int(bool(accumulate)), stream_handle()))
+    return dx
+
+
+def act_fwd(kind, x, y=None):
+    _dev(x, "x")
+    if y is None:
+        y = torch.empty_like(x)
+    _same(f"{kind}_fwd", x, y)
+    ensure_device(x.device.index)
+    fn = load().tg_gelu_fwd if kind == "gelu" else load().tg_silu_fwd
+    _check(f"tg_{kind}_fwd", fn(dtype_code(x), ptr(x), ptr(y), x.numel(), stream_handle()))
+    return y
+
+
+def axpby(x, y, alpha=1.0, beta=1.0):
+    """y = alpha*x + beta*y in place (x, y contiguous, same numel; dtypes may differ)."""
+    _dev(x, "x")
+    _dev(y, "y")
+    if x.numel() != y.numel():
+        raise ValueError(f"axpby: numel mismatch {x.numel()} vs {y.numel()}")
+    ensure_device(y.device.index)
+    _check("tg_axpby", load().tg_axpby(dtype_code(x), ptr(x), dtype_code(y), ptr(y), y.numel(),
+                                       float(alpha), float(beta), stream_handle()))
+    return y
+
+
+def fill(y, value):
+    _dev(y, "y")
+    ensure_device(y.device.index)
+    _check("tg_fill", load().tg_fill(dtype_code(y), ptr(y), y.numel(), float(value),
+                                     stream_handle()))
+    return y
+
+
+# ---------------------------------------------------------------- row-wise
+def _rows_cols(t):
+    cols = t.shape[-1] if t.dim() > 0 else 1
+    rows = t.numel() // cols if cols else 0
+    return rows, cols
+
+
+def softmax_fwd(x, y=None):
+    _dev(x, "x")
+    if y is None:
+        y = torch.empty_like(x)
+    _same("softmax_fwd", x, y)
+    rows, cols = _rows_cols(x)
+    ensure_device(x.device.index)
+    _check("tg_softmax_fwd", load().tg_softmax_fwd(dtype_code(x), ptr(x), ptr(y), rows, cols,
+                                                   stream_handle()))
+    return y
+
+
+def softmax_bwd(y, dy, dx, accumulate):
+    for n, t in (("y", y), ("dy", dy), ("dx", dx)):
+        _dev(t, n)
+    _same("softmax_bwd", y, dy, dx)
+    rows, cols = _rows_cols(y)
+    ensure_device(y.device.index)
+    _check("tg_softmax_bwd", load().tg_softmax_bwd(dtype_code(y), ptr(y), ptr(dy), ptr(dx), rows,
+                                                   cols, int(bool(accumulate)), stream_handle()))
+    return dx
+
+
+def layernorm_fwd(x, gamma, beta, eps, y=None, mean=None, rstd=None):
+    _dev(x, "x")
+    cols = gamma.numel()
+    rows = x.numel() // cols
+    if y is None:
+        y = torch.empty_like(x)
+    if mean is None:
+        mean = torch.empty(rows, dtype=torch.float32, device=x.device)
+    if rstd is None:
+        rstd = torch.empty(rows, dtype=torch.float32, device=x.device)
+    for n, t in (("gamma", gamma), ("beta", beta), ("mean", mean), ("rstd", rstd)):
+        _dev(t, n)
+        if t.dtype != torch.float32:
+            raise TypeError(f"layernorm_fwd: {n} must be float32")
+    ensure_device(x.device.index)
+    _check("tg_layernorm_fwd", load().tg_layernorm_fwd(
+        dtype_code(x), ptr(x), ptr(gamma), ptr(beta), ptr(y), ptr(mean), ptr(rstd), rows, cols,
+        float(eps), stream_handle()))
+    return y, mean, rstd
+
+
+def layernorm_bwd(x, mean, rstd, gamma, dy, dx, dgamma, dbeta, accumulate_dx,
+                  accumulate_params):
+    for n, t in (("x", x), ("dy", dy), ("dx", dx), ("mean", mean), ("rstd", rstd),
+                 ("gamma", gamma)):
+        _dev(t, n)
+    _same("layernorm_bwd", x, dy, dx)
+    cols = gamma.numel()
+    rows = x.numel() // cols
+    lib = load()
+    ensure_device(x.device.index)
+    code = dtype_code(x)
+    nbytes = lib.tg_layernorm_bwd_workspace(code, rows, cols)
+    ws = workspace(nbytes, x.device)
+    _check("tg_layernorm_bwd", lib.tg_layernorm_bwd(
+        code, ptr(x), ptr(mean), ptr(rstd), ptr(gamma), ptr(dy), ptr(dx), ptr(dgamma),
+        ptr(dbeta), rows, cols, int(bool(accumulate_dx)), int(bool(accumulate_params)), ptr(ws),
+        ws.numel(), stream_handle()))
+    return dx
+
+
+def reduce_rows(g, out, accumulate):
+    """out (+)= g.reshape(-1, out.numel()).sum(0)."""
+    _dev(g, "g")
+    _dev(out, "out")
+    cols = out.numel()
+    rows = g.numel() // cols if cols else 0
+    if rows * cols != g.numel():
+        raise ValueError("reduce_rows: grad numel is not a multiple of the target numel")
+    lib = load()
+    ensure_device(out.device.index)
+    ws = workspace(lib.tg_reduce_rows_workspace(rows, cols), out.device)
+    _check("tg_reduce_rows", lib.tg_reduce_rows(dtype_code(g), ptr(g), dtype_code(out), ptr(out),
+                                                rows, cols, int(bool(accumulate)), ptr(ws),
+                                                ws.numel(), stream_handle()))
+    return out
+
+
+# ---------------------------------------------------------------- batch norm
+def _bn_shape(x, layout):
+    if x.dim() != 4:
+        raise ValueError(f"batch norm expects a 4-D input, got {tuple(x.shape)}")
+    if layout == NHWC:
+        N, H, W, C = x.shape
+    else:
+        N, C, H, W = x.shape
+    return N, C, H * W
+
+
+def batchnorm_fwd_train(x, gamma, beta, eps, momentum, running_mean, running_var, relu,
+                        layout=NHWC):
+    _dev(x, "x")
+    if x.dtype != torch.float32:
+        raise TypeError("batch norm kernels are fp32")
+    N, C, HW = _bn_shape(x, layout)
+    y = torch.empty_like(x)
+    mean = torch.empty(C, dtype=torch.float32, device=x.device)
+    rstd = torch.empty_like(mean)
+    var = torch.empty_like(mean)
+    lib = load()
+    ensure_device(x.device.index)
+    ws = workspace(lib.tg_batchnorm_workspace(layout, N, C, HW), x.device)
+    _check("tg_batchnorm_fwd_train", lib.tg_batchnorm_fwd_train(
+        layout, ptr(x), ptr(gamma), ptr(beta), ptr(y), ptr(mean), ptr(rstd), ptr(var),
+        ptr(running_mean), ptr(running_var), float(momentum), N, C, HW, float(eps),
+        int(bool(relu)), ptr(ws), ws.numel(), stream_handle()))
+    return y, mean, rstd, var
+
+
+def batchnorm_bwd(x, mean, rstd, gamma, beta, dy, dx, dgamma, dbeta, relu, accumulate_dx,
+                  accumulate_params, layout=NHWC):
+    for n, t in (("x", x), ("dy", dy), ("dx", dx)):
+        _dev(t, n)
+    _same("batchnorm_bwd", x, dy, dx)
+    N, C, HW = _bn_shape(x, layout)
+    lib = load()
+    ensure_device(x.device.index)
+    ws = workspace(lib.tg_batchnorm_workspace(layout, N, C, HW), x.device)
+    _check("tg_batchnorm_bwd", lib.tg_batchnorm_bwd(
+        layout, ptr(x), ptr(mean), ptr(rstd), ptr(gamma), ptr(beta), ptr(dy), ptr(dx),
+        ptr(dgamma), ptr(dbeta), N, C, HW, int(bool(relu)), int(bool(accumulate_dx)),
+        int(bool(accumulate_params)), ptr(ws), ws.numel(), stream_handle()))
+    return dx
+
+
+# ---------------------------------------------------------------- multi-tensor
+def _ptr_array(ts):
+    arr = (ctypes.c_void_p * len(ts))()
+    for i, t in enumerate(ts):
+        arr[i] = t.data_ptr() if t is not None else 0
+    return arr
+
+
+def _numel_array(ts):
+    arr = (ctypes.c_int64 * len(ts))()
+    for i, t in enumerate(ts):
+        arr[i] = t.numel()
+    return arr
+
+
+def adam_step(params, grads, exp_avg, exp_avg_sq, max_exp_avg_sq, lr, beta1, beta2, eps,
+              weight_decay, bias_correction1, bias_correction2):
+    n = len(params)
+    if n == 0:
+        return
+    for group in (params, grads, exp_avg, exp_avg_sq) + ((max_exp_avg_sq,) if max_exp_avg_sq else ()):
+        for t in group:
+            _dev(t, "adam operand")
+            if t.dtype != torch.float32:
+                raise TypeError("adam_step: fp32 tensors required")
+    for p, g, m, v in zip(params, grads, exp_avg, exp_avg_sq):
+        if not (p.numel() == g.numel() == m.numel() == v.numel()):
+            raise ValueError("adam_step: param/grad/state sizes differ")
+    ensure_device(params[0].device.index)
+    _check("tg_adam_step", load().tg_adam_step(
+        n, _ptr_array(params), _ptr_array(grads), _ptr_array(exp_avg), _ptr_array(exp_avg_sq),
+        _ptr_array(max_exp_avg_sq) if max_exp_avg_sq else None, _numel_array(params),
+        float(lr), float(beta1), float(beta2), float(eps), float(weight_decay),
+        float(bias_correction1), float(bias_correction2), stream_handle()))
+
+
+def _group_by_dtype(ts):
+    groups = {}
+    for i, t in enumerate(ts):
+        groups.setdefault(t.dtype, []).append(i)
+    return groups
+
+
+def unscale_check(grads, mul, write=True):
+    """Scale grads in place by `mul`; return per-tensor flags (host list of ints):
+    bit 0 = non-finite before scaling, bit 1 = non-finite after."""
+    n = len(grads)
+    if n == 0:
+        return []
+    for t in grads:
+        _dev(t, "grad")
+    dev = grads[0].device
+    ensure_device(dev.index)
+    flags = torch.empty(n, dtype=torch.int32, device=dev)
+    out = [0] * n
+    lib = load()
+    groups = _group_by_dtype(grads)
+    for dt, idx in groups.items():
+        sub = [grads[i] for i in idx]
+        fl = flags[: len(sub)] if len(groups) == 1 else torch.empty(len(sub), dtype=torch.int32,
+                                                                    device=dev)
+        _check("tg_unscale_check", lib.tg_unscale_check(
+            len(sub), dtype_code(sub[0]), _ptr_array(sub), _numel_array(sub), float(mul),
+            int(bool(write)), ptr(fl), stream_handle()))
+        host = fl.cpu().tolist()
+        for j, i in enumerate(idx):
+            out[i] = host[j]
+    return out
+
+
+def grad_norm(grads, norm_kind, p=2.0):
+    """Return (value, flags): value = sum g^2 (kind 0), max|g| (1) or sum|g|^p (2)
+    over finite entries, as a Python float; flags[i] bit 0 = tensor i non-finite."""
+    n = len(grads)
+    if n == 0:
+        return 0.0, []
+    for t in grads:
+        _dev(t, "grad")
+    dev = grads[0].device
+    ensure_device(dev.index)
+    lib = load()
+    total = 0.0
+    flags_out = [0] * n
+    for dt, idx in _group_by_dtype(grads).items():
+        sub = [grads[i] for i in idx]
+        numel = _numel_array(sub)
+        ws = workspace(lib.tg_grad_norm_workspace(len(sub), numel), dev)
+        out = torch.empty(1, dtype=torch.float64, device=dev)
+        fl = torch.empty(len(sub), dtype=torch.int32, device=dev)
+        _check("tg_grad_norm", lib.tg_grad_norm(
+            len(sub), dtype_code(sub[0]), _ptr_array(sub), numel, int(norm_kind), float(p),
+            ptr(out), ptr(fl), ptr(ws), ws.numel(), stream_handle()))
+        v = float(out.cpu()[0])
+        total = max(total, v) if norm_kind == 1 else total + v
+        for j, f in enumerate(fl.cpu().tolist()):
+            flags_out[idx[j]] = f
+    return total, flags_out
+
+
+def zero_nonfinite(grads):
+    if not grads:
+        return
+    lib = load()
+    ensure_device(grads[0].device.index)
+    for dt, idx in _group_by_dtype(grads).items():
+        sub = [grads[i] for i in idx]
+        _check("tg_zero_nonfinite", lib.tg_zero_nonfinite(
+            len(sub), dtype_code(sub[0]), _ptr_array(sub), _numel_array(sub), stream_handle()))
+
+
+def scale_(grads, mul):
+    """g *= mul for every tensor (no checks needed by the caller)."""
+    if grads:
+        unscale_check(grads, mul, write=True)
+
+
+# ---------------------------------------------------------------- GEMM
+def gemm(a, b, c, trans_a=False, trans_b=False, alpha=1.0, beta=0.0, M=None, N=None, K=None,
+         lda=None, ldb=None, ldc=None, stride_a=0, stride_b=0, stride_c=0, batch=1):
+    """Row-major batched GEMM on raw contiguous buffers; see include/tgbwd.h."""
+    lib = load()
+    ensure_device(c.device.index)
+    if a.dtype != b.dtype:
+        raise TypeError(f"gemm: A and B dtypes differ ({a.dtype} vs {b.dtype})")
+    if c.dtype not in (torch.float32, a.dtype):
+        raise TypeError(f"gemm: C must be float32 or {a.dtype}, got {c.dtype}")
+    _check("tg_gemm", lib.tg_gemm(
+        dtype_code(a), dtype_code(c), int(bool(trans_a)), int(bool(trans_b)), M, N, K,
+        float(alpha), ptr(a), lda, stride_a, ptr(b), ldb, stride_b, float(beta), ptr(c), ldc,
+        stride_c, batch, stream_handle()))
+    return c
+
+
+def matmul2d(a, b, out=None, trans_a=False, trans_b=False, alpha=1.0, beta=0.0, out_dtype=None):
+    """out (= or +=) op(a) @ op(b) for 2-D contiguous a, b."""
+    _dev(a, "a")
+    _dev(b, "b")
+    M = a.shape[1] if trans_a else a.shape[0]
+    K = a.shape[0] if trans_a else a.shape[1]
+    Kb = b.shape[1] if trans_b else b.shape[0]
+    N = b.shape[0] if trans_b else b.shape[1]
+    if K != Kb:
+        raise ValueError(f"matmul2d: inner dims differ ({K} vs {Kb})")
+    if out is None:
+        out = torch.empty(M, N, dtype=out_dtype or a.dtype, device=a.device)
+        beta = 0.0
+    _dev(out, "out")
+    if tuple(out.shape) != (M, N):
+        raise ValueError(f"matmul2d: out shape {tuple(out.shape)} != {(M, N)}")
+    return gemm(a, b, out, trans_a, trans_b, alpha, beta, M, N, K, a.shape[1], b.shape[1], N)
+
+
+# ---------------------------------------------------------------- attention
+def flash_attn_fwd(q, k, v, scale, causal):
+    for n, t in (("q", q), ("k", k), ("v", v)):
+        _dev(t, n)
+    B, H, Sq, D = q.shape
+    Sk = k.shape[2]
+    if k.shape != (B, H, Sk, D) or v.shape != (B, H, Sk, D):
+        raise ValueError(f"flash_attn: k/v shape mismatch {tuple(k.shape)} {tuple(v.shape)}")
+    o = torch.empty_like(q)
+    lse = torch.empty(B, H, Sq, dtype=torch.float32, device=q.device)
+    ensure_device(q.device.index)
+    _check("tg_flash_attn_fwd", load().tg_flash_attn_fwd(
+        dtype_code(q), ptr(q), ptr(k), ptr(v), ptr(o), ptr(lse), B, H, Sq, Sk, D, float(scale),
+        int(bool(causal)), stream_handle()))
+    return o, lse
+
+
+def flash_attn_bwd(q, k, v, o, do, lse, dq, dk, dv, scale, causal, accumulate):
+    for n, t in (("q", q), ("k", k), ("v", v), ("o", o), ("do", do), ("lse", lse), ("dq", dq),
+                 ("dk", dk), ("dv", dv)):
+        _dev(t, n)
+    B, H, Sq, D = q.shape
+    Sk = k.shape[2]
+    lib = load()
+    ensure_device(q.device.index)
+    ws = workspace(lib.tg_flash_attn_bwd_workspace(B, H, Sq, Sk, D), q.device)
+    _check("tg_flash_attn_bwd", lib.tg_flash_attn_bwd(
+        dtype_code(q), ptr(q), ptr(k), ptr(v), ptr(o), ptr(do), ptr(lse), ptr(dq), ptr(dk),
+        ptr(dv), B, H, Sq, Sk, D, float(scale), int(bool(causal)), int(bool(accumulate)),
+        ptr(ws), ws.numel(), stream_handle()))
