@@ -1,0 +1,353 @@
+"""Benchmark of the tensor_gpu_v2 backward engine on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only NAMES]
+
+Headline workload: one "step" = GELU backward and SiLU
+backward on fp32 [8192, 8192], softmax backward on fp32 [16384, 4096] and
+LayerNorm backward on fp32 [16384, 4096] (x, dy ~ N(0,1); softmax logits
+~ N(0, 2); gamma ~ N(1, .02)), inputs resident in HBM.  `value` is the step's
+algorithmic HBM bytes (read every input once, write every output once: 12 B per
+element for each of the four) divided by the step's wall time: GB/s.
+
+Per-kernel durations come from HIP events recorded on the stream the kernels
+run on (torch's current stream, which every libtgbwd launch uses), around each
+launch inside the timed region.  Other configurations (BatchNorm-ReLU NHWC,
+AdamW, GradScaler unscale, the C5 GEMMs, FlashAttention backward, the GPT step)
+are reported under "components" with their own roofline fractions.
+
+The CPU baseline times the NumPy oracle (the reference's CPU algorithm) on a
+row sample of the same workload, single-threaded elementwise NumPy.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "project-tensor_amd"))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2500.0
+
+
+def _args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-components", action="store_true")
+    ap.add_argument("--only", default="", help="comma list of component names")
+    return ap.parse_args()
+
+
+class Timed:
+    """A named launch sequence with its algorithmic byte/flop count, timed by HIP
+    events on the current stream."""
+
+    def __init__(self, name, fn, work, unit, peak):
+        self.name, self.fn, self.work, self.unit, self.peak = name, fn, work, unit, peak
+        self.ms = []
+
+    def run(self, record):
+        import torch
+        if record:
+            s = torch.cuda.Event(enable_timing=True)
+            e = torch.cuda.Event(enable_timing=True)
+            s.record()
+            self.fn()
+            e.record()
+            self.ms.append((s, e))
+        else:
+            self.fn()
+
+    def avg_ms(self):
+        return sum(s.elapsed_time(e) for s, e in self.ms) / max(1, len(self.ms))
+
+    def summary(self):
+        ms = self.avg_ms()
+        if self.unit == "GB/s":
+            ach = self.work / (ms * 1e-3) / 1e9
+        else:
+            ach = self.work / (ms * 1e-3) / 1e12
+        return {"ms": round(ms, 5), "achieved": round(ach, 2), "unit": self.unit,
+                "peak": self.peak, "frac": round(ach / self.peak, 4), "work": self.work}
+
+
+def c2_ops(torch, L):
+    """The headline step's four backward ops on inputs resident in HBM."""
+    g = torch.Generator(device="cuda").manual_seed(0)
+    dev = "cuda"
+    n = 8192 * 8192
+    x = torch.randn(8192, 8192, device=dev, generator=g)
+    dy = torch.randn(8192, 8192, device=dev, generator=g)
+    dx = torch.empty_like(x)
+    logits = torch.randn(16384, 4096, device=dev, generator=g) * 2
+    y = torch.softmax(logits, -1)
+    dys = torch.randn(16384, 4096, device=dev, generator=g)
+    dxs = torch.empty_like(y)
+    xl = torch.randn(16384, 4096, device=dev, generator=g)
+    gam = 1 + 0.02 * torch.randn(4096, device=dev, generator=g)
+    bet = 0.02 * torch.randn(4096, device=dev, generator=g)
+    _, mean, rstd = L.layernorm_fwd(xl, gam, bet, 1e-5)
+    dyl = torch.randn(16384, 4096, device=dev, generator=g)
+    dxl = torch.empty_like(xl)
+    dgam = torch.empty_like(gam)
+    dbet = torch.empty_like(bet)
+    lib = L.load()
+    ws_ln = L.workspace(lib.tg_layernorm_bwd_workspace(0, 16384, 4096), dev)
+    s = L.stream_handle
+    p = L.ptr
+
+    def gelu():
+        L._check("gelu", lib.tg_gelu_bwd(0, p(x), p(dy), p(dx), n, 0, s()))
+
+    def silu():
+        L._check("silu", lib.tg_silu_bwd(0, p(x), p(dy), p(dx), n, 0, s()))
+
+    def softmax():
+        L._check("softmax", lib.tg_softmax_bwd(0, p(y), p(dys), p(dxs), 16384, 4096, 0, s()))
+
+    def layernorm():
+        L._check("ln", lib.tg_layernorm_bwd(0, p(xl), p(mean), p(rstd), p(gam), p(dyl), p(dxl),
+                                            p(dgam), p(dbet), 16384, 4096, 0, 0, p(ws_ln),
+                                            ws_ln.numel(), s()))
+
+    for t in (x, dy, dx):
+        _need(t, n, "act")
+    for t in (y, dys, dxs, xl, dyl, dxl):
+        _need(t, 16384 * 4096, "row op")
+    b = 12 * n
+    return [Timed("gelu_bwd", gelu, b, "GB/s", HBM_PEAK_GBS),
+            Timed("silu_bwd", silu, b, "GB/s", HBM_PEAK_GBS),
+            Timed("softmax_bwd", softmax, 12 * 16384 * 4096, "GB/s", HBM_PEAK_GBS),
+            Timed("layernorm_bwd", layernorm, 12 * 16384 * 4096 + 4 * (2 * 16384 + 3 * 4096),
+                  "GB/s", HBM_PEAK_GBS)]
+
+
+def _need(t, numel, what):
+    """Host-side check that a raw launch's extent fits the buffer it touches."""
+    if t.numel() < numel:
+        raise ValueError(f"{what}: buffer of {t.numel()} elements, launch needs {numel}")
+
+
+def _op_bn(torch, L, g):
+    """C3: FusedBatchNormReLU backward, NHWC [64, 56, 56, 256]; 20 B/elem (x and dy read
+    twice, dx written once)."""
+    lib, s, p = L.load(), L.stream_handle, L.ptr
+    N, H, W, C = 64, 56, 56, 256
+    x = torch.randn(N, H, W, C, device="cuda", generator=g)
+    gam = 1 + 0.1 * torch.randn(C, device="cuda", generator=g)
+    bet = 0.1 * torch.randn(C, device="cuda", generator=g)
+    rm, rv = torch.zeros(C, device="cuda"), torch.ones(C, device="cuda")
+    _, mean, rstd, _ = L.batchnorm_fwd_train(x, gam, bet, 1e-5, 0.1, rm, rv, True, L.NHWC)
+    dy = torch.randn_like(x)
+    dx = torch.empty_like(x)
+    dg, db = torch.empty_like(gam), torch.empty_like(bet)
+    ws = L.workspace(lib.tg_batchnorm_workspace(0, N, C, H * W), "cuda")
+    for t in (x, dy, dx):
+        _need(t, N * H * W * C, "bn")
+
+    def run():
+        L._check("bn", lib.tg_batchnorm_bwd(0, p(x), p(mean), p(rstd), p(gam), p(bet), p(dy),
+                                            p(dx), p(dg), p(db), N, C, H * W, 1, 0, 0, p(ws),
+                                            ws.numel(), s()))
+    return Timed("bn_relu_bwd_nhwc", run, 20 * x.numel(), "GB/s", HBM_PEAK_GBS)
+
+
+NPARAM = 83_200_000
+
+
+def _op_adam(torch, L, g):
+    """C5-sized AdamW over 48 fp32 tensors totalling 83.2M params: 28 B/param."""
+    sizes = [NPARAM // 48] * 47 + [NPARAM - 47 * (NPARAM // 48)]
+    ps = [torch.randn(n, device="cuda", generator=g) for n in sizes]
+    gs = [torch.randn(n, device="cuda", generator=g) * 1e-3 for n in sizes]
+    ms = [torch.zeros(n, device="cuda") for n in sizes]
+    vs = [torch.zeros(n, device="cuda") for n in sizes]
+
+    def run():
+        L.adam_step(ps, gs, ms, vs, None, 3e-4, 0.9, 0.999, 1e-8, 0.1, 0.1, 0.001)
+    return Timed("adamw_step", run, 28 * NPARAM, "GB/s", HBM_PEAK_GBS)
+
+
+def _op_unscale(torch, L, g):
+    """GradScaler unscale + non-finite check over 83.2M fp32 grads: 8 B/param."""
+    lib, s, p = L.load(), L.stream_handle, L.ptr
+    sizes = [NPARAM // 48] * 48
+    gs = [torch.randn(n, device="cuda", generator=g) for n in sizes]
+    flags = torch.empty(len(gs), dtype=torch.int32, device="cuda")
+    arr, num = L._ptr_array(gs), L._numel_array(gs)
+
+    def run():
+        L._check("unscale", lib.tg_unscale_check(len(gs), 0, arr, num, 1.0, 1, p(flags), s()))
+    return Timed("unscale_check", run, 8 * sum(sizes), "GB/s", HBM_PEAK_GBS)
+
+
+def _op_gemm(torch, L, g):
+    """C5 FC1 backward (8192 tokens, 1024 -> 4096), fp16 in, fp32 accumulate:
+    dA = dC W^T and dW = A^T dC, 4*M*N*K flops."""
+    M, K, N = 8192, 1024, 4096
+    a = torch.randn(M, K, device="cuda", generator=g).half()
+    w = torch.randn(K, N, device="cuda", generator=g).half()
+    dc = torch.randn(M, N, device="cuda", generator=g).half()
+    da = torch.empty(M, K, device="cuda", dtype=torch.float16)
+    dw = torch.empty(K, N, device="cuda", dtype=torch.float32)
+
+    def run():
+        L.matmul2d(dc, w, out=da, trans_b=True)
+        L.matmul2d(a, dc, out=dw, trans_a=True)
+    return Timed("gemm_fc1_bwd", run, 4 * M * N * K, "TFLOP/s", FP16_PEAK_TFLOPS)
+
+
+def _op_flash(torch, L, g, d, causal):
+    """C4: FlashAttention backward, B=8, H=16, S=2048, fp16; 10*B*H*S^2*d flops
+    (halved when causal)."""
+    B, H, S = 8, 16, 2048
+    q, k, v, do = (torch.randn(B, H, S, d, device="cuda", generator=g).half() for _ in range(4))
+    o, lse = L.flash_attn_fwd(q, k, v, d ** -0.5, causal)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+
+    def run():
+        L.flash_attn_bwd(q, k, v, o, do, lse, dq, dk, dv, d ** -0.5, causal, False)
+    flops = 10 * B * H * S * S * d // (2 if causal else 1)
+    return Timed(f"flash_bwd_d{d}{'_causal' if causal else ''}", run, flops, "TFLOP/s",
+                 FP16_PEAK_TFLOPS)
+
+
+def component_ops(torch, L, only):
+    """Other configurations, each built in its own scope on HBM-resident inputs."""
+    g = torch.Generator(device="cuda").manual_seed(1)
+    builders = [("bn_relu_bwd_nhwc", lambda: _op_bn(torch, L, g)),
+                ("adamw_step", lambda: _op_adam(torch, L, g)),
+                ("unscale_check", lambda: _op_unscale(torch, L, g)),
+                ("gemm_fc1_bwd", lambda: _op_gemm(torch, L, g))]
+    for d in (64, 128):
+        for causal in (False, True):
+            builders.append((f"flash_bwd_d{d}{'_causal' if causal else ''}",
+                             lambda d=d, causal=causal: _op_flash(torch, L, g, d, causal)))
+    for name, build in builders:
+        if only and name not in only:
+            continue
+        try:
+            op = build()
+        except RuntimeError as e:
+            if "not implemented" in str(e):
+                continue
+            raise
+        yield op
+
+
+def cpu_baseline():
+    """Oracle (NumPy, reference CPU algorithm, fp32) on a row sample of the C2 step."""
+    import numpy as np
+
+    import oracle as O
+    rng = np.random.default_rng(0)
+    rows_ew, rows_rw = 512, 1024
+    x = rng.standard_normal((rows_ew, 8192)).astype(np.float32)
+    dy = rng.standard_normal((rows_ew, 8192)).astype(np.float32)
+    lg = (rng.standard_normal((rows_rw, 4096)) * 2).astype(np.float32)
+    y = O.softmax_fwd(lg)
+    dys = rng.standard_normal((rows_rw, 4096)).astype(np.float32)
+    xl = rng.standard_normal((rows_rw, 4096)).astype(np.float32)
+    g = (1 + 0.02 * rng.standard_normal(4096)).astype(np.float32)
+    b = (0.02 * rng.standard_normal(4096)).astype(np.float32)
+    _, xh, _, var = O.layernorm_fwd(xl, g, b)
+    dyl = rng.standard_normal((rows_rw, 4096)).astype(np.float32)
+    nbytes = 2 * 12 * x.size + 2 * 12 * y.size
+    t_end = time.perf_counter() + 10.0
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        O.gelu_bwd(x, dy)
+        O.silu_bwd(x, dy)
+        O.softmax_bwd(y, dys)
+        O.layernorm_bwd(xh, var, g, dyl)
+        reps += 1
+        if time.perf_counter() > t_end and reps >= 2:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": round(nbytes * reps / dt / 1e9, 3), "unit": "GB/s", "cores": 1,
+            "kind": "port",
+            "sample": (f"oracle (NumPy fp32) GELU+SiLU bwd on [{rows_ew},8192], softmax+LayerNorm "
+                       f"bwd on [{rows_rw},4096]; {reps} reps in {dt:.1f}s, single thread")}
+
+
+def main():
+    a = _args()
+    if a.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                                   "(multi-GPU sharding is a design note, not measured)"}))
+        sys.exit(2)
+    import torch
+
+    from tensor_gpu_v2 import _lib as L
+
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a GPU")
+    L.ensure_device(0)
+    ops = c2_ops(torch, L)
+    for _ in range(a.warmup):
+        for op in ops:
+            op.run(False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        for op in ops:
+            op.run(True)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    step_bytes = sum(op.work for op in ops)
+    ms_step = wall / a.steps * 1e3
+    value = step_bytes / (wall / a.steps) / 1e9
+    per = {op.name: op.summary() for op in ops}
+    dom = max(ops, key=lambda o: o.avg_ms())
+    ds = dom.summary()
+    del ops
+    torch.cuda.empty_cache()
+
+    comps = {}
+    if not a.no_components:
+        only = set(x for x in a.only.split(",") if x)
+        for op in component_ops(torch, L, only):
+            for _ in range(max(1, a.warmup)):
+                op.run(False)
+            torch.cuda.synchronize()
+            for _ in range(max(3, a.steps // 2)):
+                op.run(True)
+            torch.cuda.synchronize()
+            comps[op.name] = op.summary()
+            del op
+            torch.cuda.empty_cache()
+
+    rec = {
+        "metric": "fused-grad-kernel HBM GB/s (% peak); FlashAttention bwd TFLOP/s; step ms",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded N(0,1) inputs of the configured shapes, resident in HBM)",
+        "config": {"workload": "C2: GELU+SiLU bwd fp32 [8192,8192], softmax+LayerNorm bwd fp32 "
+                               "[16384,4096]", "step_bytes": step_bytes},
+        "roofline": {"bound": "hbm", "kernel": dom.name, "achieved": ds["achieved"],
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": ds["frac"],
+                     "traffic": None},
+        "kernels": per,
+        "components": comps,
+    }
+    if not a.no_cpu:
+        rec["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(rec))
+
+
+if __name__ == "__main__":
+    main()

@@ -109,11 +109,12 @@ int tg_batchnorm_bwd(int layout, const float* x, const float* mean, const float*
  * fused_adam_step _training.py:2198-2220, launch _training.py:2250-2268):
  * decoupled decay p -= lr*wd*p first, then the moment updates and
  * p -= lr*(m/bc1)/(sqrt(v/bc2)+eps).  max_exp_avg_sq != NULL selects AMSGrad
- * (_nn.py:1436-1438). */
+ * (_nn.py:1436-1438).  Hyper-parameters are doubles (Python floats in the
+ * reference) combined in double and rounded once to fp32. */
 int tg_adam_step(int ntensors, float* const* params, const float* const* grads,
                  float* const* exp_avg, float* const* exp_avg_sq, float* const* max_exp_avg_sq,
-                 const int64_t* numel, float lr, float beta1, float beta2, float eps,
-                 float weight_decay, float bias_correction1, float bias_correction2,
+                 const int64_t* numel, double lr, double beta1, double beta2, double eps,
+                 double weight_decay, double bias_correction1, double bias_correction2,
                  void* stream);
 /* GradScaler.unscale_ (_nn.py:1795-1833): g *= mul (if write); flags[i] (device,
  * cleared first) |= 1 if tensor i had a non-finite value, |= 2 if the scaled

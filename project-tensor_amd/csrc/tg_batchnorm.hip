@@ -109,7 +109,7 @@ __global__ __launch_bounds__(kBlock) void k_nhwc_reduce(
       for (int j = 0; j < V; ++j) {
         const float t = (red[0][s][lane * V + j] + red[1][s][lane * V + j]) +
                         (red[2][s][lane * V + j] + red[3][s][lane * V + j]);
-        if (c0 + j < C) part[((int64_t)s * nsplit + blockIdx.x) * C + c0 + j] = t;
+        if (c0 + j < C) part[((int64_t)blockIdx.x * NS + s) * C + c0 + j] = t;
       }
   }
 }
@@ -170,48 +170,43 @@ __global__ __launch_bounds__(kBlock) void k_nchw_reduce(
   tg_block_sum<4, NS>(acc, red);
   if (threadIdx.x == 0) {
 #pragma unroll
-    for (int s = 0; s < NS; ++s) part[((int64_t)s * nsplit + blockIdx.x) * C + c] = acc[s];
+    for (int s = 0; s < NS; ++s) part[((int64_t)blockIdx.x * NS + s) * C + c] = acc[s];
   }
 }
 
-// Per-channel finalisation kernels (one thread per channel, fixed summation order).
+// Per-channel finalisation kernels over the reduced sums (one thread per channel).
 // Forward mean: mean = S/m.
-__global__ void k_bn_mean(const float* __restrict__ part, float* __restrict__ mean,
-                          int64_t nsplit, int64_t C, float inv_m) {
+__global__ void k_bn_mean(const float* __restrict__ sums, float* __restrict__ mean, int64_t C,
+                          float inv_m) {
   const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-  if (c >= C) return;
-  double s = 0.0;
-  for (int64_t k = 0; k < nsplit; ++k) s += part[k * C + c];
-  mean[c] = (float)(s * (double)inv_m);
+  if (c < C) mean[c] = sums[c] * inv_m;
 }
 // Forward variance (population), rstd and the running-statistics EMA.
-__global__ void k_bn_var(const float* __restrict__ part, float* __restrict__ var,
+__global__ void k_bn_var(const float* __restrict__ sums, float* __restrict__ var,
                          float* __restrict__ rstd, const float* __restrict__ mean,
                          float* __restrict__ run_mean, float* __restrict__ run_var,
-                         float momentum, int64_t nsplit, int64_t C, float inv_m, float eps) {
+                         float momentum, int64_t C, float inv_m, float eps) {
   const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   if (c >= C) return;
-  double s = 0.0;
-  for (int64_t k = 0; k < nsplit; ++k) s += part[k * C + c];
-  const float v = (float)(s * (double)inv_m);
+  const float v = sums[c] * inv_m;
   if (var) var[c] = v;
   rstd[c] = 1.0f / sqrtf(v + eps);
   if (run_mean) run_mean[c] = (1.0f - momentum) * run_mean[c] + momentum * mean[c];
   if (run_var) run_var[c] = (1.0f - momentum) * run_var[c] + momentum * v;
 }
-// Backward: parameter grads and the two per-channel coefficients of pass 2.
-__global__ void k_bn_bwd_final(const float* __restrict__ part, float* __restrict__ coef,
+// Backward: parameter grads and the per-channel coefficients of pass 2:
+// dx = P*dy_m - Q - R*xhat with P = gamma*rstd, Q = P*S1/m, R = P*S2/m.
+__global__ void k_bn_bwd_final(const float* __restrict__ sums, const float* __restrict__ gamma,
+                               const float* __restrict__ rstd, float* __restrict__ coef,
                                float* __restrict__ dgamma, float* __restrict__ dbeta,
-                               int acc_params, int64_t nsplit, int64_t C, float inv_m) {
+                               int acc_params, int64_t C, float inv_m) {
   const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   if (c >= C) return;
-  float s1 = 0.f, s2 = 0.f;
-  for (int64_t k = 0; k < nsplit; ++k) {
-    s1 += part[k * C + c];
-    s2 += part[(nsplit + k) * C + c];
-  }
-  coef[c] = s1 * inv_m;
-  coef[C + c] = s2 * inv_m;
+  const float s1 = sums[c], s2 = sums[C + c];
+  const float P = gamma[c] * rstd[c];
+  coef[c] = P;
+  coef[C + c] = P * (s1 * inv_m);
+  coef[2 * C + c] = P * (s2 * inv_m);
   if (dbeta) dbeta[c] = acc_params ? dbeta[c] + s1 : s1;
   if (dgamma) dgamma[c] = acc_params ? dgamma[c] + s2 : s2;
 }
@@ -223,14 +218,27 @@ __device__ __forceinline__ int64_t chan_of(int64_t i, int64_t C, int64_t HW) {
   return LAYOUT == TG_NHWC ? (i % C) : ((i / HW) % C);
 }
 
-template <int LAYOUT, int V, bool ACC>
+template <int LAYOUT, int V, bool ACC, bool CONST_CH>
 __global__ __launch_bounds__(kBlock) void k_bn_bwd_apply(
     const float* __restrict__ x, const float* __restrict__ dy, const float* __restrict__ mean,
     const float* __restrict__ rstd, const float* __restrict__ gamma,
     const float* __restrict__ beta, const float* __restrict__ coef, int relu,
     float* __restrict__ dx, int64_t nvec, int64_t C, int64_t HW) {
+  // CONST_CH (NHWC, grid stride a multiple of C): every iteration of a thread
+  // touches the same V channels, so their parameters are loaded once.
   const int64_t stride = (int64_t)gridDim.x * kBlock;
-  for (int64_t iv = (int64_t)blockIdx.x * kBlock + threadIdx.x; iv < nvec; iv += stride) {
+  const int64_t iv0 = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  float pmu[V], prs[V], pg[V], pb[V], pP[V], pQ[V], pR[V];
+  if (CONST_CH) {
+    const int64_t cb = (iv0 * V) % C;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      const int64_t c = cb + j;
+      pmu[j] = mean[c]; prs[j] = rstd[c]; pg[j] = gamma[c]; pb[j] = beta[c];
+      pP[j] = coef[c]; pQ[j] = coef[C + c]; pR[j] = coef[2 * C + c];
+    }
+  }
+  for (int64_t iv = iv0; iv < nvec; iv += stride) {
     const int64_t i = iv * V;
     float xv[V], dv[V], ov[V];
     if (V == 4) {
@@ -247,15 +255,21 @@ __global__ __launch_bounds__(kBlock) void k_bn_bwd_apply(
       dv[0] = dy[i];
       if (ACC) ov[0] = dx[i];
     }
+    if (!CONST_CH) {
+      const int64_t cb = chan_of<LAYOUT, V>(i, C, HW);
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const int64_t c = LAYOUT == TG_NHWC ? cb + j : cb;
+        pmu[j] = mean[c]; prs[j] = rstd[c]; pg[j] = gamma[c]; pb[j] = beta[c];
+        pP[j] = coef[c]; pQ[j] = coef[C + c]; pR[j] = coef[2 * C + c];
+      }
+    }
     float r[V];
-    const int64_t cb = chan_of<LAYOUT, V>(i, C, HW);
 #pragma unroll
     for (int j = 0; j < V; ++j) {
-      const int64_t c = LAYOUT == TG_NHWC ? cb + j : cb;
-      const float mu = mean[c], rs = rstd[c], g = gamma[c], b = beta[c];
-      const float xh = bn_xhat(xv[j], mu, rs);
-      const float dm = (!relu || bn_relu_on(xh, g, b)) ? dv[j] : 0.f;
-      r[j] = g * rs * (dm - coef[c] - xh * coef[C + c]);
+      const float xh = bn_xhat(xv[j], pmu[j], prs[j]);
+      const float dm = (!relu || bn_relu_on(xh, pg[j], pb[j])) ? dv[j] : 0.f;
+      r[j] = pP[j] * dm - pQ[j] - pR[j] * xh;
       if (ACC) r[j] += ov[j];
     }
     if (V == 4) {
@@ -323,8 +337,10 @@ BnPlan bn_plan(int layout, int64_t N, int64_t C, int64_t HW, bool aligned) {
   return p;
 }
 
+// Workspace: partials [nsplit][2][C] | sums [2C] | coef [3C] | tree scratch
 size_t bn_ws_bytes(const BnPlan& p, int64_t C) {
-  return (size_t)(2 * p.nsplit * C + 2 * C) * sizeof(float);
+  return (size_t)(2 * p.nsplit * C + 5 * C) * sizeof(float) +
+         tg_sum_partials_scratch(p.nsplit, 2 * C);
 }
 
 template <int MODE>
@@ -355,6 +371,26 @@ unsigned apply_blocks(int64_t nvec) {
   const int64_t cap = (int64_t)tg_num_cus() * 64;
   if (b > cap) b = cap;
   return (unsigned)(b < 1 ? 1 : b);
+}
+
+int64_t gcd64(int64_t a, int64_t b) {
+  while (b) {
+    const int64_t t = a % b;
+    a = b;
+    b = t;
+  }
+  return a;
+}
+
+// NHWC apply grid whose element stride (blocks*256*V) is a multiple of C, so each
+// thread keeps one channel group; returns 0 when no such grid fits.
+unsigned const_channel_blocks(int64_t nvec, int64_t C, int V) {
+  const int64_t per_block = (int64_t)kBlock * V;
+  const int64_t unit = C / gcd64(C, per_block);  // blocks per channel period
+  int64_t b = apply_blocks(nvec);
+  if (unit > b) return 0;
+  b -= b % unit;
+  return (unsigned)b;
 }
 
 int check_args(int layout, int64_t N, int64_t C, int64_t HW, const char* who) {
@@ -394,15 +430,21 @@ TG_EXPORT int tg_batchnorm_fwd_train(int layout, const float* x, const float* ga
   }
   hipStream_t s = tg_stream(stream);
   float* part = (float*)workspace;
+  float* sums = part + 2 * p.nsplit * C;
+  float* scratch = sums + 5 * C;
   const float inv_m = 1.0f / (float)p.M;
   const unsigned cb = (unsigned)((C + kBlock - 1) / kBlock);
   launch_reduce<0>(layout, p, x, nullptr, nullptr, nullptr, nullptr, nullptr, relu, part, N, C,
                    HW, s);
-  k_bn_mean<<<cb, kBlock, 0, s>>>(part, mean, p.nsplit, C, inv_m);
+  st = tg_sum_partials(part, p.nsplit, C, TG_F32, sums, 0, scratch, s);
+  if (st) return st;
+  k_bn_mean<<<cb, kBlock, 0, s>>>(sums, mean, C, inv_m);
   launch_reduce<1>(layout, p, x, nullptr, mean, nullptr, nullptr, nullptr, relu, part, N, C, HW,
                    s);
-  k_bn_var<<<cb, kBlock, 0, s>>>(part, var, rstd, mean, running_mean, running_var, momentum,
-                                 p.nsplit, C, inv_m, eps);
+  st = tg_sum_partials(part, p.nsplit, C, TG_F32, sums, 0, scratch, s);
+  if (st) return st;
+  k_bn_var<<<cb, kBlock, 0, s>>>(sums, var, rstd, mean, running_mean, running_var, momentum, C,
+                                 inv_m, eps);
   const int64_t n = N * C * HW;
   const bool vec = p.V == 4 && al;
   const int64_t nvec = vec ? n / 4 : n;
@@ -436,24 +478,32 @@ TG_EXPORT int tg_batchnorm_bwd(int layout, const float* x, const float* mean, co
   }
   hipStream_t s = tg_stream(stream);
   float* part = (float*)workspace;
-  float* coef = part + 2 * p.nsplit * C;
+  float* sums = part + 2 * p.nsplit * C;
+  float* coef = sums + 2 * C;
+  float* scratch = sums + 5 * C;
   launch_reduce<2>(layout, p, x, dy, mean, rstd, gamma, beta, relu, part, N, C, HW, s);
+  st = tg_sum_partials(part, p.nsplit, 2 * C, TG_F32, sums, 0, scratch, s);
+  if (st) return st;
   const unsigned cb = (unsigned)((C + kBlock - 1) / kBlock);
-  k_bn_bwd_final<<<cb, kBlock, 0, s>>>(part, coef, dgamma, dbeta, accumulate_params, p.nsplit, C,
-                                       1.0f / (float)p.M);
+  k_bn_bwd_final<<<cb, kBlock, 0, s>>>(sums, gamma, rstd, coef, dgamma, dbeta, accumulate_params,
+                                       C, 1.0f / (float)p.M);
   const int64_t n = N * C * HW;
   const bool vec = p.V == 4 && al;
   const int64_t nvec = vec ? n / 4 : n;
   const unsigned ab = apply_blocks(nvec);
-#define TG_BN_APPLY(LAY, VV, ACC)                                                             \
-  k_bn_bwd_apply<LAY, VV, ACC><<<ab, kBlock, 0, s>>>(x, dy, mean, rstd, gamma, beta, coef, relu, \
-                                                     dx, nvec, C, HW)
-  if (layout == TG_NHWC) {
-    if (vec) { if (accumulate_dx) TG_BN_APPLY(TG_NHWC, 4, true); else TG_BN_APPLY(TG_NHWC, 4, false); }
-    else { if (accumulate_dx) TG_BN_APPLY(TG_NHWC, 1, true); else TG_BN_APPLY(TG_NHWC, 1, false); }
+#define TG_BN_APPLY(LAY, VV, ACC, CC, NB)                                               \
+  k_bn_bwd_apply<LAY, VV, ACC, CC><<<NB, kBlock, 0, s>>>(x, dy, mean, rstd, gamma, beta, coef, \
+                                                         relu, dx, nvec, C, HW)
+  const unsigned cc = (layout == TG_NHWC && vec) ? const_channel_blocks(nvec, C, 4) : 0;
+  if (cc) {
+    if (accumulate_dx) TG_BN_APPLY(TG_NHWC, 4, true, true, cc);
+    else TG_BN_APPLY(TG_NHWC, 4, false, true, cc);
+  } else if (layout == TG_NHWC) {
+    if (vec) { if (accumulate_dx) TG_BN_APPLY(TG_NHWC, 4, true, false, ab); else TG_BN_APPLY(TG_NHWC, 4, false, false, ab); }
+    else { if (accumulate_dx) TG_BN_APPLY(TG_NHWC, 1, true, false, ab); else TG_BN_APPLY(TG_NHWC, 1, false, false, ab); }
   } else {
-    if (vec) { if (accumulate_dx) TG_BN_APPLY(TG_NCHW, 4, true); else TG_BN_APPLY(TG_NCHW, 4, false); }
-    else { if (accumulate_dx) TG_BN_APPLY(TG_NCHW, 1, true); else TG_BN_APPLY(TG_NCHW, 1, false); }
+    if (vec) { if (accumulate_dx) TG_BN_APPLY(TG_NCHW, 4, true, false, ab); else TG_BN_APPLY(TG_NCHW, 4, false, false, ab); }
+    else { if (accumulate_dx) TG_BN_APPLY(TG_NCHW, 1, true, false, ab); else TG_BN_APPLY(TG_NCHW, 1, false, false, ab); }
   }
 #undef TG_BN_APPLY
   return tg_check_launch("tg_batchnorm_bwd");

@@ -136,3 +136,10 @@ __device__ __forceinline__ void tg_store16(T* p, const tg_vec16<T>& r) {
 
 // Number of CUs on the current device, cached per device by tg_runtime.
 int tg_num_cus();
+
+// Deterministic fp32 column sums: out[c] (+)= sum_{k<K} in[k*cols + c], converted to
+// dtype_out.  `scratch` must hold tg_sum_partials_scratch(K, cols) bytes (may be
+// null when that is 0).  Defined in tg_reduce.hip.
+size_t tg_sum_partials_scratch(int64_t K, int64_t cols);
+int tg_sum_partials(const float* in, int64_t K, int64_t cols, int dtype_out, void* out, int acc,
+                    float* scratch, hipStream_t s);

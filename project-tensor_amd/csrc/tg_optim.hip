@@ -40,9 +40,13 @@ __device__ __forceinline__ int find_tensor(const MtArgs& A, int64_t blk) {
 // Adam/AdamW, reference order (_nn.py:1413-1442, _training.py:2198-2220):
 //   p -= lr*wd*p (if wd != 0); m = b1*m + (1-b1)*g; v = b2*v + (1-b2)*g^2;
 //   mhat = m/bc1; vhat = v/bc2; [vmax = max(vmax, vhat)]; p -= lr*mhat/(sqrt(v*)+eps)
+struct AdamConsts {
+  float lr, b1, omb1, b2, omb2, eps, lrwd, bc1, bc2;
+  int decay;
+};
+
 template <bool AMS>
-__global__ __launch_bounds__(kBlock) void k_adam(MtArgs A, float lr, float b1, float b2,
-                                                 float eps, float wd, float bc1, float bc2) {
+__global__ __launch_bounds__(kBlock) void k_adam(MtArgs A, AdamConsts K) {
   const int t = find_tensor(A, blockIdx.x);
   const int64_t n = A.n[t];
   const int64_t start = (blockIdx.x - A.first_block[t]) * kChunk;
@@ -54,18 +58,17 @@ __global__ __launch_bounds__(kBlock) void k_adam(MtArgs A, float lr, float b1, f
   const bool vec = ((reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(g) |
                      reinterpret_cast<uintptr_t>(m) | reinterpret_cast<uintptr_t>(v) |
                      (AMS ? reinterpret_cast<uintptr_t>(vm) : 0)) & 15) == 0;
-  const float omb1 = 1.0f - b1, omb2 = 1.0f - b2, lrwd = lr * wd;
   auto upd = [&](float& pp, float gg, float& mm, float& vv, float* vmx) {
-    if (wd != 0.f) pp -= lrwd * pp;
-    mm = b1 * mm + omb1 * gg;
-    vv = b2 * vv + omb2 * (gg * gg);
-    const float mh = mm / bc1;
-    float vh = vv / bc2;
+    if (K.decay) pp -= K.lrwd * pp;
+    mm = K.b1 * mm + K.omb1 * gg;
+    vv = K.b2 * vv + K.omb2 * (gg * gg);
+    const float mh = mm / K.bc1;
+    float vh = vv / K.bc2;
     if (AMS) {
       vh = fmaxf(*vmx, vh);
       *vmx = vh;
     }
-    pp -= lr * mh / (sqrtf(vh) + eps);
+    pp -= K.lr * mh / (sqrtf(vh) + K.eps);
   };
   if (vec && start + kChunk <= n) {
 #pragma unroll
@@ -256,9 +259,9 @@ int64_t total_blocks(int ntensors, const int64_t* numel) {
 
 TG_EXPORT int tg_adam_step(int ntensors, float* const* params, const float* const* grads,
                            float* const* exp_avg, float* const* exp_avg_sq,
-                           float* const* max_exp_avg_sq, const int64_t* numel, float lr,
-                           float beta1, float beta2, float eps, float weight_decay,
-                           float bias_correction1, float bias_correction2, void* stream) {
+                           float* const* max_exp_avg_sq, const int64_t* numel, double lr,
+                           double beta1, double beta2, double eps, double weight_decay,
+                           double bias_correction1, double bias_correction2, void* stream) {
   TG_REQUIRE(ntensors >= 0, "tg_adam_step: negative tensor count");
   if (ntensors == 0) return TG_OK;
   TG_REQUIRE(params && grads && exp_avg && exp_avg_sq && numel, "tg_adam_step: null list");
@@ -268,16 +271,28 @@ TG_EXPORT int tg_adam_step(int ntensors, float* const* params, const float* cons
                "tg_adam_step: null pointer for tensor %d", i);
   hipStream_t s = tg_stream(stream);
   const bool ams = max_exp_avg_sq != nullptr;
+  // Scalars are combined in double and rounded once to fp32, as the reference's
+  // Python-float hyper-parameters are when they meet fp32 arrays (1 - beta2 in
+  // particular must not be formed from an already-rounded fp32 beta2).
+  AdamConsts K;
+  K.lr = (float)lr;
+  K.b1 = (float)beta1;
+  K.omb1 = (float)(1.0 - beta1);
+  K.b2 = (float)beta2;
+  K.omb2 = (float)(1.0 - beta2);
+  K.eps = (float)eps;
+  K.lrwd = (float)(lr * weight_decay);
+  K.decay = weight_decay != 0.0;
+  K.bc1 = (float)bias_correction1;
+  K.bc2 = (float)bias_correction2;
   return for_each_launch(
       ntensors, (void* const*)params, (void* const*)grads, (void* const*)exp_avg,
       (void* const*)exp_avg_sq, (void* const*)max_exp_avg_sq, numel,
       [&](const MtArgs& A, int64_t nb) {
         if (ams)
-          k_adam<true><<<(unsigned)nb, kBlock, 0, s>>>(A, lr, beta1, beta2, eps, weight_decay,
-                                                       bias_correction1, bias_correction2);
+          k_adam<true><<<(unsigned)nb, kBlock, 0, s>>>(A, K);
         else
-          k_adam<false><<<(unsigned)nb, kBlock, 0, s>>>(A, lr, beta1, beta2, eps, weight_decay,
-                                                        bias_correction1, bias_correction2);
+          k_adam<false><<<(unsigned)nb, kBlock, 0, s>>>(A, K);
         return tg_check_launch("tg_adam_step");
       });
 }

@@ -399,24 +399,49 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_reg(
   // Every group iterates the same number of times so block barriers stay uniform.
   const int64_t stride = (int64_t)gridDim.x * G;
   const int64_t iters = (rows + stride - 1) / stride;
+  // Software pipeline: the next row's x/dy/mean/rstd are in flight while the
+  // current row is reduced and written.
+  tg_vec16<T> nxa[VPT], nya[VPT];
+  float nmu = 0.f, nrs = 0.f;
+  auto fetch = [&](int64_t it) {
+    const int64_t row = it * stride + (int64_t)blockIdx.x * G + grp;
+    if (row < rows) {
+      const int64_t off = row * (int64_t)cols;
+#pragma unroll
+      for (int k = 0; k < VPT; ++k) {
+        const int vi = t + k * TPR;
+        if (vi < nv) {
+          nxa[k] = tg_load16(x + off + vi * V);
+          nya[k] = tg_load16(dy + off + vi * V);
+        }
+      }
+      nmu = mean[row];
+      nrs = rstd[row];
+    }
+  };
+  if (iters > 0) fetch(0);
   for (int64_t it = 0; it < iters; ++it) {
     const int64_t row = it * stride + (int64_t)blockIdx.x * G + grp;
     const bool live = row < rows;
     const int64_t off = (live ? row : 0) * (int64_t)cols;
-    const float mu = live ? mean[row] : 0.f;
-    const float rs = live ? rstd[row] : 0.f;
+    const float mu = nmu, rs = nrs;
+    tg_vec16<T> xa[VPT], ya[VPT];
+#pragma unroll
+    for (int k = 0; k < VPT; ++k) {
+      xa[k] = nxa[k];
+      ya[k] = nya[k];
+    }
+    if (it + 1 < iters) fetch(it + 1);
     float xh[VPT][V], dyv[VPT][V];
     float sums[2] = {0.f, 0.f};
 #pragma unroll
     for (int k = 0; k < VPT; ++k) {
       const int vi = t + k * TPR;
       if (live && vi < nv) {
-        tg_vec16<T> a = tg_load16(x + off + vi * V);
-        tg_vec16<T> b = tg_load16(dy + off + vi * V);
 #pragma unroll
         for (int j = 0; j < V; ++j) {
-          xh[k][j] = (tg_to_float(a.v[j]) - mu) * rs;
-          dyv[k][j] = tg_to_float(b.v[j]);
+          xh[k][j] = (tg_to_float(xa[k].v[j]) - mu) * rs;
+          dyv[k][j] = tg_to_float(ya[k].v[j]);
           const float g = dyv[k][j] * gam[k][j];
           sums[0] += g;
           sums[1] += g * xh[k][j];
@@ -566,41 +591,6 @@ __global__ __launch_bounds__(kBlock) void k_colsum_partial(const TI* __restrict_
   part[(int64_t)blockIdx.y * cols + c] = (s0 + s1) + (s2 + s3);
 }
 
-// Stage 2: out[c] (+)= sum_{s < nsplit} part[s][c]   (fixed order: deterministic)
-template <typename TO, bool ACC>
-__global__ __launch_bounds__(kBlock) void k_colsum_final(const float* __restrict__ part,
-                                                         TO* __restrict__ out, int64_t nsplit,
-                                                         int64_t cols) {
-  const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-  if (c >= cols) return;
-  float s = 0.f;
-  for (int64_t k = 0; k < nsplit; ++k) s += part[k * cols + c];
-  if (ACC) s += tg_to_float(out[c]);
-  out[c] = tg_from_float<TO>(s);
-}
-
-template <typename TO>
-int colsum_final(const float* part, void* out, int64_t nsplit, int64_t cols, int acc,
-                 hipStream_t s) {
-  const unsigned blocks = (unsigned)((cols + kBlock - 1) / kBlock);
-  if (acc)
-    k_colsum_final<TO, true><<<blocks, kBlock, 0, s>>>(part, (TO*)out, nsplit, cols);
-  else
-    k_colsum_final<TO, false><<<blocks, kBlock, 0, s>>>(part, (TO*)out, nsplit, cols);
-  return tg_check_launch("column-sum final");
-}
-
-int colsum_final_dt(int dtype, const float* part, void* out, int64_t nsplit, int64_t cols,
-                    int acc, hipStream_t s) {
-  switch (dtype) {
-    case TG_F32: return colsum_final<float>(part, out, nsplit, cols, acc, s);
-    case TG_F16: return colsum_final<tg_half>(part, out, nsplit, cols, acc, s);
-    case TG_BF16: return colsum_final<tg_bf16>(part, out, nsplit, cols, acc, s);
-  }
-  tg_set_error("column-sum: unsupported output dtype %d", dtype);
-  return TG_ERR_UNSUPPORTED;
-}
-
 int64_t colsum_splits(int64_t rows, int64_t cols) {
   const int64_t ctiles = (cols + kBlock - 1) / kBlock;
   int64_t want = (4 * (int64_t)tg_num_cus() + ctiles - 1) / ctiles;
@@ -698,11 +688,14 @@ int ln_bwd_t(const void* x, const float* mean, const float* rstd, const float* g
   }
   int st = tg_check_launch("tg_layernorm_bwd");
   if (st) return st;
+  float* scratch = part + 2 * p.nparts * cols;
   if (dgamma) {
-    st = colsum_final<float>(part, dgamma, p.nparts, cols, acc_params, s);
+    st = tg_sum_partials(part, p.nparts, cols, TG_F32, dgamma, acc_params, scratch, s);
     if (st) return st;
   }
-  if (dbeta) st = colsum_final<float>(part + p.nparts * cols, dbeta, p.nparts, cols, acc_params, s);
+  if (dbeta)
+    st = tg_sum_partials(part + p.nparts * cols, p.nparts, cols, TG_F32, dbeta, acc_params,
+                         scratch, s);
   return st;
 }
 
@@ -762,7 +755,7 @@ TG_EXPORT size_t tg_layernorm_bwd_workspace(int dtype, int64_t rows, int64_t col
   LnBwdPlan a = ln_bwd_plan_dt(dtype, rows, cols, true);
   LnBwdPlan b = ln_bwd_plan_dt(dtype, rows, cols, false);
   const int64_t np = a.nparts > b.nparts ? a.nparts : b.nparts;
-  return (size_t)(2 * np * cols) * sizeof(float);
+  return (size_t)(2 * np * cols) * sizeof(float) + tg_sum_partials_scratch(np, cols);
 }
 
 TG_EXPORT int tg_layernorm_bwd(int dtype, const void* x, const float* mean, const float* rstd,
@@ -775,7 +768,8 @@ TG_EXPORT int tg_layernorm_bwd(int dtype, const void* x, const float* mean, cons
   TG_REQUIRE(x && mean && rstd && gamma && dy && dx, "tg_layernorm_bwd: null pointer");
   const bool al = tg_aligned16(x) && tg_aligned16(dy) && tg_aligned16(dx);
   LnBwdPlan p = ln_bwd_plan_dt(dtype, rows, cols, al);
-  const size_t need = (size_t)(2 * p.nparts * cols) * sizeof(float);
+  const size_t need =
+      (size_t)(2 * p.nparts * cols) * sizeof(float) + tg_sum_partials_scratch(p.nparts, cols);
   if (!workspace || workspace_bytes < need) {
     tg_set_error("tg_layernorm_bwd: workspace of %zu bytes needed, got %zu", need,
                  workspace ? workspace_bytes : (size_t)0);
@@ -800,7 +794,8 @@ TG_EXPORT int tg_layernorm_bwd(int dtype, const void* x, const float* mean, cons
 
 TG_EXPORT size_t tg_reduce_rows_workspace(int64_t rows, int64_t cols) {
   if (rows <= 0 || cols <= 0) return 0;
-  return (size_t)(colsum_splits(rows, cols) * cols) * sizeof(float);
+  const int64_t ns = colsum_splits(rows, cols);
+  return (size_t)(ns * cols) * sizeof(float) + tg_sum_partials_scratch(ns, cols);
 }
 
 // out[c] (+)= sum_r in[r][c] for a row-major [rows, cols] input: the reduction that
@@ -815,12 +810,11 @@ TG_EXPORT int tg_reduce_rows(int dtype_in, const void* in, int dtype_out, void* 
   if (rows == 0) {
     if (accumulate) return TG_OK;
     // sum over zero rows is zero
-    const int64_t ns = 0;
-    return colsum_final_dt(dtype_out, (const float*)workspace, out, ns, cols, 0, s);
+    return tg_sum_partials(nullptr, 0, cols, dtype_out, out, 0, nullptr, s);
   }
   TG_REQUIRE(in, "tg_reduce_rows: null input");
   const int64_t ns = colsum_splits(rows, cols);
-  const size_t need = (size_t)(ns * cols) * sizeof(float);
+  const size_t need = (size_t)(ns * cols) * sizeof(float) + tg_sum_partials_scratch(ns, cols);
   if (!workspace || workspace_bytes < need) {
     tg_set_error("tg_reduce_rows: workspace of %zu bytes needed, got %zu", need,
                  workspace ? workspace_bytes : (size_t)0);
@@ -838,5 +832,5 @@ TG_EXPORT int tg_reduce_rows(int dtype_in, const void* in, int dtype_out, void* 
   }
   int st = tg_check_launch("tg_reduce_rows");
   if (st) return st;
-  return colsum_final_dt(dtype_out, part, out, ns, cols, accumulate, s);
+  return tg_sum_partials(part, ns, cols, dtype_out, out, accumulate, part + ns * cols, s);
 }

@@ -1,0 +1,1053 @@
+"""Autograd Tensor with the reference's API (tensor_gpu_v2/_core.py:609-1467).
+
+Storage is a torch device tensor (torch serves as allocator and stream
+provider).  Every gradient on the backward hot path — activation, softmax,
+matmul, broadcast reductions, attention, normalisation — runs in libtgbwd's
+HIP kernels through _lib; view/reshape bookkeeping and the elementwise
+arithmetic of ops outside the hot path use device tensor ops, the role CuPy
+plays for the reference.
+
+Gradient buffers are allocated lazily: a tensor that records gradients starts
+with an implicit zero gradient (the reference allocates zeros eagerly,
+_core.py:637).  The first contribution is written straight into a fresh buffer
+(kernel `accumulate` = 0), later ones accumulate (`accumulate` = 1), which is
+the reference's `parent.grad += local` with one read pass fewer.  Reading
+`.grad` materialises the zeros, so observable behaviour matches.
+"""
+import math
+
+import numpy as np
+import torch
+
+from . import _config as cfg
+from . import _lib as L
+
+
+def _noop():
+    return None
+
+
+def _to_device_tensor(data, dtype):
+    """Convert array-likes / torch tensors to a device tensor of `dtype` (or the
+    inferred dtype when None).  Returns (tensor, inferred_dtype)."""
+    if isinstance(data, Tensor):
+        data = data.data
+    if isinstance(data, torch.Tensor):
+        t = data
+        inferred = t.dtype
+    else:
+        arr = np.asarray(data)
+        if arr.dtype == np.object_:
+            raise TypeError("object dtype is not supported")
+        inferred = cfg.to_torch_dtype(arr.dtype) if arr.dtype.kind != "U" else None
+        if inferred is None:
+            raise TypeError(f"unsupported data of dtype {arr.dtype}")
+        t = torch.from_numpy(np.ascontiguousarray(arr))
+    return t, inferred
+
+
+class Tensor:
+    """Autograd tensor on the MI355X (reference: _core.py:609-1467)."""
+
+    __slots__ = ("data", "_g", "_gz", "_backward", "_prev", "_op", "label", "_device",
+                 "_requires_grad", "_is_view", "_base", "_grad_fn", "__weakref__",
+                 "_tied_source", "_tied_transpose")
+
+    def __init__(self, data, _children=(), _op="", label="", device=None, requires_grad=True,
+                 dtype=None):
+        device = cfg._canonicalize_device(device or cfg._device)
+        t, inferred = _to_device_tensor(data, dtype)
+        target = cfg.resolve_dtype(inferred, dtype)
+        if t.device.type != "cuda":
+            t = t.to(device="cuda", dtype=target)
+        elif t.dtype != target:
+            t = t.to(target)
+        self.data = t
+        rg = bool(requires_grad) and cfg._grad_enabled
+        self._g = None
+        self._gz = rg  # implicit zero gradient
+        self._backward = _noop
+        self._prev = _unique(_children)
+        self._op = _op
+        self.label = label
+        self._device = device
+        self._requires_grad = rg
+        self._is_view = False
+        self._base = None
+        self._grad_fn = None
+
+    # ------------------------------------------------------------ construction
+    @staticmethod
+    def _wrap(t, children=(), op="", requires_grad=True):
+        """Fast constructor for op outputs already on the device; applies the dtype
+        policy (autocast) like Tensor.__init__."""
+        out = object.__new__(Tensor)
+        target = cfg.resolve_dtype(t.dtype)
+        out.data = t if t.dtype == target else t.to(target)
+        rg = requires_grad and cfg._grad_enabled
+        out._g = None
+        out._gz = rg
+        out._backward = _noop
+        out._prev = _unique(children) if rg else ()
+        out._op = op
+        out.label = ""
+        out._device = "cuda"
+        out._requires_grad = rg
+        out._is_view = False
+        out._base = None
+        out._grad_fn = None
+        return out
+
+    @staticmethod
+    def _create_view_fast(data, device="cuda", requires_grad=False):
+        """(_core.py:763-778)"""
+        out = Tensor._wrap(data, (), "", requires_grad)
+        out.data = data
+        out._is_view = True
+        return out
+
+    @staticmethod
+    def randn(*shape, device=None, requires_grad=True, dtype=None):
+        """Standard-normal tensor drawn from NumPy's global RNG (so np.random.seed
+        makes it reproducible), then moved to the device."""
+        if len(shape) == 1 and isinstance(shape[0], (tuple, list)):
+            shape = tuple(shape[0])
+        return Tensor(np.random.randn(*shape).astype(np.float32), device=device,
+                      requires_grad=requires_grad, dtype=dtype)
+
+    @staticmethod
+    def zeros(*shape, device=None, requires_grad=True, dtype=None):
+        if len(shape) == 1 and isinstance(shape[0], (tuple, list)):
+            shape = tuple(shape[0])
+        return Tensor(np.zeros(shape, dtype=np.float32), device=device,
+                      requires_grad=requires_grad, dtype=dtype)
+
+    @staticmethod
+    def ones(*shape, device=None, requires_grad=True, dtype=None):
+        if len(shape) == 1 and isinstance(shape[0], (tuple, list)):
+            shape = tuple(shape[0])
+        return Tensor(np.ones(shape, dtype=np.float32), device=device,
+                      requires_grad=requires_grad, dtype=dtype)
+
+    # ------------------------------------------------------------ grad storage
+    def _new_buf(self, fill=None):
+        d = self.data
+        if fill is None:
+            return torch.empty(d.shape, dtype=d.dtype, device=d.device)
+        return torch.full(d.shape, fill, dtype=d.dtype, device=d.device)
+
+    @property
+    def grad(self):
+        if self._gz:
+            self._g = self._new_buf(0)
+            self._gz = False
+        return self._g
+
+    @grad.setter
+    def grad(self, value):
+        self._gz = False
+        if value is None:
+            self._g = None
+            return
+        if isinstance(value, Tensor):
+            value = value.data
+        if not isinstance(value, torch.Tensor):
+            value = torch.as_tensor(np.asarray(value))
+        if value.device.type != "cuda":
+            value = value.to("cuda")
+        if not value.is_contiguous():
+            value = value.contiguous()
+        self._g = value
+
+    def _has_grad(self):
+        return self._gz or self._g is not None
+
+    def _grad_out(self):
+        """Gradient flowing into this node's closure (zeros if nothing arrived)."""
+        if self._gz:
+            return self._new_buf(0)
+        return self._g
+
+    def _grad_target(self):
+        """(buffer, accumulate) for a kernel that adds this tensor's gradient."""
+        if self._gz:
+            self._g = self._new_buf()
+            self._gz = False
+            return self._g, False
+        return self._g, True
+
+    def _accumulate(self, g, owned=False):
+        """self.grad += g (g: torch tensor broadcast-compatible in shape, any float dtype)."""
+        if not self._has_grad():
+            return
+        if g.shape != self.data.shape:
+            g = g.reshape(self.data.shape)
+        if self._gz:
+            self._gz = False
+            if owned and g.dtype == self.data.dtype and g.is_contiguous():
+                self._g = g
+            else:
+                buf = self._new_buf()
+                if g.is_contiguous() and g.dtype in L._TORCH_TO_CODE and buf.dtype in L._TORCH_TO_CODE:
+                    L.axpby(g, buf, 1.0, 0.0)
+                else:
+                    buf.copy_(g)
+                self._g = buf
+            return
+        if (g.is_contiguous() and self._g.is_contiguous() and g.dtype in L._TORCH_TO_CODE
+                and self._g.dtype in L._TORCH_TO_CODE):
+            L.axpby(g, self._g, 1.0, 1.0)
+        else:
+            self._g.add_(g.to(self._g.dtype))
+
+    # ------------------------------------------------------------ properties
+    @property
+    def xp(self):
+        return torch
+
+    @property
+    def shape(self):
+        return tuple(self.data.shape)
+
+    @property
+    def ndim(self):
+        return self.data.dim()
+
+    @property
+    def dtype(self):
+        return cfg.to_numpy_dtype(self.data.dtype)
+
+    @property
+    def size(self):
+        return self.data.numel()
+
+    @property
+    def T(self):
+        return self.transpose()
+
+    @property
+    def requires_grad(self):
+        return self._requires_grad
+
+    def to(self, device):
+        cfg._canonicalize_device(device)
+        return self
+
+    def cuda(self):
+        return self
+
+    def cpu(self):
+        return self.to("cpu")
+
+    def numpy(self):
+        t = self.data
+        if t.dtype == torch.bfloat16:
+            t = t.float()
+        return t.detach().cpu().numpy()
+
+    def item(self):
+        return float(self.data.reshape(-1)[0]) if self.data.numel() == 1 else float(self.data)
+
+    def clone(self):
+        return Tensor(self.data.clone(), requires_grad=self._requires_grad)
+
+    def detach(self):
+        return Tensor(self.data.clone(), requires_grad=False)
+
+    def contiguous(self):
+        if self.data.is_contiguous():
+            return self
+        return Tensor(self.data.contiguous(), requires_grad=self._requires_grad)
+
+    def half(self):
+        return Tensor(self.data.to(torch.float16), requires_grad=self._requires_grad,
+                      dtype=np.float16)
+
+    def float(self):
+        return Tensor(self.data.to(torch.float32), requires_grad=self._requires_grad,
+                      dtype=np.float32)
+
+    def zero_grad(self):
+        if self._has_grad():
+            self._g = None
+            self._gz = True
+
+    def __repr__(self):
+        rg = f", requires_grad={self._requires_grad}" if self._requires_grad else ""
+        op = f", op='{self._op}'" if self._op else ""
+        return f"Tensor({list(self.data.shape)}, dtype={self.dtype}, device='cuda'{op}{rg})"
+
+    def __len__(self):
+        return self.data.shape[0]
+
+    # ------------------------------------------------------------ helpers
+    def _other(self, other):
+        return other if isinstance(other, Tensor) else Tensor(
+            _scalar_like(other, self.data), requires_grad=False)
+
+    def _out(self, t, children, op):
+        return Tensor._wrap(t, children, op)
+
+    # ------------------------------------------------------------ arithmetic
+    def __add__(self, other):
+        other = self._other(other)
+        out = self._out(self.data + other.data, (self, other), "+")
+        if out._requires_grad:
+            def _backward():
+                g = out._grad_out()
+                if self._has_grad():
+                    self._accumulate(_unbroadcast_dev(g, self.data.shape, self.data.dtype), True)
+                if other._has_grad():
+                    other._accumulate(_unbroadcast_dev(g, other.data.shape, other.data.dtype), True)
+            out._backward = _backward
+        return out
+
+    def __radd__(self, other):
+        return self + other
+
+    def __mul__(self, other):
+        other = self._other(other)
+        out = self._out(self.data * other.data, (self, other), "*")
+        if out._requires_grad:
+            def _backward():
+                g = out._grad_out()
+                if self._has_grad():
+                    self._accumulate(_unbroadcast_dev(other.data * g, self.data.shape,
+                                                      self.data.dtype), True)
+                if other._has_grad():
+                    other._accumulate(_unbroadcast_dev(self.data * g, other.data.shape,
+                                                       other.data.dtype), True)
+            out._backward = _backward
+        return out
+
+    def __rmul__(self, other):
+        return self * other
+
+    def __pow__(self, other):
+        assert isinstance(other, (int, float)), "only supporting int/float powers"
+        out = self._out(self.data ** other, (self,), f"**{other}")
+        if out._requires_grad:
+            def _backward():
+                if self._has_grad():
+                    self._accumulate((other * self.data ** (other - 1)) * out._grad_out(), True)
+            out._backward = _backward
+        return out
+
+    def __neg__(self):
+        return self * -1
+
+    def __sub__(self, other):
+        return self + (-other)
+
+    def __rsub__(self, other):
+        return other + (-self)
+
+    def __truediv__(self, other):
+        return self * (other ** -1)
+
+    def __rtruediv__(self, other):
+        return other * (self ** -1)
+
+    def __matmul__(self, other):
+        other = self._other(other)
+        return _matmul(self, other)
+
+    # ------------------------------------------------------------ reductions
+    def sum(self, axis=None, keepdims=False):
+        if axis is None:
+            r = self.data.sum()
+            if keepdims:
+                r = r.reshape((1,) * self.data.dim())
+        else:
+            r = self.data.sum(dim=axis, keepdim=keepdims)
+        out = self._out(r, (self,), "sum")
+        if out._requires_grad:
+            def _backward():
+                if not self._has_grad():
+                    return
+                g = out._grad_out()
+                if not keepdims and axis is not None:
+                    axes = (axis,) if isinstance(axis, int) else tuple(axis)
+                    for ax in sorted(a % self.data.dim() for a in axes):
+                        g = g.unsqueeze(ax)
+                elif not keepdims:
+                    g = g.reshape((1,) * self.data.dim())
+                self._accumulate(g.expand(self.data.shape))
+            out._backward = _backward
+        return out
+
+    def mean(self, axis=None, keepdims=False):
+        s = self.sum(axis=axis, keepdims=keepdims)
+        if axis is None:
+            n = self.data.numel()
+        else:
+            axes = (axis,) if isinstance(axis, int) else axis
+            n = int(np.prod([self.data.shape[i] for i in axes]))
+        return s * (1.0 / float(n))
+
+    def var(self, axis=None, keepdims=False, correction=0):
+        m = self.mean(axis=axis, keepdims=True)
+        d = self - m
+        sq = d ** 2
+        if axis is None:
+            n = self.data.numel()
+        else:
+            axes = (axis,) if isinstance(axis, int) else axis
+            n = int(np.prod([self.data.shape[i] for i in axes]))
+        return sq.sum(axis=axis, keepdims=keepdims) * (1.0 / float(n - correction))
+
+    def std(self, axis=None, keepdims=False, correction=0):
+        return (self.var(axis=axis, keepdims=keepdims, correction=correction) + 1e-8) ** 0.5
+
+    def max(self, axis=None, keepdims=False):
+        if axis is None:
+            r = self.data.max()
+        else:
+            r = self.data.amax(dim=axis, keepdim=keepdims)
+        out = self._out(r, (self,), "max")
+        if out._requires_grad:
+            def _backward():
+                if not self._has_grad():
+                    return
+                od = r if (keepdims or axis is None) else r.unsqueeze(axis)
+                mask = (self.data == od).to(self.data.dtype)
+                cnt = mask.sum() if axis is None else mask.sum(dim=axis, keepdim=True)
+                g = out._grad_out()
+                if not keepdims and axis is not None:
+                    g = g.unsqueeze(axis)
+                self._accumulate(mask * g.expand(self.data.shape) / cnt, True)
+            out._backward = _backward
+        return out
+
+    def min(self, axis=None, keepdims=False):
+        return (-self).max(axis=axis, keepdims=keepdims) * -1
+
+    def argmax(self, axis=None):
+        return self.data.argmax() if axis is None else self.data.argmax(dim=axis)
+
+    def argmin(self, axis=None):
+        return self.data.argmin() if axis is None else self.data.argmin(dim=axis)
+
+    # ------------------------------------------------------------ activations
+    def gelu(self):
+        """tanh-approx GELU; forward and backward on libtgbwd (_core.py:1172-1209)."""
+        return _activation(self, "gelu")
+
+    def silu(self):
+        """SiLU; forward and backward on libtgbwd (_core.py:1211-1246)."""
+        return _activation(self, "silu")
+
+    def relu(self):
+        out = self._out(torch.clamp_min(self.data, 0), (self,), "ReLU")
+        if out._requires_grad:
+            def _backward():
+                if self._has_grad():
+                    self._accumulate((out.data > 0).to(self.data.dtype) * out._grad_out(), True)
+            out._backward = _backward
+        return out
+
+    def leaky_relu(self, negative_slope=0.01):
+        out = self._out(torch.where(self.data >= 0, self.data, negative_slope * self.data),
+                        (self,), "LeakyReLU")
+        if out._requires_grad:
+            def _backward():
+                if self._has_grad():
+                    m = torch.where(self.data >= 0, 1.0, negative_slope).to(self.data.dtype)
+                    self._accumulate(m * out._grad_out(), True)
+            out._backward = _backward
+        return out
+
+    def swish(self, beta=1.0):
+        if beta == 1.0:
+            return self.silu()
+        s = torch.sigmoid(beta * self.data)
+        out = self._out(self.data * s, (self,), "Swish")
+        if out._requires_grad:
+            def _backward():
+                if self._has_grad():
+                    sv = torch.sigmoid(beta * self.data)
+                    self._accumulate((sv + beta * self.data * sv * (1 - sv)) * out._grad_out(), True)
+            out._backward = _backward
+        return out
+
+    def sigmoid(self):
+        out = self._out(torch.sigmoid(self.data), (self,), "sigmoid")
+        if out._requires_grad:
+            def _backward():
+                if self._has_grad():
+                    self._accumulate(out.data * (1 - out.data) * out._grad_out(), True)
+            out._backward = _backward
+        return out
+
+    def tanh(self):
+        out = self._out(torch.tanh(self.data), (self,), "tanh")
+        if out._requires_grad:
+            def _backward():
+                if self._has_grad():
+                    self._accumulate((1 - out.data ** 2) * out._grad_out(), True)
+            out._backward = _backward
+        return out
+
+    def exp(self):
+        out = self._out(torch.exp(self.data), (self,), "exp")
+        if out._requires_grad:
+            def _backward():
+                if self._has_grad():
+                    self._accumulate(out.data * out._grad_out(), True)
+            out._backward = _backward
+        return out
+
+    def log(self):
+        out = self._out(torch.log(self.data), (self,), "log")
+        if out._requires_grad:
+            def _backward():
+                if self._has_grad():
+                    self._accumulate(out._grad_out() / self.data, True)
+            out._backward = _backward
+        return out
+
+    def softmax(self, axis=-1):
+        """Softmax; forward and backward on libtgbwd along the last axis
+        (_core.py:1286-1299); other axes are moved last around the kernel."""
+        nd = self.data.dim()
+        ax = axis % nd if nd else 0
+        moved = nd > 0 and ax != nd - 1
+        x = self.data.movedim(ax, -1).contiguous() if moved else self.data.contiguous()
+        if x.dtype not in L._TORCH_TO_CODE:
+            raise TypeError(f"softmax: unsupported dtype {x.dtype}")
+        y = L.softmax_fwd(x)
+        out = self._out(y.movedim(-1, ax) if moved else y, (self,), "softmax")
+        if out._requires_grad:
+            def _backward():
+                if not self._has_grad():
+                    return
+                yy = out.data.movedim(ax, -1).contiguous() if moved else out.data
+                g = out._grad_out()
+                g = (g.movedim(ax, -1) if moved else g).contiguous().to(yy.dtype)
+                if yy.dtype != self.data.dtype:
+                    yy = yy.to(self.data.dtype)
+                    g = g.to(self.data.dtype)
+                if moved:
+                    dx = L.softmax_bwd(yy, g, torch.empty_like(yy), False)
+                    self._accumulate(dx.movedim(-1, ax), True)
+                else:
+                    buf, acc = self._grad_target()
+                    L.softmax_bwd(yy, g, buf, acc)
+            out._backward = _backward
+        return out
+
+    def log_softmax(self, axis=-1):
+        r = torch.log_softmax(self.data.float(), dim=axis).to(self.data.dtype)
+        out = self._out(r, (self,), "log_softmax")
+        if out._requires_grad:
+            def _backward():
+                if self._has_grad():
+                    g = out._grad_out()
+                    sm = torch.exp(out.data)
+                    self._accumulate(g - sm * g.sum(dim=axis, keepdim=True), True)
+            out._backward = _backward
+        return out
+
+    # ------------------------------------------------------------ shapes / views
+    def _view_out(self, t, op, back):
+        if not self._requires_grad or not cfg._grad_enabled:
+            return Tensor._create_view_fast(t, self._device, False)
+        out = Tensor._wrap(t, (self,), op)
+        out.data = t
+        out._is_view = True
+
+        def _backward():
+            if self._has_grad() and out._has_grad():
+                self._accumulate(back(out._grad_out()))
+        out._backward = _backward
+        return out
+
+    def reshape(self, *shape):
+        if len(shape) == 1 and isinstance(shape[0], (tuple, list)):
+            shape = tuple(shape[0])
+        orig = self.data.shape
+        return self._view_out(self.data.reshape(shape), "reshape", lambda g: g.reshape(orig))
+
+    def view(self, *shape):
+        if len(shape) == 1 and isinstance(shape[0], (tuple, list)):
+            shape = tuple(shape[0])
+        orig = self.data.shape
+        return self._view_out(self.data.reshape(shape), "view", lambda g: g.reshape(orig))
+
+    def flatten(self, start_dim=0, end_dim=-1):
+        if end_dim < 0:
+            end_dim = self.ndim + end_dim
+        shape = list(self.shape[:start_dim]) + [-1] + list(self.shape[end_dim + 1:])
+        return self.reshape(tuple(shape))
+
+    def transpose(self, *axes):
+        if not axes:
+            axes = tuple(range(self.ndim - 1, -1, -1))
+        elif len(axes) == 1 and isinstance(axes[0], (tuple, list)):
+            axes = tuple(axes[0])
+        inv = [0] * len(axes)
+        for i, a in enumerate(axes):
+            inv[a] = i
+        out = self._out(self.data.permute(*axes), (self,), "transpose")
+        if out._requires_grad:
+            def _backward():
+                if self._has_grad():
+                    self._accumulate(out._grad_out().permute(*inv))
+            out._backward = _backward
+        return out
+
+    def permute(self, *dims):
+        return self.transpose(*dims)
+
+    def squeeze(self, dim=None):
+        orig = self.data.shape
+        t = self.data.squeeze() if dim is None else self.data.squeeze(dim)
+        out = self._out(t, (self,), "squeeze")
+        if out._requires_grad:
+            def _backward():
+                if self._has_grad():
+                    self._accumulate(out._grad_out().reshape(orig))
+            out._backward = _backward
+        return out
+
+    def unsqueeze(self, dim):
+        out = self._out(self.data.unsqueeze(dim), (self,), "unsqueeze")
+        if out._requires_grad:
+            def _backward():
+                if self._has_grad():
+                    self._accumulate(out._grad_out().squeeze(dim))
+            out._backward = _backward
+        return out
+
+    def expand(self, *sizes):
+        if len(sizes) == 1 and isinstance(sizes[0], (tuple, list)):
+            sizes = tuple(sizes[0])
+        out = self._out(self.data.expand(*sizes), (self,), "expand")
+        if out._requires_grad:
+            def _backward():
+                if self._has_grad():
+                    self._accumulate(_unbroadcast_dev(out._grad_out(), self.data.shape,
+                                                      self.data.dtype), True)
+            out._backward = _backward
+        return out
+
+    def __getitem__(self, idx):
+        idx_t = _index_to_torch(idx)
+        out = self._out(self.data[idx_t], (self,), "getitem")
+        if out._requires_grad:
+            def _backward():
+                if self._has_grad():
+                    leaf = torch.zeros_like(self.data, requires_grad=True)
+                    with torch.enable_grad():
+                        leaf[idx_t].backward(out._grad_out().to(leaf.dtype))
+                    z = leaf.grad
+                    self._accumulate(z, True)
+            out._backward = _backward
+        return out
+
+    def __setitem__(self, idx, value):
+        v = value.data if isinstance(value, Tensor) else value
+        self.data[_index_to_torch(idx)] = v if not isinstance(v, np.ndarray) else torch.as_tensor(
+            v, device="cuda", dtype=self.data.dtype)
+
+    # ------------------------------------------------------------ backward
+    @staticmethod
+    def _unbroadcast(grad, shape):
+        """Reference-compatible validation wrapper (_core.py:1380-1424)."""
+        if shape is None or not isinstance(shape, (tuple, list)):
+            raise TypeError(f"shape must be tuple/list of ints, got {shape!r}")
+        try:
+            target = tuple(int(d) for d in shape)
+        except Exception as exc:
+            raise TypeError(f"shape must contain integer dimensions, got {shape!r}") from exc
+        if any(d < 0 for d in target):
+            raise ValueError(f"shape dimensions must be non-negative, got {target}")
+        if grad is None:
+            raise ValueError("grad cannot be None")
+        if not isinstance(grad, torch.Tensor):
+            grad = torch.as_tensor(np.asarray(grad))
+        return _unbroadcast_dev(grad, target, grad.dtype)
+
+    def backward(self, gradient=None):
+        """Reverse-mode sweep (_core.py:1426-1461): topological order over the
+        recorded graph (iterative DFS), seed with `gradient` (added to any existing
+        grad) or ones when the grad is absent or all zero, then run each closure once
+        in reverse order and drop it."""
+        topo = []
+        visited = set()
+        stack = [(self, False)]
+        while stack:
+            v, expanded = stack.pop()
+            if expanded:
+                topo.append(v)
+                continue
+            if id(v) in visited:
+                continue
+            visited.add(id(v))
+            stack.append((v, True))
+            for c in reversed(v._prev):
+                if id(c) not in visited:
+                    stack.append((c, False))
+        if gradient is not None:
+            g = gradient.data if isinstance(gradient, Tensor) else gradient
+            if not isinstance(g, torch.Tensor):
+                g = torch.as_tensor(np.asarray(g))
+            g = g.to(device="cuda", dtype=self.data.dtype)
+            if not self._has_grad():
+                self._g = g.expand(self.data.shape).contiguous()
+                self._gz = False
+            else:
+                self._accumulate(g.expand(self.data.shape).contiguous())
+        elif self._gz or self._g is None or not bool(torch.any(self._g != 0)):
+            self._g = self._new_buf(1)
+            self._gz = False
+        for v in reversed(topo):
+            v._backward()
+            v._backward = _noop
+
+
+# ====================================================================== helpers
+def _unique(children):
+    seen = set()
+    out = []
+    for c in children:
+        if id(c) not in seen:
+            seen.add(id(c))
+            out.append(c)
+    return tuple(out)
+
+
+def _scalar_like(v, ref):
+    """Python scalars / arrays as device tensors.  Float scalars adopt the reference
+    tensor's dtype (NumPy 2 weak-scalar promotion keeps fp32 op fp32)."""
+    if isinstance(v, torch.Tensor):
+        return v
+    if isinstance(v, (bool, int, float)):
+        dt = ref.dtype if ref.is_floating_point() or isinstance(v, int) else torch.float32
+        if isinstance(v, float) and not ref.is_floating_point():
+            dt = torch.float32
+        return torch.tensor(v, dtype=dt, device="cuda")
+    arr = np.asarray(v)
+    return torch.as_tensor(arr, device="cuda")
+
+
+def _index_to_torch(idx):
+    if isinstance(idx, tuple):
+        return tuple(_index_to_torch(i) for i in idx)
+    if isinstance(idx, Tensor):
+        return idx.data.long() if not idx.data.dtype == torch.bool else idx.data
+    if isinstance(idx, np.ndarray):
+        return torch.as_tensor(idx, device="cuda")
+    if isinstance(idx, list):
+        return torch.as_tensor(np.asarray(idx), device="cuda")
+    return idx
+
+
+def _unbroadcast_dev(grad, shape, dtype):
+    """Sum `grad` down to `shape` with the reference's rules (_core.py:1380-1424).
+    Leading-axis sums onto a contiguous suffix shape (the bias-gradient case) run in
+    tg_reduce_rows; other patterns are summed by device tensor ops.  Result has `dtype`."""
+    shape = tuple(shape)
+    if tuple(grad.shape) == shape:
+        return grad if grad.dtype == dtype else grad.to(dtype)
+    if grad.dim() < len(shape):
+        raise ValueError(
+            f"cannot unbroadcast grad with shape {tuple(grad.shape)} to higher-rank shape {shape}")
+    lead = grad.dim() - len(shape)
+    tail = tuple(grad.shape[lead:])
+    if tail == shape and grad.is_cuda and grad.is_contiguous() and grad.dtype in L._TORCH_TO_CODE \
+            and dtype in L._TORCH_TO_CODE and len(shape) > 0:
+        out = torch.empty(shape, dtype=dtype, device=grad.device)
+        L.reduce_rows(grad, out, False)
+        return out
+    g = grad
+    while g.dim() > len(shape):
+        g = g.sum(dim=0)
+    for ax, (gd, sd) in enumerate(zip(g.shape, shape)):
+        if sd == 1:
+            if gd != 1:
+                g = g.sum(dim=ax, keepdim=True)
+        elif gd != sd:
+            raise ValueError(
+                f"incompatible unbroadcast axis {ax}: grad dim {gd} cannot map to target dim {sd}")
+    if tuple(g.shape) != shape:
+        raise ValueError(f"unbroadcast produced shape {tuple(g.shape)}, expected {shape}")
+    return g.to(dtype)
+
+
+def _activation(x, kind):
+    xd = x.data
+    if xd.dtype not in L._TORCH_TO_CODE:
+        raise TypeError(f"{kind}: unsupported dtype {xd.dtype}")
+    xc = xd.contiguous()
+    y = L.act_fwd(kind, xc)
+    out = Tensor._wrap(y, (x,), "GELU" if kind == "gelu" else "SiLU")
+    if out._requires_grad:
+        def _backward():
+            if not x._has_grad():
+                return
+            g = out._grad_out()
+            if g.dtype != xc.dtype or not g.is_contiguous():
+                g = g.to(xc.dtype).contiguous()
+            buf, acc = x._grad_target()
+            L.act_bwd(kind, xc, g, buf, acc)
+        out._backward = _backward
+    return out
+
+
+# ====================================================================== matmul
+_GEMM_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
+
+
+def _compute_dtype(a, b):
+    """Operand dtype of the GEMM: the autocast dtype inside autocast, else the
+    promoted dtype (CuPy promotion, then the Tensor policy)."""
+    ac = cfg.autocast_dtype()
+    if ac is not None and ac in (torch.float16, torch.bfloat16):
+        return ac
+    return torch.promote_types(a.dtype, b.dtype)
+
+
+def _matmul(self, other):
+    a, b = self.data, other.data
+    if a.dim() == 0 or b.dim() == 0:
+        raise ValueError("matmul requires operands with ndim >= 1")
+    cdt = _compute_dtype(a, b)
+    if cdt not in _GEMM_DTYPES:
+        raise TypeError(f"matmul: dtype {cdt} is not supported by the MFMA GEMM "
+                        "(float32, float16, bfloat16)")
+    ac = a.to(cdt).contiguous()
+    bc = b.to(cdt).contiguous()
+    out_t = _matmul_fwd(ac, bc)
+    out = Tensor._wrap(out_t, (self, other), "@")
+    if out._requires_grad:
+        def _backward():
+            _matmul_bwd(self, other, ac, bc, out)
+        out._backward = _backward
+    return out
+
+
+def _batch_view(x, batch_shape, m, n):
+    """Broadcast x [..., m, n] to batch_shape + [m, n]; return (tensor3d, stride) with
+    stride 0 when x has no batch extent to broadcast."""
+    bsz = int(np.prod(batch_shape)) if batch_shape else 1
+    if x.dim() == 2:
+        return x, 0, bsz
+    xb = tuple(x.shape[:-2])
+    if xb == tuple(batch_shape):
+        return x.reshape(bsz, m, n), m * n, bsz
+    xe = x.expand(*batch_shape, m, n).contiguous()
+    return xe.reshape(bsz, m, n), m * n, bsz
+
+
+def _matmul_fwd(a, b):
+    av, bv = a.dim() == 1, b.dim() == 1
+    A = a.unsqueeze(0) if av else a
+    Bm = b.unsqueeze(1) if bv else b
+    M, K = A.shape[-2], A.shape[-1]
+    N = Bm.shape[-1]
+    if Bm.shape[-2] != K:
+        raise ValueError(f"matmul: shapes {tuple(a.shape)} and {tuple(b.shape)} not aligned")
+    if Bm.dim() == 2:
+        # fold all leading dims of A into M: one GEMM
+        lead = tuple(A.shape[:-2])
+        res = L.matmul2d(A.reshape(-1, K), Bm)
+        res = res.reshape(*lead, M, N)
+    else:
+        batch_shape = torch.broadcast_shapes(tuple(A.shape[:-2]), tuple(Bm.shape[:-2]))
+        A3, sa, bsz = _batch_view(A, batch_shape, M, K)
+        B3, sb, _ = _batch_view(Bm, batch_shape, K, N)
+        res = torch.empty(bsz, M, N, dtype=a.dtype, device=a.device)
+        L.gemm(A3, B3, res, False, False, 1.0, 0.0, M, N, K, K, N, N, sa, sb, M * N, bsz)
+        res = res.reshape(*batch_shape, M, N)
+    if av:
+        res = res.squeeze(-2)
+    if bv:
+        res = res.squeeze(-1)
+    return res
+
+
+def _matmul_bwd(self, other, ac, bc, out):
+    """dA = dC @ B^T, dB = A^T @ dC on the MFMA GEMM, with the reference's vector
+    promotion, validation and unbroadcast (_core.py:1003-1068)."""
+    lhs, rhs = self.data, other.data
+    if lhs.dim() == 0 or rhs.dim() == 0:
+        raise ValueError(
+            f"matmul backward requires operands with ndim >= 1, got {lhs.dim()} and {rhs.dim()}")
+    g = out._grad_out()
+    exp = tuple(out.data.shape)
+    if exp == ():
+        if g.numel() != 1:
+            raise ValueError(f"matmul backward expected scalar grad_out, got shape {tuple(g.shape)}")
+        g = g.reshape(())
+    elif tuple(g.shape) != exp:
+        raise ValueError(
+            f"matmul backward grad_out shape mismatch: expected {exp}, got {tuple(g.shape)}")
+    if self._has_grad() and not lhs.is_floating_point():
+        raise TypeError(f"matmul backward requires floating/complex lhs, got {lhs.dtype}")
+    if other._has_grad() and not rhs.is_floating_point():
+        raise TypeError(f"matmul backward requires floating/complex rhs, got {rhs.dtype}")
+    cdt = ac.dtype
+    av, bv = ac.dim() == 1, bc.dim() == 1
+    A = ac.unsqueeze(0) if av else ac
+    Bm = bc.unsqueeze(1) if bv else bc
+    if av and bv:
+        G = g.reshape(1, 1)
+    elif av:
+        G = g.unsqueeze(-2)
+    elif bv:
+        G = g.unsqueeze(-1)
+    else:
+        G = g
+    G = G.to(cdt).contiguous()
+    M, K = A.shape[-2], A.shape[-1]
+    N = Bm.shape[-1]
+    if Bm.dim() == 2:
+        lead = tuple(A.shape[:-2])
+        G2 = G.reshape(-1, N)
+        A2 = A.reshape(-1, K)
+        if self._has_grad():
+            # dA[.., m, k] = G @ B^T
+            buf, acc = self._grad_target()
+            if buf.dtype in (torch.float32, cdt):
+                L.matmul2d(G2, Bm, out=buf.view(A2.shape[0], K), trans_b=True,
+                           beta=1.0 if acc else 0.0)
+            else:
+                da = L.matmul2d(G2, Bm, trans_b=True, out_dtype=torch.float32)
+                if acc:
+                    buf.add_(da.reshape(buf.shape).to(buf.dtype))
+                else:
+                    buf.copy_(da.reshape(buf.shape))
+        if other._has_grad():
+            # dB[k, n] = sum over all leading rows of A^T @ G: one TN GEMM with K' = rows
+            buf, acc = other._grad_target()
+            if buf.dtype in (torch.float32, cdt):
+                L.matmul2d(A2, G2, out=buf.view(K, N), trans_a=True, beta=1.0 if acc else 0.0)
+            else:
+                db = L.matmul2d(A2, G2, trans_a=True, out_dtype=torch.float32)
+                if acc:
+                    buf.add_(db.reshape(buf.shape).to(buf.dtype))
+                else:
+                    buf.copy_(db.reshape(buf.shape))
+        return
+    # batched operands
+    batch_shape = torch.broadcast_shapes(tuple(A.shape[:-2]), tuple(Bm.shape[:-2]))
+    bsz = int(np.prod(batch_shape))
+    G3 = G.expand(*batch_shape, M, N).contiguous().reshape(bsz, M, N)
+    if self._has_grad():
+        B3, sb, _ = _batch_view(Bm, batch_shape, K, N)
+        da = torch.empty(bsz, M, K, dtype=torch.float32, device=A.device)
+        L.gemm(G3, B3, da, False, True, 1.0, 0.0, M, K, N, N, N, K, M * N, sb, M * K, bsz)
+        da = da.reshape(*batch_shape, M, K)
+        if av:
+            da = da.squeeze(-2)
+        self._accumulate(_unbroadcast_dev(da, tuple(lhs.shape), lhs.dtype), True)
+    if other._has_grad():
+        A3, sa, _ = _batch_view(A, batch_shape, M, K)
+        db = torch.empty(bsz, K, N, dtype=torch.float32, device=A.device)
+        L.gemm(A3, G3, db, True, False, 1.0, 0.0, K, N, M, K, N, N, sa, M * N, K * N, bsz)
+        db = db.reshape(*batch_shape, K, N)
+        if bv:
+            db = db.squeeze(-1)
+        other._accumulate(_unbroadcast_dev(db, tuple(rhs.shape), rhs.dtype), True)
+
+
+# ====================================================================== attention
+def flash_attention(query, key, value, block_size=64, is_causal=False, scale=None,
+                    dropout_p=0.0):
+    """FlashAttention forward/backward on libtgbwd (_core.py:1686-1870).
+    query/key/value: (B, H, L, D) or (B, L, D).  The forward saves the row
+    log-sum-exp; the backward recomputes P from it (no S x S matrix is stored)."""
+    q, k, v = query.data, key.data, value.data
+    three = q.dim() == 3
+    if three:
+        B, Lq, D = q.shape
+        q4 = q.reshape(B, 1, Lq, D)
+        k4 = k.reshape(B, 1, k.shape[1], D)
+        v4 = v.reshape(B, 1, v.shape[1], D)
+    else:
+        q4, k4, v4 = q, k, v
+    D = q4.shape[-1]
+    scale = scale or D ** -0.5
+    dt = q4.dtype
+    if dt not in (torch.float16, torch.bfloat16, torch.float32):
+        raise TypeError(f"flash_attention: unsupported dtype {dt}")
+    q4c, k4c, v4c = q4.contiguous(), k4.to(dt).contiguous(), v4.to(dt).contiguous()
+    o, lse = L.flash_attn_fwd(q4c, k4c, v4c, scale, is_causal)
+    if dropout_p > 0 and cfg._grad_enabled:
+        keep = (torch.rand(o.shape, device=o.device) > dropout_p).to(o.dtype)
+        o_out = o * keep / (1 - dropout_p)
+    else:
+        o_out = o
+    out = Tensor._wrap(o_out.reshape(q.shape) if three else o_out, (query, key, value),
+                       "FlashAttention")
+    if out._requires_grad:
+        def _backward():
+            g = out._grad_out()
+            g4 = g.reshape(q4c.shape).to(dt).contiguous()
+            dq = torch.empty_like(q4c)
+            dk = torch.empty_like(k4c)
+            dv = torch.empty_like(v4c)
+            L.flash_attn_bwd(q4c, k4c, v4c, o, g4, lse, dq, dk, dv, scale, is_causal, False)
+            if query._has_grad():
+                query._accumulate(dq.reshape(query.data.shape), True)
+            if key._has_grad():
+                key._accumulate(dk.reshape(key.data.shape), True)
+            if value._has_grad():
+                value._accumulate(dv.reshape(value.data.shape), True)
+        out._backward = _backward
+    return out
+
+
+def scaled_dot_product_attention(query, key, value, attn_mask=None, dropout_p=0.0,
+                                 is_causal=False, scale=None, use_flash=False, block_size=64):
+    """Materialised attention (_core.py:1606-1683): scores = q k^T * scale, causal fill
+    -1e9, softmax, @ v — each step an autograd op (GEMM and softmax kernels)."""
+    if use_flash and query.shape[-2] > block_size:
+        return flash_attention(query, key, value, block_size=block_size, is_causal=is_causal,
+                               scale=scale, dropout_p=dropout_p)
+    squeeze = query.ndim == 3
+    if squeeze:
+        query, key, value = query.unsqueeze(1), key.unsqueeze(1), value.unsqueeze(1)
+    B, H, Lq, D = query.shape
+    S = key.shape[2]
+    scale = scale or D ** -0.5
+    scores = (query @ key.transpose(0, 1, 3, 2)) * scale
+    if is_causal:
+        m = torch.triu(torch.ones(Lq, S, dtype=torch.bool, device="cuda"), diagonal=1)
+        scores.data = torch.where(m, torch.tensor(-1e9, dtype=scores.data.dtype, device="cuda"),
+                                  scores.data)
+    if attn_mask is not None:
+        am = attn_mask.data if isinstance(attn_mask, Tensor) else torch.as_tensor(
+            np.asarray(attn_mask), device="cuda")
+        scores.data = scores.data + am.to(scores.data.dtype)
+    attn = scores.softmax(axis=-1)
+    if dropout_p > 0 and cfg._grad_enabled:
+        keep = (torch.rand(attn.shape, device="cuda") > dropout_p).float() / (1 - dropout_p)
+        attn = attn * Tensor(keep, requires_grad=False)
+    o = attn @ value
+    return o.squeeze(1) if squeeze else o
+
+
+def multi_head_attention(query, key, value, embed_dim, num_heads, q_proj, k_proj, v_proj,
+                         out_proj, attn_mask=None, dropout_p=0.0, is_causal=False):
+    """(_core.py:1873-1913)"""
+    B, Lq, _ = query.shape
+    S = key.shape[1]
+    hd = embed_dim // num_heads
+    q = q_proj(query).reshape(B, Lq, num_heads, hd).transpose(0, 2, 1, 3)
+    k = k_proj(key).reshape(B, S, num_heads, hd).transpose(0, 2, 1, 3)
+    v = v_proj(value).reshape(B, S, num_heads, hd).transpose(0, 2, 1, 3)
+    o = scaled_dot_product_attention(q, k, v, attn_mask, dropout_p, is_causal)
+    return out_proj(o.transpose(0, 2, 1, 3).reshape(B, Lq, embed_dim))
+
+
+def sync():
+    torch.cuda.synchronize()
+
+
+def memory_info():
+    used = torch.cuda.memory_allocated()
+    total = torch.cuda.memory_reserved()
+    return {"used_bytes": used, "total_bytes": total, "used_mb": used / 2 ** 20,
+            "total_mb": total / 2 ** 20, "n_free_blocks": 0}

@@ -26,6 +26,7 @@ _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int
 _f32 = ctypes.c_float
+_f64 = ctypes.c_double
 _sz = ctypes.c_size_t
 
 # name -> (restype, argtypes).  Mirrors include/tgbwd.h one to one.
@@ -53,8 +54,8 @@ SIGNATURES = {
                                       _i64, _i64, _i64, _f32, _i32, _vp, _sz, _vp]),
     "tg_batchnorm_bwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
                                 _i64, _i32, _i32, _i32, _vp, _sz, _vp]),
-    "tg_adam_step": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _f32, _f32, _f32, _f32, _f32,
-                            _f32, _f32, _vp]),
+    "tg_adam_step": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _f64, _f64, _f64, _f64, _f64,
+                            _f64, _f64, _vp]),
     "tg_unscale_check": (_i32, [_i32, _i32, _vp, _vp, _f32, _i32, _vp, _vp]),
     "tg_grad_norm_workspace": (_sz, [_i32, _vp]),
     "tg_grad_norm": (_i32, [_i32, _i32, _vp, _vp, _i32, _f32, _vp, _vp, _vp, _sz, _vp]),

@@ -1,0 +1,715 @@
+"""Modules, losses, optimizers and gradient tools (reference: tensor_gpu_v2/_nn.py).
+
+The modules on the backward hot path — Linear (matmul + bias reduction),
+LayerNorm, BatchNorm2D / FusedBatchNormReLU, Adam/AdamW, clip_grad_norm_,
+GradScaler — run their gradient math in libtgbwd's HIP kernels.
+"""
+import math
+import warnings
+
+import numpy as np
+import torch
+
+from . import _config as cfg
+from . import _lib as L
+from ._core import Tensor
+
+
+def _targets(tensors):
+    """Grad buffers for kernels that write several gradients with one accumulate
+    flag: returns (buffers, accumulate); a tensor without grad yields None."""
+    live = [t for t in tensors if t is not None and t._has_grad()]
+    if live and all(t._gz for t in live):
+        return [t._grad_target()[0] if (t is not None and t._has_grad()) else None
+                for t in tensors], False
+    bufs = []
+    for t in tensors:
+        bufs.append(t.grad if (t is not None and t._has_grad()) else None)
+    return bufs, True
+
+
+# ============================================================================ Module
+class Module:
+    """Module base (_nn.py:24-255): parameter discovery over public attributes."""
+
+    def __init__(self):
+        self._device = cfg.get_device()
+        self._training = True
+
+    def __call__(self, *args, **kwargs):
+        return self.forward(*args, **kwargs)
+
+    def forward(self, *args, **kwargs):
+        raise NotImplementedError
+
+    def zero_grad(self):
+        for p in self.parameters():
+            if p._has_grad():
+                p.zero_grad()
+
+    def named_parameters(self):
+        params, seen = [], set()
+        for name in dir(self):
+            if name.startswith("_"):
+                continue
+            try:
+                attr = getattr(self, name)
+            except AttributeError:
+                continue
+            if isinstance(attr, Tensor) and attr._requires_grad:
+                if id(attr) not in seen:
+                    params.append((name, attr))
+                    seen.add(id(attr))
+            elif isinstance(attr, Module) and attr is not self:
+                for cn, cp in attr.named_parameters():
+                    if id(cp) not in seen:
+                        params.append((f"{name}.{cn}", cp))
+                        seen.add(id(cp))
+            elif isinstance(attr, (list, tuple)):
+                for i, item in enumerate(attr):
+                    if isinstance(item, Module):
+                        for cn, cp in item.named_parameters():
+                            if id(cp) not in seen:
+                                params.append((f"{name}.{i}.{cn}", cp))
+                                seen.add(id(cp))
+        return params
+
+    def parameters(self):
+        return [p for _, p in self.named_parameters()]
+
+    def named_modules(self, memo=None, prefix=""):
+        if memo is None:
+            memo = set()
+        if id(self) in memo:
+            return
+        memo.add(id(self))
+        yield prefix, self
+        for name in dir(self):
+            if name.startswith("_"):
+                continue
+            try:
+                attr = getattr(self, name)
+            except AttributeError:
+                continue
+            if isinstance(attr, Module) and attr is not self:
+                yield from attr.named_modules(memo, prefix + ("." if prefix else "") + name)
+
+    def _children(self):
+        for name in dir(self):
+            if name.startswith("_"):
+                continue
+            try:
+                attr = getattr(self, name)
+            except AttributeError:
+                continue
+            if isinstance(attr, Module) and attr is not self:
+                yield attr
+            elif isinstance(attr, (list, tuple)):
+                for it in attr:
+                    if isinstance(it, Module):
+                        yield it
+
+    def train(self):
+        self._training = True
+        for c in self._children():
+            c.train()
+        return self
+
+    def eval(self):
+        self._training = False
+        for c in self._children():
+            c.eval()
+        return self
+
+    def to(self, device):
+        cfg._canonicalize_device(device)
+        return self
+
+    def cuda(self):
+        return self
+
+    def num_parameters(self):
+        return sum(p.size for p in self.parameters())
+
+    def state_dict(self):
+        """`param_{i}` keys in parameters() order (_nn.py:180-185)."""
+        return {f"param_{i}": p.numpy() for i, p in enumerate(self.parameters())}
+
+    def load_state_dict(self, state):
+        for i, p in enumerate(self.parameters()):
+            k = f"param_{i}"
+            if k in state:
+                p.data = torch.as_tensor(np.asarray(state[k]), device="cuda").to(p.data.dtype)
+
+    def __repr__(self):
+        return f"{self.__class__.__name__}()"
+
+
+# ============================================================================ Linear
+class Linear(Module):
+    """y = x @ w + b with w [nin, nout] (_nn.py:258-285).  Initialisation draws
+    w ~ N(0,1)*sqrt(2/nin) from NumPy's global RNG (the reference draws from the
+    array module's RNG), b = 0."""
+
+    def __init__(self, nin, nout, bias=True):
+        super().__init__()
+        scale = np.float32(np.sqrt(2.0 / nin))
+        self.w = Tensor(np.random.randn(nin, nout).astype(np.float32) * scale, dtype=np.float32)
+        self.use_bias = bias
+        self.b = Tensor(np.zeros(nout, dtype=np.float32), dtype=np.float32) if bias else None
+
+    def __call__(self, x):
+        out = x @ self.w
+        if self.use_bias:
+            out = out + self.b
+        return out
+
+    def parameters(self):
+        return [self.w, self.b] if self.use_bias else [self.w]
+
+    def __repr__(self):
+        nin, nout = self.w.shape
+        return f"Linear(in_features={nin}, out_features={nout}, bias={self.use_bias})"
+
+
+# ============================================================================ norms
+class LayerNorm(Module):
+    """LayerNorm over the trailing `normalized_shape` (_nn.py:885-951); forward saves
+    mean/rstd per row, backward runs tg_layernorm_bwd (dx, dgamma, dbeta in one pass
+    plus a partial-sum reduction)."""
+
+    def __init__(self, normalized_shape, eps=1e-5):
+        super().__init__()
+        if isinstance(normalized_shape, int):
+            normalized_shape = (normalized_shape,)
+        self.normalized_shape = tuple(normalized_shape)
+        self.eps = eps
+        size = int(np.prod(self.normalized_shape))
+        self.gamma = Tensor(np.ones(size, dtype=np.float32), dtype=np.float32)
+        self.beta = Tensor(np.zeros(size, dtype=np.float32), dtype=np.float32)
+
+    def __call__(self, x):
+        nd = len(self.normalized_shape)
+        if tuple(x.shape[-nd:]) != self.normalized_shape:
+            raise ValueError(f"LayerNorm expects trailing shape {self.normalized_shape}, "
+                             f"got {x.shape}")
+        xd = x.data.contiguous()
+        if xd.dtype not in L._TORCH_TO_CODE:
+            raise TypeError(f"LayerNorm: unsupported dtype {xd.dtype}")
+        g32 = self.gamma.data.float().contiguous()
+        b32 = self.beta.data.float().contiguous()
+        y, mean, rstd = L.layernorm_fwd(xd, g32, b32, self.eps)
+        out = Tensor._wrap(y, (x, self.gamma, self.beta), "LayerNorm")
+        self._cache = (mean, rstd)
+        gamma, beta = self.gamma, self.beta
+
+        if out._requires_grad:
+            def _backward():
+                dy = out._grad_out()
+                if dy.dtype != xd.dtype or not dy.is_contiguous():
+                    dy = dy.to(xd.dtype).contiguous()
+                (dg, db), accp = _targets([gamma, beta])
+                if dg is not None and dg.dtype != torch.float32 or db is not None and db.dtype != torch.float32:
+                    raise TypeError("LayerNorm parameters must be float32")
+                if x._has_grad():
+                    dx, accx = x._grad_target()
+                    L.layernorm_bwd(xd, mean, rstd, g32, dy, dx, dg, db, accx, accp)
+                else:
+                    L.layernorm_bwd(xd, mean, rstd, g32, dy, torch.empty_like(xd), dg, db,
+                                    False, accp)
+            out._backward = _backward
+        return out
+
+    def parameters(self):
+        return [self.gamma, self.beta]
+
+    def __repr__(self):
+        return f"LayerNorm({self.normalized_shape}, eps={self.eps})"
+
+
+class _BatchNormBase(Module):
+    _relu = False
+
+    def __init__(self, num_features, eps=1e-5, momentum=0.1, data_format="NCHW"):
+        super().__init__()
+        if data_format not in ("NCHW", "NHWC"):
+            raise ValueError("data_format must be 'NCHW' or 'NHWC'")
+        self.num_features = num_features
+        self.eps = eps
+        self.momentum = momentum
+        self.data_format = data_format
+        self.gamma = Tensor(np.ones(num_features, dtype=np.float32), dtype=np.float32)
+        self.beta = Tensor(np.zeros(num_features, dtype=np.float32), dtype=np.float32)
+        self.running_mean = torch.zeros(num_features, dtype=torch.float32, device="cuda")
+        self.running_var = torch.ones(num_features, dtype=torch.float32, device="cuda")
+
+    def _layout(self):
+        return L.NHWC if self.data_format == "NHWC" else L.NCHW
+
+    def __call__(self, x):
+        if x.ndim != 4:
+            raise ValueError(f"{type(self).__name__} expects a 4-D input, got {x.shape}")
+        xd = x.data.contiguous()
+        if xd.dtype != torch.float32:
+            xd = xd.float()
+        C = xd.shape[3] if self.data_format == "NHWC" else xd.shape[1]
+        if C != self.num_features:
+            raise ValueError(f"expected {self.num_features} channels, got {C}")
+        gamma, beta = self.gamma, self.beta
+        g32 = gamma.data.float().contiguous()
+        b32 = beta.data.float().contiguous()
+        if not self._training:
+            return self._eval_forward(xd, g32, b32)
+        y, mean, rstd, var = L.batchnorm_fwd_train(
+            xd, g32, b32, self.eps, self.momentum, self.running_mean, self.running_var,
+            self._relu, self._layout())
+        out = Tensor._wrap(y, (x, gamma, beta), type(self).__name__)
+        self._cache = (mean, rstd)
+        relu, layout = self._relu, self._layout()
+
+        if out._requires_grad:
+            def _backward():
+                dy = out._grad_out()
+                if dy.dtype != torch.float32 or not dy.is_contiguous():
+                    dy = dy.float().contiguous()
+                (dg, db), accp = _targets([gamma, beta])
+                if x._has_grad() and x.data.dtype == torch.float32:
+                    dx, accx = x._grad_target()
+                    L.batchnorm_bwd(xd, mean, rstd, g32, b32, dy, dx, dg, db, relu, accx, accp,
+                                    layout)
+                else:
+                    dx = L.batchnorm_bwd(xd, mean, rstd, g32, b32, dy, torch.empty_like(xd), dg,
+                                         db, relu, False, accp, layout)
+                    if x._has_grad():
+                        x._accumulate(dx, True)
+            out._backward = _backward
+        return out
+
+    def _eval_forward(self, xd, g32, b32):
+        inv = 1.0 / torch.sqrt(self.running_var + self.eps)
+        scale = g32 * inv
+        shift = b32 - g32 * self.running_mean * inv
+        shp = (1, 1, 1, -1) if self.data_format == "NHWC" else (1, -1, 1, 1)
+        y = xd * scale.reshape(shp) + shift.reshape(shp)
+        if self._relu:
+            y = torch.clamp_min(y, 0)
+        return Tensor(y, requires_grad=False)
+
+    def parameters(self):
+        return [self.gamma, self.beta]
+
+    def __repr__(self):
+        return (f"{type(self).__name__}({self.num_features}, eps={self.eps}, "
+                f"momentum={self.momentum})")
+
+
+class BatchNorm2D(_BatchNormBase):
+    """BatchNorm over (N,H,W) per channel (_nn.py:681-747); data_format 'NCHW'
+    (the reference layout) or 'NHWC'."""
+    _relu = False
+
+
+class FusedBatchNormReLU(_BatchNormBase):
+    """Training-mode BatchNorm + ReLU (_nn.py:750-882) with the backward of
+    _nn.py:812-833 fused into two HBM passes (tg_batchnorm_bwd).  data_format
+    'NCHW' matches the reference; 'NHWC' is the channel-last layout."""
+    _relu = True
+
+
+# ============================================================================ misc modules
+class Dropout(Module):
+    """(_nn.py:1027-1058)"""
+
+    def __init__(self, p=0.5):
+        super().__init__()
+        self.p = p
+
+    def __call__(self, x):
+        if not self._training or self.p == 0:
+            return x
+        if self.p >= 1.0:
+            return Tensor._wrap(torch.zeros_like(x.data), (x,), "Dropout")
+        mask = (torch.rand(x.data.shape, device="cuda") > self.p).to(x.data.dtype)
+        scale = 1.0 / (1.0 - self.p)
+        out = Tensor._wrap(x.data * mask * scale, (x,), "Dropout")
+        if out._requires_grad:
+            def _backward():
+                if x._has_grad():
+                    x._accumulate(out._grad_out() * mask * scale, True)
+            out._backward = _backward
+        return out
+
+
+class Embedding(Module):
+    """Lookup table (_nn.py:1061-1092): forward gathers rows, backward scatter-adds
+    the output gradient rows into weight.grad (repeated indices accumulate)."""
+
+    def __init__(self, num_embeddings, embedding_dim):
+        super().__init__()
+        self.weight = Tensor(np.random.randn(num_embeddings, embedding_dim).astype(np.float32)
+                             * np.float32(0.01), dtype=np.float32)
+        self.num_embeddings = num_embeddings
+        self.embedding_dim = embedding_dim
+
+    def __call__(self, indices):
+        idx = indices.data if isinstance(indices, Tensor) else torch.as_tensor(
+            np.asarray(indices), device="cuda")
+        idx = idx.to(device="cuda", dtype=torch.int64)
+        weight = self.weight
+        out = Tensor._wrap(weight.data[idx], (weight,), "Embedding")
+        dim = self.embedding_dim
+        if out._requires_grad:
+            def _backward():
+                if not weight._has_grad():
+                    return
+                g = out._grad_out().reshape(-1, dim)
+                buf = weight.grad
+                buf.index_add_(0, idx.reshape(-1), g.to(buf.dtype))
+            out._backward = _backward
+        return out
+
+    def parameters(self):
+        return [self.weight]
+
+
+# ============================================================================ losses
+class MSELoss(Module):
+    def __init__(self, reduction="mean"):
+        super().__init__()
+        self.reduction = reduction
+
+    def __call__(self, y_pred, y_true):
+        if not isinstance(y_true, Tensor):
+            y_true = Tensor(y_true, requires_grad=False)
+        sq = (y_pred - y_true) ** 2
+        if self.reduction == "mean":
+            return sq.mean()
+        if self.reduction == "sum":
+            return sq.sum()
+        return sq
+
+
+class CrossEntropyLoss(Module):
+    """Cross-entropy over logits [N, C] (_nn.py:1128-1185).  As in the reference,
+    the backward writes (softmax - onehot)/N (mean) into logits.grad without
+    multiplying by the loss's upstream gradient (_nn.py:1168-1180)."""
+
+    def __init__(self, reduction="mean", label_smoothing=0.0):
+        super().__init__()
+        self.reduction = reduction
+        self.label_smoothing = label_smoothing
+
+    def __call__(self, logits, targets):
+        ld = logits.data
+        N, C = ld.shape
+        tg = targets.data if isinstance(targets, Tensor) else torch.as_tensor(
+            np.asarray(targets), device="cuda")
+        tg = tg.to(device="cuda", dtype=torch.int64)
+        lf = ld.float()
+        probs = torch.softmax(lf, dim=1)
+        ar = torch.arange(N, device="cuda")
+        if self.label_smoothing > 0:
+            smooth = torch.full_like(probs, self.label_smoothing / C)
+            smooth[ar, tg] = 1 - self.label_smoothing + self.label_smoothing / C
+            loss = -(smooth * torch.log(probs + 1e-10)).sum(dim=1)
+        else:
+            smooth = None
+            loss = -torch.log(probs[ar, tg] + 1e-10)
+        if self.reduction == "mean":
+            lv = loss.mean()
+        elif self.reduction == "sum":
+            lv = loss.sum()
+        else:
+            lv = loss
+        out = Tensor._wrap(lv.to(ld.dtype), (logits,), "CrossEntropy")
+        reduction = self.reduction
+        if out._requires_grad:
+            def _backward():
+                if not logits._has_grad():
+                    return
+                g = probs.clone()
+                if smooth is not None:
+                    g -= smooth
+                else:
+                    g[ar, tg] -= 1
+                if reduction == "mean":
+                    g /= N
+                logits._accumulate(g.to(ld.dtype), True)
+            out._backward = _backward
+        return out
+
+
+# ============================================================================ optimizers
+class SGD:
+    """(_nn.py:1316-1374)"""
+
+    def __init__(self, params, lr=0.01, momentum=0.0, weight_decay=0.0, nesterov=False):
+        self.params = list(params)
+        self.lr, self.momentum, self.weight_decay, self.nesterov = lr, momentum, weight_decay, nesterov
+        self._device = "cuda"
+        self.velocities = [torch.zeros_like(p.data) for p in self.params]
+
+    def step(self):
+        for i, p in enumerate(self.params):
+            if not p._has_grad():
+                continue
+            g = p.grad
+            if self.weight_decay > 0:
+                g = g + self.weight_decay * p.data
+            if self.momentum > 0:
+                self.velocities[i] = self.momentum * self.velocities[i] + g
+                upd = g + self.momentum * self.velocities[i] if self.nesterov else self.velocities[i]
+            else:
+                upd = g
+            p.data -= self.lr * upd
+
+    def zero_grad(self):
+        for p in self.params:
+            if p._has_grad():
+                p.zero_grad()
+
+
+class Adam:
+    """Adam with decoupled weight decay (_nn.py:1377-1480).  The step for every
+    fp32 parameter is one multi-tensor launch of tg_adam_step (28 B/param)."""
+
+    def __init__(self, params, lr=0.001, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.0,
+                 amsgrad=False):
+        self.params = list(params)
+        self.lr = lr
+        self.beta1, self.beta2 = betas
+        self.eps = eps
+        self.weight_decay = weight_decay
+        self.amsgrad = amsgrad
+        self._device = "cuda"
+        self.m = [torch.zeros(p.data.shape, dtype=p.data.dtype, device="cuda") for p in self.params]
+        self.v = [torch.zeros(p.data.shape, dtype=p.data.dtype, device="cuda") for p in self.params]
+        if amsgrad:
+            self.v_max = [torch.zeros_like(m) for m in self.m]
+        self.t = 0
+
+    def clip_grad_norm(self, max_norm=1.0):
+        """Global L2 clip without NaN handling (_nn.py:1396-1411)."""
+        grads = [p.grad for p in self.params if p._has_grad()]
+        if not grads:
+            return 0.0
+        sq, _ = L.grad_norm(grads, 0)
+        total = math.sqrt(sq)
+        if total > max_norm:
+            L.scale_(grads, max_norm / (total + 1e-6))
+        return total
+
+    def _apply(self, lr, wd):
+        self.t += 1
+        bc1 = 1 - self.beta1 ** self.t
+        bc2 = 1 - self.beta2 ** self.t
+        ps, gs, ms, vs, vms = [], [], [], [], []
+        for i, p in enumerate(self.params):
+            if not p._has_grad():
+                continue
+            if p.data.dtype != torch.float32 or not p.data.is_contiguous():
+                raise TypeError("Adam: parameters must be contiguous float32 device tensors")
+            g = p.grad
+            if g.dtype != torch.float32:
+                g = g.float()
+            ps.append(p.data)
+            gs.append(g)
+            ms.append(self.m[i])
+            vs.append(self.v[i])
+            if self.amsgrad:
+                vms.append(self.v_max[i])
+        L.adam_step(ps, gs, ms, vs, vms if self.amsgrad else None, lr, self.beta1, self.beta2,
+                    self.eps, wd, bc1, bc2)
+
+    def step(self, clip_grad_norm=None):
+        if clip_grad_norm is not None:
+            self.clip_grad_norm(clip_grad_norm)
+        self._apply(self.lr, self.weight_decay)
+
+    def zero_grad(self):
+        for p in self.params:
+            if p._has_grad():
+                p.zero_grad()
+
+    def state_dict(self):
+        st = {"lr": self.lr, "betas": (self.beta1, self.beta2), "eps": self.eps,
+              "weight_decay": self.weight_decay, "amsgrad": self.amsgrad, "t": self.t,
+              "m": [m.cpu().numpy() for m in self.m], "v": [v.cpu().numpy() for v in self.v]}
+        if self.amsgrad:
+            st["v_max"] = [vm.cpu().numpy() for vm in self.v_max]
+        return st
+
+    def load_state_dict(self, state):
+        self.lr = state.get("lr", self.lr)
+        self.t = state.get("t", self.t)
+        if "betas" in state:
+            self.beta1, self.beta2 = state["betas"]
+        self.eps = state.get("eps", self.eps)
+        self.weight_decay = state.get("weight_decay", self.weight_decay)
+        if "m" in state:
+            self.m = [torch.as_tensor(np.asarray(m, dtype=np.float32), device="cuda") for m in state["m"]]
+        if "v" in state:
+            self.v = [torch.as_tensor(np.asarray(v, dtype=np.float32), device="cuda") for v in state["v"]]
+        if self.amsgrad and "v_max" in state:
+            self.v_max = [torch.as_tensor(np.asarray(v, dtype=np.float32), device="cuda")
+                          for v in state["v_max"]]
+
+
+class AdamW(Adam):
+    """Adam with decoupled weight decay, default 0.01 (_nn.py:1483-1487)."""
+
+    def __init__(self, params, lr=0.001, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01):
+        super().__init__(params, lr, betas, eps, weight_decay)
+
+
+# ============================================================================ clipping
+def clip_grad_norm_(parameters, max_norm, norm_type=2.0, error_if_nonfinite=False):
+    """Global-norm clip (_nn.py:1563-1626): non-finite entries are zeroed (warning)
+    or raise; the norm is one multi-tensor reduction; grads are rescaled by
+    max_norm/(norm+1e-6) when that is < 1.  Returns the pre-clip norm."""
+    params = [p for p in parameters if p._has_grad()]
+    if not params:
+        return 0.0
+    grads = [p.grad for p in params]
+    if norm_type == float("inf"):
+        kind, pw = 1, 1.0
+    elif norm_type == 2.0:
+        kind, pw = 0, 2.0
+    else:
+        kind, pw = 2, float(norm_type)
+    value, flags = L.grad_norm(grads, kind, pw)
+    bad = [g for g, f in zip(grads, flags) if f & 1]
+    if bad:
+        if error_if_nonfinite:
+            raise RuntimeError("Gradient contains NaN or Inf values")
+        L.zero_nonfinite(bad)
+        warnings.warn("clip_grad_norm_: Found NaN/Inf in gradients, zeroed them. "
+                      "Consider reducing learning rate or checking loss computation.")
+    total = value if kind == 1 else value ** (1.0 / pw)
+    if total == 0.0:
+        return 0.0
+    coef = max_norm / (total + 1e-6)
+    if coef < 1.0:
+        L.scale_(grads, coef)
+    return total
+
+
+def clip_grad_value_(parameters, clip_value):
+    """(_nn.py:1629-1640)"""
+    for p in parameters:
+        if p._has_grad():
+            p.grad.clamp_(-clip_value, clip_value)
+
+
+# ============================================================================ GradScaler
+class GradScaler:
+    """Dynamic loss scaling (_nn.py:1713-1912).  unscale_ is one multi-tensor
+    kernel pass (scale + non-finite flags) and one flag read-back instead of the
+    reference's per-parameter host checks; the scale state machine is unchanged."""
+
+    def __init__(self, init_scale=65536.0, growth_factor=2.0, backoff_factor=0.5,
+                 growth_interval=2000, min_scale=1.0, max_scale=2 ** 24, enabled=True):
+        if init_scale <= 0:
+            raise ValueError(f"init_scale must be positive, got {init_scale}")
+        if min_scale <= 0:
+            raise ValueError(f"min_scale must be positive, got {min_scale}")
+        if max_scale < init_scale:
+            raise ValueError(f"max_scale ({max_scale}) must be >= init_scale ({init_scale})")
+        self._scale = init_scale
+        self.growth_factor = growth_factor
+        self.backoff_factor = backoff_factor
+        self.growth_interval = growth_interval
+        self.min_scale = min_scale
+        self.max_scale = max_scale
+        self.enabled = enabled
+        self._growth_tracker = 0
+        self._found_inf = False
+        self._overflow_count = 0
+        self._step_count = 0
+        self._consecutive_successes = 0
+
+    def scale(self, loss):
+        if not self.enabled:
+            return loss
+        return loss * self._scale
+
+    def unscale_(self, optimizer, zero_nan_grads=True):
+        if not self.enabled:
+            return
+        if getattr(optimizer, "_is_unscaled", False):
+            return
+        inv = 1.0 / self._scale
+        self._found_inf = False
+        params = [p for p in optimizer.params if p._has_grad()]
+        grads = [p.grad for p in params]
+        if grads:
+            if zero_nan_grads:
+                flags = L.unscale_check(grads, inv, write=True)
+                bad = [g for g, f in zip(grads, flags) if f]
+            else:
+                pre = L.unscale_check(grads, 1.0, write=False)
+                clean = [g for g, f in zip(grads, pre) if not (f & 1)]
+                post = L.unscale_check(clean, inv, write=True) if clean else []
+                bad = [1] * sum(1 for f in pre if f & 1) + [1 for f in post if f]
+            if bad:
+                self._found_inf = True
+                if zero_nan_grads:
+                    for g in bad:
+                        L.fill(g, 0.0)
+        optimizer._is_unscaled = True
+
+    def step(self, optimizer, clip_grad_norm=None):
+        if not self.enabled:
+            optimizer.step(clip_grad_norm=clip_grad_norm)
+            return
+        if not getattr(optimizer, "_is_unscaled", False):
+            self.unscale_(optimizer)
+        if self._found_inf:
+            optimizer._is_unscaled = False
+            return
+        optimizer.step(clip_grad_norm=clip_grad_norm)
+        optimizer._is_unscaled = False
+
+    def update(self):
+        if not self.enabled:
+            return
+        self._step_count += 1
+        if self._found_inf:
+            self._overflow_count += 1
+            self._consecutive_successes = 0
+            self._scale = max(self._scale * self.backoff_factor, self.min_scale)
+            self._growth_tracker = 0
+        else:
+            self._consecutive_successes += 1
+            self._growth_tracker += 1
+            if self._growth_tracker >= self.growth_interval:
+                self._scale = min(self._scale * self.growth_factor, self.max_scale)
+                self._growth_tracker = 0
+
+    @property
+    def scale_factor(self):
+        return self._scale
+
+    def get_scale(self):
+        return self._scale
+
+    def state_dict(self):
+        return {"scale": self._scale, "growth_tracker": self._growth_tracker,
+                "overflow_count": self._overflow_count, "step_count": self._step_count,
+                "consecutive_successes": self._consecutive_successes}
+
+    def load_state_dict(self, state):
+        s = state.get("scale", self._scale)
+        if s <= 0:
+            raise ValueError(f"Checkpoint contains invalid scale ({s}), must be positive")
+        self._scale = s
+        self._growth_tracker = state.get("growth_tracker", 0)
+        self._overflow_count = state.get("overflow_count", 0)
+        self._step_count = state.get("step_count", 0)
+        self._consecutive_successes = state.get("consecutive_successes", 0)
+
+    def get_statistics(self):
+        return {"current_scale": self._scale, "total_steps": self._step_count,
+                "overflow_count": self._overflow_count,
+                "overflow_rate": self._overflow_count / max(1, self._step_count),
+                "consecutive_successes": self._consecutive_successes}

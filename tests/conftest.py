@@ -1,0 +1,67 @@
+"""Test configuration: import paths, the `gpu` marker and tolerance helpers.
+
+Tolerances follow the parity bar of the build:
+  fp32 elementwise / reductions   rtol 1e-5
+  fp32 matmul / attention         rtol 1e-4
+  fp16/bf16 (autocast) paths      rtol 1e-2
+An element passes when |a - e| <= rtol*|e| + rtol*rms(e): the rms term stands in
+for the absolute tolerance that near-zero elements need (their relative error is
+undefined), scaled to the data so it cannot hide an O(1) mistake.
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(ROOT, "project-tensor_amd")
+for p in (ROOT, PKG):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+
+RTOL_F32 = 1e-5
+RTOL_F32_MM = 1e-4
+RTOL_F16 = 1e-2
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
+
+
+def to_np(x):
+    try:
+        import torch
+        if isinstance(x, torch.Tensor):
+            return x.detach().double().cpu().numpy()
+    except ImportError:
+        pass
+    return np.asarray(x, dtype=np.float64)
+
+
+def assert_close(actual, expected, rtol, what=""):
+    a = to_np(actual)
+    e = to_np(expected)
+    assert a.shape == e.shape, f"{what}: shape {a.shape} != {e.shape}"
+    assert np.all(np.isfinite(a)), f"{what}: non-finite values in result"
+    scale = float(np.sqrt(np.mean(e ** 2))) if e.size else 0.0
+    err = np.abs(a - e)
+    lim = rtol * np.abs(e) + rtol * scale
+    bad = err > lim
+    if bad.any():
+        i = np.unravel_index(np.argmax(err - lim), err.shape)
+        raise AssertionError(
+            f"{what}: {int(bad.sum())}/{a.size} elements outside rtol={rtol} "
+            f"(worst at {i}: got {a[i]!r}, want {e[i]!r}, rms {scale:.3e})")
+
+
+@pytest.fixture(scope="session")
+def cuda():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail("GPU test run without a visible GPU")
+    from tensor_gpu_v2 import _lib
+    _lib.ensure_device(0)
+    return torch.device("cuda", 0)

@@ -1,0 +1,111 @@
+"""FlashAttention forward/backward kernels vs the oracle (float64 on the same
+fp16/bf16-rounded inputs).  GPU only.
+
+Tolerance: fp16 rtol 1e-2 (the autocast bar); bf16 rtol 3e-2, because P and dS
+enter the second GEMMs rounded to bf16's 8-bit mantissa."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from conftest import GOLDEN, RTOL_F16, assert_close
+
+pytestmark = pytest.mark.gpu
+RTOL = {torch.float16: RTOL_F16, torch.bfloat16: 3e-2}
+
+
+def L():
+    from tensor_gpu_v2 import _lib
+    return _lib
+
+
+def rnd(shape, dt, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(shape, generator=g).to(dt).cuda()
+
+
+def f64(t):
+    return t.detach().double().cpu().numpy()
+
+
+def run(q, k, v, do, causal):
+    scale = q.shape[-1] ** -0.5
+    o, lse = L().flash_attn_fwd(q, k, v, scale, causal)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    L().flash_attn_bwd(q, k, v, o, do, lse, dq, dk, dv, scale, causal, False)
+    return o, lse, dq, dk, dv
+
+
+CASES = [(1, 2, 96, 96, 64), (2, 3, 128, 128, 64), (1, 2, 200, 200, 128), (1, 1, 33, 33, 64),
+         (1, 2, 100, 150, 64), (1, 1, 150, 70, 128), (2, 1, 256, 256, 128)]
+
+
+@pytest.mark.parametrize("B,H,Sq,Sk,D", CASES)
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_flash_vs_oracle(cuda, B, H, Sq, Sk, D, causal, dt):
+    q = rnd((B, H, Sq, D), dt, 1)
+    k = rnd((B, H, Sk, D), dt, 2)
+    v = rnd((B, H, Sk, D), dt, 3)
+    do = rnd((B, H, Sq, D), dt, 4)
+    o, lse, dq, dk, dv = run(q, k, v, do, causal)
+    oo, ll = O.flash_attention_fwd(f64(q), f64(k), f64(v), causal)
+    rt = RTOL[dt]
+    assert_close(o, oo, rt, "O")
+    assert_close(lse, ll, 1e-5, "lse")
+    # backward from the kernel's own O (as the reference closure uses its forward)
+    rq, rk, rv = O.flash_attention_bwd(f64(q), f64(k), f64(v), f64(do), causal)
+    assert_close(dq, rq, rt, "dQ")
+    assert_close(dk, rk, rt, "dK")
+    assert_close(dv, rv, rt, "dV")
+
+
+def test_flash_golden(cuda):
+    f = np.load(os.path.join(GOLDEN, "flash_attn.npz"), allow_pickle=False)
+    q, k, v, do = (torch.as_tensor(f[n]).cuda() for n in ("q", "k", "v", "do"))
+    for tag, causal in (("full", False), ("causal", True)):
+        o, lse, dq, dk, dv = run(q, k, v, do, causal)
+        assert_close(o, f[f"o_{tag}"], RTOL_F16, f"golden O {tag}")
+        assert_close(lse, f[f"lse_{tag}"], 1e-5, f"golden lse {tag}")
+        assert_close(dq, f[f"dq_{tag}"], RTOL_F16, f"golden dQ {tag}")
+        assert_close(dk, f[f"dk_{tag}"], RTOL_F16, f"golden dK {tag}")
+        assert_close(dv, f[f"dv_{tag}"], RTOL_F16, f"golden dV {tag}")
+
+
+def test_flash_accumulate(cuda):
+    q, k, v, do = (rnd((1, 2, 64, 64), torch.float16, s) for s in range(4))
+    scale = 0.125
+    o, lse = L().flash_attn_fwd(q, k, v, scale, True)
+    d1 = [torch.empty_like(q) for _ in range(3)]
+    L().flash_attn_bwd(q, k, v, o, do, lse, *d1, scale, True, False)
+    d2 = [t.clone() for t in d1]
+    L().flash_attn_bwd(q, k, v, o, do, lse, *d2, scale, True, True)
+    for a, b in zip(d1, d2):
+        assert_close(b, 2 * f64(a), RTOL_F16, "accumulate doubles")
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_flash_full_size_one_head(cuda, D, causal):
+    """C4 shape B=8, H=16, S=2048: the whole batch runs, one (b, h) slice is
+    checked against the oracle (size-independent per head)."""
+    B, H, S = 8, 16, 2048
+    q, k, v, do = (rnd((B, H, S, D), torch.float16, 10 + s) for s in range(4))
+    o, lse, dq, dk, dv = run(q, k, v, do, causal)
+    b, hh = 5, 11
+    sl = (slice(b, b + 1), slice(hh, hh + 1))
+    oo, ll = O.flash_attention_fwd(f64(q[sl]), f64(k[sl]), f64(v[sl]), causal)
+    assert_close(o[sl], oo, RTOL_F16, "O head")
+    rq, rk, rv = O.flash_attention_bwd(f64(q[sl]), f64(k[sl]), f64(v[sl]), f64(do[sl]), causal)
+    assert_close(dq[sl], rq, RTOL_F16, "dQ head")
+    assert_close(dk[sl], rk, RTOL_F16, "dK head")
+    assert_close(dv[sl], rv, RTOL_F16, "dV head")
+    assert torch.isfinite(dq).all() and torch.isfinite(dk).all() and torch.isfinite(dv).all()
+
+
+def test_flash_rejects_bad_shapes(cuda):
+    q = rnd((1, 1, 16, 96), torch.float16, 0)
+    with pytest.raises(RuntimeError, match="head dim"):
+        L().flash_attn_fwd(q, q, q, 0.1, False)

@@ -1,0 +1,372 @@
+"""Parity of every libtgbwd kernel with the oracle on seeded inputs, through the
+C-ABI (the _lib wrappers pass raw pointers to libtgbwd.so).  GPU only."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from conftest import GOLDEN, RTOL_F16, RTOL_F32, RTOL_F32_MM, assert_close
+
+pytestmark = pytest.mark.gpu
+
+F16S = [torch.float16, torch.bfloat16]
+
+
+def L():
+    from tensor_gpu_v2 import _lib
+    return _lib
+
+
+def dev(a, dtype=torch.float32):
+    return torch.as_tensor(np.ascontiguousarray(a)).to(device="cuda", dtype=dtype)
+
+
+def f64(t):
+    return t.detach().double().cpu().numpy()
+
+
+def golden(name):
+    return np.load(os.path.join(GOLDEN, name + ".npz"), allow_pickle=False)
+
+
+def misaligned(t):
+    """Same values, contiguous, but the data pointer is 4 bytes off 16-byte alignment."""
+    buf = torch.empty(t.numel() + 8, dtype=t.dtype, device=t.device)
+    v = buf[1:1 + t.numel()].view(t.shape)
+    v.copy_(t)
+    return v
+
+
+# ------------------------------------------------------------------ activations
+@pytest.mark.parametrize("kind", ["gelu", "silu"])
+@pytest.mark.parametrize("n", [0, 1, 7, 4096 * 4 + 3, 1 << 20])
+@pytest.mark.parametrize("acc", [False, True])
+def test_act_bwd_fp32(cuda, kind, n, acc):
+    rng = np.random.default_rng(n + 11)
+    x = rng.standard_normal(n) * 3
+    dy = rng.standard_normal(n)
+    base = rng.standard_normal(n)
+    xt, dyt = dev(x), dev(dy)
+    dx = dev(base) if acc else torch.full((n,), float("nan"), device="cuda")
+    L().act_bwd(kind, xt, dyt, dx, acc)
+    ref = (O.gelu_bwd if kind == "gelu" else O.silu_bwd)(f64(xt), f64(dyt))
+    if acc:
+        ref = ref + f64(dev(base))
+    assert_close(dx, ref, RTOL_F32, f"{kind} n={n}")
+
+
+@pytest.mark.parametrize("kind", ["gelu", "silu"])
+@pytest.mark.parametrize("dt", F16S)
+def test_act_bwd_half(cuda, kind, dt):
+    rng = np.random.default_rng(3)
+    x = dev(rng.standard_normal(10007) * 3, dt)
+    dy = dev(rng.standard_normal(10007), dt)
+    dx = torch.empty_like(x)
+    L().act_bwd(kind, x, dy, dx, False)
+    ref = (O.gelu_bwd if kind == "gelu" else O.silu_bwd)(f64(x), f64(dy))
+    assert_close(dx, ref, RTOL_F16, f"{kind} {dt}")
+
+
+def test_act_bwd_misaligned_and_golden(cuda):
+    f = golden("act_bwd")
+    x, dy = misaligned(dev(f["x"])), misaligned(dev(f["dy"]))
+    for kind in ("gelu", "silu"):
+        dx = misaligned(torch.zeros(x.numel(), device="cuda"))
+        L().act_bwd(kind, x, dy, dx, False)
+        assert_close(dx, f[kind], RTOL_F32, f"golden {kind}")
+
+
+@pytest.mark.parametrize("kind", ["gelu", "silu"])
+def test_act_fwd(cuda, kind):
+    x = dev(np.random.default_rng(0).standard_normal(5003) * 4)
+    y = L().act_fwd(kind, x)
+    ref = (O.gelu_fwd if kind == "gelu" else O.silu_fwd)(f64(x))
+    assert_close(y, ref, RTOL_F32, kind)
+
+
+# ------------------------------------------------------------------ softmax
+SOFTMAX_SHAPES = [(1, 1), (3, 10), (64, 4096), (7, 1000), (5, 12288), (2, 40000), (130, 64)]
+
+
+@pytest.mark.parametrize("shape", SOFTMAX_SHAPES)
+@pytest.mark.parametrize("acc", [False, True])
+def test_softmax_fp32(cuda, shape, acc):
+    rng = np.random.default_rng(sum(shape))
+    lg = dev(rng.standard_normal(shape) * 2)
+    y = L().softmax_fwd(lg)
+    assert_close(y, O.softmax_fwd(f64(lg)), RTOL_F32, f"softmax fwd {shape}")
+    dy = dev(rng.standard_normal(shape))
+    base = dev(rng.standard_normal(shape))
+    dx = base.clone() if acc else torch.empty_like(y)
+    L().softmax_bwd(y, dy, dx, acc)
+    ref = O.softmax_bwd(f64(y), f64(dy)) + (f64(base) if acc else 0)
+    assert_close(dx, ref, RTOL_F32, f"softmax bwd {shape}")
+
+
+@pytest.mark.parametrize("dt", F16S)
+def test_softmax_half(cuda, dt):
+    rng = np.random.default_rng(9)
+    lg = dev(rng.standard_normal((33, 2048)) * 2, dt)
+    y = L().softmax_fwd(lg)
+    assert_close(y, O.softmax_fwd(f64(lg)), RTOL_F16, "softmax fwd half")
+    dy = dev(rng.standard_normal((33, 2048)), dt)
+    dx = torch.empty_like(y)
+    L().softmax_bwd(y, dy, dx, False)
+    assert_close(dx, O.softmax_bwd(f64(y), f64(dy)), RTOL_F16, "softmax bwd half")
+
+
+def test_softmax_golden(cuda):
+    f = golden("softmax")
+    y = L().softmax_fwd(dev(f["logits"]))
+    assert_close(y, f["y"], RTOL_F32, "golden softmax fwd")
+    dx = torch.empty_like(y)
+    L().softmax_bwd(dev(f["y"]), dev(f["dy"]), dx, False)
+    assert_close(dx, f["dx"], RTOL_F32, "golden softmax bwd")
+
+
+# ------------------------------------------------------------------ layer norm
+LN_SHAPES = [(1, 8), (37, 1024), (8, 4096), (3, 100), (2, 20000), (300, 256), (5, 8192)]
+
+
+def ln_ref(x, g, b, dy, eps=1e-5):
+    y, xh, mean, var = O.layernorm_fwd(x, g, b, eps)
+    dx, dg, db = O.layernorm_bwd(xh, var, g, dy, eps)
+    return y, dx, dg, db
+
+
+@pytest.mark.parametrize("shape", LN_SHAPES)
+@pytest.mark.parametrize("acc", [False, True])
+def test_layernorm_fp32(cuda, shape, acc):
+    rows, cols = shape
+    rng = np.random.default_rng(rows * 7 + cols)
+    x = dev(rng.standard_normal(shape))
+    g = dev(1 + 0.02 * rng.standard_normal(cols))
+    b = dev(0.02 * rng.standard_normal(cols))
+    dy = dev(rng.standard_normal(shape))
+    y, mean, rstd = L().layernorm_fwd(x, g, b, 1e-5)
+    yr, dxr, dgr, dbr = ln_ref(f64(x), f64(g), f64(b), f64(dy))
+    assert_close(y, yr, RTOL_F32, f"ln fwd {shape}")
+    bx, bg, bb = dev(rng.standard_normal(shape)), dev(rng.standard_normal(cols)), dev(rng.standard_normal(cols))
+    dx = bx.clone() if acc else torch.empty_like(x)
+    dg = bg.clone() if acc else torch.empty_like(g)
+    db = bb.clone() if acc else torch.empty_like(b)
+    L().layernorm_bwd(x, mean, rstd, g, dy, dx, dg, db, acc, acc)
+    a = 1.0 if acc else 0.0
+    assert_close(dx, dxr + a * f64(bx), RTOL_F32, f"ln dx {shape}")
+    assert_close(dg, dgr + a * f64(bg), RTOL_F32, f"ln dgamma {shape}")
+    assert_close(db, dbr + a * f64(bb), RTOL_F32, f"ln dbeta {shape}")
+
+
+@pytest.mark.parametrize("dt", F16S)
+def test_layernorm_half(cuda, dt):
+    rng = np.random.default_rng(4)
+    x = dev(rng.standard_normal((64, 1024)), dt)
+    g = dev(1 + 0.02 * rng.standard_normal(1024))
+    b = dev(0.02 * rng.standard_normal(1024))
+    dy = dev(rng.standard_normal((64, 1024)), dt)
+    y, mean, rstd = L().layernorm_fwd(x, g, b, 1e-5)
+    yr, dxr, dgr, dbr = ln_ref(f64(x), f64(g), f64(b), f64(dy))
+    assert_close(y, yr, RTOL_F16, "ln fwd half")
+    dx = torch.empty_like(x)
+    dg, db = torch.empty_like(g), torch.empty_like(b)
+    L().layernorm_bwd(x, mean, rstd, g, dy, dx, dg, db, False, False)
+    assert_close(dx, dxr, RTOL_F16, "ln dx half")
+    assert_close(dg, dgr, RTOL_F16, "ln dgamma half")
+
+
+def test_layernorm_golden(cuda):
+    f = golden("layernorm")
+    x, g, b, dy = (dev(f[k]) for k in ("x", "gamma", "beta", "dy"))
+    y, mean, rstd = L().layernorm_fwd(x, g, b, 1e-5)
+    assert_close(y, f["y"], RTOL_F32, "golden ln y")
+    assert_close(mean, f["mean"], RTOL_F32, "golden ln mean")
+    assert_close(rstd, f["rstd"], RTOL_F32, "golden ln rstd")
+    dx, dg, db = torch.empty_like(x), torch.empty_like(g), torch.empty_like(b)
+    L().layernorm_bwd(x, mean, rstd, g, dy, dx, dg, db, False, False)
+    assert_close(dx, f["dx"], RTOL_F32, "golden ln dx")
+    assert_close(dg, f["dgamma"], RTOL_F32, "golden ln dgamma")
+    assert_close(db, f["dbeta"], RTOL_F32, "golden ln dbeta")
+
+
+# ------------------------------------------------------------------ batch norm
+BN_CASES = [("NHWC", (4, 7, 9, 64)), ("NHWC", (2, 5, 5, 6)), ("NHWC", (3, 4, 4, 300)),
+            ("NCHW", (4, 64, 7, 9)), ("NCHW", (3, 5, 4, 4)), ("NCHW", (2, 8, 3, 5))]
+
+
+def bn_inputs(layout, shape, seed):
+    rng = np.random.default_rng(seed)
+    C = shape[3] if layout == "NHWC" else shape[1]
+    x = dev(rng.standard_normal(shape))
+    g = dev(1 + 0.1 * rng.standard_normal(C))
+    b = dev(0.1 * rng.standard_normal(C))
+    dy = dev(rng.standard_normal(shape))
+    return x, g, b, dy, C
+
+
+@pytest.mark.parametrize("layout,shape", BN_CASES)
+@pytest.mark.parametrize("relu", [True, False])
+def test_batchnorm(cuda, layout, shape, relu):
+    x, g, b, dy, C = bn_inputs(layout, shape, sum(shape))
+    lay = L().NHWC if layout == "NHWC" else L().NCHW
+    rm, rv = torch.zeros(C, device="cuda"), torch.ones(C, device="cuda")
+    y, mean, rstd, var = L().batchnorm_fwd_train(x, g, b, 1e-5, 0.1, rm, rv, relu, lay)
+    if layout == "NHWC":
+        yr, cache = O.batchnorm_relu_fwd_nhwc(f64(x), f64(g), f64(b), 1e-5, relu)
+    else:
+        yr, cache = O.batchnorm_relu_fwd(f64(x), f64(g), f64(b), 1e-5, relu)
+    assert_close(y, yr, RTOL_F32, "bn y")
+    assert_close(mean, cache[5], RTOL_F32, "bn mean")
+    assert_close(var, cache[6], RTOL_F32, "bn var")
+    assert_close(rm, 0.1 * cache[5], RTOL_F32, "running mean")
+    assert_close(rv, 0.9 + 0.1 * cache[6], RTOL_F32, "running var")
+    # backward with the oracle's own statistics (float32) so both sides apply the
+    # same ReLU mask; the reference mask is out > 0 on the fp32 forward output
+    mean32 = dev(cache[5])
+    rstd32 = dev(1.0 / np.sqrt(cache[6] + 1e-5))
+    dx, dg, db = torch.empty_like(x), torch.empty_like(g), torch.empty_like(b)
+    L().batchnorm_bwd(x, mean32, rstd32, g, b, dy, dx, dg, db, relu, False, False, lay)
+    if layout == "NHWC":
+        dxr, dgr, dbr = O.batchnorm_relu_bwd_nhwc(f64(dy), f64(g), cache, relu)
+    else:
+        dxr, dgr, dbr = O.batchnorm_relu_bwd(f64(dy), f64(g), cache, relu)
+    assert_close(dx, dxr, RTOL_F32, "bn dx")
+    assert_close(dg, dgr, RTOL_F32, "bn dgamma")
+    assert_close(db, dbr, RTOL_F32, "bn dbeta")
+
+
+def test_batchnorm_accumulate_and_golden(cuda):
+    f = golden("bn_relu_nhwc")
+    x, g, b, dy = (dev(f[k]) for k in ("x", "gamma", "beta", "dy"))
+    rm, rv = torch.zeros(36, device="cuda"), torch.ones(36, device="cuda")
+    y, mean, rstd, _ = L().batchnorm_fwd_train(x, g, b, 1e-5, 0.1, rm, rv, True, L().NHWC)
+    assert_close(y, f["y"], RTOL_F32, "golden bn y")
+    dx, dg, db = torch.ones_like(x), torch.ones_like(g), torch.ones_like(b)
+    L().batchnorm_bwd(x, mean, rstd, g, b, dy, dx, dg, db, True, True, True, L().NHWC)
+    assert_close(dx, f["dx"] + 1.0, RTOL_F32, "golden bn dx (+1)")
+    assert_close(dg, f["dgamma"] + 1.0, RTOL_F32, "golden bn dgamma (+1)")
+    assert_close(db, f["dbeta"] + 1.0, RTOL_F32, "golden bn dbeta (+1)")
+
+
+# ------------------------------------------------------------------ column sums
+@pytest.mark.parametrize("rows,cols", [(1, 1), (32, 10), (8192, 1024), (1000, 4097), (3, 40000)])
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16])
+def test_reduce_rows(cuda, rows, cols, dt):
+    rng = np.random.default_rng(rows + cols)
+    g = dev(rng.standard_normal((rows, cols)), dt)
+    out = dev(rng.standard_normal(cols))
+    base = f64(out)
+    L().reduce_rows(g, out, True)
+    tol = RTOL_F32 if dt == torch.float32 else 1e-4
+    assert_close(out, base + f64(g).sum(0), tol, "reduce_rows acc")
+    L().reduce_rows(g, out, False)
+    assert_close(out, f64(g).sum(0), tol, "reduce_rows")
+
+
+# ------------------------------------------------------------------ GEMM
+GEMM_SHAPES = [(256, 256, 256), (100, 70, 50), (32, 256, 784), (130, 10, 256), (1, 1, 1),
+               (257, 129, 33), (64, 64, 0)]
+
+
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16, torch.bfloat16])
+def test_gemm(cuda, M, N, K, ta, tb, dt):
+    rng = np.random.default_rng(M * 3 + N * 5 + K)
+    a = dev(rng.standard_normal((K, M) if ta else (M, K)), dt)
+    b = dev(rng.standard_normal((N, K) if tb else (K, N)), dt)
+    c0 = dev(rng.standard_normal((M, N)))
+    c = c0.clone()
+    L().gemm(a, b, c, ta, tb, 0.5, 2.0, M, N, K, a.shape[1], b.shape[1], N)
+    A = f64(a).T if ta else f64(a)
+    B = f64(b).T if tb else f64(b)
+    ref = 0.5 * (A @ B) + 2.0 * f64(c0)
+    # products of dt-rounded inputs are exact in fp32 accumulation up to the sum order
+    assert_close(c, ref, RTOL_F32_MM, f"gemm {dt} {M}x{N}x{K} ta={ta} tb={tb}")
+
+
+def test_gemm_batched_broadcast_and_half_out(cuda):
+    rng = np.random.default_rng(1)
+    a = dev(rng.standard_normal((3, 40, 24)), torch.float16)
+    b = dev(rng.standard_normal((24, 56)), torch.float16)
+    c = torch.empty(3, 40, 56, dtype=torch.float16, device="cuda")
+    L().gemm(a, b, c, False, False, 1.0, 0.0, 40, 56, 24, 24, 56, 56, 40 * 24, 0, 40 * 56, 3)
+    assert_close(c, f64(a) @ f64(b), RTOL_F16, "batched gemm, B broadcast")
+
+
+# ------------------------------------------------------------------ Adam / AdamW
+@pytest.mark.parametrize("amsgrad", [False, True])
+def test_adam_multi_tensor(cuda, amsgrad):
+    rng = np.random.default_rng(2)
+    sizes = [1, 3, 4096, 10007, 0, 65, 25 * 4096]
+    ps = [dev(rng.standard_normal(n)) for n in sizes]
+    ms = [torch.zeros_like(p) for p in ps]
+    vs = [torch.zeros_like(p) for p in ps]
+    vms = [torch.zeros_like(p) for p in ps] if amsgrad else None
+    ref = [(f64(p), np.zeros(p.numel()), np.zeros(p.numel()), np.zeros(p.numel())) for p in ps]
+    for t in range(1, 4):
+        gs = [dev(rng.standard_normal(n) * 1e-2) for n in sizes]
+        L().adam_step(ps, gs, ms, vs, vms, 3e-4, 0.9, 0.999, 1e-8, 0.1, 1 - 0.9 ** t, 1 - 0.999 ** t)
+        ref = [O.adam_step(p, f64(g), m, v, t, lr=3e-4, weight_decay=0.1, amsgrad=amsgrad,
+                           v_max=vm)
+               for (p, m, v, vm), g in zip(ref, gs)]
+    for p, m, v, r in zip(ps, ms, vs, ref):
+        assert_close(p, r[0], RTOL_F32, "adam p")
+        assert_close(m, r[1], RTOL_F32, "adam m")
+        assert_close(v, r[2], RTOL_F32, "adam v")
+
+
+def test_adamw_golden(cuda):
+    f = golden("adamw3")
+    p = dev(f["p0"])
+    m, v = torch.zeros_like(p), torch.zeros_like(p)
+    for t, g in enumerate(f["g"], start=1):
+        L().adam_step([p], [dev(g)], [m], [v], None, 3e-4, 0.9, 0.999, 1e-8, 0.1,
+                      1 - 0.9 ** t, 1 - 0.999 ** t)
+    assert_close(p, f["p"], RTOL_F32, "golden adamw p")
+    assert_close(m, f["m"], RTOL_F32, "golden adamw m")
+
+
+# ------------------------------------------------------------------ GradScaler kernels
+def test_unscale_check_bit_exact(cuda):
+    rng = np.random.default_rng(5)
+    host = [rng.standard_normal(n).astype(np.float32) * 1e3 for n in (1000, 5000, 7, 40000)]
+    host[1][17] = np.inf
+    host[3][39999] = np.nan
+    gs = [dev(h) for h in host]
+    inv = np.float32(1.0 / 65536.0)
+    flags = L().unscale_check(gs, float(inv))
+    assert flags == [0, 3, 0, 3]
+    for g, h in zip(gs, host):
+        want = h * inv  # fp32 multiply, as the kernel
+        got = g.cpu().numpy()
+        fin = np.isfinite(want)
+        assert np.array_equal(got[fin], want[fin])
+        assert np.array_equal(np.isnan(got), np.isnan(want))
+    # overflow after scaling (mul > 1) sets bit 1 only
+    big = [dev(np.array([3e38, 1.0], np.float32))]
+    assert L().unscale_check(big, 4.0) == [2]
+    # fp16 grads: finite input that overflows fp16 after scaling
+    h16 = [dev(np.array([60000.0, 1.0]), torch.float16)]
+    assert L().unscale_check(h16, 2.0) == [2]
+
+
+@pytest.mark.parametrize("kind", [0, 1, 2])
+def test_grad_norm(cuda, kind):
+    rng = np.random.default_rng(6)
+    host = [rng.standard_normal(n).astype(np.float32) for n in (10, 4096, 70000, 1)]
+    host[2][5] = np.nan
+    gs = [dev(h) for h in host]
+    val, flags = L().grad_norm(gs, kind, 3.0)
+    fin = [np.where(np.isfinite(h), h, 0).astype(np.float64) for h in host]
+    if kind == 0:
+        want = sum((f ** 2).sum() for f in fin)
+    elif kind == 1:
+        want = max(np.abs(f).max() for f in fin)
+    else:
+        want = sum((np.abs(f) ** 3).sum() for f in fin)
+    assert abs(val - want) <= 1e-9 * abs(want)
+    assert flags == [0, 0, 1, 0]
+    L().zero_nonfinite(gs)
+    assert np.array_equal(gs[2].cpu().numpy(), fin[2].astype(np.float32))
