@@ -44,6 +44,10 @@ __device__ __forceinline__ f32x16 mfma(Vec8<tg_bf16>::type a, Vec8<tg_bf16>::typ
 }
 
 constexpr float kLog2e = 1.4426950408889634f;
+
+// 2^x with the hardware v_exp_f32 (exp2(-inf) = 0; the softmax arguments here are
+// <= 0 up to rounding, far from the overflow range).
+__device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
 constexpr int kThreads = 256;
 
 template <typename T>
@@ -108,6 +112,18 @@ __device__ __forceinline__ void stage(const T* __restrict__ g, int64_t row0, int
   }
 }
 
+// Workgroup -> (tile, head) mapping.  Dispatch i lands on XCD i % 8; remap the
+// launch index so XCD x gets the contiguous range [x*T/8, (x+1)*T/8) of the
+// head-major tile order, i.e. whole heads, so causal work (which varies along the
+// tile axis) is spread evenly over the XCDs.  Returns (tile, head).
+__device__ __forceinline__ void fa_block(int64_t& tile, int64_t& head) {
+  const int64_t gx = gridDim.x, T = gx * gridDim.y;
+  int64_t lin = (int64_t)blockIdx.y * gx + blockIdx.x;
+  if (T % 8 == 0) lin = (lin % 8) * (T / 8) + lin / 8;
+  head = lin / gx;
+  tile = lin % gx;
+}
+
 // Row index (within a 32-row C tile) of accumulator register r for lane half h.
 __device__ __forceinline__ int crow(int r, int h) { return ((r >> 2) << 3) + (h << 2) + (r & 3); }
 
@@ -118,10 +134,11 @@ __global__ __launch_bounds__(kThreads) void k_fa_fwd(const T* __restrict__ Q,
                                                      const T* __restrict__ V, T* __restrict__ O,
                                                      float* __restrict__ LSE, int64_t Sq,
                                                      int64_t Sk, float scale, int causal) {
-  constexpr int BN = 64, DK = D / 16, DT = D / 32;
+  constexpr int BN = 128, DK = D / 16, DT = D / 32;
   __shared__ __attribute__((aligned(16))) T Ks[BN * (D + 8)];
   __shared__ __attribute__((aligned(16))) T Vi[BN * D];
-  const int64_t bh = blockIdx.y;
+  int64_t tile, bh;
+  fa_block(tile, bh);
   Q += bh * Sq * D;
   K += bh * Sk * D;
   V += bh * Sk * D;
@@ -129,7 +146,9 @@ __global__ __launch_bounds__(kThreads) void k_fa_fwd(const T* __restrict__ Q,
   LSE += bh * Sq;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int h = lane >> 5, l32 = lane & 31;
-  const int64_t qblk = (int64_t)blockIdx.x * 128;
+  // causal: the last query blocks carry the most keys, so they are dispatched first
+  const int64_t qb = causal ? (int64_t)gridDim.x - 1 - tile : tile;
+  const int64_t qblk = qb * 128;
   const int64_t q = qblk + wave * 32 + l32;
   const float sl2 = scale * kLog2e;
 
@@ -157,56 +176,55 @@ __global__ __launch_bounds__(kThreads) void k_fa_fwd(const T* __restrict__ Q,
     stage<T, BN, D, true, false>(K, k0, Sk, Ks, nullptr);
     stage<T, BN, D, false, true>(V, k0, Sk, nullptr, Vi);
     __syncthreads();
-    f32x16 s[2];
+#pragma unroll 1
+    for (int kt = 0; kt < BN / 32; ++kt) {
+      f32x16 s;
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[kt][r] = 0.f;
+      for (int r = 0; r < 16; ++r) s[r] = 0.f;
 #pragma unroll
       for (int ks = 0; ks < DK; ++ks)
-        s[kt] = mfma(ld8(Ks + (kt * 32 + l32) * (D + 8) + ks * 16 + h * 8), qf[ks], s[kt]);
-    }
-    float mloc = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
+        s = mfma(ld8(Ks + (kt * 32 + l32) * (D + 8) + ks * 16 + h * 8), qf[ks], s);
+      // masks are only needed where the sub-tile crosses Sk or the causal diagonal
+      const bool edge = (k0 + kt * 32 + 32 > Sk) ||
+                        (causal && k0 + kt * 32 + 31 > qblk + wave * 32);
+      float mloc = -INFINITY;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t key = k0 + kt * 32 + crow(r, h);
-        float x = s[kt][r] * sl2;
-        if (key >= Sk || (causal && key > q)) x = -INFINITY;
-        s[kt][r] = x;
+        float x = s[r] * sl2;
+        if (edge) {
+          const int64_t key = k0 + kt * 32 + crow(r, h);
+          if (key >= Sk || (causal && key > q)) x = -INFINITY;
+        }
+        s[r] = x;
         mloc = fmaxf(mloc, x);
       }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-    const float mnew = fmaxf(m, mloc);
-    const float alpha = (mnew == -INFINITY) ? 1.f : exp2f(m - mnew);
-    float lsum = 0.f;
-    float p[2][16];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+      const float mnew = fmaxf(m, mloc);
+      const float alpha = (mnew == -INFINITY) ? 1.f : fexp2(m - mnew);
+      float lsum = 0.f;
+      float p[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float e = (mnew == -INFINITY) ? 0.f : exp2f(s[kt][r] - mnew);
-        p[kt][r] = e;
+        const float e = (mnew == -INFINITY) ? 0.f : fexp2(s[r] - mnew);
+        p[r] = e;
         lsum += e;
       }
-    lsum += __shfl_xor(lsum, 32, 64);
-    l = l * alpha + lsum;
-    m = mnew;
+      lsum += __shfl_xor(lsum, 32, 64);
+      l = l * alpha + lsum;
+      m = mnew;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+      for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
+        for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
 #pragma unroll
       for (int sg = 0; sg < 2; ++sg) {
-        const typename Vec8<T>::type pb = pack8<T>(&p[kt][8 * sg]);
+        const typename Vec8<T>::type pb = pack8<T>(&p[8 * sg]);
         const int g1 = (kt * 32 + 16 * sg + 4 * h) >> 2;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
           o[dt] = mfma(ld_il<T, D>(Vi, g1, g1 + 2, dt * 32 + l32), pb, o[dt]);
       }
+    }
   }
   if (q < Sq) {
     const float inv = l > 0.f ? 1.f / l : 0.f;
@@ -262,20 +280,23 @@ __device__ __forceinline__ void store_c_tile(T* __restrict__ out, int64_t ld, in
   }
 }
 
-// dK, dV.  grid = (ceil(Sk/128), B*H).
+// dK, dV.  grid = (ceil(Sk/128), B*H).  Query tiles of 128 staged per step; the four
+// 32-query sub-tiles are processed one after another to keep P/dS in 32 registers.
 template <typename T, int D>
 __global__ __launch_bounds__(kThreads) void k_fa_bwd_dkdv(
     const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
     const T* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Dv,
     T* __restrict__ dK, T* __restrict__ dV, int64_t Sq, int64_t Sk, float scale, int causal,
     int accumulate) {
-  constexpr int BM = 64, DK = D / 16, DT = D / 32;
+  constexpr int BM = 128, DK = D / 16, DT = D / 32;
   __shared__ __attribute__((aligned(16))) T Qs[BM * (D + 8)];
   __shared__ __attribute__((aligned(16))) T Qi[BM * D];
   __shared__ __attribute__((aligned(16))) T dOs[BM * (D + 8)];
   __shared__ __attribute__((aligned(16))) T dOi[BM * D];
-  __shared__ float lse2[BM], dvec[BM];
-  const int64_t bh = blockIdx.y;
+  __shared__ __attribute__((aligned(16))) float lse2[BM];
+  __shared__ __attribute__((aligned(16))) float dvec[BM];
+  int64_t tile, bh;
+  fa_block(tile, bh);
   Q += bh * Sq * D;
   dO += bh * Sq * D;
   K += bh * Sk * D;
@@ -286,7 +307,7 @@ __global__ __launch_bounds__(kThreads) void k_fa_bwd_dkdv(
   Dv += bh * Sq;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int h = lane >> 5, l32 = lane & 31;
-  const int64_t kblk = (int64_t)blockIdx.x * 128;
+  const int64_t kblk = tile * 128;
   const int64_t key = kblk + wave * 32 + l32;  // this lane's key (C-tile column)
   const float sl2 = scale * kLog2e;
 
@@ -325,9 +346,10 @@ __global__ __launch_bounds__(kThreads) void k_fa_bwd_dkdv(
       dvec[threadIdx.x] = qq < Sq ? Dv[qq] : 0.f;
     }
     __syncthreads();
-    float p[2][16], ds[2][16];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
+#pragma unroll 1
+    for (int t = 0; t < BM / 32; ++t) {
+      // causal: a 32-query sub-tile wholly before this wave's keys contributes nothing
+      if (causal && q0 + t * 32 + 31 < kblk + wave * 32) continue;
       f32x16 s, dp;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -339,22 +361,30 @@ __global__ __launch_bounds__(kThreads) void k_fa_bwd_dkdv(
         s = mfma(ld8(Qs + (t * 32 + l32) * (D + 8) + ks * 16 + h * 8), kf[ks], s);
         dp = mfma(ld8(dOs + (t * 32 + l32) * (D + 8) + ks * 16 + h * 8), vf[ks], dp);
       }
+      // Padded query rows are zero in Qs/dOs with lse = D = 0, so they add nothing to
+      // dV (dO row 0) or dK (dS = P*(0-0) = 0); padded keys only feed dK/dV rows that
+      // are never stored.  Only the causal diagonal needs a mask.
+      const bool diag = causal && (kblk + wave * 32 + 31 > q0 + t * 32);
+      float lv[16], dvv[16];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 a = *reinterpret_cast<const float4*>(lse2 + t * 32 + 8 * g + 4 * h);
+        const float4 b = *reinterpret_cast<const float4*>(dvec + t * 32 + 8 * g + 4 * h);
+        lv[4 * g] = a.x; lv[4 * g + 1] = a.y; lv[4 * g + 2] = a.z; lv[4 * g + 3] = a.w;
+        dvv[4 * g] = b.x; dvv[4 * g + 1] = b.y; dvv[4 * g + 2] = b.z; dvv[4 * g + 3] = b.w;
+      }
+      float p[16], ds[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int qi = t * 32 + crow(r, h);
-        const int64_t qq = q0 + qi;
-        float pv = exp2f(s[r] * sl2 - lse2[qi]);
-        if (qq >= Sq || key >= Sk || (causal && key > qq)) pv = 0.f;
-        p[t][r] = pv;
-        ds[t][r] = pv * (dp[r] - dvec[qi]) * scale;
+        float pv = fexp2(fmaf(s[r], sl2, -lv[r]));
+        if (diag && key > q0 + t * 32 + crow(r, h)) pv = 0.f;
+        p[r] = pv;
+        ds[r] = pv * (dp[r] - dvv[r]) * scale;
       }
-    }
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int sg = 0; sg < 2; ++sg) {
-        const typename Vec8<T>::type pa = pack8<T>(&p[t][8 * sg]);
-        const typename Vec8<T>::type da = pack8<T>(&ds[t][8 * sg]);
+        const typename Vec8<T>::type pa = pack8<T>(&p[8 * sg]);
+        const typename Vec8<T>::type da = pack8<T>(&ds[8 * sg]);
         const int g1 = (t * 32 + 16 * sg + 4 * h) >> 2;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
@@ -362,6 +392,7 @@ __global__ __launch_bounds__(kThreads) void k_fa_bwd_dkdv(
           dk[dt] = mfma(da, ld_il<T, D>(Qi, g1, g1 + 2, dt * 32 + l32), dk[dt]);
         }
       }
+    }
   }
   // C tiles: rows = keys of this wave, cols = d
 #pragma unroll
@@ -377,11 +408,12 @@ __global__ __launch_bounds__(kThreads) void k_fa_bwd_dq(
     const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
     const T* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Dv,
     T* __restrict__ dQ, int64_t Sq, int64_t Sk, float scale, int causal, int accumulate) {
-  constexpr int BN = 64, DK = D / 16, DT = D / 32;
+  constexpr int BN = 128, DK = D / 16, DT = D / 32;
   __shared__ __attribute__((aligned(16))) T Ks[BN * (D + 8)];
   __shared__ __attribute__((aligned(16))) T Ki[BN * D];
   __shared__ __attribute__((aligned(16))) T Vs[BN * (D + 8)];
-  const int64_t bh = blockIdx.y;
+  int64_t tile, bh;
+  fa_block(tile, bh);
   Q += bh * Sq * D;
   dO += bh * Sq * D;
   dQ += bh * Sq * D;
@@ -391,7 +423,9 @@ __global__ __launch_bounds__(kThreads) void k_fa_bwd_dq(
   Dv += bh * Sq;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int h = lane >> 5, l32 = lane & 31;
-  const int64_t qblk = (int64_t)blockIdx.x * 128;
+  // causal: the last query blocks carry the most keys, so they are dispatched first
+  const int64_t qb = causal ? (int64_t)gridDim.x - 1 - tile : tile;
+  const int64_t qblk = qb * 128;
   const int64_t q = qblk + wave * 32 + l32;
   const float sl2 = scale * kLog2e;
   typename Vec8<T>::type qf[DK], of[DK];
@@ -422,8 +456,10 @@ __global__ __launch_bounds__(kThreads) void k_fa_bwd_dq(
     stage<T, BN, D, true, true>(K, k0, Sk, Ks, Ki);
     stage<T, BN, D, true, false>(V, k0, Sk, Vs, nullptr);
     __syncthreads();
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll 1
+    for (int kt = 0; kt < BN / 32; ++kt) {
+      // causal: a 32-key sub-tile wholly after this wave's queries contributes nothing
+      if (causal && k0 + kt * 32 > qblk + wave * 32 + 31) continue;
       f32x16 s, dp;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -435,12 +471,14 @@ __global__ __launch_bounds__(kThreads) void k_fa_bwd_dq(
         s = mfma(ld8(Ks + (kt * 32 + l32) * (D + 8) + ks * 16 + h * 8), qf[ks], s);
         dp = mfma(ld8(Vs + (kt * 32 + l32) * (D + 8) + ks * 16 + h * 8), of[ks], dp);
       }
+      // Padded keys are zero rows of K/V, so they add nothing to dQ (dS * 0); only the
+      // causal diagonal needs a mask.
+      const bool diag = causal && (k0 + kt * 32 + 31 > qblk + wave * 32);
       float ds[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t kk = k0 + kt * 32 + crow(r, h);
-        float pv = exp2f(s[r] * sl2 - lq);
-        if (q >= Sq || kk >= Sk || (causal && kk > q)) pv = 0.f;
+        float pv = fexp2(fmaf(s[r], sl2, -lq));
+        if (diag && k0 + kt * 32 + crow(r, h) > q) pv = 0.f;
         ds[r] = pv * (dp[r] - dq_d) * scale;
       }
 #pragma unroll

@@ -22,6 +22,19 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
+template <typename T> struct Vec8;
+template <> struct Vec8<tg_half> { typedef _Float16 type __attribute__((ext_vector_type(8))); };
+template <> struct Vec8<tg_bf16> { typedef __bf16 type __attribute__((ext_vector_type(8))); };
+
+__device__ __forceinline__ void mfma_v(const Vec8<tg_half>::type& a, const Vec8<tg_half>::type& b,
+                                       f32x16& c) {
+  c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ void mfma_v(const Vec8<tg_bf16>::type& a, const Vec8<tg_bf16>::type& b,
+                                       f32x16& c) {
+  c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
 template <typename T> struct Mfma;
 template <> struct Mfma<tg_half> {
   static constexpr int BK = 32;   // k per tile
@@ -236,6 +249,185 @@ __global__ __launch_bounds__(kThreads) void k_gemm(int64_t M, int64_t N, int64_t
     }
 }
 
+// ---------------------------------------------------------------------------
+// Pipelined kernel for fp16/bf16: block tile 128 x BN x 64 (BN = 128 or 64),
+// 4 wavefronts in a 2 x 2 grid, each owning a 64 x BN/2 sub-tile of MFMA 32x32
+// tiles; LDS double-buffered so the next k-tile's global loads overlap the
+// current MFMAs, one barrier per k-tile.  BN is chosen so the grid holds at least
+// two blocks per CU where the problem allows it.
+// LDS layout per operand:
+//   contiguous along k in memory  -> row-major [row][BK+8]: one 16-byte read per
+//                                    8-element fragment;
+//   contiguous along m/n          -> 4-k interleaved [k/4][row][4]: staged with
+//                                    8-byte writes, read as two 8-byte halves.
+// Tiles are assigned XCD-aware: dispatch i runs on XCD i % 8, so the launch index
+// is remapped to give each XCD a contiguous band of tiles (shared A rows in its L2).
+constexpr int V2_BM = 128, V2_BK = 64;
+
+template <typename T, bool KC, int ROWS>
+struct StageV2 {
+  static constexpr int NVEC = KC ? (ROWS * V2_BK) / (8 * kThreads) : 4;
+  static constexpr int UNITS = (V2_BK / 4) * (ROWS / 8);
+  static constexpr int RM_LD = V2_BK + 8;
+  static constexpr int LDS_ELEMS = KC ? ROWS * RM_LD : ROWS * V2_BK;
+  uint4 r[NVEC];
+
+  __device__ void load(const T* __restrict__ g, int64_t ld, int64_t rows_total, int64_t K,
+                       int64_t row0, int64_t k0) {
+    const int t = threadIdx.x;
+    if (KC) {
+#pragma unroll
+      for (int i = 0; i < NVEC; ++i) {
+        const int v = t + i * kThreads;
+        const int64_t row = row0 + v / (V2_BK / 8);
+        const int64_t k = k0 + (v % (V2_BK / 8)) * 8;
+        r[i] = (row < rows_total && k < K) ? *reinterpret_cast<const uint4*>(g + row * ld + k)
+                                           : make_uint4(0, 0, 0, 0);
+      }
+    } else {
+      if (t >= UNITS) return;
+      const int kg = t / (ROWS / 8), rg = t % (ROWS / 8);
+      const int64_t row = row0 + rg * 8;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t k = k0 + kg * 4 + i;
+        r[i] = (k < K && row < rows_total) ? *reinterpret_cast<const uint4*>(g + k * ld + row)
+                                           : make_uint4(0, 0, 0, 0);
+      }
+    }
+  }
+
+  __device__ void store(T* lds) const {
+    const int t = threadIdx.x;
+    if (KC) {
+#pragma unroll
+      for (int i = 0; i < NVEC; ++i) {
+        const int v = t + i * kThreads;
+        const int row = v / (V2_BK / 8), k = (v % (V2_BK / 8)) * 8;
+        *reinterpret_cast<uint4*>(lds + row * RM_LD + k) = r[i];
+      }
+    } else {
+      if (t >= UNITS) return;
+      const int kg = t / (ROWS / 8), rg = t % (ROWS / 8);
+      const T* e0 = reinterpret_cast<const T*>(&r[0]);
+      const T* e1 = reinterpret_cast<const T*>(&r[1]);
+      const T* e2 = reinterpret_cast<const T*>(&r[2]);
+      const T* e3 = reinterpret_cast<const T*>(&r[3]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        T q4[4] = {e0[j], e1[j], e2[j], e3[j]};
+        *reinterpret_cast<uint2*>(lds + (kg * ROWS + rg * 8 + j) * 4) =
+            *reinterpret_cast<const uint2*>(q4);
+      }
+    }
+  }
+
+  // 8-element fragment for `row` (tile-local) and k = ks*16 + h*8 + e.
+  __device__ __forceinline__ typename Vec8<T>::type frag(const T* lds, int row, int ks,
+                                                         int h) const {
+    union {
+      uint4 u;
+      typename Vec8<T>::type v;
+    } r;
+    if (KC) {
+      r.u = *reinterpret_cast<const uint4*>(lds + row * RM_LD + ks * 16 + h * 8);
+    } else {
+      const int g = ks * 4 + h * 2;
+      const uint2 a = *reinterpret_cast<const uint2*>(lds + (g * ROWS + row) * 4);
+      const uint2 b = *reinterpret_cast<const uint2*>(lds + ((g + 1) * ROWS + row) * 4);
+      r.u = make_uint4(a.x, a.y, b.x, b.y);
+    }
+    return r.v;
+  }
+};
+
+template <typename T, typename TC, bool TA, bool TB, int BNv>
+__global__ __launch_bounds__(kThreads) void k_gemm_v2(int64_t M, int64_t N, int64_t K, float alpha,
+                                                      const T* __restrict__ A, int64_t lda,
+                                                      int64_t sa, const T* __restrict__ B,
+                                                      int64_t ldb, int64_t sb, float beta,
+                                                      TC* __restrict__ C, int64_t ldc, int64_t sc) {
+  constexpr int NTW = BNv / 64;  // 32-wide MFMA tiles per wave along n
+  using SA = StageV2<T, !TA, V2_BM>;
+  using SB = StageV2<T, TB, BNv>;
+  __shared__ __attribute__((aligned(16))) T As[2][SA::LDS_ELEMS];
+  __shared__ __attribute__((aligned(16))) T Bs[2][SB::LDS_ELEMS];
+
+  const int64_t gx = gridDim.x, gy = gridDim.y;
+  const int64_t T_ = gx * gy;
+  int64_t lin = (int64_t)blockIdx.y * gx + blockIdx.x;
+  if (T_ % 8 == 0) lin = (lin % 8) * (T_ / 8) + lin / 8;
+  const int64_t tm = lin / gx, tn = lin % gx;
+  const int64_t bz = blockIdx.z;
+  A += bz * sa;
+  B += bz * sb;
+  C += bz * sc;
+  const int64_t m0 = tm * V2_BM, n0 = tn * BNv;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * (BNv / 2);
+  const int lr = lane & 31, lh = lane >> 5;
+
+  f32x16 acc[2][NTW];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < NTW; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  SA sa_;
+  SB sb_;
+  sa_.load(A, lda, M, K, m0, 0);
+  sb_.load(B, ldb, N, K, n0, 0);
+  sa_.store(As[0]);
+  sb_.store(Bs[0]);
+  __syncthreads();
+  int cur = 0;
+  for (int64_t k0 = 0; k0 < K; k0 += V2_BK) {
+    const bool more = k0 + V2_BK < K;
+    if (more) {
+      sa_.load(A, lda, M, K, m0, k0 + V2_BK);
+      sb_.load(B, ldb, N, K, n0, k0 + V2_BK);
+    }
+#pragma unroll
+    for (int ks = 0; ks < V2_BK / 16; ++ks) {
+      typename Vec8<T>::type af[2], bfr[NTW];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) af[i] = sa_.frag(As[cur], wm + i * 32 + lr, ks, lh);
+#pragma unroll
+      for (int j = 0; j < NTW; ++j) bfr[j] = sb_.frag(Bs[cur], wn + j * 32 + lr, ks, lh);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) mfma_v(af[i], bfr[j], acc[i][j]);
+    }
+    if (more) {
+      sa_.store(As[cur ^ 1]);
+      sb_.store(Bs[cur ^ 1]);
+    }
+    __syncthreads();
+    cur ^= 1;
+  }
+
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < NTW; ++j) {
+      const int64_t col = n0 + wn + j * 32 + lr;
+      if (col >= N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + wm + i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
+        if (row < M) {
+          float v = alpha * acc[i][j][r];
+          TC* pc = C + row * ldc + col;
+          if (beta != 0.f) v += beta * tg_to_float(*pc);
+          *pc = tg_from_float<TC>(v);
+        }
+      }
+    }
+}
+
 template <typename T, typename TC>
 int launch(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const void* A,
            int64_t lda, int64_t sa, const void* B, int64_t ldb, int64_t sb, float beta, void* C,
@@ -247,6 +439,32 @@ int launch(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const v
   const T* a = (const T*)A;
   const T* b = (const T*)B;
   TC* c = (TC*)C;
+  // v2 stages whole 16-byte vectors along every contiguous dimension: extents must be
+  // multiples of 8 so no vector straddles a row end.
+  if constexpr (sizeof(T) == 2) {
+  if (vec && M >= 128 && N >= 64 && K >= 64 && M % 8 == 0 && N % 8 == 0 && K % 8 == 0) {
+    // BN = 128 unless that leaves fewer than two blocks per CU.
+    const int64_t tiles128 = ((M + 127) / 128) * ((N + 127) / 128) * batch;
+    const bool wide = tiles128 >= 2 * (int64_t)tg_num_cus() && N >= 128;
+    const int bn = wide ? 128 : 64;
+    dim3 g2((unsigned)((N + bn - 1) / bn), (unsigned)((M + V2_BM - 1) / V2_BM), (unsigned)batch);
+#define TG_G2(TA_, TB_)                                                                        \
+  do {                                                                                         \
+    if (wide)                                                                                  \
+      k_gemm_v2<T, TC, TA_, TB_, 128><<<g2, kThreads, 0, s>>>(M, N, K, alpha, a, lda, sa, b,    \
+                                                              ldb, sb, beta, c, ldc, sc);     \
+    else                                                                                       \
+      k_gemm_v2<T, TC, TA_, TB_, 64><<<g2, kThreads, 0, s>>>(M, N, K, alpha, a, lda, sa, b, ldb, \
+                                                             sb, beta, c, ldc, sc);          \
+  } while (0)
+    if (!ta && !tb) TG_G2(false, false);
+    else if (!ta && tb) TG_G2(false, true);
+    else if (ta && !tb) TG_G2(true, false);
+    else TG_G2(true, true);
+#undef TG_G2
+    return tg_check_launch("tg_gemm");
+  }
+  }
 #define TG_G(TA_, TB_, V_) \
   k_gemm<T, TC, TA_, TB_, V_><<<grid, kThreads, 0, s>>>(M, N, K, alpha, a, lda, sa, b, ldb, sb, beta, c, ldc, sc)
   if (vec) {

@@ -469,8 +469,36 @@ def gemm(a, b, c, trans_a=False, trans_b=False, alpha=1.0, beta=0.0, M=None, N=N
     return c
 
 
+_CUS = {}
+
+
+def _num_cus(device):
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx not in _CUS:
+        _CUS[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    return _CUS[idx]
+
+
+def _split_k(M, N, K, device):
+    """K-split factor for GEMMs whose output has too few 128x128 tiles to fill the
+    CUs (e.g. weight gradients [1024, 1024] over 8192 tokens).  Returns 1 or s with
+    K % s == 0 and (K/s) % 64 == 0."""
+    tiles = ((M + 127) // 128) * ((N + 127) // 128)
+    cus = _num_cus(device)
+    if tiles >= cus or K < 2048:
+        return 1
+    want = min(-(-2 * cus // tiles), K // 1024)
+    for s_ in range(want, 1, -1):
+        if K % s_ == 0 and (K // s_) % 64 == 0:
+            return s_
+    return 1
+
+
 def matmul2d(a, b, out=None, trans_a=False, trans_b=False, alpha=1.0, beta=0.0, out_dtype=None):
-    """out (= or +=) op(a) @ op(b) for 2-D contiguous a, b."""
+    """out (= or +=) op(a) @ op(b) for 2-D contiguous a, b.
+
+    Output shapes with few tiles and a long K run as a K-split batched GEMM into
+    fp32 partials followed by the deterministic column-sum kernel."""
     _dev(a, "a")
     _dev(b, "b")
     M = a.shape[1] if trans_a else a.shape[0]
@@ -485,7 +513,17 @@ def matmul2d(a, b, out=None, trans_a=False, trans_b=False, alpha=1.0, beta=0.0, 
     _dev(out, "out")
     if tuple(out.shape) != (M, N):
         raise ValueError(f"matmul2d: out shape {tuple(out.shape)} != {(M, N)}")
-    return gemm(a, b, out, trans_a, trans_b, alpha, beta, M, N, K, a.shape[1], b.shape[1], N)
+    lda, ldb = a.shape[1], b.shape[1]
+    s_ = _split_k(M, N, K, a.device) if (alpha == 1.0 and beta in (0.0, 1.0)) else 1
+    if s_ > 1:
+        kc = K // s_
+        parts = torch.empty(s_, M, N, dtype=torch.float32, device=a.device)
+        sa = kc * M if trans_a else kc
+        sb = kc if trans_b else kc * N
+        gemm(a, b, parts, trans_a, trans_b, 1.0, 0.0, M, N, kc, lda, ldb, N, sa, sb, M * N, s_)
+        reduce_rows(parts.view(s_, M * N), out.view(M * N), beta == 1.0)
+        return out
+    return gemm(a, b, out, trans_a, trans_b, alpha, beta, M, N, K, lda, ldb, N)
 
 
 # ---------------------------------------------------------------- attention

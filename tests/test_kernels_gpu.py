@@ -266,7 +266,7 @@ def test_reduce_rows(cuda, rows, cols, dt):
 
 # ------------------------------------------------------------------ GEMM
 GEMM_SHAPES = [(256, 256, 256), (100, 70, 50), (32, 256, 784), (130, 10, 256), (1, 1, 1),
-               (257, 129, 33), (64, 64, 0)]
+               (257, 129, 33), (64, 64, 0), (384, 640, 96), (1000, 136, 48), (512, 128, 1024)]
 
 
 @pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
