@@ -217,13 +217,31 @@ def _op_flash(torch, L, g, d, causal):
                  FP16_PEAK_TFLOPS)
 
 
+def _op_gpt(torch, L, g):
+    """C5: one GPT training step (vocab 32000 tied, d 1024, 16 heads, 4 layers, batch 8 x
+    seq 1024, fp16 autocast, GradScaler, CE, backward, tied sync, unscale, clip 1.0,
+    AdamW).  Work = 6 * params * tokens (dense) + causal attention fwd+bwd flops."""
+    from gpt_harness import GPT, Trainer, synthetic_batch
+    model = GPT()
+    tr = Trainer(model)
+    ids, targets = synthetic_batch()
+    nparam = sum(p.size for p in tr.params)
+    B, T, H, hd, layers = 8, 1024, 16, 64, 4
+    flops = 6 * nparam * B * T + layers * 14 * B * H * T * T * hd // 2
+
+    def run():
+        tr.step(ids, targets)
+    return Timed("gpt_step", run, flops, "TFLOP/s", FP16_PEAK_TFLOPS)
+
+
 def component_ops(torch, L, only):
     """Other configurations, each built in its own scope on HBM-resident inputs."""
     g = torch.Generator(device="cuda").manual_seed(1)
     builders = [("bn_relu_bwd_nhwc", lambda: _op_bn(torch, L, g)),
                 ("adamw_step", lambda: _op_adam(torch, L, g)),
                 ("unscale_check", lambda: _op_unscale(torch, L, g)),
-                ("gemm_fc1_bwd", lambda: _op_gemm(torch, L, g))]
+                ("gemm_fc1_bwd", lambda: _op_gemm(torch, L, g)),
+                ("gpt_step", lambda: _op_gpt(torch, L, g))]
     for d in (64, 128):
         for causal in (False, True):
             builders.append((f"flash_bwd_d{d}{'_causal' if causal else ''}",

@@ -176,6 +176,13 @@ class Tensor:
             return self._g, False
         return self._g, True
 
+    def _accumulate_unb(self, g):
+        """self.grad += unbroadcast(g).  The reduced tensor is fresh (owned) unless no
+        reduction was needed, in which case it is `g` itself and must not be adopted as
+        this tensor's buffer (it is another node's gradient)."""
+        u = _unbroadcast_dev(g, self.data.shape, self.data.dtype)
+        self._accumulate(u, owned=u is not g)
+
     def _accumulate(self, g, owned=False):
         """self.grad += g (g: torch tensor broadcast-compatible in shape, any float dtype)."""
         if not self._has_grad():
@@ -296,9 +303,9 @@ class Tensor:
             def _backward():
                 g = out._grad_out()
                 if self._has_grad():
-                    self._accumulate(_unbroadcast_dev(g, self.data.shape, self.data.dtype), True)
+                    self._accumulate_unb(g)
                 if other._has_grad():
-                    other._accumulate(_unbroadcast_dev(g, other.data.shape, other.data.dtype), True)
+                    other._accumulate_unb(g)
             out._backward = _backward
         return out
 
@@ -626,8 +633,7 @@ class Tensor:
         if out._requires_grad:
             def _backward():
                 if self._has_grad():
-                    self._accumulate(_unbroadcast_dev(out._grad_out(), self.data.shape,
-                                                      self.data.dtype), True)
+                    self._accumulate_unb(out._grad_out())
             out._backward = _backward
         return out
 
@@ -694,7 +700,7 @@ class Tensor:
                 g = torch.as_tensor(np.asarray(g))
             g = g.to(device="cuda", dtype=self.data.dtype)
             if not self._has_grad():
-                self._g = g.expand(self.data.shape).contiguous()
+                self._g = g.expand(self.data.shape).clone()
                 self._gz = False
             else:
                 self._accumulate(g.expand(self.data.shape).contiguous())

@@ -387,3 +387,24 @@ def test_weight_tie_and_sync(tg):
     want += (np.ones((4, 20)).T @ rows)
     assert_close(emb.weight.grad, want, 1e-5, "tied embedding grad")
     assert float(head.w.grad.abs().sum()) == 0.0
+
+
+def test_residual_add_grads_not_aliased(tg):
+    """Same-shape adds must not share one gradient buffer between operands (a later
+    accumulation into one operand's grad would leak into the other's)."""
+    rng = np.random.default_rng(12)
+    x_np = rng.standard_normal((8, 16)).astype(np.float32)
+    w_np = rng.standard_normal((16, 16)).astype(np.float32)
+    x = tg.Tensor(x_np)
+    w = tg.Tensor(w_np)
+    h = x @ w
+    r = h + h.gelu()          # residual: h receives from the add and from gelu
+    out = (r + x).sum() + (r * r).sum()
+    out.backward()
+    xt = torch.tensor(x_np.astype(np.float64), requires_grad=True)
+    wt = torch.tensor(w_np.astype(np.float64), requires_grad=True)
+    ht = xt @ wt
+    rt = ht + torch.nn.functional.gelu(ht, approximate="tanh")
+    ((rt + xt).sum() + (rt * rt).sum()).backward()
+    assert_close(x.grad, xt.grad.numpy(), RTOL_F32_MM, "x grad")
+    assert_close(w.grad, wt.grad.numpy(), RTOL_F32_MM, "w grad")
