@@ -64,7 +64,11 @@ class Timed:
             self.fn()
 
     def avg_ms(self):
-        return sum(s.elapsed_time(e) for s, e in self.ms) / max(1, len(self.ms))
+        # The first timed launch can find the GPU idle, so its window also holds the
+        # host-side argument preparation; later launches are queued behind their
+        # predecessor and their windows hold device time only.
+        ms = self.ms[1:] if len(self.ms) > 1 else self.ms
+        return sum(s.elapsed_time(e) for s, e in ms) / max(1, len(ms))
 
     def summary(self):
         ms = self.avg_ms()
@@ -294,6 +298,22 @@ def cpu_baseline():
                        f"bwd on [{rows_rw},4096]; {reps} reps in {dt:.1f}s, single thread")}
 
 
+CALIB_BYTES = 256 << 20
+
+
+def calibration_copy(torch):
+    """Three plain device copies of CALIB_BYTES (read CALIB_BYTES, write CALIB_BYTES).
+    Under rocprofv3 --pmc they give the scale between the FETCH_SIZE / WRITE_SIZE
+    counters and true bytes, used to turn the counters of the kernels into HBM
+    traffic."""
+    src = torch.ones(CALIB_BYTES // 4, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def main():
     a = _args()
     if a.gpus != 1:
@@ -307,6 +327,7 @@ def main():
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a GPU")
     L.ensure_device(0)
+    calibration_copy(torch)
     ops = c2_ops(torch, L)
     for _ in range(a.warmup):
         for op in ops:
@@ -334,7 +355,7 @@ def main():
             for _ in range(max(1, a.warmup)):
                 op.run(False)
             torch.cuda.synchronize()
-            for _ in range(max(3, a.steps // 2)):
+            for _ in range(max(3, a.steps // 2) + 1):
                 op.run(True)
             torch.cuda.synchronize()
             comps[op.name] = op.summary()

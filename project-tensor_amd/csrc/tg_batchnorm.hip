@@ -223,7 +223,7 @@ __global__ __launch_bounds__(kBlock) void k_bn_bwd_apply(
     const float* __restrict__ x, const float* __restrict__ dy, const float* __restrict__ mean,
     const float* __restrict__ rstd, const float* __restrict__ gamma,
     const float* __restrict__ beta, const float* __restrict__ coef, int relu,
-    float* __restrict__ dx, int64_t nvec, int64_t C, int64_t HW) {
+    float* __restrict__ dx, int64_t nvec, int64_t C, int64_t HW, bool nt) {
   // CONST_CH (NHWC, grid stride a multiple of C): every iteration of a thread
   // touches the same V channels, so their parameters are loaded once.
   const int64_t stride = (int64_t)gridDim.x * kBlock;
@@ -273,7 +273,10 @@ __global__ __launch_bounds__(kBlock) void k_bn_bwd_apply(
       if (ACC) r[j] += ov[j];
     }
     if (V == 4) {
-      *reinterpret_cast<float4*>(dx + i) = make_float4(r[0], r[1], r[2], r[3]);
+      tg_vec16<float> o;
+      o.v[0] = r[0]; o.v[1] = r[1]; o.v[2] = r[2]; o.v[3] = r[3];
+      if (nt) tg_store16_nt(dx + i, o);
+      else tg_store16(dx + i, o);
     } else {
       dx[i] = r[0];
     }
@@ -493,7 +496,8 @@ TG_EXPORT int tg_batchnorm_bwd(int layout, const float* x, const float* mean, co
   const unsigned ab = apply_blocks(nvec);
 #define TG_BN_APPLY(LAY, VV, ACC, CC, NB)                                               \
   k_bn_bwd_apply<LAY, VV, ACC, CC><<<NB, kBlock, 0, s>>>(x, dy, mean, rstd, gamma, beta, coef, \
-                                                         relu, dx, nvec, C, HW)
+                                                         relu, dx, nvec, C, HW, nt)
+  const bool nt = n * (int64_t)sizeof(float) >= (128ll << 20);  // output too large to keep cached
   const unsigned cc = (layout == TG_NHWC && vec) ? const_channel_blocks(nvec, C, 4) : 0;
   if (cc) {
     if (accumulate_dx) TG_BN_APPLY(TG_NHWC, 4, true, true, cc);

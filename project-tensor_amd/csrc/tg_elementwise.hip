@@ -23,7 +23,7 @@ __device__ __forceinline__ float gelu_grad(float x) {
   const float x2 = x * x;
   const float u = c0 * (x + c1 * x2 * x);
   const float e = __expf(-2.0f * fabsf(u));
-  const float r = 1.0f / (1.0f + e);
+  const float r = __builtin_amdgcn_rcpf(1.0f + e);  // 1 ulp, e in (0, 1]
   const float onept = (u >= 0.f) ? 1.0f + (1.0f - e) * r : 2.0f * e * r;  // 1 + tanh(u)
   const float sech2 = 4.0f * e * r * r;                                   // 1 - tanh(u)^2
   const float du = c0 * (1.0f + 3.0f * c1 * x2);
@@ -34,7 +34,7 @@ __device__ __forceinline__ float gelu_fwd(float x) {
   const float c0 = 0.7978845608028654f, c1 = 0.044715f;
   const float u = c0 * (x + c1 * x * x * x);
   const float e = __expf(-2.0f * fabsf(u));
-  const float r = 1.0f / (1.0f + e);
+  const float r = __builtin_amdgcn_rcpf(1.0f + e);  // 1 ulp, e in (0, 1]
   const float onept = (u >= 0.f) ? 1.0f + (1.0f - e) * r : 2.0f * e * r;
   return 0.5f * x * onept;
 }
@@ -43,7 +43,7 @@ __device__ __forceinline__ float gelu_fwd(float x) {
 // s = sigmoid(x).  1-s is formed as e*s with e = exp(-x) (no cancellation).
 __device__ __forceinline__ float silu_grad(float x) {
   const float e = __expf(-x);
-  const float s = 1.0f / (1.0f + e);
+  const float s = __builtin_amdgcn_rcpf(1.0f + e);  // 1 ulp
   const float oms = (x >= 0.f) ? e * s : 1.0f - s;
   return s * (1.0f + x * oms);
 }
@@ -59,17 +59,22 @@ template <int OP> __device__ __forceinline__ float act_fwd(float x) {
   return OP == OP_GELU ? gelu_fwd(x) : silu_fwd(x);
 }
 
-// dx (+)= dy * act'(x)
-template <typename T, int OP, bool ACC>
+// dx (+)= dy * act'(x).  One 16-byte vector per operand and thread (the
+// measured optimum for two-in/one-out streams); NT marks the output store
+// non-temporal, chosen for outputs too large to stay in the Infinity Cache.
+constexpr int kUnrollBwd = 1;
+constexpr int64_t kNtBytes = 128ll << 20;
+
+template <typename T, int OP, bool ACC, bool NT>
 __global__ __launch_bounds__(kThreads) void k_act_bwd(const T* __restrict__ x,
                                                       const T* __restrict__ dy,
                                                       T* __restrict__ dx, int64_t nvec,
                                                       int64_t n) {
   constexpr int V = tg_vec16<T>::N;
-  const int64_t base = (int64_t)blockIdx.x * kThreads * kUnroll + threadIdx.x;
-  tg_vec16<T> xv[kUnroll], gv[kUnroll], ov[kUnroll];
+  const int64_t base = (int64_t)blockIdx.x * kThreads * kUnrollBwd + threadIdx.x;
+  tg_vec16<T> xv[kUnrollBwd], gv[kUnrollBwd], ov[kUnrollBwd];
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
+  for (int u = 0; u < kUnrollBwd; ++u) {
     const int64_t i = base + (int64_t)u * kThreads;
     if (i < nvec) {
       xv[u] = tg_load16(x + i * V);
@@ -78,7 +83,7 @@ __global__ __launch_bounds__(kThreads) void k_act_bwd(const T* __restrict__ x,
     }
   }
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
+  for (int u = 0; u < kUnrollBwd; ++u) {
     const int64_t i = base + (int64_t)u * kThreads;
     if (i < nvec) {
       tg_vec16<T> r;
@@ -88,7 +93,8 @@ __global__ __launch_bounds__(kThreads) void k_act_bwd(const T* __restrict__ x,
         if (ACC) g += tg_to_float(ov[u].v[j]);
         r.v[j] = tg_from_float<T>(g);
       }
-      tg_store16(dx + i * V, r);
+      if (NT) tg_store16_nt(dx + i * V, r);
+      else tg_store16(dx + i * V, r);
     }
   }
   // scalar tail (fewer than V elements), handled by the first block
@@ -134,18 +140,19 @@ int launch_act_bwd(const void* x, const void* dy, void* dx, int64_t n, int acc, 
   constexpr int V = tg_vec16<T>::N;
   const bool vec = tg_aligned16(x) && tg_aligned16(dy) && tg_aligned16(dx);
   const int64_t nvec = vec ? n / V : 0;
-  int64_t blocks = (nvec + kThreads * kUnroll - 1) / (kThreads * kUnroll);
+  int64_t blocks = (nvec + kThreads * kUnrollBwd - 1) / (kThreads * kUnrollBwd);
   if (blocks < 1) blocks = 1;
   if (blocks > 0x7fffffff) {
     tg_set_error("activation backward: n=%lld too large", (long long)n);
     return TG_ERR_INVALID;
   }
-  if (acc)
-    k_act_bwd<T, OP, true><<<(unsigned)blocks, kThreads, 0, s>>>(
-        (const T*)x, (const T*)dy, (T*)dx, nvec, n);
-  else
-    k_act_bwd<T, OP, false><<<(unsigned)blocks, kThreads, 0, s>>>(
-        (const T*)x, (const T*)dy, (T*)dx, nvec, n);
+  const bool nt = (int64_t)sizeof(T) * n >= kNtBytes;
+#define L(ACC, NT)                                                      \
+  k_act_bwd<T, OP, ACC, NT><<<(unsigned)blocks, kThreads, 0, s>>>(      \
+      (const T*)x, (const T*)dy, (T*)dx, nvec, n)
+  if (acc) { if (nt) L(true, true); else L(true, false); }
+  else { if (nt) L(false, true); else L(false, false); }
+#undef L
   return tg_check_launch(OP == OP_GELU ? "tg_gelu_bwd" : "tg_silu_bwd");
 }
 

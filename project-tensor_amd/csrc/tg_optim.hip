@@ -15,8 +15,13 @@
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kMaxT = 24;
-constexpr int64_t kChunk = kBlock * 4 * 4;  // elements per workgroup (16 per thread)
+constexpr int kMaxT = 36;
+constexpr int kEPT = 16;                     // elements per thread (grad kernels)
+constexpr int64_t kChunk = kBlock * kEPT;    // elements per workgroup
+// Adam streams four inputs and three outputs: one 16-byte vector per operand and
+// thread, with non-temporal stores, measured fastest for that mix.
+constexpr int kAdamEPT = 4;
+constexpr int64_t kAdamChunk = kBlock * kAdamEPT;
 
 struct MtArgs {
   void* a[kMaxT];  // param / grad
@@ -30,96 +35,175 @@ struct MtArgs {
   int ntensors;
 };
 
+// Largest t with first_block[t] <= blk (binary search; tensors are in block order).
 __device__ __forceinline__ int find_tensor(const MtArgs& A, int64_t blk) {
-  int t = 0;
-  while (t + 1 < A.ntensors && A.first_block[t + 1] <= blk) ++t;
-  return t;
+  int lo = 0, hi = A.ntensors - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (A.first_block[mid] <= blk) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+// Chunk access.  Thread `tid` owns the elements start + (j*kBlock + tid)*PER + k
+// (PER elements per 16-byte vector, j < kEPT/PER): every vector instruction of a
+// wavefront covers 1 KiB of contiguous memory.  FULL chunks (whole chunk in range,
+// 16-byte aligned base) use vector accesses; the others use scalar accesses with
+// the same mapping and a bound check.
+template <typename T, int EPT = kEPT>
+struct ChunkMap {
+  static constexpr int PER = 16 / sizeof(T);
+  static constexpr int NV = EPT / PER;
+  static_assert(NV >= 1, "chunk smaller than one vector");
+  __device__ static int64_t at(int64_t start, int j) {
+    return start + ((int64_t)j * kBlock + threadIdx.x) * PER;
+  }
+};
+
+template <typename T, bool FULL, int EPT = kEPT>
+__device__ __forceinline__ void load_chunk(const T* __restrict__ p, int64_t start, int64_t end,
+                                           float (&x)[EPT]) {
+  using M = ChunkMap<T, EPT>;
+  if (FULL) {
+    tg_vec16<T> v[M::NV];
+#pragma unroll
+    for (int j = 0; j < M::NV; ++j) v[j] = tg_load16(p + M::at(start, j));
+#pragma unroll
+    for (int j = 0; j < M::NV; ++j)
+#pragma unroll
+      for (int k = 0; k < M::PER; ++k) x[j * M::PER + k] = tg_to_float(v[j].v[k]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < M::NV; ++j)
+#pragma unroll
+      for (int k = 0; k < M::PER; ++k) {
+        const int64_t i = M::at(start, j) + k;
+        x[j * M::PER + k] = i < end ? tg_to_float(p[i]) : 0.f;
+      }
+  }
+}
+
+template <typename T, bool FULL, int EPT = kEPT, bool NT = false>
+__device__ __forceinline__ void store_chunk(T* __restrict__ p, int64_t start, int64_t end,
+                                            const float (&x)[EPT]) {
+  using M = ChunkMap<T, EPT>;
+#pragma unroll
+  for (int j = 0; j < M::NV; ++j) {
+    if (FULL) {
+      tg_vec16<T> v;
+#pragma unroll
+      for (int k = 0; k < M::PER; ++k) v.v[k] = tg_from_float<T>(x[j * M::PER + k]);
+      if (NT) tg_store16_nt(p + M::at(start, j), v);
+      else tg_store16(p + M::at(start, j), v);
+    } else {
+#pragma unroll
+      for (int k = 0; k < M::PER; ++k) {
+        const int64_t i = M::at(start, j) + k;
+        if (i < end) p[i] = tg_from_float<T>(x[j * M::PER + k]);
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ bool al16(const void* p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15) == 0;
 }
 
 // ---------------------------------------------------------------------------
 // Adam/AdamW, reference order (_nn.py:1413-1442, _training.py:2198-2220):
 //   p -= lr*wd*p (if wd != 0); m = b1*m + (1-b1)*g; v = b2*v + (1-b2)*g^2;
 //   mhat = m/bc1; vhat = v/bc2; [vmax = max(vmax, vhat)]; p -= lr*mhat/(sqrt(v*)+eps)
+// The divisions by the bias corrections are multiplications by their reciprocals
+// (formed in double on the host) and the last one a reciprocal of the denominator:
+// each differs from the division by at most one rounding.
 struct AdamConsts {
-  float lr, b1, omb1, b2, omb2, eps, lrwd, bc1, bc2;
+  float lr, b1, omb1, b2, omb2, eps, lrwd, ibc1, ibc2;
   int decay;
 };
+
+template <bool AMS, bool FULL>
+__device__ __forceinline__ void adam_chunk(float* __restrict__ p, const float* __restrict__ g,
+                                           float* __restrict__ m, float* __restrict__ v,
+                                           float* __restrict__ vm, int64_t start, int64_t end,
+                                           const AdamConsts& K) {
+  constexpr int E = kAdamEPT;
+  float P[E], G[E], Mv[E], Vv[E], VM[E];
+  load_chunk<float, FULL, E>(p, start, end, P);
+  load_chunk<float, FULL, E>(g, start, end, G);
+  load_chunk<float, FULL, E>(m, start, end, Mv);
+  load_chunk<float, FULL, E>(v, start, end, Vv);
+  if (AMS) load_chunk<float, FULL, E>(vm, start, end, VM);
+#pragma unroll
+  for (int i = 0; i < E; ++i) {
+    float pp = P[i];
+    if (K.decay) pp -= K.lrwd * pp;
+    const float gg = G[i];
+    const float mm = K.b1 * Mv[i] + K.omb1 * gg;
+    const float vv = K.b2 * Vv[i] + K.omb2 * (gg * gg);
+    const float mh = mm * K.ibc1;
+    float vh = vv * K.ibc2;
+    if (AMS) {
+      vh = fmaxf(VM[i], vh);
+      VM[i] = vh;
+    }
+    pp -= K.lr * mh * __frcp_rn(sqrtf(vh) + K.eps);
+    P[i] = pp;
+    Mv[i] = mm;
+    Vv[i] = vv;
+  }
+  store_chunk<float, FULL, E, true>(p, start, end, P);
+  store_chunk<float, FULL, E, true>(m, start, end, Mv);
+  store_chunk<float, FULL, E, true>(v, start, end, Vv);
+  if (AMS) store_chunk<float, FULL, E, true>(vm, start, end, VM);
+}
 
 template <bool AMS>
 __global__ __launch_bounds__(kBlock) void k_adam(MtArgs A, AdamConsts K) {
   const int t = find_tensor(A, blockIdx.x);
   const int64_t n = A.n[t];
-  const int64_t start = (blockIdx.x - A.first_block[t]) * kChunk;
-  float* __restrict__ p = (float*)A.a[t];
-  const float* __restrict__ g = (const float*)A.b[t];
-  float* __restrict__ m = (float*)A.c[t];
-  float* __restrict__ v = (float*)A.d[t];
-  float* __restrict__ vm = (float*)A.e[t];
-  const bool vec = ((reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(g) |
-                     reinterpret_cast<uintptr_t>(m) | reinterpret_cast<uintptr_t>(v) |
-                     (AMS ? reinterpret_cast<uintptr_t>(vm) : 0)) & 15) == 0;
-  auto upd = [&](float& pp, float gg, float& mm, float& vv, float* vmx) {
-    if (K.decay) pp -= K.lrwd * pp;
-    mm = K.b1 * mm + K.omb1 * gg;
-    vv = K.b2 * vv + K.omb2 * (gg * gg);
-    const float mh = mm / K.bc1;
-    float vh = vv / K.bc2;
-    if (AMS) {
-      vh = fmaxf(*vmx, vh);
-      *vmx = vh;
-    }
-    pp -= K.lr * mh / (sqrtf(vh) + K.eps);
-  };
-  if (vec && start + kChunk <= n) {
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int64_t i = start + ((int64_t)u * kBlock + threadIdx.x) * 4;
-      float4 P = *reinterpret_cast<float4*>(p + i);
-      const float4 G = *reinterpret_cast<const float4*>(g + i);
-      float4 Mv = *reinterpret_cast<float4*>(m + i);
-      float4 Vv = *reinterpret_cast<float4*>(v + i);
-      float4 VM = AMS ? *reinterpret_cast<float4*>(vm + i) : make_float4(0, 0, 0, 0);
-      upd(P.x, G.x, Mv.x, Vv.x, &VM.x);
-      upd(P.y, G.y, Mv.y, Vv.y, &VM.y);
-      upd(P.z, G.z, Mv.z, Vv.z, &VM.z);
-      upd(P.w, G.w, Mv.w, Vv.w, &VM.w);
-      *reinterpret_cast<float4*>(p + i) = P;
-      *reinterpret_cast<float4*>(m + i) = Mv;
-      *reinterpret_cast<float4*>(v + i) = Vv;
-      if (AMS) *reinterpret_cast<float4*>(vm + i) = VM;
-    }
-  } else {
-    const int64_t end = start + kChunk < n ? start + kChunk : n;
-    for (int64_t i = start + threadIdx.x; i < end; i += kBlock) {
-      float P = p[i], Mv = m[i], Vv = v[i], VM = AMS ? vm[i] : 0.f;
-      upd(P, g[i], Mv, Vv, &VM);
-      p[i] = P;
-      m[i] = Mv;
-      v[i] = Vv;
-      if (AMS) vm[i] = VM;
-    }
-  }
+  const int64_t start = (blockIdx.x - A.first_block[t]) * kAdamChunk;
+  const int64_t end = start + kAdamChunk < n ? start + kAdamChunk : n;
+  float* p = (float*)A.a[t];
+  const float* g = (const float*)A.b[t];
+  float* m = (float*)A.c[t];
+  float* v = (float*)A.d[t];
+  float* vm = (float*)A.e[t];
+  const bool full = start + kAdamChunk <= n && al16(p) && al16(g) && al16(m) && al16(v) &&
+                    (!AMS || al16(vm));
+  if (full) adam_chunk<AMS, true>(p, g, m, v, vm, start, end, K);
+  else adam_chunk<AMS, false>(p, g, m, v, vm, start, end, K);
 }
 
 // ---------------------------------------------------------------------------
 // g' = g*mul (stored if WRITE).  flags[t] |= 1 if any g is non-finite,
 // |= 2 if any g' is non-finite (GradScaler.unscale_, _nn.py:1795-1833).
+template <typename T, bool WRITE, bool FULL>
+__device__ __forceinline__ int scale_check_chunk(T* __restrict__ g, int64_t start, int64_t end,
+                                                 float mul) {
+  float x[kEPT], y[kEPT];
+  load_chunk<T, FULL>(g, start, end, x);
+  int f = 0;
+#pragma unroll
+  for (int i = 0; i < kEPT; ++i) {
+    if (!isfinite(x[i])) f |= 1;
+    // round through T so the post-check sees what is stored
+    y[i] = tg_to_float(tg_from_float<T>(x[i] * mul));
+    if (!isfinite(y[i])) f |= 2;
+  }
+  if (WRITE) store_chunk<T, FULL>(g, start, end, y);
+  return f;
+}
+
 template <typename T, bool WRITE>
 __global__ __launch_bounds__(kBlock) void k_scale_check(MtArgs A, float mul, int* flags) {
   const int t = find_tensor(A, blockIdx.x);
   const int64_t n = A.n[t];
   const int64_t start = (blockIdx.x - A.first_block[t]) * kChunk;
   const int64_t end = start + kChunk < n ? start + kChunk : n;
-  T* __restrict__ g = (T*)A.a[t];
-  int f = 0;
-  for (int64_t i = start + threadIdx.x; i < end; i += kBlock) {
-    const float x = tg_to_float(g[i]);
-    const float y = x * mul;
-    if (!isfinite(x)) f |= 1;
-    const T yt = tg_from_float<T>(y);
-    if (!isfinite(tg_to_float(yt))) f |= 2;
-    if (WRITE) g[i] = yt;
-  }
+  T* g = (T*)A.a[t];
+  int f = (start + kChunk <= n && al16(g)) ? scale_check_chunk<T, WRITE, true>(g, start, end, mul)
+                                           : scale_check_chunk<T, WRITE, false>(g, start, end, mul);
   // wave-level OR, then one atomic per wave that found something
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) f |= __shfl_xor(f, off, 64);
@@ -135,16 +219,21 @@ __global__ __launch_bounds__(kBlock) void k_norm_partial(MtArgs A, float p, doub
   const int64_t n = A.n[t];
   const int64_t start = (blockIdx.x - A.first_block[t]) * kChunk;
   const int64_t end = start + kChunk < n ? start + kChunk : n;
-  const T* __restrict__ g = (const T*)A.a[t];
+  const T* g = (const T*)A.a[t];
+  float x[kEPT];
+  if (start + kChunk <= n && al16(g)) load_chunk<T, true>(g, start, end, x);
+  else load_chunk<T, false>(g, start, end, x);  // out-of-range entries read as 0
   double acc = 0.0;
   int f = 0;
-  for (int64_t i = start + threadIdx.x; i < end; i += kBlock) {
-    const float x = tg_to_float(g[i]);
-    if (!isfinite(x)) {
+  using M = ChunkMap<T>;
+#pragma unroll
+  for (int i = 0; i < kEPT; ++i) {
+    if (M::at(start, i / M::PER) + i % M::PER >= end) continue;  // padding of a tail chunk
+    if (!isfinite(x[i])) {
       f = 1;
       continue;
     }
-    const float ax = fabsf(x);
+    const float ax = fabsf(x[i]);
     if (KIND == 0) acc += (double)ax * (double)ax;
     else if (KIND == 1) acc = fmax(acc, (double)ax);
     else acc += pow((double)ax, (double)p);
@@ -188,15 +277,34 @@ __global__ __launch_bounds__(kBlock) void k_norm_final(const double* part, int64
   if (threadIdx.x == 0) out[0] = red[0];
 }
 
+// Non-finite entries become zero; a 16-byte vector is written back only if it held one.
 template <typename T>
 __global__ __launch_bounds__(kBlock) void k_zero_nonfinite(MtArgs A) {
+  using M = ChunkMap<T>;
   const int t = find_tensor(A, blockIdx.x);
   const int64_t n = A.n[t];
   const int64_t start = (blockIdx.x - A.first_block[t]) * kChunk;
   const int64_t end = start + kChunk < n ? start + kChunk : n;
   T* __restrict__ g = (T*)A.a[t];
-  for (int64_t i = start + threadIdx.x; i < end; i += kBlock)
-    if (!isfinite(tg_to_float(g[i]))) g[i] = tg_from_float<T>(0.f);
+  if (start + kChunk <= n && al16(g)) {
+    tg_vec16<T> v[M::NV];
+#pragma unroll
+    for (int j = 0; j < M::NV; ++j) v[j] = tg_load16(g + M::at(start, j));
+#pragma unroll
+    for (int j = 0; j < M::NV; ++j) {
+      bool bad = false;
+#pragma unroll
+      for (int k = 0; k < M::PER; ++k)
+        if (!isfinite(tg_to_float(v[j].v[k]))) {
+          v[j].v[k] = tg_from_float<T>(0.f);
+          bad = true;
+        }
+      if (bad) tg_store16(g + M::at(start, j), v[j]);
+    }
+  } else {
+    for (int64_t i = start + threadIdx.x; i < end; i += kBlock)
+      if (!isfinite(tg_to_float(g[i]))) g[i] = tg_from_float<T>(0.f);
+  }
 }
 
 __global__ void k_zero_ints(int* p, int n) {
@@ -207,7 +315,8 @@ __global__ void k_zero_ints(int* p, int n) {
 // first tensor index) per launch.  Empty tensors are skipped.
 template <typename F>
 int for_each_launch(int ntensors, void* const* a, void* const* b, void* const* c,
-                    void* const* d, void* const* e, const int64_t* numel, F&& fn) {
+                    void* const* d, void* const* e, const int64_t* numel, F&& fn,
+                    int64_t chunk = kChunk) {
   MtArgs A{};
   int64_t blocks = 0;
   auto flush = [&]() -> int {
@@ -243,7 +352,7 @@ int for_each_launch(int ntensors, void* const* a, void* const* b, void* const* c
     A.n[k] = numel[i];
     A.fidx[k] = i;
     A.first_block[k] = blocks;
-    blocks += (numel[i] + kChunk - 1) / kChunk;
+    blocks += (numel[i] + chunk - 1) / chunk;
   }
   return flush();
 }
@@ -283,8 +392,8 @@ TG_EXPORT int tg_adam_step(int ntensors, float* const* params, const float* cons
   K.eps = (float)eps;
   K.lrwd = (float)(lr * weight_decay);
   K.decay = weight_decay != 0.0;
-  K.bc1 = (float)bias_correction1;
-  K.bc2 = (float)bias_correction2;
+  K.ibc1 = (float)(1.0 / bias_correction1);
+  K.ibc2 = (float)(1.0 / bias_correction2);
   return for_each_launch(
       ntensors, (void* const*)params, (void* const*)grads, (void* const*)exp_avg,
       (void* const*)exp_avg_sq, (void* const*)max_exp_avg_sq, numel,
@@ -294,7 +403,8 @@ TG_EXPORT int tg_adam_step(int ntensors, float* const* params, const float* cons
         else
           k_adam<false><<<(unsigned)nb, kBlock, 0, s>>>(A, K);
         return tg_check_launch("tg_adam_step");
-      });
+      },
+      kAdamChunk);
 }
 
 // Multiply every gradient by `mul` (when write != 0) and report non-finite values:

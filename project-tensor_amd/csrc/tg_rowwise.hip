@@ -14,6 +14,8 @@
 namespace {
 
 constexpr int kBlock = 256;
+// Outputs at least this large skip cache retention (non-temporal stores).
+constexpr int64_t kNtBytes = 128ll << 20;
 
 // ---------------------------------------------------------------------------
 // Partial sums across the TPR threads of a row group.  For TPR == 256 the block
@@ -101,7 +103,7 @@ template <typename T, int TPR, int VPT, bool ACC>
 __global__ __launch_bounds__(kBlock) void k_softmax_bwd_reg(const T* __restrict__ y,
                                                             const T* __restrict__ dy,
                                                             T* __restrict__ dx, int64_t rows,
-                                                            int cols) {
+                                                            int cols, bool nt) {
   constexpr int V = tg_vec16<T>::N;
   constexpr int G = kBlock / TPR;
   __shared__ float red[8];
@@ -136,7 +138,8 @@ __global__ __launch_bounds__(kBlock) void k_softmax_bwd_reg(const T* __restrict_
         if (ACC) r += tg_to_float(o.v[j]);
         o.v[j] = tg_from_float<T>(r);
       }
-      tg_store16(dx + off + vi * V, o);
+      if (nt) tg_store16_nt(dx + off + vi * V, o);
+      else tg_store16(dx + off + vi * V, o);
     }
   }
 }
@@ -242,16 +245,17 @@ int softmax_bwd_t(const void* y, const void* dy, void* dx, int64_t rows, int64_t
   if (pick_reg_shape<T>(cols, al, &tpr, &vpt)) {
     const int64_t g = kBlock / tpr;
     const unsigned blocks = (unsigned)((rows + g - 1) / g);
+    const bool nt = (int64_t)sizeof(T) * rows * cols >= kNtBytes;
     if (acc) {
 #define L(TPR, VPT)                                                                            \
   k_softmax_bwd_reg<T, TPR, VPT, true><<<blocks, kBlock, 0, s>>>((const T*)y, (const T*)dy, \
-                                                                 (T*)dx, rows, (int)cols)
+                                                                 (T*)dx, rows, (int)cols, nt)
       TG_REG_DISPATCH(L)
 #undef L
     } else {
 #define L(TPR, VPT)                                                                             \
   k_softmax_bwd_reg<T, TPR, VPT, false><<<blocks, kBlock, 0, s>>>((const T*)y, (const T*)dy, \
-                                                                  (T*)dx, rows, (int)cols)
+                                                                  (T*)dx, rows, (int)cols, nt)
       TG_REG_DISPATCH(L)
 #undef L
     }
@@ -377,7 +381,7 @@ template <typename T, int TPR, int VPT, bool ACC>
 __global__ __launch_bounds__(kBlock) void k_ln_bwd_reg(
     const T* __restrict__ x, const float* __restrict__ mean, const float* __restrict__ rstd,
     const float* __restrict__ gamma, const T* __restrict__ dy, T* __restrict__ dx,
-    float* __restrict__ part, int64_t rows, int cols) {
+    float* __restrict__ part, int64_t rows, int cols, bool nt) {
   constexpr int V = tg_vec16<T>::N;
   constexpr int G = kBlock / TPR;
   __shared__ float red[8];
@@ -471,7 +475,8 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_reg(
             if (ACC) r += tg_to_float(o.v[j]);
             o.v[j] = tg_from_float<T>(r);
           }
-          tg_store16(dx + off + vi * V, o);
+          if (nt) tg_store16_nt(dx + off + vi * V, o);
+          else tg_store16(dx + off + vi * V, o);
         }
       }
     }
@@ -659,18 +664,19 @@ int ln_bwd_t(const void* x, const float* mean, const float* rstd, const float* g
   if (p.reg) {
     const unsigned blocks = (unsigned)p.nparts;
     const int tpr = p.tpr, vpt = p.vpt;
+    const bool nt = (int64_t)sizeof(T) * rows * cols >= kNtBytes;
     if (acc_dx) {
 #define L(TPR, VPT)                                                                           \
   k_ln_bwd_reg<T, TPR, VPT, true><<<blocks, kBlock, 0, s>>>((const T*)x, mean, rstd, gamma, \
                                                             (const T*)dy, (T*)dx, part, rows, \
-                                                            (int)cols)
+                                                            (int)cols, nt)
       TG_REG_DISPATCH(L)
 #undef L
     } else {
 #define L(TPR, VPT)                                                                            \
   k_ln_bwd_reg<T, TPR, VPT, false><<<blocks, kBlock, 0, s>>>((const T*)x, mean, rstd, gamma, \
                                                              (const T*)dy, (T*)dx, part, rows, \
-                                                             (int)cols)
+                                                             (int)cols, nt)
       TG_REG_DISPATCH(L)
 #undef L
     }
@@ -688,15 +694,9 @@ int ln_bwd_t(const void* x, const float* mean, const float* rstd, const float* g
   }
   int st = tg_check_launch("tg_layernorm_bwd");
   if (st) return st;
-  float* scratch = part + 2 * p.nparts * cols;
-  if (dgamma) {
-    st = tg_sum_partials(part, p.nparts, cols, TG_F32, dgamma, acc_params, scratch, s);
-    if (st) return st;
-  }
-  if (dbeta)
-    st = tg_sum_partials(part + p.nparts * cols, p.nparts, cols, TG_F32, dbeta, acc_params,
-                         scratch, s);
-  return st;
+  if (!dgamma && !dbeta) return TG_OK;
+  return tg_sum_partials2(part, p.nparts, cols, TG_F32, dgamma, dbeta, acc_params,
+                          part + 2 * p.nparts * cols, s);
 }
 
 }  // namespace
@@ -755,7 +755,7 @@ TG_EXPORT size_t tg_layernorm_bwd_workspace(int dtype, int64_t rows, int64_t col
   LnBwdPlan a = ln_bwd_plan_dt(dtype, rows, cols, true);
   LnBwdPlan b = ln_bwd_plan_dt(dtype, rows, cols, false);
   const int64_t np = a.nparts > b.nparts ? a.nparts : b.nparts;
-  return (size_t)(2 * np * cols) * sizeof(float) + tg_sum_partials_scratch(np, cols);
+  return (size_t)(2 * np * cols) * sizeof(float) + tg_sum_partials_scratch(np, cols, 2);
 }
 
 TG_EXPORT int tg_layernorm_bwd(int dtype, const void* x, const float* mean, const float* rstd,
@@ -769,7 +769,7 @@ TG_EXPORT int tg_layernorm_bwd(int dtype, const void* x, const float* mean, cons
   const bool al = tg_aligned16(x) && tg_aligned16(dy) && tg_aligned16(dx);
   LnBwdPlan p = ln_bwd_plan_dt(dtype, rows, cols, al);
   const size_t need =
-      (size_t)(2 * p.nparts * cols) * sizeof(float) + tg_sum_partials_scratch(p.nparts, cols);
+      (size_t)(2 * p.nparts * cols) * sizeof(float) + tg_sum_partials_scratch(p.nparts, cols, 2);
   if (!workspace || workspace_bytes < need) {
     tg_set_error("tg_layernorm_bwd: workspace of %zu bytes needed, got %zu", need,
                  workspace ? workspace_bytes : (size_t)0);

@@ -370,3 +370,47 @@ def test_grad_norm(cuda, kind):
     assert flags == [0, 0, 1, 0]
     L().zero_nonfinite(gs)
     assert np.array_equal(gs[2].cpu().numpy(), fin[2].astype(np.float32))
+
+
+def test_multi_tensor_many_and_misaligned(cuda):
+    """More tensors than one launch holds, mixed sizes (full chunks, tails, 16-byte
+    misaligned views) through Adam, unscale, grad norm and zero_nonfinite."""
+    rng = np.random.default_rng(11)
+    sizes = [(4096 * (i % 5) + 37 * i + 1) for i in range(45)]
+
+    def make(n, i, dt=torch.float32):
+        t = dev(rng.standard_normal(n), dt)
+        return misaligned(t) if i % 7 == 3 else t
+    ps = [make(n, i) for i, n in enumerate(sizes)]
+    gs = [make(n, i) * 1e-2 for i, n in enumerate(sizes)]
+    ms = [torch.zeros_like(p) for p in ps]
+    vs = [torch.zeros_like(p) for p in ps]
+    ref = [(f64(p), np.zeros(p.numel()), np.zeros(p.numel())) for p in ps]
+    L().adam_step(ps, gs, ms, vs, None, 1e-3, 0.9, 0.999, 1e-8, 0.01, 0.1, 0.001)
+    for (p0, m0, v0), p, m, v, g in zip(ref, ps, ms, vs, gs):
+        rp, rm, rv = O.adam_step(p0, f64(g), m0, v0, 1, lr=1e-3, weight_decay=0.01)[:3]
+        assert_close(p, rp, RTOL_F32, "adam p")
+        assert_close(m, rm, RTOL_F32, "adam m")
+        assert_close(v, rv, RTOL_F32, "adam v")
+    for dt in (torch.float32, torch.float16):
+        hs = [make(n, i, dt) for i, n in enumerate(sizes)]
+        bad = {5: 0, 17: sizes[17] - 1, 40: sizes[40] // 2}
+        for i, pos in bad.items():
+            hs[i][pos] = float("inf") if i != 17 else float("nan")
+        host = [f64(h) for h in hs]
+        val, flags = L().grad_norm(hs, 0)
+        fin = [np.where(np.isfinite(h), h, 0.0) for h in host]
+        want = sum((f.astype(np.float64) ** 2).sum() for f in fin)
+        assert abs(val - want) <= 1e-9 * want
+        assert flags == [1 if i in bad else 0 for i in range(len(sizes))]
+        flags = L().unscale_check(hs, 0.5)
+        assert flags == [3 if i in bad else 0 for i in range(len(sizes))]
+        npdt = np.float16 if dt == torch.float16 else np.float32
+        half = [(x * 0.5).astype(npdt).astype(np.float64) for x in host]  # rounded as stored
+        for h, exp in zip(hs, half):
+            got = f64(h)
+            ok = np.isfinite(exp)
+            assert np.array_equal(got[ok], exp[ok])
+        L().zero_nonfinite(hs)
+        for h, exp in zip(hs, half):
+            assert np.array_equal(f64(h), np.where(np.isfinite(exp), exp, 0.0))
