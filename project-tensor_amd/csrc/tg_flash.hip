@@ -14,8 +14,10 @@
 // no data movement, provided the other operand is read with the matching
 // permutation of k.  For a 32-row tile and k-step s (0,1) the lane's 8 elements are
 // its accumulator registers r = 8*s + e, i.e. rows 16*s + 8*(e/4) + 4*h + e%4.
-// That other operand is staged in LDS "4-row interleaved" ([row/4][d][row%4]) so
-// each lane fetches its two 4-row groups with two 8-byte reads.
+// That other operand is staged in LDS "8-row interleaved": within each 16-row block
+// the rows 4h+i and 8+4h+i (h = 0,1; i = 0..3) of column d sit next to each other,
+// il[((row/16)*2 + h)*D + d][8], so each lane fetches its 8 k-elements with one
+// 16-byte read.
 //
 // Forward: one workgroup = 128 queries (4 waves x 32), K/V tiles of 64 keys.
 //   S^T = K Q^T (lane = query), online softmax per lane, O^T += V^T P^T.
@@ -55,17 +57,11 @@ __device__ __forceinline__ typename Vec8<T>::type ld8(const T* p) {
   return *reinterpret_cast<const typename Vec8<T>::type*>(p);
 }
 
-// Two 4-element groups from an interleaved tile il[rows/4][D][4]: groups g1, g2 at column d.
+// The 8 k-elements of MFMA k-step `blk` (= 16-row block * 2 + lane half) at column
+// d of an 8-row interleaved tile.
 template <typename T, int D>
-__device__ __forceinline__ typename Vec8<T>::type ld_il(const T* il, int g1, int g2, int d) {
-  union {
-    uint4 u;
-    typename Vec8<T>::type v;
-  } r;
-  const uint2 a = *reinterpret_cast<const uint2*>(il + ((g1 * D) + d) * 4);
-  const uint2 b = *reinterpret_cast<const uint2*>(il + ((g2 * D) + d) * 4);
-  r.u = make_uint4(a.x, a.y, b.x, b.y);
-  return r.v;
+__device__ __forceinline__ typename Vec8<T>::type ld_il(const T* il, int blk, int d) {
+  return ld8(il + (blk * D + d) * 8);
 }
 
 template <typename T>
@@ -77,36 +73,39 @@ __device__ __forceinline__ typename Vec8<T>::type pack8(const float* v) {
 }
 
 // Stage ROWS x D rows [row0, row0+ROWS) of a [nrows, D] matrix into LDS, row-major
-// (rm, row stride D+8) and/or 4-row interleaved (il).  Rows past nrows are zero.
+// (rm, row stride D+8) and/or 8-row interleaved (il).  Rows past nrows are zero.
+// A work unit is 8 rows (rows 16b + 4hh + i and 16b + 8 + 4hh + i) x 8 columns.
 template <typename T, int ROWS, int D, bool RM, bool IL>
 __device__ __forceinline__ void stage(const T* __restrict__ g, int64_t row0, int64_t nrows,
                                       T* rm, T* il) {
   constexpr int DG = D / 8;
-  constexpr int UNITS = (ROWS / 4) * DG;
+  constexpr int UNITS = (ROWS / 16) * 2 * DG;
   for (int u = threadIdx.x; u < UNITS; u += kThreads) {
-    const int rg = u / DG, dg = u % DG;
-    uint4 v[4];
+    const int dg = u % DG, bh2 = u / DG;  // bh2 = 16-row block * 2 + hh
+    const int rb = bh2 >> 1, hh = bh2 & 1;
+    uint4 v[8];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int64_t row = row0 + rg * 4 + r;
-      v[r] = row < nrows ? *reinterpret_cast<const uint4*>(g + row * D + dg * 8)
+    for (int j = 0; j < 8; ++j) {
+      const int r = rb * 16 + (j >> 2) * 8 + hh * 4 + (j & 3);
+      const int64_t row = row0 + r;
+      v[j] = row < nrows ? *reinterpret_cast<const uint4*>(g + row * D + dg * 8)
                          : make_uint4(0, 0, 0, 0);
     }
     if (RM) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        *reinterpret_cast<uint4*>(rm + (rg * 4 + r) * (D + 8) + dg * 8) = v[r];
+      for (int j = 0; j < 8; ++j) {
+        const int r = rb * 16 + (j >> 2) * 8 + hh * 4 + (j & 3);
+        *reinterpret_cast<uint4*>(rm + r * (D + 8) + dg * 8) = v[j];
+      }
     }
     if (IL) {
-      const T* e0 = reinterpret_cast<const T*>(&v[0]);
-      const T* e1 = reinterpret_cast<const T*>(&v[1]);
-      const T* e2 = reinterpret_cast<const T*>(&v[2]);
-      const T* e3 = reinterpret_cast<const T*>(&v[3]);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        T q4[4] = {e0[j], e1[j], e2[j], e3[j]};
-        *reinterpret_cast<uint2*>(il + ((rg * D) + dg * 8 + j) * 4) =
-            *reinterpret_cast<const uint2*>(q4);
+      for (int c = 0; c < 8; ++c) {
+        T e8[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) e8[j] = reinterpret_cast<const T*>(&v[j])[c];
+        *reinterpret_cast<uint4*>(il + (bh2 * D + dg * 8 + c) * 8) =
+            *reinterpret_cast<const uint4*>(e8);
       }
     }
   }
@@ -219,10 +218,9 @@ __global__ __launch_bounds__(kThreads) void k_fa_fwd(const T* __restrict__ Q,
 #pragma unroll
       for (int sg = 0; sg < 2; ++sg) {
         const typename Vec8<T>::type pb = pack8<T>(&p[8 * sg]);
-        const int g1 = (kt * 32 + 16 * sg + 4 * h) >> 2;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
-          o[dt] = mfma(ld_il<T, D>(Vi, g1, g1 + 2, dt * 32 + l32), pb, o[dt]);
+          o[dt] = mfma(ld_il<T, D>(Vi, (kt * 2 + sg) * 2 + h, dt * 32 + l32), pb, o[dt]);
       }
     }
   }
@@ -280,15 +278,85 @@ __device__ __forceinline__ void store_c_tile(T* __restrict__ out, int64_t ld, in
   }
 }
 
+// One 32-query x 32-key sub-tile of the dK/dV kernel for one wave.
+//   qrow/dorow: this lane's row of the row-major Q / dO tile (query t*32 + l32,
+//               d offset h*8); qil/doil: interleaved tiles at block (t*4 + h),
+//               column l32; lse/dvs: the sub-tile's 32 log2-scaled LSE values and
+//               scale*D values.
+//   DIAG: the sub-tile straddles the causal diagonal; key > query is masked, with
+//   mb = (first key of the wave's 32 + l32) - (first query of the sub-tile) - 4h,
+//   so that the mask for accumulator register r is mb > 8*(r/4) + r%4.
+template <typename T, int D, bool DIAG>
+__device__ __forceinline__ void dkdv_subtile(const T* qrow, const T* dorow, const T* qil,
+                                             const T* doil, const float* lse,
+                                             const float* dvs, int h,
+                                             const typename Vec8<T>::type (&kf)[D / 16],
+                                             const typename Vec8<T>::type (&vf)[D / 16],
+                                             f32x16 (&dk)[D / 32], f32x16 (&dv)[D / 32],
+                                             float sl2, float scale, int mb) {
+  constexpr int DK = D / 16, DT = D / 32;
+  f32x16 s, dp;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    s[r] = 0.f;
+    dp[r] = 0.f;
+  }
+#pragma unroll
+  for (int ks = 0; ks < DK; ++ks) s = mfma(ld8(qrow + ks * 16), kf[ks], s);
+#pragma unroll
+  for (int ks = 0; ks < DK; ++ks) dp = mfma(ld8(dorow + ks * 16), vf[ks], dp);
+  // Padded query rows are zero in the Q/dO tiles with lse = D = 0, so they add
+  // nothing to dV (dO row 0) or dK (dS = P*(0-0) = 0); padded keys only feed dK/dV
+  // rows that are never stored.  Only the causal diagonal needs a mask.
+  float p[16];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const float4 a = *reinterpret_cast<const float4*>(lse + 8 * g + 4 * h);
+    const float la[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * g + i;
+      float pv = fexp2(fmaf(s[r], sl2, -la[i]));
+      if (DIAG) pv = (mb > 8 * g + i) ? 0.f : pv;
+      p[r] = pv;
+    }
+  }
+#pragma unroll
+  for (int sg = 0; sg < 2; ++sg) {
+    const typename Vec8<T>::type pa = pack8<T>(&p[8 * sg]);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+      dv[dt] = mfma(pa, ld_il<T, D>(doil, 2 * sg, dt * 32), dv[dt]);
+  }
+  float ds[16];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const float4 b = *reinterpret_cast<const float4*>(dvs + 8 * g + 4 * h);
+    const float db[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * g + i;
+      ds[r] = p[r] * fmaf(dp[r], scale, -db[i]);
+    }
+  }
+#pragma unroll
+  for (int sg = 0; sg < 2; ++sg) {
+    const typename Vec8<T>::type da = pack8<T>(&ds[8 * sg]);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+      dk[dt] = mfma(da, ld_il<T, D>(qil, 2 * sg, dt * 32), dk[dt]);
+  }
+}
+
 // dK, dV.  grid = (ceil(Sk/128), B*H).  Query tiles of 128 staged per step; the four
 // 32-query sub-tiles are processed one after another to keep P/dS in 32 registers.
-template <typename T, int D>
-__global__ __launch_bounds__(kThreads) void k_fa_bwd_dkdv(
+template <typename T, int D, int BM, int OCC>
+__global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dkdv(
     const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
     const T* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Dv,
     T* __restrict__ dK, T* __restrict__ dV, int64_t Sq, int64_t Sk, float scale, int causal,
     int accumulate) {
-  constexpr int BM = 128, DK = D / 16, DT = D / 32;
+  constexpr int DK = D / 16, DT = D / 32;
   __shared__ __attribute__((aligned(16))) T Qs[BM * (D + 8)];
   __shared__ __attribute__((aligned(16))) T Qi[BM * D];
   __shared__ __attribute__((aligned(16))) T dOs[BM * (D + 8)];
@@ -333,6 +401,11 @@ __global__ __launch_bounds__(kThreads) void k_fa_bwd_dkdv(
       dk[dt][r] = 0.f;
       dv[dt][r] = 0.f;
     }
+  // per-lane bases: row-major tiles at (row l32, d h*8); interleaved at (group h, col l32)
+  const T* qrow0 = Qs + l32 * (D + 8) + h * 8;
+  const T* dorow0 = dOs + l32 * (D + 8) + h * 8;
+  const T* qil0 = Qi + (h * D + l32) * 8;
+  const T* doil0 = dOi + (h * D + l32) * 8;
   // causal: queries below the first key of this block contribute nothing
   int64_t qstart = 0;
   if (causal) qstart = (kblk / BM) * BM;
@@ -343,55 +416,25 @@ __global__ __launch_bounds__(kThreads) void k_fa_bwd_dkdv(
     if (threadIdx.x < BM) {
       const int64_t qq = q0 + threadIdx.x;
       lse2[threadIdx.x] = qq < Sq ? LSE[qq] * kLog2e : 0.f;
-      dvec[threadIdx.x] = qq < Sq ? Dv[qq] : 0.f;
+      dvec[threadIdx.x] = qq < Sq ? Dv[qq] * scale : 0.f;
     }
     __syncthreads();
+    // key offset of this wave relative to the staged query tile
+    const int kq = (int)(kblk - q0) + wave * 32;
 #pragma unroll 1
     for (int t = 0; t < BM / 32; ++t) {
       // causal: a 32-query sub-tile wholly before this wave's keys contributes nothing
-      if (causal && q0 + t * 32 + 31 < kblk + wave * 32) continue;
-      f32x16 s, dp;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s[r] = 0.f;
-        dp[r] = 0.f;
-      }
-#pragma unroll
-      for (int ks = 0; ks < DK; ++ks) {
-        s = mfma(ld8(Qs + (t * 32 + l32) * (D + 8) + ks * 16 + h * 8), kf[ks], s);
-        dp = mfma(ld8(dOs + (t * 32 + l32) * (D + 8) + ks * 16 + h * 8), vf[ks], dp);
-      }
-      // Padded query rows are zero in Qs/dOs with lse = D = 0, so they add nothing to
-      // dV (dO row 0) or dK (dS = P*(0-0) = 0); padded keys only feed dK/dV rows that
-      // are never stored.  Only the causal diagonal needs a mask.
-      const bool diag = causal && (kblk + wave * 32 + 31 > q0 + t * 32);
-      float lv[16], dvv[16];
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const float4 a = *reinterpret_cast<const float4*>(lse2 + t * 32 + 8 * g + 4 * h);
-        const float4 b = *reinterpret_cast<const float4*>(dvec + t * 32 + 8 * g + 4 * h);
-        lv[4 * g] = a.x; lv[4 * g + 1] = a.y; lv[4 * g + 2] = a.z; lv[4 * g + 3] = a.w;
-        dvv[4 * g] = b.x; dvv[4 * g + 1] = b.y; dvv[4 * g + 2] = b.z; dvv[4 * g + 3] = b.w;
-      }
-      float p[16], ds[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float pv = fexp2(fmaf(s[r], sl2, -lv[r]));
-        if (diag && key > q0 + t * 32 + crow(r, h)) pv = 0.f;
-        p[r] = pv;
-        ds[r] = pv * (dp[r] - dvv[r]) * scale;
-      }
-#pragma unroll
-      for (int sg = 0; sg < 2; ++sg) {
-        const typename Vec8<T>::type pa = pack8<T>(&p[8 * sg]);
-        const typename Vec8<T>::type da = pack8<T>(&ds[8 * sg]);
-        const int g1 = (t * 32 + 16 * sg + 4 * h) >> 2;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          dv[dt] = mfma(pa, ld_il<T, D>(dOi, g1, g1 + 2, dt * 32 + l32), dv[dt]);
-          dk[dt] = mfma(da, ld_il<T, D>(Qi, g1, g1 + 2, dt * 32 + l32), dk[dt]);
-        }
-      }
+      if (causal && t * 32 + 31 < kq) continue;
+      const T* qrow = qrow0 + t * 32 * (D + 8);
+      const T* dorow = dorow0 + t * 32 * (D + 8);
+      const T* qil = qil0 + t * 4 * D * 8;
+      const T* doil = doil0 + t * 4 * D * 8;
+      if (causal && kq + 31 > t * 32)
+        dkdv_subtile<T, D, true>(qrow, dorow, qil, doil, lse2 + t * 32, dvec + t * 32, h, kf,
+                                 vf, dk, dv, sl2, scale, kq + l32 - t * 32 - 4 * h);
+      else
+        dkdv_subtile<T, D, false>(qrow, dorow, qil, doil, lse2 + t * 32, dvec + t * 32, h, kf,
+                                  vf, dk, dv, sl2, scale, 0);
     }
   }
   // C tiles: rows = keys of this wave, cols = d
@@ -402,13 +445,53 @@ __global__ __launch_bounds__(kThreads) void k_fa_bwd_dkdv(
   }
 }
 
+// One 32-key x 32-query sub-tile of the dQ kernel for one wave (lane = query).
+//   krow/vrow: this lane's row of the row-major K / V tile (key kt*32 + l32, d h*8);
+//   kil: interleaved K at block (kt*4 + h), column l32.
+//   DIAG: masks key > query, with mq = (query of this lane) - (first key of the
+//   sub-tile) - 4h, so that register r is masked when 8*(r/4) + r%4 > mq.
+template <typename T, int D, bool DIAG>
+__device__ __forceinline__ void dq_subtile(const T* krow, const T* vrow, const T* kil,
+                                           const typename Vec8<T>::type (&qf)[D / 16],
+                                           const typename Vec8<T>::type (&of)[D / 16],
+                                           f32x16 (&acc)[D / 32], float sl2, float scale,
+                                           float lq, float dqs, int mq) {
+  constexpr int DK = D / 16, DT = D / 32;
+  f32x16 s, dp;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    s[r] = 0.f;
+    dp[r] = 0.f;
+  }
+#pragma unroll
+  for (int ks = 0; ks < DK; ++ks) s = mfma(ld8(krow + ks * 16), qf[ks], s);
+#pragma unroll
+  for (int ks = 0; ks < DK; ++ks) dp = mfma(ld8(vrow + ks * 16), of[ks], dp);
+  // Padded keys are zero rows of K/V, so they add nothing to dQ (dS * 0); only the
+  // causal diagonal needs a mask.
+  float ds[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    float pv = fexp2(fmaf(s[r], sl2, -lq));
+    if (DIAG) pv = (8 * (r >> 2) + (r & 3) > mq) ? 0.f : pv;
+    ds[r] = pv * fmaf(dp[r], scale, -dqs);
+  }
+#pragma unroll
+  for (int sg = 0; sg < 2; ++sg) {
+    const typename Vec8<T>::type da = pack8<T>(&ds[8 * sg]);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+      acc[dt] = mfma(da, ld_il<T, D>(kil, 2 * sg, dt * 32), acc[dt]);
+  }
+}
+
 // dQ.  grid = (ceil(Sq/128), B*H).
-template <typename T, int D>
-__global__ __launch_bounds__(kThreads) void k_fa_bwd_dq(
+template <typename T, int D, int BN, int OCC>
+__global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dq(
     const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
     const T* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Dv,
     T* __restrict__ dQ, int64_t Sq, int64_t Sk, float scale, int causal, int accumulate) {
-  constexpr int BN = 128, DK = D / 16, DT = D / 32;
+  constexpr int DK = D / 16, DT = D / 32;
   __shared__ __attribute__((aligned(16))) T Ks[BN * (D + 8)];
   __shared__ __attribute__((aligned(16))) T Ki[BN * D];
   __shared__ __attribute__((aligned(16))) T Vs[BN * (D + 8)];
@@ -443,12 +526,15 @@ __global__ __launch_bounds__(kThreads) void k_fa_bwd_dq(
     }
   }
   const float lq = q < Sq ? LSE[q] * kLog2e : 0.f;
-  const float dq_d = q < Sq ? Dv[q] : 0.f;
+  const float dqs = q < Sq ? Dv[q] * scale : 0.f;
   f32x16 acc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
+  const T* krow0 = Ks + l32 * (D + 8) + h * 8;
+  const T* vrow0 = Vs + l32 * (D + 8) + h * 8;
+  const T* kil0 = Ki + (h * D + l32) * 8;
   int64_t kend = Sk;
   if (causal) kend = (qblk + 128 < Sk) ? qblk + 128 : Sk;
   for (int64_t k0 = 0; k0 < kend; k0 += BN) {
@@ -456,39 +542,20 @@ __global__ __launch_bounds__(kThreads) void k_fa_bwd_dq(
     stage<T, BN, D, true, true>(K, k0, Sk, Ks, Ki);
     stage<T, BN, D, true, false>(V, k0, Sk, Vs, nullptr);
     __syncthreads();
+    // query of this wave's first lane relative to the staged key tile
+    const int qk = (int)(qblk - k0) + wave * 32;
 #pragma unroll 1
     for (int kt = 0; kt < BN / 32; ++kt) {
       // causal: a 32-key sub-tile wholly after this wave's queries contributes nothing
-      if (causal && k0 + kt * 32 > qblk + wave * 32 + 31) continue;
-      f32x16 s, dp;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s[r] = 0.f;
-        dp[r] = 0.f;
-      }
-#pragma unroll
-      for (int ks = 0; ks < DK; ++ks) {
-        s = mfma(ld8(Ks + (kt * 32 + l32) * (D + 8) + ks * 16 + h * 8), qf[ks], s);
-        dp = mfma(ld8(Vs + (kt * 32 + l32) * (D + 8) + ks * 16 + h * 8), of[ks], dp);
-      }
-      // Padded keys are zero rows of K/V, so they add nothing to dQ (dS * 0); only the
-      // causal diagonal needs a mask.
-      const bool diag = causal && (k0 + kt * 32 + 31 > qblk + wave * 32);
-      float ds[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float pv = fexp2(fmaf(s[r], sl2, -lq));
-        if (diag && k0 + kt * 32 + crow(r, h) > q) pv = 0.f;
-        ds[r] = pv * (dp[r] - dq_d) * scale;
-      }
-#pragma unroll
-      for (int sg = 0; sg < 2; ++sg) {
-        const typename Vec8<T>::type da = pack8<T>(&ds[8 * sg]);
-        const int g1 = (kt * 32 + 16 * sg + 4 * h) >> 2;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-          acc[dt] = mfma(da, ld_il<T, D>(Ki, g1, g1 + 2, dt * 32 + l32), acc[dt]);
-      }
+      if (causal && kt * 32 > qk + 31) continue;
+      const T* krow = krow0 + kt * 32 * (D + 8);
+      const T* vrow = vrow0 + kt * 32 * (D + 8);
+      const T* kil = kil0 + kt * 4 * D * 8;
+      if (causal && kt * 32 + 31 > qk)
+        dq_subtile<T, D, true>(krow, vrow, kil, qf, of, acc, sl2, scale, lq, dqs,
+                               qk + l32 - kt * 32 - 4 * h);
+      else
+        dq_subtile<T, D, false>(krow, vrow, kil, qf, of, acc, sl2, scale, lq, dqs, 0);
     }
   }
   // C tiles: rows = queries of this wave, cols = d
@@ -506,6 +573,16 @@ int fwd_t(const void* q, const void* k, const void* v, void* o, float* lse, int6
   return tg_check_launch("tg_flash_attn_fwd");
 }
 
+// Backward tile shapes per head dim: staged query rows of the dK/dV kernel, staged
+// key rows of the dQ kernel, and the workgroups per CU each is compiled for.
+template <int D> struct BwdCfg;
+template <> struct BwdCfg<64> {
+  static constexpr int BM = 64, OCC_KV = 2, BN = 64, OCC_Q = 3;
+};
+template <> struct BwdCfg<128> {
+  static constexpr int BM = 128, OCC_KV = 1, BN = 64, OCC_Q = 2;
+};
+
 template <typename T, int D>
 int bwd_t(const void* q, const void* k, const void* v, const void* o, const void* dout,
           const float* lse, void* dq, void* dk, void* dv, int64_t BH, int64_t Sq, int64_t Sk,
@@ -514,11 +591,12 @@ int bwd_t(const void* q, const void* k, const void* v, const void* o, const void
   k_fa_bwd_prep<T, D><<<(unsigned)((rows + 15) / 16), kThreads, 0, s>>>(
       (const T*)o, (const T*)dout, dvec, rows);
   dim3 gkv((unsigned)((Sk + 127) / 128), (unsigned)BH);
-  k_fa_bwd_dkdv<T, D><<<gkv, kThreads, 0, s>>>((const T*)q, (const T*)k, (const T*)v,
+  using C = BwdCfg<D>;
+  k_fa_bwd_dkdv<T, D, C::BM, C::OCC_KV><<<gkv, kThreads, 0, s>>>((const T*)q, (const T*)k, (const T*)v,
                                                (const T*)dout, lse, dvec, (T*)dk, (T*)dv, Sq, Sk,
                                                scale, causal, acc);
   dim3 gq((unsigned)((Sq + 127) / 128), (unsigned)BH);
-  k_fa_bwd_dq<T, D><<<gq, kThreads, 0, s>>>((const T*)q, (const T*)k, (const T*)v,
+  k_fa_bwd_dq<T, D, C::BN, C::OCC_Q><<<gq, kThreads, 0, s>>>((const T*)q, (const T*)k, (const T*)v,
                                             (const T*)dout, lse, dvec, (T*)dq, Sq, Sk, scale,
                                             causal, acc);
   return tg_check_launch("tg_flash_attn_bwd");
