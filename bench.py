@@ -31,6 +31,36 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2500.0
 
+# Measured HBM traffic per launch of the headline kernels: profiles/c2_traffic.txt
+# holds lines `traffic <kernel> <bytes>` made by project-tensor_amd/prof_summary.py
+# from two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) scaled by a copy of known
+# size.  Each headline op maps to the kernels it launches.
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "c2_traffic.txt")
+OP_KERNELS = {"gelu_bwd": ["k_act_bwd<float,0,"], "silu_bwd": ["k_act_bwd<float,1,"],
+              "softmax_bwd": ["k_softmax_bwd_reg<float,"],
+              "layernorm_bwd": ["k_ln_bwd_reg<float,", "k_colsum<float,"]}
+
+
+def measured_traffic(op):
+    """HBM bytes per launch of a headline op from the committed counter summary, or
+    None when the summary or one of the op's kernels is missing."""
+    try:
+        lines = open(TRAFFIC_FILE).read().splitlines()
+    except OSError:
+        return None
+    table = {}
+    for ln in lines:
+        f = ln.split()
+        if len(f) >= 3 and f[0] == "traffic":
+            table[f[1]] = float(f[2])
+    total = 0.0
+    for prefix in OP_KERNELS.get(op, []):
+        hits = [v for k, v in table.items() if k.startswith(prefix)]
+        if not hits:
+            return None
+        total += hits[0]
+    return round(total) if OP_KERNELS.get(op) else None
+
 
 def _args():
     ap = argparse.ArgumentParser()
@@ -379,7 +409,7 @@ def main():
                                "[16384,4096]", "step_bytes": step_bytes},
         "roofline": {"bound": "hbm", "kernel": dom.name, "achieved": ds["achieved"],
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": ds["frac"],
-                     "traffic": None},
+                     "traffic": measured_traffic(dom.name)},
         "kernels": per,
         "components": comps,
     }

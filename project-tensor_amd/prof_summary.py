@@ -2,6 +2,7 @@
 
     python project-tensor_amd/prof_summary.py stats <dir>     # kernel_stats.csv table
     python project-tensor_amd/prof_summary.py pmc <dir> ...   # per-kernel counter means
+    python project-tensor_amd/prof_summary.py traffic <fetch_dir> <write_dir> <calib_bytes>
 
 ``stats`` prints, per kernel, calls, total and average duration.  ``pmc`` prints,
 per kernel, the mean per dispatch of every counter in counter_collection.csv
@@ -62,7 +63,43 @@ def pmc(d):
         print(f"{n:5d} dispatches  {vals}  {k}")
 
 
+def _pmc_means(d, counter):
+    tot = collections.defaultdict(float)
+    disp = collections.defaultdict(set)
+    for path in _find(d, "counter_collection.csv"):
+        for r in csv.DictReader(open(path)):
+            if _col(r, "Counter_Name") != counter:
+                continue
+            k = short(_col(r, "Kernel_Name"))
+            tot[k] += float(_col(r, "Counter_Value"))
+            disp[k].add(_col(r, "Dispatch_Id"))
+    return {k: tot[k] / len(disp[k]) for k in tot}
+
+
+def traffic(fetch_dir, write_dir, calib_bytes):
+    """HBM bytes per dispatch from FETCH_SIZE and WRITE_SIZE (KiB per dispatch), each
+    scaled by what the counter reads for the calibration copy (a device copy of
+    calib_bytes read + calib_bytes written): lines `traffic <kernel> <bytes>`."""
+    calib_bytes = float(calib_bytes)
+    f, w = _pmc_means(fetch_dir, "FETCH_SIZE"), _pmc_means(write_dir, "WRITE_SIZE")
+    cal = [k for k in f if "copyBuffer" in k]
+    if not cal or cal[0] not in w:
+        raise SystemExit("calibration copy kernel not found in both runs")
+    fs = calib_bytes / (f[cal[0]] * 1024.0)
+    ws = calib_bytes / (w[cal[0]] * 1024.0)
+    print(f"# calibration: {cal[0]} FETCH_SIZE {f[cal[0]]:.1f} KiB, WRITE_SIZE {w[cal[0]]:.1f} KiB "
+          f"for {calib_bytes:.0f} B each way -> fetch scale {fs:.4f}, write scale {ws:.4f}")
+    for k in sorted(f):
+        name = k[5:] if k.startswith("void ") else k
+        if k in w and (name.startswith("k_") or k == cal[0]):
+            fb, wb = f[k] * 1024.0 * fs, w[k] * 1024.0 * ws
+            print(f"traffic {name.replace(' ', '')} {fb + wb:.0f} # fetch {fb:.0f} write {wb:.0f}")
+
+
 if __name__ == "__main__":
-    mode, dirs = sys.argv[1], sys.argv[2:]
-    for d in dirs:
-        {"stats": stats, "pmc": pmc}[mode](d)
+    mode, args = sys.argv[1], sys.argv[2:]
+    if mode == "traffic":
+        traffic(*args)
+    else:
+        for d in args:
+            {"stats": stats, "pmc": pmc}[mode](d)
