@@ -363,10 +363,18 @@ def main():
         for op in ops:
             op.run(False)
     torch.cuda.synchronize()
+    # One event before each step and one after each op: consecutive ops share the
+    # boundary event, so each op's window is its launches plus one event's overhead.
     t0 = time.perf_counter()
     for _ in range(a.steps):
+        prev = torch.cuda.Event(enable_timing=True)
+        prev.record()
         for op in ops:
-            op.run(True)
+            op.fn()
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record()
+            op.ms.append((prev, ev))
+            prev = ev
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     step_bytes = sum(op.work for op in ops)

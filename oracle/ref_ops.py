@@ -208,10 +208,14 @@ def flash_attention_fwd(q, k, v, is_causal=False, scale=None, block_size=64):
     return o, lse
 
 
-def flash_attention_bwd(q, k, v, do, is_causal=False, scale=None, block_size=64):
+def flash_attention_bwd(q, k, v, do, is_causal=False, scale=None, block_size=64, o=None):
     """FlashAttention backward (_core.py:1799-1867): per query block recompute
     P = softmax(QK^T s [masked -1e9]); dV += P^T dO; dP = dO V^T;
-    dS = P*(dP - rowsum(P*dP))*s (masked -> 0); dQ = dS K; dK += dS^T Q."""
+    dS = P*(dP - rowsum(P*dP))*s (masked -> 0); dQ = dS K; dK += dS^T Q.
+
+    With `o` (the forward output as stored), the row term is rowsum(dO*O) instead, the
+    identity rowsum(P*dP) = rowsum(dO*O) that holds for exact O: this isolates a
+    kernel's arithmetic from the rounding of its stored O."""
     q4, sq = _as4(q)
     k4, _ = _as4(k)
     v4, _ = _as4(v)
@@ -234,7 +238,11 @@ def flash_attention_bwd(q, k, v, do, is_causal=False, scale=None, block_size=64)
         p = e / e.sum(-1, keepdims=True)
         dv += np.einsum("bhij,bhid->bhjd", p, doi)
         dp = np.einsum("bhid,bhjd->bhij", doi, v4)
-        ds = p * (dp - (p * dp).sum(-1, keepdims=True)) * scale
+        if o is None:
+            row = (p * dp).sum(-1, keepdims=True)
+        else:
+            row = (doi * _as4(o)[0][:, :, i:j]).sum(-1, keepdims=True)
+        ds = p * (dp - row) * scale
         if mask is not None:
             ds = np.where(mask, 0.0, ds)
         dq[:, :, i:j] += np.einsum("bhij,bhjd->bhid", ds, k4)

@@ -57,8 +57,14 @@ __device__ __forceinline__ typename Vec8<T>::type ld8(const T* p) {
   return *reinterpret_cast<const typename Vec8<T>::type*>(p);
 }
 
+// Column position of column d in an interleaved tile.  The low two bits are XORed
+// with bits 3-4, which spreads the stores of staging threads 8 columns apart over
+// the LDS banks; the swizzle depends on d mod 32 only, so a lane's 32-column reads
+// stay contiguous per 8 lanes and the per-lane base absorbs it.
+__device__ __forceinline__ int swz(int d) { return d ^ ((d >> 3) & 3); }
+
 // The 8 k-elements of MFMA k-step `blk` (= 16-row block * 2 + lane half) at column
-// d of an 8-row interleaved tile.
+// position d (already swizzled) of an 8-row interleaved tile.
 template <typename T, int D>
 __device__ __forceinline__ typename Vec8<T>::type ld_il(const T* il, int blk, int d) {
   return ld8(il + (blk * D + d) * 8);
@@ -75,11 +81,15 @@ __device__ __forceinline__ typename Vec8<T>::type pack8(const float* v) {
 // Stage ROWS x D rows [row0, row0+ROWS) of a [nrows, D] matrix into LDS, row-major
 // (rm, row stride D+8) and/or 8-row interleaved (il).  Rows past nrows are zero.
 // A work unit is 8 rows (rows 16b + 4hh + i and 16b + 8 + 4hh + i) x 8 columns.
+// All 8 loads of a unit are issued before any is used: rows past the end read a
+// clamped (valid) row and are replaced by zero when stored, so no load sits behind
+// a branch (a branch per load would serialise them).
 template <typename T, int ROWS, int D, bool RM, bool IL>
 __device__ __forceinline__ void stage(const T* __restrict__ g, int64_t row0, int64_t nrows,
                                       T* rm, T* il) {
   constexpr int DG = D / 8;
   constexpr int UNITS = (ROWS / 16) * 2 * DG;
+  const bool full = row0 + ROWS <= nrows;  // uniform
   for (int u = threadIdx.x; u < UNITS; u += kThreads) {
     const int dg = u % DG, bh2 = u / DG;  // bh2 = 16-row block * 2 + hh
     const int rb = bh2 >> 1, hh = bh2 & 1;
@@ -87,9 +97,16 @@ __device__ __forceinline__ void stage(const T* __restrict__ g, int64_t row0, int
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int r = rb * 16 + (j >> 2) * 8 + hh * 4 + (j & 3);
-      const int64_t row = row0 + r;
-      v[j] = row < nrows ? *reinterpret_cast<const uint4*>(g + row * D + dg * 8)
-                         : make_uint4(0, 0, 0, 0);
+      int64_t row = row0 + r;
+      if (!full) row = row < nrows ? row : nrows - 1;
+      v[j] = *reinterpret_cast<const uint4*>(g + row * D + dg * 8);
+    }
+    if (!full) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int r = rb * 16 + (j >> 2) * 8 + hh * 4 + (j & 3);
+        if (row0 + r >= nrows) v[j] = make_uint4(0, 0, 0, 0);
+      }
     }
     if (RM) {
 #pragma unroll
@@ -104,7 +121,7 @@ __device__ __forceinline__ void stage(const T* __restrict__ g, int64_t row0, int
         T e8[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) e8[j] = reinterpret_cast<const T*>(&v[j])[c];
-        *reinterpret_cast<uint4*>(il + (bh2 * D + dg * 8 + c) * 8) =
+        *reinterpret_cast<uint4*>(il + (bh2 * D + swz(dg * 8 + c)) * 8) =
             *reinterpret_cast<const uint4*>(e8);
       }
     }
@@ -151,16 +168,11 @@ __global__ __launch_bounds__(kThreads) void k_fa_fwd(const T* __restrict__ Q,
   const int64_t q = qblk + wave * 32 + l32;
   const float sl2 = scale * kLog2e;
 
+  // A query lane past Sq reads a clamped row; its output row is never stored.
+  const int64_t qc = q < Sq ? q : Sq - 1;
   typename Vec8<T>::type qf[DK];
 #pragma unroll
-  for (int ks = 0; ks < DK; ++ks) {
-    if (q < Sq) {
-      qf[ks] = ld8(Q + q * D + ks * 16 + h * 8);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qf[ks][e] = (T)0.f;
-    }
-  }
+  for (int ks = 0; ks < DK; ++ks) qf[ks] = ld8(Q + qc * D + ks * 16 + h * 8);
   f32x16 o[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
@@ -220,7 +232,7 @@ __global__ __launch_bounds__(kThreads) void k_fa_fwd(const T* __restrict__ Q,
         const typename Vec8<T>::type pb = pack8<T>(&p[8 * sg]);
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
-          o[dt] = mfma(ld_il<T, D>(Vi, (kt * 2 + sg) * 2 + h, dt * 32 + l32), pb, o[dt]);
+          o[dt] = mfma(ld_il<T, D>(Vi, (kt * 2 + sg) * 2 + h, dt * 32 + swz(l32)), pb, o[dt]);
       }
     }
   }
@@ -266,6 +278,16 @@ template <typename T>
 __device__ __forceinline__ void store_c_tile(T* __restrict__ out, int64_t ld, int64_t row0,
                                              int64_t nrows, int col, const f32x16& acc, float mul,
                                              bool accumulate, int h) {
+  if (row0 + 32 <= nrows) {  // uniform: every row exists, all loads in flight together
+    float prev[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      prev[r] = accumulate ? (float)out[(row0 + crow(r, h)) * ld + col] : 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      out[(row0 + crow(r, h)) * ld + col] = (T)(acc[r] * mul + prev[r]);
+    return;
+  }
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int64_t row = row0 + crow(r, h);
@@ -278,23 +300,104 @@ __device__ __forceinline__ void store_c_tile(T* __restrict__ out, int64_t ld, in
   }
 }
 
-// One 32-query x 32-key sub-tile of the dK/dV kernel for one wave.
-//   qrow/dorow: this lane's row of the row-major Q / dO tile (query t*32 + l32,
-//               d offset h*8); qil/doil: interleaved tiles at block (t*4 + h),
-//               column l32; lse/dvs: the sub-tile's 32 log2-scaled LSE values and
-//               scale*D values.
+// ---------------------------------------------------------------- backward tiles
+// The backward kernels stage Q/dO (dK/dV kernel) or K/V (dQ kernel) tiles in LDS
+// row-major, with no padding and the 16-byte chunks of each row XOR-swizzled by the
+// row index (conflict-free 16-byte row reads by 32 consecutive rows).  Tiles are
+// copied global -> LDS by the DMA path (global_load_lds, 16 bytes per lane, one
+// contiguous KiB per wave instruction, no registers), double-buffered so the next
+// tile streams in while the current one is computed.  Operands whose k index runs
+// along the rows (P^T dO, dS^T Q, dS K) are read with ds_read_b64_tr_b16, which
+// returns a column of 4 consecutive rows per lane: two such reads give an 8-element
+// MFMA operand in the k order the C-tile trick needs.
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+#define TG_LDS __attribute__((address_space(3)))
+#define TG_GLB __attribute__((address_space(1)))
+
+template <int D> struct SwzTile {
+  static constexpr int CH = D / 8;  // 16-byte chunks per row
+  static constexpr int RB = D * 2;  // bytes per row
+  __device__ static int key(int r) { return CH == 16 ? (r & 15) : ((r >> 1) & 7); }
+  __device__ static int off(int r, int c) { return r * RB + ((c ^ key(r)) << 4); }
+};
+
+// Async copy of rows [row0, row0+R) of a [nrows, D] matrix into a swizzled tile.
+// Rows past nrows copy row nrows-1; the kernels make those rows contribute nothing.
+template <typename T, int D, int R>
+__device__ __forceinline__ void tile_dma(const T* __restrict__ g, int64_t row0, int64_t nrows,
+                                         char* lds) {
+  constexpr int CH = D / 8, NI = R * CH / 64;
+  static_assert(NI % (kThreads / 64) == 0, "tile must split evenly over the waves");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = wave; i < NI; i += kThreads / 64) {
+    const int u = i * 64 + lane;
+    const int r = u / CH, c = (u % CH) ^ SwzTile<D>::key(r);
+    int64_t row = row0 + r;
+    row = row < nrows ? row : nrows - 1;
+    __builtin_amdgcn_global_load_lds((const TG_GLB void*)(g + row * D + c * 8),
+                                     (TG_LDS void*)(lds + i * 1024), 16, 0, 0);
+  }
+}
+
+// Wait for this wave's outstanding DMA and global loads; a barrier then makes every
+// wave's part of the tile visible.
+__device__ __forceinline__ void dma_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+template <typename T>
+__device__ __forceinline__ typename Vec8<T>::type lds_a(const char* p) {
+  return *reinterpret_cast<const typename Vec8<T>::type*>(p);
+}
+template <typename T>
+__device__ __forceinline__ typename Vec8<T>::type lds_tr(const char* p0, const char* p1) {
+  union {
+    v4i16 h[2];
+    typename Vec8<T>::type v;
+  } u;
+  u.h[0] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((TG_LDS v4i16*)p0);
+  u.h[1] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((TG_LDS v4i16*)p1);
+  return u.v;
+}
+
+// Per-lane byte offsets within a 32-row swizzled sub-tile.
+//   a[ks]: 16-byte row read, row l32, chunk 2ks + h (A operand, k = d).
+//   t[j][dt]: transposed read j (rows 4h + s/4 + 8j, s = lane % 16; the caller adds
+//             16 rows per k-step) at column dt*32 + 16*((lane/16) % 2) + 4*(s % 4), so
+//             the lane receives column dt*32 + lane%32 of rows 4h + 8j + 0..3.
+template <int D>
+struct LaneOffs {
+  int a[D / 16];
+  int t[2][D / 32];
+  __device__ void init(int lane) {
+    const int l32 = lane & 31, h = lane >> 5, s = lane & 15, nh = (lane >> 4) & 1;
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) a[ks] = SwzTile<D>::off(l32, 2 * ks + h);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt) {
+        const int row = 4 * h + (s >> 2) + 8 * j;
+        const int col = dt * 32 + 16 * nh + 4 * (s & 3);
+        t[j][dt] = SwzTile<D>::off(row, col >> 3) + (col & 7) * 2;
+      }
+  }
+};
+
+// One 32-query x 32-key sub-tile of the dK/dV kernel for one wave (lane = key).
+//   qs/dos: the sub-tile's first row in the Q / dO tiles; lse/dvs: its 32 log2-scaled
+//   LSE values (+inf past Sq, so P = 0 there) and scale*D values.
 //   DIAG: the sub-tile straddles the causal diagonal; key > query is masked, with
 //   mb = (first key of the wave's 32 + l32) - (first query of the sub-tile) - 4h,
 //   so that the mask for accumulator register r is mb > 8*(r/4) + r%4.
+// Keys past Sk (clamped rows of K/V) only feed dK/dV rows that are never stored.
 template <typename T, int D, bool DIAG>
-__device__ __forceinline__ void dkdv_subtile(const T* qrow, const T* dorow, const T* qil,
-                                             const T* doil, const float* lse,
-                                             const float* dvs, int h,
-                                             const typename Vec8<T>::type (&kf)[D / 16],
-                                             const typename Vec8<T>::type (&vf)[D / 16],
-                                             f32x16 (&dk)[D / 32], f32x16 (&dv)[D / 32],
-                                             float sl2, float scale, int mb) {
-  constexpr int DK = D / 16, DT = D / 32;
+__device__ __forceinline__ void dkdv_sub(const char* qs, const char* dos, const float* lse,
+                                         const float* dvs, int h, const LaneOffs<D>& o,
+                                         const typename Vec8<T>::type (&kf)[D / 16],
+                                         const typename Vec8<T>::type (&vf)[D / 16],
+                                         f32x16 (&dk)[D / 32], f32x16 (&dv)[D / 32], float sl2,
+                                         float scale, int mb) {
+  constexpr int DK = D / 16, DT = D / 32, RB = D * 2;
   f32x16 s, dp;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
@@ -302,12 +405,9 @@ __device__ __forceinline__ void dkdv_subtile(const T* qrow, const T* dorow, cons
     dp[r] = 0.f;
   }
 #pragma unroll
-  for (int ks = 0; ks < DK; ++ks) s = mfma(ld8(qrow + ks * 16), kf[ks], s);
+  for (int ks = 0; ks < DK; ++ks) s = mfma(lds_a<T>(qs + o.a[ks]), kf[ks], s);
 #pragma unroll
-  for (int ks = 0; ks < DK; ++ks) dp = mfma(ld8(dorow + ks * 16), vf[ks], dp);
-  // Padded query rows are zero in the Q/dO tiles with lse = D = 0, so they add
-  // nothing to dV (dO row 0) or dK (dS = P*(0-0) = 0); padded keys only feed dK/dV
-  // rows that are never stored.  Only the causal diagonal needs a mask.
+  for (int ks = 0; ks < DK; ++ks) dp = mfma(lds_a<T>(dos + o.a[ks]), vf[ks], dp);
   float p[16];
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
@@ -315,18 +415,18 @@ __device__ __forceinline__ void dkdv_subtile(const T* qrow, const T* dorow, cons
     const float la[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int r = 4 * g + i;
-      float pv = fexp2(fmaf(s[r], sl2, -la[i]));
+      float pv = fexp2(fmaf(s[4 * g + i], sl2, -la[i]));
       if (DIAG) pv = (mb > 8 * g + i) ? 0.f : pv;
-      p[r] = pv;
+      p[4 * g + i] = pv;
     }
   }
 #pragma unroll
   for (int sg = 0; sg < 2; ++sg) {
     const typename Vec8<T>::type pa = pack8<T>(&p[8 * sg]);
+    const char* b = dos + sg * 16 * RB;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
-      dv[dt] = mfma(pa, ld_il<T, D>(doil, 2 * sg, dt * 32), dv[dt]);
+      dv[dt] = mfma(pa, lds_tr<T>(b + o.t[0][dt], b + o.t[1][dt]), dv[dt]);
   }
   float ds[16];
 #pragma unroll
@@ -334,35 +434,60 @@ __device__ __forceinline__ void dkdv_subtile(const T* qrow, const T* dorow, cons
     const float4 b = *reinterpret_cast<const float4*>(dvs + 8 * g + 4 * h);
     const float db[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = 4 * g + i;
-      ds[r] = p[r] * fmaf(dp[r], scale, -db[i]);
-    }
+    for (int i = 0; i < 4; ++i) ds[4 * g + i] = p[4 * g + i] * fmaf(dp[4 * g + i], scale, -db[i]);
   }
 #pragma unroll
   for (int sg = 0; sg < 2; ++sg) {
     const typename Vec8<T>::type da = pack8<T>(&ds[8 * sg]);
+    const char* b = qs + sg * 16 * RB;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
-      dk[dt] = mfma(da, ld_il<T, D>(qil, 2 * sg, dt * 32), dk[dt]);
+      dk[dt] = mfma(da, lds_tr<T>(b + o.t[0][dt], b + o.t[1][dt]), dk[dt]);
   }
 }
 
-// dK, dV.  grid = (ceil(Sk/128), B*H).  Query tiles of 128 staged per step; the four
-// 32-query sub-tiles are processed one after another to keep P/dS in 32 registers.
+// The BM/32 sub-tiles of one staged query tile; kq = first key of this wave minus the
+// tile's first query.
+template <typename T, int D, int BM>
+__device__ __forceinline__ void dkdv_tile(const char* qs, const char* dos, const float* lse,
+                                          const float* dvs, int kq, int causal, int h, int l32,
+                                          const LaneOffs<D>& o,
+                                          const typename Vec8<T>::type (&kf)[D / 16],
+                                          const typename Vec8<T>::type (&vf)[D / 16],
+                                          f32x16 (&dk)[D / 32], f32x16 (&dv)[D / 32], float sl2,
+                                          float scale) {
+  constexpr int RB = D * 2;
+#pragma unroll 1
+  for (int t = 0; t < BM / 32; ++t) {
+    // causal: a 32-query sub-tile wholly before this wave's keys contributes nothing
+    if (causal && t * 32 + 31 < kq) continue;
+    const char* q = qs + t * 32 * RB;
+    const char* d = dos + t * 32 * RB;
+    if (causal && kq + 31 > t * 32)
+      dkdv_sub<T, D, true>(q, d, lse + t * 32, dvs + t * 32, h, o, kf, vf, dk, dv, sl2, scale,
+                           kq + l32 - t * 32 - 4 * h);
+    else
+      dkdv_sub<T, D, false>(q, d, lse + t * 32, dvs + t * 32, h, o, kf, vf, dk, dv, sl2, scale,
+                            0);
+  }
+}
+
+// dK, dV.  grid = (ceil(Sk/128), B*H); one workgroup = 128 keys (4 waves x 32 keys,
+// K/V fragments in registers), looping over query tiles of BM rows double-buffered
+// in LDS (stage buffers are separate arrays so the compiler can tell the tile being
+// read from the one being written by the DMA).
 template <typename T, int D, int BM, int OCC>
 __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dkdv(
     const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
     const T* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Dv,
     T* __restrict__ dK, T* __restrict__ dV, int64_t Sq, int64_t Sk, float scale, int causal,
     int accumulate) {
-  constexpr int DK = D / 16, DT = D / 32;
-  __shared__ __attribute__((aligned(16))) T Qs[BM * (D + 8)];
-  __shared__ __attribute__((aligned(16))) T Qi[BM * D];
-  __shared__ __attribute__((aligned(16))) T dOs[BM * (D + 8)];
-  __shared__ __attribute__((aligned(16))) T dOi[BM * D];
-  __shared__ __attribute__((aligned(16))) float lse2[BM];
-  __shared__ __attribute__((aligned(16))) float dvec[BM];
+  constexpr int DK = D / 16, DT = D / 32, TB = BM * D * 2;
+  __shared__ __attribute__((aligned(1024))) char q0s[TB];
+  __shared__ __attribute__((aligned(1024))) char do0s[TB];
+  __shared__ __attribute__((aligned(1024))) char q1s[TB];
+  __shared__ __attribute__((aligned(1024))) char do1s[TB];
+  __shared__ __attribute__((aligned(16))) float lse0[BM], dvs0[BM], lse1[BM], dvs1[BM];
   int64_t tile, bh;
   fa_block(tile, bh);
   Q += bh * Sq * D;
@@ -378,20 +503,14 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dkdv(
   const int64_t kblk = tile * 128;
   const int64_t key = kblk + wave * 32 + l32;  // this lane's key (C-tile column)
   const float sl2 = scale * kLog2e;
-
+  // A key lane past Sk reads a clamped row: it only feeds dK/dV rows of that key,
+  // which are never stored.
+  const int64_t kc = key < Sk ? key : Sk - 1;
   typename Vec8<T>::type kf[DK], vf[DK];
 #pragma unroll
   for (int ks = 0; ks < DK; ++ks) {
-    if (key < Sk) {
-      kf[ks] = ld8(K + key * D + ks * 16 + h * 8);
-      vf[ks] = ld8(V + key * D + ks * 16 + h * 8);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        kf[ks][e] = (T)0.f;
-        vf[ks][e] = (T)0.f;
-      }
-    }
+    kf[ks] = ld8(K + kc * D + ks * 16 + h * 8);
+    vf[ks] = ld8(V + kc * D + ks * 16 + h * 8);
   }
   f32x16 dk[DT], dv[DT];
 #pragma unroll
@@ -401,40 +520,60 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dkdv(
       dk[dt][r] = 0.f;
       dv[dt][r] = 0.f;
     }
-  // per-lane bases: row-major tiles at (row l32, d h*8); interleaved at (group h, col l32)
-  const T* qrow0 = Qs + l32 * (D + 8) + h * 8;
-  const T* dorow0 = dOs + l32 * (D + 8) + h * 8;
-  const T* qil0 = Qi + (h * D + l32) * 8;
-  const T* doil0 = dOi + (h * D + l32) * 8;
+  LaneOffs<D> o;
+  o.init(lane);
   // causal: queries below the first key of this block contribute nothing
-  int64_t qstart = 0;
-  if (causal) qstart = (kblk / BM) * BM;
-  for (int64_t q0 = qstart; q0 < Sq; q0 += BM) {
-    __syncthreads();
-    stage<T, BM, D, true, true>(Q, q0, Sq, Qs, Qi);
-    stage<T, BM, D, true, true>(dO, q0, Sq, dOs, dOi);
+  const int64_t qstart = causal ? (kblk / BM) * BM : 0;
+  // log2-scaled LSE (+inf past Sq: P = 0 for padded rows) and scale*D of one tile
+  float pl = 0.f, pd = 0.f;
+  auto lsed = [&](int64_t q0) {
+    const int64_t qq = q0 + (threadIdx.x % BM);
+    const int64_t qqc = qq < Sq ? qq : Sq - 1;  // load unconditionally, select after
+    const float lv = LSE[qqc], dd = Dv[qqc];
+    pl = qq < Sq ? lv * kLog2e : INFINITY;
+    pd = qq < Sq ? dd * scale : 0.f;
+  };
+  if (qstart < Sq) {
+    tile_dma<T, D, BM>(Q, qstart, Sq, q0s);
+    tile_dma<T, D, BM>(dO, qstart, Sq, do0s);
+    lsed(qstart);
     if (threadIdx.x < BM) {
-      const int64_t qq = q0 + threadIdx.x;
-      lse2[threadIdx.x] = qq < Sq ? LSE[qq] * kLog2e : 0.f;
-      dvec[threadIdx.x] = qq < Sq ? Dv[qq] * scale : 0.f;
+      lse0[threadIdx.x] = pl;
+      dvs0[threadIdx.x] = pd;
     }
+  }
+  for (int64_t q0 = qstart; q0 < Sq; q0 += 2 * BM) {
+    // stage 0 holds tile q0; stage 1 is free (its last readers passed the barrier)
+    dma_wait();
     __syncthreads();
-    // key offset of this wave relative to the staged query tile
-    const int kq = (int)(kblk - q0) + wave * 32;
-#pragma unroll 1
-    for (int t = 0; t < BM / 32; ++t) {
-      // causal: a 32-query sub-tile wholly before this wave's keys contributes nothing
-      if (causal && t * 32 + 31 < kq) continue;
-      const T* qrow = qrow0 + t * 32 * (D + 8);
-      const T* dorow = dorow0 + t * 32 * (D + 8);
-      const T* qil = qil0 + t * 4 * D * 8;
-      const T* doil = doil0 + t * 4 * D * 8;
-      if (causal && kq + 31 > t * 32)
-        dkdv_subtile<T, D, true>(qrow, dorow, qil, doil, lse2 + t * 32, dvec + t * 32, h, kf,
-                                 vf, dk, dv, sl2, scale, kq + l32 - t * 32 - 4 * h);
-      else
-        dkdv_subtile<T, D, false>(qrow, dorow, qil, doil, lse2 + t * 32, dvec + t * 32, h, kf,
-                                  vf, dk, dv, sl2, scale, 0);
+    const bool more1 = q0 + BM < Sq;
+    if (more1) {
+      tile_dma<T, D, BM>(Q, q0 + BM, Sq, q1s);
+      tile_dma<T, D, BM>(dO, q0 + BM, Sq, do1s);
+      lsed(q0 + BM);
+    }
+    dkdv_tile<T, D, BM>(q0s, do0s, lse0, dvs0, (int)(kblk - q0) + wave * 32, causal, h, l32, o,
+                        kf, vf, dk, dv, sl2, scale);
+    if (!more1) break;
+    if (threadIdx.x < BM) {
+      lse1[threadIdx.x] = pl;
+      dvs1[threadIdx.x] = pd;
+    }
+    // stage 1 holds tile q0 + BM
+    dma_wait();
+    __syncthreads();
+    const bool more2 = q0 + 2 * BM < Sq;
+    if (more2) {
+      tile_dma<T, D, BM>(Q, q0 + 2 * BM, Sq, q0s);
+      tile_dma<T, D, BM>(dO, q0 + 2 * BM, Sq, do0s);
+      lsed(q0 + 2 * BM);
+    }
+    dkdv_tile<T, D, BM>(q1s, do1s, lse1, dvs1, (int)(kblk - q0 - BM) + wave * 32, causal, h, l32,
+                        o, kf, vf, dk, dv, sl2, scale);
+    if (!more2) break;
+    if (threadIdx.x < BM) {
+      lse0[threadIdx.x] = pl;
+      dvs0[threadIdx.x] = pd;
     }
   }
   // C tiles: rows = keys of this wave, cols = d
@@ -446,17 +585,17 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dkdv(
 }
 
 // One 32-key x 32-query sub-tile of the dQ kernel for one wave (lane = query).
-//   krow/vrow: this lane's row of the row-major K / V tile (key kt*32 + l32, d h*8);
-//   kil: interleaved K at block (kt*4 + h), column l32.
-//   DIAG: masks key > query, with mq = (query of this lane) - (first key of the
-//   sub-tile) - 4h, so that register r is masked when 8*(r/4) + r%4 > mq.
-template <typename T, int D, bool DIAG>
-__device__ __forceinline__ void dq_subtile(const T* krow, const T* vrow, const T* kil,
-                                           const typename Vec8<T>::type (&qf)[D / 16],
-                                           const typename Vec8<T>::type (&of)[D / 16],
-                                           f32x16 (&acc)[D / 32], float sl2, float scale,
-                                           float lq, float dqs, int mq) {
-  constexpr int DK = D / 16, DT = D / 32;
+//   ks/vs: the sub-tile's first row in the K / V tiles.
+//   MASK: keys are masked when 8*(r/4) + r%4 > thr for accumulator register r, where
+//   thr folds the causal limit (query of this lane - first key of the sub-tile - 4h)
+//   and the end of the keys (keys - first key of the sub-tile - 4h - 1).
+template <typename T, int D, bool MASK>
+__device__ __forceinline__ void dq_sub(const char* ks, const char* vs, const LaneOffs<D>& o,
+                                       const typename Vec8<T>::type (&qf)[D / 16],
+                                       const typename Vec8<T>::type (&of)[D / 16],
+                                       f32x16 (&acc)[D / 32], float sl2, float scale, float lq,
+                                       float dqs, int thr) {
+  constexpr int DK = D / 16, DT = D / 32, RB = D * 2;
   f32x16 s, dp;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
@@ -464,37 +603,71 @@ __device__ __forceinline__ void dq_subtile(const T* krow, const T* vrow, const T
     dp[r] = 0.f;
   }
 #pragma unroll
-  for (int ks = 0; ks < DK; ++ks) s = mfma(ld8(krow + ks * 16), qf[ks], s);
+  for (int k = 0; k < DK; ++k) s = mfma(lds_a<T>(ks + o.a[k]), qf[k], s);
 #pragma unroll
-  for (int ks = 0; ks < DK; ++ks) dp = mfma(ld8(vrow + ks * 16), of[ks], dp);
-  // Padded keys are zero rows of K/V, so they add nothing to dQ (dS * 0); only the
-  // causal diagonal needs a mask.
+  for (int k = 0; k < DK; ++k) dp = mfma(lds_a<T>(vs + o.a[k]), of[k], dp);
   float ds[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     float pv = fexp2(fmaf(s[r], sl2, -lq));
-    if (DIAG) pv = (8 * (r >> 2) + (r & 3) > mq) ? 0.f : pv;
+    if (MASK) pv = (8 * (r >> 2) + (r & 3) > thr) ? 0.f : pv;
     ds[r] = pv * fmaf(dp[r], scale, -dqs);
   }
 #pragma unroll
   for (int sg = 0; sg < 2; ++sg) {
     const typename Vec8<T>::type da = pack8<T>(&ds[8 * sg]);
+    const char* b = ks + sg * 16 * RB;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
-      acc[dt] = mfma(da, ld_il<T, D>(kil, 2 * sg, dt * 32), acc[dt]);
+      acc[dt] = mfma(da, lds_tr<T>(b + o.t[0][dt], b + o.t[1][dt]), acc[dt]);
   }
 }
 
-// dQ.  grid = (ceil(Sq/128), B*H).
+// The BN/32 sub-tiles of one staged key tile starting at key k0.
+template <typename T, int D, int BN>
+__device__ __forceinline__ void dq_tile(const char* ks, const char* vs, int64_t k0, int64_t Sk,
+                                        int qk, int causal, int h, int l32, const LaneOffs<D>& o,
+                                        const typename Vec8<T>::type (&qf)[D / 16],
+                                        const typename Vec8<T>::type (&of)[D / 16],
+                                        f32x16 (&acc)[D / 32], float sl2, float scale, float lq,
+                                        float dqs) {
+  constexpr int RB = D * 2;
+#pragma unroll 1
+  for (int kt = 0; kt < BN / 32; ++kt) {
+    const int64_t kb0 = k0 + kt * 32;
+    if (kb0 >= Sk) break;
+    // causal: a 32-key sub-tile wholly after this wave's queries contributes nothing
+    if (causal && kt * 32 > qk + 31) continue;
+    const bool diag = causal && kt * 32 + 31 > qk;
+    const bool edge = kb0 + 32 > Sk;
+    const char* k = ks + kt * 32 * RB;
+    const char* v = vs + kt * 32 * RB;
+    if (diag || edge) {
+      int thr = 1 << 30;
+      if (diag) thr = qk + l32 - kt * 32 - 4 * h;
+      if (edge) {
+        const int kb = (int)(Sk - kb0) - 4 * h - 1;
+        thr = kb < thr ? kb : thr;
+      }
+      dq_sub<T, D, true>(k, v, o, qf, of, acc, sl2, scale, lq, dqs, thr);
+    } else {
+      dq_sub<T, D, false>(k, v, o, qf, of, acc, sl2, scale, lq, dqs, 0);
+    }
+  }
+}
+
+// dQ.  grid = (ceil(Sq/128), B*H); one workgroup = 128 queries (4 waves x 32, Q/dO
+// fragments in registers), looping over key tiles of BN rows double-buffered in LDS.
 template <typename T, int D, int BN, int OCC>
 __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dq(
     const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
     const T* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Dv,
     T* __restrict__ dQ, int64_t Sq, int64_t Sk, float scale, int causal, int accumulate) {
-  constexpr int DK = D / 16, DT = D / 32;
-  __shared__ __attribute__((aligned(16))) T Ks[BN * (D + 8)];
-  __shared__ __attribute__((aligned(16))) T Ki[BN * D];
-  __shared__ __attribute__((aligned(16))) T Vs[BN * (D + 8)];
+  constexpr int DK = D / 16, DT = D / 32, TB = BN * D * 2;
+  __shared__ __attribute__((aligned(1024))) char k0s[TB];
+  __shared__ __attribute__((aligned(1024))) char v0s[TB];
+  __shared__ __attribute__((aligned(1024))) char k1s[TB];
+  __shared__ __attribute__((aligned(1024))) char v1s[TB];
   int64_t tile, bh;
   fa_block(tile, bh);
   Q += bh * Sq * D;
@@ -511,52 +684,50 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dq(
   const int64_t qblk = qb * 128;
   const int64_t q = qblk + wave * 32 + l32;
   const float sl2 = scale * kLog2e;
+  // A query lane past Sq reads a clamped row; its dQ row is never stored.
+  const int64_t qc = q < Sq ? q : Sq - 1;
   typename Vec8<T>::type qf[DK], of[DK];
 #pragma unroll
   for (int ks = 0; ks < DK; ++ks) {
-    if (q < Sq) {
-      qf[ks] = ld8(Q + q * D + ks * 16 + h * 8);
-      of[ks] = ld8(dO + q * D + ks * 16 + h * 8);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        qf[ks][e] = (T)0.f;
-        of[ks][e] = (T)0.f;
-      }
-    }
+    qf[ks] = ld8(Q + qc * D + ks * 16 + h * 8);
+    of[ks] = ld8(dO + qc * D + ks * 16 + h * 8);
   }
-  const float lq = q < Sq ? LSE[q] * kLog2e : 0.f;
-  const float dqs = q < Sq ? Dv[q] * scale : 0.f;
+  const float lq = LSE[qc] * kLog2e;
+  const float dqs = Dv[qc] * scale;
   f32x16 acc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
-  const T* krow0 = Ks + l32 * (D + 8) + h * 8;
-  const T* vrow0 = Vs + l32 * (D + 8) + h * 8;
-  const T* kil0 = Ki + (h * D + l32) * 8;
+  LaneOffs<D> o;
+  o.init(lane);
   int64_t kend = Sk;
   if (causal) kend = (qblk + 128 < Sk) ? qblk + 128 : Sk;
-  for (int64_t k0 = 0; k0 < kend; k0 += BN) {
+  if (kend > 0) {
+    tile_dma<T, D, BN>(K, 0, Sk, k0s);
+    tile_dma<T, D, BN>(V, 0, Sk, v0s);
+  }
+  for (int64_t k0 = 0; k0 < kend; k0 += 2 * BN) {
+    dma_wait();
     __syncthreads();
-    stage<T, BN, D, true, true>(K, k0, Sk, Ks, Ki);
-    stage<T, BN, D, true, false>(V, k0, Sk, Vs, nullptr);
-    __syncthreads();
-    // query of this wave's first lane relative to the staged key tile
-    const int qk = (int)(qblk - k0) + wave * 32;
-#pragma unroll 1
-    for (int kt = 0; kt < BN / 32; ++kt) {
-      // causal: a 32-key sub-tile wholly after this wave's queries contributes nothing
-      if (causal && kt * 32 > qk + 31) continue;
-      const T* krow = krow0 + kt * 32 * (D + 8);
-      const T* vrow = vrow0 + kt * 32 * (D + 8);
-      const T* kil = kil0 + kt * 4 * D * 8;
-      if (causal && kt * 32 + 31 > qk)
-        dq_subtile<T, D, true>(krow, vrow, kil, qf, of, acc, sl2, scale, lq, dqs,
-                               qk + l32 - kt * 32 - 4 * h);
-      else
-        dq_subtile<T, D, false>(krow, vrow, kil, qf, of, acc, sl2, scale, lq, dqs, 0);
+    const bool more1 = k0 + BN < kend;
+    if (more1) {
+      tile_dma<T, D, BN>(K, k0 + BN, Sk, k1s);
+      tile_dma<T, D, BN>(V, k0 + BN, Sk, v1s);
     }
+    dq_tile<T, D, BN>(k0s, v0s, k0, Sk, (int)(qblk - k0) + wave * 32, causal, h, l32, o, qf, of,
+                      acc, sl2, scale, lq, dqs);
+    if (!more1) break;
+    dma_wait();
+    __syncthreads();
+    const bool more2 = k0 + 2 * BN < kend;
+    if (more2) {
+      tile_dma<T, D, BN>(K, k0 + 2 * BN, Sk, k0s);
+      tile_dma<T, D, BN>(V, k0 + 2 * BN, Sk, v0s);
+    }
+    dq_tile<T, D, BN>(k1s, v1s, k0 + BN, Sk, (int)(qblk - k0 - BN) + wave * 32, causal, h, l32,
+                      o, qf, of, acc, sl2, scale, lq, dqs);
+    if (!more2) break;
   }
   // C tiles: rows = queries of this wave, cols = d
 #pragma unroll
@@ -577,7 +748,7 @@ int fwd_t(const void* q, const void* k, const void* v, void* o, float* lse, int6
 // key rows of the dQ kernel, and the workgroups per CU each is compiled for.
 template <int D> struct BwdCfg;
 template <> struct BwdCfg<64> {
-  static constexpr int BM = 64, OCC_KV = 2, BN = 64, OCC_Q = 3;
+  static constexpr int BM = 128, OCC_KV = 2, BN = 64, OCC_Q = 3;
 };
 template <> struct BwdCfg<128> {
   static constexpr int BM = 128, OCC_KV = 1, BN = 64, OCC_Q = 2;

@@ -185,6 +185,11 @@ def test_flash_attention_vs_naive_torch(causal, shape):
     close(dq, qt.grad.numpy(), 1e-9)
     close(dk, kt.grad.numpy(), 1e-9)
     close(dv, vt.grad.numpy(), 1e-9)
+    # the rowsum(dO*O) form with the exact O gives the same gradients
+    dq2, dk2, dv2 = O.flash_attention_bwd(q, k, v, do, causal, scale, block_size=32, o=oo)
+    close(dq2, qt.grad.numpy(), 1e-9)
+    close(dk2, kt.grad.numpy(), 1e-9)
+    close(dv2, vt.grad.numpy(), 1e-9)
 
 
 # ------------------------------------------------------------------ Adam
