@@ -428,6 +428,195 @@ __global__ __launch_bounds__(kThreads) void k_gemm_v2(int64_t M, int64_t N, int6
     }
 }
 
+
+// ---------------------------------------------------------------------------- v3
+// fp16/bf16 GEMM with DMA-staged operands: 128x128 block tile, k-tiles of 64, four
+// waves in a 2x2 grid each owning 64x64 of C (2x2 MFMA 32x32x16 tiles).  Both
+// operand tiles are copied global -> LDS with global_load_lds (16 bytes per lane,
+// one contiguous KiB per wave instruction), double-buffered so the next k-tile
+// streams in while the current one is multiplied; no VGPRs and no LDS store
+// instructions are spent on staging.  Tiles keep the operand's global orientation:
+//   k-contiguous operand (A, or B^T): [128 rows][64 k], fragments are 16-byte row
+//     reads (lane = row, 8 consecutive k);
+//   m/n-contiguous operand (A^T, or B): [64 k][128 cols], fragments are two
+//     ds_read_b64_tr_b16 reads (lane = column, 4 consecutive k each).
+// Rows are unpadded with the 16-byte chunks XOR-swizzled by the row index, so both
+// read kinds are free of LDS bank conflicts.  Requires K % 64 == 0 and 16-byte
+// aligned operands; rows/columns past M or N read clamped addresses and only feed
+// C entries that are never stored.
+typedef short v4i16_g __attribute__((ext_vector_type(4)));
+#define TG_LDS_G __attribute__((address_space(3)))
+#define TG_GLB_G __attribute__((address_space(1)))
+
+constexpr int V3_BK = 64;
+
+template <int CH> __device__ __forceinline__ int v3_key(int r) {
+  return CH == 16 ? (r & 15) : ((r >> 1) & 7);
+}
+template <int CH> __device__ __forceinline__ int v3_off(int r, int c) {
+  return r * CH * 16 + ((c ^ v3_key<CH>(r)) << 4);
+}
+
+// DMA of an R x CW tile (CW elements per row) at (row0, col0) of a matrix with
+// leading dimension ld, by NW waves; rows >= nrows and columns >= ncols are clamped.
+template <typename T, int R, int CW, int NW>
+__device__ __forceinline__ void v3_dma(const T* __restrict__ g, int64_t ld, int64_t row0,
+                                       int64_t nrows, int64_t col0, int64_t ncols, char* lds) {
+  constexpr int CH = CW / 8, NI = R * CH / 64;
+  static_assert(NI % NW == 0, "tile must split evenly over the waves");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = wave; i < NI; i += NW) {
+    const int u = i * 64 + lane;
+    const int r = u / CH, c = (u % CH) ^ v3_key<CH>(r);
+    int64_t row = row0 + r;
+    row = row < nrows ? row : nrows - 1;
+    int64_t col = col0 + c * 8;
+    col = col + 8 <= ncols ? col : ncols - 8;
+    __builtin_amdgcn_global_load_lds((const TG_GLB_G void*)(g + row * ld + col),
+                                     (TG_LDS_G void*)(lds + i * 1024), 16, 0, 0);
+  }
+}
+
+// Fragment reader for one operand tile of EXT rows (m or n) and 64 k.
+//   KC: [EXT rows][64 k], 128-byte rows; else [64 k][EXT], EXT*2-byte rows.
+// S slabs of 32 rows/columns per wave, starting at the wave's offset wbase.
+template <typename T, bool KC, int EXT, int S>
+struct V3Frag {
+  static constexpr int CHM = EXT / 8;  // chunks per row of the m/n-contiguous layout
+  int off[KC ? 4 : 2 * S];
+  __device__ void init(int lane, int wbase) {
+    const int l32 = lane & 31, h = lane >> 5;
+    if (KC) {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) off[ks] = v3_off<8>(l32, 2 * ks + h) - l32 * 128;
+    } else {
+      const int s = lane & 15, nh = (lane >> 4) & 1;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < S; ++i) {
+          const int row = 8 * h + 4 * j + (s >> 2);
+          const int col = wbase + 32 * i + 16 * nh + 4 * (s & 3);
+          off[j * S + i] = v3_off<CHM>(row, col >> 3) + (col & 7) * 2;
+        }
+    }
+  }
+  // 8 k-elements k = ks*16 + 8h + e of row/column wbase + 32 i + l32.
+  __device__ __forceinline__ typename Vec8<T>::type get(const char* tile, int wbase, int i,
+                                                        int ks, int l32) const {
+    if (KC) {
+      const int row = wbase + 32 * i + l32;  // swizzle key = row bits 1-3 = l32's
+      return *reinterpret_cast<const typename Vec8<T>::type*>(tile + row * 128 + off[ks]);
+    } else {
+      union {
+        v4i16_g h[2];
+        typename Vec8<T>::type v;
+      } u;
+      const char* b = tile + ks * 16 * EXT * 2;
+      u.h[0] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((TG_LDS_G v4i16_g*)(b + off[i]));
+      u.h[1] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((TG_LDS_G v4i16_g*)(b + off[S + i]));
+      return u.v;
+    }
+  }
+};
+
+// Block = WGM x WGN waves, each owning (SM*32) x (SN*32) of C.
+template <typename T, typename TC, bool TA, bool TB, int WGM, int WGN, int SM, int SN, int OCC>
+__global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_v3(
+    int64_t M, int64_t N, int64_t K, float alpha, const T* __restrict__ A, int64_t lda,
+    int64_t sa, const T* __restrict__ B, int64_t ldb, int64_t sb, float beta,
+    TC* __restrict__ C, int64_t ldc, int64_t sc) {
+  constexpr int NW = WGM * WGN, TBM = WGM * SM * 32, TBN = WGN * SN * 32;
+  constexpr int ATILE = TBM * V3_BK * 2, BTILE = TBN * V3_BK * 2;
+  __shared__ __attribute__((aligned(1024))) char a0[ATILE];
+  __shared__ __attribute__((aligned(1024))) char b0[BTILE];
+  __shared__ __attribute__((aligned(1024))) char a1[ATILE];
+  __shared__ __attribute__((aligned(1024))) char b1[BTILE];
+  constexpr bool AKC = !TA, BKC = TB;
+  const int64_t gx = gridDim.x, gy = gridDim.y;
+  const int64_t T_ = gx * gy;
+  int64_t lin = (int64_t)blockIdx.y * gx + blockIdx.x;
+  if (T_ % 8 == 0) lin = (lin % 8) * (T_ / 8) + lin / 8;  // XCD-contiguous bands
+  const int64_t tm = lin / gx, tn = lin % gx;
+  const int64_t bz = blockIdx.z;
+  A += bz * sa;
+  B += bz * sb;
+  C += bz * sc;
+  const int64_t m0 = tm * TBM, n0 = tn * TBN;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = (wave / WGN) * SM * 32, wn = (wave % WGN) * SN * 32;
+  const int l32 = lane & 31, lh = lane >> 5;
+  V3Frag<T, AKC, TBM, SM> fa;
+  V3Frag<T, BKC, TBN, SN> fb;
+  fa.init(lane, wm);
+  fb.init(lane, wn);
+  f32x16 acc[SM][SN];
+#pragma unroll
+  for (int i = 0; i < SM; ++i)
+#pragma unroll
+    for (int j = 0; j < SN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  // A is [M][K] (lda) or, transposed, [K][M]; B is [K][N] or, transposed, [N][K].
+  auto dma = [&](int64_t k0, char* as, char* bs) {
+    if (AKC) v3_dma<T, TBM, 64, NW>(A, lda, m0, M, k0, K, as);
+    else v3_dma<T, 64, TBM, NW>(A, lda, k0, K, m0, M, as);
+    if (BKC) v3_dma<T, TBN, 64, NW>(B, ldb, n0, N, k0, K, bs);
+    else v3_dma<T, 64, TBN, NW>(B, ldb, k0, K, n0, N, bs);
+  };
+  auto mul = [&](const char* as, const char* bs) {
+#pragma unroll
+    for (int ks = 0; ks < V3_BK / 16; ++ks) {
+      typename Vec8<T>::type af[SM], bf[SN];
+#pragma unroll
+      for (int i = 0; i < SM; ++i) af[i] = fa.get(as, wm, i, ks, l32);
+#pragma unroll
+      for (int j = 0; j < SN; ++j) bf[j] = fb.get(bs, wn, j, ks, l32);
+#pragma unroll
+      for (int i = 0; i < SM; ++i)
+#pragma unroll
+        for (int j = 0; j < SN; ++j) mfma_v(af[i], bf[j], acc[i][j]);
+    }
+  };
+  if (K > 0) dma(0, a0, b0);
+  for (int64_t k0 = 0; k0 < K; k0 += 2 * V3_BK) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    const bool more1 = k0 + V3_BK < K;
+    if (more1) dma(k0 + V3_BK, a1, b1);
+    mul(a0, b0);
+    if (!more1) break;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    const bool more2 = k0 + 2 * V3_BK < K;
+    if (more2) dma(k0 + 2 * V3_BK, a0, b0);
+    mul(a1, b1);
+    if (!more2) break;
+  }
+#pragma unroll
+  for (int i = 0; i < SM; ++i)
+#pragma unroll
+    for (int j = 0; j < SN; ++j) {
+      const int64_t col = n0 + wn + j * 32 + l32;
+      if (col >= N) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + wm + i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
+        if (row < M) {
+          float v = alpha * acc[i][j][r];
+          TC* pc = C + row * ldc + col;
+          if (beta != 0.f) v += beta * tg_to_float(*pc);
+          *pc = tg_from_float<TC>(v);
+        }
+      }
+    }
+}
+
+// Block shapes of the DMA-staged kernel (waves of 64 x 64 of C): 4 x 2 waves
+// (256 x 128, one block per CU, two waves per SIMD) when the problem has at least
+// one such tile per CU, else 2 x 2 waves (128 x 128, two blocks per CU).
+
 template <typename T, typename TC>
 int launch(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const void* A,
            int64_t lda, int64_t sa, const void* B, int64_t ldb, int64_t sb, float beta, void* C,
@@ -442,6 +631,29 @@ int launch(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const v
   // v2 stages whole 16-byte vectors along every contiguous dimension: extents must be
   // multiples of 8 so no vector straddles a row end.
   if constexpr (sizeof(T) == 2) {
+  if (vec && M >= 64 && N >= 64 && K >= 64 && M % 8 == 0 && N % 8 == 0 && K % V3_BK == 0) {
+    const int64_t big_tiles = ((M + 255) / 256) * ((N + 127) / 128) * batch;
+    const bool big = big_tiles >= (int64_t)tg_num_cus();
+#define TG_G3_SHAPE(TA_, TB_, WGM, OCC)                                                    \
+  do {                                                                                     \
+    constexpr int TBM = WGM * 64;                                                          \
+    dim3 g3((unsigned)((N + 127) / 128), (unsigned)((M + TBM - 1) / TBM), (unsigned)batch); \
+    k_gemm_v3<T, TC, TA_, TB_, WGM, 2, 2, 2, OCC><<<g3, 64 * WGM * 2, 0, s>>>(               \
+        M, N, K, alpha, a, lda, sa, b, ldb, sb, beta, c, ldc, sc);                          \
+  } while (0)
+#define TG_G3(TA_, TB_)                          \
+  do {                                           \
+    if (big) TG_G3_SHAPE(TA_, TB_, 4, 1);        \
+    else TG_G3_SHAPE(TA_, TB_, 2, 2);            \
+  } while (0)
+    if (!ta && !tb) TG_G3(false, false);
+    else if (!ta && tb) TG_G3(false, true);
+    else if (ta && !tb) TG_G3(true, false);
+    else TG_G3(true, true);
+#undef TG_G3_SHAPE
+#undef TG_G3
+    return tg_check_launch("tg_gemm");
+  }
   if (vec && M >= 128 && N >= 64 && K >= 64 && M % 8 == 0 && N % 8 == 0 && K % 8 == 0) {
     // BN = 128 unless that leaves fewer than two blocks per CU.
     const int64_t tiles128 = ((M + 127) / 128) * ((N + 127) / 128) * batch;

@@ -266,7 +266,9 @@ def test_reduce_rows(cuda, rows, cols, dt):
 
 # ------------------------------------------------------------------ GEMM
 GEMM_SHAPES = [(256, 256, 256), (100, 70, 50), (32, 256, 784), (130, 10, 256), (1, 1, 1),
-               (257, 129, 33), (64, 64, 0), (384, 640, 96), (1000, 136, 48), (512, 128, 1024)]
+               (257, 129, 33), (64, 64, 0), (384, 640, 96), (1000, 136, 48), (512, 128, 1024),
+               # DMA-staged path (K % 64 == 0) with partial 128-row/column tiles
+               (200, 136, 128), (72, 520, 192), (1000, 1000, 64), (136, 64, 256)]
 
 
 @pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
@@ -284,6 +286,21 @@ def test_gemm(cuda, M, N, K, ta, tb, dt):
     ref = 0.5 * (A @ B) + 2.0 * f64(c0)
     # products of dt-rounded inputs are exact in fp32 accumulation up to the sum order
     assert_close(c, ref, RTOL_F32_MM, f"gemm {dt} {M}x{N}x{K} ta={ta} tb={tb}")
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+def test_gemm_large_tiles(cuda, ta, tb):
+    """Shape with >= one 256x128 tile per CU (the 8-wave block) and partial edge tiles;
+    reference: torch float64 matmul of the same fp16 inputs."""
+    M, N, K = 4104, 2056, 128
+    g = torch.Generator(device="cuda").manual_seed(7)
+    a = torch.randn((K, M) if ta else (M, K), device="cuda", generator=g).half()
+    b = torch.randn((N, K) if tb else (K, N), device="cuda", generator=g).half()
+    c = torch.empty(M, N, device="cuda")
+    L().gemm(a, b, c, ta, tb, 1.0, 0.0, M, N, K, a.shape[1], b.shape[1], N)
+    ref = (a.double().T if ta else a.double()) @ (b.double().T if tb else b.double())
+    err = float((c.double() - ref).abs().max())
+    assert err <= RTOL_F32_MM * float(ref.abs().max()), f"max error {err}"
 
 
 def test_gemm_batched_broadcast_and_half_out(cuda):
