@@ -268,6 +268,22 @@ def _op_gpt(torch, L, g):
     return Timed("gpt_step", run, flops, "TFLOP/s", FP16_PEAK_TFLOPS)
 
 
+def _op_ce(torch, L, g):
+    """C5 cross-entropy over fp16 logits [8192, 32000]: forward (row statistics and
+    losses) then backward (gradient written in fp16).  Algorithmic bytes: the logits
+    read twice and the gradient written once, 3 x 524 MB."""
+    N, C = 8192, 32000
+    x = (torch.randn(N, C, device="cuda", generator=g) * 2).half()
+    y = torch.randint(0, C, (N,), device="cuda", generator=g)
+    grad = torch.empty_like(x)
+    _need(grad, N * C, "ce")
+
+    def run():
+        lse, loss = L.cross_entropy_fwd(x, y)
+        L.cross_entropy_bwd(x, y, lse, grad, 1.0 / N, False)
+    return Timed("cross_entropy_fwd_bwd", run, 3 * 2 * N * C, "GB/s", HBM_PEAK_GBS)
+
+
 def component_ops(torch, L, only):
     """Other configurations, each built in its own scope on HBM-resident inputs."""
     g = torch.Generator(device="cuda").manual_seed(1)
@@ -275,6 +291,7 @@ def component_ops(torch, L, only):
                 ("adamw_step", lambda: _op_adam(torch, L, g)),
                 ("unscale_check", lambda: _op_unscale(torch, L, g)),
                 ("gemm_fc1_bwd", lambda: _op_gemm(torch, L, g)),
+                ("cross_entropy_fwd_bwd", lambda: _op_ce(torch, L, g)),
                 ("gpt_step", lambda: _op_gpt(torch, L, g))]
     for d in (64, 128):
         for causal in (False, True):

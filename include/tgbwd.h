@@ -160,6 +160,20 @@ int tg_flash_attn_bwd(int dtype, const void* q, const void* k, const void* v, co
                       int64_t H, int64_t Sq, int64_t Sk, int64_t D, float scale, int causal,
                       int accumulate, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Cross-entropy over logits [N, C] with int64 targets (CrossEntropyLoss,
+ * _nn.py:1128-1185).  Forward: per-row log-sum-exp lse[N] and per-row loss
+ * -log(p[t] + 1e-10) (label smoothing s: -sum_c w_c log(p_c + 1e-10), w = s/C +
+ * (1-s) onehot); the caller reduces loss[N].  A target outside [0, C) gives a NaN
+ * loss.  dtype fp32/fp16/bf16. */
+int tg_cross_entropy_fwd(int dtype, const void* logits, const int64_t* targets, int64_t N,
+                         int64_t C, float label_smoothing, float* lse, float* loss, void* stream);
+/* Backward (_nn.py:1168-1180): grad (+)= (softmax(logits) - w) * scale, with
+ * scale = 1/N for the mean reduction and no upstream-gradient factor, as in the
+ * reference.  grad has dtype dtype_grad. */
+int tg_cross_entropy_bwd(int dtype, const void* logits, const int64_t* targets, const float* lse,
+                         int64_t N, int64_t C, float label_smoothing, float scale, int dtype_grad,
+                         void* grad, int accumulate, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

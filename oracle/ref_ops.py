@@ -356,23 +356,40 @@ def clip_grad_norm(grads, max_norm, norm_type=2.0):
 
 
 # ---------------------------------------------------------------- losses / embedding
-def cross_entropy_fwd(logits, targets):
-    """Mean cross-entropy with logits (_nn.py:1136-1164, no label smoothing):
-    probs by max shift, loss = mean(-log(p_target + 1e-10)).  Returns (loss, probs)."""
+def _ce_weights(n, c, targets, label_smoothing):
+    w = np.full((n, c), label_smoothing / c)
+    w[np.arange(n), targets] += 1.0 - label_smoothing
+    return w
+
+
+def cross_entropy_fwd(logits, targets, label_smoothing=0.0, reduction="mean"):
+    """Cross-entropy with logits (_nn.py:1136-1164): probs by max shift;
+    loss_i = -log(p_target + 1e-10), or with label smoothing s
+    loss_i = -sum_c w_c log(p_c + 1e-10), w = s/C + (1-s) onehot (_nn.py:1152-1156);
+    reduced by mean / sum / none.  Returns (loss, probs)."""
     sh = logits - logits.max(axis=1, keepdims=True)
     e = np.exp(sh)
     probs = e / e.sum(axis=1, keepdims=True)
-    n = logits.shape[0]
-    loss = -np.log(probs[np.arange(n), targets] + 1e-10).mean()
-    return loss, probs
+    n, c = logits.shape
+    if label_smoothing > 0:
+        w = _ce_weights(n, c, targets, label_smoothing)
+        rows = -(w * np.log(probs + 1e-10)).sum(axis=1)
+    else:
+        rows = -np.log(probs[np.arange(n), targets] + 1e-10)
+    if reduction == "mean":
+        return rows.mean(), probs
+    if reduction == "sum":
+        return rows.sum(), probs
+    return rows, probs
 
 
-def cross_entropy_bwd(probs, targets):
-    """(_nn.py:1168-1180): logits.grad += (probs - onehot)/N.  The upstream gradient
-    of the loss is NOT applied (the reference closure never reads out.grad)."""
-    g = probs.copy()
-    g[np.arange(g.shape[0]), targets] -= 1
-    return g / g.shape[0]
+def cross_entropy_bwd(probs, targets, label_smoothing=0.0, reduction="mean"):
+    """(_nn.py:1168-1180): logits.grad += (probs - w)/N for the mean (w the target
+    distribution), unscaled for sum / none.  The upstream gradient of the loss is NOT
+    applied (the reference closure never reads out.grad)."""
+    n, c = probs.shape
+    g = probs - _ce_weights(n, c, targets, label_smoothing)
+    return g / n if reduction == "mean" else g
 
 
 def embedding_bwd(idx, dout, num_embeddings):

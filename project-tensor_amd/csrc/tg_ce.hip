@@ -1,0 +1,240 @@
+// Cross-entropy over logits [N, C] with integer targets, reference
+// CrossEntropyLoss (_nn.py:1128-1185):
+//   p = softmax(x) per row; loss_i = -log(p[t_i] + 1e-10)
+//   (label smoothing s: loss_i = -sum_c w_c log(p_c + 1e-10), w = s/C + (1-s) onehot)
+//   backward: grad (+)= (p - w) * scale, scale = 1/N for the mean reduction; the
+//   reference applies it without the loss's upstream gradient (_nn.py:1168-1180).
+//
+// One workgroup per row.  The forward streams the row once, each thread keeping an
+// online (max, sum of exp) pair per 16-byte vector, merged across the workgroup; it
+// stores the row's log-sum-exp for the backward, which streams the row once more
+// and writes the gradient.  Arithmetic is fp32; the gradient is rounded to its
+// storage dtype once (for fp16 logits, (p - w)/N below fp16's range rounds to zero
+// as in the reference's fp16 arithmetic).  A target outside [0, C) yields a NaN
+// loss and an all-(p*scale) gradient row instead of an out-of-bounds access.
+#include "tg_common.h"
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ void lse_merge(float& m, float& s, float m2, float s2) {
+  const float mn = fmaxf(m, m2);
+  if (mn == -INFINITY) return;  // both empty
+  s = s * exp2f(m - mn) + s2 * exp2f(m2 - mn);
+  m = mn;
+}
+
+// Online (max, sum) of x*log2e over this thread's elements of a row.
+template <typename T, bool VEC>
+__device__ __forceinline__ void row_stats(const T* __restrict__ x, int64_t C, float& m,
+                                          float& s) {
+  m = -INFINITY;
+  s = 0.f;
+  if (VEC) {
+    constexpr int V = tg_vec16<T>::N;
+    const int64_t nv = C / V;
+    for (int64_t i = threadIdx.x; i < nv; i += kBlock) {
+      const tg_vec16<T> v = tg_load16(x + i * V);
+      float e[V];
+      float vm = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        e[j] = tg_to_float(v.v[j]) * kLog2e;
+        vm = fmaxf(vm, e[j]);
+      }
+      float vs = 0.f;
+#pragma unroll
+      for (int j = 0; j < V; ++j) vs += exp2f(e[j] - vm);
+      lse_merge(m, s, vm, vs);
+    }
+  } else {
+    for (int64_t i = threadIdx.x; i < C; i += kBlock) lse_merge(m, s, tg_to_float(x[i]) * kLog2e, 1.f);
+  }
+}
+
+// Row log-sum-exp (natural log) over the workgroup; every thread gets it.
+__device__ __forceinline__ float block_lse(float m, float s) {
+  __shared__ float rm[kBlock / 64], rs[kBlock / 64];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float m2 = __shfl_xor(m, off, 64), s2 = __shfl_xor(s, off, 64);
+    lse_merge(m, s, m2, s2);
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    rm[wave] = m;
+    rs[wave] = s;
+  }
+  __syncthreads();
+  m = rm[0];
+  s = rs[0];
+#pragma unroll
+  for (int w = 1; w < kBlock / 64; ++w) lse_merge(m, s, rm[w], rs[w]);
+  __syncthreads();
+  return (m + log2f(s)) * kLn2;
+}
+
+template <typename T, bool VEC>
+__global__ __launch_bounds__(kBlock) void k_ce_fwd(const T* __restrict__ X,
+                                                   const int64_t* __restrict__ tgt, int64_t C,
+                                                   float smooth, float* __restrict__ lse_out,
+                                                   float* __restrict__ loss_out) {
+  const int64_t row = blockIdx.x;
+  const T* x = X + row * C;
+  float m, s;
+  row_stats<T, VEC>(x, C, m, s);
+  const float lse = block_lse(m, s);
+  const int64_t t = tgt[row];
+  const bool valid = t >= 0 && t < C;
+  float sum_log = 0.f;
+  if (smooth > 0.f) {
+    // sum_c log(p_c + 1e-10): second pass over the row
+    for (int64_t i = threadIdx.x; i < C; i += kBlock)
+      sum_log += logf(expf(tg_to_float(x[i]) - lse) + 1e-10f);
+    float v[1] = {sum_log};
+    __shared__ float red[kBlock / 64];
+    tg_block_sum<kBlock / 64, 1>(v, red);
+    sum_log = v[0];
+  }
+  if (threadIdx.x == 0) {
+    lse_out[row] = lse;
+    float loss = NAN;
+    if (valid) {
+      const float lpt = logf(expf(tg_to_float(x[t]) - lse) + 1e-10f);
+      loss = smooth > 0.f ? -((smooth / (float)C) * sum_log + (1.f - smooth) * lpt) : -lpt;
+    }
+    loss_out[row] = loss;
+  }
+}
+
+template <typename T, typename TG, bool ACC, bool VEC>
+__global__ __launch_bounds__(kBlock) void k_ce_bwd(const T* __restrict__ X,
+                                                   const int64_t* __restrict__ tgt,
+                                                   const float* __restrict__ lse_in, int64_t C,
+                                                   float smooth, float scale, TG* __restrict__ G) {
+  const int64_t row = blockIdx.x;
+  const T* x = X + row * C;
+  TG* g = G + row * C;
+  const float l2 = lse_in[row] * kLog2e;
+  const int64_t t = tgt[row];
+  const float wu = smooth / (float)C;  // weight of every class
+  const float wt = 1.f - smooth;       // extra weight of the target
+  if constexpr (VEC) {
+    constexpr int V = tg_vec16<T>::N;
+    static_assert(sizeof(T) == sizeof(TG), "vector path needs equal element sizes");
+    const int64_t nv = C / V;
+    for (int64_t i = threadIdx.x; i < nv; i += kBlock) {
+      const tg_vec16<T> v = tg_load16(x + i * V);
+      tg_vec16<TG> o;
+      if (ACC) o = tg_load16(g + i * V);
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        const int64_t c = i * V + j;
+        const float p = exp2f(fmaf(tg_to_float(v.v[j]), kLog2e, -l2));
+        float r = (p - wu - (c == t ? wt : 0.f)) * scale;
+        if (ACC) r += tg_to_float(o.v[j]);
+        o.v[j] = tg_from_float<TG>(r);
+      }
+      tg_store16(g + i * V, o);
+    }
+  } else {
+    for (int64_t c = threadIdx.x; c < C; c += kBlock) {
+      const float p = exp2f(fmaf(tg_to_float(x[c]), kLog2e, -l2));
+      float r = (p - wu - (c == t ? wt : 0.f)) * scale;
+      if (ACC) r += tg_to_float(g[c]);
+      g[c] = tg_from_float<TG>(r);
+    }
+  }
+}
+
+template <typename T>
+int fwd_t(const void* x, const int64_t* tg, int64_t N, int64_t C, float smooth, float* lse,
+          float* loss, hipStream_t s) {
+  constexpr int V = tg_vec16<T>::N;
+  const bool vec = tg_aligned16(x) && C % V == 0;
+  if (vec)
+    k_ce_fwd<T, true><<<(unsigned)N, kBlock, 0, s>>>((const T*)x, tg, C, smooth, lse, loss);
+  else
+    k_ce_fwd<T, false><<<(unsigned)N, kBlock, 0, s>>>((const T*)x, tg, C, smooth, lse, loss);
+  return tg_check_launch("tg_cross_entropy_fwd");
+}
+
+template <typename T, typename TG>
+int bwd_t(const void* x, const int64_t* tg, const float* lse, int64_t N, int64_t C, float smooth,
+          float scale, void* g, int acc, hipStream_t s) {
+  constexpr int V = tg_vec16<T>::N;
+  const bool vec = sizeof(T) == sizeof(TG) && tg_aligned16(x) && tg_aligned16(g) && C % V == 0;
+#define L(ACC, VEC)                                                                         \
+  k_ce_bwd<T, TG, ACC, VEC><<<(unsigned)N, kBlock, 0, s>>>((const T*)x, tg, lse, C, smooth, \
+                                                           scale, (TG*)g)
+  if constexpr (sizeof(T) == sizeof(TG)) {
+    if (vec) {
+      if (acc) L(true, true);
+      else L(false, true);
+      return tg_check_launch("tg_cross_entropy_bwd");
+    }
+  }
+  if (acc) L(true, false);
+  else L(false, false);
+#undef L
+  return tg_check_launch("tg_cross_entropy_bwd");
+}
+
+int check(int64_t N, int64_t C, float smooth, const char* who) {
+  TG_REQUIRE(N >= 0 && C > 0, "%s: bad shape N=%lld C=%lld", who, (long long)N, (long long)C);
+  TG_REQUIRE(N <= 0x7fffffff, "%s: N=%lld too large", who, (long long)N);
+  TG_REQUIRE(smooth >= 0.f && smooth < 1.f, "%s: label_smoothing %g outside [0, 1)", who,
+             (double)smooth);
+  return TG_OK;
+}
+
+}  // namespace
+
+TG_EXPORT int tg_cross_entropy_fwd(int dtype, const void* logits, const int64_t* targets,
+                                   int64_t N, int64_t C, float label_smoothing, float* lse,
+                                   float* loss, void* stream) {
+  int st = check(N, C, label_smoothing, "tg_cross_entropy_fwd");
+  if (st) return st;
+  if (N == 0) return TG_OK;
+  TG_REQUIRE(logits && targets && lse && loss, "tg_cross_entropy_fwd: null pointer");
+  hipStream_t s = tg_stream(stream);
+  switch (dtype) {
+    case TG_F32: return fwd_t<float>(logits, targets, N, C, label_smoothing, lse, loss, s);
+    case TG_F16: return fwd_t<tg_half>(logits, targets, N, C, label_smoothing, lse, loss, s);
+    case TG_BF16: return fwd_t<tg_bf16>(logits, targets, N, C, label_smoothing, lse, loss, s);
+  }
+  tg_set_error("tg_cross_entropy_fwd: unsupported dtype %d", dtype);
+  return TG_ERR_UNSUPPORTED;
+}
+
+TG_EXPORT int tg_cross_entropy_bwd(int dtype, const void* logits, const int64_t* targets,
+                                   const float* lse, int64_t N, int64_t C, float label_smoothing,
+                                   float scale, int dtype_grad, void* grad, int accumulate,
+                                   void* stream) {
+  int st = check(N, C, label_smoothing, "tg_cross_entropy_bwd");
+  if (st) return st;
+  if (N == 0) return TG_OK;
+  TG_REQUIRE(logits && targets && lse && grad, "tg_cross_entropy_bwd: null pointer");
+  hipStream_t s = tg_stream(stream);
+#define D2(TX)                                                                                 \
+  switch (dtype_grad) {                                                                        \
+    case TG_F32: return bwd_t<TX, float>(logits, targets, lse, N, C, label_smoothing, scale,   \
+                                         grad, accumulate, s);                                 \
+    case TG_F16: return bwd_t<TX, tg_half>(logits, targets, lse, N, C, label_smoothing, scale, \
+                                           grad, accumulate, s);                               \
+    case TG_BF16: return bwd_t<TX, tg_bf16>(logits, targets, lse, N, C, label_smoothing,       \
+                                            scale, grad, accumulate, s);                       \
+  }                                                                                            \
+  break;
+  switch (dtype) {
+    case TG_F32: D2(float)
+    case TG_F16: D2(tg_half)
+    case TG_BF16: D2(tg_bf16)
+  }
+#undef D2
+  tg_set_error("tg_cross_entropy_bwd: unsupported dtype combination %d/%d", dtype, dtype_grad);
+  return TG_ERR_UNSUPPORTED;
+}

@@ -67,6 +67,9 @@ SIGNATURES = {
     "tg_flash_attn_bwd_workspace": (_sz, [_i64, _i64, _i64, _i64, _i64]),
     "tg_flash_attn_bwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
                                  _i64, _i64, _i64, _f32, _i32, _i32, _vp, _sz, _vp]),
+    "tg_cross_entropy_fwd": (_i32, [_i32, _vp, _vp, _i64, _i64, _f32, _vp, _vp, _vp]),
+    "tg_cross_entropy_bwd": (_i32, [_i32, _vp, _vp, _vp, _i64, _i64, _f32, _f32, _i32, _vp, _i32,
+                                    _vp]),
 }
 
 _lib = None
@@ -556,3 +559,34 @@ def flash_attn_bwd(q, k, v, o, do, lse, dq, dk, dv, scale, causal, accumulate):
         dtype_code(q), ptr(q), ptr(k), ptr(v), ptr(o), ptr(do), ptr(lse), ptr(dq), ptr(dk),
         ptr(dv), B, H, Sq, Sk, D, float(scale), int(bool(causal)), int(bool(accumulate)),
         ptr(ws), ws.numel(), stream_handle()))
+
+
+def cross_entropy_fwd(logits, targets, label_smoothing=0.0):
+    """Per-row log-sum-exp and loss of logits [N, C] against int64 targets [N]:
+    returns (lse, loss), both fp32 [N]."""
+    _dev(logits, "logits")
+    _dev(targets, "targets")
+    if logits.dim() != 2 or not logits.is_contiguous():
+        raise ValueError("cross_entropy: logits must be a contiguous [N, C] tensor")
+    if targets.dtype != torch.int64 or targets.numel() != logits.shape[0]:
+        raise ValueError("cross_entropy: targets must be int64 [N]")
+    N, C = logits.shape
+    lse = torch.empty(N, dtype=torch.float32, device=logits.device)
+    loss = torch.empty(N, dtype=torch.float32, device=logits.device)
+    ensure_device(logits.device.index)
+    _check("tg_cross_entropy_fwd", load().tg_cross_entropy_fwd(
+        dtype_code(logits), ptr(logits), ptr(targets), N, C, float(label_smoothing), ptr(lse),
+        ptr(loss), stream_handle()))
+    return lse, loss
+
+
+def cross_entropy_bwd(logits, targets, lse, grad, scale, accumulate, label_smoothing=0.0):
+    """grad (+)= (softmax(logits) - target distribution) * scale."""
+    for n, t in (("logits", logits), ("targets", targets), ("lse", lse), ("grad", grad)):
+        _dev(t, n)
+    if grad.shape != logits.shape or not grad.is_contiguous():
+        raise ValueError("cross_entropy: grad must be contiguous with the logits' shape")
+    N, C = logits.shape
+    _check("tg_cross_entropy_bwd", load().tg_cross_entropy_bwd(
+        dtype_code(logits), ptr(logits), ptr(targets), ptr(lse), N, C, float(label_smoothing),
+        float(scale), dtype_code(grad), ptr(grad), int(bool(accumulate)), stream_handle()))

@@ -401,20 +401,24 @@ class CrossEntropyLoss(Module):
 
     def __call__(self, logits, targets):
         ld = logits.data
+        if ld.dim() != 2:
+            raise ValueError(f"CrossEntropyLoss expects logits [N, C], got {tuple(ld.shape)}")
         N, C = ld.shape
-        tg = targets.data if isinstance(targets, Tensor) else torch.as_tensor(
-            np.asarray(targets), device="cuda")
-        tg = tg.to(device="cuda", dtype=torch.int64)
-        lf = ld.float()
-        probs = torch.softmax(lf, dim=1)
-        ar = torch.arange(N, device="cuda")
-        if self.label_smoothing > 0:
-            smooth = torch.full_like(probs, self.label_smoothing / C)
-            smooth[ar, tg] = 1 - self.label_smoothing + self.label_smoothing / C
-            loss = -(smooth * torch.log(probs + 1e-10)).sum(dim=1)
+        if isinstance(targets, Tensor):
+            tg = targets.data
+        elif isinstance(targets, torch.Tensor):
+            tg = targets
         else:
-            smooth = None
-            loss = -torch.log(probs[ar, tg] + 1e-10)
+            host = np.asarray(targets)
+            # the reference indexes probs[arange(N), targets]: out-of-range targets raise
+            if host.size and (host.min() < 0 or host.max() >= C):
+                raise IndexError(f"CrossEntropyLoss: target outside [0, {C})")
+            tg = torch.as_tensor(host.astype(np.int64), device=ld.device)
+        tg = tg.to(device=ld.device, dtype=torch.int64).reshape(-1).contiguous()
+        if tg.numel() != N:
+            raise ValueError(f"CrossEntropyLoss: {tg.numel()} targets for {N} rows")
+        ldc = ld.contiguous()
+        lse, loss = L.cross_entropy_fwd(ldc, tg, self.label_smoothing)
         if self.reduction == "mean":
             lv = loss.mean()
         elif self.reduction == "sum":
@@ -422,19 +426,19 @@ class CrossEntropyLoss(Module):
         else:
             lv = loss
         out = Tensor._wrap(lv.to(ld.dtype), (logits,), "CrossEntropy")
-        reduction = self.reduction
+        scale = 1.0 / N if self.reduction == "mean" else 1.0
+        smoothing = self.label_smoothing
         if out._requires_grad:
             def _backward():
                 if not logits._has_grad():
                     return
-                g = probs.clone()
-                if smooth is not None:
-                    g -= smooth
+                buf, acc = logits._grad_target()
+                if buf.is_contiguous() and buf.shape == ldc.shape:
+                    L.cross_entropy_bwd(ldc, tg, lse, buf, scale, acc, smoothing)
                 else:
-                    g[ar, tg] -= 1
-                if reduction == "mean":
-                    g /= N
-                logits._accumulate(g.to(ld.dtype), True)
+                    g = torch.empty_like(ldc)
+                    L.cross_entropy_bwd(ldc, tg, lse, g, scale, False, smoothing)
+                    logits._accumulate(g, True)
             out._backward = _backward
         return out
 

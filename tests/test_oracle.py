@@ -271,6 +271,25 @@ def test_cross_entropy_vs_torch():
     close(O.cross_entropy_bwd(probs, y), xt.grad.numpy(), 1e-9)
 
 
+def test_cross_entropy_label_smoothing_vs_torch():
+    """With label smoothing s the reference's target weights (1 - s + s/C at the target,
+    s/C elsewhere) are torch's; the losses differ only by the +1e-10 inside the log."""
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((7, 11)) * 2
+    y = rng.integers(0, 11, 7)
+    for red in ("mean", "sum"):
+        xt = tt(x)
+        loss = torch.nn.functional.cross_entropy(xt, torch.tensor(y), label_smoothing=0.2,
+                                                 reduction=red)
+        loss.backward()
+        lo, probs = O.cross_entropy_fwd(x, y, 0.2, red)
+        assert abs(lo - loss.item()) < 1e-6 * 11 * 7
+        close(O.cross_entropy_bwd(probs, y, 0.2, red), xt.grad.numpy(), 1e-9)
+    rows, _ = O.cross_entropy_fwd(x, y, 0.0, "none")
+    assert rows.shape == (7,)
+    close(rows.mean(), O.cross_entropy_fwd(x, y)[0], 1e-14)
+
+
 def test_embedding_bwd_repeated_indices():
     idx = np.array([[0, 2, 2], [1, 2, 0]])
     d = np.arange(6 * 4, dtype=np.float64).reshape(2, 3, 4)
