@@ -284,6 +284,34 @@ def _op_ce(torch, L, g):
     return Timed("cross_entropy_fwd_bwd", run, 3 * 2 * N * C, "GB/s", HBM_PEAK_GBS)
 
 
+def _op_embedding(torch, L, g):
+    """C5 embedding backward: fp32 output gradient [8192, 1024] scattered into a fresh
+    [32000, 1024] fp32 gradient (zero-fill + deterministic sorted scatter-add).
+    Algorithmic bytes: fill V*dim*4, read dout, read+write each touched row."""
+    V, dim, n = 32000, 1024, 8192
+    idx = torch.randint(0, V, (n,), device="cuda", generator=g)
+    dout = torch.randn(n, dim, device="cuda", generator=g)
+    grad = torch.empty(V, dim, device="cuda")
+    touched = int(torch.unique(idx).numel())
+
+    def run():
+        L.embedding_bwd(dout, idx, grad, False)
+    work = V * dim * 4 + n * dim * 4 + 2 * touched * dim * 4 + n * 8
+    return Timed("embedding_bwd", run, work, "GB/s", HBM_PEAK_GBS)
+
+
+def _op_tied(torch, L, g):
+    """C5 tied-weight transfer: embedding.grad [32000, 1024] += head.grad.T, fp32.
+    Algorithmic bytes: read both, write the source gradient (3 x 131 MB)."""
+    V, dim = 32000, 1024
+    src = torch.randn(dim, V, device="cuda", generator=g)
+    dst = torch.randn(V, dim, device="cuda", generator=g)
+
+    def run():
+        L.transpose_add(src, dst)
+    return Timed("tied_grad_sync", run, 3 * V * dim * 4, "GB/s", HBM_PEAK_GBS)
+
+
 def component_ops(torch, L, only):
     """Other configurations, each built in its own scope on HBM-resident inputs."""
     g = torch.Generator(device="cuda").manual_seed(1)
@@ -292,6 +320,8 @@ def component_ops(torch, L, only):
                 ("unscale_check", lambda: _op_unscale(torch, L, g)),
                 ("gemm_fc1_bwd", lambda: _op_gemm(torch, L, g)),
                 ("cross_entropy_fwd_bwd", lambda: _op_ce(torch, L, g)),
+                ("embedding_bwd", lambda: _op_embedding(torch, L, g)),
+                ("tied_grad_sync", lambda: _op_tied(torch, L, g)),
                 ("gpt_step", lambda: _op_gpt(torch, L, g))]
     for d in (64, 128):
         for causal in (False, True):

@@ -174,6 +174,20 @@ int tg_cross_entropy_bwd(int dtype, const void* logits, const int64_t* targets, 
                          int64_t N, int64_t C, float label_smoothing, float scale, int dtype_grad,
                          void* grad, int accumulate, void* stream);
 
+/* Embedding backward (Embedding._backward, _nn.py:1083-1089): grad[idx[i]] (+)=
+ * dout[i] for n_tokens rows of dim elements, grad [num_embeddings, dim].
+ * Deterministic: a stable sort of the indices, then each index's rows summed in their
+ * original order (np.add.at's order).  Indices outside [0, num_embeddings) are
+ * skipped.  Workspace from tg_embedding_bwd_workspace. */
+size_t tg_embedding_bwd_workspace(int64_t n_tokens, int64_t num_embeddings);
+int tg_embedding_bwd(int dtype_dout, const void* dout, const int64_t* indices, int64_t n_tokens,
+                     int64_t dim, int dtype_grad, void* grad, int64_t num_embeddings,
+                     int accumulate, void* workspace, size_t workspace_bytes, void* stream);
+/* dst[c][r] += alpha * src[r][c] for src [rows, cols] (sync_tied_gradients,
+ * _training.py:264-284: source.grad += param.grad.T). */
+int tg_transpose_add(int dtype_src, const void* src, int64_t rows, int64_t cols, int dtype_dst,
+                     void* dst, float alpha, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -212,8 +212,66 @@ __global__ __launch_bounds__(kThreads) void k_axpby(const TX* __restrict__ x, TY
   }
 }
 
+// 8 consecutive elements through 16-byte accesses (two for fp32).
+template <typename T>
+__device__ __forceinline__ void ld8f(const T* p, float (&f)[8]) {
+  constexpr int V = tg_vec16<T>::N;
+#pragma unroll
+  for (int h = 0; h < 8 / V; ++h) {
+    const tg_vec16<T> v = tg_load16(p + h * V);
+#pragma unroll
+    for (int j = 0; j < V; ++j) f[h * V + j] = tg_to_float(v.v[j]);
+  }
+}
+template <typename T>
+__device__ __forceinline__ void st8f(T* p, const float (&f)[8]) {
+  constexpr int V = tg_vec16<T>::N;
+#pragma unroll
+  for (int h = 0; h < 8 / V; ++h) {
+    tg_vec16<T> v;
+#pragma unroll
+    for (int j = 0; j < V; ++j) v.v[j] = tg_from_float<T>(f[h * V + j]);
+    tg_store16(p + h * V, v);
+  }
+}
+
+// Vector form: n8 groups of 8 elements, then a scalar tail in block 0.
+template <typename TX, typename TY, bool READ_Y>
+__global__ __launch_bounds__(kThreads) void k_axpby8(const TX* __restrict__ x, TY* __restrict__ y,
+                                                     float alpha, float beta, int64_t n8,
+                                                     int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n8; i += stride) {
+    float a[8], b[8];
+    ld8f(x + i * 8, a);
+    if (READ_Y) ld8f(y + i * 8, b);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) a[j] = READ_Y ? alpha * a[j] + beta * b[j] : alpha * a[j];
+    st8f(y + i * 8, a);
+  }
+  if (blockIdx.x == 0) {
+    for (int64_t i = n8 * 8 + threadIdx.x; i < n; i += kThreads) {
+      float v = alpha * tg_to_float(x[i]);
+      if (READ_Y) v += beta * tg_to_float(y[i]);
+      y[i] = tg_from_float<TY>(v);
+    }
+  }
+}
+
 template <typename TX, typename TY>
 int launch_axpby(const void* x, void* y, float a, float b, int64_t n, hipStream_t s) {
+  if (tg_aligned16(x) && tg_aligned16(y)) {
+    const int64_t n8 = n / 8;
+    int64_t blocks = (n8 + kThreads - 1) / kThreads;
+    const int64_t cap = (int64_t)tg_num_cus() * 16;
+    if (blocks > cap) blocks = cap;
+    if (blocks < 1) blocks = 1;
+    if (b != 0.f)
+      k_axpby8<TX, TY, true><<<(unsigned)blocks, kThreads, 0, s>>>((const TX*)x, (TY*)y, a, b, n8, n);
+    else
+      k_axpby8<TX, TY, false><<<(unsigned)blocks, kThreads, 0, s>>>((const TX*)x, (TY*)y, a, b, n8, n);
+    return tg_check_launch("tg_axpby");
+  }
   int64_t blocks = (n + kThreads * 4 - 1) / (kThreads * 4);
   const int64_t cap = (int64_t)tg_num_cus() * 32;
   if (blocks > cap) blocks = cap;

@@ -68,6 +68,9 @@ SIGNATURES = {
     "tg_flash_attn_bwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
                                  _i64, _i64, _i64, _f32, _i32, _i32, _vp, _sz, _vp]),
     "tg_cross_entropy_fwd": (_i32, [_i32, _vp, _vp, _i64, _i64, _f32, _vp, _vp, _vp]),
+    "tg_embedding_bwd_workspace": (_sz, [_i64, _i64]),
+    "tg_embedding_bwd": (_i32, [_i32, _vp, _vp, _i64, _i64, _i32, _vp, _i64, _i32, _vp, _sz, _vp]),
+    "tg_transpose_add": (_i32, [_i32, _vp, _i64, _i64, _i32, _vp, _f32, _vp]),
     "tg_cross_entropy_bwd": (_i32, [_i32, _vp, _vp, _vp, _i64, _i64, _f32, _f32, _i32, _vp, _i32,
                                     _vp]),
 }
@@ -590,3 +593,35 @@ def cross_entropy_bwd(logits, targets, lse, grad, scale, accumulate, label_smoot
     _check("tg_cross_entropy_bwd", load().tg_cross_entropy_bwd(
         dtype_code(logits), ptr(logits), ptr(targets), ptr(lse), N, C, float(label_smoothing),
         float(scale), dtype_code(grad), ptr(grad), int(bool(accumulate)), stream_handle()))
+
+
+def embedding_bwd(dout, indices, grad, accumulate):
+    """grad[indices[i]] (+)= dout[i]: dout [..., dim] with indices [...] (int64),
+    grad [num_embeddings, dim]."""
+    for n, t in (("dout", dout), ("indices", indices), ("grad", grad)):
+        _dev(t, n)
+    if indices.dtype != torch.int64:
+        raise TypeError("embedding_bwd: indices must be int64")
+    V, dim = grad.shape
+    n = indices.numel()
+    if dout.numel() != n * dim:
+        raise ValueError(f"embedding_bwd: dout has {dout.numel()} elements for {n} x {dim}")
+    lib = load()
+    ensure_device(grad.device.index)
+    ws = workspace(lib.tg_embedding_bwd_workspace(n, V), grad.device)
+    _check("tg_embedding_bwd", lib.tg_embedding_bwd(
+        dtype_code(dout), ptr(dout), ptr(indices), n, dim, dtype_code(grad), ptr(grad), V,
+        int(bool(accumulate)), ptr(ws), ws.numel(), stream_handle()))
+
+
+def transpose_add(src, dst, alpha=1.0):
+    """dst += alpha * src.T for a contiguous 2-D src [R, C] and dst [C, R]."""
+    _dev(src, "src")
+    _dev(dst, "dst")
+    R, C = src.shape
+    if tuple(dst.shape) != (C, R):
+        raise ValueError(f"transpose_add: dst {tuple(dst.shape)} is not {(C, R)}")
+    ensure_device(dst.device.index)
+    _check("tg_transpose_add", load().tg_transpose_add(
+        dtype_code(src), ptr(src), R, C, dtype_code(dst), ptr(dst), float(alpha),
+        stream_handle()))

@@ -352,19 +352,30 @@ class Embedding(Module):
         self.embedding_dim = embedding_dim
 
     def __call__(self, indices):
-        idx = indices.data if isinstance(indices, Tensor) else torch.as_tensor(
-            np.asarray(indices), device="cuda")
-        idx = idx.to(device="cuda", dtype=torch.int64)
+        V = self.num_embeddings
+        if isinstance(indices, Tensor):
+            idx = indices.data
+        elif isinstance(indices, torch.Tensor):
+            idx = indices
+        else:
+            host = np.asarray(indices)
+            # checked here: an out-of-range gather on the device would assert in-kernel
+            if host.size and (host.min() < -V or host.max() >= V):
+                raise IndexError(f"Embedding: index outside [-{V}, {V})")
+            idx = torch.as_tensor(host.astype(np.int64), device=self.weight.data.device)
+        idx = idx.to(device=self.weight.data.device, dtype=torch.int64)
+        idx = torch.where(idx < 0, idx + V, idx)  # negative indices wrap, as NumPy's
         weight = self.weight
         out = Tensor._wrap(weight.data[idx], (weight,), "Embedding")
         dim = self.embedding_dim
+        flat = idx.reshape(-1).contiguous()
         if out._requires_grad:
             def _backward():
                 if not weight._has_grad():
                     return
-                g = out._grad_out().reshape(-1, dim)
-                buf = weight.grad
-                buf.index_add_(0, idx.reshape(-1), g.to(buf.dtype))
+                g = out._grad_out().reshape(-1, dim).contiguous()
+                buf, acc = weight._grad_target()
+                L.embedding_bwd(g, flat, buf, acc)
             out._backward = _backward
         return out
 

@@ -77,5 +77,11 @@ def sync_tied_gradients(model):
             continue
         if src._has_grad():
             g = p.grad
-            src._accumulate(g.t() if p._tied_transpose else g)
+            if p._tied_transpose and g.dim() == 2 and g.is_contiguous():
+                buf, acc = src._grad_target()
+                if not acc:
+                    L.fill(buf, 0.0)
+                L.transpose_add(g, buf)
+            else:
+                src._accumulate(g.t() if p._tied_transpose else g)
             p.zero_grad()

@@ -1,0 +1,92 @@
+"""Embedding backward (deterministic sorted scatter-add) and the tied-weight transfer
+(tg_transpose_add) vs the oracle / closed forms.  GPU only.
+
+fp32 embedding gradients are compared bit-exactly with np.add.at (the kernel sums
+each index's rows in their original order, as np.add.at does)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from conftest import RTOL_F16, RTOL_F32, assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def L():
+    from tensor_gpu_v2 import _lib
+    return _lib
+
+
+@pytest.mark.parametrize("n,V,dim", [(1, 1, 1), (24, 5, 7), (8192, 32000, 64), (300, 50, 1000)])
+def test_embedding_bwd_bit_exact_fp32(cuda, n, V, dim):
+    rng = np.random.default_rng(n + V)
+    idx = rng.integers(0, V, n)
+    idx[: n // 3] = idx[0]  # many repeats of one index
+    d = rng.standard_normal((n, dim)).astype(np.float32)
+    want = O.embedding_bwd(idx, d, V)
+    grad = torch.empty(V, dim, device="cuda")
+    L().embedding_bwd(torch.tensor(d, device="cuda"), torch.tensor(idx, device="cuda"), grad,
+                      False)
+    assert np.array_equal(grad.cpu().numpy(), want)
+
+
+def test_embedding_bwd_half_accumulate_and_bounds(cuda):
+    rng = np.random.default_rng(9)
+    V, dim = 40, 33
+    idx = rng.integers(0, V, 200)
+    idx[5], idx[6] = -1, V  # out of range: skipped
+    d = rng.standard_normal((200, dim)).astype(np.float16)
+    base = rng.standard_normal((V, dim)).astype(np.float32)
+    grad = torch.tensor(base, device="cuda")
+    L().embedding_bwd(torch.tensor(d, device="cuda"), torch.tensor(idx, device="cuda"), grad, True)
+    ok = (idx >= 0) & (idx < V)
+    want = base.astype(np.float64) + O.embedding_bwd(idx[ok], d[ok].astype(np.float64), V)
+    assert_close(grad, want, RTOL_F32, "accumulated fp16 rows")
+
+
+def test_embedding_module(cuda):
+    import tensor_gpu_v2 as tg
+    rng = np.random.default_rng(2)
+    emb = tg.Embedding(10, 4)
+    ids = np.array([[1, 2, 2], [-1, 0, 9]])
+    out = emb(ids)
+    w = emb.weight.data.cpu().numpy()
+    assert np.array_equal(out.data.cpu().numpy(), w[ids % 10])
+    g = rng.standard_normal((2, 3, 4)).astype(np.float32)
+    (out * tg.Tensor(g, requires_grad=False)).sum().backward()
+    assert np.array_equal(emb.weight.grad.cpu().numpy(), O.embedding_bwd(ids % 10, g, 10))
+    with pytest.raises(IndexError):
+        emb(np.array([10]))
+
+
+@pytest.mark.parametrize("R,C", [(1, 1), (100, 70), (130, 1000)])
+@pytest.mark.parametrize("ds,dd", [(torch.float32, torch.float32), (torch.float16, torch.float32)])
+def test_transpose_add(cuda, R, C, ds, dd):
+    g = torch.Generator(device="cuda").manual_seed(R * C)
+    src = torch.randn(R, C, device="cuda", generator=g).to(ds)
+    dst = torch.randn(C, R, device="cuda", generator=g).to(dd)
+    want = dst.double() + 0.5 * src.double().t()
+    L().transpose_add(src, dst, 0.5)
+    assert_close(dst, want.cpu().numpy(), RTOL_F32 if ds == torch.float32 else RTOL_F16, "dst")
+
+
+def test_sync_tied_gradients(cuda):
+    """source.grad += target.grad.T and the target's grad is reset
+    (_training.py:264-284), for a source with and without a gradient yet."""
+    import tensor_gpu_v2 as tg
+    emb = tg.Embedding(6, 3)
+    head = tg.Linear(3, 6, bias=False)
+    tg.weight_tie(emb.weight, head, "w", transpose=True)
+    model = tg.Module()
+    model.emb, model.head = emb, head
+    rng = np.random.default_rng(1)
+    ht = rng.standard_normal((3, 6)).astype(np.float32)
+    head.w.grad = ht
+    emb.weight.zero_grad()
+    tg.sync_tied_gradients(model)
+    assert np.array_equal(emb.weight.grad.cpu().numpy(), ht.T)
+    assert not head.w.grad.cpu().numpy().any()
+    head.w.grad = ht
+    tg.sync_tied_gradients(model)
+    assert_close(emb.weight.grad, 2.0 * ht.T.astype(np.float64), RTOL_F32, "accumulated")

@@ -431,3 +431,25 @@ def test_multi_tensor_many_and_misaligned(cuda):
         L().zero_nonfinite(hs)
         for h, exp in zip(hs, half):
             assert np.array_equal(f64(h), np.where(np.isfinite(exp), exp, 0.0))
+
+
+@pytest.mark.parametrize("n", [1, 7, 8, 4099, 1 << 20])
+@pytest.mark.parametrize("dx,dy", [(torch.float16, torch.float16), (torch.float16, torch.float32),
+                                   (torch.float32, torch.float16), (torch.bfloat16, torch.float32),
+                                   (torch.float32, torch.float32)])
+@pytest.mark.parametrize("mis", [False, True])
+def test_axpby(cuda, n, dx, dy, mis):
+    """y = alpha*x + beta*y (fp32 arithmetic, one rounding to y's dtype); beta = 0 must
+    not read y (NaN-filled y stays out of the result)."""
+    rng = np.random.default_rng(n)
+    x = dev(rng.standard_normal(n), dx)
+    y0 = dev(rng.standard_normal(n), dy)
+    if mis:
+        x, y0 = misaligned(x), misaligned(y0)
+    y = y0.clone() if not mis else misaligned(y0.clone())
+    L().axpby(x, y, 0.5, -2.0)
+    want = (0.5 * x.float() + -2.0 * y0.float()).to(dy)
+    assert torch.equal(y, want)
+    y.fill_(float("nan"))
+    L().axpby(x, y, 3.0, 0.0)
+    assert torch.equal(y, (3.0 * x.float()).to(dy))
