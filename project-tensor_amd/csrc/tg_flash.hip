@@ -317,7 +317,16 @@ typedef short v4i16 __attribute__((ext_vector_type(4)));
 template <int D> struct SwzTile {
   static constexpr int CH = D / 8;  // 16-byte chunks per row
   static constexpr int RB = D * 2;  // bytes per row
-  __device__ static int key(int r) { return CH == 16 ? (r & 15) : ((r >> 1) & 7); }
+  // XOR key of row r: 16 consecutive rows get distinct chunk positions (16-byte row
+  // reads by 16 lanes hit every bank once) and rows r..r+3 of a transpose read land in
+  // different 64-byte bank groups.
+  __device__ static int key(int r) {
+    if (CH == 8) {
+      const int x = (r >> 1) & 7;
+      return ((x & 1) << 2) | (x >> 1);
+    }
+    return ((r & 3) << 2) | ((r >> 2) & 3);
+  }
   __device__ static int off(int r, int c) { return r * RB + ((c ^ key(r)) << 4); }
 };
 

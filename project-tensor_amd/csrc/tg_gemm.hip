@@ -450,8 +450,15 @@ typedef short v4i16_g __attribute__((ext_vector_type(4)));
 
 constexpr int V3_BK = 64;
 
+// XOR key of row r (CH 16-byte chunks per row): 16 consecutive rows get distinct
+// chunk positions and rows r..r+3 of a transpose read land in different 64-byte bank
+// groups, so both read kinds are conflict-free.
 template <int CH> __device__ __forceinline__ int v3_key(int r) {
-  return CH == 16 ? (r & 15) : ((r >> 1) & 7);
+  if (CH == 8) {
+    const int x = (r >> 1) & 7;
+    return ((x & 1) << 2) | (x >> 1);
+  }
+  return ((r & 3) << 2) | ((r >> 2) & 3);
 }
 template <int CH> __device__ __forceinline__ int v3_off(int r, int c) {
   return r * CH * 16 + ((c ^ v3_key<CH>(r)) << 4);
