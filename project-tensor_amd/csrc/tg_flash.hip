@@ -332,22 +332,45 @@ template <int D> struct SwzTile {
 
 // Async copy of rows [row0, row0+R) of a [nrows, D] matrix into a swizzled tile.
 // Rows past nrows copy row nrows-1; the kernels make those rows contribute nothing.
+// A wave issues NI/4 instructions; DmaPlan holds each one's element offset within the
+// tile for this lane (the same for every tile), so a whole tile costs one 64-bit add
+// per instruction unless it is the partial last tile.
 template <typename T, int D, int R>
-__device__ __forceinline__ void tile_dma(const T* __restrict__ g, int64_t row0, int64_t nrows,
-                                         char* lds) {
-  constexpr int CH = D / 8, NI = R * CH / 64;
+struct DmaPlan {
+  static constexpr int CH = D / 8, NI = R * CH / 64, NPW = NI / (kThreads / 64);
   static_assert(NI % (kThreads / 64) == 0, "tile must split evenly over the waves");
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int off[NPW];
+  __device__ void init(int lane, int wave) {
 #pragma unroll
-  for (int i = wave; i < NI; i += kThreads / 64) {
-    const int u = i * 64 + lane;
-    const int r = u / CH, c = (u % CH) ^ SwzTile<D>::key(r);
-    int64_t row = row0 + r;
-    row = row < nrows ? row : nrows - 1;
-    __builtin_amdgcn_global_load_lds((const TG_GLB void*)(g + row * D + c * 8),
-                                     (TG_LDS void*)(lds + i * 1024), 16, 0, 0);
+    for (int k = 0; k < NPW; ++k) {
+      const int u = (wave + k * (kThreads / 64)) * 64 + lane;
+      const int r = u / CH, c = (u % CH) ^ SwzTile<D>::key(r);
+      off[k] = r * D + c * 8;
+    }
   }
-}
+  __device__ __forceinline__ void copy(const T* __restrict__ g, int64_t row0, int64_t nrows,
+                                       char* lds) const {
+    const int wave = threadIdx.x >> 6;
+    if (row0 + R <= nrows) {  // uniform
+      const T* base = g + row0 * D;
+#pragma unroll
+      for (int k = 0; k < NPW; ++k)
+        __builtin_amdgcn_global_load_lds((const TG_GLB void*)(base + off[k]),
+                                         (TG_LDS void*)(lds + (wave + k * (kThreads / 64)) * 1024),
+                                         16, 0, 0);
+    } else {
+#pragma unroll
+      for (int k = 0; k < NPW; ++k) {
+        const int r = off[k] / D;
+        int64_t row = row0 + r;
+        row = row < nrows ? row : nrows - 1;
+        __builtin_amdgcn_global_load_lds((const TG_GLB void*)(g + row * D + (off[k] - r * D)),
+                                         (TG_LDS void*)(lds + (wave + k * (kThreads / 64)) * 1024),
+                                         16, 0, 0);
+      }
+    }
+  }
+};
 
 // Wait for this wave's outstanding DMA and global loads; a barrier then makes every
 // wave's part of the tile visible.
@@ -392,6 +415,119 @@ struct LaneOffs {
   }
 };
 
+// Hand-ordered variant of dkdv_sub for one key group.  The compiler, at one wave per
+// SIMD and ~400 live registers, issues each LDS fragment read right before the MFMA
+// that consumes it and waits for it there, so every MFMA pays a full LDS latency.
+// Here sched_barrier fences fix the order: fragment reads run PF ahead of their
+// MFMAs, the exp of S is spread over the dP MFMAs, dS over the dV MFMAs, and the
+// transpose reads of each phase are issued during the previous one.
+#ifndef TG_FA_PIPE
+#define TG_FA_PIPE 1
+#endif
+constexpr bool kPipe = TG_FA_PIPE;
+#define TG_SB() __builtin_amdgcn_sched_barrier(0)
+template <typename T, int D, bool DIAG>
+__device__ __forceinline__ void dkdv_sub_pipe(const char* qs, const char* dos,
+                                              const float* lse, const float* dvs, int h,
+                                              const LaneOffs<D>& o,
+                                              const typename Vec8<T>::type (&kf)[D / 16],
+                                              const typename Vec8<T>::type (&vf)[D / 16],
+                                              f32x16 (&dk)[D / 32], f32x16 (&dv)[D / 32],
+                                              float sl2, float scale, int mb) {
+  using V8 = typename Vec8<T>::type;
+  constexpr int DK = D / 16, DT = D / 32, RB = D * 2, PF = 4;
+  constexpr int NB = 2 * DT;          // MFMAs of the dV (and of the dK) phase
+  constexpr int EA = 16 / DK;         // exp elements per dP MFMA
+  constexpr int EB = 16 / NB;         // dS elements per dV MFMA
+  // transpose operand n of a phase: sg = n / DT, dt = n % DT
+  auto tr = [&](const char* base, int n) {
+    const char* b = base + (n / DT) * 16 * RB;
+    return lds_tr<T>(b + o.t[0][n % DT], b + o.t[1][n % DT]);
+  };
+  V8 qa[DK], da[DK], bv[NB], bk[NB];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) qa[i] = lds_a<T>(qs + o.a[i]);
+  float la[16], db[16];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const float4 a = *reinterpret_cast<const float4*>(lse + 8 * g + 4 * h);
+    const float4 b = *reinterpret_cast<const float4*>(dvs + 8 * g + 4 * h);
+    la[4 * g] = a.x; la[4 * g + 1] = a.y; la[4 * g + 2] = a.z; la[4 * g + 3] = a.w;
+    db[4 * g] = b.x; db[4 * g + 1] = b.y; db[4 * g + 2] = b.z; db[4 * g + 3] = b.w;
+  }
+  f32x16 sa, dpa;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    sa[r] = 0.f;
+    dpa[r] = 0.f;
+  }
+  TG_SB();
+  // phase A: S = Q K^T while the Q then dO fragment reads run PF ahead
+#pragma unroll
+  for (int ks = 0; ks < DK; ++ks) {
+    sa = mfma(qa[ks], kf[ks], sa);
+    const int n = ks + PF;
+    if (n < DK) qa[n] = lds_a<T>(qs + o.a[n]);
+    else da[n - DK] = lds_a<T>(dos + o.a[n - DK]);
+    TG_SB();
+  }
+  // phase A': dP = dO V^T; exp of S spread behind it; dO^T transpose reads start
+  float p[16];
+  auto expo = [&](int r) {
+    float pv = fexp2(fmaf(sa[r], sl2, -la[r]));
+    if (DIAG) pv = (mb > 8 * (r >> 2) + (r & 3)) ? 0.f : pv;
+    p[r] = pv;
+  };
+  int nv = 0;
+#pragma unroll
+  for (int ks = 0; ks < DK; ++ks) {
+    dpa = mfma(da[ks], vf[ks], dpa);
+    const int n = ks + PF;
+    if (n < DK) da[n] = lds_a<T>(dos + o.a[n]);
+    else if (nv < NB) { bv[nv] = tr(dos, nv); ++nv; }
+    if (ks > 0)
+#pragma unroll
+      for (int e = 0; e < EA; ++e) expo((ks - 1) * EA + e);
+    TG_SB();
+  }
+#pragma unroll
+  for (int e = 0; e < EA; ++e) expo((DK - 1) * EA + e);
+  V8 pa[2] = {pack8<T>(&p[0]), pack8<T>(&p[8])};
+  TG_SB();
+  // phase B: dV += P^T dO; dS spread behind it; remaining dO^T then Q^T reads
+  float ds[16];
+  int nk = 0;
+#pragma unroll
+  for (int n = 0; n < NB; ++n) {
+    while (nv <= n) { bv[nv] = tr(dos, nv); ++nv; }
+    dv[n % DT] = mfma(pa[n / DT], bv[n], dv[n % DT]);
+    if (nv < NB) { bv[nv] = tr(dos, nv); ++nv; }
+    else if (nk < NB) { bk[nk] = tr(qs, nk); ++nk; }
+    if (n > 0)
+#pragma unroll
+      for (int e = 0; e < EB; ++e) {
+        const int r = (n - 1) * EB + e;
+        ds[r] = p[r] * fmaf(dpa[r], scale, -db[r]);
+      }
+    TG_SB();
+  }
+#pragma unroll
+  for (int e = 0; e < EB; ++e) {
+    const int r = (NB - 1) * EB + e;
+    ds[r] = p[r] * fmaf(dpa[r], scale, -db[r]);
+  }
+  V8 dsa[2] = {pack8<T>(&ds[0]), pack8<T>(&ds[8])};
+  TG_SB();
+  // phase C: dK += dS^T Q
+#pragma unroll
+  for (int n = 0; n < NB; ++n) {
+    while (nk <= n) { bk[nk] = tr(qs, nk); ++nk; }
+    dk[n % DT] = mfma(dsa[n / DT], bk[n], dk[n % DT]);
+    if (nk < NB) { bk[nk] = tr(qs, nk); ++nk; }
+    TG_SB();
+  }
+}
+
 // One 32-query x 32-key sub-tile of the dK/dV kernel for one wave (lane = key).
 //   qs/dos: the sub-tile's first row in the Q / dO tiles; lse/dvs: its 32 log2-scaled
 //   LSE values (+inf past Sq, so P = 0 there) and scale*D values.
@@ -399,93 +535,128 @@ struct LaneOffs {
 //   mb = (first key of the wave's 32 + l32) - (first query of the sub-tile) - 4h,
 //   so that the mask for accumulator register r is mb > 8*(r/4) + r%4.
 // Keys past Sk (clamped rows of K/V) only feed dK/dV rows that are never stored.
-template <typename T, int D, bool DIAG>
+template <typename T, int D, int KG, bool DIAG>
 __device__ __forceinline__ void dkdv_sub(const char* qs, const char* dos, const float* lse,
                                          const float* dvs, int h, const LaneOffs<D>& o,
-                                         const typename Vec8<T>::type (&kf)[D / 16],
-                                         const typename Vec8<T>::type (&vf)[D / 16],
-                                         f32x16 (&dk)[D / 32], f32x16 (&dv)[D / 32], float sl2,
-                                         float scale, int mb) {
+                                         const typename Vec8<T>::type (&kf)[KG][D / 16],
+                                         const typename Vec8<T>::type (&vf)[KG][D / 16],
+                                         f32x16 (&dk)[KG][D / 32], f32x16 (&dv)[KG][D / 32],
+                                         float sl2, float scale, int mb) {
   constexpr int DK = D / 16, DT = D / 32, RB = D * 2;
-  f32x16 s, dp;
+  f32x16 s[KG], dp[KG];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    s[r] = 0.f;
-    dp[r] = 0.f;
+  for (int j = 0; j < KG; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      s[j][r] = 0.f;
+      dp[j][r] = 0.f;
+    }
+  // one LDS read of each Q / dO fragment feeds all KG key groups
+#pragma unroll
+  for (int ks = 0; ks < DK; ++ks) {
+    const auto qa = lds_a<T>(qs + o.a[ks]);
+#pragma unroll
+    for (int j = 0; j < KG; ++j) s[j] = mfma(qa, kf[j][ks], s[j]);
   }
 #pragma unroll
-  for (int ks = 0; ks < DK; ++ks) s = mfma(lds_a<T>(qs + o.a[ks]), kf[ks], s);
+  for (int ks = 0; ks < DK; ++ks) {
+    const auto da = lds_a<T>(dos + o.a[ks]);
 #pragma unroll
-  for (int ks = 0; ks < DK; ++ks) dp = mfma(lds_a<T>(dos + o.a[ks]), vf[ks], dp);
-  float p[16];
+    for (int j = 0; j < KG; ++j) dp[j] = mfma(da, vf[j][ks], dp[j]);
+  }
+  float p[KG][16];
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     const float4 a = *reinterpret_cast<const float4*>(lse + 8 * g + 4 * h);
     const float la[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float pv = fexp2(fmaf(s[4 * g + i], sl2, -la[i]));
-      if (DIAG) pv = (mb > 8 * g + i) ? 0.f : pv;
-      p[4 * g + i] = pv;
-    }
+    for (int j = 0; j < KG; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float pv = fexp2(fmaf(s[j][4 * g + i], sl2, -la[i]));
+        if (DIAG) pv = (mb + 32 * j > 8 * g + i) ? 0.f : pv;
+        p[j][4 * g + i] = pv;
+      }
   }
 #pragma unroll
   for (int sg = 0; sg < 2; ++sg) {
-    const typename Vec8<T>::type pa = pack8<T>(&p[8 * sg]);
+    typename Vec8<T>::type pa[KG];
+#pragma unroll
+    for (int j = 0; j < KG; ++j) pa[j] = pack8<T>(&p[j][8 * sg]);
     const char* b = dos + sg * 16 * RB;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-      dv[dt] = mfma(pa, lds_tr<T>(b + o.t[0][dt], b + o.t[1][dt]), dv[dt]);
+    for (int dt = 0; dt < DT; ++dt) {
+      const auto bt = lds_tr<T>(b + o.t[0][dt], b + o.t[1][dt]);
+#pragma unroll
+      for (int j = 0; j < KG; ++j) dv[j][dt] = mfma(pa[j], bt, dv[j][dt]);
+    }
   }
-  float ds[16];
+  float ds[KG][16];
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     const float4 b = *reinterpret_cast<const float4*>(dvs + 8 * g + 4 * h);
     const float db[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ds[4 * g + i] = p[4 * g + i] * fmaf(dp[4 * g + i], scale, -db[i]);
+    for (int j = 0; j < KG; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        ds[j][4 * g + i] = p[j][4 * g + i] * fmaf(dp[j][4 * g + i], scale, -db[i]);
   }
 #pragma unroll
   for (int sg = 0; sg < 2; ++sg) {
-    const typename Vec8<T>::type da = pack8<T>(&ds[8 * sg]);
+    typename Vec8<T>::type da[KG];
+#pragma unroll
+    for (int j = 0; j < KG; ++j) da[j] = pack8<T>(&ds[j][8 * sg]);
     const char* b = qs + sg * 16 * RB;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-      dk[dt] = mfma(da, lds_tr<T>(b + o.t[0][dt], b + o.t[1][dt]), dk[dt]);
+    for (int dt = 0; dt < DT; ++dt) {
+      const auto bt = lds_tr<T>(b + o.t[0][dt], b + o.t[1][dt]);
+#pragma unroll
+      for (int j = 0; j < KG; ++j) dk[j][dt] = mfma(da[j], bt, dk[j][dt]);
+    }
   }
 }
 
 // The BM/32 sub-tiles of one staged query tile; kq = first key of this wave minus the
-// tile's first query.
-template <typename T, int D, int BM>
+// tile's first query.  The wave's keys are kq .. kq + 32*KG - 1.
+template <typename T, int D, int BM, int KG>
 __device__ __forceinline__ void dkdv_tile(const char* qs, const char* dos, const float* lse,
                                           const float* dvs, int kq, int causal, int h, int l32,
                                           const LaneOffs<D>& o,
-                                          const typename Vec8<T>::type (&kf)[D / 16],
-                                          const typename Vec8<T>::type (&vf)[D / 16],
-                                          f32x16 (&dk)[D / 32], f32x16 (&dv)[D / 32], float sl2,
-                                          float scale) {
+                                          const typename Vec8<T>::type (&kf)[KG][D / 16],
+                                          const typename Vec8<T>::type (&vf)[KG][D / 16],
+                                          f32x16 (&dk)[KG][D / 32], f32x16 (&dv)[KG][D / 32],
+                                          float sl2, float scale) {
   constexpr int RB = D * 2;
-#pragma unroll 1
+#pragma unroll
   for (int t = 0; t < BM / 32; ++t) {
     // causal: a 32-query sub-tile wholly before this wave's keys contributes nothing
     if (causal && t * 32 + 31 < kq) continue;
     const char* q = qs + t * 32 * RB;
     const char* d = dos + t * 32 * RB;
-    if (causal && kq + 31 > t * 32)
-      dkdv_sub<T, D, true>(q, d, lse + t * 32, dvs + t * 32, h, o, kf, vf, dk, dv, sl2, scale,
-                           kq + l32 - t * 32 - 4 * h);
-    else
-      dkdv_sub<T, D, false>(q, d, lse + t * 32, dvs + t * 32, h, o, kf, vf, dk, dv, sl2, scale,
-                            0);
+    if constexpr (KG == 1 && kPipe) {
+      if (causal && kq + 31 > t * 32)
+        dkdv_sub_pipe<T, D, true>(q, d, lse + t * 32, dvs + t * 32, h, o, kf[0], vf[0], dk[0],
+                                  dv[0], sl2, scale, kq + l32 - t * 32 - 4 * h);
+      else
+        dkdv_sub_pipe<T, D, false>(q, d, lse + t * 32, dvs + t * 32, h, o, kf[0], vf[0], dk[0],
+                                   dv[0], sl2, scale, 0);
+    } else {
+      if (causal && kq + 32 * KG - 1 > t * 32)
+        dkdv_sub<T, D, KG, true>(q, d, lse + t * 32, dvs + t * 32, h, o, kf, vf, dk, dv, sl2,
+                                 scale, kq + l32 - t * 32 - 4 * h);
+      else
+        dkdv_sub<T, D, KG, false>(q, d, lse + t * 32, dvs + t * 32, h, o, kf, vf, dk, dv, sl2,
+                                  scale, 0);
+    }
   }
 }
 
-// dK, dV.  grid = (ceil(Sk/128), B*H); one workgroup = 128 keys (4 waves x 32 keys,
-// K/V fragments in registers), looping over query tiles of BM rows double-buffered
+// dK, dV.  grid = (ceil(Sk/(128*KG)), B*H); one workgroup = 128*KG keys (4 waves x
+// 32*KG keys, K/V fragments in registers), looping over query tiles of BM rows double-buffered
 // in LDS (stage buffers are separate arrays so the compiler can tell the tile being
 // read from the one being written by the DMA).
-template <typename T, int D, int BM, int OCC>
+template <typename T, int D, int BM, int KG, int OCC>
 __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dkdv(
     const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
     const T* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Dv,
@@ -509,47 +680,63 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dkdv(
   Dv += bh * Sq;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int h = lane >> 5, l32 = lane & 31;
-  const int64_t kblk = tile * 128;
-  const int64_t key = kblk + wave * 32 + l32;  // this lane's key (C-tile column)
+  const int64_t kblk = tile * (128 * KG);
+  const int64_t kw = kblk + wave * (32 * KG);  // first key of this wave
   const float sl2 = scale * kLog2e;
-  // A key lane past Sk reads a clamped row: it only feeds dK/dV rows of that key,
-  // which are never stored.
-  const int64_t kc = key < Sk ? key : Sk - 1;
-  typename Vec8<T>::type kf[DK], vf[DK];
+  // Lane l32 of key group j holds key kw + 32j + l32 (C-tile column).  A key past Sk
+  // reads a clamped row: it only feeds dK/dV rows of that key, which are never stored.
+  typename Vec8<T>::type kf[KG][DK], vf[KG][DK];
 #pragma unroll
-  for (int ks = 0; ks < DK; ++ks) {
-    kf[ks] = ld8(K + kc * D + ks * 16 + h * 8);
-    vf[ks] = ld8(V + kc * D + ks * 16 + h * 8);
-  }
-  f32x16 dk[DT], dv[DT];
+  for (int j = 0; j < KG; ++j) {
+    const int64_t key = kw + 32 * j + l32;
+    const int64_t kc = key < Sk ? key : Sk - 1;
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      dk[dt][r] = 0.f;
-      dv[dt][r] = 0.f;
+    for (int ks = 0; ks < DK; ++ks) {
+      kf[j][ks] = ld8(K + kc * D + ks * 16 + h * 8);
+      vf[j][ks] = ld8(V + kc * D + ks * 16 + h * 8);
     }
+  }
+  f32x16 dk[KG][DT], dv[KG][DT];
+#pragma unroll
+  for (int j = 0; j < KG; ++j)
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        dk[j][dt][r] = 0.f;
+        dv[j][dt][r] = 0.f;
+      }
   LaneOffs<D> o;
   o.init(lane);
+  DmaPlan<T, D, BM> plan;
+  plan.init(lane, wave);
   // causal: queries below the first key of this block contribute nothing
   const int64_t qstart = causal ? (kblk / BM) * BM : 0;
   // log2-scaled LSE (+inf past Sq: P = 0 for padded rows) and scale*D of one tile
-  float pl = 0.f, pd = 0.f;
+  // LSE and D of one tile's rows (+inf / 0 past Sq, so P = 0 for padded rows).  The
+  // two global loads are issued before the tile's DMA and converted only when stored
+  // to LDS after the current tile's compute: vector-memory loads retire in issue order,
+  // so a use right behind the DMA would wait for the whole DMA.
+  float lv = 0.f, dd = 0.f;
+  bool lok = false;
   auto lsed = [&](int64_t q0) {
     const int64_t qq = q0 + (threadIdx.x % BM);
     const int64_t qqc = qq < Sq ? qq : Sq - 1;  // load unconditionally, select after
-    const float lv = LSE[qqc], dd = Dv[qqc];
-    pl = qq < Sq ? lv * kLog2e : INFINITY;
-    pd = qq < Sq ? dd * scale : 0.f;
+    lv = LSE[qqc];
+    dd = Dv[qqc];
+    lok = qq < Sq;
+  };
+  auto put = [&](float* lse_s, float* dvs_s) {
+    if (threadIdx.x < BM) {
+      lse_s[threadIdx.x] = lok ? lv * kLog2e : INFINITY;
+      dvs_s[threadIdx.x] = lok ? dd * scale : 0.f;
+    }
   };
   if (qstart < Sq) {
-    tile_dma<T, D, BM>(Q, qstart, Sq, q0s);
-    tile_dma<T, D, BM>(dO, qstart, Sq, do0s);
     lsed(qstart);
-    if (threadIdx.x < BM) {
-      lse0[threadIdx.x] = pl;
-      dvs0[threadIdx.x] = pd;
-    }
+    plan.copy(Q, qstart, Sq, q0s);
+    plan.copy(dO, qstart, Sq, do0s);
+    put(lse0, dvs0);
   }
   for (int64_t q0 = qstart; q0 < Sq; q0 += 2 * BM) {
     // stage 0 holds tile q0; stage 1 is free (its last readers passed the barrier)
@@ -557,40 +744,36 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dkdv(
     __syncthreads();
     const bool more1 = q0 + BM < Sq;
     if (more1) {
-      tile_dma<T, D, BM>(Q, q0 + BM, Sq, q1s);
-      tile_dma<T, D, BM>(dO, q0 + BM, Sq, do1s);
       lsed(q0 + BM);
+      plan.copy(Q, q0 + BM, Sq, q1s);
+      plan.copy(dO, q0 + BM, Sq, do1s);
     }
-    dkdv_tile<T, D, BM>(q0s, do0s, lse0, dvs0, (int)(kblk - q0) + wave * 32, causal, h, l32, o,
-                        kf, vf, dk, dv, sl2, scale);
+    dkdv_tile<T, D, BM, KG>(q0s, do0s, lse0, dvs0, (int)(kw - q0), causal, h, l32, o, kf, vf,
+                            dk, dv, sl2, scale);
     if (!more1) break;
-    if (threadIdx.x < BM) {
-      lse1[threadIdx.x] = pl;
-      dvs1[threadIdx.x] = pd;
-    }
+    put(lse1, dvs1);
     // stage 1 holds tile q0 + BM
     dma_wait();
     __syncthreads();
     const bool more2 = q0 + 2 * BM < Sq;
     if (more2) {
-      tile_dma<T, D, BM>(Q, q0 + 2 * BM, Sq, q0s);
-      tile_dma<T, D, BM>(dO, q0 + 2 * BM, Sq, do0s);
       lsed(q0 + 2 * BM);
+      plan.copy(Q, q0 + 2 * BM, Sq, q0s);
+      plan.copy(dO, q0 + 2 * BM, Sq, do0s);
     }
-    dkdv_tile<T, D, BM>(q1s, do1s, lse1, dvs1, (int)(kblk - q0 - BM) + wave * 32, causal, h, l32,
-                        o, kf, vf, dk, dv, sl2, scale);
+    dkdv_tile<T, D, BM, KG>(q1s, do1s, lse1, dvs1, (int)(kw - q0 - BM), causal, h, l32, o, kf,
+                            vf, dk, dv, sl2, scale);
     if (!more2) break;
-    if (threadIdx.x < BM) {
-      lse0[threadIdx.x] = pl;
-      dvs0[threadIdx.x] = pd;
-    }
+    put(lse0, dvs0);
   }
   // C tiles: rows = keys of this wave, cols = d
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt) {
-    store_c_tile<T>(dK, D, kblk + wave * 32, Sk, dt * 32 + l32, dk[dt], 1.f, accumulate, h);
-    store_c_tile<T>(dV, D, kblk + wave * 32, Sk, dt * 32 + l32, dv[dt], 1.f, accumulate, h);
-  }
+  for (int j = 0; j < KG; ++j)
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      store_c_tile<T>(dK, D, kw + 32 * j, Sk, dt * 32 + l32, dk[j][dt], 1.f, accumulate, h);
+      store_c_tile<T>(dV, D, kw + 32 * j, Sk, dt * 32 + l32, dv[j][dt], 1.f, accumulate, h);
+    }
 }
 
 // One 32-key x 32-query sub-tile of the dQ kernel for one wave (lane = query).
@@ -641,7 +824,7 @@ __device__ __forceinline__ void dq_tile(const char* ks, const char* vs, int64_t 
                                         f32x16 (&acc)[D / 32], float sl2, float scale, float lq,
                                         float dqs) {
   constexpr int RB = D * 2;
-#pragma unroll 1
+#pragma unroll
   for (int kt = 0; kt < BN / 32; ++kt) {
     const int64_t kb0 = k0 + kt * 32;
     if (kb0 >= Sk) break;
@@ -710,19 +893,21 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dq(
     for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
   LaneOffs<D> o;
   o.init(lane);
+  DmaPlan<T, D, BN> plan;
+  plan.init(lane, wave);
   int64_t kend = Sk;
   if (causal) kend = (qblk + 128 < Sk) ? qblk + 128 : Sk;
   if (kend > 0) {
-    tile_dma<T, D, BN>(K, 0, Sk, k0s);
-    tile_dma<T, D, BN>(V, 0, Sk, v0s);
+    plan.copy(K, 0, Sk, k0s);
+    plan.copy(V, 0, Sk, v0s);
   }
   for (int64_t k0 = 0; k0 < kend; k0 += 2 * BN) {
     dma_wait();
     __syncthreads();
     const bool more1 = k0 + BN < kend;
     if (more1) {
-      tile_dma<T, D, BN>(K, k0 + BN, Sk, k1s);
-      tile_dma<T, D, BN>(V, k0 + BN, Sk, v1s);
+      plan.copy(K, k0 + BN, Sk, k1s);
+      plan.copy(V, k0 + BN, Sk, v1s);
     }
     dq_tile<T, D, BN>(k0s, v0s, k0, Sk, (int)(qblk - k0) + wave * 32, causal, h, l32, o, qf, of,
                       acc, sl2, scale, lq, dqs);
@@ -731,8 +916,8 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dq(
     __syncthreads();
     const bool more2 = k0 + 2 * BN < kend;
     if (more2) {
-      tile_dma<T, D, BN>(K, k0 + 2 * BN, Sk, k0s);
-      tile_dma<T, D, BN>(V, k0 + 2 * BN, Sk, v0s);
+      plan.copy(K, k0 + 2 * BN, Sk, k0s);
+      plan.copy(V, k0 + 2 * BN, Sk, v0s);
     }
     dq_tile<T, D, BN>(k1s, v1s, k0 + BN, Sk, (int)(qblk - k0 - BN) + wave * 32, causal, h, l32,
                       o, qf, of, acc, sl2, scale, lq, dqs);
@@ -757,10 +942,10 @@ int fwd_t(const void* q, const void* k, const void* v, void* o, float* lse, int6
 // key rows of the dQ kernel, and the workgroups per CU each is compiled for.
 template <int D> struct BwdCfg;
 template <> struct BwdCfg<64> {
-  static constexpr int BM = 128, OCC_KV = 2, BN = 64, OCC_Q = 3;
+  static constexpr int BM = 128, KG = 1, OCC_KV = 2, BN = 64, OCC_Q = 3;
 };
 template <> struct BwdCfg<128> {
-  static constexpr int BM = 128, OCC_KV = 1, BN = 64, OCC_Q = 2;
+  static constexpr int BM = 128, KG = 1, OCC_KV = 1, BN = 64, OCC_Q = 2;
 };
 
 template <typename T, int D>
@@ -770,9 +955,9 @@ int bwd_t(const void* q, const void* k, const void* v, const void* o, const void
   const int64_t rows = BH * Sq;
   k_fa_bwd_prep<T, D><<<(unsigned)((rows + 15) / 16), kThreads, 0, s>>>(
       (const T*)o, (const T*)dout, dvec, rows);
-  dim3 gkv((unsigned)((Sk + 127) / 128), (unsigned)BH);
   using C = BwdCfg<D>;
-  k_fa_bwd_dkdv<T, D, C::BM, C::OCC_KV><<<gkv, kThreads, 0, s>>>((const T*)q, (const T*)k, (const T*)v,
+  dim3 gkv((unsigned)((Sk + 128 * C::KG - 1) / (128 * C::KG)), (unsigned)BH);
+  k_fa_bwd_dkdv<T, D, C::BM, C::KG, C::OCC_KV><<<gkv, kThreads, 0, s>>>((const T*)q, (const T*)k, (const T*)v,
                                                (const T*)dout, lse, dvec, (T*)dk, (T*)dv, Sq, Sk,
                                                scale, causal, acc);
   dim3 gq((unsigned)((Sq + 127) / 128), (unsigned)BH);
