@@ -815,6 +815,87 @@ __device__ __forceinline__ void dq_sub(const char* ks, const char* vs, const Lan
   }
 }
 
+// Hand-ordered dq_sub (same scheme as dkdv_sub_pipe): K then V fragment reads run PF
+// ahead of their MFMAs, exp(S) is spread over the dP MFMAs, the dS of the second half
+// is computed behind the first half's dQ MFMAs, and K^T transpose reads are issued
+// during the dP phase.
+template <typename T, int D, bool MASK>
+__device__ __forceinline__ void dq_sub_pipe(const char* ks, const char* vs,
+                                            const LaneOffs<D>& o,
+                                            const typename Vec8<T>::type (&qf)[D / 16],
+                                            const typename Vec8<T>::type (&of)[D / 16],
+                                            f32x16 (&acc)[D / 32], float sl2, float scale,
+                                            float lq, float dqs, int thr) {
+  using V8 = typename Vec8<T>::type;
+  constexpr int DK = D / 16, DT = D / 32, RB = D * 2, PF = 4;
+  constexpr int NB = 2 * DT;
+  constexpr int EA = 16 / DK;
+  auto tr = [&](int n) {
+    const char* b = ks + (n / DT) * 16 * RB;
+    return lds_tr<T>(b + o.t[0][n % DT], b + o.t[1][n % DT]);
+  };
+  V8 ka[DK], va[DK], bk[NB];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) ka[i] = lds_a<T>(ks + o.a[i]);
+  f32x16 sa, dpa;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    sa[r] = 0.f;
+    dpa[r] = 0.f;
+  }
+  TG_SB();
+#pragma unroll
+  for (int k = 0; k < DK; ++k) {
+    sa = mfma(ka[k], qf[k], sa);
+    const int n = k + PF;
+    if (n < DK) ka[n] = lds_a<T>(ks + o.a[n]);
+    else va[n - DK] = lds_a<T>(vs + o.a[n - DK]);
+    TG_SB();
+  }
+  float p[16];
+  auto expo = [&](int r) {
+    float pv = fexp2(fmaf(sa[r], sl2, -lq));
+    if (MASK) pv = (8 * (r >> 2) + (r & 3) > thr) ? 0.f : pv;
+    p[r] = pv;
+  };
+  int nk = 0;
+#pragma unroll
+  for (int k = 0; k < DK; ++k) {
+    dpa = mfma(va[k], of[k], dpa);
+    const int n = k + PF;
+    if (n < DK) va[n] = lds_a<T>(vs + o.a[n]);
+    else if (nk < NB) { bk[nk] = tr(nk); ++nk; }
+    if (k > 0)
+#pragma unroll
+      for (int e = 0; e < EA; ++e) expo((k - 1) * EA + e);
+    TG_SB();
+  }
+#pragma unroll
+  for (int e = 0; e < EA; ++e) expo((DK - 1) * EA + e);
+  float ds[16];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) ds[r] = p[r] * fmaf(dpa[r], scale, -dqs);
+  const V8 d0 = pack8<T>(&ds[0]);
+  TG_SB();
+  constexpr int EB = 8 / DT;
+  V8 d1;
+#pragma unroll
+  for (int n = 0; n < NB; ++n) {
+    while (nk <= n) { bk[nk] = tr(nk); ++nk; }
+    acc[n % DT] = mfma(n < DT ? d0 : d1, bk[n], acc[n % DT]);
+    if (nk < NB) { bk[nk] = tr(nk); ++nk; }
+    if (n < DT) {
+#pragma unroll
+      for (int e = 0; e < EB; ++e) {
+        const int r = 8 + n * EB + e;
+        ds[r] = p[r] * fmaf(dpa[r], scale, -dqs);
+      }
+      if (n == DT - 1) d1 = pack8<T>(&ds[8]);
+    }
+    TG_SB();
+  }
+}
+
 // The BN/32 sub-tiles of one staged key tile starting at key k0.
 template <typename T, int D, int BN>
 __device__ __forceinline__ void dq_tile(const char* ks, const char* vs, int64_t k0, int64_t Sk,
@@ -841,9 +922,11 @@ __device__ __forceinline__ void dq_tile(const char* ks, const char* vs, int64_t 
         const int kb = (int)(Sk - kb0) - 4 * h - 1;
         thr = kb < thr ? kb : thr;
       }
-      dq_sub<T, D, true>(k, v, o, qf, of, acc, sl2, scale, lq, dqs, thr);
+      if constexpr (kPipe) dq_sub_pipe<T, D, true>(k, v, o, qf, of, acc, sl2, scale, lq, dqs, thr);
+      else dq_sub<T, D, true>(k, v, o, qf, of, acc, sl2, scale, lq, dqs, thr);
     } else {
-      dq_sub<T, D, false>(k, v, o, qf, of, acc, sl2, scale, lq, dqs, 0);
+      if constexpr (kPipe) dq_sub_pipe<T, D, false>(k, v, o, qf, of, acc, sl2, scale, lq, dqs, 0);
+      else dq_sub<T, D, false>(k, v, o, qf, of, acc, sl2, scale, lq, dqs, 0);
     }
   }
 }
