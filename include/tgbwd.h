@@ -55,6 +55,12 @@ int tg_silu_fwd(int dtype, const void* x, void* y, int64_t n, void* stream);
  * The generic `parent.grad += g` accumulation of the closures (_core.py:945-966). */
 int tg_axpby(int dtype_x, const void* x, int dtype_y, void* y, int64_t n, float alpha,
              float beta, void* stream);
+/* z = alpha*x + beta*y with z of y's dtype (z may equal y).  The out-of-place form of
+ * the same accumulation, used when the gradient buffer being added to is shared with
+ * another node (copy-on-write; the reference's `+=` creates a new array there too,
+ * _core.py:945-966). */
+int tg_axpbyz(int dtype_x, const void* x, int dtype_y, const void* y, void* z, int64_t n,
+              float alpha, float beta, void* stream);
 /* Fill with a constant by a kernel (grad zeroing; graph-capture safe). */
 int tg_fill(int dtype, void* y, int64_t n, float value, void* stream);
 

@@ -199,16 +199,18 @@ int dispatch_fwd(int dtype, const void* x, void* y, int64_t n, void* stream) {
 }
 
 // ---------------------------------------------------------------------------
-// y = alpha*x + beta*y   (beta == 0: y is not read).  x and y may differ in dtype;
-// arithmetic is fp32.  Used for `grad += g` with a dtype cast and for scaling.
+// z = alpha*x + beta*y   (beta == 0: y is not read; z == y is the in-place update).
+// x and y may differ in dtype, z has y's; arithmetic is fp32.  Used for `grad += g`
+// with a dtype cast, for scaling, and for the out-of-place accumulation into a
+// gradient buffer that another node shares.
 template <typename TX, typename TY>
-__global__ __launch_bounds__(kThreads) void k_axpby(const TX* __restrict__ x, TY* __restrict__ y,
-                                                    float alpha, float beta, int64_t n) {
+__global__ __launch_bounds__(kThreads) void k_axpby(const TX* __restrict__ x, const TY* y,
+                                                    TY* z, float alpha, float beta, int64_t n) {
   const int64_t stride = (int64_t)gridDim.x * kThreads;
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
     float v = alpha * tg_to_float(x[i]);
     if (beta != 0.f) v += beta * tg_to_float(y[i]);
-    y[i] = tg_from_float<TY>(v);
+    z[i] = tg_from_float<TY>(v);
   }
 }
 
@@ -237,8 +239,8 @@ __device__ __forceinline__ void st8f(T* p, const float (&f)[8]) {
 
 // Vector form: n8 groups of 8 elements, then a scalar tail in block 0.
 template <typename TX, typename TY, bool READ_Y>
-__global__ __launch_bounds__(kThreads) void k_axpby8(const TX* __restrict__ x, TY* __restrict__ y,
-                                                     float alpha, float beta, int64_t n8,
+__global__ __launch_bounds__(kThreads) void k_axpby8(const TX* __restrict__ x, const TY* y,
+                                                     TY* z, float alpha, float beta, int64_t n8,
                                                      int64_t n) {
   const int64_t stride = (int64_t)gridDim.x * kThreads;
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n8; i += stride) {
@@ -247,36 +249,40 @@ __global__ __launch_bounds__(kThreads) void k_axpby8(const TX* __restrict__ x, T
     if (READ_Y) ld8f(y + i * 8, b);
 #pragma unroll
     for (int j = 0; j < 8; ++j) a[j] = READ_Y ? alpha * a[j] + beta * b[j] : alpha * a[j];
-    st8f(y + i * 8, a);
+    st8f(z + i * 8, a);
   }
   if (blockIdx.x == 0) {
     for (int64_t i = n8 * 8 + threadIdx.x; i < n; i += kThreads) {
       float v = alpha * tg_to_float(x[i]);
       if (READ_Y) v += beta * tg_to_float(y[i]);
-      y[i] = tg_from_float<TY>(v);
+      z[i] = tg_from_float<TY>(v);
     }
   }
 }
 
 template <typename TX, typename TY>
-int launch_axpby(const void* x, void* y, float a, float b, int64_t n, hipStream_t s) {
-  if (tg_aligned16(x) && tg_aligned16(y)) {
+int launch_axpby(const void* x, const void* y, void* z, float a, float b, int64_t n,
+                 hipStream_t s) {
+  if (tg_aligned16(x) && tg_aligned16(y) && tg_aligned16(z)) {
     const int64_t n8 = n / 8;
     int64_t blocks = (n8 + kThreads - 1) / kThreads;
     const int64_t cap = (int64_t)tg_num_cus() * 16;
     if (blocks > cap) blocks = cap;
     if (blocks < 1) blocks = 1;
     if (b != 0.f)
-      k_axpby8<TX, TY, true><<<(unsigned)blocks, kThreads, 0, s>>>((const TX*)x, (TY*)y, a, b, n8, n);
+      k_axpby8<TX, TY, true><<<(unsigned)blocks, kThreads, 0, s>>>((const TX*)x, (const TY*)y,
+                                                                   (TY*)z, a, b, n8, n);
     else
-      k_axpby8<TX, TY, false><<<(unsigned)blocks, kThreads, 0, s>>>((const TX*)x, (TY*)y, a, b, n8, n);
+      k_axpby8<TX, TY, false><<<(unsigned)blocks, kThreads, 0, s>>>((const TX*)x, (const TY*)y,
+                                                                    (TY*)z, a, b, n8, n);
     return tg_check_launch("tg_axpby");
   }
   int64_t blocks = (n + kThreads * 4 - 1) / (kThreads * 4);
   const int64_t cap = (int64_t)tg_num_cus() * 32;
   if (blocks > cap) blocks = cap;
   if (blocks < 1) blocks = 1;
-  k_axpby<TX, TY><<<(unsigned)blocks, kThreads, 0, s>>>((const TX*)x, (TY*)y, a, b, n);
+  k_axpby<TX, TY><<<(unsigned)blocks, kThreads, 0, s>>>((const TX*)x, (const TY*)y, (TY*)z, a, b,
+                                                       n);
   return tg_check_launch("tg_axpby");
 }
 
@@ -306,14 +312,15 @@ TG_EXPORT int tg_silu_fwd(int dtype, const void* x, void* y, int64_t n, void* st
   return dispatch_fwd<OP_SILU>(dtype, x, y, n, stream);
 }
 
-TG_EXPORT int tg_axpby(int dtype_x, const void* x, int dtype_y, void* y, int64_t n, float alpha,
-                       float beta, void* stream) {
-  TG_REQUIRE(n >= 0, "tg_axpby: negative n");
+TG_EXPORT int tg_axpbyz(int dtype_x, const void* x, int dtype_y, const void* y, void* z,
+                        int64_t n, float alpha, float beta, void* stream) {
+  TG_REQUIRE(n >= 0, "tg_axpbyz: negative n");
   if (n == 0) return TG_OK;
-  TG_REQUIRE(x && y, "tg_axpby: null pointer");
+  TG_REQUIRE(x && z && (y || beta == 0.f), "tg_axpbyz: null pointer");
+  if (!y) y = z;
   hipStream_t s = tg_stream(stream);
 #define TG_AXPBY_CASE(DX, TX, DY, TY) \
-  if (dtype_x == DX && dtype_y == DY) return launch_axpby<TX, TY>(x, y, alpha, beta, n, s);
+  if (dtype_x == DX && dtype_y == DY) return launch_axpby<TX, TY>(x, y, z, alpha, beta, n, s);
   TG_AXPBY_CASE(TG_F32, float, TG_F32, float)
   TG_AXPBY_CASE(TG_F32, float, TG_F16, tg_half)
   TG_AXPBY_CASE(TG_F32, float, TG_BF16, tg_bf16)
@@ -324,6 +331,12 @@ TG_EXPORT int tg_axpby(int dtype_x, const void* x, int dtype_y, void* y, int64_t
 #undef TG_AXPBY_CASE
   tg_set_error("tg_axpby: unsupported dtype pair (%d,%d)", dtype_x, dtype_y);
   return TG_ERR_UNSUPPORTED;
+}
+
+TG_EXPORT int tg_axpby(int dtype_x, const void* x, int dtype_y, void* y, int64_t n, float alpha,
+                       float beta, void* stream) {
+  TG_REQUIRE(y || n == 0, "tg_axpby: null pointer");
+  return tg_axpbyz(dtype_x, x, dtype_y, y, y, n, alpha, beta, stream);
 }
 
 // Fill n elements with `value` (a kernel, not a memset node, so it is safe to

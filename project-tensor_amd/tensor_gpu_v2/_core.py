@@ -49,7 +49,7 @@ def _to_device_tensor(data, dtype):
 class Tensor:
     """Autograd tensor on the MI355X (reference: _core.py:609-1467)."""
 
-    __slots__ = ("data", "_g", "_gz", "_backward", "_prev", "_op", "label", "_device",
+    __slots__ = ("data", "_g", "_gz", "_gsh", "_backward", "_prev", "_op", "label", "_device",
                  "_requires_grad", "_is_view", "_base", "_grad_fn", "__weakref__",
                  "_tied_source", "_tied_transpose")
 
@@ -66,6 +66,7 @@ class Tensor:
         rg = bool(requires_grad) and cfg._grad_enabled
         self._g = None
         self._gz = rg  # implicit zero gradient
+        self._gsh = False  # _g may alias another node's gradient (copy-on-write)
         self._backward = _noop
         self._prev = _unique(_children)
         self._op = _op
@@ -87,6 +88,7 @@ class Tensor:
         rg = requires_grad and cfg._grad_enabled
         out._g = None
         out._gz = rg
+        out._gsh = False
         out._backward = _noop
         out._prev = _unique(children) if rg else ()
         out._op = op
@@ -141,11 +143,14 @@ class Tensor:
         if self._gz:
             self._g = self._new_buf(0)
             self._gz = False
+        elif self._gsh:
+            self._privatize()
         return self._g
 
     @grad.setter
     def grad(self, value):
         self._gz = False
+        self._gsh = False
         if value is None:
             self._g = None
             return
@@ -163,10 +168,18 @@ class Tensor:
         return self._gz or self._g is not None
 
     def _grad_out(self):
-        """Gradient flowing into this node's closure (zeros if nothing arrived)."""
+        """Gradient flowing into this node's closure (zeros if nothing arrived).
+        Read-only: it may be shared with other nodes."""
         if self._gz:
             return self._new_buf(0)
         return self._g
+
+    def _privatize(self):
+        """Give this node its own copy of a gradient buffer it shares."""
+        buf = self._new_buf()
+        L.axpby(self._g, buf, 1.0, 0.0)
+        self._g = buf
+        self._gsh = False
 
     def _grad_target(self):
         """(buffer, accumulate) for a kernel that adds this tensor's gradient."""
@@ -174,14 +187,35 @@ class Tensor:
             self._g = self._new_buf()
             self._gz = False
             return self._g, False
+        if self._gsh:
+            self._privatize()
         return self._g, True
 
-    def _accumulate_unb(self, g):
+    def _share_grad(self, donor, g):
+        """First gradient of this node is `g`, a read-only view of donor's gradient
+        buffer (the reshape/view/add pass-through).  Adopted without a copy; both
+        nodes are marked shared, so the first in-place write to either one copies
+        (out of place for an accumulation, which moves no more bytes than the
+        in-place one would)."""
+        if not self._gz or g.dtype != self.data.dtype or not g.is_contiguous():
+            self._accumulate(g)
+            return
+        if g.shape != self.data.shape:
+            g = g.reshape(self.data.shape)
+        self._g = g
+        self._gz = False
+        self._gsh = True
+        donor._gsh = True
+
+    def _accumulate_unb(self, g, donor=None):
         """self.grad += unbroadcast(g).  The reduced tensor is fresh (owned) unless no
-        reduction was needed, in which case it is `g` itself and must not be adopted as
-        this tensor's buffer (it is another node's gradient)."""
+        reduction was needed, in which case it is `g` itself: another node's gradient,
+        adopted as a shared buffer when the donor is known, else copied."""
         u = _unbroadcast_dev(g, self.data.shape, self.data.dtype)
-        self._accumulate(u, owned=u is not g)
+        if u is g and donor is not None:
+            self._share_grad(donor, g)
+        else:
+            self._accumulate(u, owned=u is not g)
 
     def _accumulate(self, g, owned=False):
         """self.grad += g (g: torch tensor broadcast-compatible in shape, any float dtype)."""
@@ -203,9 +237,17 @@ class Tensor:
             return
         if (g.is_contiguous() and self._g.is_contiguous() and g.dtype in L._TORCH_TO_CODE
                 and self._g.dtype in L._TORCH_TO_CODE):
-            L.axpby(g, self._g, 1.0, 1.0)
+            if self._gsh:
+                self._g = L.axpbyz(g, self._g, 1.0, 1.0)
+                self._gsh = False
+            else:
+                L.axpby(g, self._g, 1.0, 1.0)
         else:
-            self._g.add_(g.to(self._g.dtype))
+            if self._gsh:
+                self._g = self._g + g.to(self._g.dtype)
+                self._gsh = False
+            else:
+                self._g.add_(g.to(self._g.dtype))
 
     # ------------------------------------------------------------ properties
     @property
@@ -278,6 +320,7 @@ class Tensor:
         if self._has_grad():
             self._g = None
             self._gz = True
+            self._gsh = False
 
     def __repr__(self):
         rg = f", requires_grad={self._requires_grad}" if self._requires_grad else ""
@@ -303,9 +346,9 @@ class Tensor:
             def _backward():
                 g = out._grad_out()
                 if self._has_grad():
-                    self._accumulate_unb(g)
+                    self._accumulate_unb(g, out)
                 if other._has_grad():
-                    other._accumulate_unb(g)
+                    other._accumulate_unb(g, out)
             out._backward = _backward
         return out
 
@@ -565,7 +608,7 @@ class Tensor:
 
         def _backward():
             if self._has_grad() and out._has_grad():
-                self._accumulate(back(out._grad_out()))
+                self._share_grad(out, back(out._grad_out()))
         out._backward = _backward
         return out
 
@@ -613,7 +656,7 @@ class Tensor:
         if out._requires_grad:
             def _backward():
                 if self._has_grad():
-                    self._accumulate(out._grad_out().reshape(orig))
+                    self._share_grad(out, out._grad_out().reshape(orig))
             out._backward = _backward
         return out
 
@@ -622,7 +665,7 @@ class Tensor:
         if out._requires_grad:
             def _backward():
                 if self._has_grad():
-                    self._accumulate(out._grad_out().squeeze(dim))
+                    self._share_grad(out, out._grad_out().squeeze(dim))
             out._backward = _backward
         return out
 
@@ -702,11 +745,13 @@ class Tensor:
             if not self._has_grad():
                 self._g = g.expand(self.data.shape).clone()
                 self._gz = False
+                self._gsh = False
             else:
                 self._accumulate(g.expand(self.data.shape).contiguous())
         elif self._gz or self._g is None or not bool(torch.any(self._g != 0)):
             self._g = self._new_buf(1)
             self._gz = False
+            self._gsh = False
         for v in reversed(topo):
             v._backward()
             v._backward = _noop

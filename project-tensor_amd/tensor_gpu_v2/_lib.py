@@ -40,6 +40,7 @@ SIGNATURES = {
     "tg_gelu_fwd": (_i32, [_i32, _vp, _vp, _i64, _vp]),
     "tg_silu_fwd": (_i32, [_i32, _vp, _vp, _i64, _vp]),
     "tg_axpby": (_i32, [_i32, _vp, _i32, _vp, _i64, _f32, _f32, _vp]),
+    "tg_axpbyz": (_i32, [_i32, _vp, _i32, _vp, _vp, _i64, _f32, _f32, _vp]),
     "tg_fill": (_i32, [_i32, _vp, _i64, _f32, _vp]),
     "tg_softmax_fwd": (_i32, [_i32, _vp, _vp, _i64, _i64, _vp]),
     "tg_softmax_bwd": (_i32, [_i32, _vp, _vp, _vp, _i64, _i64, _i32, _vp]),
@@ -197,6 +198,22 @@ def axpby(x, y, alpha=1.0, beta=1.0):
     _check("tg_axpby", load().tg_axpby(dtype_code(x), ptr(x), dtype_code(y), ptr(y), y.numel(),
                                        float(alpha), float(beta), stream_handle()))
     return y
+
+
+def axpbyz(x, y, alpha=1.0, beta=1.0, out=None):
+    """out = alpha*x + beta*y (contiguous, same numel; out has y's dtype)."""
+    _dev(x, "x")
+    _dev(y, "y")
+    if x.numel() != y.numel():
+        raise ValueError(f"axpbyz: numel mismatch {x.numel()} vs {y.numel()}")
+    if out is None:
+        out = torch.empty(y.shape, dtype=y.dtype, device=y.device)
+    elif out.dtype != y.dtype or out.numel() != y.numel() or not out.is_contiguous():
+        raise ValueError("axpbyz: out must be contiguous with y's dtype and numel")
+    ensure_device(y.device.index)
+    _check("tg_axpbyz", load().tg_axpbyz(dtype_code(x), ptr(x), dtype_code(y), ptr(y), ptr(out),
+                                         y.numel(), float(alpha), float(beta), stream_handle()))
+    return out
 
 
 def fill(y, value):

@@ -408,3 +408,47 @@ def test_residual_add_grads_not_aliased(tg):
     ((rt + xt).sum() + (rt * rt).sum()).backward()
     assert_close(x.grad, xt.grad.numpy(), RTOL_F32_MM, "x grad")
     assert_close(w.grad, wt.grad.numpy(), RTOL_F32_MM, "w grad")
+
+
+def test_view_and_add_grads_copy_on_write(tg):
+    """Views and same-shape adds hand their gradient buffer on without a copy; every
+    later write to either side must leave the other's values intact: a second graph
+    accumulating into the same leaf, in-place edits of a read .grad, x + x."""
+    rng = np.random.default_rng(21)
+    x_np = rng.standard_normal((4, 6)).astype(np.float32)
+    c_np = rng.standard_normal((6, 4)).astype(np.float32)
+    x = tg.Tensor(x_np)
+    c = tg.Tensor(c_np, requires_grad=False)
+
+    def graph():
+        y = x.reshape(6, 4)
+        a = y + y * c          # y: shared from the add, then accumulated by the mul
+        b = a.reshape(24)      # a: shares b's gradient
+        return y, a, (b * b).sum()
+
+    y1, a1, l1 = graph()
+    l1.backward()
+    xt = torch.tensor(x_np.astype(np.float64), requires_grad=True)
+    yt = xt.reshape(6, 4)
+    yt.retain_grad()
+    at = yt + yt * torch.tensor(c_np.astype(np.float64))
+    at.retain_grad()
+    (at.reshape(24) ** 2).sum().backward()
+    gx, gy, ga = xt.grad.numpy(), yt.grad.numpy(), at.grad.numpy()
+    assert_close(x.grad, gx, RTOL_F32, "x grad")
+    assert_close(y1.grad, gy, RTOL_F32, "y grad")
+    assert_close(a1.grad, ga, RTOL_F32, "a grad")
+    # a second graph accumulates into x.grad; the first graph's intermediates keep theirs
+    y2, a2, l2 = graph()
+    l2.backward()
+    assert_close(x.grad, 2 * gx, RTOL_F32, "x grad after two graphs")
+    assert_close(y1.grad, gy, RTOL_F32, "first graph's y grad")
+    assert_close(a1.grad, ga, RTOL_F32, "first graph's a grad")
+    # editing one node's grad in place leaves its sharers alone
+    y2.grad.mul_(0.0)
+    assert_close(a2.grad, ga, RTOL_F32, "a grad after editing y grad")
+    assert_close(x.grad, 2 * gx, RTOL_F32, "x grad after editing y grad")
+    # x + x: both operands are the same tensor
+    z = tg.Tensor(x_np)
+    (z + z).reshape(24).sum().backward()
+    assert_close(z.grad, np.full((4, 6), 2.0, np.float32), 0.0, "x + x")
