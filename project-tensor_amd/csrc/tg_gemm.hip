@@ -449,6 +449,25 @@ typedef short v4i16_g __attribute__((ext_vector_type(4)));
 #define TG_GLB_G __attribute__((address_space(1)))
 
 constexpr int V3_BK = 64;
+#ifndef TG_GEMM_HUGE
+#define TG_GEMM_HUGE 4
+#endif
+#ifndef TG_GEMM_BIG4
+#define TG_GEMM_BIG4 0
+#endif
+#ifndef TG_GEMM_PIPE
+#define TG_GEMM_PIPE 1
+#endif
+constexpr bool kGemmPipe = TG_GEMM_PIPE;
+#ifndef TG_GEMM_LDS_EPI
+#define TG_GEMM_LDS_EPI 1
+#endif
+constexpr bool kGemmLdsEpi = TG_GEMM_LDS_EPI;
+// 256x256 blocks once there are kHugeTiles/4 of them per CU.
+constexpr int kHugeTiles = TG_GEMM_HUGE;
+// 256x128 blocks: 2x2 waves of 128x64 (TG_GEMM_BIG4) or 4x2 waves of 64x64.
+constexpr int kBigWGM = TG_GEMM_BIG4 ? 2 : 4, kBigWGN = 2, kBigSM = TG_GEMM_BIG4 ? 4 : 2,
+              kBigSN = 2;
 
 // XOR key of row r (CH 16-byte chunks per row): 16 consecutive rows get distinct
 // chunk positions and rows r..r+3 of a transpose read land in different 64-byte bank
@@ -464,26 +483,57 @@ template <int CH> __device__ __forceinline__ int v3_off(int r, int c) {
   return r * CH * 16 + ((c ^ v3_key<CH>(r)) << 4);
 }
 
-// DMA of an R x CW tile (CW elements per row) at (row0, col0) of a matrix with
-// leading dimension ld, by NW waves; rows >= nrows and columns >= ncols are clamped.
-template <typename T, int R, int CW, int NW>
-__device__ __forceinline__ void v3_dma(const T* __restrict__ g, int64_t ld, int64_t row0,
-                                       int64_t nrows, int64_t col0, int64_t ncols, char* lds) {
-  constexpr int CH = CW / 8, NI = R * CH / 64;
+// DMA of R x CW tiles (CW elements per row) of a matrix with leading dimension ld, by
+// NW waves.  One operand's tiles all start at the same row (KROWS false: rows are
+// m or n, fixed per block; the column is k) or at the same column (KROWS true: rows
+// are k, the column is m or n).  The clamp of rows or columns past the matrix edge
+// therefore depends only on the block, so each lane's byte offset within a tile is
+// computed once; a tile then costs one uniform pointer per wave instruction.  The
+// k extent needs no clamp (K % 64 == 0).
+template <typename T, int R, int CW, int NW, bool KROWS>
+struct V3Dma {
+  static constexpr int CH = CW / 8, NI = R * CH / 64, NPW = NI / NW;
   static_assert(NI % NW == 0, "tile must split evenly over the waves");
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t off[NPW];
+  // base0: first row (KROWS false) or first column (KROWS true) of the block; nlim:
+  // rows (resp. columns) of the matrix.
+  __device__ void init(int64_t ld, int64_t base0, int64_t nlim) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-  for (int i = wave; i < NI; i += NW) {
-    const int u = i * 64 + lane;
-    const int r = u / CH, c = (u % CH) ^ v3_key<CH>(r);
-    int64_t row = row0 + r;
-    row = row < nrows ? row : nrows - 1;
-    int64_t col = col0 + c * 8;
-    col = col + 8 <= ncols ? col : ncols - 8;
-    __builtin_amdgcn_global_load_lds((const TG_GLB_G void*)(g + row * ld + col),
-                                     (TG_LDS_G void*)(lds + i * 1024), 16, 0, 0);
+    for (int k = 0; k < NPW; ++k) {
+      const int u = (wave + k * NW) * 64 + lane;
+      const int r = u / CH, c = (u % CH) ^ v3_key<CH>(r);
+      int64_t e;
+      if (!KROWS) {
+        int64_t row = base0 + r;
+        row = row < nlim ? row : nlim - 1;
+        e = (row - base0) * ld + c * 8;
+      } else {
+        int64_t col = base0 + c * 8;
+        col = col + 8 <= nlim ? col : nlim - 8;
+        e = r * ld + (col - base0);
+      }
+      off[k] = (uint32_t)(e * (int64_t)sizeof(T));
+    }
   }
-}
+  // Copy the tile whose origin is soff bytes past base (both uniform): a raw buffer
+  // load into LDS takes the lane offset in a VGPR and the tile offset in an SGPR, so
+  // the copy costs no vector ALU work.  The resource spans [base, base + 2 GiB) (word
+  // 3: 32-bit untyped access, no swizzle; the gfx9 raw-buffer format).
+  __device__ __forceinline__ void copy(const T* base, uint32_t soff, char* lds) const {
+    // The buffer-resource type is compiled in the device pass only: the host pass of
+    // this compiler drops the launch stubs of kernel instantiations whose bodies hold it.
+#if defined(__HIP_DEVICE_COMPILE__)
+    const int wave = threadIdx.x >> 6;
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<T*>(base), (short)0, 0x7fffffff, 0x00020000);
+#pragma unroll
+    for (int k = 0; k < NPW; ++k)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (TG_LDS_G void*)(lds + (wave + k * NW) * 1024),
+                                               16, off[k], soff, 0, 0);
+#endif
+  }
+};
 
 // Fragment reader for one operand tile of EXT rows (m or n) and 64 k.
 //   KC: [EXT rows][64 k], 128-byte rows; else [64 k][EXT], EXT*2-byte rows.
@@ -566,24 +616,64 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_v3(
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
   // A is [M][K] (lda) or, transposed, [K][M]; B is [K][N] or, transposed, [N][K].
+  // Tile origins: k-contiguous operands start at (row m0|n0, column k0), the others
+  // at (row k0, column m0|n0); the clamps at the M / N edge are per block.
+  V3Dma<T, AKC ? TBM : 64, AKC ? 64 : TBM, NW, !AKC> da;
+  V3Dma<T, BKC ? TBN : 64, BKC ? 64 : TBN, NW, !BKC> db;
+  da.init(lda, m0, M);
+  db.init(ldb, n0, N);
+  const T* a_org = A + (AKC ? m0 * lda : m0);
+  const T* b_org = B + (BKC ? n0 * ldb : n0);
   auto dma = [&](int64_t k0, char* as, char* bs) {
-    if (AKC) v3_dma<T, TBM, 64, NW>(A, lda, m0, M, k0, K, as);
-    else v3_dma<T, 64, TBM, NW>(A, lda, k0, K, m0, M, as);
-    if (BKC) v3_dma<T, TBN, 64, NW>(B, ldb, n0, N, k0, K, bs);
-    else v3_dma<T, 64, TBN, NW>(B, ldb, k0, K, n0, N, bs);
+    da.copy(a_org, (uint32_t)((AKC ? k0 : k0 * lda) * (int64_t)sizeof(T)), as);
+    db.copy(b_org, (uint32_t)((BKC ? k0 : k0 * ldb) * (int64_t)sizeof(T)), bs);
   };
   auto mul = [&](const char* as, const char* bs) {
+    if constexpr (OCC == 1 && kGemmPipe) {
+      // One wave per SIMD: software pipeline.  The fragment reads of k-step ks+1 are
+      // issued between the MFMAs of k-step ks (sched_barrier keeps the order), so only
+      // the first k-step of a tile waits on LDS latency.
+      typename Vec8<T>::type fr[2][SM + SN];
+      auto rd = [&](int buf, int ks, int n) {
+        if (n < SM) fr[buf][n] = fa.get(as, wm, n, ks, l32);
+        else fr[buf][n] = fb.get(bs, wn, n - SM, ks, l32);
+      };
 #pragma unroll
-    for (int ks = 0; ks < V3_BK / 16; ++ks) {
-      typename Vec8<T>::type af[SM], bf[SN];
+      for (int n = 0; n < SM + SN; ++n) rd(0, 0, n);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 0; i < SM; ++i) af[i] = fa.get(as, wm, i, ks, l32);
+      for (int ks = 0; ks < V3_BK / 16; ++ks) {
+        const int cur = ks & 1;
+        int nr = 0;
 #pragma unroll
-      for (int j = 0; j < SN; ++j) bf[j] = fb.get(bs, wn, j, ks, l32);
+        for (int i = 0; i < SM; ++i)
 #pragma unroll
-      for (int i = 0; i < SM; ++i)
+          for (int j = 0; j < SN; ++j) {
+            mfma_v(fr[cur][i], fr[cur][SM + j], acc[i][j]);
+            if (ks + 1 < V3_BK / 16 && nr < SM + SN && (i * SN + j) % 2 == 1) {
+              rd(cur ^ 1, ks + 1, nr);
+              ++nr;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        if (ks + 1 < V3_BK / 16)
 #pragma unroll
-        for (int j = 0; j < SN; ++j) mfma_v(af[i], bf[j], acc[i][j]);
+          for (; nr < SM + SN; ++nr) rd(cur ^ 1, ks + 1, nr);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < V3_BK / 16; ++ks) {
+        typename Vec8<T>::type af[SM], bf[SN];
+#pragma unroll
+        for (int i = 0; i < SM; ++i) af[i] = fa.get(as, wm, i, ks, l32);
+#pragma unroll
+        for (int j = 0; j < SN; ++j) bf[j] = fb.get(bs, wn, j, ks, l32);
+#pragma unroll
+        for (int i = 0; i < SM; ++i)
+#pragma unroll
+          for (int j = 0; j < SN; ++j) mfma_v(af[i], bf[j], acc[i][j]);
+      }
     }
   };
   if (K > 0) dma(0, a0, b0);
@@ -600,6 +690,61 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_v3(
     if (more2) dma(k0 + 2 * V3_BK, a0, b0);
     mul(a1, b1);
     if (!more2) break;
+  }
+  if (m0 + TBM <= M && n0 + TBN <= N && kGemmLdsEpi) {
+    // Full tile: each wave stages one slab of HR rows (32, or 16 when two 32-row
+    // slabs per stage array do not fit) of its C tile at a time in its own LDS region
+    // (the operand stages are free once every wave has passed the barrier) and writes
+    // it back as 16-byte row-contiguous stores.  Row padding puts the two lane halves'
+    // stores (4 rows apart) in disjoint banks.
+    constexpr int SC = SN * 32;                                          // slab columns
+    constexpr int RS = SC * (int)sizeof(TC) + (sizeof(TC) == 4 ? 32 : 16);  // row bytes
+    constexpr int NSL = (NW + 3) / 4;                    // slabs per stage array
+    constexpr int MINT = ATILE < BTILE ? ATILE : BTILE;
+    constexpr int HR = NSL * 32 * RS <= MINT ? 32 : 16;
+    static_assert(NSL * HR * RS <= MINT, "slab staging exceeds a stage array");
+    constexpr int CPR = SC * (int)sizeof(TC) / 16;                       // chunks per row
+    __syncthreads();
+    const int st = wave & 3;  // wave w stages in array w % 4, slab w / 4
+    char* slab = (st == 0 ? a0 : st == 1 ? b0 : st == 2 ? a1 : b1) + (wave >> 2) * HR * RS;
+#pragma unroll
+    for (int i = 0; i < SM; ++i) {
+#pragma unroll
+      for (int half = 0; half < 32 / HR; ++half) {
+        // accumulator registers r in [half*16*HR/32, ...): rows half*HR .. half*HR+HR-1
+#pragma unroll
+        for (int j = 0; j < SN; ++j)
+#pragma unroll
+          for (int rr = 0; rr < HR / 2; ++rr) {
+            const int r = half * (HR / 2) + rr;
+            const int row = (r >> 2) * 8 + lh * 4 + (r & 3) - half * HR;
+            *reinterpret_cast<TC*>(slab + row * RS + (j * 32 + l32) * (int)sizeof(TC)) =
+                tg_from_float<TC>(alpha * acc[i][j][r]);
+          }
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's slab is written
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int q = 0; q < HR * CPR / 64; ++q) {
+          const int u = q * 64 + lane, row = u / CPR, ch = u % CPR;
+          const uint4 v = *reinterpret_cast<const uint4*>(slab + row * RS + ch * 16);
+          TC* pc = C + (m0 + wm + i * 32 + half * HR + row) * ldc + n0 + wn +
+                   ch * (16 / (int)sizeof(TC));
+          if (beta != 0.f) {
+            tg_vec16<TC> o, c = tg_load16(pc);
+            *reinterpret_cast<uint4*>(&o) = v;
+#pragma unroll
+            for (int e = 0; e < tg_vec16<TC>::N; ++e)
+              o.v[e] = tg_from_float<TC>(tg_to_float(o.v[e]) + beta * tg_to_float(c.v[e]));
+            tg_store16(pc, o);
+          } else {
+            *reinterpret_cast<uint4*>(pc) = v;
+          }
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();
+      }
+    }
+    return;
   }
 #pragma unroll
   for (int i = 0; i < SM; ++i)
@@ -638,20 +783,32 @@ int launch(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const v
   // v2 stages whole 16-byte vectors along every contiguous dimension: extents must be
   // multiples of 8 so no vector straddles a row end.
   if constexpr (sizeof(T) == 2) {
-  if (vec && M >= 64 && N >= 64 && K >= 64 && M % 8 == 0 && N % 8 == 0 && K % V3_BK == 0) {
-    const int64_t big_tiles = ((M + 255) / 256) * ((N + 127) / 128) * batch;
-    const bool big = big_tiles >= (int64_t)tg_num_cus();
-#define TG_G3_SHAPE(TA_, TB_, WGM, OCC)                                                    \
+  // The DMA addresses each operand (one batch entry) through a 2 GiB buffer window.
+  const int64_t a_span = (ta ? K * lda : M * lda) * (int64_t)sizeof(T);
+  const int64_t b_span = (tb ? N * ldb : K * ldb) * (int64_t)sizeof(T);
+  if (vec && M >= 64 && N >= 64 && K >= 64 && M % 8 == 0 && N % 8 == 0 && K % V3_BK == 0 &&
+      a_span < (int64_t{1} << 31) && b_span < (int64_t{1} << 31)) {
+    // Block shapes (waves x per-wave tile): 2x2 waves of 128x128 (256x256, one block
+    // and one wave per SIMD, accumulators in AGPRs) when the problem has enough such
+    // tiles to fill the CUs: half the LDS fragment bytes and global tile bytes per flop
+    // of the smaller shapes.  Else 2x2 waves of 128x64 (256x128), else 2x2 waves of
+    // 64x64 (128x128, two blocks per CU).
+    const int64_t ncu = tg_num_cus();
+    const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256) * batch;
+    const int64_t t128 = ((M + 255) / 256) * ((N + 127) / 128) * batch;
+    const int shape = t256 >= kHugeTiles * ncu / 4 ? 2 : (t128 >= ncu ? 1 : 0);
+#define TG_G3_SHAPE(TA_, TB_, WGM, WGN, SM, SN, OCC)                                       \
   do {                                                                                     \
-    constexpr int TBM = WGM * 64;                                                          \
-    dim3 g3((unsigned)((N + 127) / 128), (unsigned)((M + TBM - 1) / TBM), (unsigned)batch); \
-    k_gemm_v3<T, TC, TA_, TB_, WGM, 2, 2, 2, OCC><<<g3, 64 * WGM * 2, 0, s>>>(               \
+    constexpr int TBM = WGM * SM * 32, TBN = WGN * SN * 32;                                \
+    dim3 g3((unsigned)((N + TBN - 1) / TBN), (unsigned)((M + TBM - 1) / TBM), (unsigned)batch); \
+    k_gemm_v3<T, TC, TA_, TB_, WGM, WGN, SM, SN, OCC><<<g3, 64 * WGM * WGN, 0, s>>>(        \
         M, N, K, alpha, a, lda, sa, b, ldb, sb, beta, c, ldc, sc);                          \
   } while (0)
-#define TG_G3(TA_, TB_)                          \
-  do {                                           \
-    if (big) TG_G3_SHAPE(TA_, TB_, 4, 1);        \
-    else TG_G3_SHAPE(TA_, TB_, 2, 2);            \
+#define TG_G3(TA_, TB_)                                          \
+  do {                                                           \
+    if (shape == 2) TG_G3_SHAPE(TA_, TB_, 2, 2, 4, 4, 1);        \
+    else if (shape == 1) TG_G3_SHAPE(TA_, TB_, kBigWGM, kBigWGN, kBigSM, kBigSN, 1); \
+    else TG_G3_SHAPE(TA_, TB_, 2, 2, 2, 2, 2);                   \
   } while (0)
     if (!ta && !tb) TG_G3(false, false);
     else if (!ta && tb) TG_G3(false, true);
