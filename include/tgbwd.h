@@ -149,6 +149,12 @@ int tg_gemm(int dtype_ab, int dtype_c, int trans_a, int trans_b, int64_t M, int6
             float alpha, const void* A, int64_t lda, int64_t stride_a, const void* B,
             int64_t ldb, int64_t stride_b, float beta, void* C, int64_t ldc, int64_t stride_c,
             int64_t batch, void* stream);
+/* C = alpha*op(A)@op(B) + bias[n] (fp32 bias of length N, added in the epilogue before
+ * the rounding to dtype_c): the Linear forward y = x @ w + b (_nn.py:258-285, the
+ * matmul then the broadcast add of _core.py:941-968) as one GEMM. */
+int tg_gemm_bias(int dtype_ab, int dtype_c, int trans_a, int trans_b, int64_t M, int64_t N,
+                 int64_t K, float alpha, const void* A, int64_t lda, const void* B, int64_t ldb,
+                 const float* bias, void* C, int64_t ldc, void* stream);
 
 /* ---- attention ------------------------------------------------------------ */
 /* FlashAttention forward on contiguous (B,H,S,D) tensors, saving the row

@@ -170,7 +170,8 @@ __global__ __launch_bounds__(kThreads) void k_gemm(int64_t M, int64_t N, int64_t
                                                    const T* __restrict__ A, int64_t lda,
                                                    int64_t sa, const T* __restrict__ B,
                                                    int64_t ldb, int64_t sb, float beta,
-                                                   TC* __restrict__ C, int64_t ldc, int64_t sc) {
+                                                   TC* __restrict__ C, int64_t ldc, int64_t sc,
+    const float* __restrict__ bias) {
   constexpr int BK = Mfma<T>::BK;
   constexpr int EPL = Mfma<T>::EPL;
   constexpr int KPL = BK / 2;  // k elements per lane per tile (lane half h owns k in [h*KPL, h*KPL+KPL))
@@ -241,6 +242,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm(int64_t M, int64_t N, int64_t
         const int64_t row = m0 + wm + i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
         if (row < M) {
           float v = alpha * acc[i][j][r];
+          if (bias) v += bias[col];
           TC* pc = C + row * ldc + col;
           if (beta != 0.f) v += beta * tg_to_float(*pc);
           *pc = tg_from_float<TC>(v);
@@ -346,7 +348,8 @@ __global__ __launch_bounds__(kThreads) void k_gemm_v2(int64_t M, int64_t N, int6
                                                       const T* __restrict__ A, int64_t lda,
                                                       int64_t sa, const T* __restrict__ B,
                                                       int64_t ldb, int64_t sb, float beta,
-                                                      TC* __restrict__ C, int64_t ldc, int64_t sc) {
+                                                      TC* __restrict__ C, int64_t ldc, int64_t sc,
+    const float* __restrict__ bias) {
   constexpr int NTW = BNv / 64;  // 32-wide MFMA tiles per wave along n
   using SA = StageV2<T, !TA, V2_BM>;
   using SB = StageV2<T, TB, BNv>;
@@ -420,6 +423,7 @@ __global__ __launch_bounds__(kThreads) void k_gemm_v2(int64_t M, int64_t N, int6
         const int64_t row = m0 + wm + i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
         if (row < M) {
           float v = alpha * acc[i][j][r];
+          if (bias) v += bias[col];
           TC* pc = C + row * ldc + col;
           if (beta != 0.f) v += beta * tg_to_float(*pc);
           *pc = tg_from_float<TC>(v);
@@ -583,7 +587,8 @@ template <typename T, typename TC, bool TA, bool TB, int WGM, int WGN, int SM, i
 __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_v3(
     int64_t M, int64_t N, int64_t K, float alpha, const T* __restrict__ A, int64_t lda,
     int64_t sa, const T* __restrict__ B, int64_t ldb, int64_t sb, float beta,
-    TC* __restrict__ C, int64_t ldc, int64_t sc) {
+    TC* __restrict__ C, int64_t ldc, int64_t sc,
+    const float* __restrict__ bias) {
   constexpr int NW = WGM * WGN, TBM = WGM * SM * 32, TBN = WGN * SN * 32;
   constexpr int ATILE = TBM * V3_BK * 2, BTILE = TBN * V3_BK * 2;
   __shared__ __attribute__((aligned(1024))) char a0[ATILE];
@@ -707,6 +712,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_v3(
     __syncthreads();
     const int st = wave & 3;  // wave w stages in array w % 4, slab w / 4
     char* slab = (st == 0 ? a0 : st == 1 ? b0 : st == 2 ? a1 : b1) + (wave >> 2) * HR * RS;
+    float bv[SN];  // bias of this lane's column in each 32-column tile
+#pragma unroll
+    for (int j = 0; j < SN; ++j) bv[j] = bias ? bias[n0 + wn + j * 32 + l32] : 0.f;
 #pragma unroll
     for (int i = 0; i < SM; ++i) {
 #pragma unroll
@@ -719,7 +727,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_v3(
             const int r = half * (HR / 2) + rr;
             const int row = (r >> 2) * 8 + lh * 4 + (r & 3) - half * HR;
             *reinterpret_cast<TC*>(slab + row * RS + (j * 32 + l32) * (int)sizeof(TC)) =
-                tg_from_float<TC>(alpha * acc[i][j][r]);
+                tg_from_float<TC>(alpha * acc[i][j][r] + bv[j]);
           }
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's slab is written
         __builtin_amdgcn_wave_barrier();
@@ -757,6 +765,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_v3(
         const int64_t row = m0 + wm + i * 32 + (r >> 2) * 8 + lh * 4 + (r & 3);
         if (row < M) {
           float v = alpha * acc[i][j][r];
+          if (bias) v += bias[col];
           TC* pc = C + row * ldc + col;
           if (beta != 0.f) v += beta * tg_to_float(*pc);
           *pc = tg_from_float<TC>(v);
@@ -772,7 +781,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_v3(
 template <typename T, typename TC>
 int launch(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const void* A,
            int64_t lda, int64_t sa, const void* B, int64_t ldb, int64_t sb, float beta, void* C,
-           int64_t ldc, int64_t sc, int64_t batch, hipStream_t s) {
+           int64_t ldc, int64_t sc, int64_t batch, hipStream_t s, const float* bias = nullptr) {
   constexpr int VE = 16 / sizeof(T);
   const bool vec = tg_aligned16(A) && tg_aligned16(B) && lda % VE == 0 && ldb % VE == 0 &&
                    sa % VE == 0 && sb % VE == 0;
@@ -802,7 +811,7 @@ int launch(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const v
     constexpr int TBM = WGM * SM * 32, TBN = WGN * SN * 32;                                \
     dim3 g3((unsigned)((N + TBN - 1) / TBN), (unsigned)((M + TBM - 1) / TBM), (unsigned)batch); \
     k_gemm_v3<T, TC, TA_, TB_, WGM, WGN, SM, SN, OCC><<<g3, 64 * WGM * WGN, 0, s>>>(        \
-        M, N, K, alpha, a, lda, sa, b, ldb, sb, beta, c, ldc, sc);                          \
+        M, N, K, alpha, a, lda, sa, b, ldb, sb, beta, c, ldc, sc, bias);                    \
   } while (0)
 #define TG_G3(TA_, TB_)                                          \
   do {                                                           \
@@ -828,10 +837,10 @@ int launch(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const v
   do {                                                                                         \
     if (wide)                                                                                  \
       k_gemm_v2<T, TC, TA_, TB_, 128><<<g2, kThreads, 0, s>>>(M, N, K, alpha, a, lda, sa, b,    \
-                                                              ldb, sb, beta, c, ldc, sc);     \
+                                                              ldb, sb, beta, c, ldc, sc, bias); \
     else                                                                                       \
       k_gemm_v2<T, TC, TA_, TB_, 64><<<g2, kThreads, 0, s>>>(M, N, K, alpha, a, lda, sa, b, ldb, \
-                                                             sb, beta, c, ldc, sc);          \
+                                                             sb, beta, c, ldc, sc, bias);    \
   } while (0)
     if (!ta && !tb) TG_G2(false, false);
     else if (!ta && tb) TG_G2(false, true);
@@ -842,7 +851,7 @@ int launch(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const v
   }
   }
 #define TG_G(TA_, TB_, V_) \
-  k_gemm<T, TC, TA_, TB_, V_><<<grid, kThreads, 0, s>>>(M, N, K, alpha, a, lda, sa, b, ldb, sb, beta, c, ldc, sc)
+  k_gemm<T, TC, TA_, TB_, V_><<<grid, kThreads, 0, s>>>(M, N, K, alpha, a, lda, sa, b, ldb, sb, beta, c, ldc, sc, bias)
   if (vec) {
     if (!ta && !tb) TG_G(false, false, true);
     else if (!ta && tb) TG_G(false, true, true);
@@ -860,41 +869,56 @@ int launch(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const v
 
 }  // namespace
 
+namespace {
+int gemm_dispatch(const char* who, int dtype_ab, int dtype_c, int trans_a, int trans_b,
+                  int64_t M, int64_t N, int64_t K, float alpha, const void* A, int64_t lda,
+                  int64_t stride_a, const void* B, int64_t ldb, int64_t stride_b, float beta,
+                  void* C, int64_t ldc, int64_t stride_c, int64_t batch, const float* bias,
+                  void* stream) {
+  TG_REQUIRE(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "%s: negative extent", who);
+  if (M == 0 || N == 0 || batch == 0) return TG_OK;
+  TG_REQUIRE(C, "%s: null C", who);
+  TG_REQUIRE(ldc >= N, "%s: ldc %lld < N %lld", who, (long long)ldc, (long long)N);
+  TG_REQUIRE(batch <= 65535, "%s: batch %lld exceeds 65535", who, (long long)batch);
+  TG_REQUIRE((M + BM - 1) / BM <= 65535, "%s: M too large", who);
+  hipStream_t s = tg_stream(stream);
+  if (K == 0) {
+    // C = beta*C (+ bias): no product term; reuse the kernel with K = 0 (acc stays zero).
+  } else {
+    TG_REQUIRE(A && B, "%s: null operand", who);
+    TG_REQUIRE(lda >= (trans_a ? M : K) && ldb >= (trans_b ? K : N), "%s: bad leading dim", who);
+  }
+#define TG_GEMM_CALL(TA, TC)                                                                  \
+  return launch<TA, TC>(trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb, stride_b, \
+                        beta, C, ldc, stride_c, batch, s, bias)
+  if (dtype_ab == TG_F16) {
+    if (dtype_c == TG_F32) TG_GEMM_CALL(tg_half, float);
+    if (dtype_c == TG_F16) TG_GEMM_CALL(tg_half, tg_half);
+  } else if (dtype_ab == TG_BF16) {
+    if (dtype_c == TG_F32) TG_GEMM_CALL(tg_bf16, float);
+    if (dtype_c == TG_BF16) TG_GEMM_CALL(tg_bf16, tg_bf16);
+  } else if (dtype_ab == TG_F32 && dtype_c == TG_F32) {
+    TG_GEMM_CALL(float, float);
+  }
+#undef TG_GEMM_CALL
+  tg_set_error("%s: unsupported dtype combination ab=%d c=%d", who, dtype_ab, dtype_c);
+  return TG_ERR_UNSUPPORTED;
+}
+}  // namespace
+
 TG_EXPORT int tg_gemm(int dtype_ab, int dtype_c, int trans_a, int trans_b, int64_t M, int64_t N,
                       int64_t K, float alpha, const void* A, int64_t lda, int64_t stride_a,
                       const void* B, int64_t ldb, int64_t stride_b, float beta, void* C,
                       int64_t ldc, int64_t stride_c, int64_t batch, void* stream) {
-  TG_REQUIRE(M >= 0 && N >= 0 && K >= 0 && batch >= 0, "tg_gemm: negative extent");
-  if (M == 0 || N == 0 || batch == 0) return TG_OK;
-  TG_REQUIRE(C, "tg_gemm: null C");
-  TG_REQUIRE(ldc >= N, "tg_gemm: ldc %lld < N %lld", (long long)ldc, (long long)N);
-  TG_REQUIRE(batch <= 65535, "tg_gemm: batch %lld exceeds 65535", (long long)batch);
-  TG_REQUIRE((M + BM - 1) / BM <= 65535, "tg_gemm: M too large");
-  hipStream_t s = tg_stream(stream);
-  if (K == 0) {
-    // C = beta*C: no product term; reuse the kernel with K = 0 (acc stays zero).
-  } else {
-    TG_REQUIRE(A && B, "tg_gemm: null operand");
-    TG_REQUIRE(lda >= (trans_a ? M : K) && ldb >= (trans_b ? K : N), "tg_gemm: bad leading dim");
-  }
-  if (dtype_ab == TG_F16) {
-    if (dtype_c == TG_F32)
-      return launch<tg_half, float>(trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb,
-                                    stride_b, beta, C, ldc, stride_c, batch, s);
-    if (dtype_c == TG_F16)
-      return launch<tg_half, tg_half>(trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb,
-                                      stride_b, beta, C, ldc, stride_c, batch, s);
-  } else if (dtype_ab == TG_BF16) {
-    if (dtype_c == TG_F32)
-      return launch<tg_bf16, float>(trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb,
-                                    stride_b, beta, C, ldc, stride_c, batch, s);
-    if (dtype_c == TG_BF16)
-      return launch<tg_bf16, tg_bf16>(trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb,
-                                      stride_b, beta, C, ldc, stride_c, batch, s);
-  } else if (dtype_ab == TG_F32 && dtype_c == TG_F32) {
-    return launch<float, float>(trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb,
-                                stride_b, beta, C, ldc, stride_c, batch, s);
-  }
-  tg_set_error("tg_gemm: unsupported dtype combination ab=%d c=%d", dtype_ab, dtype_c);
-  return TG_ERR_UNSUPPORTED;
+  return gemm_dispatch("tg_gemm", dtype_ab, dtype_c, trans_a, trans_b, M, N, K, alpha, A, lda,
+                       stride_a, B, ldb, stride_b, beta, C, ldc, stride_c, batch, nullptr, stream);
+}
+
+TG_EXPORT int tg_gemm_bias(int dtype_ab, int dtype_c, int trans_a, int trans_b, int64_t M,
+                           int64_t N, int64_t K, float alpha, const void* A, int64_t lda,
+                           const void* B, int64_t ldb, const float* bias, void* C, int64_t ldc,
+                           void* stream) {
+  TG_REQUIRE(bias, "tg_gemm_bias: null bias");
+  return gemm_dispatch("tg_gemm_bias", dtype_ab, dtype_c, trans_a, trans_b, M, N, K, alpha, A,
+                       lda, 0, B, ldb, 0, 0.f, C, ldc, 0, 1, bias, stream);
 }

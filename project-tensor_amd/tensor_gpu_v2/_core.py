@@ -878,6 +878,65 @@ def _matmul(self, other):
     return out
 
 
+def _linear(x, w, b):
+    """y = x @ w + b for a 2-D weight as one GEMM with the bias added in its epilogue
+    (Linear.__call__, _nn.py:258-285, which builds a matmul node and a broadcast-add
+    node; the gradients are those of the pair: dx = g @ w^T, dw = x^T @ g, db = g
+    summed over the leading axes).  A weight that is the transpose of a contiguous
+    tensor (a tied head) is cast without transposing and used through op(B) = B^T."""
+    a, wd = x.data, w.data
+    if a.dim() < 2 or wd.dim() != 2 or a.shape[-1] != wd.shape[0]:
+        out = x @ w
+        return out + b if b is not None else out
+    cdt = _compute_dtype(a, wd)
+    if cdt not in _GEMM_DTYPES:
+        raise TypeError(f"matmul: dtype {cdt} is not supported by the MFMA GEMM "
+                        "(float32, float16, bfloat16)")
+    K, N = wd.shape
+    lead = tuple(a.shape[:-1])
+    A2 = a.to(cdt).contiguous().reshape(-1, K)
+    wt = not wd.is_contiguous() and wd.t().is_contiguous()
+    bc = wd.t().to(cdt).contiguous() if wt else wd.to(cdt).contiguous()  # [N, K] if wt
+    if b is not None:
+        odt = cfg.resolve_dtype(torch.promote_types(cdt, b.data.dtype))
+        bias = b.data.to(torch.float32).contiguous().reshape(N)
+        if odt in (torch.float32, cdt):
+            y = torch.empty(A2.shape[0], N, dtype=odt, device=a.device)
+            L.gemm_bias(A2, bc, bias, y, trans_b=wt)
+        else:
+            y = torch.empty(A2.shape[0], N, dtype=torch.float32, device=a.device)
+            L.gemm_bias(A2, bc, bias, y, trans_b=wt)
+            y = y.to(odt)
+    else:
+        y = L.matmul2d(A2, bc, trans_b=wt)
+    children = (x, w) if b is None else (x, w, b)
+    out = Tensor._wrap(y.reshape(*lead, N), children, "linear")
+    if out._requires_grad:
+        def _backward():
+            g = out._grad_out()
+            G2 = g.to(cdt).contiguous().reshape(-1, N)
+            if x._has_grad():
+                buf, acc = x._grad_target()
+                if buf.dtype in (torch.float32, cdt):
+                    L.matmul2d(G2, bc, out=buf.view(-1, K), trans_b=not wt,
+                               beta=1.0 if acc else 0.0)
+                else:
+                    da = L.matmul2d(G2, bc, trans_b=not wt, out_dtype=torch.float32)
+                    x._accumulate(da.reshape(buf.shape), True) if acc else buf.copy_(
+                        da.reshape(buf.shape))
+            if w._has_grad():
+                buf, acc = w._grad_target()
+                if buf.dtype in (torch.float32, cdt):
+                    L.matmul2d(A2, G2, out=buf.view(K, N), trans_a=True, beta=1.0 if acc else 0.0)
+                else:
+                    dw = L.matmul2d(A2, G2, trans_a=True, out_dtype=torch.float32)
+                    w._accumulate(dw, True) if acc else buf.copy_(dw)
+            if b is not None and b._has_grad():
+                b._accumulate_unb(g)
+        out._backward = _backward
+    return out
+
+
 def _batch_view(x, batch_shape, m, n):
     """Broadcast x [..., m, n] to batch_shape + [m, n]; return (tensor3d, stride) with
     stride 0 when x has no batch extent to broadcast."""

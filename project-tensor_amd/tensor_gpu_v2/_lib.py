@@ -63,6 +63,8 @@ SIGNATURES = {
     "tg_zero_nonfinite": (_i32, [_i32, _i32, _vp, _vp, _vp]),
     "tg_gemm": (_i32, [_i32, _i32, _i32, _i32, _i64, _i64, _i64, _f32, _vp, _i64, _i64, _vp,
                        _i64, _i64, _f32, _vp, _i64, _i64, _i64, _vp]),
+    "tg_gemm_bias": (_i32, [_i32, _i32, _i32, _i32, _i64, _i64, _i64, _f32, _vp, _i64, _vp, _i64,
+                            _vp, _vp, _i64, _vp]),
     "tg_flash_attn_fwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                  _f32, _i32, _vp]),
     "tg_flash_attn_bwd_workspace": (_sz, [_i64, _i64, _i64, _i64, _i64]),
@@ -490,6 +492,25 @@ def gemm(a, b, c, trans_a=False, trans_b=False, alpha=1.0, beta=0.0, M=None, N=N
         float(alpha), ptr(a), lda, stride_a, ptr(b), ldb, stride_b, float(beta), ptr(c), ldc,
         stride_c, batch, stream_handle()))
     return c
+
+
+def gemm_bias(a, b, bias, out, trans_b=False):
+    """out = a @ op(b) + bias (a [M, K], b [K, N] or, transposed, [N, K]; bias fp32 [N])."""
+    for n, t in (("a", a), ("b", b), ("bias", bias), ("out", out)):
+        _dev(t, n)
+    M, K = a.shape
+    N = b.shape[0] if trans_b else b.shape[1]
+    if (b.shape[1] if trans_b else b.shape[0]) != K:
+        raise ValueError(f"gemm_bias: inner dims differ ({tuple(a.shape)} @ {tuple(b.shape)})")
+    if bias.dtype != torch.float32 or bias.numel() != N or tuple(out.shape) != (M, N):
+        raise ValueError("gemm_bias: bias must be fp32 [N] and out [M, N]")
+    if a.dtype != b.dtype or out.dtype not in (torch.float32, a.dtype):
+        raise TypeError(f"gemm_bias: dtypes a={a.dtype} b={b.dtype} out={out.dtype}")
+    ensure_device(out.device.index)
+    _check("tg_gemm_bias", load().tg_gemm_bias(
+        dtype_code(a), dtype_code(out), 0, int(bool(trans_b)), M, N, K, 1.0, ptr(a), K, ptr(b),
+        b.shape[1], ptr(bias), ptr(out), N, stream_handle()))
+    return out
 
 
 _CUS = {}

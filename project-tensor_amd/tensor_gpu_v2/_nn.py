@@ -12,7 +12,7 @@ import torch
 
 from . import _config as cfg
 from . import _lib as L
-from ._core import Tensor
+from ._core import Tensor, _linear
 
 
 def _targets(tensors):
@@ -159,10 +159,9 @@ class Linear(Module):
         self.b = Tensor(np.zeros(nout, dtype=np.float32), dtype=np.float32) if bias else None
 
     def __call__(self, x):
-        out = x @ self.w
-        if self.use_bias:
-            out = out + self.b
-        return out
+        # one GEMM with the bias in its epilogue (same values and gradients as
+        # x @ w followed by + b)
+        return _linear(x, self.w, self.b if self.use_bias else None)
 
     def parameters(self):
         return [self.w, self.b] if self.use_bias else [self.w]

@@ -452,3 +452,48 @@ def test_view_and_add_grads_copy_on_write(tg):
     z = tg.Tensor(x_np)
     (z + z).reshape(24).sum().backward()
     assert_close(z.grad, np.full((4, 6), 2.0, np.float32), 0.0, "x + x")
+
+
+@pytest.mark.parametrize("autocast", [False, True])
+@pytest.mark.parametrize("bias,tied", [(True, False), (False, False), (False, True)])
+def test_linear_fused_bias_and_transposed_weight(tg, autocast, bias, tied):
+    """Linear runs as one GEMM with the bias in its epilogue; a weight tied as the
+    transpose of another parameter is used without a transposing copy.  Values and
+    gradients vs float64 torch of x @ w + b (autocast: fp16 operands, 1e-2)."""
+    rng = np.random.default_rng(5)
+    B, T, nin, nout = 2, 96, 128, 200
+    x_np = rng.standard_normal((B, T, nin)).astype(np.float32)
+    lin = tg.Linear(nin, nout, bias=bias)
+    if bias:
+        lin.b.data = tg.Tensor(rng.standard_normal(nout).astype(np.float32),
+                               requires_grad=False).data
+    src = None
+    if tied:
+        src = tg.Tensor(rng.standard_normal((nout, nin)).astype(np.float32) * 0.1)
+        tg.weight_tie(src, lin, "w", transpose=True)
+    w_np = lin.w.data.double().cpu().numpy()
+    x = tg.Tensor(x_np)
+    if autocast:
+        with tg.autocast():
+            y = lin(x)
+            loss = (y * y).sum()
+    else:
+        y = lin(x)
+        loss = (y * y).sum()
+    loss.backward()
+    xt = torch.tensor(x_np.astype(np.float64), requires_grad=True)
+    wt = torch.tensor(w_np, requires_grad=True)
+    yt = xt @ wt
+    if bias:
+        bt = torch.tensor(lin.b.data.double().cpu().numpy(), requires_grad=True)
+        yt = yt + bt
+    (yt * yt).sum().backward()
+    tol = RTOL_F16 if autocast else RTOL_F32_MM
+    assert_close(y.data.float(), yt.detach().numpy(), tol, "y")
+    assert_close(x.grad.float(), xt.grad.numpy(), tol, "x grad")
+    assert_close(lin.w.grad, wt.grad.numpy(), tol, "w grad")
+    if bias:
+        assert_close(lin.b.grad, bt.grad.numpy(), tol, "b grad")
+    if tied:
+        tg.sync_tied_gradients(lin)
+        assert_close(src.grad, wt.grad.numpy().T, tol, "tied source grad")

@@ -303,6 +303,48 @@ def test_gemm_large_tiles(cuda, ta, tb):
     assert err <= RTOL_F32_MM * float(ref.abs().max()), f"max error {err}"
 
 
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("odt,beta", [(torch.float32, 0.0), (torch.float16, 0.0),
+                                      (torch.float32, 1.0), (torch.float16, 1.0)])
+def test_gemm_huge_tiles(cuda, ta, tb, odt, beta):
+    """Enough 256x256 tiles for the one-wave-per-SIMD block, with partial edge tiles
+    (per-element epilogue) and full interior tiles (LDS-staged epilogue, beta read);
+    reference: torch float64 matmul of the same fp16 inputs."""
+    M, N, K = 4104, 4104, 192
+    g = torch.Generator(device="cuda").manual_seed(11)
+    a = torch.randn((K, M) if ta else (M, K), device="cuda", generator=g).half()
+    b = torch.randn((N, K) if tb else (K, N), device="cuda", generator=g).half()
+    c0 = torch.randn(M, N, device="cuda", generator=g).to(odt)
+    c = c0.clone()
+    L().gemm(a, b, c, ta, tb, 1.0, beta, M, N, K, a.shape[1], b.shape[1], N)
+    ref = (a.double().T if ta else a.double()) @ (b.double().T if tb else b.double())
+    ref = ref + beta * c0.double()
+    tol = RTOL_F32_MM if odt == torch.float32 else 2.0 ** -10
+    err = float((c.double() - ref).abs().max())
+    assert err <= tol * float(ref.abs().max()), f"max error {err}"
+
+
+@pytest.mark.parametrize("M,N,K,tb", [(8, 24, 40, False), (200, 136, 72, True),
+                                      (1000, 1000, 64, False), (4104, 2056, 128, True),
+                                      (4104, 4104, 128, False)])
+@pytest.mark.parametrize("dt,odt", [(torch.float16, torch.float16), (torch.float16, torch.float32),
+                                    (torch.bfloat16, torch.bfloat16), (torch.float32, torch.float32)])
+def test_gemm_bias(cuda, M, N, K, tb, dt, odt):
+    """tg_gemm_bias = A @ op(B) + bias[n] with the bias added before the output
+    rounding, on every kernel path (scalar, register-staged, DMA-staged 128/256 with
+    edge tiles); reference: float64 of the same rounded inputs."""
+    g = torch.Generator(device="cuda").manual_seed(M + N + K)
+    a = torch.randn(M, K, device="cuda", generator=g).to(dt)
+    b = torch.randn((N, K) if tb else (K, N), device="cuda", generator=g).to(dt)
+    bias = torch.randn(N, device="cuda", generator=g)
+    out = torch.empty(M, N, device="cuda", dtype=odt)
+    L().gemm_bias(a, b, bias, out, trans_b=tb)
+    ref = a.double() @ (b.double().T if tb else b.double()) + bias.double()
+    tol = RTOL_F32_MM if odt == torch.float32 else (2.0 ** -10 if odt == torch.float16 else 2.0 ** -7)
+    err = float((out.double() - ref).abs().max())
+    assert err <= tol * float(ref.abs().max()), f"max error {err}"
+
+
 def test_gemm_batched_broadcast_and_half_out(cuda):
     rng = np.random.default_rng(1)
     a = dev(rng.standard_normal((3, 40, 24)), torch.float16)
