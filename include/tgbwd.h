@@ -171,6 +171,19 @@ int tg_flash_attn_bwd(int dtype, const void* q, const void* k, const void* v, co
                       const void* dout, const float* lse, void* dq, void* dk, void* dv, int64_t B,
                       int64_t H, int64_t Sq, int64_t Sk, int64_t D, float scale, int causal,
                       int accumulate, void* workspace, size_t workspace_bytes, void* stream);
+/* Layout variants of the two calls above.  layout 0: q/k/v/o/dout/dq/dk/dv are
+ * contiguous (B,H,S,D); layout 1: they are contiguous (B,S,H,D) in memory (the head
+ * split of a (B,S,H*D) projection: the reference's reshape + transpose views before
+ * flash_attention, _core.py:1686-1700), read and written in place of a transposing
+ * copy.  lse and the workspace stay (B,H,S). */
+int tg_flash_attn_fwd_layout(int dtype, const void* q, const void* k, const void* v, void* o,
+                             float* lse, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
+                             float scale, int causal, int layout, void* stream);
+int tg_flash_attn_bwd_layout(int dtype, const void* q, const void* k, const void* v,
+                             const void* o, const void* dout, const float* lse, void* dq,
+                             void* dk, void* dv, int64_t B, int64_t H, int64_t Sq, int64_t Sk,
+                             int64_t D, float scale, int causal, int accumulate, int layout,
+                             void* workspace, size_t workspace_bytes, void* stream);
 
 /* Cross-entropy over logits [N, C] with int64 targets (CrossEntropyLoss,
  * _nn.py:1128-1185).  Forward: per-row log-sum-exp lse[N] and per-row loss

@@ -85,8 +85,8 @@ __device__ __forceinline__ typename Vec8<T>::type pack8(const float* v) {
 // clamped (valid) row and are replaced by zero when stored, so no load sits behind
 // a branch (a branch per load would serialise them).
 template <typename T, int ROWS, int D, bool RM, bool IL>
-__device__ __forceinline__ void stage(const T* __restrict__ g, int64_t row0, int64_t nrows,
-                                      T* rm, T* il) {
+__device__ __forceinline__ void stage(const T* __restrict__ g, int64_t rs, int64_t row0,
+                                      int64_t nrows, T* rm, T* il) {
   constexpr int DG = D / 8;
   constexpr int UNITS = (ROWS / 16) * 2 * DG;
   const bool full = row0 + ROWS <= nrows;  // uniform
@@ -99,7 +99,7 @@ __device__ __forceinline__ void stage(const T* __restrict__ g, int64_t row0, int
       const int r = rb * 16 + (j >> 2) * 8 + hh * 4 + (j & 3);
       int64_t row = row0 + r;
       if (!full) row = row < nrows ? row : nrows - 1;
-      v[j] = *reinterpret_cast<const uint4*>(g + row * D + dg * 8);
+      v[j] = *reinterpret_cast<const uint4*>(g + row * rs + dg * 8);
     }
     if (!full) {
 #pragma unroll
@@ -140,6 +140,19 @@ __device__ __forceinline__ void fa_block(int64_t& tile, int64_t& head) {
   tile = lin % gx;
 }
 
+// Layout of Q/K/V/O/dO/dQ/dK/dV.  Logical [B, H, S, D]; in memory either
+// contiguous [B, H, S, D] (bshd = 0) or contiguous [B, S, H, D] (bshd = 1: the head
+// split of a [B, S, H*D] projection, used without a transposing copy).  Rows of one
+// head are rs = D or H*D elements apart.  LSE and D stay [B, H, S].
+struct FaLay {
+  int64_t H;
+  int bshd;
+  __device__ __forceinline__ int64_t head(int64_t bh, int64_t S, int D) const {
+    return bshd ? ((bh / H) * S * H + (bh % H)) * D : bh * S * D;
+  }
+  __device__ __forceinline__ int rs(int D) const { return bshd ? (int)(H * D) : D; }
+};
+
 // Row index (within a 32-row C tile) of accumulator register r for lane half h.
 __device__ __forceinline__ int crow(int r, int h) { return ((r >> 2) << 3) + (h << 2) + (r & 3); }
 
@@ -149,17 +162,19 @@ __global__ __launch_bounds__(kThreads) void k_fa_fwd(const T* __restrict__ Q,
                                                      const T* __restrict__ K,
                                                      const T* __restrict__ V, T* __restrict__ O,
                                                      float* __restrict__ LSE, int64_t Sq,
-                                                     int64_t Sk, float scale, int causal) {
+                                                     int64_t Sk, float scale, int causal,
+                                                     FaLay lay) {
   constexpr int BN = 128, DK = D / 16, DT = D / 32;
   __shared__ __attribute__((aligned(16))) T Ks[BN * (D + 8)];
   __shared__ __attribute__((aligned(16))) T Vi[BN * D];
   int64_t tile, bh;
   fa_block(tile, bh);
-  Q += bh * Sq * D;
-  K += bh * Sk * D;
-  V += bh * Sk * D;
-  O += bh * Sq * D;
+  Q += lay.head(bh, Sq, D);
+  K += lay.head(bh, Sk, D);
+  V += lay.head(bh, Sk, D);
+  O += lay.head(bh, Sq, D);
   LSE += bh * Sq;
+  const int rs = lay.rs(D);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int h = lane >> 5, l32 = lane & 31;
   // causal: the last query blocks carry the most keys, so they are dispatched first
@@ -172,7 +187,7 @@ __global__ __launch_bounds__(kThreads) void k_fa_fwd(const T* __restrict__ Q,
   const int64_t qc = q < Sq ? q : Sq - 1;
   typename Vec8<T>::type qf[DK];
 #pragma unroll
-  for (int ks = 0; ks < DK; ++ks) qf[ks] = ld8(Q + qc * D + ks * 16 + h * 8);
+  for (int ks = 0; ks < DK; ++ks) qf[ks] = ld8(Q + qc * rs + ks * 16 + h * 8);
   f32x16 o[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
@@ -184,8 +199,8 @@ __global__ __launch_bounds__(kThreads) void k_fa_fwd(const T* __restrict__ Q,
   if (causal) kend = (qblk + 128 < Sk) ? qblk + 128 : Sk;
   for (int64_t k0 = 0; k0 < kend; k0 += BN) {
     __syncthreads();
-    stage<T, BN, D, true, false>(K, k0, Sk, Ks, nullptr);
-    stage<T, BN, D, false, true>(V, k0, Sk, nullptr, Vi);
+    stage<T, BN, D, true, false>(K, rs, k0, Sk, Ks, nullptr);
+    stage<T, BN, D, false, true>(V, rs, k0, Sk, nullptr, Vi);
     __syncthreads();
 #pragma unroll 1
     for (int kt = 0; kt < BN / 32; ++kt) {
@@ -245,7 +260,7 @@ __global__ __launch_bounds__(kThreads) void k_fa_fwd(const T* __restrict__ Q,
         T w[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) w[i] = (T)(o[dt][g * 4 + i] * inv);
-        *reinterpret_cast<uint2*>(O + q * D + dt * 32 + g * 8 + h * 4) =
+        *reinterpret_cast<uint2*>(O + q * rs + dt * 32 + g * 8 + h * 4) =
             *reinterpret_cast<const uint2*>(w);
       }
     if (h == 0) LSE[q] = (m + log2f(l)) / kLog2e;
@@ -257,7 +272,9 @@ __global__ __launch_bounds__(kThreads) void k_fa_fwd(const T* __restrict__ Q,
 template <typename T, int D>
 __global__ __launch_bounds__(kThreads) void k_fa_bwd_prep(const T* __restrict__ O,
                                                           const T* __restrict__ dO,
-                                                          float* __restrict__ Dv, int64_t rows) {
+                                                          float* __restrict__ Dv, int64_t rows,
+                                                          int64_t S, FaLay lay) {
+  // row: memory row of O / dO (both in the same layout); Dv is [B, H, S]
   const int64_t row = (int64_t)blockIdx.x * (kThreads / 16) + threadIdx.x / 16;
   const int sub = threadIdx.x & 15;
   float acc = 0.f;
@@ -271,7 +288,14 @@ __global__ __launch_bounds__(kThreads) void k_fa_bwd_prep(const T* __restrict__ 
   }
 #pragma unroll
   for (int off = 8; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 16);
-  if (row < rows && sub == 0) Dv[row] = acc;
+  if (row < rows && sub == 0) {
+    int64_t di = row;
+    if (lay.bshd) {  // row = (b*S + s)*H + h  ->  (b*H + h)*S + s
+      const int64_t b = row / (S * lay.H), rem = row % (S * lay.H);
+      di = (b * lay.H + rem % lay.H) * S + rem / lay.H;
+    }
+    Dv[di] = acc;
+  }
 }
 
 template <typename T>
@@ -330,43 +354,51 @@ template <int D> struct SwzTile {
   __device__ static int off(int r, int c) { return r * RB + ((c ^ key(r)) << 4); }
 };
 
-// Async copy of rows [row0, row0+R) of a [nrows, D] matrix into a swizzled tile.
-// Rows past nrows copy row nrows-1; the kernels make those rows contribute nothing.
-// A wave issues NI/4 instructions; DmaPlan holds each one's element offset within the
-// tile for this lane (the same for every tile), so a whole tile costs one 64-bit add
-// per instruction unless it is the partial last tile.
+// Async copy of rows [row0, row0+R) (rows rs elements apart, D contiguous elements
+// each) into a swizzled tile.  Rows past nrows copy row nrows-1; the kernels make
+// those rows contribute nothing.  A wave issues NI/4 instructions; DmaPlan holds each
+// one's byte offset within a full tile for this lane, and a raw buffer load takes it
+// as the per-lane offset against the tile's origin, so a full tile costs no vector
+// ALU work (the clamp of a partial last tile recomputes the offsets).
 template <typename T, int D, int R>
 struct DmaPlan {
-  static constexpr int CH = D / 8, NI = R * CH / 64, NPW = NI / (kThreads / 64);
-  static_assert(NI % (kThreads / 64) == 0, "tile must split evenly over the waves");
-  int off[NPW];
-  __device__ void init(int lane, int wave) {
+  static constexpr int CH = D / 8, NI = R * CH / 64, NW = kThreads / 64, NPW = NI / NW;
+  static_assert(NI % NW == 0, "tile must split evenly over the waves");
+  uint32_t off[NPW];
+  int rs;
+  __device__ void init(int lane, int wave, int rs_) {
+    rs = rs_;
 #pragma unroll
     for (int k = 0; k < NPW; ++k) {
-      const int u = (wave + k * (kThreads / 64)) * 64 + lane;
+      const int u = (wave + k * NW) * 64 + lane;
       const int r = u / CH, c = (u % CH) ^ SwzTile<D>::key(r);
-      off[k] = r * D + c * 8;
+      off[k] = (uint32_t)((r * rs + c * 8) * (int)sizeof(T));
     }
+  }
+  __device__ __forceinline__ static void dma(const T* base, uint32_t o, char* l) {
+    // the buffer-resource type is compiled in the device pass only (the host pass of
+    // this compiler drops launch stubs of kernel instantiations whose bodies hold it)
+#if defined(__HIP_DEVICE_COMPILE__)
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<T*>(base), (short)0, 0x7fffffff, 0x00020000);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (TG_LDS void*)l, 16, o, 0, 0, 0);
+#endif
   }
   __device__ __forceinline__ void copy(const T* __restrict__ g, int64_t row0, int64_t nrows,
                                        char* lds) const {
-    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const T* base = g + row0 * rs;
     if (row0 + R <= nrows) {  // uniform
-      const T* base = g + row0 * D;
 #pragma unroll
-      for (int k = 0; k < NPW; ++k)
-        __builtin_amdgcn_global_load_lds((const TG_GLB void*)(base + off[k]),
-                                         (TG_LDS void*)(lds + (wave + k * (kThreads / 64)) * 1024),
-                                         16, 0, 0);
+      for (int k = 0; k < NPW; ++k) dma(base, off[k], lds + (wave + k * NW) * 1024);
     } else {
 #pragma unroll
       for (int k = 0; k < NPW; ++k) {
-        const int r = off[k] / D;
-        int64_t row = row0 + r;
-        row = row < nrows ? row : nrows - 1;
-        __builtin_amdgcn_global_load_lds((const TG_GLB void*)(g + row * D + (off[k] - r * D)),
-                                         (TG_LDS void*)(lds + (wave + k * (kThreads / 64)) * 1024),
-                                         16, 0, 0);
+        const int u = (wave + k * NW) * 64 + lane;
+        const int r = u / CH, c = (u % CH) ^ SwzTile<D>::key(r);
+        const int64_t rr = (row0 + r < nrows ? row0 + r : nrows - 1) - row0;
+        dma(base, (uint32_t)((rr * rs + c * 8) * (int64_t)sizeof(T)),
+            lds + (wave + k * NW) * 1024);
       }
     }
   }
@@ -661,7 +693,7 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dkdv(
     const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
     const T* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Dv,
     T* __restrict__ dK, T* __restrict__ dV, int64_t Sq, int64_t Sk, float scale, int causal,
-    int accumulate) {
+    int accumulate, FaLay lay) {
   constexpr int DK = D / 16, DT = D / 32, TB = BM * D * 2;
   __shared__ __attribute__((aligned(1024))) char q0s[TB];
   __shared__ __attribute__((aligned(1024))) char do0s[TB];
@@ -670,14 +702,15 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dkdv(
   __shared__ __attribute__((aligned(16))) float lse0[BM], dvs0[BM], lse1[BM], dvs1[BM];
   int64_t tile, bh;
   fa_block(tile, bh);
-  Q += bh * Sq * D;
-  dO += bh * Sq * D;
-  K += bh * Sk * D;
-  V += bh * Sk * D;
-  dK += bh * Sk * D;
-  dV += bh * Sk * D;
+  Q += lay.head(bh, Sq, D);
+  dO += lay.head(bh, Sq, D);
+  K += lay.head(bh, Sk, D);
+  V += lay.head(bh, Sk, D);
+  dK += lay.head(bh, Sk, D);
+  dV += lay.head(bh, Sk, D);
   LSE += bh * Sq;
   Dv += bh * Sq;
+  const int rs = lay.rs(D);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int h = lane >> 5, l32 = lane & 31;
   const int64_t kblk = tile * (128 * KG);
@@ -692,8 +725,8 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dkdv(
     const int64_t kc = key < Sk ? key : Sk - 1;
 #pragma unroll
     for (int ks = 0; ks < DK; ++ks) {
-      kf[j][ks] = ld8(K + kc * D + ks * 16 + h * 8);
-      vf[j][ks] = ld8(V + kc * D + ks * 16 + h * 8);
+      kf[j][ks] = ld8(K + kc * rs + ks * 16 + h * 8);
+      vf[j][ks] = ld8(V + kc * rs + ks * 16 + h * 8);
     }
   }
   f32x16 dk[KG][DT], dv[KG][DT];
@@ -709,7 +742,7 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dkdv(
   LaneOffs<D> o;
   o.init(lane);
   DmaPlan<T, D, BM> plan;
-  plan.init(lane, wave);
+  plan.init(lane, wave, rs);
   // causal: queries below the first key of this block contribute nothing
   const int64_t qstart = causal ? (kblk / BM) * BM : 0;
   // log2-scaled LSE (+inf past Sq: P = 0 for padded rows) and scale*D of one tile
@@ -771,8 +804,8 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dkdv(
   for (int j = 0; j < KG; ++j)
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      store_c_tile<T>(dK, D, kw + 32 * j, Sk, dt * 32 + l32, dk[j][dt], 1.f, accumulate, h);
-      store_c_tile<T>(dV, D, kw + 32 * j, Sk, dt * 32 + l32, dv[j][dt], 1.f, accumulate, h);
+      store_c_tile<T>(dK, rs, kw + 32 * j, Sk, dt * 32 + l32, dk[j][dt], 1.f, accumulate, h);
+      store_c_tile<T>(dV, rs, kw + 32 * j, Sk, dt * 32 + l32, dv[j][dt], 1.f, accumulate, h);
     }
 }
 
@@ -937,7 +970,8 @@ template <typename T, int D, int BN, int OCC>
 __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dq(
     const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
     const T* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Dv,
-    T* __restrict__ dQ, int64_t Sq, int64_t Sk, float scale, int causal, int accumulate) {
+    T* __restrict__ dQ, int64_t Sq, int64_t Sk, float scale, int causal, int accumulate,
+    FaLay lay) {
   constexpr int DK = D / 16, DT = D / 32, TB = BN * D * 2;
   __shared__ __attribute__((aligned(1024))) char k0s[TB];
   __shared__ __attribute__((aligned(1024))) char v0s[TB];
@@ -945,13 +979,14 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dq(
   __shared__ __attribute__((aligned(1024))) char v1s[TB];
   int64_t tile, bh;
   fa_block(tile, bh);
-  Q += bh * Sq * D;
-  dO += bh * Sq * D;
-  dQ += bh * Sq * D;
-  K += bh * Sk * D;
-  V += bh * Sk * D;
+  Q += lay.head(bh, Sq, D);
+  dO += lay.head(bh, Sq, D);
+  dQ += lay.head(bh, Sq, D);
+  K += lay.head(bh, Sk, D);
+  V += lay.head(bh, Sk, D);
   LSE += bh * Sq;
   Dv += bh * Sq;
+  const int rs = lay.rs(D);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int h = lane >> 5, l32 = lane & 31;
   // causal: the last query blocks carry the most keys, so they are dispatched first
@@ -964,8 +999,8 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dq(
   typename Vec8<T>::type qf[DK], of[DK];
 #pragma unroll
   for (int ks = 0; ks < DK; ++ks) {
-    qf[ks] = ld8(Q + qc * D + ks * 16 + h * 8);
-    of[ks] = ld8(dO + qc * D + ks * 16 + h * 8);
+    qf[ks] = ld8(Q + qc * rs + ks * 16 + h * 8);
+    of[ks] = ld8(dO + qc * rs + ks * 16 + h * 8);
   }
   const float lq = LSE[qc] * kLog2e;
   const float dqs = Dv[qc] * scale;
@@ -977,7 +1012,7 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dq(
   LaneOffs<D> o;
   o.init(lane);
   DmaPlan<T, D, BN> plan;
-  plan.init(lane, wave);
+  plan.init(lane, wave, rs);
   int64_t kend = Sk;
   if (causal) kend = (qblk + 128 < Sk) ? qblk + 128 : Sk;
   if (kend > 0) {
@@ -1009,15 +1044,15 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dq(
   // C tiles: rows = queries of this wave, cols = d
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
-    store_c_tile<T>(dQ, D, qblk + wave * 32, Sq, dt * 32 + l32, acc[dt], 1.f, accumulate, h);
+    store_c_tile<T>(dQ, rs, qblk + wave * 32, Sq, dt * 32 + l32, acc[dt], 1.f, accumulate, h);
 }
 
 template <typename T, int D>
 int fwd_t(const void* q, const void* k, const void* v, void* o, float* lse, int64_t BH,
-          int64_t Sq, int64_t Sk, float scale, int causal, hipStream_t s) {
+          int64_t Sq, int64_t Sk, float scale, int causal, FaLay lay, hipStream_t s) {
   dim3 grid((unsigned)((Sq + 127) / 128), (unsigned)BH);
   k_fa_fwd<T, D><<<grid, kThreads, 0, s>>>((const T*)q, (const T*)k, (const T*)v, (T*)o, lse, Sq,
-                                           Sk, scale, causal);
+                                           Sk, scale, causal, lay);
   return tg_check_launch("tg_flash_attn_fwd");
 }
 
@@ -1034,19 +1069,19 @@ template <> struct BwdCfg<128> {
 template <typename T, int D>
 int bwd_t(const void* q, const void* k, const void* v, const void* o, const void* dout,
           const float* lse, void* dq, void* dk, void* dv, int64_t BH, int64_t Sq, int64_t Sk,
-          float scale, int causal, int acc, float* dvec, hipStream_t s) {
+          float scale, int causal, int acc, float* dvec, FaLay lay, hipStream_t s) {
   const int64_t rows = BH * Sq;
   k_fa_bwd_prep<T, D><<<(unsigned)((rows + 15) / 16), kThreads, 0, s>>>(
-      (const T*)o, (const T*)dout, dvec, rows);
+      (const T*)o, (const T*)dout, dvec, rows, Sq, lay);
   using C = BwdCfg<D>;
   dim3 gkv((unsigned)((Sk + 128 * C::KG - 1) / (128 * C::KG)), (unsigned)BH);
   k_fa_bwd_dkdv<T, D, C::BM, C::KG, C::OCC_KV><<<gkv, kThreads, 0, s>>>((const T*)q, (const T*)k, (const T*)v,
                                                (const T*)dout, lse, dvec, (T*)dk, (T*)dv, Sq, Sk,
-                                               scale, causal, acc);
+                                               scale, causal, acc, lay);
   dim3 gq((unsigned)((Sq + 127) / 128), (unsigned)BH);
   k_fa_bwd_dq<T, D, C::BN, C::OCC_Q><<<gq, kThreads, 0, s>>>((const T*)q, (const T*)k, (const T*)v,
                                             (const T*)dout, lse, dvec, (T*)dq, Sq, Sk, scale,
-                                            causal, acc);
+                                            causal, acc, lay);
   return tg_check_launch("tg_flash_attn_bwd");
 }
 
@@ -1062,21 +1097,71 @@ int check_fa(int dtype, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
 
 }  // namespace
 
+namespace {
+int fa_fwd(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
+           int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D, float scale, int causal,
+           int layout, void* stream, const char* who) {
+  int st = check_fa(dtype, B, H, Sq, Sk, D, who);
+  if (st) return st;
+  TG_REQUIRE(layout == 0 || layout == 1, "%s: layout must be 0 (BHSD) or 1 (BSHD)", who);
+  TG_REQUIRE(q && k && v && o && lse, "%s: null pointer", who);
+  TG_REQUIRE(tg_aligned16(q) && tg_aligned16(k) && tg_aligned16(v) && tg_aligned16(o),
+             "%s: operands must be 16-byte aligned", who);
+  hipStream_t s = tg_stream(stream);
+  const int64_t BH = B * H;
+  const FaLay lay{H, layout};
+  if (dtype == TG_F16)
+    return D == 64 ? fwd_t<tg_half, 64>(q, k, v, o, lse, BH, Sq, Sk, scale, causal, lay, s)
+                   : fwd_t<tg_half, 128>(q, k, v, o, lse, BH, Sq, Sk, scale, causal, lay, s);
+  return D == 64 ? fwd_t<tg_bf16, 64>(q, k, v, o, lse, BH, Sq, Sk, scale, causal, lay, s)
+                 : fwd_t<tg_bf16, 128>(q, k, v, o, lse, BH, Sq, Sk, scale, causal, lay, s);
+}
+
+int fa_bwd(int dtype, const void* q, const void* k, const void* v, const void* o,
+           const void* dout, const float* lse, void* dq, void* dk, void* dv, int64_t B,
+           int64_t H, int64_t Sq, int64_t Sk, int64_t D, float scale, int causal, int accumulate,
+           int layout, void* workspace, size_t workspace_bytes, void* stream, const char* who) {
+  int st = check_fa(dtype, B, H, Sq, Sk, D, who);
+  if (st) return st;
+  TG_REQUIRE(layout == 0 || layout == 1, "%s: layout must be 0 (BHSD) or 1 (BSHD)", who);
+  TG_REQUIRE(q && k && v && o && dout && lse && dq && dk && dv, "%s: null pointer", who);
+  TG_REQUIRE(tg_aligned16(q) && tg_aligned16(k) && tg_aligned16(v) && tg_aligned16(o) &&
+                 tg_aligned16(dout) && tg_aligned16(dq) && tg_aligned16(dk) && tg_aligned16(dv),
+             "%s: operands must be 16-byte aligned", who);
+  const size_t need = (size_t)(B * H * Sq) * sizeof(float);
+  if (!workspace || workspace_bytes < need) {
+    tg_set_error("%s: workspace of %zu bytes needed", who, need);
+    return TG_ERR_WORKSPACE;
+  }
+  hipStream_t s = tg_stream(stream);
+  const int64_t BH = B * H;
+  const FaLay lay{H, layout};
+  float* dvec = (float*)workspace;
+  if (dtype == TG_F16)
+    return D == 64 ? bwd_t<tg_half, 64>(q, k, v, o, dout, lse, dq, dk, dv, BH, Sq, Sk, scale,
+                                        causal, accumulate, dvec, lay, s)
+                   : bwd_t<tg_half, 128>(q, k, v, o, dout, lse, dq, dk, dv, BH, Sq, Sk, scale,
+                                         causal, accumulate, dvec, lay, s);
+  return D == 64 ? bwd_t<tg_bf16, 64>(q, k, v, o, dout, lse, dq, dk, dv, BH, Sq, Sk, scale,
+                                      causal, accumulate, dvec, lay, s)
+                 : bwd_t<tg_bf16, 128>(q, k, v, o, dout, lse, dq, dk, dv, BH, Sq, Sk, scale,
+                                       causal, accumulate, dvec, lay, s);
+}
+}  // namespace
+
 TG_EXPORT int tg_flash_attn_fwd(int dtype, const void* q, const void* k, const void* v, void* o,
                                 float* lse, int64_t B, int64_t H, int64_t Sq, int64_t Sk,
                                 int64_t D, float scale, int causal, void* stream) {
-  int st = check_fa(dtype, B, H, Sq, Sk, D, "tg_flash_attn_fwd");
-  if (st) return st;
-  TG_REQUIRE(q && k && v && o && lse, "tg_flash_attn_fwd: null pointer");
-  TG_REQUIRE(tg_aligned16(q) && tg_aligned16(k) && tg_aligned16(v) && tg_aligned16(o),
-             "tg_flash_attn_fwd: operands must be 16-byte aligned");
-  hipStream_t s = tg_stream(stream);
-  const int64_t BH = B * H;
-  if (dtype == TG_F16)
-    return D == 64 ? fwd_t<tg_half, 64>(q, k, v, o, lse, BH, Sq, Sk, scale, causal, s)
-                   : fwd_t<tg_half, 128>(q, k, v, o, lse, BH, Sq, Sk, scale, causal, s);
-  return D == 64 ? fwd_t<tg_bf16, 64>(q, k, v, o, lse, BH, Sq, Sk, scale, causal, s)
-                 : fwd_t<tg_bf16, 128>(q, k, v, o, lse, BH, Sq, Sk, scale, causal, s);
+  return fa_fwd(dtype, q, k, v, o, lse, B, H, Sq, Sk, D, scale, causal, 0, stream,
+                "tg_flash_attn_fwd");
+}
+
+TG_EXPORT int tg_flash_attn_fwd_layout(int dtype, const void* q, const void* k, const void* v,
+                                       void* o, float* lse, int64_t B, int64_t H, int64_t Sq,
+                                       int64_t Sk, int64_t D, float scale, int causal, int layout,
+                                       void* stream) {
+  return fa_fwd(dtype, q, k, v, o, lse, B, H, Sq, Sk, D, scale, causal, layout, stream,
+                "tg_flash_attn_fwd_layout");
 }
 
 TG_EXPORT size_t tg_flash_attn_bwd_workspace(int64_t B, int64_t H, int64_t Sq, int64_t Sk,
@@ -1092,27 +1177,17 @@ TG_EXPORT int tg_flash_attn_bwd(int dtype, const void* q, const void* k, const v
                                 void* dk, void* dv, int64_t B, int64_t H, int64_t Sq, int64_t Sk,
                                 int64_t D, float scale, int causal, int accumulate,
                                 void* workspace, size_t workspace_bytes, void* stream) {
-  int st = check_fa(dtype, B, H, Sq, Sk, D, "tg_flash_attn_bwd");
-  if (st) return st;
-  TG_REQUIRE(q && k && v && o && dout && lse && dq && dk && dv, "tg_flash_attn_bwd: null pointer");
-  TG_REQUIRE(tg_aligned16(q) && tg_aligned16(k) && tg_aligned16(v) && tg_aligned16(o) &&
-                 tg_aligned16(dout),
-             "tg_flash_attn_bwd: operands must be 16-byte aligned");
-  const size_t need = tg_flash_attn_bwd_workspace(B, H, Sq, Sk, D);
-  if (!workspace || workspace_bytes < need) {
-    tg_set_error("tg_flash_attn_bwd: workspace of %zu bytes needed", need);
-    return TG_ERR_WORKSPACE;
-  }
-  hipStream_t s = tg_stream(stream);
-  const int64_t BH = B * H;
-  float* dvec = (float*)workspace;
-  if (dtype == TG_F16)
-    return D == 64 ? bwd_t<tg_half, 64>(q, k, v, o, dout, lse, dq, dk, dv, BH, Sq, Sk, scale,
-                                        causal, accumulate, dvec, s)
-                   : bwd_t<tg_half, 128>(q, k, v, o, dout, lse, dq, dk, dv, BH, Sq, Sk, scale,
-                                         causal, accumulate, dvec, s);
-  return D == 64 ? bwd_t<tg_bf16, 64>(q, k, v, o, dout, lse, dq, dk, dv, BH, Sq, Sk, scale,
-                                      causal, accumulate, dvec, s)
-                 : bwd_t<tg_bf16, 128>(q, k, v, o, dout, lse, dq, dk, dv, BH, Sq, Sk, scale,
-                                       causal, accumulate, dvec, s);
+  return fa_bwd(dtype, q, k, v, o, dout, lse, dq, dk, dv, B, H, Sq, Sk, D, scale, causal,
+                accumulate, 0, workspace, workspace_bytes, stream, "tg_flash_attn_bwd");
+}
+
+TG_EXPORT int tg_flash_attn_bwd_layout(int dtype, const void* q, const void* k, const void* v,
+                                       const void* o, const void* dout, const float* lse,
+                                       void* dq, void* dk, void* dv, int64_t B, int64_t H,
+                                       int64_t Sq, int64_t Sk, int64_t D, float scale, int causal,
+                                       int accumulate, int layout, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
+  return fa_bwd(dtype, q, k, v, o, dout, lse, dq, dk, dv, B, H, Sq, Sk, D, scale, causal,
+                accumulate, layout, workspace, workspace_bytes, stream,
+                "tg_flash_attn_bwd_layout");
 }

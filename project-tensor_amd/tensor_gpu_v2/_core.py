@@ -143,7 +143,7 @@ class Tensor:
         if self._gz:
             self._g = self._new_buf(0)
             self._gz = False
-        elif self._gsh:
+        elif self._gsh or (self._g is not None and not self._g.is_contiguous()):
             self._privatize()
         return self._g
 
@@ -175,9 +175,13 @@ class Tensor:
         return self._g
 
     def _privatize(self):
-        """Give this node its own copy of a gradient buffer it shares."""
+        """Give this node its own contiguous copy of a gradient buffer it shares (or
+        holds with strides)."""
         buf = self._new_buf()
-        L.axpby(self._g, buf, 1.0, 0.0)
+        if self._g.is_contiguous():
+            L.axpby(self._g, buf, 1.0, 0.0)
+        else:
+            buf.copy_(self._g)
         self._g = buf
         self._gsh = False
 
@@ -187,7 +191,7 @@ class Tensor:
             self._g = self._new_buf()
             self._gz = False
             return self._g, False
-        if self._gsh:
+        if self._gsh or not self._g.is_contiguous():
             self._privatize()
         return self._g, True
 
@@ -225,7 +229,9 @@ class Tensor:
             g = g.reshape(self.data.shape)
         if self._gz:
             self._gz = False
-            if owned and g.dtype == self.data.dtype and g.is_contiguous():
+            if owned and g.dtype == self.data.dtype and (g.is_contiguous() or _dense(g)):
+                # an owned strided buffer (e.g. a head-split attention gradient) is kept
+                # as is; the first write or read through .grad makes it contiguous
                 self._g = g
             else:
                 buf = self._new_buf()
@@ -642,7 +648,7 @@ class Tensor:
         if out._requires_grad:
             def _backward():
                 if self._has_grad():
-                    self._accumulate(out._grad_out().permute(*inv))
+                    self._share_grad(out, out._grad_out().permute(*inv))
             out._backward = _backward
         return out
 
@@ -758,6 +764,19 @@ class Tensor:
 
 
 # ====================================================================== helpers
+def _dense(t):
+    """True if t covers its storage span without gaps or overlaps (a permutation of a
+    contiguous tensor)."""
+    n = 1
+    for size, stride in sorted(zip(t.shape, t.stride()), key=lambda x: x[1]):
+        if size == 1:
+            continue
+        if stride != n:
+            return False
+        n *= size
+    return True
+
+
 def _unique(children):
     seen = set()
     out = []
@@ -1082,8 +1101,13 @@ def flash_attention(query, key, value, block_size=64, is_causal=False, scale=Non
     dt = q4.dtype
     if dt not in (torch.float16, torch.bfloat16, torch.float32):
         raise TypeError(f"flash_attention: unsupported dtype {dt}")
-    q4c, k4c, v4c = q4.contiguous(), k4.to(dt).contiguous(), v4.to(dt).contiguous()
-    o, lse = L.flash_attn_fwd(q4c, k4c, v4c, scale, is_causal)
+    q4c, k4c, v4c = q4, k4.to(dt), v4.to(dt)
+    # (B, S, H, D) memory (the head split of a projection, viewed as (B, H, S, D)) is read
+    # and written in place; any other strides are made contiguous.
+    lay = 1 if all(L._fa_in(t, 1) for t in (q4c, k4c, v4c)) else 0
+    if lay == 0:
+        q4c, k4c, v4c = q4c.contiguous(), k4c.contiguous(), v4c.contiguous()
+    o, lse = L.flash_attn_fwd(q4c, k4c, v4c, scale, is_causal, lay)
     if dropout_p > 0 and cfg._grad_enabled:
         keep = (torch.rand(o.shape, device=o.device) > dropout_p).to(o.dtype)
         o_out = o * keep / (1 - dropout_p)
@@ -1093,12 +1117,16 @@ def flash_attention(query, key, value, block_size=64, is_causal=False, scale=Non
                        "FlashAttention")
     if out._requires_grad:
         def _backward():
-            g = out._grad_out()
-            g4 = g.reshape(q4c.shape).to(dt).contiguous()
-            dq = torch.empty_like(q4c)
-            dk = torch.empty_like(k4c)
-            dv = torch.empty_like(v4c)
-            L.flash_attn_bwd(q4c, k4c, v4c, o, g4, lse, dq, dk, dv, scale, is_causal, False)
+            g = out._grad_out().reshape(q4c.shape).to(dt)
+            if not L._fa_in(g, lay):
+                g = (g.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3) if lay == 1
+                     else g.contiguous())
+            B_, H_, Sq_, D_ = q4c.shape
+            Sk_ = k4c.shape[2]
+            dq = L.fa_empty(B_, H_, Sq_, D_, dt, q4c.device, lay)
+            dk = L.fa_empty(B_, H_, Sk_, D_, dt, q4c.device, lay)
+            dv = L.fa_empty(B_, H_, Sk_, D_, dt, q4c.device, lay)
+            L.flash_attn_bwd(q4c, k4c, v4c, o, g, lse, dq, dk, dv, scale, is_causal, False, lay)
             if query._has_grad():
                 query._accumulate(dq.reshape(query.data.shape), True)
             if key._has_grad():

@@ -67,6 +67,11 @@ SIGNATURES = {
                             _vp, _vp, _i64, _vp]),
     "tg_flash_attn_fwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                  _f32, _i32, _vp]),
+    "tg_flash_attn_fwd_layout": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
+                                        _i64, _f32, _i32, _i32, _vp]),
+    "tg_flash_attn_bwd_layout": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
+                                        _i64, _i64, _i64, _i64, _f32, _i32, _i32, _i32, _vp, _sz,
+                                        _vp]),
     "tg_flash_attn_bwd_workspace": (_sz, [_i64, _i64, _i64, _i64, _i64]),
     "tg_flash_attn_bwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
                                  _i64, _i64, _i64, _f32, _i32, _i32, _vp, _sz, _vp]),
@@ -571,35 +576,73 @@ def matmul2d(a, b, out=None, trans_a=False, trans_b=False, alpha=1.0, beta=0.0, 
 
 
 # ---------------------------------------------------------------- attention
-def flash_attn_fwd(q, k, v, scale, causal):
+def _fa_in(t, layout):
+    """True if t (B, H, S, D) has the strides of `layout` on every dimension longer
+    than 1 (0: contiguous (B, H, S, D); 1: contiguous (B, S, H, D) memory)."""
+    if t.dim() != 4:
+        return False
+    B, H, S, D = t.shape
+    want = (H * S * D, S * D, D, 1) if layout == 0 else (S * H * D, D, H * D, 1)
+    return all(n == 1 or st == w for n, st, w in zip(t.shape, t.stride(), want))
+
+
+def fa_layout(t):
+    """0 if t (B, H, S, D) is contiguous, 1 if it is the (0, 2, 1, 3) view of a contiguous
+    (B, S, H, D) tensor, else None."""
+    if _fa_in(t, 0):
+        return 0
+    if _fa_in(t, 1):
+        return 1
+    return None
+
+
+def fa_empty(B, H, S, D, dtype, device, layout):
+    """Uninitialised (B, H, S, D) tensor in the given memory layout."""
+    if layout == 1:
+        return torch.empty(B, S, H, D, dtype=dtype, device=device).permute(0, 2, 1, 3)
+    return torch.empty(B, H, S, D, dtype=dtype, device=device)
+
+
+def _fa_dev(t, name, layout):
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise TypeError(f"{name} must be a torch device tensor")
+    if not _fa_in(t, layout):
+        raise ValueError(f"{name} must be in layout {layout} "
+                         "(0: contiguous (B,H,S,D); 1: (B,S,H,D) memory)")
+
+
+def flash_attn_fwd(q, k, v, scale, causal, layout=0):
+    """o, lse = FlashAttention forward of (B, H, S, D) q/k/v in `layout`; o is returned in
+    the same layout, lse as (B, H, Sq) fp32."""
     for n, t in (("q", q), ("k", k), ("v", v)):
-        _dev(t, n)
+        _fa_dev(t, n, layout)
     B, H, Sq, D = q.shape
     Sk = k.shape[2]
     if k.shape != (B, H, Sk, D) or v.shape != (B, H, Sk, D):
         raise ValueError(f"flash_attn: k/v shape mismatch {tuple(k.shape)} {tuple(v.shape)}")
-    o = torch.empty_like(q)
+    o = fa_empty(B, H, Sq, D, q.dtype, q.device, layout)
     lse = torch.empty(B, H, Sq, dtype=torch.float32, device=q.device)
     ensure_device(q.device.index)
-    _check("tg_flash_attn_fwd", load().tg_flash_attn_fwd(
+    _check("tg_flash_attn_fwd", load().tg_flash_attn_fwd_layout(
         dtype_code(q), ptr(q), ptr(k), ptr(v), ptr(o), ptr(lse), B, H, Sq, Sk, D, float(scale),
-        int(bool(causal)), stream_handle()))
+        int(bool(causal)), int(layout), stream_handle()))
     return o, lse
 
 
-def flash_attn_bwd(q, k, v, o, do, lse, dq, dk, dv, scale, causal, accumulate):
-    for n, t in (("q", q), ("k", k), ("v", v), ("o", o), ("do", do), ("lse", lse), ("dq", dq),
-                 ("dk", dk), ("dv", dv)):
-        _dev(t, n)
+def flash_attn_bwd(q, k, v, o, do, lse, dq, dk, dv, scale, causal, accumulate, layout=0):
+    for n, t in (("q", q), ("k", k), ("v", v), ("o", o), ("do", do), ("dq", dq), ("dk", dk),
+                 ("dv", dv)):
+        _fa_dev(t, n, layout)
+    _dev(lse, "lse")
     B, H, Sq, D = q.shape
     Sk = k.shape[2]
     lib = load()
     ensure_device(q.device.index)
     ws = workspace(lib.tg_flash_attn_bwd_workspace(B, H, Sq, Sk, D), q.device)
-    _check("tg_flash_attn_bwd", lib.tg_flash_attn_bwd(
+    _check("tg_flash_attn_bwd", lib.tg_flash_attn_bwd_layout(
         dtype_code(q), ptr(q), ptr(k), ptr(v), ptr(o), ptr(do), ptr(lse), ptr(dq), ptr(dk),
         ptr(dv), B, H, Sq, Sk, D, float(scale), int(bool(causal)), int(bool(accumulate)),
-        ptr(ws), ws.numel(), stream_handle()))
+        int(layout), ptr(ws), ws.numel(), stream_handle()))
 
 
 def cross_entropy_fwd(logits, targets, label_smoothing=0.0):

@@ -128,3 +128,31 @@ def test_flash_rejects_bad_shapes(cuda):
     q = rnd((1, 1, 16, 96), torch.float16, 0)
     with pytest.raises(RuntimeError, match="head dim"):
         L().flash_attn_fwd(q, q, q, 0.1, False)
+
+
+@pytest.mark.parametrize("B,H,Sq,Sk,D", [(2, 3, 257, 513, 64), (1, 4, 192, 192, 128),
+                                         (2, 2, 1, 5, 64), (1, 1, 130, 70, 128)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_flash_bshd_layout_matches_contiguous(cuda, B, H, Sq, Sk, D, causal):
+    """(B,S,H,D) memory read and written in place (layout 1) gives bit-identical O,
+    LSE, dQ, dK, dV to the same values in contiguous (B,H,S,D) (layout 0): only the
+    addressing differs."""
+    g = torch.Generator(device="cuda").manual_seed(B * 7 + Sq + Sk)
+    mk = lambda S: torch.randn(B, S, H, D, device="cuda", generator=g).half()  # noqa: E731
+    qs, ks, vs, dos = mk(Sq), mk(Sk), mk(Sk), mk(Sq)
+    q1, k1, v1, do1 = (t.permute(0, 2, 1, 3) for t in (qs, ks, vs, dos))
+    q0, k0, v0, do0 = (t.contiguous() for t in (q1, k1, v1, do1))
+    s = D ** -0.5
+    o0, l0 = L().flash_attn_fwd(q0, k0, v0, s, causal, 0)
+    o1, l1 = L().flash_attn_fwd(q1, k1, v1, s, causal, 1)
+    assert L()._fa_in(o1, 1)
+    assert torch.equal(o0, o1) and torch.equal(l0, l1)
+    outs = []
+    for lay, (q, k, v, o, do) in ((0, (q0, k0, v0, o0, do0)), (1, (q1, k1, v1, o1, do1))):
+        dq = L().fa_empty(B, H, Sq, D, q.dtype, q.device, lay)
+        dk = L().fa_empty(B, H, Sk, D, q.dtype, q.device, lay)
+        dv = L().fa_empty(B, H, Sk, D, q.dtype, q.device, lay)
+        L().flash_attn_bwd(q, k, v, o, do, l0, dq, dk, dv, s, causal, False, lay)
+        outs.append((dq, dk, dv))
+    for a, b, n in zip(outs[0], outs[1], ("dq", "dk", "dv")):
+        assert torch.equal(a, b), n
