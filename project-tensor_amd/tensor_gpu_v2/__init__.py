@@ -14,6 +14,7 @@ from ._core import (Tensor, flash_attention, memory_info, multi_head_attention,
 from ._nn import (SGD, Adam, AdamW, BatchNorm2D, CrossEntropyLoss, Dropout, Embedding,
                   FusedBatchNormReLU, GradScaler, LayerNorm, Linear, Module, MSELoss,
                   clip_grad_norm_, clip_grad_value_)
-from ._training import FusedAdam, TiedWeight, sync_tied_gradients, weight_tie
+from ._training import (CHECKPOINT_VERSION, FusedAdam, TiedWeight, load_checkpoint,
+                        save_checkpoint, sync_tied_gradients, weight_tie)
 
 __version__ = "2.0.0+mi355x"
