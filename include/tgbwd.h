@@ -199,6 +199,14 @@ int tg_cross_entropy_bwd(int dtype, const void* logits, const int64_t* targets, 
                          int64_t N, int64_t C, float label_smoothing, float scale, int dtype_grad,
                          void* grad, int accumulate, void* stream);
 
+/* Embedding forward (Embedding.__call__, _nn.py:1076-1082): out[i, :] =
+ * weight[indices[i], :] converted to dtype_out (the autocast cast of the gathered
+ * rows folded into the gather).  Negative indices wrap by num_embeddings, as NumPy's;
+ * rows of indices outside [-num_embeddings, num_embeddings) are written as zeros (the
+ * caller checks host indices and raises IndexError, as the reference does). */
+int tg_embedding_fwd(int dtype_w, const void* weight, const int64_t* indices, int64_t n_tokens,
+                     int64_t dim, int64_t num_embeddings, int dtype_out, void* out,
+                     void* stream);
 /* Embedding backward (Embedding._backward, _nn.py:1083-1089): grad[idx[i]] (+)=
  * dout[i] for n_tokens rows of dim elements, grad [num_embeddings, dim].
  * Deterministic: a stable sort of the indices, then each index's rows summed in their

@@ -103,6 +103,64 @@ size_t sort_temp_bytes(int64_t n, int64_t V) {
   return bytes;
 }
 
+// Gather: out[i, :] = weight[idx[i], :] converted to the output dtype (negative
+// indices wrap by V; rows of indices outside [-V, V) are zero).  8 elements per thread,
+// 16-byte accesses when dim % 8 == 0 and both rows are 16-byte aligned.
+template <typename TW, typename TO, bool VEC>
+__global__ __launch_bounds__(kBlock) void k_embed_fwd(const TW* __restrict__ w,
+                                                      const int64_t* __restrict__ idx, int64_t n,
+                                                      int64_t dim, int64_t V,
+                                                      TO* __restrict__ out) {
+  const int64_t per = (dim + 7) / 8;  // 8-element groups per row
+  const int64_t total = n * per;
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  for (int64_t u = (int64_t)blockIdx.x * kBlock + threadIdx.x; u < total; u += stride) {
+    const int64_t i = u / per, c = (u % per) * 8;
+    int64_t r = idx[i];
+    if (r < 0) r += V;
+    const bool ok = r >= 0 && r < V;
+    const TW* src = w + (ok ? r : 0) * dim + c;
+    TO* dst = out + i * dim + c;
+    float f[8];
+    if (VEC) {
+#pragma unroll
+      for (int h = 0; h < 8 / tg_vec16<TW>::N; ++h) {
+        const tg_vec16<TW> v = tg_load16(src + h * tg_vec16<TW>::N);
+#pragma unroll
+        for (int j = 0; j < tg_vec16<TW>::N; ++j) f[h * tg_vec16<TW>::N + j] = ok ? tg_to_float(v.v[j]) : 0.f;
+      }
+#pragma unroll
+      for (int h = 0; h < 8 / tg_vec16<TO>::N; ++h) {
+        tg_vec16<TO> o;
+#pragma unroll
+        for (int j = 0; j < tg_vec16<TO>::N; ++j) o.v[j] = tg_from_float<TO>(f[h * tg_vec16<TO>::N + j]);
+        tg_store16(dst + h * tg_vec16<TO>::N, o);
+      }
+    } else {
+      for (int j = 0; j < 8 && c + j < dim; ++j)
+        dst[j] = tg_from_float<TO>(ok ? tg_to_float(src[j]) : 0.f);
+    }
+  }
+}
+
+template <typename TW, typename TO>
+int embed_fwd_t(const void* w, const int64_t* idx, int64_t n, int64_t dim, int64_t V, void* out,
+                hipStream_t s) {
+  const int64_t total = n * ((dim + 7) / 8);
+  int64_t blocks = (total + kBlock - 1) / kBlock;
+  const int64_t cap = (int64_t)tg_num_cus() * 16;
+  if (blocks > cap) blocks = cap;
+  if (blocks < 1) blocks = 1;
+  const bool vec = dim % 8 == 0 && tg_aligned16(w) && tg_aligned16(out);
+  if (vec)
+    k_embed_fwd<TW, TO, true><<<(unsigned)blocks, kBlock, 0, s>>>((const TW*)w, idx, n, dim, V,
+                                                                  (TO*)out);
+  else
+    k_embed_fwd<TW, TO, false><<<(unsigned)blocks, kBlock, 0, s>>>((const TW*)w, idx, n, dim, V,
+                                                                   (TO*)out);
+  return tg_check_launch("tg_embedding_fwd");
+}
+
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 template <typename TD, typename TG>
@@ -175,6 +233,33 @@ TG_EXPORT int tg_embedding_bwd(int dtype_dout, const void* dout, const int64_t* 
   }
 #undef G
   tg_set_error("tg_embedding_bwd: unsupported dtypes %d/%d", dtype_dout, dtype_grad);
+  return TG_ERR_UNSUPPORTED;
+}
+
+TG_EXPORT int tg_embedding_fwd(int dtype_w, const void* weight, const int64_t* indices,
+                               int64_t n_tokens, int64_t dim, int64_t num_embeddings,
+                               int dtype_out, void* out, void* stream) {
+  TG_REQUIRE(n_tokens >= 0 && dim >= 0 && num_embeddings > 0, "tg_embedding_fwd: bad shape");
+  if (n_tokens == 0 || dim == 0) return TG_OK;
+  TG_REQUIRE(weight && indices && out, "tg_embedding_fwd: null pointer");
+  hipStream_t s = tg_stream(stream);
+#define EF(TW)                                                                                 \
+  switch (dtype_out) {                                                                         \
+    case TG_F32: return embed_fwd_t<TW, float>(weight, indices, n_tokens, dim, num_embeddings, \
+                                               out, s);                                        \
+    case TG_F16: return embed_fwd_t<TW, tg_half>(weight, indices, n_tokens, dim,               \
+                                                 num_embeddings, out, s);                      \
+    case TG_BF16: return embed_fwd_t<TW, tg_bf16>(weight, indices, n_tokens, dim,              \
+                                                  num_embeddings, out, s);                     \
+  }                                                                                            \
+  break;
+  switch (dtype_w) {
+    case TG_F32: EF(float)
+    case TG_F16: EF(tg_half)
+    case TG_BF16: EF(tg_bf16)
+  }
+#undef EF
+  tg_set_error("tg_embedding_fwd: unsupported dtypes %d/%d", dtype_w, dtype_out);
   return TG_ERR_UNSUPPORTED;
 }
 

@@ -77,6 +77,7 @@ SIGNATURES = {
                                  _i64, _i64, _i64, _f32, _i32, _i32, _vp, _sz, _vp]),
     "tg_cross_entropy_fwd": (_i32, [_i32, _vp, _vp, _i64, _i64, _f32, _vp, _vp, _vp]),
     "tg_embedding_bwd_workspace": (_sz, [_i64, _i64]),
+    "tg_embedding_fwd": (_i32, [_i32, _vp, _vp, _i64, _i64, _i64, _i32, _vp, _vp]),
     "tg_embedding_bwd": (_i32, [_i32, _vp, _vp, _i64, _i64, _i32, _vp, _i64, _i32, _vp, _sz, _vp]),
     "tg_transpose_add": (_i32, [_i32, _vp, _i64, _i64, _i32, _vp, _f32, _vp]),
     "tg_cross_entropy_bwd": (_i32, [_i32, _vp, _vp, _vp, _i64, _i64, _f32, _f32, _i32, _vp, _i32,
@@ -674,6 +675,22 @@ def cross_entropy_bwd(logits, targets, lse, grad, scale, accumulate, label_smoot
     _check("tg_cross_entropy_bwd", load().tg_cross_entropy_bwd(
         dtype_code(logits), ptr(logits), ptr(targets), ptr(lse), N, C, float(label_smoothing),
         float(scale), dtype_code(grad), ptr(grad), int(bool(accumulate)), stream_handle()))
+
+
+def embedding_fwd(weight, indices, out_dtype=None):
+    """weight[indices] (indices int64 of any shape) as a new [..., dim] tensor of
+    out_dtype (default: weight's)."""
+    _dev(weight, "weight")
+    _dev(indices, "indices")
+    if weight.dim() != 2 or indices.dtype != torch.int64:
+        raise ValueError("embedding_fwd: weight must be [V, dim] and indices int64")
+    V, dim = weight.shape
+    out = torch.empty(*indices.shape, dim, dtype=out_dtype or weight.dtype, device=weight.device)
+    ensure_device(weight.device.index)
+    _check("tg_embedding_fwd", load().tg_embedding_fwd(
+        dtype_code(weight), ptr(weight), ptr(indices), indices.numel(), dim, V, dtype_code(out),
+        ptr(out), stream_handle()))
+    return out
 
 
 def embedding_bwd(dout, indices, grad, accumulate):

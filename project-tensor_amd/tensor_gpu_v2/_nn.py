@@ -362,12 +362,14 @@ class Embedding(Module):
             if host.size and (host.min() < -V or host.max() >= V):
                 raise IndexError(f"Embedding: index outside [-{V}, {V})")
             idx = torch.as_tensor(host.astype(np.int64), device=self.weight.data.device)
-        idx = idx.to(device=self.weight.data.device, dtype=torch.int64)
-        idx = torch.where(idx < 0, idx + V, idx)  # negative indices wrap, as NumPy's
+        idx = idx.to(device=self.weight.data.device, dtype=torch.int64).contiguous()
         weight = self.weight
-        out = Tensor._wrap(weight.data[idx], (weight,), "Embedding")
+        # gather and the dtype policy's cast in one kernel; negative indices wrap
+        w = weight.data if weight.data.is_contiguous() else weight.data.contiguous()
+        rows = L.embedding_fwd(w, idx, cfg.resolve_dtype(w.dtype))
+        out = Tensor._wrap(rows, (weight,), "Embedding")
         dim = self.embedding_dim
-        flat = idx.reshape(-1).contiguous()
+        flat = torch.where(idx < 0, idx + V, idx).reshape(-1)
         if out._requires_grad:
             def _backward():
                 if not weight._has_grad():

@@ -90,3 +90,20 @@ def test_sync_tied_gradients(cuda):
     head.w.grad = ht
     tg.sync_tied_gradients(model)
     assert_close(emb.weight.grad, 2.0 * ht.T.astype(np.float64), RTOL_F32, "accumulated")
+
+
+@pytest.mark.parametrize("dim,odt", [(1024, torch.float16), (64, torch.float32), (13, torch.bfloat16)])
+def test_embedding_fwd_gather(cuda, dim, odt):
+    """tg_embedding_fwd = weight[idx] cast to the output dtype, bit-exact with torch's
+    gather + cast; negative indices wrap, indices outside [-V, V) give zero rows."""
+    from tensor_gpu_v2 import _lib as L
+    V = 300
+    g = torch.Generator(device="cuda").manual_seed(dim)
+    w = torch.randn(V, dim, device="cuda", generator=g)
+    idx = torch.randint(-V, V, (5, 37), device="cuda", generator=g)
+    out = L.embedding_fwd(w, idx, odt)
+    want = w[torch.where(idx < 0, idx + V, idx)].to(odt)
+    assert out.shape == (5, 37, dim) and torch.equal(out, want)
+    bad = torch.tensor([V, -V - 1, 3], device="cuda")
+    o2 = L.embedding_fwd(w, bad, odt)
+    assert float(o2[:2].abs().sum()) == 0.0 and torch.equal(o2[2], w[3].to(odt))
