@@ -1047,12 +1047,207 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dq(
     store_c_tile<T>(dQ, rs, qblk + wave * 32, Sq, dt * 32 + l32, acc[dt], 1.f, accumulate, h);
 }
 
+// ---------------------------------------------------------------- forward, DMA-staged
+// One 32-key sub-tile of the forward for one wave (lane = query).  S^T = K Q^T (keys on
+// the accumulator rows), online softmax per lane, O^T += V^T P^T with V^T read by
+// transpose reads and P^T taken straight from the accumulator registers.  O^T is only
+// rescaled when some lane's running maximum rose by more than kLazy (log2 units): P is
+// then at most 2^kLazy against the stale maximum, O and l use the same maximum, and
+// the result is exact.
+constexpr float kLazy = 8.f;
+template <typename T, int D, bool MASK>
+__device__ __forceinline__ void fwd_sub(const char* ks, const char* vs, const LaneOffs<D>& o,
+                                        const typename Vec8<T>::type (&qf)[D / 16],
+                                        f32x16 (&acc)[D / 32], float sl2, float& m, float& l,
+                                        int thr) {
+  using V8 = typename Vec8<T>::type;
+  constexpr int DK = D / 16, DT = D / 32, RB = D * 2, PF = 4, NB = 2 * DT;
+  auto tr = [&](int n) {
+    const char* b = vs + (n / DT) * 16 * RB;
+    return lds_tr<T>(b + o.t[0][n % DT], b + o.t[1][n % DT]);
+  };
+  V8 ka[DK], bt[NB];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) ka[i] = lds_a<T>(ks + o.a[i]);
+  f32x16 sa;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) sa[r] = 0.f;
+  TG_SB();
+  int nt = 0;
+#pragma unroll
+  for (int k = 0; k < DK; ++k) {
+    sa = mfma(ka[k], qf[k], sa);
+    if (k + PF < DK) ka[k + PF] = lds_a<T>(ks + o.a[k + PF]);
+    else if (nt < NB) { bt[nt] = tr(nt); ++nt; }
+    TG_SB();
+  }
+  while (nt < NB) { bt[nt] = tr(nt); ++nt; }
+  // scores in log2 units, masked keys at -inf; this lane's 16 keys, then the other half
+  float x[16];
+  float mloc = -INFINITY;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    float v = sa[r] * sl2;
+    if (MASK) v = (8 * (r >> 2) + (r & 3) > thr) ? -INFINITY : v;
+    x[r] = v;
+    mloc = fmaxf(mloc, v);
+  }
+  mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+  // lazy rescale (uniform branch): only when some lane's maximum rose by > kLazy
+  const bool grow = mloc > m + kLazy;
+  if (__any(grow)) {
+    const float mn = fmaxf(m, mloc);
+    const float alpha = (m == -INFINITY) ? 0.f : fexp2(m - mn);
+    l *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
+    m = mn;
+  }
+  float p[16], ls = 0.f;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const float e = (m == -INFINITY) ? 0.f : fexp2(x[r] - m);
+    p[r] = e;
+    ls += e;
+  }
+  l += ls + __shfl_xor(ls, 32, 64);
+#pragma unroll
+  for (int sg = 0; sg < 2; ++sg) {
+    const V8 pb = pack8<T>(&p[8 * sg]);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc[dt] = mfma(bt[sg * DT + dt], pb, acc[dt]);
+  }
+}
+
+// Forward with DMA-staged K/V tiles.  grid = (ceil(Sq/128), B*H); one workgroup = 128
+// queries (4 waves x 32, Q fragments in registers) looping over key tiles of BN rows
+// double-buffered in swizzled LDS.  Writes O and the row log-sum-exp (natural log).
+template <typename T, int D, int BN, int OCC>
+__global__ __launch_bounds__(kThreads, OCC) void k_fa_fwd2(
+    const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V, T* __restrict__ O,
+    float* __restrict__ LSE, int64_t Sq, int64_t Sk, float scale, int causal, FaLay lay) {
+  constexpr int DK = D / 16, DT = D / 32, TB = BN * D * 2, RB = D * 2;
+  __shared__ __attribute__((aligned(1024))) char k0s[TB];
+  __shared__ __attribute__((aligned(1024))) char v0s[TB];
+  __shared__ __attribute__((aligned(1024))) char k1s[TB];
+  __shared__ __attribute__((aligned(1024))) char v1s[TB];
+  int64_t tile, bh;
+  fa_block(tile, bh);
+  Q += lay.head(bh, Sq, D);
+  O += lay.head(bh, Sq, D);
+  K += lay.head(bh, Sk, D);
+  V += lay.head(bh, Sk, D);
+  LSE += bh * Sq;
+  const int rs = lay.rs(D);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int h = lane >> 5, l32 = lane & 31;
+  // causal: the last query blocks carry the most keys, so they are dispatched first
+  const int64_t qb = causal ? (int64_t)gridDim.x - 1 - tile : tile;
+  const int64_t qblk = qb * 128;
+  const int64_t q = qblk + wave * 32 + l32;
+  const float sl2 = scale * kLog2e;
+  // A query lane past Sq reads a clamped row; its output row is never stored.
+  const int64_t qc = q < Sq ? q : Sq - 1;
+  typename Vec8<T>::type qf[DK];
+#pragma unroll
+  for (int ks = 0; ks < DK; ++ks) qf[ks] = ld8(Q + qc * rs + ks * 16 + h * 8);
+  f32x16 acc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
+  float m = -INFINITY, l = 0.f;
+  LaneOffs<D> o;
+  o.init(lane);
+  DmaPlan<T, D, BN> plan;
+  plan.init(lane, wave, rs);
+  int64_t kend = Sk;
+  if (causal) kend = (qblk + 128 < Sk) ? qblk + 128 : Sk;
+  // the sub-tiles of one staged key tile (first key k0); qk = first query of this wave
+  // minus k0
+  auto tile_fn = [&](const char* ks_, const char* vs_, int64_t k0) {
+    const int qk = (int)(qblk - k0) + wave * 32;
+#pragma unroll
+    for (int kt = 0; kt < BN / 32; ++kt) {
+      const int64_t kb0 = k0 + kt * 32;
+      if (kb0 >= Sk) break;
+      if (causal && kt * 32 > qk + 31) continue;  // wholly after this wave's queries
+      const bool diag = causal && kt * 32 + 31 > qk;
+      const bool edge = kb0 + 32 > Sk;
+      const char* kk = ks_ + kt * 32 * RB;
+      const char* vv = vs_ + kt * 32 * RB;
+      if (diag || edge) {
+        int thr = 1 << 30;
+        if (diag) thr = qk + l32 - kt * 32 - 4 * h;
+        if (edge) {
+          const int kb = (int)(Sk - kb0) - 4 * h - 1;
+          thr = kb < thr ? kb : thr;
+        }
+        fwd_sub<T, D, true>(kk, vv, o, qf, acc, sl2, m, l, thr);
+      } else {
+        fwd_sub<T, D, false>(kk, vv, o, qf, acc, sl2, m, l, 0);
+      }
+    }
+  };
+  if (kend > 0) {
+    plan.copy(K, 0, Sk, k0s);
+    plan.copy(V, 0, Sk, v0s);
+  }
+  for (int64_t k0 = 0; k0 < kend; k0 += 2 * BN) {
+    dma_wait();
+    __syncthreads();
+    const bool more1 = k0 + BN < kend;
+    if (more1) {
+      plan.copy(K, k0 + BN, Sk, k1s);
+      plan.copy(V, k0 + BN, Sk, v1s);
+    }
+    tile_fn(k0s, v0s, k0);
+    if (!more1) break;
+    dma_wait();
+    __syncthreads();
+    const bool more2 = k0 + 2 * BN < kend;
+    if (more2) {
+      plan.copy(K, k0 + 2 * BN, Sk, k0s);
+      plan.copy(V, k0 + 2 * BN, Sk, v0s);
+    }
+    tile_fn(k1s, v1s, k0 + BN);
+    if (!more2) break;
+  }
+  if (q < Sq) {
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        T w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = (T)(acc[dt][g * 4 + i] * inv);
+        *reinterpret_cast<uint2*>(O + q * rs + dt * 32 + g * 8 + h * 4) =
+            *reinterpret_cast<const uint2*>(w);
+      }
+    if (h == 0) LSE[q] = (m + log2f(l)) / kLog2e;
+  }
+}
+
+template <int D> struct FwdCfg;
+template <> struct FwdCfg<64> { static constexpr int BN = 64, OCC = 3; };
+template <> struct FwdCfg<128> { static constexpr int BN = 64, OCC = 2; };
+#ifndef TG_FA_FWD2
+#define TG_FA_FWD2 1
+#endif
+
 template <typename T, int D>
 int fwd_t(const void* q, const void* k, const void* v, void* o, float* lse, int64_t BH,
           int64_t Sq, int64_t Sk, float scale, int causal, FaLay lay, hipStream_t s) {
   dim3 grid((unsigned)((Sq + 127) / 128), (unsigned)BH);
-  k_fa_fwd<T, D><<<grid, kThreads, 0, s>>>((const T*)q, (const T*)k, (const T*)v, (T*)o, lse, Sq,
-                                           Sk, scale, causal, lay);
+  if (TG_FA_FWD2)
+    k_fa_fwd2<T, D, FwdCfg<D>::BN, FwdCfg<D>::OCC><<<grid, kThreads, 0, s>>>(
+        (const T*)q, (const T*)k, (const T*)v, (T*)o, lse, Sq, Sk, scale, causal, lay);
+  else
+    k_fa_fwd<T, D><<<grid, kThreads, 0, s>>>((const T*)q, (const T*)k, (const T*)v, (T*)o, lse,
+                                             Sq, Sk, scale, causal, lay);
   return tg_check_launch("tg_flash_attn_fwd");
 }
 
