@@ -197,14 +197,18 @@ class Tensor:
 
     def _share_grad(self, donor, g):
         """First gradient of this node is `g`, a read-only view of donor's gradient
-        buffer (the reshape/view/add pass-through).  Adopted without a copy; both
-        nodes are marked shared, so the first in-place write to either one copies
-        (out of place for an accumulation, which moves no more bytes than the
+        buffer (the reshape/view/transpose/add pass-through).  Adopted without a copy,
+        also when it is a permuted view of a dense buffer (a transpose's gradient);
+        both nodes are marked shared, so the first in-place write to either one
+        copies (out of place for an accumulation, which moves no more bytes than the
         in-place one would)."""
-        if not self._gz or g.dtype != self.data.dtype or not g.is_contiguous():
+        if not self._gz or g.dtype != self.data.dtype or not (g.is_contiguous() or _dense(g)):
             self._accumulate(g)
             return
         if g.shape != self.data.shape:
+            if not g.is_contiguous():  # a strided buffer is only adopted in its own shape
+                self._accumulate(g)
+                return
             g = g.reshape(self.data.shape)
         self._g = g
         self._gz = False
