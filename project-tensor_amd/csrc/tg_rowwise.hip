@@ -403,11 +403,17 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_reg(
   // Every group iterates the same number of times so block barriers stay uniform.
   const int64_t stride = (int64_t)gridDim.x * G;
   const int64_t iters = (rows + stride - 1) / stride;
-  // Software pipeline: the next row's x/dy/mean/rstd are in flight while the
-  // current row is reduced and written.
-  tg_vec16<T> nxa[VPT], nya[VPT];
-  float nmu = 0.f, nrs = 0.f;
-  auto fetch = [&](int64_t it) {
+  // Software pipeline: the next row's x/dy (and, when accumulating, the old dx, for
+  // rows that leave room for it) and mean/rstd are loaded while the current row is
+  // reduced and written; two rows ahead when that fits in registers.  Row buffers are whole structs copied by value, so
+  // every register index is known at compile time.
+  struct RowBuf {
+    tg_vec16<T> x[VPT], y[VPT], o[ACC ? VPT : 1];
+    float mu, rs;
+  };
+  constexpr bool kPreO = ACC && VPT <= 4;  // wider rows load the old dx late (no spill)
+  constexpr int kDepth = (ACC ? VPT <= 2 : VPT <= 4) ? 2 : 1;
+  auto fetch = [&](int64_t it, RowBuf& b) {
     const int64_t row = it * stride + (int64_t)blockIdx.x * G + grp;
     if (row < rows) {
       const int64_t off = row * (int64_t)cols;
@@ -415,27 +421,20 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_reg(
       for (int k = 0; k < VPT; ++k) {
         const int vi = t + k * TPR;
         if (vi < nv) {
-          nxa[k] = tg_load16(x + off + vi * V);
-          nya[k] = tg_load16(dy + off + vi * V);
+          b.x[k] = tg_load16(x + off + vi * V);
+          b.y[k] = tg_load16(dy + off + vi * V);
+          if (kPreO) b.o[k] = tg_load16(dx + off + vi * V);
         }
       }
-      nmu = mean[row];
-      nrs = rstd[row];
+      b.mu = mean[row];
+      b.rs = rstd[row];
     }
   };
-  if (iters > 0) fetch(0);
-  for (int64_t it = 0; it < iters; ++it) {
+  auto body = [&](int64_t it, const RowBuf& b) {
     const int64_t row = it * stride + (int64_t)blockIdx.x * G + grp;
     const bool live = row < rows;
     const int64_t off = (live ? row : 0) * (int64_t)cols;
-    const float mu = nmu, rs = nrs;
-    tg_vec16<T> xa[VPT], ya[VPT];
-#pragma unroll
-    for (int k = 0; k < VPT; ++k) {
-      xa[k] = nxa[k];
-      ya[k] = nya[k];
-    }
-    if (it + 1 < iters) fetch(it + 1);
+    const float mu = b.mu, rs = b.rs;
     float xh[VPT][V], dyv[VPT][V];
     float sums[2] = {0.f, 0.f};
 #pragma unroll
@@ -444,8 +443,8 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_reg(
       if (live && vi < nv) {
 #pragma unroll
         for (int j = 0; j < V; ++j) {
-          xh[k][j] = (tg_to_float(xa[k].v[j]) - mu) * rs;
-          dyv[k][j] = tg_to_float(ya[k].v[j]);
+          xh[k][j] = (tg_to_float(b.x[k].v[j]) - mu) * rs;
+          dyv[k][j] = tg_to_float(b.y[k].v[j]);
           const float g = dyv[k][j] * gam[k][j];
           sums[0] += g;
           sums[1] += g * xh[k][j];
@@ -468,17 +467,39 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_reg(
         const int vi = t + k * TPR;
         if (vi < nv) {
           tg_vec16<T> o;
-          if (ACC) o = tg_load16(dx + off + vi * V);
+          if (ACC && !kPreO) o = tg_load16(dx + off + vi * V);
 #pragma unroll
           for (int j = 0; j < V; ++j) {
             float r = rs * (dyv[k][j] * gam[k][j] - mg - xh[k][j] * mgx);
-            if (ACC) r += tg_to_float(o.v[j]);
+            if (ACC) r += tg_to_float(kPreO ? b.o[k].v[j] : o.v[j]);
             o.v[j] = tg_from_float<T>(r);
           }
           if (nt) tg_store16_nt(dx + off + vi * V, o);
           else tg_store16(dx + off + vi * V, o);
         }
       }
+    }
+  };
+  RowBuf ra, cur;
+  if (iters > 0) fetch(0, ra);
+  if constexpr (kDepth == 2) {
+    RowBuf rb;
+    if (iters > 1) fetch(1, rb);
+    for (int64_t it = 0; it < iters; it += 2) {
+      cur = ra;
+      if (it + 2 < iters) fetch(it + 2, ra);
+      body(it, cur);
+      if (it + 1 < iters) {  // uniform across the block, as iters is
+        cur = rb;
+        if (it + 3 < iters) fetch(it + 3, rb);
+        body(it + 1, cur);
+      }
+    }
+  } else {
+    for (int64_t it = 0; it < iters; ++it) {
+      cur = ra;
+      if (it + 1 < iters) fetch(it + 1, ra);
+      body(it, cur);
     }
   }
   // Combine the G row groups of this block, then write the block partial.
@@ -606,10 +627,13 @@ int64_t colsum_splits(int64_t rows, int64_t cols) {
   return want;
 }
 
-// Row-groups per LayerNorm-backward launch (the number of dgamma/dbeta partials).
+// Row-groups per LayerNorm-backward launch (the number of dgamma/dbeta partials): one
+// block per CU.  Measured on the MI355X against two and three per CU, one is faster at
+// every shape tried (fewer partials to write and finish; the two-row prefetch keeps
+// enough loads in flight).
 int64_t ln_bwd_blocks(int64_t rows, int tpr) {
   const int64_t g = kBlock / tpr;
-  int64_t want = 2 * (int64_t)tg_num_cus();
+  int64_t want = (int64_t)tg_num_cus();
   const int64_t maxb = (rows + g - 1) / g;
   if (want > maxb) want = maxb;
   if (want < 1) want = 1;
@@ -813,6 +837,10 @@ TG_EXPORT int tg_reduce_rows(int dtype_in, const void* in, int dtype_out, void* 
     return tg_sum_partials(nullptr, 0, cols, dtype_out, out, 0, nullptr, s);
   }
   TG_REQUIRE(in, "tg_reduce_rows: null input");
+  // A few fp32 rows over many columns (split-K GEMM partials): the finishing column
+  // sum reads them directly, one launch instead of partials plus a copy.
+  if (dtype_in == TG_F32 && rows <= 64 && cols >= 4096)
+    return tg_sum_partials((const float*)in, rows, cols, dtype_out, out, accumulate, nullptr, s);
   const int64_t ns = colsum_splits(rows, cols);
   const size_t need = (size_t)(ns * cols) * sizeof(float) + tg_sum_partials_scratch(ns, cols);
   if (!workspace || workspace_bytes < need) {

@@ -454,14 +454,17 @@ def grad_norm(grads, norm_kind, p=2.0):
         sub = [grads[i] for i in idx]
         numel = _numel_array(sub)
         ws = workspace(lib.tg_grad_norm_workspace(len(sub), numel), dev)
-        out = torch.empty(1, dtype=torch.float64, device=dev)
-        fl = torch.empty(len(sub), dtype=torch.int32, device=dev)
+        # value (fp64) and flags share one buffer: one device-to-host copy per group
+        buf = torch.empty(2 + len(sub), dtype=torch.int32, device=dev)
+        out = buf[:2].view(torch.float64)
+        fl = buf[2:]
         _check("tg_grad_norm", lib.tg_grad_norm(
             len(sub), dtype_code(sub[0]), _ptr_array(sub), numel, int(norm_kind), float(p),
             ptr(out), ptr(fl), ptr(ws), ws.numel(), stream_handle()))
-        v = float(out.cpu()[0])
+        host = buf.cpu()
+        v = float(host[:2].view(torch.float64)[0])
         total = max(total, v) if norm_kind == 1 else total + v
-        for j, f in enumerate(fl.cpu().tolist()):
+        for j, f in enumerate(host[2:].tolist()):
             flags_out[idx[j]] = f
     return total, flags_out
 

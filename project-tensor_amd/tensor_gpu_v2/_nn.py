@@ -5,6 +5,7 @@ LayerNorm, BatchNorm2D / FusedBatchNormReLU, Adam/AdamW, clip_grad_norm_,
 GradScaler — run their gradient math in libtgbwd's HIP kernels.
 """
 import math
+import types
 import warnings
 
 import numpy as np
@@ -29,6 +30,35 @@ def _targets(tensors):
 
 
 # ============================================================================ Module
+_CLASS_NAMES = {}
+
+
+def _walk_names(obj):
+    """The public names ``dir(obj)`` lists, in its sorted order, minus those that are
+    plain functions (or static/class methods) on the class and not shadowed by an
+    instance attribute: those yield bound methods, never a Tensor, Module or list.
+    Properties and class-level data are kept and evaluated by the caller."""
+    cls = type(obj)
+    names = _CLASS_NAMES.get(cls)
+    if names is None:
+        names = set()
+        for name in dir(cls):
+            if name.startswith("_"):
+                continue
+            for k in cls.__mro__:
+                if name in k.__dict__:
+                    if not isinstance(k.__dict__[name],
+                                      (types.FunctionType, staticmethod, classmethod)):
+                        names.add(name)
+                    break
+        names = frozenset(names)
+        _CLASS_NAMES[cls] = names
+    inst = getattr(obj, "__dict__", None)
+    if inst:
+        return sorted(names.union(n for n in inst if not n.startswith("_")))
+    return sorted(names)
+
+
 class Module:
     """Module base (_nn.py:24-255): parameter discovery over public attributes."""
 
@@ -49,9 +79,7 @@ class Module:
 
     def named_parameters(self):
         params, seen = [], set()
-        for name in dir(self):
-            if name.startswith("_"):
-                continue
+        for name in _walk_names(self):
             try:
                 attr = getattr(self, name)
             except AttributeError:

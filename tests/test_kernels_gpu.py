@@ -127,7 +127,10 @@ def test_softmax_golden(cuda):
 
 
 # ------------------------------------------------------------------ layer norm
-LN_SHAPES = [(1, 8), (37, 1024), (8, 4096), (3, 100), (2, 20000), (300, 256), (5, 8192)]
+LN_SHAPES = [(1, 8), (37, 1024), (8, 4096), (3, 100), (2, 20000), (300, 256), (5, 8192),
+             # several rows per block (one block per CU): odd and even iteration counts,
+             # a partial last round, both prefetch depths
+             (773, 4096), (2309, 512), (2048, 1024)]
 
 
 def ln_ref(x, g, b, dy, eps=1e-5):
@@ -160,20 +163,25 @@ def test_layernorm_fp32(cuda, shape, acc):
 
 
 @pytest.mark.parametrize("dt", F16S)
-def test_layernorm_half(cuda, dt):
-    rng = np.random.default_rng(4)
-    x = dev(rng.standard_normal((64, 1024)), dt)
-    g = dev(1 + 0.02 * rng.standard_normal(1024))
-    b = dev(0.02 * rng.standard_normal(1024))
-    dy = dev(rng.standard_normal((64, 1024)), dt)
+@pytest.mark.parametrize("rows,cols,acc", [(64, 1024, False), (2309, 1024, True),
+                                           (1029, 4096, True), (600, 8192, False)])
+def test_layernorm_half(cuda, dt, rows, cols, acc):
+    rng = np.random.default_rng(4 + rows)
+    x = dev(rng.standard_normal((rows, cols)), dt)
+    g = dev(1 + 0.02 * rng.standard_normal(cols))
+    b = dev(0.02 * rng.standard_normal(cols))
+    dy = dev(rng.standard_normal((rows, cols)), dt)
     y, mean, rstd = L().layernorm_fwd(x, g, b, 1e-5)
     yr, dxr, dgr, dbr = ln_ref(f64(x), f64(g), f64(b), f64(dy))
     assert_close(y, yr, RTOL_F16, "ln fwd half")
-    dx = torch.empty_like(x)
+    bx = dev(rng.standard_normal((rows, cols)), dt)
+    dx = bx.clone() if acc else torch.empty_like(x)
     dg, db = torch.empty_like(g), torch.empty_like(b)
-    L().layernorm_bwd(x, mean, rstd, g, dy, dx, dg, db, False, False)
-    assert_close(dx, dxr, RTOL_F16, "ln dx half")
+    L().layernorm_bwd(x, mean, rstd, g, dy, dx, dg, db, acc, False)
+    a = 1.0 if acc else 0.0
+    assert_close(dx, dxr + a * f64(bx), RTOL_F16, "ln dx half")
     assert_close(dg, dgr, RTOL_F16, "ln dgamma half")
+    assert_close(db, dbr, RTOL_F16, "ln dbeta half")
 
 
 def test_layernorm_golden(cuda):
@@ -250,7 +258,8 @@ def test_batchnorm_accumulate_and_golden(cuda):
 
 
 # ------------------------------------------------------------------ column sums
-@pytest.mark.parametrize("rows,cols", [(1, 1), (32, 10), (8192, 1024), (1000, 4097), (3, 40000)])
+@pytest.mark.parametrize("rows,cols", [(1, 1), (32, 10), (8192, 1024), (1000, 4097), (3, 40000),
+                                       (64, 8192), (8, 4098), (65, 4096)])
 @pytest.mark.parametrize("dt", [torch.float32, torch.float16])
 def test_reduce_rows(cuda, rows, cols, dt):
     rng = np.random.default_rng(rows + cols)
