@@ -617,6 +617,74 @@ __global__ __launch_bounds__(kBlock) void k_colsum_partial(const TI* __restrict_
   part[(int64_t)blockIdx.y * cols + c] = (s0 + s1) + (s2 + s3);
 }
 
+// Stage 1 with 16-byte loads, for a [rows, cols] input with cols % V == 0 and a
+// 16-byte aligned base: a block covers 64 vector columns (one per lane, so a wave
+// reads a contiguous 1 KiB row segment for 16-bit input); its 4 waves take rows
+// r0+w, r0+w+4, ... of the block's split with four loads in flight; the wave sums
+// are combined through LDS in a fixed order (deterministic).
+template <typename TI>
+__global__ __launch_bounds__(kBlock) void k_colsum_partial_v(const TI* __restrict__ in,
+                                                             float* __restrict__ part,
+                                                             int64_t rows, int64_t cols,
+                                                             int64_t per) {
+  constexpr int V = tg_vec16<TI>::N;
+  constexpr int W = kBlock / 64;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t nvc = cols / V;
+  const int64_t cv = (int64_t)blockIdx.x * 64 + lane;
+  const int64_t r0 = (int64_t)blockIdx.y * per;
+  const int64_t r1 = r0 + per < rows ? r0 + per : rows;
+  float acc[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) acc[j] = 0.f;
+  if (cv < nvc) {
+    const TI* p = in + cv * V;
+    int64_t r = r0 + wave;
+    for (; r + 3 * W < r1; r += 4 * W) {
+      tg_vec16<TI> v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = tg_load16(p + (r + u * W) * cols);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int j = 0; j < V; ++j) acc[j] += tg_to_float(v[u].v[j]);
+    }
+    for (; r < r1; r += W) {
+      const tg_vec16<TI> v = tg_load16(p + r * cols);
+#pragma unroll
+      for (int j = 0; j < V; ++j) acc[j] += tg_to_float(v.v[j]);
+    }
+  }
+  __shared__ float red[W - 1][V][64];
+  if (wave > 0) {
+#pragma unroll
+    for (int j = 0; j < V; ++j) red[wave - 1][j][lane] = acc[j];
+  }
+  __syncthreads();
+  if (wave == 0 && cv < nvc) {
+#pragma unroll
+    for (int w = 0; w < W - 1; ++w)
+#pragma unroll
+      for (int j = 0; j < V; ++j) acc[j] += red[w][j][lane];
+    float* o = part + (int64_t)blockIdx.y * cols + cv * V;
+#pragma unroll
+    for (int j = 0; j < V; j += 4)
+      *reinterpret_cast<float4*>(o + j) = make_float4(acc[j], acc[j + 1], acc[j + 2], acc[j + 3]);
+  }
+}
+
+// Row splits of tg_reduce_rows: enough blocks to fill the CUs (counted in 512-column
+// tiles, the vector kernel's width for 16-bit input) with at least 32 rows per split.
+int64_t rr_splits(int64_t rows, int64_t cols) {
+  const int64_t ctiles = (cols + 511) / 512;
+  int64_t want = (4 * (int64_t)tg_num_cus() + ctiles - 1) / ctiles;
+  int64_t maxs = rows / 32;
+  if (want > maxs) want = maxs;
+  if (want > 2048) want = 2048;
+  if (want < 1) want = 1;
+  return want;
+}
+
 int64_t colsum_splits(int64_t rows, int64_t cols) {
   const int64_t ctiles = (cols + kBlock - 1) / kBlock;
   int64_t want = (4 * (int64_t)tg_num_cus() + ctiles - 1) / ctiles;
@@ -818,7 +886,7 @@ TG_EXPORT int tg_layernorm_bwd(int dtype, const void* x, const float* mean, cons
 
 TG_EXPORT size_t tg_reduce_rows_workspace(int64_t rows, int64_t cols) {
   if (rows <= 0 || cols <= 0) return 0;
-  const int64_t ns = colsum_splits(rows, cols);
+  const int64_t ns = rr_splits(rows, cols);
   return (size_t)(ns * cols) * sizeof(float) + tg_sum_partials_scratch(ns, cols);
 }
 
@@ -841,7 +909,7 @@ TG_EXPORT int tg_reduce_rows(int dtype_in, const void* in, int dtype_out, void* 
   // sum reads them directly, one launch instead of partials plus a copy.
   if (dtype_in == TG_F32 && rows <= 64 && cols >= 4096)
     return tg_sum_partials((const float*)in, rows, cols, dtype_out, out, accumulate, nullptr, s);
-  const int64_t ns = colsum_splits(rows, cols);
+  const int64_t ns = rr_splits(rows, cols);
   const size_t need = (size_t)(ns * cols) * sizeof(float) + tg_sum_partials_scratch(ns, cols);
   if (!workspace || workspace_bytes < need) {
     tg_set_error("tg_reduce_rows: workspace of %zu bytes needed, got %zu", need,
@@ -849,6 +917,20 @@ TG_EXPORT int tg_reduce_rows(int dtype_in, const void* in, int dtype_out, void* 
     return TG_ERR_WORKSPACE;
   }
   float* part = (float*)workspace;
+  const int64_t per = (rows + ns - 1) / ns;
+  const int vw = dtype_in == TG_F32 ? 4 : 8;  // elements per 16-byte vector
+  if ((dtype_in == TG_F32 || dtype_in == TG_F16 || dtype_in == TG_BF16) && cols % vw == 0 &&
+      tg_aligned16(in)) {
+    dim3 gv((unsigned)((cols / vw + 63) / 64), (unsigned)ns);
+    switch (dtype_in) {
+      case TG_F32: k_colsum_partial_v<float><<<gv, kBlock, 0, s>>>((const float*)in, part, rows, cols, per); break;
+      case TG_F16: k_colsum_partial_v<tg_half><<<gv, kBlock, 0, s>>>((const tg_half*)in, part, rows, cols, per); break;
+      default: k_colsum_partial_v<tg_bf16><<<gv, kBlock, 0, s>>>((const tg_bf16*)in, part, rows, cols, per); break;
+    }
+    int st = tg_check_launch("tg_reduce_rows");
+    if (st) return st;
+    return tg_sum_partials(part, ns, cols, dtype_out, out, accumulate, part + ns * cols, s);
+  }
   dim3 grid((unsigned)((cols + kBlock - 1) / kBlock), (unsigned)ns);
   switch (dtype_in) {
     case TG_F32: k_colsum_partial<float><<<grid, kBlock, 0, s>>>((const float*)in, part, rows, cols); break;

@@ -259,8 +259,9 @@ def test_batchnorm_accumulate_and_golden(cuda):
 
 # ------------------------------------------------------------------ column sums
 @pytest.mark.parametrize("rows,cols", [(1, 1), (32, 10), (8192, 1024), (1000, 4097), (3, 40000),
-                                       (64, 8192), (8, 4098), (65, 4096)])
-@pytest.mark.parametrize("dt", [torch.float32, torch.float16])
+                                       (64, 8192), (8, 4098), (65, 4096), (8192, 4096),
+                                       (777, 1000), (40, 24)])
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16, torch.bfloat16])
 def test_reduce_rows(cuda, rows, cols, dt):
     rng = np.random.default_rng(rows + cols)
     g = dev(rng.standard_normal((rows, cols)), dt)
