@@ -122,6 +122,18 @@ int tg_adam_step(int ntensors, float* const* params, const float* const* grads,
                  const int64_t* numel, double lr, double beta1, double beta2, double eps,
                  double weight_decay, double bias_correction1, double bias_correction2,
                  void* stream);
+/* tg_adam_step that also writes each updated parameter, rounded to lowp_dtype (fp16
+ * or bf16 code), to lowp[i] where lowp[i] != NULL.  Replaces the per-forward weight
+ * cast of autocast (_core.py:185-191 casts every fp32 parameter to fp16 when the
+ * forward reads it): the copy is produced in the optimizer pass that changes the
+ * weights, so the next forward finds it current.  No reference counterpart of its
+ * own; results of the update are those of tg_adam_step. */
+int tg_adam_step_lowp(int ntensors, float* const* params, const float* const* grads,
+                      float* const* exp_avg, float* const* exp_avg_sq,
+                      float* const* max_exp_avg_sq, const int64_t* numel, double lr,
+                      double beta1, double beta2, double eps, double weight_decay,
+                      double bias_correction1, double bias_correction2, int lowp_dtype,
+                      void* const* lowp, void* stream);
 /* GradScaler.unscale_ (_nn.py:1795-1833): g *= mul (if write); flags[i] (device,
  * cleared first) |= 1 if tensor i had a non-finite value, |= 2 if the scaled
  * tensor has one. */

@@ -29,6 +29,7 @@ struct MtArgs {
   void* c[kMaxT];  // exp_avg
   void* d[kMaxT];  // exp_avg_sq
   void* e[kMaxT];  // max_exp_avg_sq (AMSGrad) or null
+  void* f[kMaxT];  // low-precision copy of the updated param (Adam) or null
   int64_t n[kMaxT];
   int64_t first_block[kMaxT + 1];
   int fidx[kMaxT];  // index of each tensor in the caller's list (flag slot)
@@ -122,11 +123,31 @@ struct AdamConsts {
   int decay;
 };
 
-template <bool AMS, bool FULL>
+// The 4 fp32 elements a thread owns in an Adam chunk (ChunkMap<float, 4>: elements
+// start + 4*tid .. +3), stored as 4 low-precision values: one 8-byte store when FULL.
+template <typename TL, bool FULL>
+__device__ __forceinline__ void store_lowp4(TL* __restrict__ p, int64_t start, int64_t end,
+                                            const float (&x)[4]) {
+  const int64_t i0 = start + (int64_t)threadIdx.x * 4;
+  if (FULL) {
+    TL v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = tg_from_float<TL>(x[k]);
+    *reinterpret_cast<uint2*>(p + i0) = *reinterpret_cast<const uint2*>(v);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (i0 + k < end) p[i0 + k] = tg_from_float<TL>(x[k]);
+  }
+}
+
+// LP: 0 = no low-precision copy, 1 = fp16 copy, 2 = bf16 copy of the updated param
+// (written in the same pass, so the next autocast forward needs no cast launch).
+template <bool AMS, bool FULL, int LP = 0>
 __device__ __forceinline__ void adam_chunk(float* __restrict__ p, const float* __restrict__ g,
                                            float* __restrict__ m, float* __restrict__ v,
-                                           float* __restrict__ vm, int64_t start, int64_t end,
-                                           const AdamConsts& K) {
+                                           float* __restrict__ vm, void* __restrict__ lp,
+                                           int64_t start, int64_t end, const AdamConsts& K) {
   constexpr int E = kAdamEPT;
   float P[E], G[E], Mv[E], Vv[E], VM[E];
   load_chunk<float, FULL, E>(p, start, end, P);
@@ -153,12 +174,15 @@ __device__ __forceinline__ void adam_chunk(float* __restrict__ p, const float* _
     Vv[i] = vv;
   }
   store_chunk<float, FULL, E, true>(p, start, end, P);
+  static_assert(E == 4, "store_lowp4 covers four elements per thread");
+  if (LP == 1 && lp) store_lowp4<tg_half, FULL>((tg_half*)lp, start, end, P);
+  if (LP == 2 && lp) store_lowp4<tg_bf16, FULL>((tg_bf16*)lp, start, end, P);
   store_chunk<float, FULL, E, true>(m, start, end, Mv);
   store_chunk<float, FULL, E, true>(v, start, end, Vv);
   if (AMS) store_chunk<float, FULL, E, true>(vm, start, end, VM);
 }
 
-template <bool AMS>
+template <bool AMS, int LP = 0>
 __global__ __launch_bounds__(kBlock) void k_adam(MtArgs A, AdamConsts K) {
   const int t = find_tensor(A, blockIdx.x);
   const int64_t n = A.n[t];
@@ -169,10 +193,11 @@ __global__ __launch_bounds__(kBlock) void k_adam(MtArgs A, AdamConsts K) {
   float* m = (float*)A.c[t];
   float* v = (float*)A.d[t];
   float* vm = (float*)A.e[t];
+  void* lp = LP ? A.f[t] : nullptr;
   const bool full = start + kAdamChunk <= n && al16(p) && al16(g) && al16(m) && al16(v) &&
-                    (!AMS || al16(vm));
-  if (full) adam_chunk<AMS, true>(p, g, m, v, vm, start, end, K);
-  else adam_chunk<AMS, false>(p, g, m, v, vm, start, end, K);
+                    (!AMS || al16(vm)) && (reinterpret_cast<uintptr_t>(lp) & 7) == 0;
+  if (full) adam_chunk<AMS, true, LP>(p, g, m, v, vm, lp, start, end, K);
+  else adam_chunk<AMS, false, LP>(p, g, m, v, vm, lp, start, end, K);
 }
 
 // ---------------------------------------------------------------------------
@@ -315,8 +340,8 @@ __global__ void k_zero_ints(int* p, int n) {
 // first tensor index) per launch.  Empty tensors are skipped.
 template <typename F>
 int for_each_launch(int ntensors, void* const* a, void* const* b, void* const* c,
-                    void* const* d, void* const* e, const int64_t* numel, F&& fn,
-                    int64_t chunk = kChunk) {
+                    void* const* d, void* const* e, void* const* f, const int64_t* numel,
+                    F&& fn, int64_t chunk = kChunk) {
   MtArgs A{};
   int64_t blocks = 0;
   auto flush = [&]() -> int {
@@ -349,6 +374,7 @@ int for_each_launch(int ntensors, void* const* a, void* const* b, void* const* c
     A.c[k] = c ? c[i] : nullptr;
     A.d[k] = d ? d[i] : nullptr;
     A.e[k] = e ? e[i] : nullptr;
+    A.f[k] = f ? f[i] : nullptr;
     A.n[k] = numel[i];
     A.fidx[k] = i;
     A.first_block[k] = blocks;
@@ -366,18 +392,27 @@ int64_t total_blocks(int ntensors, const int64_t* numel) {
 
 }  // namespace
 
-TG_EXPORT int tg_adam_step(int ntensors, float* const* params, const float* const* grads,
-                           float* const* exp_avg, float* const* exp_avg_sq,
-                           float* const* max_exp_avg_sq, const int64_t* numel, double lr,
-                           double beta1, double beta2, double eps, double weight_decay,
-                           double bias_correction1, double bias_correction2, void* stream) {
-  TG_REQUIRE(ntensors >= 0, "tg_adam_step: negative tensor count");
+namespace {
+
+int adam_step_impl(const char* who, int ntensors, float* const* params,
+                   const float* const* grads, float* const* exp_avg, float* const* exp_avg_sq,
+                   float* const* max_exp_avg_sq, const int64_t* numel, double lr, double beta1,
+                   double beta2, double eps, double weight_decay, double bias_correction1,
+                   double bias_correction2, int lowp_dtype, void* const* lowp, void* stream) {
+  TG_REQUIRE(ntensors >= 0, "%s: negative tensor count", who);
   if (ntensors == 0) return TG_OK;
-  TG_REQUIRE(params && grads && exp_avg && exp_avg_sq && numel, "tg_adam_step: null list");
+  TG_REQUIRE(params && grads && exp_avg && exp_avg_sq && numel, "%s: null list", who);
   for (int i = 0; i < ntensors; ++i)
     TG_REQUIRE(numel[i] == 0 || (params[i] && grads[i] && exp_avg[i] && exp_avg_sq[i] &&
                                  (!max_exp_avg_sq || max_exp_avg_sq[i])),
-               "tg_adam_step: null pointer for tensor %d", i);
+               "%s: null pointer for tensor %d", who, i);
+  int lp = 0;
+  if (lowp) {
+    TG_REQUIRE(lowp_dtype == TG_F16 || lowp_dtype == TG_BF16,
+               "%s: low-precision copies must be float16 or bfloat16 (dtype %d)", who,
+               lowp_dtype);
+    lp = lowp_dtype == TG_F16 ? 1 : 2;
+  }
   hipStream_t s = tg_stream(stream);
   const bool ams = max_exp_avg_sq != nullptr;
   // Scalars are combined in double and rounded once to fp32, as the reference's
@@ -396,15 +431,45 @@ TG_EXPORT int tg_adam_step(int ntensors, float* const* params, const float* cons
   K.ibc2 = (float)(1.0 / bias_correction2);
   return for_each_launch(
       ntensors, (void* const*)params, (void* const*)grads, (void* const*)exp_avg,
-      (void* const*)exp_avg_sq, (void* const*)max_exp_avg_sq, numel,
+      (void* const*)exp_avg_sq, (void* const*)max_exp_avg_sq, lowp, numel,
       [&](const MtArgs& A, int64_t nb) {
-        if (ams)
-          k_adam<true><<<(unsigned)nb, kBlock, 0, s>>>(A, K);
-        else
-          k_adam<false><<<(unsigned)nb, kBlock, 0, s>>>(A, K);
-        return tg_check_launch("tg_adam_step");
+#define L(AMS, LP) k_adam<AMS, LP><<<(unsigned)nb, kBlock, 0, s>>>(A, K)
+        if (ams) {
+          if (lp == 1) L(true, 1); else if (lp == 2) L(true, 2); else L(true, 0);
+        } else {
+          if (lp == 1) L(false, 1); else if (lp == 2) L(false, 2); else L(false, 0);
+        }
+#undef L
+        return tg_check_launch(who);
       },
       kAdamChunk);
+}
+
+}  // namespace
+
+TG_EXPORT int tg_adam_step(int ntensors, float* const* params, const float* const* grads,
+                           float* const* exp_avg, float* const* exp_avg_sq,
+                           float* const* max_exp_avg_sq, const int64_t* numel, double lr,
+                           double beta1, double beta2, double eps, double weight_decay,
+                           double bias_correction1, double bias_correction2, void* stream) {
+  return adam_step_impl("tg_adam_step", ntensors, params, grads, exp_avg, exp_avg_sq,
+                        max_exp_avg_sq, numel, lr, beta1, beta2, eps, weight_decay,
+                        bias_correction1, bias_correction2, 0, nullptr, stream);
+}
+
+// tg_adam_step that also writes each updated parameter, rounded to `lowp_dtype`
+// (fp16 or bf16), to lowp[i] when lowp[i] is not null: the autocast copy of the
+// weights refreshed in the same pass (2 B/param more written, no separate cast).
+TG_EXPORT int tg_adam_step_lowp(int ntensors, float* const* params, const float* const* grads,
+                                float* const* exp_avg, float* const* exp_avg_sq,
+                                float* const* max_exp_avg_sq, const int64_t* numel, double lr,
+                                double beta1, double beta2, double eps, double weight_decay,
+                                double bias_correction1, double bias_correction2,
+                                int lowp_dtype, void* const* lowp, void* stream) {
+  TG_REQUIRE(lowp, "tg_adam_step_lowp: null copy list");
+  return adam_step_impl("tg_adam_step_lowp", ntensors, params, grads, exp_avg, exp_avg_sq,
+                        max_exp_avg_sq, numel, lr, beta1, beta2, eps, weight_decay,
+                        bias_correction1, bias_correction2, lowp_dtype, lowp, stream);
 }
 
 // Multiply every gradient by `mul` (when write != 0) and report non-finite values:
@@ -419,7 +484,7 @@ TG_EXPORT int tg_unscale_check(int ntensors, int dtype, void* const* grads, cons
              "tg_unscale_check: unsupported dtype %d", dtype);
   hipStream_t s = tg_stream(stream);
   k_zero_ints<<<1, kBlock, 0, s>>>(flags, ntensors);
-  return for_each_launch(ntensors, grads, nullptr, nullptr, nullptr, nullptr, numel,
+  return for_each_launch(ntensors, grads, nullptr, nullptr, nullptr, nullptr, nullptr, numel,
                          [&](const MtArgs& A, int64_t nb) {
 #define L(T, W) k_scale_check<T, W><<<(unsigned)nb, kBlock, 0, s>>>(A, mul, flags)
                            if (dtype == TG_F32) { if (write) L(float, true); else L(float, false); }
@@ -460,7 +525,7 @@ TG_EXPORT int tg_grad_norm(int ntensors, int dtype, void* const* grads, const in
   int64_t part_base = 0;
   int st = TG_OK;
   if (ntensors > 0)
-    st = for_each_launch(ntensors, grads, nullptr, nullptr, nullptr, nullptr, numel,
+    st = for_each_launch(ntensors, grads, nullptr, nullptr, nullptr, nullptr, nullptr, numel,
                          [&](const MtArgs& A, int64_t nb) {
 #define L(T, K) k_norm_partial<T, K><<<(unsigned)nb, kBlock, 0, s>>>(A, p, part, part_base, flags)
 #define LK(T) if (norm_kind == 0) L(T, 0); else if (norm_kind == 1) L(T, 1); else L(T, 2);
@@ -487,7 +552,7 @@ TG_EXPORT int tg_zero_nonfinite(int ntensors, int dtype, void* const* grads, con
   if (ntensors == 0) return TG_OK;
   TG_REQUIRE(grads && numel, "tg_zero_nonfinite: null argument");
   hipStream_t s = tg_stream(stream);
-  return for_each_launch(ntensors, grads, nullptr, nullptr, nullptr, nullptr, numel,
+  return for_each_launch(ntensors, grads, nullptr, nullptr, nullptr, nullptr, nullptr, numel,
                          [&](const MtArgs& A, int64_t nb) {
                            if (dtype == TG_F32) k_zero_nonfinite<float><<<(unsigned)nb, kBlock, 0, s>>>(A);
                            else if (dtype == TG_F16) k_zero_nonfinite<tg_half><<<(unsigned)nb, kBlock, 0, s>>>(A);

@@ -21,6 +21,7 @@ import torch
 
 from . import _config as cfg
 from . import _lib as L
+from . import _lowp
 
 
 def _noop():
@@ -42,7 +43,8 @@ def _to_device_tensor(data, dtype):
         inferred = cfg.to_torch_dtype(arr.dtype) if arr.dtype.kind != "U" else None
         if inferred is None:
             raise TypeError(f"unsupported data of dtype {arr.dtype}")
-        t = torch.from_numpy(np.ascontiguousarray(arr))
+        # (np.ascontiguousarray would turn a 0-d array into shape (1,))
+        t = torch.from_numpy(arr if arr.flags.c_contiguous else np.ascontiguousarray(arr))
     return t, inferred
 
 
@@ -59,8 +61,11 @@ class Tensor:
         t, inferred = _to_device_tensor(data, dtype)
         target = cfg.resolve_dtype(inferred, dtype)
         if t.device.type != "cuda":
-            t = t.to(device="cuda", dtype=target)
-        elif t.dtype != target:
+            try:  # pinned staging, non-blocking copy; the dtype cast runs on the device
+                t = L.to_device(t.numpy())
+            except (TypeError, RuntimeError):
+                t = t.to(device="cuda")
+        if t.dtype != target:
             t = t.to(target)
         self.data = t
         rg = bool(requires_grad) and cfg._grad_enabled
@@ -901,6 +906,23 @@ def _matmul(self, other):
     return out
 
 
+def _weight_operand(w, wd, wt, cdt):
+    """The GEMM operand for weight `w` in compute dtype `cdt`: wd ([K, N]), or its
+    contiguous transpose ([N, K]) when `wt`.  A leaf parameter cast to a lower precision
+    (autocast) comes from the cast cache, owned by the tensor whose storage it is (the
+    source of a tied weight), so the optimizer can refresh it in its update pass."""
+    src = wd.t() if wt else wd
+    if src.dtype == cdt or w._prev or not src.is_contiguous():
+        return src.to(cdt).contiguous()
+    tied = getattr(w, "_tied_source", None)
+    if tied is not None:
+        sd = tied.data
+        if (sd.data_ptr() == src.data_ptr() and tuple(sd.shape) == tuple(src.shape)
+                and sd.is_contiguous()):
+            src = sd  # the persistent tensor the optimizer updates
+    return _lowp.cast(src, cdt)
+
+
 def _linear(x, w, b):
     """y = x @ w + b for a 2-D weight as one GEMM with the bias added in its epilogue
     (Linear.__call__, _nn.py:258-285, which builds a matmul node and a broadcast-add
@@ -919,7 +941,7 @@ def _linear(x, w, b):
     lead = tuple(a.shape[:-1])
     A2 = a.to(cdt).contiguous().reshape(-1, K)
     wt = not wd.is_contiguous() and wd.t().is_contiguous()
-    bc = wd.t().to(cdt).contiguous() if wt else wd.to(cdt).contiguous()  # [N, K] if wt
+    bc = _weight_operand(w, wd, wt, cdt)  # [N, K] if wt
     if b is not None:
         odt = cfg.resolve_dtype(torch.promote_types(cdt, b.data.dtype))
         bias = b.data.to(torch.float32).contiguous().reshape(N)

@@ -12,6 +12,7 @@ import ctypes
 import os
 import threading
 
+import numpy as np
 import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
@@ -57,6 +58,8 @@ SIGNATURES = {
                                 _i64, _i32, _i32, _i32, _vp, _sz, _vp]),
     "tg_adam_step": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _f64, _f64, _f64, _f64, _f64,
                             _f64, _f64, _vp]),
+    "tg_adam_step_lowp": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _f64, _f64, _f64, _f64,
+                                 _f64, _f64, _f64, _i32, _vp, _vp]),
     "tg_unscale_check": (_i32, [_i32, _i32, _vp, _vp, _f32, _i32, _vp, _vp]),
     "tg_grad_norm_workspace": (_sz, [_i32, _vp]),
     "tg_grad_norm": (_i32, [_i32, _i32, _vp, _vp, _i32, _f32, _vp, _vp, _vp, _sz, _vp]),
@@ -135,8 +138,52 @@ def ensure_device(device_index=None):
         _inited.add(device_index)
 
 
-def stream_handle():
-    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+if hasattr(torch._C, "_cuda_getCurrentRawStream") and hasattr(torch._C, "_cuda_getDevice"):
+    _raw_stream = torch._C._cuda_getCurrentRawStream
+    _cur_dev = torch._C._cuda_getDevice
+
+    def stream_handle():
+        """The current HIP stream of the current device (torch's current stream)."""
+        return ctypes.c_void_p(_raw_stream(_cur_dev()))
+else:
+    def stream_handle():
+        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+# Host-to-device copies of NumPy inputs (token ids, targets, data batches) go through a
+# small ring of reusable pinned buffers with a non-blocking copy on the current stream:
+# a pageable copy would block the host until the device queue drains, so the host could
+# never run ahead of the GPU.  A slot is reused only after the event recorded behind
+# its previous copy has completed.
+_STAGE_SLOTS = 4
+_STAGE_MAX = 64 << 20
+_stage = [[None, None] for _ in range(_STAGE_SLOTS)]
+_stage_next = [0]
+
+
+def to_device(arr, device=None):
+    """A contiguous device copy of the NumPy array `arr` (same dtype and shape)."""
+    a = np.asarray(arr)
+    if not a.flags.c_contiguous:
+        a = np.ascontiguousarray(a)  # (only for ndim >= 1: it would make a 0-d array 1-d)
+    dev = torch.device("cuda") if device is None else torch.device(device)
+    if a.nbytes == 0 or a.nbytes > _STAGE_MAX or a.dtype.hasobject:
+        return torch.as_tensor(a, device=dev)
+    src_t = torch.from_numpy(a)
+    slot = _stage[_stage_next[0] % _STAGE_SLOTS]
+    _stage_next[0] += 1
+    if slot[1] is not None:
+        slot[1].synchronize()
+    if slot[0] is None or slot[0].numel() < a.nbytes:
+        slot[0] = torch.empty(max(a.nbytes, 1 << 20), dtype=torch.uint8, pin_memory=True)
+    pinned = slot[0][: a.nbytes].view(src_t.dtype).view(src_t.shape)
+    pinned.copy_(src_t)
+    out = torch.empty(src_t.shape, dtype=src_t.dtype, device=dev)
+    out.copy_(pinned, non_blocking=True)
+    ev = torch.cuda.Event()
+    ev.record()
+    slot[1] = ev
+    return out
 
 
 def dtype_code(t):
@@ -383,7 +430,10 @@ def _numel_array(ts):
 
 
 def adam_step(params, grads, exp_avg, exp_avg_sq, max_exp_avg_sq, lr, beta1, beta2, eps,
-              weight_decay, bias_correction1, bias_correction2):
+              weight_decay, bias_correction1, bias_correction2, lowp=None):
+    """Multi-tensor Adam/AdamW step.  `lowp`, if given, is a list parallel to `params`
+    of None or a contiguous fp16/bf16 tensor of the param's size (one dtype for the
+    list) that receives the updated param rounded to that dtype in the same pass."""
     n = len(params)
     if n == 0:
         return
@@ -396,11 +446,28 @@ def adam_step(params, grads, exp_avg, exp_avg_sq, max_exp_avg_sq, lr, beta1, bet
         if not (p.numel() == g.numel() == m.numel() == v.numel()):
             raise ValueError("adam_step: param/grad/state sizes differ")
     ensure_device(params[0].device.index)
-    _check("tg_adam_step", load().tg_adam_step(
-        n, _ptr_array(params), _ptr_array(grads), _ptr_array(exp_avg), _ptr_array(exp_avg_sq),
-        _ptr_array(max_exp_avg_sq) if max_exp_avg_sq else None, _numel_array(params),
-        float(lr), float(beta1), float(beta2), float(eps), float(weight_decay),
-        float(bias_correction1), float(bias_correction2), stream_handle()))
+    args = (_ptr_array(params), _ptr_array(grads), _ptr_array(exp_avg), _ptr_array(exp_avg_sq),
+            _ptr_array(max_exp_avg_sq) if max_exp_avg_sq else None, _numel_array(params),
+            float(lr), float(beta1), float(beta2), float(eps), float(weight_decay),
+            float(bias_correction1), float(bias_correction2))
+    if lowp is not None and any(t is not None for t in lowp):
+        if len(lowp) != n:
+            raise ValueError("adam_step: lowp list length differs from params")
+        lp = [t for t in lowp if t is not None]
+        dt = lp[0].dtype
+        for p, t in zip(params, lowp):
+            if t is None:
+                continue
+            _dev(t, "adam low-precision copy")
+            if t.dtype != dt or dt not in (torch.float16, torch.bfloat16):
+                raise TypeError("adam_step: low-precision copies must share one fp16/bf16 dtype")
+            if t.numel() != p.numel() or not t.is_contiguous():
+                raise ValueError("adam_step: low-precision copy must be contiguous and of its "
+                                 "param's size")
+        _check("tg_adam_step_lowp", load().tg_adam_step_lowp(
+            n, *args, dtype_code(lp[0]), _ptr_array(lowp), stream_handle()))
+        return
+    _check("tg_adam_step", load().tg_adam_step(n, *args, stream_handle()))
 
 
 def _group_by_dtype(ts):

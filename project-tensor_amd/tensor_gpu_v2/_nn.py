@@ -13,6 +13,7 @@ import torch
 
 from . import _config as cfg
 from . import _lib as L
+from . import _lowp
 from ._core import Tensor, _linear
 
 
@@ -389,7 +390,7 @@ class Embedding(Module):
             # checked here: an out-of-range gather on the device would assert in-kernel
             if host.size and (host.min() < -V or host.max() >= V):
                 raise IndexError(f"Embedding: index outside [-{V}, {V})")
-            idx = torch.as_tensor(host.astype(np.int64), device=self.weight.data.device)
+            idx = L.to_device(host.astype(np.int64, copy=False), self.weight.data.device)
         idx = idx.to(device=self.weight.data.device, dtype=torch.int64).contiguous()
         weight = self.weight
         # gather and the dtype policy's cast in one kernel; negative indices wrap
@@ -453,7 +454,7 @@ class CrossEntropyLoss(Module):
             # the reference indexes probs[arange(N), targets]: out-of-range targets raise
             if host.size and (host.min() < 0 or host.max() >= C):
                 raise IndexError(f"CrossEntropyLoss: target outside [0, {C})")
-            tg = torch.as_tensor(host.astype(np.int64), device=ld.device)
+            tg = L.to_device(host.astype(np.int64, copy=False), ld.device)
         tg = tg.to(device=ld.device, dtype=torch.int64).reshape(-1).contiguous()
         if tg.numel() != N:
             raise ValueError(f"CrossEntropyLoss: {tg.numel()} targets for {N} rows")
@@ -563,7 +564,7 @@ class Adam:
             if self.amsgrad:
                 vms.append(self.v_max[i])
         L.adam_step(ps, gs, ms, vs, vms if self.amsgrad else None, lr, self.beta1, self.beta2,
-                    self.eps, wd, bc1, bc2)
+                    self.eps, wd, bc1, bc2, lowp=_lowp.refresh_targets(ps))
 
     def step(self, clip_grad_norm=None):
         if clip_grad_norm is not None:

@@ -497,3 +497,37 @@ def test_linear_fused_bias_and_transposed_weight(tg, autocast, bias, tied):
     if tied:
         tg.sync_tied_gradients(lin)
         assert_close(src.grad, wt.grad.numpy().T, tol, "tied source grad")
+
+
+def test_host_inputs_staged_copy(tg):
+    """NumPy inputs reach the device through reusable pinned buffers and a non-blocking
+    copy: every copy holds its own values although slots are reused, a later change to
+    the source array does not leak in, and every dtype/shape round-trips."""
+    from tensor_gpu_v2 import _lib as L
+    rng = np.random.default_rng(5)
+    outs, srcs = [], []
+    for i in range(11):  # more copies than slots
+        a = rng.integers(-1000, 1000, size=(3 + i, 17)).astype(np.int64)
+        outs.append(L.to_device(a))
+        srcs.append(a.copy())
+        a[:] = 0  # the copy was taken at call time
+    for o, a in zip(outs, srcs):
+        assert o.is_cuda and np.array_equal(o.cpu().numpy(), a)
+    for a in (np.float32(2.5), np.arange(7, dtype=np.float64), np.zeros((0, 3), np.float32),
+              rng.standard_normal((4, 5)).astype(np.float16), np.array([True, False])):
+        o = L.to_device(a)
+        assert o.shape == np.asarray(a).shape and np.array_equal(o.cpu().numpy(), a)
+    a = rng.standard_normal((6, 6))
+    t = tg.Tensor(a)  # float64 data keeps its dtype (the reference's dtype policy)
+    assert t.data.dtype == torch.float64 and t.data.is_cuda
+    assert np.array_equal(t.data.cpu().numpy(), a)
+    t32 = tg.Tensor(a, dtype=np.float32)  # cast on the device after the copy
+    assert t32.data.dtype == torch.float32
+    assert np.array_equal(t32.data.cpu().numpy(), a.astype(np.float32))
+
+
+def test_scalar_tensor_is_zero_dim(tg):
+    """Tensor(3.0) is 0-d, as cp.asarray(3.0) is in the reference (_core.py:625-655)."""
+    t = tg.Tensor(3.0)
+    assert tuple(t.shape) == () and float(t.item()) == 3.0
+    assert tuple(tg.Tensor(np.array(2.0)).shape) == ()
