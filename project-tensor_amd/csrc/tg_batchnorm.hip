@@ -41,7 +41,7 @@ __device__ __forceinline__ float bn_affine(float xh, float g, float b) {
 // vector (blockIdx.y*64 + l) (V channels), the 4 waves take interleaved rows of
 // the block's row range; the block writes one partial per channel.
 // MODE 0: sum x.  MODE 1: sum (x-mean)^2.  MODE 2 (backward): sum dy_m, sum dy_m*xhat.
-template <int V, int MODE>
+template <int V, int MODE, bool NTL = false>
 __global__ __launch_bounds__(kBlock) void k_nhwc_reduce(
     const float* __restrict__ x, const float* __restrict__ dy, const float* __restrict__ mean,
     const float* __restrict__ rstd, const float* __restrict__ gamma,
@@ -65,34 +65,53 @@ __global__ __launch_bounds__(kBlock) void k_nhwc_reduce(
 #pragma unroll
     for (int s = 0; s < NS; ++s) acc[s][j] = 0.f;
   }
-  if (cl) {
-    for (int64_t r = r0 + wave; r < r1; r += 4) {
-      float xv[V], dv[V];
-      if (V == 4) {
-        const float4 a = *reinterpret_cast<const float4*>(x + r * C + c0);
-        xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w;
-        if (MODE == 2) {
-          const float4 d = *reinterpret_cast<const float4*>(dy + r * C + c0);
-          dv[0] = d.x; dv[1] = d.y; dv[2] = d.z; dv[3] = d.w;
-        }
-      } else {
-        xv[0] = x[r * C + c0];
-        if (MODE == 2) dv[0] = dy[r * C + c0];
-      }
+  auto row = [&](int64_t r, float (&xv)[V], float (&dv)[V]) {
+    if (V == 4) {
+      const tg_vec16<float> a = tg_ld16<NTL>(x + r * C + c0);
 #pragma unroll
-      for (int j = 0; j < V; ++j) {
-        if (MODE == 0) {
-          acc[0][j] += xv[j];
-        } else if (MODE == 1) {
-          const float d = xv[j] - mu[j];
-          acc[0][j] += d * d;
-        } else {
-          const float xh = bn_xhat(xv[j], mu[j], rs[j]);
-          const float dm = (!relu || bn_relu_on(xh, g[j], b[j])) ? dv[j] : 0.f;
-          acc[0][j] += dm;
-          acc[1][j] += dm * xh;
-        }
+      for (int j = 0; j < V; ++j) xv[j] = a.v[j];
+      if (MODE == 2) {
+        const tg_vec16<float> d = tg_ld16<NTL>(dy + r * C + c0);
+#pragma unroll
+        for (int j = 0; j < V; ++j) dv[j] = d.v[j];
       }
+    } else {
+      xv[0] = x[r * C + c0];
+      if (MODE == 2) dv[0] = dy[r * C + c0];
+    }
+  };
+  auto accum = [&](const float (&xv)[V], const float (&dv)[V]) {
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+      if (MODE == 0) {
+        acc[0][j] += xv[j];
+      } else if (MODE == 1) {
+        const float d = xv[j] - mu[j];
+        acc[0][j] += d * d;
+      } else {
+        const float xh = bn_xhat(xv[j], mu[j], rs[j]);
+        const float dm = (!relu || bn_relu_on(xh, g[j], b[j])) ? dv[j] : 0.f;
+        acc[0][j] += dm;
+        acc[1][j] += dm * xh;
+      }
+    }
+  };
+  if (cl) {
+    // Four rows per wave in flight (all loads issued before any is used), then the
+    // remaining rows one at a time.  The accumulation order per wave is the row order.
+    constexpr int U = 4;
+    int64_t r = r0 + wave;
+    for (; r + 4 * (U - 1) < r1; r += 4 * U) {
+      float xv[U][V], dv[U][V];
+#pragma unroll
+      for (int u = 0; u < U; ++u) row(r + 4 * u, xv[u], dv[u]);
+#pragma unroll
+      for (int u = 0; u < U; ++u) accum(xv[u], dv[u]);
+    }
+    for (; r < r1; r += 4) {
+      float xv[V], dv[V];
+      row(r, xv, dv);
+      accum(xv, dv);
     }
   }
   // combine the 4 waves through LDS
@@ -218,7 +237,7 @@ __device__ __forceinline__ int64_t chan_of(int64_t i, int64_t C, int64_t HW) {
   return LAYOUT == TG_NHWC ? (i % C) : ((i / HW) % C);
 }
 
-template <int LAYOUT, int V, bool ACC, bool CONST_CH>
+template <int LAYOUT, int V, bool ACC, bool CONST_CH, bool NTL = false>
 __global__ __launch_bounds__(kBlock) void k_bn_bwd_apply(
     const float* __restrict__ x, const float* __restrict__ dy, const float* __restrict__ mean,
     const float* __restrict__ rstd, const float* __restrict__ gamma,
@@ -242,13 +261,16 @@ __global__ __launch_bounds__(kBlock) void k_bn_bwd_apply(
     const int64_t i = iv * V;
     float xv[V], dv[V], ov[V];
     if (V == 4) {
-      const float4 a = *reinterpret_cast<const float4*>(x + i);
-      const float4 d = *reinterpret_cast<const float4*>(dy + i);
-      xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w;
-      dv[0] = d.x; dv[1] = d.y; dv[2] = d.z; dv[3] = d.w;
+      const tg_vec16<float> a = tg_ld16<NTL>(x + i), d = tg_ld16<NTL>(dy + i);
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        xv[j] = a.v[j];
+        dv[j] = d.v[j];
+      }
       if (ACC) {
-        const float4 o = *reinterpret_cast<const float4*>(dx + i);
-        ov[0] = o.x; ov[1] = o.y; ov[2] = o.z; ov[3] = o.w;
+        const tg_vec16<float> o = tg_ld16<NTL>(dx + i);
+#pragma unroll
+        for (int j = 0; j < V; ++j) ov[j] = o.v[j];
       }
     } else {
       xv[0] = x[i];
@@ -349,10 +371,14 @@ size_t bn_ws_bytes(const BnPlan& p, int64_t C) {
 template <int MODE>
 void launch_reduce(int layout, const BnPlan& p, const float* x, const float* dy,
                    const float* mean, const float* rstd, const float* gamma, const float* beta,
-                   int relu, float* part, int64_t N, int64_t C, int64_t HW, hipStream_t s) {
+                   int relu, float* part, int64_t N, int64_t C, int64_t HW, hipStream_t s,
+                   bool ntl = false) {
   if (layout == TG_NHWC) {
     dim3 grid((unsigned)p.nsplit, (unsigned)p.ctiles);
-    if (p.V == 4)
+    if (p.V == 4 && ntl)
+      k_nhwc_reduce<4, MODE, true><<<grid, kBlock, 0, s>>>(x, dy, mean, rstd, gamma, beta, relu,
+                                                           part, p.M, C);
+    else if (p.V == 4)
       k_nhwc_reduce<4, MODE><<<grid, kBlock, 0, s>>>(x, dy, mean, rstd, gamma, beta, relu, part,
                                                      p.M, C);
     else
@@ -484,7 +510,9 @@ TG_EXPORT int tg_batchnorm_bwd(int layout, const float* x, const float* mean, co
   float* sums = part + 2 * p.nsplit * C;
   float* coef = sums + 2 * C;
   float* scratch = sums + 5 * C;
-  launch_reduce<2>(layout, p, x, dy, mean, rstd, gamma, beta, relu, part, N, C, HW, s);
+  // x and dy too large to stay cached: both passes read them non-temporally
+  const bool big = N * C * HW * (int64_t)sizeof(float) >= (128ll << 20);
+  launch_reduce<2>(layout, p, x, dy, mean, rstd, gamma, beta, relu, part, N, C, HW, s, big);
   st = tg_sum_partials(part, p.nsplit, 2 * C, TG_F32, sums, 0, scratch, s);
   if (st) return st;
   const unsigned cb = (unsigned)((C + kBlock - 1) / kBlock);
@@ -494,9 +522,15 @@ TG_EXPORT int tg_batchnorm_bwd(int layout, const float* x, const float* mean, co
   const bool vec = p.V == 4 && al;
   const int64_t nvec = vec ? n / 4 : n;
   const unsigned ab = apply_blocks(nvec);
-#define TG_BN_APPLY(LAY, VV, ACC, CC, NB)                                               \
-  k_bn_bwd_apply<LAY, VV, ACC, CC><<<NB, kBlock, 0, s>>>(x, dy, mean, rstd, gamma, beta, coef, \
-                                                         relu, dx, nvec, C, HW, nt)
+#define TG_BN_APPLY(LAY, VV, ACC, CC, NB)                                                    \
+  do {                                                                                       \
+  if (nt)                                                                                   \
+    k_bn_bwd_apply<LAY, VV, ACC, CC, true><<<NB, kBlock, 0, s>>>(x, dy, mean, rstd, gamma, beta, \
+                                                                 coef, relu, dx, nvec, C, HW, nt); \
+  else                                                                                       \
+    k_bn_bwd_apply<LAY, VV, ACC, CC><<<NB, kBlock, 0, s>>>(x, dy, mean, rstd, gamma, beta, coef, \
+                                                           relu, dx, nvec, C, HW, nt); \
+  } while (0)
   const bool nt = n * (int64_t)sizeof(float) >= (128ll << 20);  // output too large to keep cached
   const unsigned cc = (layout == TG_NHWC && vec) ? const_channel_blocks(nvec, C, 4) : 0;
   if (cc) {

@@ -27,6 +27,32 @@ __device__ __forceinline__ void lse_merge(float& m, float& s, float m2, float s2
   m = mn;
 }
 
+// Maximum over U 16-byte vectors, as fp32.  fp16 pairs use the packed half
+// maximum (exact: the maximum of fp16 values is one of them).
+template <typename T, int U>
+__device__ __forceinline__ float vec_max(const tg_vec16<T> (&v)[U]) {
+  constexpr int V = tg_vec16<T>::N;
+  if constexpr (sizeof(T) == 2 && __is_same(T, tg_half)) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    h2 acc = {(tg_half)-INFINITY, (tg_half)-INFINITY};
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int j = 0; j < V; j += 2) {
+        const h2 p = {v[u].v[j], v[u].v[j + 1]};
+        acc = __builtin_elementwise_max(acc, p);
+      }
+    return fmaxf((float)acc.x, (float)acc.y);
+  } else {
+    float r = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int j = 0; j < V; ++j) r = fmaxf(r, tg_to_float(v[u].v[j]));
+    return r;
+  }
+}
+
 // Online (max, sum) of x*log2e over this thread's elements of a row.
 template <typename T, bool VEC>
 __device__ __forceinline__ void row_stats(const T* __restrict__ x, int64_t C, float& m,
@@ -34,21 +60,30 @@ __device__ __forceinline__ void row_stats(const T* __restrict__ x, int64_t C, fl
   m = -INFINITY;
   s = 0.f;
   if (VEC) {
-    constexpr int V = tg_vec16<T>::N;
+    // U vectors per step, all loads issued before the first is used.  The thread's
+    // running maximum m (log2 units) is raised once per step to cover the step's
+    // elements (s rescaled by one exp2), then every element costs one fused
+    // multiply-add, one exp2 and one add.  Elements past the row end read as -inf.
+    constexpr int V = tg_vec16<T>::N, U = 4;
     const int64_t nv = C / V;
-    for (int64_t i = threadIdx.x; i < nv; i += kBlock) {
-      const tg_vec16<T> v = tg_load16(x + i * V);
-      float e[V];
-      float vm = -INFINITY;
+    for (int64_t i0 = threadIdx.x; i0 < nv; i0 += U * kBlock) {
+      tg_vec16<T> v[U];
 #pragma unroll
-      for (int j = 0; j < V; ++j) {
-        e[j] = tg_to_float(v.v[j]) * kLog2e;
-        vm = fmaxf(vm, e[j]);
+      for (int u = 0; u < U; ++u) {
+        if (i0 + u * kBlock < nv) v[u] = tg_load16(x + (i0 + u * kBlock) * V);
+        else
+#pragma unroll
+          for (int j = 0; j < V; ++j) v[u].v[j] = tg_from_float<T>(-INFINITY);
       }
-      float vs = 0.f;
+      const float vm = vec_max<T, U>(v) * kLog2e;
+      const float mn = fmaxf(m, vm);
+      const float mref = mn == -INFINITY ? 0.f : mn;
+      s *= exp2f(m - mref);
+      m = mn;
 #pragma unroll
-      for (int j = 0; j < V; ++j) vs += exp2f(e[j] - vm);
-      lse_merge(m, s, vm, vs);
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int j = 0; j < V; ++j) s += exp2f(fmaf(tg_to_float(v[u].v[j]), kLog2e, -mref));
     }
   } else {
     for (int64_t i = threadIdx.x; i < C; i += kBlock) lse_merge(m, s, tg_to_float(x[i]) * kLog2e, 1.f);
@@ -114,8 +149,11 @@ template <typename T, typename TG, bool ACC, bool VEC>
 __global__ __launch_bounds__(kBlock) void k_ce_bwd(const T* __restrict__ X,
                                                    const int64_t* __restrict__ tgt,
                                                    const float* __restrict__ lse_in, int64_t C,
-                                                   float smooth, float scale, TG* __restrict__ G) {
-  const int64_t row = blockIdx.x;
+                                                   float smooth, float scale, TG* __restrict__ G,
+                                                   int rev) {
+  // rev: rows in reverse launch order, so the first rows processed are the ones the
+  // forward read last (still in the memory-side cache when the backward follows it).
+  const int64_t row = rev ? (int64_t)gridDim.x - 1 - blockIdx.x : (int64_t)blockIdx.x;
   const T* x = X + row * C;
   TG* g = G + row * C;
   const float l2 = lse_in[row] * kLog2e;
@@ -125,20 +163,34 @@ __global__ __launch_bounds__(kBlock) void k_ce_bwd(const T* __restrict__ X,
   if constexpr (VEC) {
     constexpr int V = tg_vec16<T>::N;
     static_assert(sizeof(T) == sizeof(TG), "vector path needs equal element sizes");
+    constexpr int U = 4;
     const int64_t nv = C / V;
-    for (int64_t i = threadIdx.x; i < nv; i += kBlock) {
-      const tg_vec16<T> v = tg_load16(x + i * V);
-      tg_vec16<TG> o;
-      if (ACC) o = tg_load16(g + i * V);
+    for (int64_t i0 = threadIdx.x; i0 < nv; i0 += U * kBlock) {
+      tg_vec16<T> v[U];
+      tg_vec16<TG> o[U];
 #pragma unroll
-      for (int j = 0; j < V; ++j) {
-        const int64_t c = i * V + j;
-        const float p = exp2f(fmaf(tg_to_float(v.v[j]), kLog2e, -l2));
-        float r = (p - wu - (c == t ? wt : 0.f)) * scale;
-        if (ACC) r += tg_to_float(o.v[j]);
-        o.v[j] = tg_from_float<TG>(r);
+      for (int u = 0; u < U; ++u) {
+        const int64_t i = i0 + u * kBlock;
+        if (i < nv) {
+          v[u] = tg_load16(x + i * V);
+          if (ACC) o[u] = tg_load16(g + i * V);
+        }
       }
-      tg_store16(g + i * V, o);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t i = i0 + u * kBlock;
+        if (i < nv) {
+#pragma unroll
+          for (int j = 0; j < V; ++j) {
+            const int64_t c = i * V + j;
+            const float p = exp2f(fmaf(tg_to_float(v[u].v[j]), kLog2e, -l2));
+            float r = (p - wu - (c == t ? wt : 0.f)) * scale;
+            if (ACC) r += tg_to_float(o[u].v[j]);
+            o[u].v[j] = tg_from_float<TG>(r);
+          }
+          tg_store16(g + i * V, o[u]);
+        }
+      }
     }
   } else {
     for (int64_t c = threadIdx.x; c < C; c += kBlock) {
@@ -167,9 +219,10 @@ int bwd_t(const void* x, const int64_t* tg, const float* lse, int64_t N, int64_t
           float scale, void* g, int acc, hipStream_t s) {
   constexpr int V = tg_vec16<T>::N;
   const bool vec = sizeof(T) == sizeof(TG) && tg_aligned16(x) && tg_aligned16(g) && C % V == 0;
+  const int rev = 1;
 #define L(ACC, VEC)                                                                         \
   k_ce_bwd<T, TG, ACC, VEC><<<(unsigned)N, kBlock, 0, s>>>((const T*)x, tg, lse, C, smooth, \
-                                                           scale, (TG*)g)
+                                                           scale, (TG*)g, rev)
   if constexpr (sizeof(T) == sizeof(TG)) {
     if (vec) {
       if (acc) L(true, true);

@@ -118,15 +118,16 @@ __device__ __forceinline__ tg_vec16<T> tg_load16(const T* p) {
   *reinterpret_cast<uint4*>(&r) = *reinterpret_cast<const uint4*>(p);
   return r;
 }
+// 16-byte load with the non-temporal hint (one dwordx4 with the nt bit): inputs
+// streamed once, too large to stay in the caches, skip cache retention.  Measured on
+// gfx950 for a two-in/one-out fp32 stream of 256 MiB operands: 6.0 TB/s with plain
+// loads, 6.6 TB/s with non-temporal loads (both with non-temporal stores).
+typedef unsigned tg_u32x4 __attribute__((ext_vector_type(4)));
 template <typename T>
 __device__ __forceinline__ tg_vec16<T> tg_load16_nt(const T* p) {
   tg_vec16<T> r;
-  uint4 u;
-  u.x = __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(p) + 0);
-  u.y = __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(p) + 1);
-  u.z = __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(p) + 2);
-  u.w = __builtin_nontemporal_load(reinterpret_cast<const unsigned*>(p) + 3);
-  *reinterpret_cast<uint4*>(&r) = u;
+  *reinterpret_cast<tg_u32x4*>(&r) =
+      __builtin_nontemporal_load(reinterpret_cast<const tg_u32x4*>(p));
   return r;
 }
 template <typename T>
@@ -137,11 +138,22 @@ __device__ __forceinline__ void tg_store16(T* p, const tg_vec16<T>& r) {
 // 16-byte store with the non-temporal hint: streaming outputs that no later kernel
 // reads soon skip the cache-retention path (measured 3-6% more HBM throughput for
 // streaming kernels on gfx950).
-typedef unsigned tg_u32x4 __attribute__((ext_vector_type(4)));
 template <typename T>
 __device__ __forceinline__ void tg_store16_nt(T* p, const tg_vec16<T>& r) {
   __builtin_nontemporal_store(*reinterpret_cast<const tg_u32x4*>(&r),
                               reinterpret_cast<tg_u32x4*>(p));
+}
+
+// Load/store chosen at compile time: NT selects the non-temporal forms.
+template <bool NT, typename T>
+__device__ __forceinline__ tg_vec16<T> tg_ld16(const T* p) {
+  if constexpr (NT) return tg_load16_nt(p);
+  else return tg_load16(p);
+}
+template <bool NT, typename T>
+__device__ __forceinline__ void tg_st16(T* p, const tg_vec16<T>& r) {
+  if constexpr (NT) tg_store16_nt(p, r);
+  else tg_store16(p, r);
 }
 
 // Number of CUs on the current device, cached per device by tg_runtime.

@@ -60,8 +60,8 @@ template <int OP> __device__ __forceinline__ float act_fwd(float x) {
 }
 
 // dx (+)= dy * act'(x).  One 16-byte vector per operand and thread (the
-// measured optimum for two-in/one-out streams); NT marks the output store
-// non-temporal, chosen for outputs too large to stay in the Infinity Cache.
+// measured optimum for two-in/one-out streams); NT marks loads and stores
+// non-temporal, chosen for operands too large to stay in the Infinity Cache.
 constexpr int kUnrollBwd = 1;
 constexpr int64_t kNtBytes = 128ll << 20;
 
@@ -77,9 +77,9 @@ __global__ __launch_bounds__(kThreads) void k_act_bwd(const T* __restrict__ x,
   for (int u = 0; u < kUnrollBwd; ++u) {
     const int64_t i = base + (int64_t)u * kThreads;
     if (i < nvec) {
-      xv[u] = tg_load16(x + i * V);
-      gv[u] = tg_load16(dy + i * V);
-      if (ACC) ov[u] = tg_load16(dx + i * V);
+      xv[u] = tg_ld16<NT>(x + i * V);
+      gv[u] = tg_ld16<NT>(dy + i * V);
+      if (ACC) ov[u] = tg_ld16<NT>(dx + i * V);
     }
   }
 #pragma unroll
@@ -93,8 +93,7 @@ __global__ __launch_bounds__(kThreads) void k_act_bwd(const T* __restrict__ x,
         if (ACC) g += tg_to_float(ov[u].v[j]);
         r.v[j] = tg_from_float<T>(g);
       }
-      if (NT) tg_store16_nt(dx + i * V, r);
-      else tg_store16(dx + i * V, r);
+      tg_st16<NT>(dx + i * V, r);
     }
   }
   // scalar tail (fewer than V elements), handled by the first block

@@ -89,6 +89,34 @@ __global__ __launch_bounds__(kBlock) void k_transpose_add(const TS* __restrict__
   }
 }
 
+// fp32 transpose-add over whole 64 x 64 tiles (R and C multiples of 64, 16-byte
+// aligned rows): 16-byte loads of src rows and 16-byte read-modify-writes of dst
+// rows, all non-temporal (each element is touched once).
+__global__ __launch_bounds__(kBlock) void k_transpose_add_v4(const float* __restrict__ src,
+                                                             int64_t R, int64_t C,
+                                                             float* __restrict__ dst,
+                                                             float alpha) {
+  __shared__ float tile[64][65];
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const int q = (threadIdx.x & 15) * 4, w = threadIdx.x >> 4;  // 16 x 16
+  tg_vec16<float> v[4], o[4];  // both operands' loads in flight before the exchange
+#pragma unroll
+  for (int k = 0; k < 4; ++k) v[k] = tg_load16_nt(src + (r0 + w + 16 * k) * C + c0 + q);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) o[k] = tg_load16_nt(dst + (c0 + w + 16 * k) * R + r0 + q);
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) tile[w + 16 * k][q + i] = v[k].v[i];
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[k].v[i] += alpha * tile[q + i][w + 16 * k];
+    tg_store16_nt(dst + (c0 + w + 16 * k) * R + r0 + q, o[k]);
+  }
+}
+
 int sort_bits(int64_t V) {
   int b = 1;
   while (b < 63 && ((int64_t)1 << b) < V) ++b;
@@ -271,6 +299,11 @@ TG_EXPORT int tg_transpose_add(int dtype_src, const void* src, int64_t rows, int
   TG_REQUIRE((rows + 63) / 64 <= 65535, "tg_transpose_add: too many rows");
   hipStream_t s = tg_stream(stream);
   dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64));
+  if (dtype_src == TG_F32 && dtype_dst == TG_F32 && rows % 64 == 0 && cols % 64 == 0 &&
+      tg_aligned16(src) && tg_aligned16(dst)) {
+    k_transpose_add_v4<<<grid, kBlock, 0, s>>>((const float*)src, rows, cols, (float*)dst, alpha);
+    return tg_check_launch("tg_transpose_add");
+  }
 #define T2(TS)                                                                                  \
   switch (dtype_dst) {                                                                          \
     case TG_F32: k_transpose_add<TS, float><<<grid, kBlock, 0, s>>>((const TS*)src, rows, cols, \

@@ -99,11 +99,11 @@ __global__ __launch_bounds__(kBlock) void k_softmax_fwd_reg(const T* __restrict_
 }
 
 // Backward: dx (+)= y * (dy - sum(dy * y))   (_core.py:1294-1297)
-template <typename T, int TPR, int VPT, bool ACC>
+template <typename T, int TPR, int VPT, bool ACC, bool NT>
 __global__ __launch_bounds__(kBlock) void k_softmax_bwd_reg(const T* __restrict__ y,
                                                             const T* __restrict__ dy,
                                                             T* __restrict__ dx, int64_t rows,
-                                                            int cols, bool nt) {
+                                                            int cols) {
   constexpr int V = tg_vec16<T>::N;
   constexpr int G = kBlock / TPR;
   __shared__ float red[8];
@@ -118,8 +118,8 @@ __global__ __launch_bounds__(kBlock) void k_softmax_bwd_reg(const T* __restrict_
   for (int k = 0; k < VPT; ++k) {
     const int vi = t + k * TPR;
     if (live && vi < nv) {
-      yv[k] = tg_load16(y + off + vi * V);
-      gv[k] = tg_load16(dy + off + vi * V);
+      yv[k] = tg_ld16<NT>(y + off + vi * V);
+      gv[k] = tg_ld16<NT>(dy + off + vi * V);
 #pragma unroll
       for (int j = 0; j < V; ++j) s[0] += tg_to_float(yv[k].v[j]) * tg_to_float(gv[k].v[j]);
     }
@@ -131,15 +131,14 @@ __global__ __launch_bounds__(kBlock) void k_softmax_bwd_reg(const T* __restrict_
     const int vi = t + k * TPR;
     if (vi < nv) {
       tg_vec16<T> o;
-      if (ACC) o = tg_load16(dx + off + vi * V);
+      if (ACC) o = tg_ld16<NT>(dx + off + vi * V);
 #pragma unroll
       for (int j = 0; j < V; ++j) {
         float r = tg_to_float(yv[k].v[j]) * (tg_to_float(gv[k].v[j]) - s[0]);
         if (ACC) r += tg_to_float(o.v[j]);
         o.v[j] = tg_from_float<T>(r);
       }
-      if (nt) tg_store16_nt(dx + off + vi * V, o);
-      else tg_store16(dx + off + vi * V, o);
+      tg_st16<NT>(dx + off + vi * V, o);
     }
   }
 }
@@ -246,19 +245,21 @@ int softmax_bwd_t(const void* y, const void* dy, void* dx, int64_t rows, int64_t
     const int64_t g = kBlock / tpr;
     const unsigned blocks = (unsigned)((rows + g - 1) / g);
     const bool nt = (int64_t)sizeof(T) * rows * cols >= kNtBytes;
+#define SMARGS (const T*)y, (const T*)dy, (T*)dx, rows, (int)cols
     if (acc) {
 #define L(TPR, VPT)                                                                            \
-  k_softmax_bwd_reg<T, TPR, VPT, true><<<blocks, kBlock, 0, s>>>((const T*)y, (const T*)dy, \
-                                                                 (T*)dx, rows, (int)cols, nt)
+  if (nt) k_softmax_bwd_reg<T, TPR, VPT, true, true><<<blocks, kBlock, 0, s>>>(SMARGS); \
+  else k_softmax_bwd_reg<T, TPR, VPT, true, false><<<blocks, kBlock, 0, s>>>(SMARGS)
       TG_REG_DISPATCH(L)
 #undef L
     } else {
 #define L(TPR, VPT)                                                                             \
-  k_softmax_bwd_reg<T, TPR, VPT, false><<<blocks, kBlock, 0, s>>>((const T*)y, (const T*)dy, \
-                                                                  (T*)dx, rows, (int)cols, nt)
+  if (nt) k_softmax_bwd_reg<T, TPR, VPT, false, true><<<blocks, kBlock, 0, s>>>(SMARGS); \
+  else k_softmax_bwd_reg<T, TPR, VPT, false, false><<<blocks, kBlock, 0, s>>>(SMARGS)
       TG_REG_DISPATCH(L)
 #undef L
     }
+#undef SMARGS
   } else {
     const unsigned blocks = (unsigned)((rows + 3) / 4);
     if (acc)
@@ -377,11 +378,11 @@ __global__ __launch_bounds__(kBlock) void k_ln_fwd_loop(const T* __restrict__ x,
 // Block b walks rows b, b+nblocks, ...; its threads own fixed columns, so the
 // dgamma/dbeta partials stay in registers and are written once per block to
 // part[b][0:cols] and part[nblocks + b][0:cols].
-template <typename T, int TPR, int VPT, bool ACC>
+template <typename T, int TPR, int VPT, bool ACC, bool NT>
 __global__ __launch_bounds__(kBlock) void k_ln_bwd_reg(
     const T* __restrict__ x, const float* __restrict__ mean, const float* __restrict__ rstd,
     const float* __restrict__ gamma, const T* __restrict__ dy, T* __restrict__ dx,
-    float* __restrict__ part, int64_t rows, int cols, bool nt) {
+    float* __restrict__ part, int64_t rows, int cols) {
   constexpr int V = tg_vec16<T>::N;
   constexpr int G = kBlock / TPR;
   __shared__ float red[8];
@@ -421,9 +422,9 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_reg(
       for (int k = 0; k < VPT; ++k) {
         const int vi = t + k * TPR;
         if (vi < nv) {
-          b.x[k] = tg_load16(x + off + vi * V);
-          b.y[k] = tg_load16(dy + off + vi * V);
-          if (kPreO) b.o[k] = tg_load16(dx + off + vi * V);
+          b.x[k] = tg_ld16<NT>(x + off + vi * V);
+          b.y[k] = tg_ld16<NT>(dy + off + vi * V);
+          if (kPreO) b.o[k] = tg_ld16<NT>(dx + off + vi * V);
         }
       }
       b.mu = mean[row];
@@ -467,15 +468,14 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_reg(
         const int vi = t + k * TPR;
         if (vi < nv) {
           tg_vec16<T> o;
-          if (ACC && !kPreO) o = tg_load16(dx + off + vi * V);
+          if (ACC && !kPreO) o = tg_ld16<NT>(dx + off + vi * V);
 #pragma unroll
           for (int j = 0; j < V; ++j) {
             float r = rs * (dyv[k][j] * gam[k][j] - mg - xh[k][j] * mgx);
             if (ACC) r += tg_to_float(kPreO ? b.o[k].v[j] : o.v[j]);
             o.v[j] = tg_from_float<T>(r);
           }
-          if (nt) tg_store16_nt(dx + off + vi * V, o);
-          else tg_store16(dx + off + vi * V, o);
+          tg_st16<NT>(dx + off + vi * V, o);
         }
       }
     }
@@ -757,21 +757,21 @@ int ln_bwd_t(const void* x, const float* mean, const float* rstd, const float* g
     const unsigned blocks = (unsigned)p.nparts;
     const int tpr = p.tpr, vpt = p.vpt;
     const bool nt = (int64_t)sizeof(T) * rows * cols >= kNtBytes;
+#define LNARGS (const T*)x, mean, rstd, gamma, (const T*)dy, (T*)dx, part, rows, (int)cols
     if (acc_dx) {
 #define L(TPR, VPT)                                                                           \
-  k_ln_bwd_reg<T, TPR, VPT, true><<<blocks, kBlock, 0, s>>>((const T*)x, mean, rstd, gamma, \
-                                                            (const T*)dy, (T*)dx, part, rows, \
-                                                            (int)cols, nt)
+  if (nt) k_ln_bwd_reg<T, TPR, VPT, true, true><<<blocks, kBlock, 0, s>>>(LNARGS); \
+  else k_ln_bwd_reg<T, TPR, VPT, true, false><<<blocks, kBlock, 0, s>>>(LNARGS)
       TG_REG_DISPATCH(L)
 #undef L
     } else {
 #define L(TPR, VPT)                                                                            \
-  k_ln_bwd_reg<T, TPR, VPT, false><<<blocks, kBlock, 0, s>>>((const T*)x, mean, rstd, gamma, \
-                                                             (const T*)dy, (T*)dx, part, rows, \
-                                                             (int)cols, nt)
+  if (nt) k_ln_bwd_reg<T, TPR, VPT, false, true><<<blocks, kBlock, 0, s>>>(LNARGS); \
+  else k_ln_bwd_reg<T, TPR, VPT, false, false><<<blocks, kBlock, 0, s>>>(LNARGS)
       TG_REG_DISPATCH(L)
 #undef L
     }
+#undef LNARGS
   } else {
     const unsigned blocks = (unsigned)((rows + 3) / 4);
     if (acc_dx)

@@ -60,7 +60,7 @@ def test_embedding_module(cuda):
         emb(np.array([10]))
 
 
-@pytest.mark.parametrize("R,C", [(1, 1), (100, 70), (130, 1000)])
+@pytest.mark.parametrize("R,C", [(1, 1), (100, 70), (130, 1000), (64, 128), (320, 192)])
 @pytest.mark.parametrize("ds,dd", [(torch.float32, torch.float32), (torch.float16, torch.float32)])
 def test_transpose_add(cuda, R, C, ds, dd):
     g = torch.Generator(device="cuda").manual_seed(R * C)
