@@ -15,7 +15,7 @@
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kMaxT = 36;
+constexpr int kMaxT = 56;  // tensors per launch: 68 B each in the kernel argument block (< 4 KiB)
 constexpr int kEPT = 16;                     // elements per thread (grad kernels)
 constexpr int64_t kChunk = kBlock * kEPT;    // elements per workgroup
 // Adam streams four inputs and three outputs: one 16-byte vector per operand and
@@ -36,13 +36,13 @@ struct MtArgs {
   void* e[kMaxT];  // max_exp_avg_sq (AMSGrad) or null
   void* f[kMaxT];  // low-precision copy of the updated param (Adam) or null
   int64_t n[kMaxT];
-  int64_t first_block[kMaxT + 1];
+  int first_block[kMaxT + 1];  // entries past the last tensor hold INT32_MAX
   int fidx[kMaxT];  // index of each tensor in the caller's list (flag slot)
   int ntensors;
 };
 
 // Largest t with first_block[t] <= blk (binary search; tensors are in block order).
-__device__ __forceinline__ int find_tensor(const MtArgs& A, int64_t blk) {
+__device__ __forceinline__ int find_tensor(const MtArgs& A, int blk) {
   int lo = 0, hi = A.ntensors - 1;
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
@@ -352,11 +352,7 @@ int for_each_launch(int ntensors, void* const* a, void* const* b, void* const* c
   int64_t blocks = 0;
   auto flush = [&]() -> int {
     if (A.ntensors > 0) {
-      A.first_block[A.ntensors] = blocks;
-      if (blocks > 0x7fffffff) {
-        tg_set_error("multi-tensor launch: too many blocks");
-        return TG_ERR_INVALID;
-      }
+      for (int i = A.ntensors; i <= kMaxT; ++i) A.first_block[i] = 0x7fffffff;
       int st = fn(A, blocks);
       if (st) return st;
     }
@@ -374,6 +370,10 @@ int for_each_launch(int ntensors, void* const* a, void* const* b, void* const* c
       int st = flush();
       if (st) return st;
     }
+    if (blocks + (numel[i] + chunk - 1) / chunk > 0x7fffffff) {
+      tg_set_error("multi-tensor launch: too many blocks");
+      return TG_ERR_INVALID;
+    }
     const int k = A.ntensors++;
     A.a[k] = a ? a[i] : nullptr;
     A.b[k] = b ? b[i] : nullptr;
@@ -383,7 +383,7 @@ int for_each_launch(int ntensors, void* const* a, void* const* b, void* const* c
     A.f[k] = f ? f[i] : nullptr;
     A.n[k] = numel[i];
     A.fidx[k] = i;
-    A.first_block[k] = blocks;
+    A.first_block[k] = (int)blocks;
     blocks += (numel[i] + chunk - 1) / chunk;
   }
   return flush();
