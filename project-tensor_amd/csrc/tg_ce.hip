@@ -20,10 +20,15 @@ constexpr int kBlock = 256;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
+// 2^x by the hardware v_exp_f32 alone.  The arguments are <= 0 (values relative to a
+// running maximum); results below the normal range flush to zero, which changes no
+// sum of terms relative to a maximum term of 1 and no gradient rounded to fp16.
+__device__ __forceinline__ float fexp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 __device__ __forceinline__ void lse_merge(float& m, float& s, float m2, float s2) {
   const float mn = fmaxf(m, m2);
   if (mn == -INFINITY) return;  // both empty
-  s = s * exp2f(m - mn) + s2 * exp2f(m2 - mn);
+  s = s * fexp2(m - mn) + s2 * fexp2(m2 - mn);
   m = mn;
 }
 
@@ -78,12 +83,12 @@ __device__ __forceinline__ void row_stats(const T* __restrict__ x, int64_t C, fl
       const float vm = vec_max<T, U>(v) * kLog2e;
       const float mn = fmaxf(m, vm);
       const float mref = mn == -INFINITY ? 0.f : mn;
-      s *= exp2f(m - mref);
+      s *= fexp2(m - mref);
       m = mn;
 #pragma unroll
       for (int u = 0; u < U; ++u)
 #pragma unroll
-        for (int j = 0; j < V; ++j) s += exp2f(fmaf(tg_to_float(v[u].v[j]), kLog2e, -mref));
+        for (int j = 0; j < V; ++j) s += fexp2(fmaf(tg_to_float(v[u].v[j]), kLog2e, -mref));
     }
   } else {
     for (int64_t i = threadIdx.x; i < C; i += kBlock) lse_merge(m, s, tg_to_float(x[i]) * kLog2e, 1.f);
@@ -160,11 +165,17 @@ __global__ __launch_bounds__(kBlock) void k_ce_bwd(const T* __restrict__ X,
   const int64_t t = tgt[row];
   const float wu = smooth / (float)C;  // weight of every class
   const float wt = 1.f - smooth;       // extra weight of the target
+  const float wus = wu * scale, wts = wt * scale;
   if constexpr (VEC) {
     constexpr int V = tg_vec16<T>::N;
     static_assert(sizeof(T) == sizeof(TG), "vector path needs equal element sizes");
     constexpr int U = 4;
     const int64_t nv = C / V;
+    // The thread whose vectors hold the target writes its element once more, after its
+    // own loop store of it (same thread, same address: the later store wins), with the
+    // target weight included; it reads the old value first when accumulating.
+    const bool own = t >= 0 && t < C && (t / V) % kBlock == threadIdx.x;
+    const float old_t = (ACC && own) ? tg_to_float(g[t]) : 0.f;
     for (int64_t i0 = threadIdx.x; i0 < nv; i0 += U * kBlock) {
       tg_vec16<T> v[U];
       tg_vec16<TG> o[U];
@@ -180,11 +191,10 @@ __global__ __launch_bounds__(kBlock) void k_ce_bwd(const T* __restrict__ X,
       for (int u = 0; u < U; ++u) {
         const int64_t i = i0 + u * kBlock;
         if (i < nv) {
+          // (p - wu)*scale as p*scale - wu*scale; the target element is rewritten below
 #pragma unroll
           for (int j = 0; j < V; ++j) {
-            const int64_t c = i * V + j;
-            const float p = exp2f(fmaf(tg_to_float(v[u].v[j]), kLog2e, -l2));
-            float r = (p - wu - (c == t ? wt : 0.f)) * scale;
+            float r = fmaf(fexp2(fmaf(tg_to_float(v[u].v[j]), kLog2e, -l2)), scale, -wus);
             if (ACC) r += tg_to_float(o[u].v[j]);
             o[u].v[j] = tg_from_float<TG>(r);
           }
@@ -192,9 +202,14 @@ __global__ __launch_bounds__(kBlock) void k_ce_bwd(const T* __restrict__ X,
         }
       }
     }
+    if (own) {
+      float r = fmaf(fexp2(fmaf(tg_to_float(x[t]), kLog2e, -l2)), scale, -wus) - wts;
+      if (ACC) r += old_t;
+      g[t] = tg_from_float<TG>(r);
+    }
   } else {
     for (int64_t c = threadIdx.x; c < C; c += kBlock) {
-      const float p = exp2f(fmaf(tg_to_float(x[c]), kLog2e, -l2));
+      const float p = fexp2(fmaf(tg_to_float(x[c]), kLog2e, -l2));
       float r = (p - wu - (c == t ? wt : 0.f)) * scale;
       if (ACC) r += tg_to_float(g[c]);
       g[c] = tg_from_float<TG>(r);

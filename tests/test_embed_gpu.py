@@ -18,7 +18,10 @@ def L():
     return _lib
 
 
-@pytest.mark.parametrize("n,V,dim", [(1, 1, 1), (24, 5, 7), (8192, 32000, 64), (300, 50, 1000)])
+# (8192, 32000, ...) and smaller take the one-workgroup sort path; (20000, 64, 8) and
+# (500, 70000, 4) exceed its token / row limits and take the radix-sort path.
+@pytest.mark.parametrize("n,V,dim", [(1, 1, 1), (24, 5, 7), (8192, 32000, 64), (300, 50, 1000),
+                                     (16384, 3, 12), (20000, 64, 8), (500, 70000, 4)])
 def test_embedding_bwd_bit_exact_fp32(cuda, n, V, dim):
     rng = np.random.default_rng(n + V)
     idx = rng.integers(0, V, n)
@@ -31,12 +34,13 @@ def test_embedding_bwd_bit_exact_fp32(cuda, n, V, dim):
     assert np.array_equal(grad.cpu().numpy(), want)
 
 
-def test_embedding_bwd_half_accumulate_and_bounds(cuda):
+@pytest.mark.parametrize("n,V", [(200, 40), (17000, 40)])
+def test_embedding_bwd_half_accumulate_and_bounds(cuda, n, V):
     rng = np.random.default_rng(9)
-    V, dim = 40, 33
-    idx = rng.integers(0, V, 200)
+    dim = 33
+    idx = rng.integers(0, V, n)
     idx[5], idx[6] = -1, V  # out of range: skipped
-    d = rng.standard_normal((200, dim)).astype(np.float16)
+    d = rng.standard_normal((n, dim)).astype(np.float16)
     base = rng.standard_normal((V, dim)).astype(np.float32)
     grad = torch.tensor(base, device="cuda")
     L().embedding_bwd(torch.tensor(d, device="cuda"), torch.tensor(idx, device="cuda"), grad, True)
