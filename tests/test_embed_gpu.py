@@ -18,8 +18,7 @@ def L():
     return _lib
 
 
-# (8192, 32000, ...) and smaller take the one-workgroup sort path; (20000, 64, 8) and
-# (500, 70000, 4) exceed its token / row limits and take the radix-sort path.
+# includes many-token, few-row and few-token, many-row cases
 @pytest.mark.parametrize("n,V,dim", [(1, 1, 1), (24, 5, 7), (8192, 32000, 64), (300, 50, 1000),
                                      (16384, 3, 12), (20000, 64, 8), (500, 70000, 4)])
 def test_embedding_bwd_bit_exact_fp32(cuda, n, V, dim):
