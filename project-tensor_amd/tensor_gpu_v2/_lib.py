@@ -429,6 +429,40 @@ def _numel_array(ts):
     return arr
 
 
+# Validated optimizer-state lists, keyed by their device addresses: the checks and the
+# pointer arrays of params / exp_avg / exp_avg_sq (/ max_exp_avg_sq) are built once for
+# a given set of buffers and reused on every later step with the same buffers.
+_ADAM_STATE = {}
+
+
+def _adam_state(params, exp_avg, exp_avg_sq, max_exp_avg_sq):
+    key = (tuple(t.data_ptr() for t in params), tuple(t.data_ptr() for t in exp_avg),
+           tuple(t.data_ptr() for t in exp_avg_sq),
+           tuple(t.data_ptr() for t in max_exp_avg_sq) if max_exp_avg_sq else None)
+    st = _ADAM_STATE.get(key)
+    if st is not None and all(p.numel() == n for p, n in zip(params, st[1])):
+        return st
+    groups = (params, exp_avg, exp_avg_sq) + ((max_exp_avg_sq,) if max_exp_avg_sq else ())
+    for group in groups:
+        if len(group) != len(params):
+            raise ValueError("adam_step: param/state list lengths differ")
+        for t in group:
+            _dev(t, "adam operand")
+            if t.dtype != torch.float32:
+                raise TypeError("adam_step: fp32 tensors required")
+    numels = [p.numel() for p in params]
+    for p, m, v in zip(params, exp_avg, exp_avg_sq):
+        if not (p.numel() == m.numel() == v.numel()):
+            raise ValueError("adam_step: param/grad/state sizes differ")
+    if len(_ADAM_STATE) >= 16:
+        _ADAM_STATE.clear()
+    st = ((_ptr_array(params), _ptr_array(exp_avg), _ptr_array(exp_avg_sq),
+           _ptr_array(max_exp_avg_sq) if max_exp_avg_sq else None), numels,
+          _numel_array(params))
+    _ADAM_STATE[key] = st
+    return st
+
+
 def adam_step(params, grads, exp_avg, exp_avg_sq, max_exp_avg_sq, lr, beta1, beta2, eps,
               weight_decay, bias_correction1, bias_correction2, lowp=None):
     """Multi-tensor Adam/AdamW step.  `lowp`, if given, is a list parallel to `params`
@@ -437,17 +471,17 @@ def adam_step(params, grads, exp_avg, exp_avg_sq, max_exp_avg_sq, lr, beta1, bet
     n = len(params)
     if n == 0:
         return
-    for group in (params, grads, exp_avg, exp_avg_sq) + ((max_exp_avg_sq,) if max_exp_avg_sq else ()):
-        for t in group:
-            _dev(t, "adam operand")
-            if t.dtype != torch.float32:
-                raise TypeError("adam_step: fp32 tensors required")
-    for p, g, m, v in zip(params, grads, exp_avg, exp_avg_sq):
-        if not (p.numel() == g.numel() == m.numel() == v.numel()):
+    arrs, numels, numel_arr = _adam_state(params, exp_avg, exp_avg_sq, max_exp_avg_sq)
+    if len(grads) != n:
+        raise ValueError("adam_step: param/grad list lengths differ")
+    for g, k in zip(grads, numels):
+        _dev(g, "adam operand")
+        if g.dtype != torch.float32:
+            raise TypeError("adam_step: fp32 tensors required")
+        if g.numel() != k:
             raise ValueError("adam_step: param/grad/state sizes differ")
     ensure_device(params[0].device.index)
-    args = (_ptr_array(params), _ptr_array(grads), _ptr_array(exp_avg), _ptr_array(exp_avg_sq),
-            _ptr_array(max_exp_avg_sq) if max_exp_avg_sq else None, _numel_array(params),
+    args = (arrs[0], _ptr_array(grads), arrs[1], arrs[2], arrs[3], numel_arr,
             float(lr), float(beta1), float(beta2), float(eps), float(weight_decay),
             float(bias_correction1), float(bias_correction2))
     if lowp is not None and any(t is not None for t in lowp):
