@@ -505,3 +505,18 @@ def test_axpby(cuda, n, dx, dy, mis):
     y.fill_(float("nan"))
     L().axpby(x, y, 3.0, 0.0)
     assert torch.equal(y, (3.0 * x.float()).to(dy))
+
+
+@pytest.mark.parametrize("M,N,K,beta", [(1024, 4096, 8192, 0.0), (1024, 1024, 8192, 1.0),
+                                        (256, 512, 4096, 0.0)])
+def test_matmul2d_k_split(cuda, M, N, K, beta):
+    """Weight-gradient shapes (op(A) = X^T over a long token axis) that run as a K-split
+    batched GEMM plus the deterministic partial sum; fp16 operands, fp32 output,
+    overwrite and accumulate, against a float64 product (rtol 1e-4)."""
+    g = torch.Generator(device="cuda").manual_seed(M + N + K)
+    x = torch.randn(K, M, device="cuda", generator=g).half()
+    y = torch.randn(K, N, device="cuda", generator=g).half()
+    out = torch.randn(M, N, device="cuda", generator=g)
+    want = x.double().t() @ y.double() + (out.double() if beta else 0.0)
+    L().matmul2d(x, y, out, trans_a=True, beta=beta)
+    assert_close(out, want.cpu().numpy(), RTOL_F32_MM, "k-split matmul")
