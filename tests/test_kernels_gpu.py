@@ -507,7 +507,7 @@ def test_axpby(cuda, n, dx, dy, mis):
     assert torch.equal(y, (3.0 * x.float()).to(dy))
 
 
-@pytest.mark.parametrize("M,N,K,beta", [(1024, 4096, 8192, 0.0), (1024, 1024, 8192, 1.0),
+@pytest.mark.parametrize("M,N,K,beta", [(1024, 4096, 8192, 0.0), (1024, 1024, 8192, 1.0), (512, 256, 32000, 1.0),
                                         (256, 512, 4096, 0.0)])
 def test_matmul2d_k_split(cuda, M, N, K, beta):
     """Weight-gradient shapes (op(A) = X^T over a long token axis) that run as a K-split
