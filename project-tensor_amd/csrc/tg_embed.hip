@@ -97,7 +97,9 @@ __global__ __launch_bounds__(kBlock) void k_transpose_add_v4(const float* __rest
                                                              float* __restrict__ dst,
                                                              float alpha) {
   __shared__ float tile[64][65];
-  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  // blockIdx.x walks src rows (= dst columns): blocks running together cover one band
+  // of dst rows contiguously instead of striding across dst rows R*4 bytes apart.
+  const int64_t r0 = (int64_t)blockIdx.x * 64, c0 = (int64_t)blockIdx.y * 64;
   const int q = (threadIdx.x & 15) * 4, w = threadIdx.x >> 4;  // 16 x 16
   tg_vec16<float> v[4], o[4];  // both operands' loads in flight before the exchange
 #pragma unroll
@@ -300,8 +302,9 @@ TG_EXPORT int tg_transpose_add(int dtype_src, const void* src, int64_t rows, int
   hipStream_t s = tg_stream(stream);
   dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64));
   if (dtype_src == TG_F32 && dtype_dst == TG_F32 && rows % 64 == 0 && cols % 64 == 0 &&
-      tg_aligned16(src) && tg_aligned16(dst)) {
-    k_transpose_add_v4<<<grid, kBlock, 0, s>>>((const float*)src, rows, cols, (float*)dst, alpha);
+      cols / 64 <= 65535 && tg_aligned16(src) && tg_aligned16(dst)) {
+    const dim3 gt((unsigned)(rows / 64), (unsigned)(cols / 64));
+    k_transpose_add_v4<<<gt, kBlock, 0, s>>>((const float*)src, rows, cols, (float*)dst, alpha);
     return tg_check_launch("tg_transpose_add");
   }
 #define T2(TS)                                                                                  \
