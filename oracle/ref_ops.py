@@ -3,7 +3,6 @@
 Each function states the reference lines it follows.  Inputs are NumPy arrays;
 the arithmetic runs in the inputs' dtype.
 """
-import math
 
 import numpy as np
 

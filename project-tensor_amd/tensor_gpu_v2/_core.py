@@ -14,7 +14,6 @@ _core.py:637).  The first contribution is written straight into a fresh buffer
 the reference's `parent.grad += local` with one read pass fewer.  Reading
 `.grad` materialises the zeros, so observable behaviour matches.
 """
-import math
 
 import numpy as np
 import torch
