@@ -18,11 +18,6 @@ namespace {
 
 constexpr int kBlock = 256;
 
-__global__ __launch_bounds__(kBlock) void k_iota(int* __restrict__ p, int64_t n) {
-  const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-  if (i < n) p[i] = (int)i;
-}
-
 template <typename T>
 __global__ __launch_bounds__(kBlock) void k_fill_zero(T* __restrict__ p, int64_t n) {
   const int64_t stride = (int64_t)gridDim.x * kBlock;
@@ -30,36 +25,114 @@ __global__ __launch_bounds__(kBlock) void k_fill_zero(T* __restrict__ p, int64_t
     p[i] = tg_from_float<T>(0.f);
 }
 
-// One wavefront per sorted position; a wave whose position starts a run of equal
-// keys sums the run.  dim is processed in chunks of 64 lanes x 4 columns.
-template <typename TD, typename TG>
-__global__ __launch_bounds__(kBlock) void k_embed_seg(const int64_t* __restrict__ keys,
+// Sort input: positions 0..n-1 and 32-bit keys, every index outside [0, V) mapped to
+// the sentinel V (sorted after all valid keys, then skipped).  When not accumulating,
+// also clears the per-row "touched" flags.
+__global__ __launch_bounds__(kBlock) void k_embed_prep(const int64_t* __restrict__ idx,
+                                                       int64_t n, int64_t V,
+                                                       int* __restrict__ keys,
+                                                       int* __restrict__ pos,
+                                                       int* __restrict__ touched) {
+  const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (i < n) {
+    const int64_t k = idx[i];
+    keys[i] = (k >= 0 && k < V) ? (int)k : (int)V;
+    pos[i] = (int)i;
+  }
+  if (touched && i < V) touched[i] = 0;
+}
+
+// One wavefront per sorted position; a wave whose position starts a run of equal keys
+// sums the run's dout rows in their original order (four rows in flight) and writes
+// the gradient row: grad (+)= sum when accumulating, else grad = sum and the row is
+// marked touched.  VEC: each lane owns PER = 16/sizeof(TD) adjacent columns (16-byte
+// loads); else 4 columns 64 apart.
+template <typename TD, typename TG, bool VEC>
+__global__ __launch_bounds__(kBlock) void k_embed_seg(const int* __restrict__ keys,
                                                       const int* __restrict__ pos, int64_t n,
                                                       const TD* __restrict__ dout, int64_t dim,
-                                                      int64_t V, TG* __restrict__ grad) {
+                                                      int64_t V, int accumulate,
+                                                      int* __restrict__ touched,
+                                                      TG* __restrict__ grad) {
+  constexpr int PER = VEC ? 16 / (int)sizeof(TD) : 4;
+  constexpr int U = 4;
   const int lane = threadIdx.x & 63;
   const int64_t i = (int64_t)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
   if (i >= n) return;
-  const int64_t key = keys[i];
+  const int key = keys[i];
   if (i > 0 && keys[i - 1] == key) return;  // not the start of a run
-  if (key < 0 || key >= V) return;
+  if (key >= V) return;                     // sentinel: index outside [0, V)
   int64_t end = i + 1;
   while (end < n && keys[end] == key) ++end;
-  TG* grow = grad + key * dim;
-  for (int64_t c0 = 0; c0 < dim; c0 += 64 * 4) {
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int64_t j = i; j < end; ++j) {
-      const TD* drow = dout + (int64_t)pos[j] * dim;
+  TG* grow = grad + (int64_t)key * dim;
+  auto col = [&](int64_t c0, int e) {
+    return VEC ? c0 + (int64_t)lane * PER + e : c0 + (int64_t)e * 64 + lane;
+  };
+  for (int64_t c0 = 0; c0 < dim; c0 += 64 * PER) {
+    float acc[PER];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int64_t c = c0 + u * 64 + lane;
-        if (c < dim) acc[u] += tg_to_float(drow[c]);
+    for (int e = 0; e < PER; ++e) acc[e] = 0.f;
+    auto load = [&](int64_t j, float (&v)[PER]) {
+      const TD* drow = dout + (int64_t)pos[j] * dim;
+      if (VEC) {
+        if (col(c0, 0) < dim) {
+          const tg_vec16<TD> t = tg_load16(drow + col(c0, 0));
+#pragma unroll
+          for (int e = 0; e < PER; ++e) v[e] = tg_to_float(t.v[e]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < PER; ++e) v[e] = 0.f;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < PER; ++e) v[e] = col(c0, e) < dim ? tg_to_float(drow[col(c0, e)]) : 0.f;
       }
+    };
+    int64_t j = i;
+    for (; j + U <= end; j += U) {
+      float v[U][PER];
+#pragma unroll
+      for (int u = 0; u < U; ++u) load(j + u, v[u]);
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int e = 0; e < PER; ++e) acc[e] += v[u][e];
+    }
+    for (; j < end; ++j) {
+      float v[PER];
+      load(j, v);
+#pragma unroll
+      for (int e = 0; e < PER; ++e) acc[e] += v[e];
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int64_t c = c0 + u * 64 + lane;
-      if (c < dim) grow[c] = tg_from_float<TG>(tg_to_float(grow[c]) + acc[u]);
+    for (int e = 0; e < PER; ++e) {
+      const int64_t c = col(c0, e);
+      if (c < dim)
+        grow[c] = tg_from_float<TG>((accumulate ? tg_to_float(grow[c]) : 0.f) + acc[e]);
+    }
+  }
+  if (!accumulate && lane == 0) touched[key] = 1;
+}
+
+// Zero every gradient row that no index touched (not accumulating): one wavefront per
+// row, 16-byte non-temporal stores when rows are 16-byte multiples.
+template <typename TG, bool VZ>
+__global__ __launch_bounds__(kBlock) void k_embed_zero_rows(const int* __restrict__ touched,
+                                                            int64_t V, int64_t dim,
+                                                            TG* __restrict__ grad) {
+  const int lane = threadIdx.x & 63;
+  const int64_t stride = (int64_t)gridDim.x * (kBlock / 64);
+  for (int64_t r = (int64_t)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6); r < V; r += stride) {
+    if (touched[r]) continue;
+    TG* grow = grad + r * dim;
+    if (VZ) {
+      constexpr int PER = 16 / (int)sizeof(TG);
+      tg_vec16<TG> z;
+#pragma unroll
+      for (int e = 0; e < PER; ++e) z.v[e] = tg_from_float<TG>(0.f);
+      for (int64_t c = (int64_t)lane * PER; c < dim; c += 64 * PER) tg_store16_nt(grow + c, z);
+    } else {
+      for (int64_t c = lane; c < dim; c += 64) grow[c] = tg_from_float<TG>(0.f);
     }
   }
 }
@@ -127,9 +200,9 @@ int sort_bits(int64_t V) {
 
 size_t sort_temp_bytes(int64_t n, int64_t V) {
   size_t bytes = 0;
-  (void)rocprim::radix_sort_pairs(nullptr, bytes, (const int64_t*)nullptr, (int64_t*)nullptr,
+  (void)rocprim::radix_sort_pairs(nullptr, bytes, (const int*)nullptr, (int*)nullptr,
                                   (const int*)nullptr, (int*)nullptr, (size_t)n, 0,
-                                  sort_bits(V));
+                                  sort_bits(V + 1));
   return bytes;
 }
 
@@ -193,31 +266,62 @@ int embed_fwd_t(const void* w, const int64_t* idx, int64_t n, int64_t dim, int64
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
+// Workspace: keys_in, keys_out, pos_in, pos_out (n ints each), touched (V ints), then
+// rocPRIM's radix-sort scratch.
+size_t embed_ws(int64_t n, int64_t V, size_t* tmp_off) {
+  const size_t fixed = 4 * align256(n * sizeof(int)) + align256(V * sizeof(int));
+  if (tmp_off) *tmp_off = fixed;
+  return fixed + align256(sort_temp_bytes(n, V));
+}
+
 template <typename TD, typename TG>
 int embed_t(const void* dout, const int64_t* idx, int64_t n, int64_t dim, void* grad, int64_t V,
             int accumulate, char* ws, size_t ws_bytes, hipStream_t s) {
-  if (!accumulate) {
-    const int64_t total = V * dim;
-    int64_t blocks = (total + kBlock - 1) / kBlock;
-    if (blocks > (int64_t)tg_num_cus() * 16) blocks = (int64_t)tg_num_cus() * 16;
-    if (blocks < 1) blocks = 1;
-    k_fill_zero<TG><<<(unsigned)blocks, kBlock, 0, s>>>((TG*)grad, total);
+  if (n == 0) {  // nothing indexed: the gradient is zero (or unchanged)
+    if (!accumulate) {
+      const int64_t total = V * dim;
+      int64_t blocks = (total + kBlock - 1) / kBlock;
+      if (blocks > (int64_t)tg_num_cus() * 16) blocks = (int64_t)tg_num_cus() * 16;
+      k_fill_zero<TG><<<(unsigned)(blocks < 1 ? 1 : blocks), kBlock, 0, s>>>((TG*)grad, total);
+    }
+    return tg_check_launch("tg_embedding_bwd");
   }
-  if (n == 0) return tg_check_launch("tg_embedding_bwd");
-  int64_t* keys_out = (int64_t*)ws;
-  int* pos_in = (int*)(ws + align256(n * sizeof(int64_t)));
-  int* pos_out = (int*)((char*)pos_in + align256(n * sizeof(int)));
-  char* tmp = (char*)pos_out + align256(n * sizeof(int));
-  size_t tmp_bytes = ws_bytes - (size_t)(tmp - ws);
-  k_iota<<<(unsigned)((n + kBlock - 1) / kBlock), kBlock, 0, s>>>(pos_in, n);
-  if (rocprim::radix_sort_pairs(tmp, tmp_bytes, idx, keys_out, pos_in, pos_out, (size_t)n, 0,
-                                sort_bits(V), s) != hipSuccess) {
+  size_t tmp_off = 0;
+  embed_ws(n, V, &tmp_off);
+  const size_t nb = align256(n * sizeof(int));
+  int* keys_in = (int*)ws;
+  int* keys_out = (int*)(ws + nb);
+  int* pos_in = (int*)(ws + 2 * nb);
+  int* pos_out = (int*)(ws + 3 * nb);
+  int* touched = accumulate ? nullptr : (int*)(ws + 4 * nb);
+  char* tmp = ws + tmp_off;
+  size_t tmp_bytes = ws_bytes - tmp_off;
+  const int64_t m = n > V ? n : V;
+  k_embed_prep<<<(unsigned)((m + kBlock - 1) / kBlock), kBlock, 0, s>>>(idx, n, V, keys_in, pos_in,
+                                                                        touched);
+  if (rocprim::radix_sort_pairs(tmp, tmp_bytes, keys_in, keys_out, pos_in, pos_out, (size_t)n, 0,
+                                sort_bits(V + 1), s) != hipSuccess) {
     tg_set_error("tg_embedding_bwd: radix sort failed");
     return TG_ERR_HIP;
   }
-  k_embed_seg<TD, TG><<<(unsigned)((n + 3) / 4), kBlock, 0, s>>>(keys_out, pos_out, n,
-                                                                   (const TD*)dout, dim, V,
-                                                                   (TG*)grad);
+  constexpr int PER = 16 / (int)sizeof(TD);
+  const bool vec = dim % PER == 0 && tg_aligned16(dout);
+  const unsigned sb = (unsigned)((n + 3) / 4);
+  if (vec)
+    k_embed_seg<TD, TG, true><<<sb, kBlock, 0, s>>>(keys_out, pos_out, n, (const TD*)dout, dim, V,
+                                                    accumulate, touched, (TG*)grad);
+  else
+    k_embed_seg<TD, TG, false><<<sb, kBlock, 0, s>>>(keys_out, pos_out, n, (const TD*)dout, dim,
+                                                     V, accumulate, touched, (TG*)grad);
+  if (!accumulate) {
+    int64_t blocks = (V + 3) / 4;
+    if (blocks > (int64_t)tg_num_cus() * 32) blocks = (int64_t)tg_num_cus() * 32;
+    const bool vz = (dim * (int64_t)sizeof(TG)) % 16 == 0 && tg_aligned16(grad);
+    if (vz)
+      k_embed_zero_rows<TG, true><<<(unsigned)blocks, kBlock, 0, s>>>(touched, V, dim, (TG*)grad);
+    else
+      k_embed_zero_rows<TG, false><<<(unsigned)blocks, kBlock, 0, s>>>(touched, V, dim, (TG*)grad);
+  }
   return tg_check_launch("tg_embedding_bwd");
 }
 
@@ -225,8 +329,7 @@ int embed_t(const void* dout, const int64_t* idx, int64_t n, int64_t dim, void* 
 
 TG_EXPORT size_t tg_embedding_bwd_workspace(int64_t n_tokens, int64_t num_embeddings) {
   if (n_tokens <= 0) return 0;
-  return align256(n_tokens * sizeof(int64_t)) + 2 * align256(n_tokens * sizeof(int)) +
-         align256(sort_temp_bytes(n_tokens, num_embeddings > 1 ? num_embeddings : 2));
+  return embed_ws(n_tokens, num_embeddings > 1 ? num_embeddings : 1, nullptr);
 }
 
 TG_EXPORT int tg_embedding_bwd(int dtype_dout, const void* dout, const int64_t* indices,
@@ -234,6 +337,7 @@ TG_EXPORT int tg_embedding_bwd(int dtype_dout, const void* dout, const int64_t* 
                                int64_t num_embeddings, int accumulate, void* workspace,
                                size_t workspace_bytes, void* stream) {
   TG_REQUIRE(n_tokens >= 0 && dim > 0 && num_embeddings > 0, "tg_embedding_bwd: bad shape");
+  TG_REQUIRE(num_embeddings < 0x7fffffff, "tg_embedding_bwd: too many rows");
   TG_REQUIRE(n_tokens <= 0x7fffffff, "tg_embedding_bwd: too many tokens");
   TG_REQUIRE(grad && (n_tokens == 0 || (dout && indices)), "tg_embedding_bwd: null pointer");
   const size_t need = tg_embedding_bwd_workspace(n_tokens, num_embeddings);

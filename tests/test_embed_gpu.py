@@ -63,6 +63,24 @@ def test_embedding_module(cuda):
         emb(np.array([10]))
 
 
+@pytest.mark.parametrize("acc", [False, True])
+def test_embedding_bwd_out_of_range_power_of_two_rows(cuda, acc):
+    """Indices -1 and V with V a power of two share their low bits with the valid keys
+    V-1 and 0; they must still be skipped, and rows V-1 and 0 summed exactly once."""
+    V, dim = 64, 24
+    rng = np.random.default_rng(21)
+    idx = np.array([63, -1, 0, 64, 63, -1, 0, 64, 5] * 7)
+    d = rng.standard_normal((idx.size, dim)).astype(np.float32)
+    base = rng.standard_normal((V, dim)).astype(np.float32)
+    grad = torch.tensor(base, device="cuda")
+    L().embedding_bwd(torch.tensor(d, device="cuda"), torch.tensor(idx, device="cuda"), grad, acc)
+    ok = (idx >= 0) & (idx < V)
+    want = O.embedding_bwd(idx[ok], d[ok], V)
+    if acc:
+        want = base + want.astype(np.float32)
+    assert np.array_equal(grad.cpu().numpy(), want.astype(np.float32))
+
+
 @pytest.mark.parametrize("R,C", [(1, 1), (100, 70), (130, 1000), (64, 128), (320, 192)])
 @pytest.mark.parametrize("ds,dd", [(torch.float32, torch.float32), (torch.float16, torch.float32)])
 def test_transpose_add(cuda, R, C, ds, dd):
