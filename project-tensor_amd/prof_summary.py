@@ -3,10 +3,15 @@
     python project-tensor_amd/prof_summary.py stats <dir>     # kernel_stats.csv table
     python project-tensor_amd/prof_summary.py pmc <dir> ...   # per-kernel counter means
     python project-tensor_amd/prof_summary.py traffic <fetch_dir> <write_dir> <calib_bytes>
+    python project-tensor_amd/prof_summary.py mfma <dir> [n_xcd] [n_simd]
 
 ``stats`` prints, per kernel, calls, total and average duration.  ``pmc`` prints,
 per kernel, the mean per dispatch of every counter in counter_collection.csv
-(FETCH_SIZE and WRITE_SIZE are in KiB per dispatch).
+(FETCH_SIZE and WRITE_SIZE are in KiB per dispatch).  ``mfma`` reads a run with
+SQ_VALU_MFMA_BUSY_CYCLES, SQ_INSTS_VALU_MFMA_MOPS_F16 and GRBM_GUI_ACTIVE and prints,
+per MFMA kernel, the fp16 flops executed per dispatch (MOPS x 512) and the MFMA
+utilisation busy / (active cycles x SIMDs), where GRBM_GUI_ACTIVE is summed over the
+n_xcd XCDs (default 8) and n_simd is the SIMD count (default 1024).
 """
 import collections
 import csv
@@ -96,10 +101,25 @@ def traffic(fetch_dir, write_dir, calib_bytes):
             print(f"traffic {name.replace(' ', '')} {fb + wb:.0f} # fetch {fb:.0f} write {wb:.0f}")
 
 
+def mfma(d, n_xcd=8, n_simd=1024):
+    n_xcd, n_simd = int(n_xcd), int(n_simd)
+    busy = _pmc_means(d, "SQ_VALU_MFMA_BUSY_CYCLES")
+    mops = _pmc_means(d, "SQ_INSTS_VALU_MFMA_MOPS_F16")
+    act = _pmc_means(d, "GRBM_GUI_ACTIVE")
+    print(f"{'GFLOP/disp':>11} {'MFMA util':>9}  kernel   (GRBM_GUI_ACTIVE / {n_xcd} XCDs, {n_simd} SIMDs)")
+    for k in sorted(busy):
+        if not mops.get(k) or k not in act:
+            continue
+        util = busy[k] / (act[k] / n_xcd * n_simd)
+        print(f"{mops[k] * 512 / 1e9:11.1f} {100 * util:8.1f}%  {k}")
+
+
 if __name__ == "__main__":
     mode, args = sys.argv[1], sys.argv[2:]
     if mode == "traffic":
         traffic(*args)
+    elif mode == "mfma":
+        mfma(*args)
     else:
         for d in args:
             {"stats": stats, "pmc": pmc}[mode](d)
