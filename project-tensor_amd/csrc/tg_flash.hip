@@ -27,7 +27,8 @@
 //     dS = P*(dP - D)*scale, dV += P^T dO, dK += dS^T Q.
 //   k_fa_bwd_dq: one workgroup = 128 queries, loop over key tiles of 64:
 //     S^T = K Q^T (lane = query), dP^T = V dO^T, dQ += dS K.
-//   D = rowsum(dO * O) comes from k_fa_bwd_prep.
+//   D = rowsum(dO * O) is formed by k_fa_bwd_dq (launched first) for its queries and
+//   stored for k_fa_bwd_dkdv.
 #include "tg_common.h"
 
 namespace {
@@ -274,36 +275,6 @@ __global__ __launch_bounds__(kThreads) void k_fa_fwd(const T* __restrict__ Q,
 }
 
 // ============================================================================ backward
-// D[q] = sum_d dO[q][d] * O[q][d] (fp32); 16 lanes per row.
-template <typename T, int D>
-__global__ __launch_bounds__(kThreads) void k_fa_bwd_prep(const T* __restrict__ O,
-                                                          const T* __restrict__ dO,
-                                                          float* __restrict__ Dv, int64_t rows,
-                                                          int64_t S, FaLay lay) {
-  // row: memory row of O / dO (both in the same layout); Dv is [B, H, S]
-  const int64_t row = (int64_t)blockIdx.x * (kThreads / 16) + threadIdx.x / 16;
-  const int sub = threadIdx.x & 15;
-  float acc = 0.f;
-  if (row < rows) {
-    for (int d = sub * 8; d < D; d += 128) {
-      const typename Vec8<T>::type a = ld8(O + row * D + d);
-      const typename Vec8<T>::type b = ld8(dO + row * D + d);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc += (float)a[e] * (float)b[e];
-    }
-  }
-#pragma unroll
-  for (int off = 8; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 16);
-  if (row < rows && sub == 0) {
-    int64_t di = row;
-    if (lay.bshd) {  // row = (b*S + s)*H + h  ->  (b*H + h)*S + s
-      const int64_t b = row / (S * lay.H), rem = row % (S * lay.H);
-      di = (b * lay.H + rem % lay.H) * S + rem / lay.H;
-    }
-    Dv[di] = acc;
-  }
-}
-
 template <typename T>
 __device__ __forceinline__ void store_c_tile(T* __restrict__ out, int64_t ld, int64_t row0,
                                              int64_t nrows, int col, const f32x16& acc, float mul,
@@ -975,9 +946,9 @@ __device__ __forceinline__ void dq_tile(const char* ks, const char* vs, int64_t 
 template <typename T, int D, int BN, int OCC>
 __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dq(
     const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
-    const T* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Dv,
-    T* __restrict__ dQ, int64_t Sq, int64_t Sk, float scale, int causal, int accumulate,
-    FaLay lay) {
+    const T* __restrict__ O, const T* __restrict__ dO, const float* __restrict__ LSE,
+    float* __restrict__ Dv, T* __restrict__ dQ, int64_t Sq, int64_t Sk, float scale,
+    int causal, int accumulate, FaLay lay) {
   constexpr int DK = D / 16, DT = D / 32, TB = BN * D * 2;
   __shared__ __attribute__((aligned(1024))) char k0s[TB];
   __shared__ __attribute__((aligned(1024))) char v0s[TB];
@@ -986,6 +957,7 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dq(
   int64_t tile, bh;
   fa_block(tile, bh, lay.G);
   Q += lay.head(bh, Sq, D);
+  O += lay.head(bh, Sq, D);
   dO += lay.head(bh, Sq, D);
   dQ += lay.head(bh, Sq, D);
   K += lay.head(bh, Sk, D);
@@ -1009,7 +981,18 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dq(
     of[ks] = ld8(dO + qc * rs + ks * 16 + h * 8);
   }
   const float lq = LSE[qc] * kLog2e;
-  const float dqs = Dv[qc] * scale;
+  // D = rowsum(dO * O) of this lane's query: the two lane halves hold the two halves of
+  // the head dimension.  Stored for the dK/dV kernel, which runs after this one.
+  float dsum = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < DK; ++ks) {
+    const typename Vec8<T>::type ov = ld8(O + qc * rs + ks * 16 + h * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dsum += (float)ov[e] * (float)of[ks][e];
+  }
+  dsum += __shfl_xor(dsum, 32, 64);
+  if (h == 0 && q < Sq) Dv[q] = dsum;
+  const float dqs = dsum * scale;
   f32x16 acc[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
@@ -1271,18 +1254,16 @@ template <typename T, int D>
 int bwd_t(const void* q, const void* k, const void* v, const void* o, const void* dout,
           const float* lse, void* dq, void* dk, void* dv, int64_t BH, int64_t Sq, int64_t Sk,
           float scale, int causal, int acc, float* dvec, FaLay lay, hipStream_t s) {
-  const int64_t rows = BH * Sq;
-  k_fa_bwd_prep<T, D><<<(unsigned)((rows + 15) / 16), kThreads, 0, s>>>(
-      (const T*)o, (const T*)dout, dvec, rows, Sq, lay);
   using C = BwdCfg<D>;
+  // dQ first: it also forms D = rowsum(dO * O) per query, which the dK/dV kernel reads.
+  dim3 gq((unsigned)((Sq + 127) / 128), (unsigned)BH);
+  k_fa_bwd_dq<T, D, C::BN, C::OCC_Q><<<gq, kThreads, 0, s>>>((const T*)q, (const T*)k, (const T*)v,
+                                            (const T*)o, (const T*)dout, lse, dvec, (T*)dq, Sq,
+                                            Sk, scale, causal, acc, lay);
   dim3 gkv((unsigned)((Sk + 128 * C::KG - 1) / (128 * C::KG)), (unsigned)BH);
   k_fa_bwd_dkdv<T, D, C::BM, C::KG, C::OCC_KV><<<gkv, kThreads, 0, s>>>((const T*)q, (const T*)k, (const T*)v,
                                                (const T*)dout, lse, dvec, (T*)dk, (T*)dv, Sq, Sk,
                                                scale, causal, acc, lay);
-  dim3 gq((unsigned)((Sq + 127) / 128), (unsigned)BH);
-  k_fa_bwd_dq<T, D, C::BN, C::OCC_Q><<<gq, kThreads, 0, s>>>((const T*)q, (const T*)k, (const T*)v,
-                                            (const T*)dout, lse, dvec, (T*)dq, Sq, Sk, scale,
-                                            causal, acc, lay);
   return tg_check_launch("tg_flash_attn_bwd");
 }
 
