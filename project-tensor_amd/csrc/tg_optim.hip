@@ -18,10 +18,10 @@ constexpr int kBlock = 256;
 constexpr int kMaxT = 56;  // tensors per launch: 68 B each in the kernel argument block (< 4 KiB)
 constexpr int kEPT = 16;                     // elements per thread (grad kernels)
 constexpr int64_t kChunk = kBlock * kEPT;    // elements per workgroup
-// Adam streams four inputs and three outputs: one 16-byte vector per operand and
-// thread in 64-thread workgroups, with non-temporal loads and stores, measured
-// fastest for that mix (0.78 of peak against 0.69 with 256-thread workgroups).
-constexpr int kAdamEPT = 4;
+// Adam streams four inputs and three outputs: two 16-byte vectors per operand and
+// thread in 64-thread workgroups, with non-temporal loads and stores (measured 0.73 of
+// peak; one vector per thread 0.69, four 0.67, 256-thread workgroups 0.66).
+constexpr int kAdamEPT = 8;
 constexpr int kAdamBlock = 64;
 constexpr int64_t kAdamChunk = kAdamBlock * kAdamEPT;
 // Unscale (one stream in, one out): one 16-byte vector per thread.
@@ -127,21 +127,25 @@ struct AdamConsts {
   int decay;
 };
 
-// The 4 fp32 elements a thread owns in an Adam chunk (ChunkMap<float, 4>: elements
-// start + 4*tid .. +3), stored as 4 low-precision values: one 8-byte store when FULL.
-template <typename TL, bool FULL>
-__device__ __forceinline__ void store_lowp4(TL* __restrict__ p, int64_t start, int64_t end,
-                                            const float (&x)[4]) {
-  const int64_t i0 = start + (int64_t)threadIdx.x * 4;
-  if (FULL) {
-    TL v[4];
+// The E fp32 elements a thread owns in an Adam chunk (ChunkMap<float, E, kAdamBlock>:
+// groups of 4 at start + 4*(j*kAdamBlock + tid)), stored as low-precision values: one
+// 8-byte store per group when FULL.
+template <typename TL, bool FULL, int E>
+__device__ __forceinline__ void store_lowp(TL* __restrict__ p, int64_t start, int64_t end,
+                                           const float (&x)[E]) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) v[k] = tg_from_float<TL>(x[k]);
-    *reinterpret_cast<uint2*>(p + i0) = *reinterpret_cast<const uint2*>(v);
-  } else {
+  for (int j = 0; j < E / 4; ++j) {
+    const int64_t i0 = start + ((int64_t)j * kAdamBlock + threadIdx.x) * 4;
+    if (FULL) {
+      TL v[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
-      if (i0 + k < end) p[i0 + k] = tg_from_float<TL>(x[k]);
+      for (int k = 0; k < 4; ++k) v[k] = tg_from_float<TL>(x[4 * j + k]);
+      *reinterpret_cast<uint2*>(p + i0) = *reinterpret_cast<const uint2*>(v);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (i0 + k < end) p[i0 + k] = tg_from_float<TL>(x[4 * j + k]);
+    }
   }
 }
 
@@ -178,9 +182,8 @@ __device__ __forceinline__ void adam_chunk(float* __restrict__ p, const float* _
     Vv[i] = vv;
   }
   store_chunk<float, FULL, E, true, kAdamBlock>(p, start, end, P);
-  static_assert(E == 4, "store_lowp4 covers four elements per thread");
-  if (LP == 1 && lp) store_lowp4<tg_half, FULL>((tg_half*)lp, start, end, P);
-  if (LP == 2 && lp) store_lowp4<tg_bf16, FULL>((tg_bf16*)lp, start, end, P);
+  if (LP == 1 && lp) store_lowp<tg_half, FULL, E>((tg_half*)lp, start, end, P);
+  if (LP == 2 && lp) store_lowp<tg_bf16, FULL, E>((tg_bf16*)lp, start, end, P);
   store_chunk<float, FULL, E, true, kAdamBlock>(m, start, end, Mv);
   store_chunk<float, FULL, E, true, kAdamBlock>(v, start, end, Vv);
   if (AMS) store_chunk<float, FULL, E, true, kAdamBlock>(vm, start, end, VM);
