@@ -9,7 +9,6 @@
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kUnroll = 4;
 
 enum { OP_GELU = 0, OP_SILU = 1 };
 
@@ -63,6 +62,7 @@ template <int OP> __device__ __forceinline__ float act_fwd(float x) {
 // measured optimum for two-in/one-out streams); NT marks loads and stores
 // non-temporal, chosen for operands too large to stay in the Infinity Cache.
 constexpr int kUnrollBwd = 1;
+constexpr int kUnrollFwd = 1;  // one-in/one-out: one 16-byte vector per thread as well
 constexpr int64_t kNtBytes = 128ll << 20;
 
 template <typename T, int OP, bool ACC, bool NT>
@@ -106,26 +106,26 @@ __global__ __launch_bounds__(kThreads) void k_act_bwd(const T* __restrict__ x,
   }
 }
 
-template <typename T, int OP>
+template <typename T, int OP, bool NT>
 __global__ __launch_bounds__(kThreads) void k_act_fwd(const T* __restrict__ x,
                                                       T* __restrict__ y, int64_t nvec,
                                                       int64_t n) {
   constexpr int V = tg_vec16<T>::N;
-  const int64_t base = (int64_t)blockIdx.x * kThreads * kUnroll + threadIdx.x;
-  tg_vec16<T> xv[kUnroll];
+  const int64_t base = (int64_t)blockIdx.x * kThreads * kUnrollFwd + threadIdx.x;
+  tg_vec16<T> xv[kUnrollFwd];
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
+  for (int u = 0; u < kUnrollFwd; ++u) {
     const int64_t i = base + (int64_t)u * kThreads;
-    if (i < nvec) xv[u] = tg_load16(x + i * V);
+    if (i < nvec) xv[u] = tg_ld16<NT>(x + i * V);
   }
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
+  for (int u = 0; u < kUnrollFwd; ++u) {
     const int64_t i = base + (int64_t)u * kThreads;
     if (i < nvec) {
       tg_vec16<T> r;
 #pragma unroll
       for (int j = 0; j < V; ++j) r.v[j] = tg_from_float<T>(act_fwd<OP>(tg_to_float(xv[u].v[j])));
-      tg_store16(y + i * V, r);
+      tg_st16<NT>(y + i * V, r);
     }
   }
   if (blockIdx.x == 0) {
@@ -160,9 +160,12 @@ int launch_act_fwd(const void* x, void* y, int64_t n, hipStream_t s) {
   constexpr int V = tg_vec16<T>::N;
   const bool vec = tg_aligned16(x) && tg_aligned16(y);
   const int64_t nvec = vec ? n / V : 0;
-  int64_t blocks = (nvec + kThreads * kUnroll - 1) / (kThreads * kUnroll);
+  int64_t blocks = (nvec + kThreads * kUnrollFwd - 1) / (kThreads * kUnrollFwd);
   if (blocks < 1) blocks = 1;
-  k_act_fwd<T, OP><<<(unsigned)blocks, kThreads, 0, s>>>((const T*)x, (T*)y, nvec, n);
+  if ((int64_t)sizeof(T) * n >= kNtBytes)
+    k_act_fwd<T, OP, true><<<(unsigned)blocks, kThreads, 0, s>>>((const T*)x, (T*)y, nvec, n);
+  else
+    k_act_fwd<T, OP, false><<<(unsigned)blocks, kThreads, 0, s>>>((const T*)x, (T*)y, nvec, n);
   return tg_check_launch(OP == OP_GELU ? "tg_gelu_fwd" : "tg_silu_fwd");
 }
 
