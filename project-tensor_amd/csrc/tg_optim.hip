@@ -292,20 +292,34 @@ __global__ __launch_bounds__(kBlock) void k_norm_partial(MtArgs A, float p, doub
   }
 }
 
-// Deterministic single-block reduction of the partials.
+// Deterministic single-block reduction of the partials: 1024 threads, each with
+// kNF independent accumulators over a fixed stride (kNF loads in flight instead of
+// one dependent chain), then a fixed-order tree.
+constexpr int kNormFinal = 1024;
+constexpr int kNF = 8;
 template <int KIND>
-__global__ __launch_bounds__(kBlock) void k_norm_final(const double* part, int64_t n,
-                                                       double* out) {
-  double acc = 0.0;
-  for (int64_t i = threadIdx.x; i < n; i += kBlock)
-    acc = KIND == 1 ? fmax(acc, part[i]) : acc + part[i];
-  __shared__ double red[kBlock];
-  red[threadIdx.x] = acc;
+__global__ __launch_bounds__(kNormFinal) void k_norm_final(const double* part, int64_t n,
+                                                           double* out) {
+  auto comb = [](double a, double b) { return KIND == 1 ? fmax(a, b) : a + b; };
+  double acc[kNF];
+#pragma unroll
+  for (int u = 0; u < kNF; ++u) acc[u] = 0.0;
+  for (int64_t i0 = threadIdx.x; i0 < n; i0 += (int64_t)kNormFinal * kNF) {
+#pragma unroll
+    for (int u = 0; u < kNF; ++u) {
+      const int64_t i = i0 + (int64_t)u * kNormFinal;
+      if (i < n) acc[u] = comb(acc[u], part[i]);
+    }
+  }
+#pragma unroll
+  for (int w = kNF / 2; w >= 1; w /= 2)
+#pragma unroll
+    for (int u = 0; u < w; ++u) acc[u] = comb(acc[u], acc[u + w]);
+  __shared__ double red[kNormFinal];
+  red[threadIdx.x] = acc[0];
   __syncthreads();
-  for (int s = kBlock / 2; s > 0; s >>= 1) {
-    if (threadIdx.x < s)
-      red[threadIdx.x] = KIND == 1 ? fmax(red[threadIdx.x], red[threadIdx.x + s])
-                                   : red[threadIdx.x] + red[threadIdx.x + s];
+  for (int s = kNormFinal / 2; s > 0; s >>= 1) {
+    if (threadIdx.x < s) red[threadIdx.x] = comb(red[threadIdx.x], red[threadIdx.x + s]);
     __syncthreads();
   }
   if (threadIdx.x == 0) out[0] = red[0];
@@ -549,9 +563,9 @@ TG_EXPORT int tg_grad_norm(int ntensors, int dtype, void* const* grads, const in
                          });
   if (st) return st;
   if (norm_kind == 1)
-    k_norm_final<1><<<1, kBlock, 0, s>>>(part, nb_total, out);
+    k_norm_final<1><<<1, kNormFinal, 0, s>>>(part, nb_total, out);
   else
-    k_norm_final<0><<<1, kBlock, 0, s>>>(part, nb_total, out);
+    k_norm_final<0><<<1, kNormFinal, 0, s>>>(part, nb_total, out);
   return tg_check_launch("tg_grad_norm final");
 }
 
