@@ -511,9 +511,25 @@ def _group_by_dtype(ts):
     return groups
 
 
-def unscale_check(grads, mul, write=True):
+# Per-device buffers reused by the multi-tensor checks (flags, norm results and
+# partials): allocating them anew on every call costs more host time than the calls
+# themselves, and that host time sits between two read-backs with the GPU idle.
+_SCRATCH = {}
+
+
+def _scratch(key, nbytes, device):
+    k = (key, device, stream_handle().value)  # per stream: calls on one stream are ordered
+    t = _SCRATCH.get(k)
+    if t is None or t.numel() < nbytes:
+        t = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+        _SCRATCH[k] = t
+    return t
+
+
+def unscale_check(grads, mul, write=True, readback=True):
     """Scale grads in place by `mul`; return per-tensor flags (host list of ints):
-    bit 0 = non-finite before scaling, bit 1 = non-finite after."""
+    bit 0 = non-finite before scaling, bit 1 = non-finite after.  With readback False
+    nothing is read back (no host synchronisation) and None is returned."""
     n = len(grads)
     if n == 0:
         return []
@@ -521,20 +537,26 @@ def unscale_check(grads, mul, write=True):
         _dev(t, "grad")
     dev = grads[0].device
     ensure_device(dev.index)
-    flags = torch.empty(n, dtype=torch.int32, device=dev)
+    flags = _scratch("flags", 4 * n, dev)[: 4 * n].view(torch.int32)
     out = [0] * n
     lib = load()
     groups = _group_by_dtype(grads)
+    off = 0
     for dt, idx in groups.items():
         sub = [grads[i] for i in idx]
-        fl = flags[: len(sub)] if len(groups) == 1 else torch.empty(len(sub), dtype=torch.int32,
-                                                                    device=dev)
+        fl = flags[off: off + len(sub)]
+        off += len(sub)
         _check("tg_unscale_check", lib.tg_unscale_check(
             len(sub), dtype_code(sub[0]), _ptr_array(sub), _numel_array(sub), float(mul),
             int(bool(write)), ptr(fl), stream_handle()))
-        host = fl.cpu().tolist()
+    if not readback:
+        return None
+    host = flags.cpu().tolist()
+    off = 0
+    for dt, idx in groups.items():
         for j, i in enumerate(idx):
-            out[i] = host[j]
+            out[i] = host[off + j]
+        off += len(idx)
     return out
 
 
@@ -549,24 +571,35 @@ def grad_norm(grads, norm_kind, p=2.0):
     dev = grads[0].device
     ensure_device(dev.index)
     lib = load()
-    total = 0.0
-    flags_out = [0] * n
-    for dt, idx in _group_by_dtype(grads).items():
+    groups = list(_group_by_dtype(grads).items())
+    # one buffer for every group's result (fp64 value, 8 bytes) and flags (4 bytes each):
+    # a single device-to-host copy
+    buf = _scratch("norm", 8 * len(groups) + 4 * n, dev)[: 8 * len(groups) + 4 * n]
+    vals = buf[: 8 * len(groups)].view(torch.float64)
+    fls = buf[8 * len(groups):].view(torch.int32)
+    off = 0
+    for gi, (dt, idx) in enumerate(groups):
         sub = [grads[i] for i in idx]
         numel = _numel_array(sub)
-        ws = workspace(lib.tg_grad_norm_workspace(len(sub), numel), dev)
-        # value (fp64) and flags share one buffer: one device-to-host copy per group
-        buf = torch.empty(2 + len(sub), dtype=torch.int32, device=dev)
-        out = buf[:2].view(torch.float64)
-        fl = buf[2:]
+        nb = lib.tg_grad_norm_workspace(len(sub), numel)
+        ws = _scratch(("normws", gi), nb, dev)
         _check("tg_grad_norm", lib.tg_grad_norm(
             len(sub), dtype_code(sub[0]), _ptr_array(sub), numel, int(norm_kind), float(p),
-            ptr(out), ptr(fl), ptr(ws), ws.numel(), stream_handle()))
-        host = buf.cpu()
-        v = float(host[:2].view(torch.float64)[0])
+            ptr(vals[gi:gi + 1]), ptr(fls[off: off + len(sub)]), ptr(ws), ws.numel(),
+            stream_handle()))
+        off += len(sub)
+    host = buf.cpu()
+    hv = host[: 8 * len(groups)].view(torch.float64).tolist()
+    hf = host[8 * len(groups):].view(torch.int32).tolist()
+    total = 0.0
+    flags_out = [0] * n
+    off = 0
+    for gi, (dt, idx) in enumerate(groups):
+        v = float(hv[gi])
         total = max(total, v) if norm_kind == 1 else total + v
-        for j, f in enumerate(host[2:].tolist()):
-            flags_out[idx[j]] = f
+        for j, i in enumerate(idx):
+            flags_out[i] = hf[off + j]
+        off += len(idx)
     return total, flags_out
 
 
@@ -582,9 +615,9 @@ def zero_nonfinite(grads):
 
 
 def scale_(grads, mul):
-    """g *= mul for every tensor (no checks needed by the caller)."""
+    """g *= mul for every tensor (no checks needed by the caller, no read-back)."""
     if grads:
-        unscale_check(grads, mul, write=True)
+        unscale_check(grads, mul, write=True, readback=False)
 
 
 # ---------------------------------------------------------------- GEMM
