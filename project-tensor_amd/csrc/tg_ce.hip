@@ -6,12 +6,13 @@
 //   reference applies it without the loss's upstream gradient (_nn.py:1168-1180).
 //
 // One workgroup per row.  The forward streams the row once, each thread keeping an
-// online (max, sum of exp) pair per 16-byte vector, merged across the workgroup; it
+// online (max, sum of exp) pair over its elements, merged across the workgroup; it
 // stores the row's log-sum-exp for the backward, which streams the row once more
-// and writes the gradient.  Arithmetic is fp32; the gradient is rounded to its
-// storage dtype once (for fp16 logits, (p - w)/N below fp16's range rounds to zero
-// as in the reference's fp16 arithmetic).  A target outside [0, C) yields a NaN
-// loss and an all-(p*scale) gradient row instead of an out-of-bounds access.
+// (rows in reverse launch order) and writes the gradient.  Arithmetic is fp32; the
+// gradient is rounded to its storage dtype once (for fp16 logits, (p - w)/N below
+// fp16's range rounds to zero as in the reference's fp16 arithmetic).  A target
+// outside [0, C) yields a NaN loss and an all-(p*scale) gradient row instead of an
+// out-of-bounds access.
 #include "tg_common.h"
 
 namespace {
