@@ -11,9 +11,10 @@ element for each of the four) divided by the step's wall time: GB/s.
 
 Per-kernel durations come from HIP events recorded on the stream the kernels
 run on (torch's current stream, which every libtgbwd launch uses), around each
-launch inside the timed region.  Other configurations (BatchNorm-ReLU NHWC,
-AdamW, GradScaler unscale, the C5 GEMMs, FlashAttention backward, the GPT step)
-are reported under "components" with their own roofline fractions.
+launch inside the timed region.  Other configurations (the C1 README MLP step,
+BatchNorm-ReLU NHWC, AdamW, GradScaler unscale, the C5 GEMMs, FlashAttention
+backward, the GPT step) are reported under "components" with their own roofline
+fractions.
 
 The CPU baseline times the NumPy oracle (the reference's CPU algorithm) on a
 row sample of the same workload, single-threaded elementwise NumPy.
@@ -268,6 +269,29 @@ def _op_gpt(torch, L, g):
     return Timed("gpt_step", run, flops, "TFLOP/s", FP16_PEAK_TFLOPS)
 
 
+def _op_mlp(torch, L, g):
+    """C1: the README MLP, x fp32 [32, 784] -> Linear(784, 256) -> GELU -> Linear(256, 10),
+    loss = out.mean(), full backward and one Adam step (lr 1e-3) through the tensor_gpu_v2
+    API; a latency-bound step (launches), reported in ms.  Work = 3 x 2 x 32 x
+    (784*256 + 256*10) flops (forward, dA, dB)."""
+    import numpy as np
+    import tensor_gpu_v2 as tg
+    np.random.seed(0)
+    x = tg.Tensor(np.random.randn(32, 784).astype(np.float32), requires_grad=False)
+    l1, l2 = tg.Linear(784, 256), tg.Linear(256, 10)
+    params = [l1.w, l1.b, l2.w, l2.b]
+    opt = tg.Adam(params, lr=1e-3)
+
+    def run():
+        for p in params:
+            p.zero_grad()
+        loss = l2(l1(x).gelu()).mean()
+        loss.backward()
+        opt.step()
+    return Timed("mlp_step", run, 3 * 2 * 32 * (784 * 256 + 256 * 10), "TFLOP/s",
+                 FP16_PEAK_TFLOPS)
+
+
 def _op_ce(torch, L, g):
     """C5 cross-entropy over fp16 logits [8192, 32000]: forward (row statistics and
     losses) then backward (gradient written in fp16).  Algorithmic bytes: the logits
@@ -315,7 +339,8 @@ def _op_tied(torch, L, g):
 def component_ops(torch, L, only):
     """Other configurations, each built in its own scope on HBM-resident inputs."""
     g = torch.Generator(device="cuda").manual_seed(1)
-    builders = [("bn_relu_bwd_nhwc", lambda: _op_bn(torch, L, g)),
+    builders = [("mlp_step", lambda: _op_mlp(torch, L, g)),
+                ("bn_relu_bwd_nhwc", lambda: _op_bn(torch, L, g)),
                 ("adamw_step", lambda: _op_adam(torch, L, g)),
                 ("unscale_check", lambda: _op_unscale(torch, L, g)),
                 ("gemm_fc1_bwd", lambda: _op_gemm(torch, L, g)),
