@@ -213,21 +213,16 @@ __global__ void k_bn_var(const float* __restrict__ sums, float* __restrict__ var
   if (run_mean) run_mean[c] = (1.0f - momentum) * run_mean[c] + momentum * mean[c];
   if (run_var) run_var[c] = (1.0f - momentum) * run_var[c] + momentum * v;
 }
-// Backward: parameter grads and the per-channel coefficients of pass 2:
+
+// Per-channel apply coefficients from the channel sums S1, S2 (sums[c], sums[C + c]),
+// formed by the apply kernel itself (no separate per-channel launch):
 // dx = P*dy_m - Q - R*xhat with P = gamma*rstd, Q = P*S1/m, R = P*S2/m.
-__global__ void k_bn_bwd_final(const float* __restrict__ sums, const float* __restrict__ gamma,
-                               const float* __restrict__ rstd, float* __restrict__ coef,
-                               float* __restrict__ dgamma, float* __restrict__ dbeta,
-                               int acc_params, int64_t C, float inv_m) {
-  const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-  if (c >= C) return;
-  const float s1 = sums[c], s2 = sums[C + c];
-  const float P = gamma[c] * rstd[c];
-  coef[c] = P;
-  coef[C + c] = P * (s1 * inv_m);
-  coef[2 * C + c] = P * (s2 * inv_m);
-  if (dbeta) dbeta[c] = acc_params ? dbeta[c] + s1 : s1;
-  if (dgamma) dgamma[c] = acc_params ? dgamma[c] + s2 : s2;
+__device__ __forceinline__ void bn_coef(const float* __restrict__ sums, float g, float rs,
+                                        float inv_m, int64_t C, int64_t c, float& P, float& Q,
+                                        float& R) {
+  P = g * rs;
+  Q = P * (sums[c] * inv_m);
+  R = P * (sums[C + c] * inv_m);
 }
 
 // Elementwise apply kernels.  Channel of flat index i: NHWC i % C, NCHW (i / HW) % C.
@@ -241,12 +236,18 @@ template <int LAYOUT, int V, bool ACC, bool CONST_CH, bool NTL = false>
 __global__ __launch_bounds__(kBlock) void k_bn_bwd_apply(
     const float* __restrict__ x, const float* __restrict__ dy, const float* __restrict__ mean,
     const float* __restrict__ rstd, const float* __restrict__ gamma,
-    const float* __restrict__ beta, const float* __restrict__ coef, int relu,
-    float* __restrict__ dx, int64_t nvec, int64_t C, int64_t HW, bool nt) {
+    const float* __restrict__ beta, const float* __restrict__ sums, float inv_m, int relu,
+    float* __restrict__ dx, int64_t nvec, int64_t C, int64_t HW, bool nt,
+    float* __restrict__ dgamma, float* __restrict__ dbeta, int acc_params) {
   // CONST_CH (NHWC, grid stride a multiple of C): every iteration of a thread
   // touches the same V channels, so their parameters are loaded once.
   const int64_t stride = (int64_t)gridDim.x * kBlock;
   const int64_t iv0 = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  // dgamma (+)= S2, dbeta (+)= S1: one thread per channel
+  for (int64_t c = iv0; c < C; c += stride) {
+    if (dbeta) dbeta[c] = acc_params ? dbeta[c] + sums[c] : sums[c];
+    if (dgamma) dgamma[c] = acc_params ? dgamma[c] + sums[C + c] : sums[C + c];
+  }
   float pmu[V], prs[V], pg[V], pb[V], pP[V], pQ[V], pR[V];
   if (CONST_CH) {
     const int64_t cb = (iv0 * V) % C;
@@ -254,7 +255,7 @@ __global__ __launch_bounds__(kBlock) void k_bn_bwd_apply(
     for (int j = 0; j < V; ++j) {
       const int64_t c = cb + j;
       pmu[j] = mean[c]; prs[j] = rstd[c]; pg[j] = gamma[c]; pb[j] = beta[c];
-      pP[j] = coef[c]; pQ[j] = coef[C + c]; pR[j] = coef[2 * C + c];
+      bn_coef(sums, pg[j], prs[j], inv_m, C, c, pP[j], pQ[j], pR[j]);
     }
   }
   for (int64_t iv = iv0; iv < nvec; iv += stride) {
@@ -283,7 +284,7 @@ __global__ __launch_bounds__(kBlock) void k_bn_bwd_apply(
       for (int j = 0; j < V; ++j) {
         const int64_t c = LAYOUT == TG_NHWC ? cb + j : cb;
         pmu[j] = mean[c]; prs[j] = rstd[c]; pg[j] = gamma[c]; pb[j] = beta[c];
-        pP[j] = coef[c]; pQ[j] = coef[C + c]; pR[j] = coef[2 * C + c];
+        bn_coef(sums, pg[j], prs[j], inv_m, C, c, pP[j], pQ[j], pR[j]);
       }
     }
     float r[V];
@@ -362,7 +363,7 @@ BnPlan bn_plan(int layout, int64_t N, int64_t C, int64_t HW, bool aligned) {
   return p;
 }
 
-// Workspace: partials [nsplit][2][C] | sums [2C] | coef [3C] | tree scratch
+// Workspace: partials [nsplit][2][C] | sums [2C] | 3C reserved | tree scratch
 size_t bn_ws_bytes(const BnPlan& p, int64_t C) {
   return (size_t)(2 * p.nsplit * C + 5 * C) * sizeof(float) +
          tg_sum_partials_scratch(p.nsplit, 2 * C);
@@ -508,16 +509,13 @@ TG_EXPORT int tg_batchnorm_bwd(int layout, const float* x, const float* mean, co
   hipStream_t s = tg_stream(stream);
   float* part = (float*)workspace;
   float* sums = part + 2 * p.nsplit * C;
-  float* coef = sums + 2 * C;
   float* scratch = sums + 5 * C;
   // x and dy too large to stay cached: both passes read them non-temporally
   const bool big = N * C * HW * (int64_t)sizeof(float) >= (128ll << 20);
   launch_reduce<2>(layout, p, x, dy, mean, rstd, gamma, beta, relu, part, N, C, HW, s, big);
   st = tg_sum_partials(part, p.nsplit, 2 * C, TG_F32, sums, 0, scratch, s);
   if (st) return st;
-  const unsigned cb = (unsigned)((C + kBlock - 1) / kBlock);
-  k_bn_bwd_final<<<cb, kBlock, 0, s>>>(sums, gamma, rstd, coef, dgamma, dbeta, accumulate_params,
-                                       C, 1.0f / (float)p.M);
+  const float inv_m = 1.0f / (float)p.M;
   const int64_t n = N * C * HW;
   const bool vec = p.V == 4 && al;
   const int64_t nvec = vec ? n / 4 : n;
@@ -526,10 +524,10 @@ TG_EXPORT int tg_batchnorm_bwd(int layout, const float* x, const float* mean, co
   do {                                                                                       \
   if (nt)                                                                                   \
     k_bn_bwd_apply<LAY, VV, ACC, CC, true><<<NB, kBlock, 0, s>>>(x, dy, mean, rstd, gamma, beta, \
-                                                                 coef, relu, dx, nvec, C, HW, nt); \
+        sums, inv_m, relu, dx, nvec, C, HW, nt, dgamma, dbeta, accumulate_params);           \
   else                                                                                       \
-    k_bn_bwd_apply<LAY, VV, ACC, CC><<<NB, kBlock, 0, s>>>(x, dy, mean, rstd, gamma, beta, coef, \
-                                                           relu, dx, nvec, C, HW, nt); \
+    k_bn_bwd_apply<LAY, VV, ACC, CC><<<NB, kBlock, 0, s>>>(x, dy, mean, rstd, gamma, beta,     \
+        sums, inv_m, relu, dx, nvec, C, HW, nt, dgamma, dbeta, accumulate_params);           \
   } while (0)
   const bool nt = n * (int64_t)sizeof(float) >= (128ll << 20);  // output too large to keep cached
   const unsigned cc = (layout == TG_NHWC && vec) ? const_channel_blocks(nvec, C, 4) : 0;
