@@ -75,7 +75,8 @@ class Trainer:
     """One optimizer step per call: the C5 recipe (AdamW lr 3e-4, wd 0.1, clip 1.0,
     GradScaler init 2^16, fp16 autocast)."""
 
-    def __init__(self, model, lr=3e-4, weight_decay=0.1, clip=1.0, init_scale=2.0 ** 16):
+    def __init__(self, model, lr=3e-4, weight_decay=0.1, clip=1.0, init_scale=2.0 ** 16,
+                 strict_chain_rule=False):
         self.model = model
         params = model.parameters()
         # the tied head weight is a view of the embedding: optimise the source only
@@ -83,7 +84,7 @@ class Trainer:
         self.opt = tg.AdamW(self.params, lr=lr, weight_decay=weight_decay)
         self.scaler = tg.GradScaler(init_scale=init_scale)
         self.clip = clip
-        self.loss_fn = tg.CrossEntropyLoss()
+        self.loss_fn = tg.CrossEntropyLoss(strict_chain_rule=strict_chain_rule)
 
     def step(self, ids, targets):
         self.opt.zero_grad()

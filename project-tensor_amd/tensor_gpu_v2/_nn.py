@@ -433,12 +433,23 @@ class MSELoss(Module):
 class CrossEntropyLoss(Module):
     """Cross-entropy over logits [N, C] (_nn.py:1128-1185).  As in the reference,
     the backward writes (softmax - onehot)/N (mean) into logits.grad without
-    multiplying by the loss's upstream gradient (_nn.py:1168-1180)."""
+    multiplying by the loss's upstream gradient (_nn.py:1168-1180), so a GradScaler
+    loss scale never reaches the gradients.
 
-    def __init__(self, reduction="mean", label_smoothing=0.0):
+    strict_chain_rule=True (not in the reference; default off) multiplies by the
+    upstream gradient as the chain rule asks, so scaled fp16 gradients stay in fp16's
+    normal range.  It needs a scalar loss (reduction 'mean' or 'sum'), keeps the loss
+    in fp32 also under autocast (an fp16 loss times a 2^16 scale overflows fp16's
+    65504, and so would its upstream gradient) and reads the upstream gradient back to
+    the host once per backward."""
+
+    def __init__(self, reduction="mean", label_smoothing=0.0, strict_chain_rule=False):
         super().__init__()
+        if strict_chain_rule and reduction not in ("mean", "sum"):
+            raise ValueError("strict_chain_rule needs reduction 'mean' or 'sum'")
         self.reduction = reduction
         self.label_smoothing = label_smoothing
+        self.strict_chain_rule = bool(strict_chain_rule)
 
     def __call__(self, logits, targets):
         ld = logits.data
@@ -466,19 +477,23 @@ class CrossEntropyLoss(Module):
             lv = loss.sum()
         else:
             lv = loss
+        strict = self.strict_chain_rule
         out = Tensor._wrap(lv.to(ld.dtype), (logits,), "CrossEntropy")
+        if strict:
+            out.data = lv  # fp32, past the autocast cast of _wrap
         scale = 1.0 / N if self.reduction == "mean" else 1.0
         smoothing = self.label_smoothing
         if out._requires_grad:
             def _backward():
                 if not logits._has_grad():
                     return
+                sc = scale * float(out._grad_out().reshape(-1)[0]) if strict else scale
                 buf, acc = logits._grad_target()
                 if buf.is_contiguous() and buf.shape == ldc.shape:
-                    L.cross_entropy_bwd(ldc, tg, lse, buf, scale, acc, smoothing)
+                    L.cross_entropy_bwd(ldc, tg, lse, buf, sc, acc, smoothing)
                 else:
                     g = torch.empty_like(ldc)
-                    L.cross_entropy_bwd(ldc, tg, lse, g, scale, False, smoothing)
+                    L.cross_entropy_bwd(ldc, tg, lse, g, sc, False, smoothing)
                     logits._accumulate(g, True)
             out._backward = _backward
         return out

@@ -105,23 +105,57 @@ def test_flash_accumulate(cuda):
         assert_close(b, 2 * f64(a), RTOL_F16, "accumulate doubles")
 
 
+def _head_invariants(q, k, v, o, do, dq, dk, dv):
+    """Per-head identities of attention's gradients, in float64 on the device, for
+    every (b, h) at once.  With P's rows summing to 1 and dS = P*(dP - rowsum):
+      sum_keys dV = sum_queries dO                 (dV = P^T dO)
+      sum_keys dK = 0                              (each row of dS sums to 0)
+      <dQ, Q> = <dK, K>                            (both are sum(dS * Q K^T))
+      <dV, V> = <dO, O>                            (O = P V)
+    Each returns the worst ratio |lhs - rhs| / sqrt(sum of squared terms), i.e. the
+    error against the size the identity's terms would have if it failed; fp16
+    rounding gives ~1e-3, a gradient taken from the wrong head or row gives ~1."""
+    d = lambda t: t.double()  # noqa: E731
+    q, k, v, o, do, dq, dk, dv = map(d, (q, k, v, o, do, dq, dk, dv))
+    out = {}
+    lhs, rhs = dv.sum(2), do.sum(2)
+    out["sum dV = sum dO"] = ((lhs - rhs).abs() / (dv.pow(2).sum(2).sqrt() + 1e-30)).max()
+    out["sum dK = 0"] = (dk.sum(2).abs() / (dk.pow(2).sum(2).sqrt() + 1e-30)).max()
+    a, b = (dq * q).sum((2, 3)), (dk * k).sum((2, 3))
+    sc = ((dq * q).pow(2).sum((2, 3)) + (dk * k).pow(2).sum((2, 3))).sqrt()
+    out["<dQ,Q> = <dK,K>"] = ((a - b).abs() / sc).max()
+    a, b = (dv * v).sum((2, 3)), (do * o).sum((2, 3))
+    sc = ((dv * v).pow(2).sum((2, 3)) + (do * o).pow(2).sum((2, 3))).sqrt()
+    out["<dV,V> = <dO,O>"] = ((a - b).abs() / sc).max()
+    return {n: float(x) for n, x in out.items()}
+
+
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("causal", [False, True])
-def test_flash_full_size_one_head(cuda, D, causal):
-    """C4 shape B=8, H=16, S=2048: the whole batch runs, one (b, h) slice is
-    checked against the oracle (size-independent per head)."""
+def test_flash_full_size_all_heads(cuda, D, causal):
+    """C4 shape B=8, H=16, S=2048.  All 128 (b, h) heads are checked through the
+    per-head identities; six heads spread over the dispatch's head groups (groups of
+    8 heads per XCD range: first, last of group 0, first of group 1, both sides of
+    the middle, last) are checked element by element against the oracle."""
     B, H, S = 8, 16, 2048
+    print(f"C4 full size D={D} causal={causal}", flush=True)
     q, k, v, do = (rnd((B, H, S, D), torch.float16, 10 + s) for s in range(4))
     o, lse, dq, dk, dv = run(q, k, v, do, causal)
-    b, hh = 5, 11
-    sl = (slice(b, b + 1), slice(hh, hh + 1))
-    oo, ll = O.flash_attention_fwd(f64(q[sl]), f64(k[sl]), f64(v[sl]), causal)
-    assert_close(o[sl], oo, RTOL_F16, "O head")
-    rq, rk, rv = O.flash_attention_bwd(f64(q[sl]), f64(k[sl]), f64(v[sl]), f64(do[sl]), causal)
-    assert_close(dq[sl], rq, RTOL_F16, "dQ head")
-    assert_close(dk[sl], rk, RTOL_F16, "dK head")
-    assert_close(dv[sl], rv, RTOL_F16, "dV head")
-    assert torch.isfinite(dq).all() and torch.isfinite(dk).all() and torch.isfinite(dv).all()
+    inv = _head_invariants(q, k, v, o, do, dq, dk, dv)
+    print("identity errors:", {n: f"{x:.2e}" for n, x in inv.items()}, flush=True)
+    for n, x in inv.items():
+        assert x < 2e-2, f"{n}: {x:.3e}"
+    for flat in (0, 7, 8, 63, 64, 127):
+        b, hh = divmod(flat, H)
+        sl = (slice(b, b + 1), slice(hh, hh + 1))
+        oo, ll = O.flash_attention_fwd(f64(q[sl]), f64(k[sl]), f64(v[sl]), causal)
+        assert_close(o[sl], oo, RTOL_F16, f"O head {flat}")
+        assert_close(lse[sl], ll, 1e-5, f"lse head {flat}")
+        rq, rk, rv = O.flash_attention_bwd(f64(q[sl]), f64(k[sl]), f64(v[sl]), f64(do[sl]),
+                                           causal)
+        assert_close(dq[sl], rq, RTOL_F16, f"dQ head {flat}")
+        assert_close(dk[sl], rk, RTOL_F16, f"dK head {flat}")
+        assert_close(dv[sl], rv, RTOL_F16, f"dV head {flat}")
 
 
 def test_flash_rejects_bad_shapes(cuda):

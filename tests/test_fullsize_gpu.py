@@ -98,19 +98,32 @@ def test_c3_bn_relu_bwd_nhwc_full(cuda):
     dx = torch.empty_like(x)
     dg, db = torch.empty_like(gam), torch.empty_like(bet)
     L().batchnorm_bwd(x, mean, rstd, gam, bet, dy, dx, dg, db, True, False, False, L().NHWC)
-    # The ReLU mask as the kernel forms it: fp32, ((x - mean) * rstd) * gamma + beta > 0
-    # in that order without contraction (NumPy does not fuse), from the kernel's own
-    # statistics; the oracle then runs without ReLU on the masked gradient.
+    # The statistics and the ReLU mask are first checked against the oracle's float64
+    # forward: mean and rstd per channel at the fp32 bar, and the mask wherever the
+    # float64 pre-activation is farther from 0 than fp32 rounding of its terms reaches.
     x32 = x.cpu().numpy()
-    m32, r32 = mean.cpu().numpy(), rstd.cpu().numpy()
     g32, b32 = gam.cpu().numpy(), bet.cpu().numpy()
-    on = (g32 * ((x32 - m32) * r32) + b32) > 0
-    dym = dy.cpu().numpy().astype(np.float64) * on
-    del on
     x64 = x32.astype(np.float64)
-    del x32
     _, cache = O.batchnorm_relu_fwd_nhwc(x64, g32.astype(np.float64), b32.astype(np.float64),
                                          1e-5, relu=False)
+    assert_close(mean, cache[5], RTOL_F32, "bn mean")
+    assert_close(rstd, 1.0 / np.sqrt(cache[6] + 1e-5), RTOL_F32, "bn rstd")
+    pre = cache[4].transpose(0, 2, 3, 1)  # float64 gamma*xhat + beta, NHWC
+    band = 1e-5 * (np.abs(g32) * np.abs(cache[0].transpose(0, 2, 3, 1)) + np.abs(b32))
+    # the mask as the kernel forms it: fp32, ((x - mean) * rstd) * gamma + beta > 0 in
+    # that order without contraction (NumPy does not fuse), from its own statistics
+    m32, r32 = mean.cpu().numpy(), rstd.cpu().numpy()
+    on = (g32 * ((x32 - m32) * r32) + b32) > 0
+    del x32
+    differ = on != (pre > 0)
+    assert not (differ & (np.abs(pre) > band)).any(), "ReLU mask differs from the oracle's"
+    assert int(differ.sum()) <= 1000, int(differ.sum())
+    del pre, band, differ
+    # the oracle's backward then runs without ReLU on the gradient masked as the kernel
+    # masked it (the few elements inside the rounding band would otherwise move dgamma
+    # and dbeta by one element's contribution)
+    dym = dy.cpu().numpy().astype(np.float64) * on
+    del on
     dxr, dgr, dbr = O.batchnorm_relu_bwd_nhwc(dym, g32.astype(np.float64), cache, relu=False)
     assert_close(dg, dgr, RTOL_F32, "bn dgamma")
     assert_close(db, dbr, RTOL_F32, "bn dbeta")

@@ -1,17 +1,60 @@
 """C5 composition on a small GPT: the engine's fp16-autocast forward/backward vs the
 same network in torch float64 autograd with identical weights.  GPU only.
 
-Tolerance: per-parameter relative Frobenius error 3e-2 (fp16 autocast through
-several layers; the per-kernel 1e-2 bar is tested elsewhere)."""
+The float64 composition follows the reference's semantics at the loss: the
+cross-entropy gradient (softmax - onehot)/N ignores the upstream gradient (the loss
+scale) and is held in the logits' dtype (reference _nn.py:1168-1180), so under fp16
+autocast it is rounded to fp16 once (values below fp16's range flush to zero).
+Everything else in the composition is float64.
+
+At the full C5 size that reference behaviour leaves the activation gradients in
+fp16's subnormal range (|dlogits| ~ 1/8192, times 0.02-sized weights: ~2e-6, where
+fp16 keeps 5 bits or fewer), in the reference as here, so they carry several per cent
+of rounding error and the query/key gradients flush to zero almost entirely.  The
+full-size parity check therefore runs with CrossEntropyLoss(strict_chain_rule=True),
+where the 2^16 loss scale reaches the gradients, against the float64 composition with
+the same upstream factor; the reference-faithful mode is then checked to give exactly
+the strict mode's gradients at loss scale 1.
+
+Tolerance: loss and per-parameter relative Frobenius error 1e-2 (the fp16 autocast
+bar)."""
 import numpy as np
 import pytest
 import torch
 
+from conftest import RTOL_F16, RTOL_F32, assert_close
+
 pytestmark = pytest.mark.gpu
 
 
-def torch_reference(model, ids, targets):
-    """The same network in float64 torch autograd; returns (loss, {param id: grad})."""
+class _RefCE(torch.autograd.Function):
+    """Mean cross-entropy -log(p_t + 1e-10) whose backward is the reference's
+    (softmax - onehot)/N, independent of the upstream gradient, rounded through
+    `gdt` (the logits' dtype under autocast)."""
+
+    @staticmethod
+    def forward(ctx, logits, tgt, gdt, mult):
+        p = torch.softmax(logits, -1)
+        ctx.save_for_backward(p, tgt)
+        ctx.gdt = gdt
+        ctx.mult = mult
+        n = logits.shape[0]
+        return -torch.log(p[torch.arange(n, device=p.device), tgt] + 1e-10).mean()
+
+    @staticmethod
+    def backward(ctx, _upstream):
+        p, tgt = ctx.saved_tensors
+        n = p.shape[0]
+        g = p.clone()
+        g[torch.arange(n, device=p.device), tgt] -= 1.0
+        g = (g * (ctx.mult / n)).to(ctx.gdt).double()
+        return g, None, None, None
+
+
+def torch_reference(model, ids, targets, ce_grad_dtype=torch.float16, mult=1.0):
+    """The same network in float64 torch autograd; returns (loss, {param id: grad}).
+    `mult` multiplies the cross-entropy gradient (the loss scale under the strict
+    chain rule; 1 for the reference's behaviour)."""
     import torch.nn.functional as F
     leaves = {}
 
@@ -44,33 +87,33 @@ def torch_reference(model, ids, targets):
         h = h + lin(F.gelu(lin(m, blk.fc1), approximate="tanh"), blk.fc2)
     h = F.layer_norm(h, (h.shape[-1],), leaf(model.lnf.gamma), leaf(model.lnf.beta), 1e-5)
     logits = (h @ E.T).reshape(-1, E.shape[0])
-    p = torch.softmax(logits, -1)
-    loss = -torch.log(p[torch.arange(p.shape[0]), torch.as_tensor(targets, device="cuda")]
-                      + 1e-10).mean()
+    loss = _RefCE.apply(logits, torch.as_tensor(targets, device="cuda"), ce_grad_dtype, mult)
     loss.backward()
     return float(loss.detach()), {k: v.grad for k, v in leaves.items()}
 
 
-def test_small_gpt_step_matches_float64(cuda):
+def _engine_grads(model, ids, targets, **trainer_kw):
+    """One fp16-autocast forward + scaled backward + tied sync through the engine;
+    returns (loss, trainer)."""
     import tensor_gpu_v2 as tg
-    from gpt_harness import GPT, Trainer, synthetic_batch
-    model = GPT(vocab=96, d=128, heads=2, layers=2, seed=3)
-    ids, targets = synthetic_batch(vocab=96, batch=2, seq=64, seed=4)
-    ref_loss, ref_grads = torch_reference(model, ids, targets)
-
-    tr = Trainer(model)
+    from gpt_harness import Trainer
+    tr = Trainer(model, **trainer_kw)
     with tg.autocast():
         logits = model(ids)
         loss = tr.loss_fn(logits, targets)
     tr.scaler.scale(loss).backward()
     tg.sync_tied_gradients(model)
-    assert abs(loss.item() - ref_loss) < 1e-2 * abs(ref_loss)
-    # The key bias has an exactly zero gradient: it adds q.b_k to every score of a
-    # query row and softmax is shift-invariant.  A relative error is meaningless
-    # there; check instead that the engine's value (a column sum of dK) is rounding noise
-    # next to the key weight's gradient (a^T dK).
+    return loss, tr
+
+
+def _check_grads(model, tr, ref_grads, rtol):
+    """Every optimised parameter's gradient within `rtol` (relative Frobenius) of the
+    float64 composition.  The key bias has an exactly zero gradient: it adds q.b_k to
+    every score of a query row and softmax is shift-invariant, so a relative error is
+    meaningless there; its value (a column sum of dK) must instead be rounding noise
+    next to the key weight's gradient (a^T dK).  Returns {name: error}."""
     key_bias = {id(blk.k.b): blk for blk in model.blocks}
-    checked = 0
+    errs, bad = {}, []
     for name, p in model.named_parameters():
         if all(p is not q for q in tr.params):
             continue
@@ -78,12 +121,26 @@ def test_small_gpt_step_matches_float64(cuda):
         r = ref_grads[id(p)]
         if id(p) in key_bias:
             kw = key_bias[id(p)].k.w.grad.double().norm()
-            assert float(g.norm()) < 1e-2 * float(kw), f"{name}: |grad| {float(g.norm()):.3e}"
+            errs[name] = float(g.norm()) / float(kw)
         else:
-            rel = float((g - r).norm() / (r.norm() + 1e-30))
-            assert rel < 3e-2, f"{name} {tuple(p.shape)}: relative error {rel:.3e}"
-        checked += 1
-    assert checked == len(tr.params) == 2 * 16 + 3
+            errs[name] = float((g - r).norm() / (r.norm() + 1e-30))
+        if not errs[name] < rtol:
+            bad.append(name)
+    print("relative gradient errors:", {k: f"{v:.2e}" for k, v in errs.items()}, flush=True)
+    assert not bad, {k: errs[k] for k in bad}
+    return errs
+
+
+def test_small_gpt_step_matches_float64(cuda):
+    import tensor_gpu_v2 as tg
+    from gpt_harness import GPT, synthetic_batch
+    model = GPT(vocab=96, d=128, heads=2, layers=2, seed=3)
+    ids, targets = synthetic_batch(vocab=96, batch=2, seq=64, seed=4)
+    ref_loss, ref_grads = torch_reference(model, ids, targets)
+    loss, tr = _engine_grads(model, ids, targets)
+    assert abs(loss.item() - ref_loss) < RTOL_F16 * abs(ref_loss)
+    errs = _check_grads(model, tr, ref_grads, RTOL_F16)
+    assert len(errs) == len(tr.params) == 2 * 16 + 3
     # the rest of the step: unscale (CE ignores the scale: grads shrink by 2^-16), clip,
     # AdamW, update
     w0 = model.blocks[0].fc1.w.data.clone()
@@ -95,6 +152,61 @@ def test_small_gpt_step_matches_float64(cuda):
     tr.scaler.update()
     assert not torch.equal(model.blocks[0].fc1.w.data, w0)
     assert all(torch.isfinite(p.data).all() for p in tr.params)
+
+
+def test_full_size_c5_step_matches_float64(cuda):
+    """C5 at its configured size: vocab 32000 (tied), d 1024, 16 heads, 4 layers,
+    batch 8 x seq 1024, weights N(0, 0.02), fp16 autocast, GradScaler 2^16.  This runs
+    the K-split GEMMs, the head-split FlashAttention layout and its XCD head grouping,
+    the 32000-way cross-entropy and the tied transpose-add at their real shapes.  Then
+    the rest of the step (unscale, clip 1.0, AdamW) against a float64 restatement."""
+    import tensor_gpu_v2 as tg
+    from gpt_harness import GPT, synthetic_batch
+    print("C5 full size: vocab 32000, d 1024, 16 heads, 4 layers, 8 x 1024", flush=True)
+    model = GPT(vocab=32000, d=1024, heads=16, layers=4, seed=0)
+    ids, targets = synthetic_batch(vocab=32000, batch=8, seq=1024, seed=0)
+    # reference-faithful mode (CE ignores the loss scale) == strict mode at scale 1
+    loss_f, tr_f = _engine_grads(model, ids, targets)
+    g_f = [p.grad.clone() for p in tr_f.params]
+    for p in model.parameters():
+        p.zero_grad()
+    _, tr_1 = _engine_grads(model, ids, targets, strict_chain_rule=True, init_scale=1.0)
+    for p, a in zip(tr_1.params, g_f):
+        assert torch.equal(p.grad, a)
+    del g_f
+    for p in model.parameters():
+        p.zero_grad()
+    scale = 2.0 ** 16
+    ref_loss, ref_grads = torch_reference(model, ids, targets, mult=scale)
+    print(f"faithful loss {loss_f.item():.6f} vs float64 {ref_loss:.6f}", flush=True)
+    assert abs(loss_f.item() - ref_loss) < RTOL_F16 * abs(ref_loss)
+    loss, tr = _engine_grads(model, ids, targets, strict_chain_rule=True, init_scale=scale)
+    assert abs(loss.item() - ref_loss) < RTOL_F16 * abs(ref_loss)
+    errs = _check_grads(model, tr, ref_grads, RTOL_F16)
+    assert len(errs) == len(tr.params) == 4 * 16 + 3
+    del ref_grads
+    # unscale -> clip -> AdamW in float64 from the engine's own gradients
+    g = [p.grad.double() for p in tr.params]
+    w = [p.data.double() for p in tr.params]
+    tr.scaler.unscale_(tr.opt)
+    assert not tr.scaler._found_inf
+    gu = [x / scale for x in g]
+    for p, x in zip(tr.params, gu):
+        assert torch.equal(p.grad.double(), x)
+    norm = tg.clip_grad_norm_(tr.params, 1.0)
+    ref_norm = float(torch.sqrt(sum((x * x).sum() for x in gu)))
+    assert abs(norm - ref_norm) <= 1e-5 * ref_norm
+    coef = 1.0 / (ref_norm + 1e-6)
+    gc = [x * coef for x in gu] if coef < 1 else gu
+    tr.scaler.step(tr.opt)
+    tr.scaler.update()
+    lr, wd, b1, b2, eps = 3e-4, 0.1, 0.9, 0.999, 1e-8
+    for p, w0, x in zip(tr.params, w, gc):
+        w0 = w0 - lr * wd * w0
+        m = (1 - b1) * x
+        v = (1 - b2) * x * x
+        want = w0 - lr * (m / (1 - b1)) / (torch.sqrt(v / (1 - b2)) + eps)
+        assert_close(p.data, want, RTOL_F32, "AdamW update")
 
 
 def test_gpt_trainer_step_runs_twice(cuda):

@@ -167,3 +167,11 @@ def test_autocast_tied_head_identical_with_and_without_cache(cuda):
     lb, wb = run(False)
     assert la == lb, (la, lb)
     assert torch.equal(wa, wb)
+
+
+def test_cross_entropy_strict_chain_rule_needs_scalar_loss():
+    import tensor_gpu_v2 as tg
+    with pytest.raises(ValueError, match="strict_chain_rule"):
+        tg.CrossEntropyLoss(reduction="none", strict_chain_rule=True)
+    assert tg.CrossEntropyLoss(strict_chain_rule=True).strict_chain_rule
+    assert not tg.CrossEntropyLoss().strict_chain_rule
