@@ -83,6 +83,17 @@ int tg_layernorm_bwd(int dtype, const void* x, const float* mean, const float* r
                      const float* gamma, const void* dy, void* dx, float* dgamma, float* dbeta,
                      int64_t rows, int64_t cols, int accumulate_dx, int accumulate_params,
                      void* workspace, size_t workspace_bytes, void* stream);
+/* tg_layernorm_bwd without a workspace argument and without any allocation: the
+ * partial sums live in a fixed device array of the library (one per GPU, held until
+ * the process ends; tg_layernorm_bwd_noalloc_max_scratch() bytes).  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops).  Shapes whose partials exceed the scratch
+ * return -1 with a message.  Calls that overlap on one GPU share the scratch and race. */
+size_t tg_layernorm_bwd_noalloc_max_scratch(void);
+int tg_layernorm_bwd_noalloc(int dtype, const void* x, const float* mean, const float* rstd,
+                             const float* gamma, const void* dy, void* dx, float* dgamma,
+                             float* dbeta, int64_t rows, int64_t cols, int accumulate_dx,
+                             int accumulate_params, void* stream);
 /* out[c] (+)= sum_r in[r][c]: Tensor._unbroadcast's leading-dimension sums
  * (_core.py:1380-1424), e.g. the Linear bias gradient. */
 size_t tg_reduce_rows_workspace(int64_t rows, int64_t cols);

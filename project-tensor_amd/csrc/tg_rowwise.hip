@@ -11,6 +11,8 @@
 // take the looping wavefront-per-row path, which re-reads the row from cache.
 #include "tg_common.h"
 
+#include <mutex>
+
 namespace {
 
 constexpr int kBlock = 256;
@@ -882,6 +884,70 @@ TG_EXPORT int tg_layernorm_bwd(int dtype, const void* x, const float* mean, cons
   }
   tg_set_error("tg_layernorm_bwd: unsupported dtype %d", dtype);
   return TG_ERR_UNSUPPORTED;
+}
+
+// ---- LayerNorm backward without a caller workspace -------------------------
+// The dgamma/dbeta partial rows (and the staging of their column sum) live in this
+// file-scope device array instead of a workspace argument.  Every GPU the library
+// runs on holds its own copy until the process ends.  Host code must not pass the
+// array's name to a kernel (on the host it names a stand-in, not device memory): the
+// device address is looked up once per device and kept in g_ln_scratch.  Every
+// partial row is written before it is read, so nothing needs clearing between calls.
+static constexpr size_t kLnScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) unsigned char scratch[kLnScratchBytes];
+
+static std::mutex g_ln_scratch_mu;
+static void* g_ln_scratch[64];
+
+static int ln_scratch_ptr(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= 64) {
+    tg_set_error("tg_layernorm_bwd_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    return TG_ERR_HIP;
+  }
+  std::lock_guard<std::mutex> lk(g_ln_scratch_mu);
+  if (!g_ln_scratch[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      tg_set_error("tg_layernorm_bwd_noalloc: hipGetSymbolAddress(scratch) on device %d: %s",
+                   dev, hipGetErrorString(e));
+      return TG_ERR_HIP;
+    }
+    g_ln_scratch[dev] = p;
+  }
+  *out = g_ln_scratch[dev];
+  return TG_OK;
+}
+
+TG_EXPORT size_t tg_layernorm_bwd_noalloc_max_scratch(void) { return kLnScratchBytes; }
+
+TG_EXPORT int tg_layernorm_bwd_noalloc(int dtype, const void* x, const float* mean,
+                                       const float* rstd, const float* gamma, const void* dy,
+                                       void* dx, float* dgamma, float* dbeta, int64_t rows,
+                                       int64_t cols, int accumulate_dx, int accumulate_params,
+                                       void* stream) {
+  TG_REQUIRE(rows >= 0 && cols > 0, "tg_layernorm_bwd_noalloc: bad shape");
+  if (rows == 0) return TG_OK;
+  TG_REQUIRE(x && mean && rstd && gamma && dy && dx, "tg_layernorm_bwd_noalloc: null pointer");
+  TG_REQUIRE(dtype == TG_F32 || dtype == TG_F16 || dtype == TG_BF16,
+             "tg_layernorm_bwd_noalloc: unsupported dtype %d", dtype);
+  const bool al = tg_aligned16(x) && tg_aligned16(dy) && tg_aligned16(dx);
+  LnBwdPlan p = ln_bwd_plan_dt(dtype, rows, cols, al);
+  const size_t need =
+      (size_t)(2 * p.nparts * cols) * sizeof(float) + tg_sum_partials_scratch(p.nparts, cols, 2);
+  if (need > kLnScratchBytes) {
+    tg_set_error("tg_layernorm_bwd_noalloc: [%lld, %lld] needs %zu bytes of scratch, above the "
+                 "fixed %zu; use tg_layernorm_bwd with a workspace",
+                 (long long)rows, (long long)cols, need, kLnScratchBytes);
+    return TG_ERR_INVALID;
+  }
+  void* ws = nullptr;
+  int st = ln_scratch_ptr(&ws);
+  if (st) return st;
+  return tg_layernorm_bwd(dtype, x, mean, rstd, gamma, dy, dx, dgamma, dbeta, rows, cols,
+                          accumulate_dx, accumulate_params, ws, kLnScratchBytes, stream);
 }
 
 TG_EXPORT size_t tg_reduce_rows_workspace(int64_t rows, int64_t cols) {

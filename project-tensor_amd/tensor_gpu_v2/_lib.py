@@ -49,6 +49,9 @@ SIGNATURES = {
     "tg_layernorm_bwd_workspace": (_sz, [_i32, _i64, _i64]),
     "tg_layernorm_bwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
                                 _i32, _i32, _vp, _sz, _vp]),
+    "tg_layernorm_bwd_noalloc_max_scratch": (_sz, []),
+    "tg_layernorm_bwd_noalloc": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
+                                        _i64, _i32, _i32, _vp]),
     "tg_reduce_rows_workspace": (_sz, [_i64, _i64]),
     "tg_reduce_rows": (_i32, [_i32, _vp, _i32, _vp, _i64, _i64, _i32, _vp, _sz, _vp]),
     "tg_batchnorm_workspace": (_sz, [_i32, _i64, _i64, _i64]),
@@ -347,6 +350,24 @@ def layernorm_bwd(x, mean, rstd, gamma, dy, dx, dgamma, dbeta, accumulate_dx,
         code, ptr(x), ptr(mean), ptr(rstd), ptr(gamma), ptr(dy), ptr(dx), ptr(dgamma),
         ptr(dbeta), rows, cols, int(bool(accumulate_dx)), int(bool(accumulate_params)), ptr(ws),
         ws.numel(), stream_handle()))
+    return dx
+
+
+def layernorm_bwd_noalloc(x, mean, rstd, gamma, dy, dx, dgamma, dbeta, accumulate_dx,
+                          accumulate_params):
+    """layernorm_bwd with the library's fixed device scratch in place of a workspace:
+    allocates nothing.  Calls that overlap on one GPU share the scratch and race."""
+    for n, t in (("x", x), ("dy", dy), ("dx", dx), ("mean", mean), ("rstd", rstd),
+                 ("gamma", gamma)):
+        _dev(t, n)
+    _same("layernorm_bwd_noalloc", x, dy, dx)
+    cols = gamma.numel()
+    rows = x.numel() // cols
+    ensure_device(x.device.index)
+    _check("tg_layernorm_bwd_noalloc", load().tg_layernorm_bwd_noalloc(
+        dtype_code(x), ptr(x), ptr(mean), ptr(rstd), ptr(gamma), ptr(dy), ptr(dx), ptr(dgamma),
+        ptr(dbeta), rows, cols, int(bool(accumulate_dx)), int(bool(accumulate_params)),
+        stream_handle()))
     return dx
 
 
