@@ -94,6 +94,19 @@ int tg_layernorm_bwd_noalloc(int dtype, const void* x, const float* mean, const 
                              const float* gamma, const void* dy, void* dx, float* dgamma,
                              float* dbeta, int64_t rows, int64_t cols, int accumulate_dx,
                              int accumulate_params, void* stream);
+/* Strided broadcast multiply with reduction over one ndim-dimensional index space:
+ *   out[o(i)] (+)= alpha * sum_i a[a(i)] * b[b(i)]
+ * with element strides per dimension (input stride 0 = broadcast, output stride 0 =
+ * summed away); b may be NULL (taken as 1); dtypes 0-3 (fp32, fp16, bf16, fp64) in any
+ * mix.  Replaces Tensor._unbroadcast (_core.py:1380-1424), the __mul__ backward
+ * (_core.py:955-968: other * grad, unbroadcast) and the sum/mean backward broadcast
+ * (_core.py:1078-1087), and strided copies/casts of gradient buffers.  Deterministic
+ * (fixed summation order, fp32 or fp64 accumulation). */
+int tg_broadcast_mul_sum(int ndim, const int64_t* shape, int dtype_a, const void* a,
+                         const int64_t* strides_a, int dtype_b, const void* b,
+                         const int64_t* strides_b, int dtype_out, void* out,
+                         const int64_t* strides_out, double alpha, int accumulate,
+                         void* stream);
 /* out[c] (+)= sum_r in[r][c]: Tensor._unbroadcast's leading-dimension sums
  * (_core.py:1380-1424), e.g. the Linear bias gradient. */
 size_t tg_reduce_rows_workspace(int64_t rows, int64_t cols);

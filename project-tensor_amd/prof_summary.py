@@ -4,6 +4,7 @@
     python project-tensor_amd/prof_summary.py pmc <dir> ...   # per-kernel counter means
     python project-tensor_amd/prof_summary.py traffic <fetch_dir> <write_dir> <calib_bytes>
     python project-tensor_amd/prof_summary.py mfma <dir> [n_xcd] [n_simd]
+    python project-tensor_amd/prof_summary.py ranges <dir>   # kernels per roctx range
 
 ``stats`` prints, per kernel, calls, total and average duration.  ``pmc`` prints,
 per kernel, the mean per dispatch of every counter in counter_collection.csv
@@ -11,7 +12,10 @@ per kernel, the mean per dispatch of every counter in counter_collection.csv
 SQ_VALU_MFMA_BUSY_CYCLES, SQ_INSTS_VALU_MFMA_MOPS_F16 and GRBM_GUI_ACTIVE and prints,
 per MFMA kernel, the fp16 flops executed per dispatch (MOPS x 512) and the MFMA
 utilisation busy / (active cycles x SIMDs), where GRBM_GUI_ACTIVE is summed over the
-n_xcd XCDs (default 8) and n_simd is the SIMD count (default 1024).
+n_xcd XCDs (default 8) and n_simd is the SIMD count (default 1024).  ``ranges``
+reads a run with --kernel-trace --marker-trace and prints, per roctx push/pop range,
+the kernels that started and ended inside it (count and total duration per kernel),
+marking those that are not this library's (torch's at::native kernels and the like).
 """
 import collections
 import csv
@@ -114,6 +118,43 @@ def mfma(d, n_xcd=8, n_simd=1024):
         print(f"{mops[k] * 512 / 1e9:11.1f} {100 * util:8.1f}%  {k}")
 
 
+def _ranges(d):
+    """(name, start_ns, end_ns) of every roctx push/pop range in a marker trace."""
+    out = []
+    for path in _find(d, "marker_api_trace.csv"):
+        for r in csv.DictReader(open(path)):
+            name = r.get("Function") or r.get("Message") or r.get("Marker_Message") or ""
+            if not name:
+                continue
+            out.append((name, int(_col(r, "Start_Timestamp")), int(_col(r, "End_Timestamp"))))
+    return sorted(out, key=lambda x: x[1])
+
+
+def ranges(d):
+    kernels = []
+    for path in _find(d, "kernel_trace.csv"):
+        for r in csv.DictReader(open(path)):
+            kernels.append((int(_col(r, "Start_Timestamp")), int(_col(r, "End_Timestamp")),
+                            short(_col(r, "Kernel_Name"), 120)))
+    for name, t0, t1 in _ranges(d):
+        inside = [k for k in kernels if k[0] >= t0 and k[1] <= t1]
+        per = collections.OrderedDict()
+        for s0, s1, k in sorted(inside):
+            c = per.setdefault(k, [0, 0.0])
+            c[0] += 1
+            c[1] += (s1 - s0) / 1e3
+        foreign = [k for k in per if not _ours(k)]
+        print(f"## {name}: {len(inside)} kernels, {sum(c[1] for c in per.values()):.1f} us of "
+              f"kernel time, {len(foreign)} kernel names not from libtgbwd")
+        for k, (n, us) in per.items():
+            print(f"  {'  ' if _ours(k) else '**'} {n:4d} {us:10.1f} us  {k}")
+
+
+def _ours(name):
+    n = name[5:] if name.startswith("void ") else name
+    return n.startswith("k_") or "_GLOBAL__N_" in n
+
+
 if __name__ == "__main__":
     mode, args = sys.argv[1], sys.argv[2:]
     if mode == "traffic":
@@ -122,4 +163,4 @@ if __name__ == "__main__":
         mfma(*args)
     else:
         for d in args:
-            {"stats": stats, "pmc": pmc}[mode](d)
+            {"stats": stats, "pmc": pmc, "ranges": ranges}[mode](d)

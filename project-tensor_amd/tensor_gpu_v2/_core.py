@@ -138,9 +138,10 @@ class Tensor:
     # ------------------------------------------------------------ grad storage
     def _new_buf(self, fill=None):
         d = self.data
-        if fill is None:
-            return torch.empty(d.shape, dtype=d.dtype, device=d.device)
-        return torch.full(d.shape, fill, dtype=d.dtype, device=d.device)
+        buf = torch.empty(d.shape, dtype=d.dtype, device=d.device)
+        if fill is not None:
+            _fill(buf, fill)
+        return buf
 
     @property
     def grad(self):
@@ -182,10 +183,7 @@ class Tensor:
         """Give this node its own contiguous copy of a gradient buffer it shares (or
         holds with strides)."""
         buf = self._new_buf()
-        if self._g.is_contiguous():
-            L.axpby(self._g, buf, 1.0, 0.0)
-        else:
-            buf.copy_(self._g)
+        _copy_into(buf, self._g)
         self._g = buf
         self._gsh = False
 
@@ -243,10 +241,7 @@ class Tensor:
                 self._g = g
             else:
                 buf = self._new_buf()
-                if g.is_contiguous() and g.dtype in L._TORCH_TO_CODE and buf.dtype in L._TORCH_TO_CODE:
-                    L.axpby(g, buf, 1.0, 0.0)
-                else:
-                    buf.copy_(g)
+                _copy_into(buf, g)
                 self._g = buf
             return
         if (g.is_contiguous() and self._g.is_contiguous() and g.dtype in L._TORCH_TO_CODE
@@ -257,11 +252,9 @@ class Tensor:
             else:
                 L.axpby(g, self._g, 1.0, 1.0)
         else:
-            if self._gsh:
-                self._g = self._g + g.to(self._g.dtype)
-                self._gsh = False
-            else:
-                self._g.add_(g.to(self._g.dtype))
+            if self._gsh or not self._g.is_contiguous():
+                self._privatize()
+            L.broadcast_mul_sum(self._g, g, accumulate=True)
 
     # ------------------------------------------------------------ properties
     @property
@@ -375,12 +368,12 @@ class Tensor:
         if out._requires_grad:
             def _backward():
                 g = out._grad_out()
-                if self._has_grad():
-                    self._accumulate(_unbroadcast_dev(other.data * g, self.data.shape,
-                                                      self.data.dtype), True)
-                if other._has_grad():
-                    other._accumulate(_unbroadcast_dev(self.data * g, other.data.shape,
-                                                       other.data.dtype), True)
+                # t.grad (+)= unbroadcast(u * g): one strided multiply-and-sum kernel
+                for t, u in ((self, other), (other, self)):
+                    if t._has_grad():
+                        _check_unbroadcast(tuple(g.shape), tuple(t.data.shape))
+                        buf, acc = t._grad_target()
+                        L.broadcast_mul_sum(buf, g, u.data, accumulate=acc)
             out._backward = _backward
         return out
 
@@ -436,7 +429,8 @@ class Tensor:
                         g = g.unsqueeze(ax)
                 elif not keepdims:
                     g = g.reshape((1,) * self.data.dim())
-                self._accumulate(g.expand(self.data.shape))
+                buf, acc = self._grad_target()  # a broadcast fill of the upstream grad
+                L.broadcast_mul_sum(buf, g, accumulate=acc)
             out._backward = _backward
         return out
 
@@ -585,12 +579,10 @@ class Tensor:
             def _backward():
                 if not self._has_grad():
                     return
-                yy = out.data.movedim(ax, -1).contiguous() if moved else out.data
+                dt = self.data.dtype
+                yy = _as(out.data.movedim(ax, -1) if moved else out.data, dt)
                 g = out._grad_out()
-                g = (g.movedim(ax, -1) if moved else g).contiguous().to(yy.dtype)
-                if yy.dtype != self.data.dtype:
-                    yy = yy.to(self.data.dtype)
-                    g = g.to(self.data.dtype)
+                g = _as(g.movedim(ax, -1) if moved else g, dt)
                 if moved:
                     dx = L.softmax_bwd(yy, g, torch.empty_like(yy), False)
                     self._accumulate(dx.movedim(-1, ax), True)
@@ -699,12 +691,20 @@ class Tensor:
         out = self._out(self.data[idx_t], (self,), "getitem")
         if out._requires_grad:
             def _backward():
-                if self._has_grad():
+                if not self._has_grad():
+                    return
+                g = out._grad_out()
+                buf, acc = self._grad_target()
+                if not acc:
+                    _fill(buf, 0.0)
+                if _basic_index(idx_t):
+                    # a view of the gradient buffer: one strided add into it
+                    L.broadcast_mul_sum(buf[idx_t], g, accumulate=True)
+                else:  # integer-array / mask indexing: torch's indexing backward
                     leaf = torch.zeros_like(self.data, requires_grad=True)
                     with torch.enable_grad():
-                        leaf[idx_t].backward(out._grad_out().to(leaf.dtype))
-                    z = leaf.grad
-                    self._accumulate(z, True)
+                        leaf[idx_t].backward(_as(g, leaf.dtype))
+                    L.broadcast_mul_sum(buf, leaf.grad, accumulate=True)
             out._backward = _backward
         return out
 
@@ -755,13 +755,22 @@ class Tensor:
             g = gradient.data if isinstance(gradient, Tensor) else gradient
             if not isinstance(g, torch.Tensor):
                 g = torch.as_tensor(np.asarray(g))
-            g = g.to(device="cuda", dtype=self.data.dtype)
+            if g.device.type != "cuda":
+                g = g.to(device="cuda")
             if not self._has_grad():
-                self._g = g.expand(self.data.shape).clone()
+                self._g = self._new_buf()
+                _copy_into(self._g, g)
                 self._gz = False
                 self._gsh = False
             else:
-                self._accumulate(g.expand(self.data.shape).contiguous())
+                if self._gz:
+                    self._g = self._new_buf()
+                    _copy_into(self._g, g)
+                    self._gz = False
+                else:
+                    if self._gsh or not self._g.is_contiguous():
+                        self._privatize()
+                    L.broadcast_mul_sum(self._g, g, accumulate=True)
         elif self._gz or self._g is None or not bool(torch.any(self._g != 0)):
             self._g = self._new_buf(1)
             self._gz = False
@@ -809,6 +818,11 @@ def _scalar_like(v, ref):
     return torch.as_tensor(arr, device="cuda")
 
 
+def _basic_index(idx):
+    items = idx if isinstance(idx, tuple) else (idx,)
+    return all(i is None or i is Ellipsis or isinstance(i, (int, slice)) for i in items)
+
+
 def _index_to_torch(idx):
     if isinstance(idx, tuple):
         return tuple(_index_to_torch(i) for i in idx)
@@ -838,19 +852,48 @@ def _unbroadcast_dev(grad, shape, dtype):
         out = torch.empty(shape, dtype=dtype, device=grad.device)
         L.reduce_rows(grad, out, False)
         return out
-    g = grad
-    while g.dim() > len(shape):
-        g = g.sum(dim=0)
-    for ax, (gd, sd) in enumerate(zip(g.shape, shape)):
-        if sd == 1:
-            if gd != 1:
-                g = g.sum(dim=ax, keepdim=True)
-        elif gd != sd:
+    _check_unbroadcast(tuple(grad.shape), shape)
+    out = torch.empty(shape, dtype=dtype, device=grad.device)
+    return L.broadcast_mul_sum(out, grad)
+
+
+def _check_unbroadcast(gshape, shape):
+    """The reference's unbroadcast rules (_core.py:1402-1422): the target has no more
+    axes than the gradient, and each target axis equals the gradient's or is 1."""
+    if len(gshape) < len(shape):
+        raise ValueError(
+            f"cannot unbroadcast grad with shape {gshape} to higher-rank shape {shape}")
+    tail = gshape[len(gshape) - len(shape):]
+    for ax, (gd, sd) in enumerate(zip(tail, shape)):
+        if sd != 1 and gd != sd:
             raise ValueError(
                 f"incompatible unbroadcast axis {ax}: grad dim {gd} cannot map to target dim {sd}")
-    if tuple(g.shape) != shape:
-        raise ValueError(f"unbroadcast produced shape {tuple(g.shape)}, expected {shape}")
-    return g.to(dtype)
+
+
+def _as(t, dtype):
+    """t as a contiguous tensor of `dtype`: t itself when it already is one, else a new
+    buffer written by the strided copy kernel (which also materialises broadcasts)."""
+    if t.dtype == dtype and t.is_contiguous():
+        return t
+    out = torch.empty(t.shape, dtype=dtype, device=t.device)
+    _copy_into(out, t)
+    return out
+
+
+def _fill(buf, value):
+    if buf.dtype in L._TORCH_TO_CODE and buf.is_contiguous():
+        L.fill(buf, value)
+    else:
+        buf.fill_(value)
+
+
+def _copy_into(dst, src):
+    """dst = src (broadcast to dst's shape), any strides and float dtypes, on the kernels."""
+    if (dst.is_contiguous() and src.is_contiguous() and src.shape == dst.shape
+            and src.dtype in L._TORCH_TO_CODE and dst.dtype in L._TORCH_TO_CODE):
+        L.axpby(src, dst, 1.0, 0.0)
+    else:
+        L.broadcast_mul_sum(dst, src)
 
 
 def _activation(x, kind):
@@ -865,8 +908,7 @@ def _activation(x, kind):
             if not x._has_grad():
                 return
             g = out._grad_out()
-            if g.dtype != xc.dtype or not g.is_contiguous():
-                g = g.to(xc.dtype).contiguous()
+            g = _as(g, xc.dtype)
             buf, acc = x._grad_target()
             L.act_bwd(kind, xc, g, buf, acc)
         out._backward = _backward
@@ -958,7 +1000,7 @@ def _linear(x, w, b):
     if out._requires_grad:
         def _backward():
             g = out._grad_out()
-            G2 = g.to(cdt).contiguous().reshape(-1, N)
+            G2 = _as(g, cdt).reshape(-1, N)
             if x._has_grad():
                 buf, acc = x._grad_target()
                 if buf.dtype in (torch.float32, cdt):
@@ -966,15 +1008,20 @@ def _linear(x, w, b):
                                beta=1.0 if acc else 0.0)
                 else:
                     da = L.matmul2d(G2, bc, trans_b=not wt, out_dtype=torch.float32)
-                    x._accumulate(da.reshape(buf.shape), True) if acc else buf.copy_(
-                        da.reshape(buf.shape))
+                    if acc:
+                        x._accumulate(da.reshape(buf.shape), True)
+                    else:
+                        _copy_into(buf, da.reshape(buf.shape))
             if w._has_grad():
                 buf, acc = w._grad_target()
                 if buf.dtype in (torch.float32, cdt):
                     L.matmul2d(A2, G2, out=buf.view(K, N), trans_a=True, beta=1.0 if acc else 0.0)
                 else:
                     dw = L.matmul2d(A2, G2, trans_a=True, out_dtype=torch.float32)
-                    w._accumulate(dw, True) if acc else buf.copy_(dw)
+                    if acc:
+                        w._accumulate(dw, True)
+                    else:
+                        _copy_into(buf, dw)
             if b is not None and b._has_grad():
                 b._accumulate_unb(g)
         out._backward = _backward
@@ -990,7 +1037,7 @@ def _batch_view(x, batch_shape, m, n):
     xb = tuple(x.shape[:-2])
     if xb == tuple(batch_shape):
         return x.reshape(bsz, m, n), m * n, bsz
-    xe = x.expand(*batch_shape, m, n).contiguous()
+    xe = _as(x.expand(*batch_shape, m, n), x.dtype)
     return xe.reshape(bsz, m, n), m * n, bsz
 
 
@@ -1053,7 +1100,7 @@ def _matmul_bwd(self, other, ac, bc, out):
         G = g.unsqueeze(-1)
     else:
         G = g
-    G = G.to(cdt).contiguous()
+    G = _as(G, cdt)
     M, K = A.shape[-2], A.shape[-1]
     N = Bm.shape[-1]
     if Bm.dim() == 2:
@@ -1068,10 +1115,7 @@ def _matmul_bwd(self, other, ac, bc, out):
                            beta=1.0 if acc else 0.0)
             else:
                 da = L.matmul2d(G2, Bm, trans_b=True, out_dtype=torch.float32)
-                if acc:
-                    buf.add_(da.reshape(buf.shape).to(buf.dtype))
-                else:
-                    buf.copy_(da.reshape(buf.shape))
+                L.broadcast_mul_sum(buf, da.reshape(buf.shape), accumulate=acc)
         if other._has_grad():
             # dB[k, n] = sum over all leading rows of A^T @ G: one TN GEMM with K' = rows
             buf, acc = other._grad_target()
@@ -1079,15 +1123,12 @@ def _matmul_bwd(self, other, ac, bc, out):
                 L.matmul2d(A2, G2, out=buf.view(K, N), trans_a=True, beta=1.0 if acc else 0.0)
             else:
                 db = L.matmul2d(A2, G2, trans_a=True, out_dtype=torch.float32)
-                if acc:
-                    buf.add_(db.reshape(buf.shape).to(buf.dtype))
-                else:
-                    buf.copy_(db.reshape(buf.shape))
+                L.broadcast_mul_sum(buf, db.reshape(buf.shape), accumulate=acc)
         return
     # batched operands
     batch_shape = torch.broadcast_shapes(tuple(A.shape[:-2]), tuple(Bm.shape[:-2]))
     bsz = int(np.prod(batch_shape))
-    G3 = G.expand(*batch_shape, M, N).contiguous().reshape(bsz, M, N)
+    G3 = _as(G.expand(*batch_shape, M, N), cdt).reshape(bsz, M, N)
     if self._has_grad():
         B3, sb, _ = _batch_view(Bm, batch_shape, K, N)
         da = torch.empty(bsz, M, K, dtype=torch.float32, device=A.device)
@@ -1142,11 +1183,12 @@ def flash_attention(query, key, value, block_size=64, is_causal=False, scale=Non
                        "FlashAttention")
     if out._requires_grad:
         def _backward():
-            g = out._grad_out().reshape(q4c.shape).to(dt)
-            if not L._fa_in(g, lay):
-                g = (g.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3) if lay == 1
-                     else g.contiguous())
+            g = out._grad_out().reshape(q4c.shape)
             B_, H_, Sq_, D_ = q4c.shape
+            if g.dtype != dt or not L._fa_in(g, lay):
+                gl = L.fa_empty(B_, H_, Sq_, D_, dt, q4c.device, lay)
+                _copy_into(gl, g)
+                g = gl
             Sk_ = k4c.shape[2]
             dq = L.fa_empty(B_, H_, Sq_, D_, dt, q4c.device, lay)
             dk = L.fa_empty(B_, H_, Sk_, D_, dt, q4c.device, lay)

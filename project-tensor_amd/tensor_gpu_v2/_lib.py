@@ -52,6 +52,8 @@ SIGNATURES = {
     "tg_layernorm_bwd_noalloc_max_scratch": (_sz, []),
     "tg_layernorm_bwd_noalloc": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
                                         _i64, _i32, _i32, _vp]),
+    "tg_broadcast_mul_sum": (_i32, [_i32, _vp, _i32, _vp, _vp, _i32, _vp, _vp, _i32, _vp, _vp,
+                                    _f64, _i32, _vp]),
     "tg_reduce_rows_workspace": (_sz, [_i64, _i64]),
     "tg_reduce_rows": (_i32, [_i32, _vp, _i32, _vp, _i64, _i64, _i32, _vp, _sz, _vp]),
     "tg_batchnorm_workspace": (_sz, [_i32, _i64, _i64, _i64]),
@@ -280,6 +282,45 @@ def fill(y, value):
     _check("tg_fill", load().tg_fill(dtype_code(y), ptr(y), y.numel(), float(value),
                                      stream_handle()))
     return y
+
+
+_BCAST_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.float64: 3}
+
+
+def _i64_array(vals):
+    return (ctypes.c_int64 * max(len(vals), 1))(*vals)
+
+
+def broadcast_mul_sum(out, a, b=None, alpha=1.0, accumulate=False):
+    """out (+)= alpha * a * b, with a and b broadcast (NumPy rules) to the index space
+    broadcast(a, b, out) and the result summed over every axis where out has extent 1
+    (or that out lacks, counted from the right).  Any strides and any mix of fp32 /
+    fp16 / bf16 / fp64; b may be None.  Returns out."""
+    for n, t in (("out", out), ("a", a), ("b", b)):
+        if t is None:
+            continue
+        if not isinstance(t, torch.Tensor) or not t.is_cuda:
+            raise TypeError(f"broadcast_mul_sum: {n} must be a torch device tensor")
+        if t.dtype not in _BCAST_CODE:
+            raise TypeError(f"broadcast_mul_sum: unsupported dtype {t.dtype} for {n}")
+    shapes = [tuple(a.shape), tuple(out.shape)] + ([tuple(b.shape)] if b is not None else [])
+    space = torch.broadcast_shapes(*shapes)
+    if len(out.shape) > len(space):
+        raise ValueError(f"broadcast_mul_sum: out {tuple(out.shape)} has more axes than {space}")
+    for size, stride in zip(out.shape, out.stride()):
+        if size > 1 and stride == 0:
+            raise ValueError("broadcast_mul_sum: out overlaps itself (a zero stride)")
+    sa = a.expand(space).stride()
+    so = out.expand(space).stride()
+    sb = b.expand(space).stride() if b is not None else ()
+    nd = len(space)
+    ensure_device(out.device.index)
+    _check("tg_broadcast_mul_sum", load().tg_broadcast_mul_sum(
+        nd, _i64_array(space), _BCAST_CODE[a.dtype], ptr(a), _i64_array(sa),
+        _BCAST_CODE[b.dtype] if b is not None else 0, ptr(b), _i64_array(sb) if nd else None,
+        _BCAST_CODE[out.dtype], ptr(out), _i64_array(so), float(alpha), int(bool(accumulate)),
+        stream_handle()))
+    return out
 
 
 # ---------------------------------------------------------------- row-wise
