@@ -1,69 +1,177 @@
 // Embedding backward and the tied-weight gradient transfer.
 //
 // tg_embedding_bwd: grad[idx[i]] (+)= dout[i] (Embedding._backward, _nn.py:1083-1089,
-// a scatter-add).  Deterministic: (index, position) pairs are radix-sorted (stable,
-// rocPRIM), then one wavefront per run of equal indices sums the run's dout rows in
-// their original order in fp32 and adds the sum to the gradient row once -- the
-// order np.add.at uses, so fp32 results match it exactly.  Indices outside [0, V)
-// are skipped.  Rows never indexed are left as they are (zeroed first when not
-// accumulating).
+// a scatter-add).  Deterministic: the tokens are sorted by (index, position) -- 64-bit
+// keys index << 32 | position, all distinct -- with a radix sort of 8192-key chunks in
+// LDS (stable, so equal indices keep their token order) and, for more tokens, merge
+// passes of the sorted chunks.  One wavefront per run of equal indices then sums the
+// run's dout rows in their original order in fp32 and writes the gradient row once --
+// the order np.add.at uses, so fp32 results match it exactly.  When not accumulating,
+// every gradient row is zeroed first; for up to 8192 tokens that fill runs in the same
+// launch as the sort (one workgroup sorts, the others write zeros), so the sort's
+// latency hides behind the fill.  Indices outside [0, V) are skipped.
 //
 // tg_transpose_add: dst[c][r] += alpha * src[r][c] through 64x64 LDS tiles
 // (sync_tied_gradients, _training.py:264-284: source.grad += param.grad.T).
-#include <rocprim/device/device_radix_sort.hpp>
-
 #include "tg_common.h"
 
 namespace {
 
 constexpr int kBlock = 256;
 
-template <typename T>
-__global__ __launch_bounds__(kBlock) void k_fill_zero(T* __restrict__ p, int64_t n) {
-  const int64_t stride = (int64_t)gridDim.x * kBlock;
-  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
-    p[i] = tg_from_float<T>(0.f);
+constexpr int kSortThreads = 1024;
+constexpr int kChunk = 8192;  // keys sorted per workgroup in LDS (two 64 KiB buffers)
+
+// Sort keys: index << pb | position, with pb position bits (32 in 64-bit keys; in
+// 32-bit keys, used when the index and position bits fit, the fewest that hold n - 1).
+template <typename K>
+__device__ __forceinline__ K sort_key(const int64_t* idx, int64_t i, int64_t V, int pb) {
+  const int64_t k = idx[i];
+  const K key = (k >= 0 && k < V) ? (K)k : (K)V;  // V: skipped
+  return key << pb | (K)i;
 }
 
-// Sort input: positions 0..n-1 and 32-bit keys, every index outside [0, V) mapped to
-// the sentinel V (sorted after all valid keys, then skipped).  When not accumulating,
-// also clears the per-row "touched" flags.
-__global__ __launch_bounds__(kBlock) void k_embed_prep(const int64_t* __restrict__ idx,
-                                                       int64_t n, int64_t V,
-                                                       int* __restrict__ keys,
-                                                       int* __restrict__ pos,
-                                                       int* __restrict__ touched) {
-  const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-  if (i < n) {
-    const int64_t k = idx[i];
-    keys[i] = (k >= 0 && k < V) ? (int)k : (int)V;
-    pos[i] = (int)i;
+// Each workgroup sorts one chunk of kChunk tokens by index in LDS and writes it to
+// out[chunk]: a least-significant-digit radix sort on 8-bit digits of the index, which
+// is stable, so equal indices keep their token order and the chunk ends sorted by the
+// whole 64-bit key.  A pass: each wavefront owns 512 consecutive keys (8 rounds of 64);
+// lanes holding the same digit are found with 8 ballots, so each key's rank among equal
+// digits in its wavefront comes from a per-wavefront digit histogram; a scan over
+// (digit, wavefront) gives every group's destination.  Workgroups from `nsort` on do
+// not sort: they write zeros over `fill` (fill_n elements of type TG; none if null).
+template <typename K, typename TG>
+__global__ __launch_bounds__(kSortThreads) void k_embed_sort_chunk(const int64_t* __restrict__ idx,
+                                                                   int64_t n, int64_t V, int pb,
+                                                                   int passes, int nsort,
+                                                                   K* __restrict__ out,
+                                                                   TG* __restrict__ fill,
+                                                                   int64_t fill_n) {
+  if ((int)blockIdx.x >= nsort) {
+    constexpr int PZ = 16 / (int)sizeof(TG);
+    tg_vec16<TG> z;
+#pragma unroll
+    for (int e = 0; e < PZ; ++e) z.v[e] = tg_from_float<TG>(0.f);
+    const bool al = (reinterpret_cast<uintptr_t>(fill) & 15) == 0;
+    const int64_t nv = al ? fill_n / PZ : 0, fb = (int64_t)gridDim.x - nsort;
+    const int64_t stride = fb * kSortThreads;
+    const int64_t t0 = ((int64_t)blockIdx.x - nsort) * kSortThreads + threadIdx.x;
+    for (int64_t v = t0; v < nv; v += stride) tg_store16_nt(fill + v * PZ, z);
+    for (int64_t e = nv * PZ + t0; e < fill_n; e += stride) fill[e] = tg_from_float<TG>(0.f);
+    return;
   }
-  if (touched && i < V) touched[i] = 0;
+  constexpr int kWaves = kSortThreads / 64, kPer = kChunk / kWaves, kRounds = kPer / 64;
+  __shared__ K buf[2][kChunk];
+  __shared__ int hist[kWaves][256];
+  __shared__ int wtot[4];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const uint64_t lt = (1ull << lane) - 1;
+  const int64_t base = (int64_t)blockIdx.x * kChunk;
+  const int cnt = (int)(n - base < kChunk ? n - base : kChunk);
+  for (int i = threadIdx.x; i < cnt; i += kSortThreads) buf[0][i] = sort_key<K>(idx, base + i, V, pb);
+  int cur = 0;
+  for (int pass = 0; pass < passes; ++pass, cur ^= 1) {
+    const int sh = pb + 8 * pass;
+    for (int d = lane; d < 256; d += 64) hist[w][d] = 0;
+    __syncthreads();
+    K val[kRounds];
+    int dig[kRounds], rank[kRounds];
+#pragma unroll
+    for (int it = 0; it < kRounds; ++it) {
+      const int i = w * kPer + it * 64 + lane;
+      const bool ok = i < cnt;
+      val[it] = ok ? buf[cur][i] : 0;
+      const int d = (int)((val[it] >> sh) & 255);
+      uint64_t m = __ballot(ok);
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        const uint64_t bb = __ballot((d >> b) & 1);
+        m &= ((d >> b) & 1) ? bb : ~bb;
+      }
+      const int h = ok ? hist[w][d] : 0;
+      dig[it] = d;
+      rank[it] = h + __popcll(m & lt);
+      if (ok && (m & lt) == 0) hist[w][d] = h + __popcll(m);  // the group's first lane
+    }
+    __syncthreads();
+    // exclusive offsets in (digit, wavefront) order: threads 0..255 own one digit each
+    int run = 0, inc = 0;
+    if (threadIdx.x < 256) {
+      const int d = threadIdx.x;
+      for (int ww = 0; ww < kWaves; ++ww) {
+        const int c = hist[ww][d];
+        hist[ww][d] = run;
+        run += c;
+      }
+      inc = run;  // inclusive scan of the digit totals within the wavefront
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(inc, off, 64);
+        if (lane >= off) inc += y;
+      }
+      if (lane == 63) wtot[w] = inc;
+    }
+    __syncthreads();
+    if (threadIdx.x < 256) {
+      int add = inc - run;  // digits of lower wavefronts come first
+      for (int ww = 0; ww < w; ++ww) add += wtot[ww];
+      for (int ww = 0; ww < kWaves; ++ww) hist[ww][threadIdx.x] += add;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < kRounds; ++it) {
+      const int i = w * kPer + it * 64 + lane;
+      if (i < cnt) buf[cur ^ 1][hist[w][dig[it]] + rank[it]] = val[it];
+    }
+    __syncthreads();
+  }
+  for (int i = threadIdx.x; i < cnt; i += kSortThreads) out[base + i] = buf[cur][i];
 }
 
-// One wavefront per sorted position; a wave whose position starts a run of equal keys
-// sums the run's dout rows in their original order (four rows in flight) and writes
-// the gradient row: grad (+)= sum when accumulating, else grad = sum and the row is
-// marked touched.  VEC: each lane owns PER = 16/sizeof(TD) adjacent columns (16-byte
-// loads); else 4 columns 64 apart.
-template <typename TD, typename TG, bool VEC>
-__global__ __launch_bounds__(kBlock) void k_embed_seg(const int* __restrict__ keys,
-                                                      const int* __restrict__ pos, int64_t n,
-                                                      const TD* __restrict__ dout, int64_t dim,
-                                                      int64_t V, int accumulate,
-                                                      int* __restrict__ touched,
+// One merge pass: adjacent sorted runs of `width` keys (all keys distinct) merged into
+// runs of 2*width.  Each element's output position is its rank in its own run plus
+// the number of keys of the partner run below it (binary search).
+template <typename K>
+__global__ __launch_bounds__(256) void k_embed_merge(const K* __restrict__ in, int64_t n,
+                                                     int64_t width, K* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const K v = in[i];
+  const int64_t pair = i / (2 * width) * (2 * width);
+  const bool left = i - pair < width;
+  const int64_t own0 = left ? pair : pair + width;
+  int64_t o0 = left ? pair + width : pair;
+  int64_t o1 = left ? pair + 2 * width : pair + width;
+  if (o0 > n) o0 = n;
+  if (o1 > n) o1 = n;
+  int64_t lo = o0, hi = o1;  // first partner key > v (keys are distinct)
+  while (lo < hi) {
+    const int64_t m = (lo + hi) >> 1;
+    if (in[m] < v) lo = m + 1;
+    else hi = m;
+  }
+  out[pair + (i - own0) + (lo - o0)] = v;
+}
+
+// One wavefront per sorted position; a wave whose position starts a run of equal
+// indices sums the run's dout rows in their original order (four rows in flight) and
+// writes the gradient row once: grad (+)= sum.  VEC: each lane owns PER = 16/sizeof(TD)
+// adjacent columns (16-byte loads); else 4 columns 64 apart.
+template <typename K, typename TD, typename TG, bool VEC, bool VG>
+__global__ __launch_bounds__(kBlock) void k_embed_seg(const K* __restrict__ sorted, int pb,
+                                                      int64_t n, const TD* __restrict__ dout,
+                                                      int64_t dim, int64_t V, int accumulate,
                                                       TG* __restrict__ grad) {
   constexpr int PER = VEC ? 16 / (int)sizeof(TD) : 4;
   constexpr int U = 4;
   const int lane = threadIdx.x & 63;
   const int64_t i = (int64_t)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
   if (i >= n) return;
-  const int key = keys[i];
-  if (i > 0 && keys[i - 1] == key) return;  // not the start of a run
-  if (key >= V) return;                     // sentinel: index outside [0, V)
+  const K pmask = ((K)1 << pb) - 1;
+  const K key = sorted[i] >> pb;
+  if (key >= (K)V) return;                            // index outside [0, V)
+  if (i > 0 && (sorted[i - 1] >> pb) == key) return;  // not the start of a run
   int64_t end = i + 1;
-  while (end < n && keys[end] == key) ++end;
+  while (end < n && (sorted[end] >> pb) == key) ++end;
   TG* grow = grad + (int64_t)key * dim;
   auto col = [&](int64_t c0, int e) {
     return VEC ? c0 + (int64_t)lane * PER + e : c0 + (int64_t)e * 64 + lane;
@@ -73,7 +181,7 @@ __global__ __launch_bounds__(kBlock) void k_embed_seg(const int* __restrict__ ke
 #pragma unroll
     for (int e = 0; e < PER; ++e) acc[e] = 0.f;
     auto load = [&](int64_t j, float (&v)[PER]) {
-      const TD* drow = dout + (int64_t)pos[j] * dim;
+      const TD* drow = dout + (int64_t)(sorted[j] & pmask) * dim;
       if (VEC) {
         if (col(c0, 0) < dim) {
           const tg_vec16<TD> t = tg_load16(drow + col(c0, 0));
@@ -104,35 +212,25 @@ __global__ __launch_bounds__(kBlock) void k_embed_seg(const int* __restrict__ ke
 #pragma unroll
       for (int e = 0; e < PER; ++e) acc[e] += v[e];
     }
+    if (VG && col(c0, 0) < dim) {  // PER adjacent outputs per lane as 16-byte stores
+      constexpr int NG = tg_vec16<TG>::N;
 #pragma unroll
-    for (int e = 0; e < PER; ++e) {
-      const int64_t c = col(c0, e);
-      if (c < dim)
-        grow[c] = tg_from_float<TG>((accumulate ? tg_to_float(grow[c]) : 0.f) + acc[e]);
-    }
-  }
-  if (!accumulate && lane == 0) touched[key] = 1;
-}
-
-// Zero every gradient row that no index touched (not accumulating): one wavefront per
-// row, 16-byte non-temporal stores when rows are 16-byte multiples.
-template <typename TG, bool VZ>
-__global__ __launch_bounds__(kBlock) void k_embed_zero_rows(const int* __restrict__ touched,
-                                                            int64_t V, int64_t dim,
-                                                            TG* __restrict__ grad) {
-  const int lane = threadIdx.x & 63;
-  const int64_t stride = (int64_t)gridDim.x * (kBlock / 64);
-  for (int64_t r = (int64_t)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6); r < V; r += stride) {
-    if (touched[r]) continue;
-    TG* grow = grad + r * dim;
-    if (VZ) {
-      constexpr int PER = 16 / (int)sizeof(TG);
-      tg_vec16<TG> z;
+      for (int h = 0; h < PER / NG; ++h) {
+        TG* p = grow + col(c0, h * NG);
+        tg_vec16<TG> o;
+        if (accumulate) o = tg_load16(p);
 #pragma unroll
-      for (int e = 0; e < PER; ++e) z.v[e] = tg_from_float<TG>(0.f);
-      for (int64_t c = (int64_t)lane * PER; c < dim; c += 64 * PER) tg_store16_nt(grow + c, z);
-    } else {
-      for (int64_t c = lane; c < dim; c += 64) grow[c] = tg_from_float<TG>(0.f);
+        for (int e = 0; e < NG; ++e)
+          o.v[e] = tg_from_float<TG>((accumulate ? tg_to_float(o.v[e]) : 0.f) + acc[h * NG + e]);
+        tg_store16(p, o);
+      }
+    } else if (!VG) {
+#pragma unroll
+      for (int e = 0; e < PER; ++e) {
+        const int64_t c = col(c0, e);
+        if (c < dim)
+          grow[c] = tg_from_float<TG>((accumulate ? tg_to_float(grow[c]) : 0.f) + acc[e]);
+      }
     }
   }
 }
@@ -190,20 +288,6 @@ __global__ __launch_bounds__(kBlock) void k_transpose_add_v4(const float* __rest
     for (int i = 0; i < 4; ++i) o[k].v[i] += alpha * tile[q + i][w + 16 * k];
     tg_store16_nt(dst + (c0 + w + 16 * k) * R + r0 + q, o[k]);
   }
-}
-
-int sort_bits(int64_t V) {
-  int b = 1;
-  while (b < 63 && ((int64_t)1 << b) < V) ++b;
-  return b;
-}
-
-size_t sort_temp_bytes(int64_t n, int64_t V) {
-  size_t bytes = 0;
-  (void)rocprim::radix_sort_pairs(nullptr, bytes, (const int*)nullptr, (int*)nullptr,
-                                  (const int*)nullptr, (int*)nullptr, (size_t)n, 0,
-                                  sort_bits(V + 1));
-  return bytes;
 }
 
 // Gather: out[i, :] = weight[idx[i], :] converted to the output dtype (negative
@@ -266,70 +350,72 @@ int embed_fwd_t(const void* w, const int64_t* idx, int64_t n, int64_t dim, int64
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
-// Workspace: keys_in, keys_out, pos_in, pos_out (n ints each), touched (V ints), then
-// rocPRIM's radix-sort scratch.
-size_t embed_ws(int64_t n, int64_t V, size_t* tmp_off) {
-  const size_t fixed = 4 * align256(n * sizeof(int)) + align256(V * sizeof(int));
-  if (tmp_off) *tmp_off = fixed;
-  return fixed + align256(sort_temp_bytes(n, V));
+// Workspace: two n-key buffers of 64-bit keys (the sorted keys and the merge passes'
+// partner); 32-bit keys use the front of each.
+size_t embed_ws(int64_t n) { return 2 * align256(n * sizeof(uint64_t)); }
+
+int bits_for(int64_t v) {  // bits holding 0..v
+  int b = 1;
+  while (b < 63 && (v >> b) > 0) ++b;
+  return b;
+}
+
+template <typename K, typename TD, typename TG>
+int embed_k(const void* dout, const int64_t* idx, int64_t n, int64_t dim, void* grad, int64_t V,
+            int accumulate, char* ws, int pb, hipStream_t s) {
+  const int64_t total = V * dim;
+  int64_t fill_blocks = (total + 8 * kSortThreads - 1) / (8 * kSortThreads);
+  if (fill_blocks > (int64_t)tg_num_cus() * 2) fill_blocks = (int64_t)tg_num_cus() * 2;
+  if (fill_blocks < 1) fill_blocks = 1;
+  if (n == 0) {  // nothing indexed: the gradient is zero (or unchanged)
+    if (!accumulate)
+      k_embed_sort_chunk<K, TG><<<(unsigned)fill_blocks, kSortThreads, 0, s>>>(
+          nullptr, 0, V, pb, 0, 0, nullptr, (TG*)grad, total);
+    return tg_check_launch("tg_embedding_bwd");
+  }
+  const size_t nb = align256(n * sizeof(uint64_t));
+  K* buf[2] = {(K*)ws, (K*)(ws + nb)};
+  const int64_t chunks = (n + kChunk - 1) / kChunk;
+  const int passes = (bits_for(V) + 7) / 8;  // 8-bit digits of indices 0..V (V: skipped)
+  // one chunk: the zero fill rides in the sort's launch; else it is its own launch
+  const bool fused = !accumulate && chunks == 1;
+  k_embed_sort_chunk<K, TG><<<(unsigned)(chunks + (fused ? fill_blocks : 0)), kSortThreads, 0, s>>>(
+      idx, n, V, pb, passes, (int)chunks, buf[0], fused ? (TG*)grad : nullptr, fused ? total : 0);
+  if (!accumulate && !fused)
+    k_embed_sort_chunk<K, TG><<<(unsigned)fill_blocks, kSortThreads, 0, s>>>(
+        nullptr, 0, V, pb, 0, 0, nullptr, (TG*)grad, total);
+  int cur = 0;
+  for (int64_t w = kChunk; w < n; w *= 2, cur ^= 1)
+    k_embed_merge<K><<<(unsigned)((n + 255) / 256), 256, 0, s>>>(buf[cur], n, w, buf[cur ^ 1]);
+  constexpr int PER = 16 / (int)sizeof(TD);
+  const bool vec = dim % PER == 0 && tg_aligned16(dout);
+  const bool vg = vec && (PER * sizeof(TG)) % 16 == 0 && (dim * sizeof(TG)) % 16 == 0 &&
+                  tg_aligned16(grad);
+  const unsigned sb = (unsigned)((n + 3) / 4);
+#define SEG(VE, VGE)                                                                        \
+  k_embed_seg<K, TD, TG, VE, VGE><<<sb, kBlock, 0, s>>>(buf[cur], pb, n, (const TD*)dout, dim, \
+                                                        V, accumulate, (TG*)grad)
+  if (vg) SEG(true, true);
+  else if (vec) SEG(true, false);
+  else SEG(false, false);
+#undef SEG
+  return tg_check_launch("tg_embedding_bwd");
 }
 
 template <typename TD, typename TG>
 int embed_t(const void* dout, const int64_t* idx, int64_t n, int64_t dim, void* grad, int64_t V,
-            int accumulate, char* ws, size_t ws_bytes, hipStream_t s) {
-  if (n == 0) {  // nothing indexed: the gradient is zero (or unchanged)
-    if (!accumulate) {
-      const int64_t total = V * dim;
-      int64_t blocks = (total + kBlock - 1) / kBlock;
-      if (blocks > (int64_t)tg_num_cus() * 16) blocks = (int64_t)tg_num_cus() * 16;
-      k_fill_zero<TG><<<(unsigned)(blocks < 1 ? 1 : blocks), kBlock, 0, s>>>((TG*)grad, total);
-    }
-    return tg_check_launch("tg_embedding_bwd");
-  }
-  size_t tmp_off = 0;
-  embed_ws(n, V, &tmp_off);
-  const size_t nb = align256(n * sizeof(int));
-  int* keys_in = (int*)ws;
-  int* keys_out = (int*)(ws + nb);
-  int* pos_in = (int*)(ws + 2 * nb);
-  int* pos_out = (int*)(ws + 3 * nb);
-  int* touched = accumulate ? nullptr : (int*)(ws + 4 * nb);
-  char* tmp = ws + tmp_off;
-  size_t tmp_bytes = ws_bytes - tmp_off;
-  const int64_t m = n > V ? n : V;
-  k_embed_prep<<<(unsigned)((m + kBlock - 1) / kBlock), kBlock, 0, s>>>(idx, n, V, keys_in, pos_in,
-                                                                        touched);
-  if (rocprim::radix_sort_pairs(tmp, tmp_bytes, keys_in, keys_out, pos_in, pos_out, (size_t)n, 0,
-                                sort_bits(V + 1), s) != hipSuccess) {
-    tg_set_error("tg_embedding_bwd: radix sort failed");
-    return TG_ERR_HIP;
-  }
-  constexpr int PER = 16 / (int)sizeof(TD);
-  const bool vec = dim % PER == 0 && tg_aligned16(dout);
-  const unsigned sb = (unsigned)((n + 3) / 4);
-  if (vec)
-    k_embed_seg<TD, TG, true><<<sb, kBlock, 0, s>>>(keys_out, pos_out, n, (const TD*)dout, dim, V,
-                                                    accumulate, touched, (TG*)grad);
-  else
-    k_embed_seg<TD, TG, false><<<sb, kBlock, 0, s>>>(keys_out, pos_out, n, (const TD*)dout, dim,
-                                                     V, accumulate, touched, (TG*)grad);
-  if (!accumulate) {
-    int64_t blocks = (V + 3) / 4;
-    if (blocks > (int64_t)tg_num_cus() * 32) blocks = (int64_t)tg_num_cus() * 32;
-    const bool vz = (dim * (int64_t)sizeof(TG)) % 16 == 0 && tg_aligned16(grad);
-    if (vz)
-      k_embed_zero_rows<TG, true><<<(unsigned)blocks, kBlock, 0, s>>>(touched, V, dim, (TG*)grad);
-    else
-      k_embed_zero_rows<TG, false><<<(unsigned)blocks, kBlock, 0, s>>>(touched, V, dim, (TG*)grad);
-  }
-  return tg_check_launch("tg_embedding_bwd");
+            int accumulate, char* ws, hipStream_t s) {
+  const int pb = n > 1 ? bits_for(n - 1) : 1;
+  if (bits_for(V) + pb <= 32)
+    return embed_k<uint32_t, TD, TG>(dout, idx, n, dim, grad, V, accumulate, ws, pb, s);
+  return embed_k<uint64_t, TD, TG>(dout, idx, n, dim, grad, V, accumulate, ws, 32, s);
 }
 
 }  // namespace
 
 TG_EXPORT size_t tg_embedding_bwd_workspace(int64_t n_tokens, int64_t num_embeddings) {
   if (n_tokens <= 0) return 0;
-  return embed_ws(n_tokens, num_embeddings > 1 ? num_embeddings : 1, nullptr);
+  return embed_ws(n_tokens);
 }
 
 TG_EXPORT int tg_embedding_bwd(int dtype_dout, const void* dout, const int64_t* indices,
@@ -348,17 +434,18 @@ TG_EXPORT int tg_embedding_bwd(int dtype_dout, const void* dout, const int64_t* 
   }
   hipStream_t s = tg_stream(stream);
   char* ws = (char*)workspace;
-#define G(TD)                                                                                  \
-  switch (dtype_grad) {                                                                        \
-    case TG_F32: return embed_t<TD, float>(dout, indices, n_tokens, dim, grad, num_embeddings, \
-                                           accumulate, ws, workspace_bytes, s);                \
-    case TG_F16: return embed_t<TD, tg_half>(dout, indices, n_tokens, dim, grad,               \
-                                             num_embeddings, accumulate, ws, workspace_bytes,  \
-                                             s);                                               \
-    case TG_BF16: return embed_t<TD, tg_bf16>(dout, indices, n_tokens, dim, grad,              \
-                                              num_embeddings, accumulate, ws, workspace_bytes, \
-                                              s);                                              \
-  }                                                                                            \
+#define G(TD)                                                                              \
+  switch (dtype_grad) {                                                                    \
+    case TG_F32:                                                                           \
+      return embed_t<TD, float>(dout, indices, n_tokens, dim, grad, num_embeddings,        \
+                                accumulate, ws, s);                                        \
+    case TG_F16:                                                                           \
+      return embed_t<TD, tg_half>(dout, indices, n_tokens, dim, grad, num_embeddings,      \
+                                  accumulate, ws, s);                                      \
+    case TG_BF16:                                                                          \
+      return embed_t<TD, tg_bf16>(dout, indices, n_tokens, dim, grad, num_embeddings,      \
+                                  accumulate, ws, s);                                      \
+  }                                                                                        \
   break;
   switch (dtype_dout) {
     case TG_F32: G(float)
