@@ -195,7 +195,10 @@ int tg_gemm_bias(int dtype_ab, int dtype_c, int trans_a, int trans_b, int64_t M,
 /* ---- attention ------------------------------------------------------------ */
 /* FlashAttention forward on contiguous (B,H,S,D) tensors, saving the row
  * log-sum-exp lse[B,H,Sq] (fp32) for the backward.  causal masks col > row
- * (_core.py:1686-1786).  dtype fp16 or bf16, D in {64, 128}. */
+ * (_core.py:1686-1786).  dtype fp32, fp16 or bf16; head dim D from 1 to 256 (fp16/bf16
+ * with D 64 or 128 and 16-byte aligned operands run the tuned kernels, everything else
+ * the generic ones on fp32 matrix cores); any B*H (split over launches of at most
+ * 65535 heads), H <= 65535. */
 int tg_flash_attn_fwd(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
                       int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D, float scale,
                       int causal, void* stream);

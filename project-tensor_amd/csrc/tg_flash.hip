@@ -1,5 +1,6 @@
-// FlashAttention forward and backward for gfx950 (fp16 / bf16, head dim 64 or 128),
-// reference: flash_attention (_core.py:1686-1870).
+// FlashAttention forward and backward for gfx950, reference: flash_attention
+// (_core.py:1686-1870).  Tuned kernels for fp16 / bf16 with head dim 64 or 128; generic
+// kernels (fp32 matrix cores, any head dim up to 256) for fp32 and other head dims.
 //
 // Tensors are contiguous [B, H, S, D]; lse is [B, H, Sq] fp32 (natural log).
 // causal masks key > query (top-left aligned, as the reference's col > row).
@@ -30,6 +31,8 @@
 //   D = rowsum(dO * O) is formed by k_fa_bwd_dq (launched first) for its queries and
 //   stored for k_fa_bwd_dkdv.
 #include "tg_common.h"
+
+#include <initializer_list>
 
 namespace {
 
@@ -1267,13 +1270,406 @@ int bwd_t(const void* q, const void* k, const void* v, const void* o, const void
   return tg_check_launch("tg_flash_attn_bwd");
 }
 
+// ============================================================ generic head dims / fp32
+// Any head dim D <= 256 and fp32 as well as fp16/bf16 inputs: the same algorithm as
+// the kernels above on the fp32 matrix cores (v_mfma_f32_32x32x2_f32), so fp32
+// attention keeps fp32 precision.  D is padded with zeros to DP, a multiple of 32,
+// inside the kernels; loads and stores are element-wise (no alignment requirement).
+//
+// 32x32x2 MFMA: A lane (row i = lane%32, k = lane/32) supplies one element, B lane
+// (col j = lane%32, k = lane/32) one element, C as above.  A contraction over the head
+// dim takes DP/2 steps; in step s lane half h supplies head-dim index
+// kap(s, h) = 8*(s/4) + 4h + s%4, so a lane's operand for four steps is one 16-byte
+// read of 4 adjacent elements.  A contraction over 32 keys (or queries) held in a C
+// tile takes 16 steps; in step s lane half h supplies row crow(s, h), i.e. its own
+// accumulator register s, and the other operand is read at that row.
+typedef float gf32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x16 mfma2(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+template <typename T>
+__device__ __forceinline__ float gld(const T* p, int64_t i) { return (float)p[i]; }
+
+// Row `row` of a [*, D] operand, head-dim indices kap(s, h) for s < DP/2, into
+// registers (zero past D or for an invalid row).
+template <typename T, int DP>
+__device__ __forceinline__ void load_kap(const T* __restrict__ g, int64_t row, int rs, int D,
+                                         bool valid, int h, float (&r)[DP / 2]) {
+#pragma unroll
+  for (int t = 0; t < DP / 8; ++t)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int d = 8 * t + 4 * h + e;
+      r[4 * t + e] = (valid && d < D) ? gld(g, row * rs + d) : 0.f;
+    }
+}
+
+// Stage rows [row0, row0+32) x DP of a [nrows, D] operand into LDS (row stride LD),
+// zero past nrows or D.  All 256 threads of the workgroup take part.
+template <typename T, int DP>
+__device__ __forceinline__ void stage32(const T* __restrict__ g, int64_t row0, int64_t nrows,
+                                        int rs, int D, float* s) {
+  constexpr int LD = DP + 4;
+  for (int e = threadIdx.x; e < 32 * DP; e += kThreads) {
+    const int r = e / DP, d = e - r * DP;
+    const int64_t row = row0 + r;
+    s[r * LD + d] = (row < nrows && d < D) ? gld(g, row * rs + d) : 0.f;
+  }
+}
+
+// S^T (or S) tile: sum over the head dim of A rows (LDS, row = lane%32) against the
+// B operand registers b (kap order).
+template <int DP>
+__device__ __forceinline__ f32x16 gen_dot(const float* As, int l32, int h, const float (&b)[DP / 2]) {
+  constexpr int LD = DP + 4;
+  f32x16 c;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) c[r] = 0.f;
+#pragma unroll
+  for (int t = 0; t < DP / 8; ++t) {
+    const gf32x4 a = *reinterpret_cast<const gf32x4*>(As + l32 * LD + 8 * t + 4 * h);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) c = mfma2(a[e], b[4 * t + e], c);
+  }
+  return c;
+}
+
+// acc[db] += X^T[d][row] * P[row][col] over the 32 rows of a C tile P (registers p):
+// A operand X read from LDS at rows crow(s, h), head-dim columns d0 + 32*db + lane%32.
+template <int DP, int NDB>
+__device__ __forceinline__ void gen_acc(f32x16 (&acc)[NDB], const float* Xs, int d0, int l32,
+                                        int h, const f32x16& p) {
+  constexpr int LD = DP + 4;
+#pragma unroll
+  for (int s = 0; s < 16; ++s) {
+    const float* row = Xs + crow(s, h) * LD + d0 + l32;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) acc[db] = mfma2(row[32 * db], p[s], acc[db]);
+  }
+}
+
+// Forward.  grid = (ceil(Sq/128), B*H); one workgroup = 128 queries (4 waves x 32,
+// lane = query, Q in registers), key tiles of 32 staged in LDS.
+template <typename T, int DP>
+__global__ __launch_bounds__(kThreads) void k_fa_fwd_gen(const T* __restrict__ Q,
+                                                         const T* __restrict__ K,
+                                                         const T* __restrict__ V,
+                                                         T* __restrict__ O, float* __restrict__ LSE,
+                                                         int64_t Sq, int64_t Sk, int D,
+                                                         float scale, int causal, FaLay lay) {
+  constexpr int NS = DP / 2, NDB = DP / 32, LD = DP + 4;
+  __shared__ __attribute__((aligned(16))) float Ks[32 * LD];
+  __shared__ __attribute__((aligned(16))) float Vs[32 * LD];
+  int64_t tile, bh;
+  fa_block(tile, bh, lay.G);
+  Q += lay.head(bh, Sq, D);
+  O += lay.head(bh, Sq, D);
+  K += lay.head(bh, Sk, D);
+  V += lay.head(bh, Sk, D);
+  LSE += bh * Sq;
+  const int rs = lay.rs(D);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int h = lane >> 5, l32 = lane & 31;
+  const int64_t qb = causal ? (int64_t)gridDim.x - 1 - tile : tile;
+  const int64_t q = qb * 128 + wave * 32 + l32;
+  float qr[NS];
+  load_kap<T, DP>(Q, q, rs, D, q < Sq, h, qr);
+  f32x16 acc[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
+  const float sl2 = scale * kLog2e;
+  float m = -INFINITY, l = 0.f;
+  const int64_t kend = causal ? (qb * 128 + 128 < Sk ? qb * 128 + 128 : Sk) : Sk;
+  for (int64_t k0 = 0; k0 < kend; k0 += 32) {
+    __syncthreads();
+    stage32<T, DP>(K, k0, Sk, rs, D, Ks);
+    stage32<T, DP>(V, k0, Sk, rs, D, Vs);
+    __syncthreads();
+    f32x16 s = gen_dot<DP>(Ks, l32, h, qr);
+    float smax = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int64_t key = k0 + crow(r, h);
+      const bool ok = key < Sk && (!causal || key <= q);
+      s[r] = ok ? s[r] * sl2 : -INFINITY;
+      smax = fmaxf(smax, s[r]);
+    }
+    smax = fmaxf(smax, __shfl_xor(smax, 32, 64));
+    const float mn = fmaxf(m, smax);
+    // every key so far masked for this query: p = 0 and nothing is rescaled (no branch,
+    // so the whole wavefront reaches the MFMAs)
+    const float mref = mn == -INFINITY ? 0.f : mn;
+    const float alpha = fexp2(m - mref);
+    float ps = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      s[r] = fexp2(s[r] - mref);
+      ps += s[r];
+    }
+    l = l * alpha + ps;
+    m = mn;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
+    gen_acc<DP, NDB>(acc, Vs, 0, l32, h, s);
+  }
+  l += __shfl_xor(l, 32, 64);
+  if (q < Sq) {
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int d = 32 * db + crow(r, h);
+        if (d < D) O[q * rs + d] = (T)(acc[db][r] * inv);
+      }
+    if (h == 0) LSE[q] = l > 0.f ? (m + log2f(l)) / kLog2e : -INFINITY;
+  }
+}
+
+// dQ (and D = rowsum(dO * O)).  grid = (ceil(Sq/128), B*H, DP/DO); lane = query, Q and
+// dO in registers, key tiles of 32 in LDS; the workgroup writes head-dim columns
+// [z*DO, z*DO + DO) of dQ (S and dP are recomputed per column range).
+template <typename T, int DP, int DO>
+__global__ __launch_bounds__(kThreads) void k_fa_bwd_dq_gen(
+    const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
+    const T* __restrict__ O, const T* __restrict__ dO, const float* __restrict__ LSE,
+    float* __restrict__ Dv, T* __restrict__ dQ, int64_t Sq, int64_t Sk, int D, float scale,
+    int causal, int accumulate, FaLay lay) {
+  constexpr int NS = DP / 2, NDB = DO / 32, LD = DP + 4;
+  __shared__ __attribute__((aligned(16))) float Ks[32 * LD];
+  __shared__ __attribute__((aligned(16))) float Vs[32 * LD];
+  int64_t tile, bh;
+  fa_block(tile, bh, lay.G);
+  Q += lay.head(bh, Sq, D);
+  O += lay.head(bh, Sq, D);
+  dO += lay.head(bh, Sq, D);
+  dQ += lay.head(bh, Sq, D);
+  K += lay.head(bh, Sk, D);
+  V += lay.head(bh, Sk, D);
+  LSE += bh * Sq;
+  Dv += bh * Sq;
+  const int rs = lay.rs(D);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int h = lane >> 5, l32 = lane & 31;
+  const int d0 = blockIdx.z * DO;
+  const int64_t qb = causal ? (int64_t)gridDim.x - 1 - tile : tile;
+  const int64_t q = qb * 128 + wave * 32 + l32;
+  const bool qv = q < Sq;
+  float qr[NS], dor[NS];
+  load_kap<T, DP>(Q, q, rs, D, qv, h, qr);
+  load_kap<T, DP>(dO, q, rs, D, qv, h, dor);
+  float dsum = 0.f;
+#pragma unroll
+  for (int t = 0; t < DP / 8; ++t)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int d = 8 * t + 4 * h + e;
+      if (qv && d < D) dsum += gld(O, q * rs + d) * dor[4 * t + e];
+    }
+  dsum += __shfl_xor(dsum, 32, 64);
+  if (qv && h == 0 && blockIdx.z == 0) Dv[q] = dsum;
+  const float lq = qv ? LSE[q] * kLog2e : 0.f;
+  const float sl2 = scale * kLog2e;
+  f32x16 acc[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
+  const int64_t kend = causal ? (qb * 128 + 128 < Sk ? qb * 128 + 128 : Sk) : Sk;
+  for (int64_t k0 = 0; k0 < kend; k0 += 32) {
+    __syncthreads();
+    stage32<T, DP>(K, k0, Sk, rs, D, Ks);
+    stage32<T, DP>(V, k0, Sk, rs, D, Vs);
+    __syncthreads();
+    f32x16 p = gen_dot<DP>(Ks, l32, h, qr);
+    const f32x16 dp = gen_dot<DP>(Vs, l32, h, dor);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int64_t key = k0 + crow(r, h);
+      const bool ok = qv && key < Sk && (!causal || key <= q);
+      const float pr = ok ? fexp2(p[r] * sl2 - lq) : 0.f;
+      p[r] = pr * (dp[r] - dsum) * scale;  // dS^T
+    }
+    gen_acc<DP, NDB>(acc, Ks, d0, l32, h, p);
+  }
+  if (qv) {
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int d = d0 + 32 * db + crow(r, h);
+        if (d < D) {
+          const int64_t i = q * rs + d;
+          dQ[i] = (T)(acc[db][r] + (accumulate ? (float)dQ[i] : 0.f));
+        }
+      }
+  }
+}
+
+// dK, dV.  grid = (ceil(Sk/128), B*H, DP/DO); lane = key, K and V in registers, query
+// tiles of 32 (Q, dO, their LSE and D) in LDS; the workgroup writes head-dim columns
+// [z*DO, z*DO + DO) of dK and dV.
+template <typename T, int DP, int DO>
+__global__ __launch_bounds__(kThreads) void k_fa_bwd_dkdv_gen(
+    const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
+    const T* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Dv,
+    T* __restrict__ dK, T* __restrict__ dV, int64_t Sq, int64_t Sk, int D, float scale,
+    int causal, int accumulate, FaLay lay) {
+  constexpr int NS = DP / 2, NDB = DO / 32, LD = DP + 4;
+  __shared__ __attribute__((aligned(16))) float Qs[32 * LD];
+  __shared__ __attribute__((aligned(16))) float dOs[32 * LD];
+  __shared__ float ls[32], ds[32];
+  int64_t tile, bh;
+  fa_block(tile, bh, lay.G);
+  Q += lay.head(bh, Sq, D);
+  dO += lay.head(bh, Sq, D);
+  K += lay.head(bh, Sk, D);
+  V += lay.head(bh, Sk, D);
+  dK += lay.head(bh, Sk, D);
+  dV += lay.head(bh, Sk, D);
+  LSE += bh * Sq;
+  Dv += bh * Sq;
+  const int rs = lay.rs(D);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int h = lane >> 5, l32 = lane & 31;
+  const int d0 = blockIdx.z * DO;
+  // causal: the first key blocks see the most queries, so they are dispatched first
+  const int64_t kb = tile;
+  const int64_t key = kb * 128 + wave * 32 + l32;
+  const bool kv = key < Sk;
+  float kr[NS], vr[NS];
+  load_kap<T, DP>(K, key, rs, D, kv, h, kr);
+  load_kap<T, DP>(V, key, rs, D, kv, h, vr);
+  const float sl2 = scale * kLog2e;
+  f32x16 ak[NDB], av[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) ak[db][r] = av[db][r] = 0.f;
+  const int64_t qstart = causal ? kb * 128 : 0;
+  for (int64_t q0 = qstart; q0 < Sq; q0 += 32) {
+    __syncthreads();
+    stage32<T, DP>(Q, q0, Sq, rs, D, Qs);
+    stage32<T, DP>(dO, q0, Sq, rs, D, dOs);
+    if (threadIdx.x < 32) {
+      const int64_t qq = q0 + threadIdx.x;
+      ls[threadIdx.x] = qq < Sq ? LSE[qq] * kLog2e : 0.f;
+      ds[threadIdx.x] = qq < Sq ? Dv[qq] : 0.f;
+    }
+    __syncthreads();
+    f32x16 p = gen_dot<DP>(Qs, l32, h, kr);
+    const f32x16 dp = gen_dot<DP>(dOs, l32, h, vr);
+    f32x16 dsv;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int qi = crow(r, h);
+      const int64_t qq = q0 + qi;
+      const bool ok = kv && qq < Sq && (!causal || key <= qq);
+      p[r] = ok ? fexp2(p[r] * sl2 - ls[qi]) : 0.f;
+      dsv[r] = p[r] * (dp[r] - ds[qi]) * scale;
+    }
+    gen_acc<DP, NDB>(av, dOs, d0, l32, h, p);
+    gen_acc<DP, NDB>(ak, Qs, d0, l32, h, dsv);
+  }
+  if (kv) {
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int d = d0 + 32 * db + crow(r, h);
+        if (d < D) {
+          const int64_t i = key * rs + d;
+          dK[i] = (T)(ak[db][r] + (accumulate ? (float)dK[i] : 0.f));
+          dV[i] = (T)(av[db][r] + (accumulate ? (float)dV[i] : 0.f));
+        }
+      }
+  }
+}
+
+// Output head-dim columns per workgroup of the generic backward: all of DP up to 128,
+// else half of it (the registers of a wave then hold K, V (or Q, dO) for the whole
+// head dim plus accumulators for half of it).
+template <int DP> struct GenSplit {
+  static constexpr int DO = DP <= 128 ? DP : DP / 2;
+  static_assert(DP % DO == 0 && DO % 32 == 0, "head-dim split");
+};
+
+template <typename T, int DP>
+int fwd_gen_t(const void* q, const void* k, const void* v, void* o, float* lse, int64_t BH,
+              int64_t Sq, int64_t Sk, int D, float scale, int causal, FaLay lay, hipStream_t s) {
+  dim3 grid((unsigned)((Sq + 127) / 128), (unsigned)BH);
+  k_fa_fwd_gen<T, DP><<<grid, kThreads, 0, s>>>((const T*)q, (const T*)k, (const T*)v, (T*)o, lse,
+                                                Sq, Sk, D, scale, causal, lay);
+  return tg_check_launch("tg_flash_attn_fwd");
+}
+
+template <typename T, int DP>
+int bwd_gen_t(const void* q, const void* k, const void* v, const void* o, const void* dout,
+              const float* lse, void* dq, void* dk, void* dv, int64_t BH, int64_t Sq, int64_t Sk,
+              int D, float scale, int causal, int acc, float* dvec, FaLay lay, hipStream_t s) {
+  constexpr int DO = GenSplit<DP>::DO;
+  dim3 gq((unsigned)((Sq + 127) / 128), (unsigned)BH, DP / DO);
+  k_fa_bwd_dq_gen<T, DP, DO><<<gq, kThreads, 0, s>>>(
+      (const T*)q, (const T*)k, (const T*)v, (const T*)o, (const T*)dout, lse, dvec, (T*)dq, Sq,
+      Sk, D, scale, causal, acc, lay);
+  dim3 gkv((unsigned)((Sk + 127) / 128), (unsigned)BH, DP / DO);
+  k_fa_bwd_dkdv_gen<T, DP, DO><<<gkv, kThreads, 0, s>>>(
+      (const T*)q, (const T*)k, (const T*)v, (const T*)dout, lse, dvec, (T*)dk, (T*)dv, Sq, Sk, D,
+      scale, causal, acc, lay);
+  return tg_check_launch("tg_flash_attn_bwd");
+}
+
+// Padded head dims of the generic path.
+#define TG_GEN_DP(X) X(32) X(64) X(96) X(128) X(192) X(256)
+
+int gen_dp(int64_t D) {
+  if (D <= 32) return 32;
+  if (D <= 64) return 64;
+  if (D <= 96) return 96;
+  if (D <= 128) return 128;
+  if (D <= 192) return 192;
+  return 256;
+}
+
+template <typename T>
+int fwd_gen(const void* q, const void* k, const void* v, void* o, float* lse, int64_t BH,
+            int64_t Sq, int64_t Sk, int D, float scale, int causal, FaLay lay, hipStream_t s) {
+  switch (gen_dp(D)) {
+#define C(DP) \
+  case DP: return fwd_gen_t<T, DP>(q, k, v, o, lse, BH, Sq, Sk, D, scale, causal, lay, s);
+    TG_GEN_DP(C)
+#undef C
+  }
+  return TG_ERR_UNSUPPORTED;
+}
+
+template <typename T>
+int bwd_gen(const void* q, const void* k, const void* v, const void* o, const void* dout,
+            const float* lse, void* dq, void* dk, void* dv, int64_t BH, int64_t Sq, int64_t Sk,
+            int D, float scale, int causal, int acc, float* dvec, FaLay lay, hipStream_t s) {
+  switch (gen_dp(D)) {
+#define C(DP)                                                                                  \
+  case DP: return bwd_gen_t<T, DP>(q, k, v, o, dout, lse, dq, dk, dv, BH, Sq, Sk, D, scale,   \
+                                   causal, acc, dvec, lay, s);
+    TG_GEN_DP(C)
+#undef C
+  }
+  return TG_ERR_UNSUPPORTED;
+}
+
 int check_fa(int dtype, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
              const char* who) {
-  TG_REQUIRE(dtype == TG_F16 || dtype == TG_BF16, "%s: dtype must be fp16 or bf16", who);
-  TG_REQUIRE(D == 64 || D == 128, "%s: head dim %lld not supported (64, 128)", who,
-             (long long)D);
+  TG_REQUIRE(dtype == TG_F16 || dtype == TG_BF16 || dtype == TG_F32,
+             "%s: dtype must be fp32, fp16 or bf16", who);
+  TG_REQUIRE(D >= 1 && D <= 256, "%s: head dim %lld not supported (1..256)", who, (long long)D);
   TG_REQUIRE(B > 0 && H > 0 && Sq > 0 && Sk > 0, "%s: empty or negative shape", who);
-  TG_REQUIRE(B * H <= 65535, "%s: B*H = %lld exceeds 65535", who, (long long)(B * H));
+  TG_REQUIRE(H <= 65535, "%s: H = %lld exceeds 65535", who, (long long)H);
   return TG_OK;
 }
 
@@ -1289,6 +1685,25 @@ int fa_group(int64_t BH, int causal) {
   return g;
 }
 
+// The tuned fp16/bf16 kernels serve head dims 64 and 128 with 16-byte aligned operands;
+// everything else runs on the generic fp32-MFMA kernels.
+bool fa_fast(int dtype, int64_t D, std::initializer_list<const void*> ptrs) {
+  if (dtype == TG_F32 || (D != 64 && D != 128)) return false;
+  for (const void* p : ptrs)
+    if (!tg_aligned16(p)) return false;
+  return true;
+}
+
+// Batches per launch: the grid's y dimension (B*H heads) is limited to 65535.
+int64_t fa_batch_chunk(int64_t B, int64_t H) {
+  const int64_t nb = 65535 / H;
+  return nb < B ? nb : B;
+}
+
+const char* off(const void* p, int64_t elems, int esz) {
+  return (const char*)p + elems * esz;
+}
+
 int fa_fwd(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
            int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D, float scale, int causal,
            int layout, void* stream, const char* who) {
@@ -1296,16 +1711,35 @@ int fa_fwd(int dtype, const void* q, const void* k, const void* v, void* o, floa
   if (st) return st;
   TG_REQUIRE(layout == 0 || layout == 1, "%s: layout must be 0 (BHSD) or 1 (BSHD)", who);
   TG_REQUIRE(q && k && v && o && lse, "%s: null pointer", who);
-  TG_REQUIRE(tg_aligned16(q) && tg_aligned16(k) && tg_aligned16(v) && tg_aligned16(o),
-             "%s: operands must be 16-byte aligned", who);
   hipStream_t s = tg_stream(stream);
-  const int64_t BH = B * H;
-  const FaLay lay{H, layout, fa_group(B * H, causal)};
-  if (dtype == TG_F16)
-    return D == 64 ? fwd_t<tg_half, 64>(q, k, v, o, lse, BH, Sq, Sk, scale, causal, lay, s)
-                   : fwd_t<tg_half, 128>(q, k, v, o, lse, BH, Sq, Sk, scale, causal, lay, s);
-  return D == 64 ? fwd_t<tg_bf16, 64>(q, k, v, o, lse, BH, Sq, Sk, scale, causal, lay, s)
-                 : fwd_t<tg_bf16, 128>(q, k, v, o, lse, BH, Sq, Sk, scale, causal, lay, s);
+  const bool fast = fa_fast(dtype, D, {q, k, v, o});
+  const int es = tg_dtype_size(dtype);
+  const int64_t nb = fa_batch_chunk(B, H);
+  for (int64_t b0 = 0; b0 < B; b0 += nb) {
+    const int64_t bn = B - b0 < nb ? B - b0 : nb, BH = bn * H;
+    const int64_t qo = b0 * H * Sq * D, ko = b0 * H * Sk * D;
+    const void *qc = off(q, qo, es), *kc = off(k, ko, es), *vc = off(v, ko, es);
+    void* oc = (void*)off(o, qo, es);
+    float* lc = lse + b0 * H * Sq;
+    const FaLay lay{H, layout, fa_group(BH, causal)};
+    const int Di = (int)D;
+    if (fast) {
+      if (dtype == TG_F16)
+        st = D == 64 ? fwd_t<tg_half, 64>(qc, kc, vc, oc, lc, BH, Sq, Sk, scale, causal, lay, s)
+                     : fwd_t<tg_half, 128>(qc, kc, vc, oc, lc, BH, Sq, Sk, scale, causal, lay, s);
+      else
+        st = D == 64 ? fwd_t<tg_bf16, 64>(qc, kc, vc, oc, lc, BH, Sq, Sk, scale, causal, lay, s)
+                     : fwd_t<tg_bf16, 128>(qc, kc, vc, oc, lc, BH, Sq, Sk, scale, causal, lay, s);
+    } else if (dtype == TG_F32) {
+      st = fwd_gen<float>(qc, kc, vc, oc, lc, BH, Sq, Sk, Di, scale, causal, lay, s);
+    } else if (dtype == TG_F16) {
+      st = fwd_gen<tg_half>(qc, kc, vc, oc, lc, BH, Sq, Sk, Di, scale, causal, lay, s);
+    } else {
+      st = fwd_gen<tg_bf16>(qc, kc, vc, oc, lc, BH, Sq, Sk, Di, scale, causal, lay, s);
+    }
+    if (st) return st;
+  }
+  return TG_OK;
 }
 
 int fa_bwd(int dtype, const void* q, const void* k, const void* v, const void* o,
@@ -1316,27 +1750,51 @@ int fa_bwd(int dtype, const void* q, const void* k, const void* v, const void* o
   if (st) return st;
   TG_REQUIRE(layout == 0 || layout == 1, "%s: layout must be 0 (BHSD) or 1 (BSHD)", who);
   TG_REQUIRE(q && k && v && o && dout && lse && dq && dk && dv, "%s: null pointer", who);
-  TG_REQUIRE(tg_aligned16(q) && tg_aligned16(k) && tg_aligned16(v) && tg_aligned16(o) &&
-                 tg_aligned16(dout) && tg_aligned16(dq) && tg_aligned16(dk) && tg_aligned16(dv),
-             "%s: operands must be 16-byte aligned", who);
   const size_t need = (size_t)(B * H * Sq) * sizeof(float);
   if (!workspace || workspace_bytes < need) {
     tg_set_error("%s: workspace of %zu bytes needed", who, need);
     return TG_ERR_WORKSPACE;
   }
   hipStream_t s = tg_stream(stream);
-  const int64_t BH = B * H;
-  const FaLay lay{H, layout, fa_group(B * H, causal)};
-  float* dvec = (float*)workspace;
-  if (dtype == TG_F16)
-    return D == 64 ? bwd_t<tg_half, 64>(q, k, v, o, dout, lse, dq, dk, dv, BH, Sq, Sk, scale,
-                                        causal, accumulate, dvec, lay, s)
-                   : bwd_t<tg_half, 128>(q, k, v, o, dout, lse, dq, dk, dv, BH, Sq, Sk, scale,
-                                         causal, accumulate, dvec, lay, s);
-  return D == 64 ? bwd_t<tg_bf16, 64>(q, k, v, o, dout, lse, dq, dk, dv, BH, Sq, Sk, scale,
-                                      causal, accumulate, dvec, lay, s)
-                 : bwd_t<tg_bf16, 128>(q, k, v, o, dout, lse, dq, dk, dv, BH, Sq, Sk, scale,
-                                       causal, accumulate, dvec, lay, s);
+  const bool fast = fa_fast(dtype, D, {q, k, v, o, dout, dq, dk, dv});
+  const int es = tg_dtype_size(dtype);
+  const int64_t nb = fa_batch_chunk(B, H);
+  for (int64_t b0 = 0; b0 < B; b0 += nb) {
+    const int64_t bn = B - b0 < nb ? B - b0 : nb, BH = bn * H;
+    const int64_t qo = b0 * H * Sq * D, ko = b0 * H * Sk * D;
+    const void *qc = off(q, qo, es), *kc = off(k, ko, es), *vc = off(v, ko, es);
+    const void *oc = off(o, qo, es), *gc = off(dout, qo, es);
+    void* dqc = (void*)off(dq, qo, es);
+    void* dkc = (void*)off(dk, ko, es);
+    void* dvc = (void*)off(dv, ko, es);
+    const float* lc = lse + b0 * H * Sq;
+    float* dvec = (float*)workspace + b0 * H * Sq;
+    const FaLay lay{H, layout, fa_group(BH, causal)};
+    const int Di = (int)D;
+    if (fast) {
+      if (dtype == TG_F16)
+        st = D == 64 ? bwd_t<tg_half, 64>(qc, kc, vc, oc, gc, lc, dqc, dkc, dvc, BH, Sq, Sk,
+                                          scale, causal, accumulate, dvec, lay, s)
+                     : bwd_t<tg_half, 128>(qc, kc, vc, oc, gc, lc, dqc, dkc, dvc, BH, Sq, Sk,
+                                           scale, causal, accumulate, dvec, lay, s);
+      else
+        st = D == 64 ? bwd_t<tg_bf16, 64>(qc, kc, vc, oc, gc, lc, dqc, dkc, dvc, BH, Sq, Sk,
+                                          scale, causal, accumulate, dvec, lay, s)
+                     : bwd_t<tg_bf16, 128>(qc, kc, vc, oc, gc, lc, dqc, dkc, dvc, BH, Sq, Sk,
+                                           scale, causal, accumulate, dvec, lay, s);
+    } else if (dtype == TG_F32) {
+      st = bwd_gen<float>(qc, kc, vc, oc, gc, lc, dqc, dkc, dvc, BH, Sq, Sk, Di, scale, causal,
+                          accumulate, dvec, lay, s);
+    } else if (dtype == TG_F16) {
+      st = bwd_gen<tg_half>(qc, kc, vc, oc, gc, lc, dqc, dkc, dvc, BH, Sq, Sk, Di, scale, causal,
+                            accumulate, dvec, lay, s);
+    } else {
+      st = bwd_gen<tg_bf16>(qc, kc, vc, oc, gc, lc, dqc, dkc, dvc, BH, Sq, Sk, Di, scale, causal,
+                            accumulate, dvec, lay, s);
+    }
+    if (st) return st;
+  }
+  return TG_OK;
 }
 }  // namespace
 

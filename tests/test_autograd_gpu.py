@@ -221,6 +221,26 @@ def test_flash_attention_tensor_api(tg):
         assert_close(v.grad, dv, RTOL_F16, "fa dv")
 
 
+@pytest.mark.parametrize("shape,causal", [((2, 3, 80, 64), True), ((2, 70, 64), False),
+                                          ((1, 2, 50, 40), False), ((3, 33, 96), True)])
+def test_flash_attention_tensor_api_fp32(tg, shape, causal):
+    """fp32 inputs (the reference's default dtype), 4-D (B, H, L, D) and 3-D (B, L, D),
+    head dims inside and outside 64/128, at the fp32 attention bar."""
+    rng = np.random.default_rng(18)
+    qn, kn, vn, don = (rng.standard_normal(shape).astype(np.float32) for _ in range(4))
+    q, k, v = (tg.Tensor(a) for a in (qn, kn, vn))
+    out = tg.flash_attention(q, k, v, is_causal=causal)
+    out.backward(don)
+    args = [a.astype(np.float64) for a in (qn, kn, vn)]
+    oo, _ = O.flash_attention_fwd(*args, is_causal=causal)
+    dq, dk, dv = O.flash_attention_bwd(*args, don.astype(np.float64), is_causal=causal)
+    assert out.data.dtype == torch.float32
+    assert_close(out.data, oo, RTOL_F32_MM, "fa out")
+    assert_close(q.grad, dq, RTOL_F32_MM, "fa dq")
+    assert_close(k.grad, dk, RTOL_F32_MM, "fa dk")
+    assert_close(v.grad, dv, RTOL_F32_MM, "fa dv")
+
+
 def test_cross_entropy_ignores_upstream_grad(tg):
     # (_nn.py:1168-1180): logits.grad = (softmax - onehot)/N, out.grad never read
     rng = np.random.default_rng(9)

@@ -10,7 +10,7 @@ import pytest
 import torch
 
 import oracle as O
-from conftest import GOLDEN, RTOL_F16, assert_close
+from conftest import GOLDEN, RTOL_F16, RTOL_F32_MM, assert_close
 
 pytestmark = pytest.mark.gpu
 RTOL = {torch.float16: RTOL_F16, torch.bfloat16: 3e-2}
@@ -159,9 +159,93 @@ def test_flash_full_size_all_heads(cuda, D, causal):
 
 
 def test_flash_rejects_bad_shapes(cuda):
-    q = rnd((1, 1, 16, 96), torch.float16, 0)
+    q = rnd((1, 1, 16, 264), torch.float16, 0)
     with pytest.raises(RuntimeError, match="head dim"):
         L().flash_attn_fwd(q, q, q, 0.1, False)
+
+
+# fp32 (the reference's default dtype) and head dims the fp16/bf16 tuned kernels do not
+# cover run on the generic kernels (fp32 matrix cores): fp32 at the 1e-4 attention bar
+GEN_CASES = [(1, 2, 96, 96, 64), (2, 1, 70, 70, 8), (1, 2, 33, 100, 40), (1, 1, 130, 65, 80),
+             (2, 2, 64, 64, 96), (1, 1, 100, 100, 128), (1, 1, 77, 140, 160),
+             (1, 1, 64, 96, 256), (1, 3, 1, 7, 32), (1, 1, 200, 50, 200)]
+
+
+@pytest.mark.parametrize("B,H,Sq,Sk,D", GEN_CASES)
+@pytest.mark.parametrize("causal", [False, True])
+def test_flash_fp32_vs_oracle(cuda, B, H, Sq, Sk, D, causal):
+    q = rnd((B, H, Sq, D), torch.float32, 1)
+    k = rnd((B, H, Sk, D), torch.float32, 2)
+    v = rnd((B, H, Sk, D), torch.float32, 3)
+    do = rnd((B, H, Sq, D), torch.float32, 4)
+    o, lse, dq, dk, dv = run(q, k, v, do, causal)
+    oo, ll = O.flash_attention_fwd(f64(q), f64(k), f64(v), causal)
+    assert_close(o, oo, RTOL_F32_MM, "O")
+    assert_close(lse, ll, 1e-5, "lse")
+    rq, rk, rv = O.flash_attention_bwd(f64(q), f64(k), f64(v), f64(do), causal)
+    for got, want, n in ((dq, rq, "dQ"), (dk, rk, "dK"), (dv, rv, "dV")):
+        if not np.any(want):
+            # one visible key per query (causal, Sq = 1): dS = P*(dP - D) is 0 exactly,
+            # the kernel's dP and D round differently: an absolute bound
+            assert float(got.abs().max()) < 1e-5, n
+        else:
+            assert_close(got, want, RTOL_F32_MM, n)
+
+
+@pytest.mark.parametrize("D", [32, 48, 96, 256])
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_flash_generic_head_dims_half(cuda, D, dt):
+    q, k, v, do = (rnd((1, 2, 150, D), dt, s) for s in range(4))
+    o, lse, dq, dk, dv = run(q, k, v, do, True)
+    oo, _ = O.flash_attention_fwd(f64(q), f64(k), f64(v), True)
+    assert_close(o, oo, RTOL[dt], "O")
+    rq, rk, rv = O.flash_attention_bwd(f64(q), f64(k), f64(v), f64(do), True, o=f64(o))
+    assert_close(dq, rq, RTOL[dt], "dQ")
+    assert_close(dk, rk, RTOL[dt], "dK")
+    assert_close(dv, rv, RTOL[dt], "dV")
+
+
+@pytest.mark.parametrize("D", [40, 64])
+def test_flash_fp32_bshd_layout_and_accumulate(cuda, D):
+    """The generic kernels read and write the (B, S, H, D) head split in place, and
+    accumulate adds to existing gradients."""
+    B, H, S = 2, 3, 90
+    g = torch.Generator(device="cuda").manual_seed(D)
+    mk = lambda: torch.randn(B, S, H, D, device="cuda", generator=g)  # noqa: E731
+    qs, ks, vs, dos = mk(), mk(), mk(), mk()
+    q1, k1, v1, do1 = (t.permute(0, 2, 1, 3) for t in (qs, ks, vs, dos))
+    q0, k0, v0, do0 = (t.contiguous() for t in (q1, k1, v1, do1))
+    sc = D ** -0.5
+    o0, l0 = L().flash_attn_fwd(q0, k0, v0, sc, True, 0)
+    o1, l1 = L().flash_attn_fwd(q1, k1, v1, sc, True, 1)
+    assert torch.equal(o0, o1) and torch.equal(l0, l1)
+    outs = []
+    for lay, (q, k, v, o, do) in ((0, (q0, k0, v0, o0, do0)), (1, (q1, k1, v1, o1, do1))):
+        d = [L().fa_empty(B, H, S, D, q.dtype, q.device, lay) for _ in range(3)]
+        for t in d:
+            t.fill_(0.5)
+        L().flash_attn_bwd(q, k, v, o, do, l0, *d, sc, True, True, lay)
+        outs.append(d)
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    rq, rk, rv = O.flash_attention_bwd(f64(q0), f64(k0), f64(v0), f64(do0), True)
+    for got, want, n in zip(outs[0], (rq, rk, rv), ("dq", "dk", "dv")):
+        assert_close(got, want + 0.5, RTOL_F32_MM, n)
+
+
+def test_flash_many_heads_chunked(cuda):
+    """B*H above the 65535 limit of one launch's grid: the batches are split over
+    several launches."""
+    B, H, S, D = 33000, 2, 3, 8
+    q, k, v, do = (rnd((B, H, S, D), torch.float32, s) for s in range(4))
+    o, lse, dq, dk, dv = run(q, k, v, do, False)
+    for b in (0, 32767, 32768, B - 1):
+        sl = slice(b, b + 1)
+        oo, ll = O.flash_attention_fwd(f64(q[sl]), f64(k[sl]), f64(v[sl]), False)
+        assert_close(o[sl], oo, RTOL_F32_MM, f"O b={b}")
+        rq, rk, rv = O.flash_attention_bwd(f64(q[sl]), f64(k[sl]), f64(v[sl]), f64(do[sl]), False)
+        assert_close(dq[sl], rq, RTOL_F32_MM, f"dQ b={b}")
+        assert_close(dv[sl], rv, RTOL_F32_MM, f"dV b={b}")
 
 
 @pytest.mark.parametrize("B,H,Sq,Sk,D", [(2, 3, 257, 513, 64), (1, 4, 192, 192, 128),
