@@ -16,14 +16,22 @@ BatchNorm-ReLU NHWC, AdamW, GradScaler unscale, the C5 GEMMs, FlashAttention
 backward, the GPT step) are reported under "components" with their own roofline
 fractions.
 
-The CPU baseline times the NumPy oracle (the reference's CPU algorithm) on a
-row sample of the same workload, single-threaded elementwise NumPy.
+The CPU baseline times the NumPy oracle (the reference's CPU algorithm) on the
+host's threads: the C2 step at full shape is `cpu_baseline.value`; C1, C3, C4 (fp32,
+scaled from a batch of heads) and C5 (one layer scaled to four, plus head, loss,
+embedding and AdamW) are under `cpu_baseline.configs`.
 """
 import argparse
 import json
 import os
 import sys
 import time
+
+# BLAS threads of the CPU baseline: the job's share of the host (OMP_NUM_THREADS when
+# the environment sets it), else every core; set before NumPy loads its BLAS.
+_THREADS = os.environ.get("OMP_NUM_THREADS") or str(os.cpu_count() or 1)
+os.environ.setdefault("OMP_NUM_THREADS", _THREADS)
+os.environ.setdefault("OPENBLAS_NUM_THREADS", _THREADS)
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "project-tensor_amd"))
@@ -237,19 +245,25 @@ def _op_gemm(torch, L, g):
     return Timed("gemm_fc1_bwd", run, 4 * M * N * K, "TFLOP/s", FP16_PEAK_TFLOPS)
 
 
-def _op_flash(torch, L, g, d, causal):
+FP32_PEAK_TFLOPS = 157.3
+
+
+def _op_flash(torch, L, g, d, causal, dt=None):
     """C4: FlashAttention backward, B=8, H=16, S=2048, fp16; 10*B*H*S^2*d flops
-    (halved when causal)."""
+    (halved when causal).  With dt = float32: the same shape in fp32 (the reference's
+    default dtype) on the fp32 matrix cores, against their 157.3 TFLOP/s."""
     B, H, S = 8, 16, 2048
-    q, k, v, do = (torch.randn(B, H, S, d, device="cuda", generator=g).half() for _ in range(4))
+    dt = dt or torch.float16
+    q, k, v, do = (torch.randn(B, H, S, d, device="cuda", generator=g).to(dt) for _ in range(4))
     o, lse = L.flash_attn_fwd(q, k, v, d ** -0.5, causal)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
 
     def run():
         L.flash_attn_bwd(q, k, v, o, do, lse, dq, dk, dv, d ** -0.5, causal, False)
     flops = 10 * B * H * S * S * d // (2 if causal else 1)
-    return Timed(f"flash_bwd_d{d}{'_causal' if causal else ''}", run, flops, "TFLOP/s",
-                 FP16_PEAK_TFLOPS)
+    fp32 = dt == torch.float32
+    return Timed(f"flash_bwd{'_fp32' if fp32 else ''}_d{d}{'_causal' if causal else ''}", run,
+                 flops, "TFLOP/s", FP32_PEAK_TFLOPS if fp32 else FP16_PEAK_TFLOPS)
 
 
 def _op_gpt(torch, L, g):
@@ -352,6 +366,8 @@ def component_ops(torch, L, only):
         for causal in (False, True):
             builders.append((f"flash_bwd_d{d}{'_causal' if causal else ''}",
                              lambda d=d, causal=causal: _op_flash(torch, L, g, d, causal)))
+    builders.append(("flash_bwd_fp32_d64",
+                     lambda: _op_flash(torch, L, g, 64, False, torch.float32)))
     for name, build in builders:
         if only and name not in only:
             continue
@@ -364,40 +380,232 @@ def component_ops(torch, L, only):
         yield op
 
 
+def _cpu_threads():
+    """Host threads for the CPU baseline: the process's OMP_NUM_THREADS when set (the
+    share of the host a job gets), else every core os.cpu_count() reports."""
+    try:
+        return max(1, int(os.environ.get("OMP_NUM_THREADS", "")))
+    except ValueError:
+        return os.cpu_count() or 1
+
+
+def _median_s(fn, warmup=2, reps=5):
+    import statistics
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def _log(msg):
+    print(f"cpu_baseline: {msg}", file=sys.stderr, flush=True)
+
+
 def cpu_baseline():
-    """Oracle (NumPy, reference CPU algorithm, fp32) on a row sample of the C2 step."""
+    """The reference's CPU algorithm (the NumPy oracle, fp32) timed on the host: per
+    config the median of 5 runs after 2 warm-ups (C5: 3 after 1), at the configured
+    shapes.  NumPy's elementwise ufuncs run on one thread, so row-, channel- and
+    head-independent work is split over a pool of host threads (ufuncs release the
+    GIL); BLAS calls use OPENBLAS/OMP_NUM_THREADS threads.  C4 runs in fp32 (NumPy has
+    no fast fp16 matmul): a thread-pool batch of heads is timed and scaled to the 128
+    heads.  C5 is one transformer layer forward + backward timed and scaled to the
+    step (4 layers), plus the head, loss, embedding and optimizer pieces."""
+    import concurrent.futures as cf
+
     import numpy as np
 
     import oracle as O
+    T = _cpu_threads()
+    pool = cf.ThreadPoolExecutor(T)
     rng = np.random.default_rng(0)
-    rows_ew, rows_rw = 512, 1024
-    x = rng.standard_normal((rows_ew, 8192)).astype(np.float32)
-    dy = rng.standard_normal((rows_ew, 8192)).astype(np.float32)
-    lg = (rng.standard_normal((rows_rw, 4096)) * 2).astype(np.float32)
-    y = O.softmax_fwd(lg)
-    dys = rng.standard_normal((rows_rw, 4096)).astype(np.float32)
-    xl = rng.standard_normal((rows_rw, 4096)).astype(np.float32)
+
+    def rows(fn, n, *arrs):
+        """fn over T row chunks of the arrays in the pool; returns the chunk results."""
+        cuts = np.linspace(0, n, T + 1).astype(int)
+        futs = [pool.submit(fn, *(a[c0:c1] for a in arrs)) for c0, c1 in zip(cuts[:-1], cuts[1:])
+                if c1 > c0]
+        return [f.result() for f in futs]
+
+    out = {"threads": T, "os_cpu_count": os.cpu_count()}
+    # ---- C2 at full shape
+    c2 = {}
+    x = rng.standard_normal((8192, 8192)).astype(np.float32)
+    dy = rng.standard_normal((8192, 8192)).astype(np.float32)
+    for name, fn in (("gelu_bwd", O.gelu_bwd), ("silu_bwd", O.silu_bwd)):
+        _log(f"C2 {name} [8192,8192]")
+        t = _median_s(lambda: rows(fn, 8192, x, dy))
+        c2[name] = {"ms": round(t * 1e3, 1), "GB/s": round(12 * x.size / t / 1e9, 2)}
+    del x, dy
+    lg = (rng.standard_normal((16384, 4096)) * 2).astype(np.float32)
+    y = np.concatenate(rows(O.softmax_fwd, 16384, lg))
+    del lg
+    dys = rng.standard_normal((16384, 4096)).astype(np.float32)
+    _log("C2 softmax_bwd [16384,4096]")
+    t = _median_s(lambda: rows(O.softmax_bwd, 16384, y, dys))
+    c2["softmax_bwd"] = {"ms": round(t * 1e3, 1), "GB/s": round(12 * y.size / t / 1e9, 2)}
+    del y
+    xl = rng.standard_normal((16384, 4096)).astype(np.float32)
     g = (1 + 0.02 * rng.standard_normal(4096)).astype(np.float32)
     b = (0.02 * rng.standard_normal(4096)).astype(np.float32)
-    _, xh, _, var = O.layernorm_fwd(xl, g, b)
-    dyl = rng.standard_normal((rows_rw, 4096)).astype(np.float32)
-    nbytes = 2 * 12 * x.size + 2 * 12 * y.size
-    t_end = time.perf_counter() + 10.0
-    t0 = time.perf_counter()
-    reps = 0
-    while True:
-        O.gelu_bwd(x, dy)
-        O.silu_bwd(x, dy)
-        O.softmax_bwd(y, dys)
-        O.layernorm_bwd(xh, var, g, dyl)
-        reps += 1
-        if time.perf_counter() > t_end and reps >= 2:
-            break
-    dt = time.perf_counter() - t0
-    return {"value": round(nbytes * reps / dt / 1e9, 3), "unit": "GB/s", "cores": 1,
-            "kind": "port",
-            "sample": (f"oracle (NumPy fp32) GELU+SiLU bwd on [{rows_ew},8192], softmax+LayerNorm "
-                       f"bwd on [{rows_rw},4096]; {reps} reps in {dt:.1f}s, single thread")}
+    parts = rows(lambda a: O.layernorm_fwd(a, g, b), 16384, xl)
+    xh = np.concatenate([p[1] for p in parts])
+    var = np.concatenate([p[3] for p in parts])
+    del parts, xl
+
+    def ln_bwd():
+        res = rows(lambda a, v, d: O.layernorm_bwd(a, v, g, d), 16384, xh, var, dys)
+        return sum(r[1] for r in res), sum(r[2] for r in res)  # dgamma, dbeta partials
+    _log("C2 layernorm_bwd [16384,4096]")
+    t = _median_s(ln_bwd)
+    c2["layernorm_bwd"] = {"ms": round(t * 1e3, 1), "GB/s": round(12 * xh.size / t / 1e9, 2)}
+    del xh, var, dys
+    step_s = sum(v["ms"] for v in c2.values()) / 1e3
+    out["C2"] = c2
+    value = 3221405696 / step_s / 1e9
+    # ---- C1: the README MLP step (forward, backward, Adam), BLAS threads
+    _log("C1 MLP step")
+    np.random.seed(0)
+    xm = np.random.randn(32, 784).astype(np.float32)
+    w1 = (np.random.randn(784, 256) * np.sqrt(2 / 784)).astype(np.float32)
+    w2 = (np.random.randn(256, 10) * np.sqrt(2 / 256)).astype(np.float32)
+    z1, z2 = np.zeros(256, np.float32), np.zeros(10, np.float32)
+    t = _median_s(lambda: O.mlp_step(xm, w1, z1, w2, z2, dtype=np.float32))
+    out["C1_mlp_step_ms"] = round(t * 1e3, 3)
+    # ---- C3: BatchNorm-ReLU backward NHWC, channels split over the pool
+    _log("C3 BN-ReLU bwd NHWC [64,56,56,256]")
+    xb = rng.standard_normal((64, 56, 56, 256)).astype(np.float32)
+    gb = (1 + 0.1 * rng.standard_normal(256)).astype(np.float32)
+    bb = (0.1 * rng.standard_normal(256)).astype(np.float32)
+    dyb = rng.standard_normal((64, 56, 56, 256)).astype(np.float32)
+    cuts = np.linspace(0, 256, T + 1).astype(int)
+    chunks = [(c0, c1) for c0, c1 in zip(cuts[:-1], cuts[1:]) if c1 > c0]
+    caches = [O.batchnorm_relu_fwd_nhwc(xb[..., c0:c1], gb[c0:c1], bb[c0:c1])[1]
+              for c0, c1 in chunks]
+    del xb
+
+    def bn_bwd():
+        fs = [pool.submit(O.batchnorm_relu_bwd_nhwc, dyb[..., c0:c1], gb[c0:c1], cc)
+              for (c0, c1), cc in zip(chunks, caches)]
+        return [f.result() for f in fs]
+    t = _median_s(bn_bwd)
+    out["C3_bn_relu_bwd"] = {"ms": round(t * 1e3, 1), "GB/s": round(20 * dyb.size / t / 1e9, 2)}
+    del caches, dyb
+    # ---- C4: FlashAttention bwd fp32, T heads at once, scaled to B*H = 128
+    c4 = {}
+    for d in (64, 128):
+        qh = [rng.standard_normal((1, 1, 2048, d)).astype(np.float32) for _ in range(4 * T)]
+        for causal in (False, True):
+            name = f"flash_bwd_d{d}{'_causal' if causal else ''}"
+            _log(f"C4 {name} fp32, {T} heads in parallel")
+
+            def heads():
+                fs = [pool.submit(O.flash_attention_bwd, *qh[4 * i:4 * i + 4], causal)
+                      for i in range(T)]
+                return [f.result() for f in fs]
+            t = _median_s(heads) * 128 / T
+            flops = 10 * 128 * 2048 * 2048 * d // (2 if causal else 1)
+            c4[name] = {"ms": round(t * 1e3, 1), "TFLOP/s": round(flops / t / 1e12, 4)}
+    out["C4_fp32_extrapolated"] = c4
+    # ---- C5: one layer forward + backward (scaled x4) + head, loss, embedding, AdamW
+    out["C5"] = _cpu_c5(O, np, pool, T, rows, rng)
+    pool.shutdown()
+    return {"value": round(value, 3), "unit": "GB/s", "cores": T, "kind": "port",
+            "sample": (f"NumPy oracle fp32 on {T} host threads (os.cpu_count() "
+                       f"{os.cpu_count()}): the C2 step at full shape (median of 5 after 2 "
+                       "warm-ups per op); other configs under 'configs'"),
+            "configs": out}
+
+
+def _cpu_c5(O, np, pool, T, rows, rng):
+    """C5 on the host: one pre-LN decoder layer at batch 8 x seq 1024, d 1024, 16 heads
+    (forward and backward with the oracle's formulas and NumPy matmuls), timed and
+    scaled to the 4 layers, plus the tied head (logits GEMM and its two gradient
+    GEMMs), cross-entropy forward + backward over [8192, 32000], the embedding
+    backward and the AdamW step over the 83.2 M parameters."""
+    N, C, H, hd, V = 8192, 1024, 16, 64, 32000
+
+    def w(*shape):
+        return (rng.standard_normal(shape) * 0.02).astype(np.float32)
+    h0 = rng.standard_normal((N, C)).astype(np.float32)
+    wq, wk, wv, wo, w1, w2 = w(C, C), w(C, C), w(C, C), w(C, C), w(C, 4 * C), w(4 * C, C)
+    g1 = np.ones(C, np.float32)
+    z = np.zeros(C, np.float32)
+
+    def attn_heads(fn, *arrs):
+        """fn per (batch, head) on (1, 1, 1024, 64) slices, over the pool."""
+        sl = [(b, hh) for b in range(8) for hh in range(H)]
+        split = [a.reshape(8, 1024, H, hd) for a in arrs]
+        fs = [pool.submit(fn, *(s[b, :, hh][None, None] for s in split)) for b, hh in sl]
+        return [f.result() for f in fs]
+
+    def layer():
+        a, xh1, _, var1 = O.layernorm_fwd(h0, g1, z)
+        q, k, v = a @ wq, a @ wk, a @ wv
+        outs = attn_heads(lambda qq, kk, vv: O.flash_attention_fwd(qq, kk, vv, True)[0], q, k, v)
+        o = np.stack([r[0, 0] for r in outs]).reshape(8, H, 1024, hd).transpose(0, 2, 1, 3)
+        o = np.ascontiguousarray(o).reshape(N, C)
+        h1 = h0 + o @ wo
+        m, xh2, _, var2 = O.layernorm_fwd(h1, g1, z)
+        f = m @ w1
+        gl = np.concatenate(rows(O.gelu_fwd, N, f))
+        dh = rng.standard_normal((N, C)).astype(np.float32) * 1e-3  # upstream gradient
+        # backward (the weight gradients are computed and dropped)
+        _ = gl.T @ dh                            # dW2
+        dgl = dh @ w2.T                          # gradient of the GELU output
+        df = np.concatenate(rows(O.gelu_bwd, N, f, dgl))
+        _ = m.T @ df
+        dm = df @ w1.T
+        dh1 = dh + np.concatenate([r[0] for r in rows(lambda x, vv, d: O.layernorm_bwd(
+            x, vv, g1, d), N, xh2, var2, dm)])
+        _ = o.T @ dh1
+        do = dh1 @ wo.T
+        grads = attn_heads(lambda qq, kk, vv, dd: O.flash_attention_bwd(qq, kk, vv, dd, True),
+                           q, k, v, do)
+        def merge(j):
+            t = np.stack([r[j][0, 0] for r in grads]).reshape(8, H, 1024, hd)
+            return np.ascontiguousarray(t.transpose(0, 2, 1, 3)).reshape(N, C)
+        dq, dk, dv = merge(0), merge(1), merge(2)
+        da = dq @ wq.T + dk @ wk.T + dv @ wv.T
+        _ = a.T @ dq, a.T @ dk, a.T @ dv
+        return np.concatenate([r[0] for r in rows(lambda x, vv, d: O.layernorm_bwd(
+            x, vv, g1, d), N, xh1, var1, da)])
+
+    _log("C5 one layer fwd+bwd (8 x 1024 tokens, d 1024, 16 heads)")
+    t_layer = _median_s(layer, warmup=1, reps=3)
+    hf = rng.standard_normal((N, C)).astype(np.float32)
+    E = w(V, C)
+    tg = rng.integers(0, V, N)
+
+    def head_loss():
+        logits = hf @ E.T
+        res = rows(lambda lg, tt: O.cross_entropy_bwd(O.cross_entropy_fwd(lg, tt)[1], tt), N,
+                   logits, tg)
+        dl = np.concatenate(res)
+        return dl @ E, dl.T @ hf
+    _log("C5 head GEMMs + cross-entropy [8192, 32000]")
+    t_head = _median_s(head_loss, warmup=1, reps=3)
+    _log("C5 embedding bwd + AdamW (83.2 M params)")
+    dout = rng.standard_normal((N, C)).astype(np.float32)
+    t_emb = _median_s(lambda: O.embedding_bwd(tg, dout, V), warmup=1, reps=3)
+    sizes = [83_200_000 // 48] * 48
+    ps = [rng.standard_normal(n).astype(np.float32) for n in sizes]
+    gs = [(rng.standard_normal(n) * 1e-3).astype(np.float32) for n in sizes]
+    ms = [np.zeros(n, np.float32) for n in sizes]
+
+    def adamw():
+        fs = [pool.submit(O.adam_step, p, gg, mm, mm, 1, 3e-4, (0.9, 0.999), 1e-8, 0.1)
+              for p, gg, mm in zip(ps, gs, ms)]
+        return [f.result() for f in fs]
+    t_adam = _median_s(adamw, warmup=1, reps=3)
+    step = 4 * t_layer + t_head + t_emb + t_adam
+    return {"layer_fwd_bwd_ms": round(t_layer * 1e3, 1), "head_and_loss_ms": round(t_head * 1e3, 1),
+            "embedding_bwd_ms": round(t_emb * 1e3, 1), "adamw_ms": round(t_adam * 1e3, 1),
+            "step_ms_estimate": round(step * 1e3, 1),
+            "note": "step = 4 x layer + head/loss + embedding + AdamW (extrapolated)"}
 
 
 CALIB_BYTES = 256 << 20
