@@ -15,10 +15,8 @@
 // no data movement, provided the other operand is read with the matching
 // permutation of k.  For a 32-row tile and k-step s (0,1) the lane's 8 elements are
 // its accumulator registers r = 8*s + e, i.e. rows 16*s + 8*(e/4) + 4*h + e%4.
-// That other operand is staged in LDS "8-row interleaved": within each 16-row block
-// the rows 4h+i and 8+4h+i (h = 0,1; i = 0..3) of column d sit next to each other,
-// il[((row/16)*2 + h)*D + d][8], so each lane fetches its 8 k-elements with one
-// 16-byte read.
+// That other operand is read from LDS in that row order with transpose reads
+// (ds_read_b64_tr_b16, see the backward tiles below).
 //
 // Forward: one workgroup = 128 queries (4 waves x 32), K/V tiles of 64 keys.
 //   S^T = K Q^T (lane = query), online softmax per lane, O^T += V^T P^T.
@@ -61,75 +59,12 @@ __device__ __forceinline__ typename Vec8<T>::type ld8(const T* p) {
   return *reinterpret_cast<const typename Vec8<T>::type*>(p);
 }
 
-// Column position of column d in an interleaved tile.  The low two bits are XORed
-// with bits 3-4, which spreads the stores of staging threads 8 columns apart over
-// the LDS banks; the swizzle depends on d mod 32 only, so a lane's 32-column reads
-// stay contiguous per 8 lanes and the per-lane base absorbs it.
-__device__ __forceinline__ int swz(int d) { return d ^ ((d >> 3) & 3); }
-
-// The 8 k-elements of MFMA k-step `blk` (= 16-row block * 2 + lane half) at column
-// position d (already swizzled) of an 8-row interleaved tile.
-template <typename T, int D>
-__device__ __forceinline__ typename Vec8<T>::type ld_il(const T* il, int blk, int d) {
-  return ld8(il + (blk * D + d) * 8);
-}
-
 template <typename T>
 __device__ __forceinline__ typename Vec8<T>::type pack8(const float* v) {
   typename Vec8<T>::type r;
 #pragma unroll
   for (int e = 0; e < 8; ++e) r[e] = (T)v[e];
   return r;
-}
-
-// Stage ROWS x D rows [row0, row0+ROWS) of a [nrows, D] matrix into LDS, row-major
-// (rm, row stride D+8) and/or 8-row interleaved (il).  Rows past nrows are zero.
-// A work unit is 8 rows (rows 16b + 4hh + i and 16b + 8 + 4hh + i) x 8 columns.
-// All 8 loads of a unit are issued before any is used: rows past the end read a
-// clamped (valid) row and are replaced by zero when stored, so no load sits behind
-// a branch (a branch per load would serialise them).
-template <typename T, int ROWS, int D, bool RM, bool IL>
-__device__ __forceinline__ void stage(const T* __restrict__ g, int64_t rs, int64_t row0,
-                                      int64_t nrows, T* rm, T* il) {
-  constexpr int DG = D / 8;
-  constexpr int UNITS = (ROWS / 16) * 2 * DG;
-  const bool full = row0 + ROWS <= nrows;  // uniform
-  for (int u = threadIdx.x; u < UNITS; u += kThreads) {
-    const int dg = u % DG, bh2 = u / DG;  // bh2 = 16-row block * 2 + hh
-    const int rb = bh2 >> 1, hh = bh2 & 1;
-    uint4 v[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int r = rb * 16 + (j >> 2) * 8 + hh * 4 + (j & 3);
-      int64_t row = row0 + r;
-      if (!full) row = row < nrows ? row : nrows - 1;
-      v[j] = *reinterpret_cast<const uint4*>(g + row * rs + dg * 8);
-    }
-    if (!full) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int r = rb * 16 + (j >> 2) * 8 + hh * 4 + (j & 3);
-        if (row0 + r >= nrows) v[j] = make_uint4(0, 0, 0, 0);
-      }
-    }
-    if (RM) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int r = rb * 16 + (j >> 2) * 8 + hh * 4 + (j & 3);
-        *reinterpret_cast<uint4*>(rm + r * (D + 8) + dg * 8) = v[j];
-      }
-    }
-    if (IL) {
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        T e8[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) e8[j] = reinterpret_cast<const T*>(&v[j])[c];
-        *reinterpret_cast<uint4*>(il + (bh2 * D + swz(dg * 8 + c)) * 8) =
-            *reinterpret_cast<const uint4*>(e8);
-      }
-    }
-  }
 }
 
 // Workgroup -> (tile, head) mapping.  Dispatch i lands on XCD i % 8.  The launch
@@ -165,117 +100,6 @@ struct FaLay {
 
 // Row index (within a 32-row C tile) of accumulator register r for lane half h.
 __device__ __forceinline__ int crow(int r, int h) { return ((r >> 2) << 3) + (h << 2) + (r & 3); }
-
-// ============================================================================ forward
-template <typename T, int D>
-__global__ __launch_bounds__(kThreads) void k_fa_fwd(const T* __restrict__ Q,
-                                                     const T* __restrict__ K,
-                                                     const T* __restrict__ V, T* __restrict__ O,
-                                                     float* __restrict__ LSE, int64_t Sq,
-                                                     int64_t Sk, float scale, int causal,
-                                                     FaLay lay) {
-  constexpr int BN = 128, DK = D / 16, DT = D / 32;
-  __shared__ __attribute__((aligned(16))) T Ks[BN * (D + 8)];
-  __shared__ __attribute__((aligned(16))) T Vi[BN * D];
-  int64_t tile, bh;
-  fa_block(tile, bh, lay.G);
-  Q += lay.head(bh, Sq, D);
-  K += lay.head(bh, Sk, D);
-  V += lay.head(bh, Sk, D);
-  O += lay.head(bh, Sq, D);
-  LSE += bh * Sq;
-  const int rs = lay.rs(D);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int h = lane >> 5, l32 = lane & 31;
-  // causal: the last query blocks carry the most keys, so they are dispatched first
-  const int64_t qb = causal ? (int64_t)gridDim.x - 1 - tile : tile;
-  const int64_t qblk = qb * 128;
-  const int64_t q = qblk + wave * 32 + l32;
-  const float sl2 = scale * kLog2e;
-
-  // A query lane past Sq reads a clamped row; its output row is never stored.
-  const int64_t qc = q < Sq ? q : Sq - 1;
-  typename Vec8<T>::type qf[DK];
-#pragma unroll
-  for (int ks = 0; ks < DK; ++ks) qf[ks] = ld8(Q + qc * rs + ks * 16 + h * 8);
-  f32x16 o[DT];
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
-  float m = -INFINITY, l = 0.f;
-
-  int64_t kend = Sk;
-  if (causal) kend = (qblk + 128 < Sk) ? qblk + 128 : Sk;
-  for (int64_t k0 = 0; k0 < kend; k0 += BN) {
-    __syncthreads();
-    stage<T, BN, D, true, false>(K, rs, k0, Sk, Ks, nullptr);
-    stage<T, BN, D, false, true>(V, rs, k0, Sk, nullptr, Vi);
-    __syncthreads();
-#pragma unroll 1
-    for (int kt = 0; kt < BN / 32; ++kt) {
-      f32x16 s;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[r] = 0.f;
-#pragma unroll
-      for (int ks = 0; ks < DK; ++ks)
-        s = mfma(ld8(Ks + (kt * 32 + l32) * (D + 8) + ks * 16 + h * 8), qf[ks], s);
-      // masks are only needed where the sub-tile crosses Sk or the causal diagonal
-      const bool edge = (k0 + kt * 32 + 32 > Sk) ||
-                        (causal && k0 + kt * 32 + 31 > qblk + wave * 32);
-      float mloc = -INFINITY;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float x = s[r] * sl2;
-        if (edge) {
-          const int64_t key = k0 + kt * 32 + crow(r, h);
-          if (key >= Sk || (causal && key > q)) x = -INFINITY;
-        }
-        s[r] = x;
-        mloc = fmaxf(mloc, x);
-      }
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-      const float mnew = fmaxf(m, mloc);
-      const float alpha = (mnew == -INFINITY) ? 1.f : fexp2(m - mnew);
-      float lsum = 0.f;
-      float p[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float e = (mnew == -INFINITY) ? 0.f : fexp2(s[r] - mnew);
-        p[r] = e;
-        lsum += e;
-      }
-      lsum += __shfl_xor(lsum, 32, 64);
-      l = l * alpha + lsum;
-      m = mnew;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
-#pragma unroll
-      for (int sg = 0; sg < 2; ++sg) {
-        const typename Vec8<T>::type pb = pack8<T>(&p[8 * sg]);
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-          o[dt] = mfma(ld_il<T, D>(Vi, (kt * 2 + sg) * 2 + h, dt * 32 + swz(l32)), pb, o[dt]);
-      }
-    }
-  }
-  if (q < Sq) {
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        T w[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) w[i] = (T)(o[dt][g * 4 + i] * inv);
-        *reinterpret_cast<uint2*>(O + q * rs + dt * 32 + g * 8 + h * 4) =
-            *reinterpret_cast<const uint2*>(w);
-      }
-    if (h == 0) LSE[q] = (m + log2f(l)) / kLog2e;
-  }
-}
 
 // ============================================================================ backward
 template <typename T>
@@ -433,10 +257,6 @@ struct LaneOffs {
 // Here sched_barrier fences fix the order: fragment reads run PF ahead of their
 // MFMAs, the exp of S is spread over the dP MFMAs, dS over the dV MFMAs, and the
 // transpose reads of each phase are issued during the previous one.
-#ifndef TG_FA_PIPE
-#define TG_FA_PIPE 1
-#endif
-constexpr bool kPipe = TG_FA_PIPE;
 #define TG_SB() __builtin_amdgcn_sched_barrier(0)
 template <typename T, int D, bool DIAG>
 __device__ __forceinline__ void dkdv_sub_pipe(const char* qs, const char* dos,
@@ -540,104 +360,15 @@ __device__ __forceinline__ void dkdv_sub_pipe(const char* qs, const char* dos,
   }
 }
 
-// One 32-query x 32-key sub-tile of the dK/dV kernel for one wave (lane = key).
-//   qs/dos: the sub-tile's first row in the Q / dO tiles; lse/dvs: its 32 log2-scaled
-//   LSE values (+inf past Sq, so P = 0 there) and scale*D values.
-//   DIAG: the sub-tile straddles the causal diagonal; key > query is masked, with
-//   mb = (first key of the wave's 32 + l32) - (first query of the sub-tile) - 4h,
-//   so that the mask for accumulator register r is mb > 8*(r/4) + r%4.
-// Keys past Sk (clamped rows of K/V) only feed dK/dV rows that are never stored.
-template <typename T, int D, int KG, bool DIAG>
-__device__ __forceinline__ void dkdv_sub(const char* qs, const char* dos, const float* lse,
-                                         const float* dvs, int h, const LaneOffs<D>& o,
-                                         const typename Vec8<T>::type (&kf)[KG][D / 16],
-                                         const typename Vec8<T>::type (&vf)[KG][D / 16],
-                                         f32x16 (&dk)[KG][D / 32], f32x16 (&dv)[KG][D / 32],
-                                         float sl2, float scale, int mb) {
-  constexpr int DK = D / 16, DT = D / 32, RB = D * 2;
-  f32x16 s[KG], dp[KG];
-#pragma unroll
-  for (int j = 0; j < KG; ++j)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      s[j][r] = 0.f;
-      dp[j][r] = 0.f;
-    }
-  // one LDS read of each Q / dO fragment feeds all KG key groups
-#pragma unroll
-  for (int ks = 0; ks < DK; ++ks) {
-    const auto qa = lds_a<T>(qs + o.a[ks]);
-#pragma unroll
-    for (int j = 0; j < KG; ++j) s[j] = mfma(qa, kf[j][ks], s[j]);
-  }
-#pragma unroll
-  for (int ks = 0; ks < DK; ++ks) {
-    const auto da = lds_a<T>(dos + o.a[ks]);
-#pragma unroll
-    for (int j = 0; j < KG; ++j) dp[j] = mfma(da, vf[j][ks], dp[j]);
-  }
-  float p[KG][16];
-#pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const float4 a = *reinterpret_cast<const float4*>(lse + 8 * g + 4 * h);
-    const float la[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-    for (int j = 0; j < KG; ++j)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float pv = fexp2(fmaf(s[j][4 * g + i], sl2, -la[i]));
-        if (DIAG) pv = (mb + 32 * j > 8 * g + i) ? 0.f : pv;
-        p[j][4 * g + i] = pv;
-      }
-  }
-#pragma unroll
-  for (int sg = 0; sg < 2; ++sg) {
-    typename Vec8<T>::type pa[KG];
-#pragma unroll
-    for (int j = 0; j < KG; ++j) pa[j] = pack8<T>(&p[j][8 * sg]);
-    const char* b = dos + sg * 16 * RB;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      const auto bt = lds_tr<T>(b + o.t[0][dt], b + o.t[1][dt]);
-#pragma unroll
-      for (int j = 0; j < KG; ++j) dv[j][dt] = mfma(pa[j], bt, dv[j][dt]);
-    }
-  }
-  float ds[KG][16];
-#pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const float4 b = *reinterpret_cast<const float4*>(dvs + 8 * g + 4 * h);
-    const float db[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-    for (int j = 0; j < KG; ++j)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        ds[j][4 * g + i] = p[j][4 * g + i] * fmaf(dp[j][4 * g + i], scale, -db[i]);
-  }
-#pragma unroll
-  for (int sg = 0; sg < 2; ++sg) {
-    typename Vec8<T>::type da[KG];
-#pragma unroll
-    for (int j = 0; j < KG; ++j) da[j] = pack8<T>(&ds[j][8 * sg]);
-    const char* b = qs + sg * 16 * RB;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      const auto bt = lds_tr<T>(b + o.t[0][dt], b + o.t[1][dt]);
-#pragma unroll
-      for (int j = 0; j < KG; ++j) dk[j][dt] = mfma(da[j], bt, dk[j][dt]);
-    }
-  }
-}
-
 // The BM/32 sub-tiles of one staged query tile; kq = first key of this wave minus the
-// tile's first query.  The wave's keys are kq .. kq + 32*KG - 1.
-template <typename T, int D, int BM, int KG>
+// tile's first query.  The wave's keys are kq .. kq + 31.
+template <typename T, int D, int BM>
 __device__ __forceinline__ void dkdv_tile(const char* qs, const char* dos, const float* lse,
                                           const float* dvs, int kq, int causal, int h, int l32,
                                           const LaneOffs<D>& o,
-                                          const typename Vec8<T>::type (&kf)[KG][D / 16],
-                                          const typename Vec8<T>::type (&vf)[KG][D / 16],
-                                          f32x16 (&dk)[KG][D / 32], f32x16 (&dv)[KG][D / 32],
+                                          const typename Vec8<T>::type (&kf)[D / 16],
+                                          const typename Vec8<T>::type (&vf)[D / 16],
+                                          f32x16 (&dk)[D / 32], f32x16 (&dv)[D / 32],
                                           float sl2, float scale) {
   constexpr int RB = D * 2;
 #pragma unroll
@@ -646,29 +377,20 @@ __device__ __forceinline__ void dkdv_tile(const char* qs, const char* dos, const
     if (causal && t * 32 + 31 < kq) continue;
     const char* q = qs + t * 32 * RB;
     const char* d = dos + t * 32 * RB;
-    if constexpr (KG == 1 && kPipe) {
-      if (causal && kq + 31 > t * 32)
-        dkdv_sub_pipe<T, D, true>(q, d, lse + t * 32, dvs + t * 32, h, o, kf[0], vf[0], dk[0],
-                                  dv[0], sl2, scale, kq + l32 - t * 32 - 4 * h);
-      else
-        dkdv_sub_pipe<T, D, false>(q, d, lse + t * 32, dvs + t * 32, h, o, kf[0], vf[0], dk[0],
-                                   dv[0], sl2, scale, 0);
-    } else {
-      if (causal && kq + 32 * KG - 1 > t * 32)
-        dkdv_sub<T, D, KG, true>(q, d, lse + t * 32, dvs + t * 32, h, o, kf, vf, dk, dv, sl2,
-                                 scale, kq + l32 - t * 32 - 4 * h);
-      else
-        dkdv_sub<T, D, KG, false>(q, d, lse + t * 32, dvs + t * 32, h, o, kf, vf, dk, dv, sl2,
-                                  scale, 0);
-    }
+    if (causal && kq + 31 > t * 32)
+      dkdv_sub_pipe<T, D, true>(q, d, lse + t * 32, dvs + t * 32, h, o, kf, vf, dk, dv, sl2,
+                                scale, kq + l32 - t * 32 - 4 * h);
+    else
+      dkdv_sub_pipe<T, D, false>(q, d, lse + t * 32, dvs + t * 32, h, o, kf, vf, dk, dv, sl2,
+                                 scale, 0);
   }
 }
 
-// dK, dV.  grid = (ceil(Sk/(128*KG)), B*H); one workgroup = 128*KG keys (4 waves x
-// 32*KG keys, K/V fragments in registers), looping over query tiles of BM rows double-buffered
+// dK, dV.  grid = (ceil(Sk/128), B*H); one workgroup = 128 keys (4 waves x 32 keys,
+// K/V fragments in registers), looping over query tiles of BM rows double-buffered
 // in LDS (stage buffers are separate arrays so the compiler can tell the tile being
 // read from the one being written by the DMA).
-template <typename T, int D, int BM, int KG, int OCC>
+template <typename T, int D, int BM, int OCC>
 __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dkdv(
     const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
     const T* __restrict__ dO, const float* __restrict__ LSE, const float* __restrict__ Dv,
@@ -693,32 +415,29 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dkdv(
   const int rs = lay.rs(D);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int h = lane >> 5, l32 = lane & 31;
-  const int64_t kblk = tile * (128 * KG);
-  const int64_t kw = kblk + wave * (32 * KG);  // first key of this wave
+  const int64_t kblk = tile * 128;
+  const int64_t kw = kblk + wave * 32;  // first key of this wave
   const float sl2 = scale * kLog2e;
-  // Lane l32 of key group j holds key kw + 32j + l32 (C-tile column).  A key past Sk
-  // reads a clamped row: it only feeds dK/dV rows of that key, which are never stored.
-  typename Vec8<T>::type kf[KG][DK], vf[KG][DK];
-#pragma unroll
-  for (int j = 0; j < KG; ++j) {
-    const int64_t key = kw + 32 * j + l32;
+  // Lane l32 holds key kw + l32 (C-tile column).  A key past Sk reads a clamped row:
+  // it only feeds dK/dV rows of that key, which are never stored.
+  typename Vec8<T>::type kf[DK], vf[DK];
+  {
+    const int64_t key = kw + l32;
     const int64_t kc = key < Sk ? key : Sk - 1;
 #pragma unroll
     for (int ks = 0; ks < DK; ++ks) {
-      kf[j][ks] = ld8(K + kc * rs + ks * 16 + h * 8);
-      vf[j][ks] = ld8(V + kc * rs + ks * 16 + h * 8);
+      kf[ks] = ld8(K + kc * rs + ks * 16 + h * 8);
+      vf[ks] = ld8(V + kc * rs + ks * 16 + h * 8);
     }
   }
-  f32x16 dk[KG][DT], dv[KG][DT];
+  f32x16 dk[DT], dv[DT];
 #pragma unroll
-  for (int j = 0; j < KG; ++j)
+  for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        dk[j][dt][r] = 0.f;
-        dv[j][dt][r] = 0.f;
-      }
+    for (int r = 0; r < 16; ++r) {
+      dk[dt][r] = 0.f;
+      dv[dt][r] = 0.f;
+    }
   LaneOffs<D> o;
   o.init(lane);
   DmaPlan<T, D, BM> plan;
@@ -761,8 +480,8 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dkdv(
       plan.copy(Q, q0 + BM, Sq, q1s);
       plan.copy(dO, q0 + BM, Sq, do1s);
     }
-    dkdv_tile<T, D, BM, KG>(q0s, do0s, lse0, dvs0, (int)(kw - q0), causal, h, l32, o, kf, vf,
-                            dk, dv, sl2, scale);
+    dkdv_tile<T, D, BM>(q0s, do0s, lse0, dvs0, (int)(kw - q0), causal, h, l32, o, kf, vf, dk,
+                        dv, sl2, scale);
     if (!more1) break;
     put(lse1, dvs1);
     // stage 1 holds tile q0 + BM
@@ -774,61 +493,25 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dkdv(
       plan.copy(Q, q0 + 2 * BM, Sq, q0s);
       plan.copy(dO, q0 + 2 * BM, Sq, do0s);
     }
-    dkdv_tile<T, D, BM, KG>(q1s, do1s, lse1, dvs1, (int)(kw - q0 - BM), causal, h, l32, o, kf,
-                            vf, dk, dv, sl2, scale);
+    dkdv_tile<T, D, BM>(q1s, do1s, lse1, dvs1, (int)(kw - q0 - BM), causal, h, l32, o, kf, vf,
+                        dk, dv, sl2, scale);
     if (!more2) break;
     put(lse0, dvs0);
   }
   // C tiles: rows = keys of this wave, cols = d
 #pragma unroll
-  for (int j = 0; j < KG; ++j)
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      store_c_tile<T>(dK, rs, kw + 32 * j, Sk, dt * 32 + l32, dk[j][dt], 1.f, accumulate, h);
-      store_c_tile<T>(dV, rs, kw + 32 * j, Sk, dt * 32 + l32, dv[j][dt], 1.f, accumulate, h);
-    }
+  for (int dt = 0; dt < DT; ++dt) {
+    store_c_tile<T>(dK, rs, kw, Sk, dt * 32 + l32, dk[dt], 1.f, accumulate, h);
+    store_c_tile<T>(dV, rs, kw, Sk, dt * 32 + l32, dv[dt], 1.f, accumulate, h);
+  }
 }
 
-// One 32-key x 32-query sub-tile of the dQ kernel for one wave (lane = query).
+// One 32-key x 32-query sub-tile of the dQ kernel for one wave (lane = query):
 //   ks/vs: the sub-tile's first row in the K / V tiles.
 //   MASK: keys are masked when 8*(r/4) + r%4 > thr for accumulator register r, where
 //   thr folds the causal limit (query of this lane - first key of the sub-tile - 4h)
 //   and the end of the keys (keys - first key of the sub-tile - 4h - 1).
-template <typename T, int D, bool MASK>
-__device__ __forceinline__ void dq_sub(const char* ks, const char* vs, const LaneOffs<D>& o,
-                                       const typename Vec8<T>::type (&qf)[D / 16],
-                                       const typename Vec8<T>::type (&of)[D / 16],
-                                       f32x16 (&acc)[D / 32], float sl2, float scale, float lq,
-                                       float dqs, int thr) {
-  constexpr int DK = D / 16, DT = D / 32, RB = D * 2;
-  f32x16 s, dp;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    s[r] = 0.f;
-    dp[r] = 0.f;
-  }
-#pragma unroll
-  for (int k = 0; k < DK; ++k) s = mfma(lds_a<T>(ks + o.a[k]), qf[k], s);
-#pragma unroll
-  for (int k = 0; k < DK; ++k) dp = mfma(lds_a<T>(vs + o.a[k]), of[k], dp);
-  float ds[16];
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    float pv = fexp2(fmaf(s[r], sl2, -lq));
-    if (MASK) pv = (8 * (r >> 2) + (r & 3) > thr) ? 0.f : pv;
-    ds[r] = pv * fmaf(dp[r], scale, -dqs);
-  }
-#pragma unroll
-  for (int sg = 0; sg < 2; ++sg) {
-    const typename Vec8<T>::type da = pack8<T>(&ds[8 * sg]);
-    const char* b = ks + sg * 16 * RB;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-      acc[dt] = mfma(da, lds_tr<T>(b + o.t[0][dt], b + o.t[1][dt]), acc[dt]);
-  }
-}
-
-// Hand-ordered dq_sub (same scheme as dkdv_sub_pipe): K then V fragment reads run PF
+// Hand-ordered (same scheme as dkdv_sub_pipe): K then V fragment reads run PF
 // ahead of their MFMAs, exp(S) is spread over the dP MFMAs, the dS of the second half
 // is computed behind the first half's dQ MFMAs, and K^T transpose reads are issued
 // during the dP phase.
@@ -935,11 +618,9 @@ __device__ __forceinline__ void dq_tile(const char* ks, const char* vs, int64_t 
         const int kb = (int)(Sk - kb0) - 4 * h - 1;
         thr = kb < thr ? kb : thr;
       }
-      if constexpr (kPipe) dq_sub_pipe<T, D, true>(k, v, o, qf, of, acc, sl2, scale, lq, dqs, thr);
-      else dq_sub<T, D, true>(k, v, o, qf, of, acc, sl2, scale, lq, dqs, thr);
+      dq_sub_pipe<T, D, true>(k, v, o, qf, of, acc, sl2, scale, lq, dqs, thr);
     } else {
-      if constexpr (kPipe) dq_sub_pipe<T, D, false>(k, v, o, qf, of, acc, sl2, scale, lq, dqs, 0);
-      else dq_sub<T, D, false>(k, v, o, qf, of, acc, sl2, scale, lq, dqs, 0);
+      dq_sub_pipe<T, D, false>(k, v, o, qf, of, acc, sl2, scale, lq, dqs, 0);
     }
   }
 }
@@ -1226,20 +907,13 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_fwd2(
 template <int D> struct FwdCfg;
 template <> struct FwdCfg<64> { static constexpr int BN = 64, OCC = 3; };
 template <> struct FwdCfg<128> { static constexpr int BN = 64, OCC = 2; };
-#ifndef TG_FA_FWD2
-#define TG_FA_FWD2 1
-#endif
 
 template <typename T, int D>
 int fwd_t(const void* q, const void* k, const void* v, void* o, float* lse, int64_t BH,
           int64_t Sq, int64_t Sk, float scale, int causal, FaLay lay, hipStream_t s) {
   dim3 grid((unsigned)((Sq + 127) / 128), (unsigned)BH);
-  if (TG_FA_FWD2)
-    k_fa_fwd2<T, D, FwdCfg<D>::BN, FwdCfg<D>::OCC><<<grid, kThreads, 0, s>>>(
-        (const T*)q, (const T*)k, (const T*)v, (T*)o, lse, Sq, Sk, scale, causal, lay);
-  else
-    k_fa_fwd<T, D><<<grid, kThreads, 0, s>>>((const T*)q, (const T*)k, (const T*)v, (T*)o, lse,
-                                             Sq, Sk, scale, causal, lay);
+  k_fa_fwd2<T, D, FwdCfg<D>::BN, FwdCfg<D>::OCC><<<grid, kThreads, 0, s>>>(
+      (const T*)q, (const T*)k, (const T*)v, (T*)o, lse, Sq, Sk, scale, causal, lay);
   return tg_check_launch("tg_flash_attn_fwd");
 }
 
@@ -1247,10 +921,10 @@ int fwd_t(const void* q, const void* k, const void* v, void* o, float* lse, int6
 // key rows of the dQ kernel, and the workgroups per CU each is compiled for.
 template <int D> struct BwdCfg;
 template <> struct BwdCfg<64> {
-  static constexpr int BM = 128, KG = 1, OCC_KV = 2, BN = 64, OCC_Q = 3;
+  static constexpr int BM = 128, OCC_KV = 2, BN = 64, OCC_Q = 3;
 };
 template <> struct BwdCfg<128> {
-  static constexpr int BM = 128, KG = 1, OCC_KV = 1, BN = 64, OCC_Q = 2;
+  static constexpr int BM = 128, OCC_KV = 1, BN = 64, OCC_Q = 2;
 };
 
 template <typename T, int D>
@@ -1263,8 +937,8 @@ int bwd_t(const void* q, const void* k, const void* v, const void* o, const void
   k_fa_bwd_dq<T, D, C::BN, C::OCC_Q><<<gq, kThreads, 0, s>>>((const T*)q, (const T*)k, (const T*)v,
                                             (const T*)o, (const T*)dout, lse, dvec, (T*)dq, Sq,
                                             Sk, scale, causal, acc, lay);
-  dim3 gkv((unsigned)((Sk + 128 * C::KG - 1) / (128 * C::KG)), (unsigned)BH);
-  k_fa_bwd_dkdv<T, D, C::BM, C::KG, C::OCC_KV><<<gkv, kThreads, 0, s>>>((const T*)q, (const T*)k, (const T*)v,
+  dim3 gkv((unsigned)((Sk + 127) / 128), (unsigned)BH);
+  k_fa_bwd_dkdv<T, D, C::BM, C::OCC_KV><<<gkv, kThreads, 0, s>>>((const T*)q, (const T*)k, (const T*)v,
                                                (const T*)dout, lse, dvec, (T*)dk, (T*)dv, Sq, Sk,
                                                scale, causal, acc, lay);
   return tg_check_launch("tg_flash_attn_bwd");

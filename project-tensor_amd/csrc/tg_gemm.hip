@@ -453,25 +453,10 @@ typedef short v4i16_g __attribute__((ext_vector_type(4)));
 #define TG_GLB_G __attribute__((address_space(1)))
 
 constexpr int V3_BK = 64;
-#ifndef TG_GEMM_HUGE
-#define TG_GEMM_HUGE 4
-#endif
-#ifndef TG_GEMM_BIG4
-#define TG_GEMM_BIG4 0
-#endif
-#ifndef TG_GEMM_PIPE
-#define TG_GEMM_PIPE 1
-#endif
-constexpr bool kGemmPipe = TG_GEMM_PIPE;
-#ifndef TG_GEMM_LDS_EPI
-#define TG_GEMM_LDS_EPI 1
-#endif
-constexpr bool kGemmLdsEpi = TG_GEMM_LDS_EPI;
 // 256x256 blocks once there are kHugeTiles/4 of them per CU.
-constexpr int kHugeTiles = TG_GEMM_HUGE;
-// 256x128 blocks: 2x2 waves of 128x64 (TG_GEMM_BIG4) or 4x2 waves of 64x64.
-constexpr int kBigWGM = TG_GEMM_BIG4 ? 2 : 4, kBigWGN = 2, kBigSM = TG_GEMM_BIG4 ? 4 : 2,
-              kBigSN = 2;
+constexpr int kHugeTiles = 4;
+// 256x128 blocks: 4x2 waves of 64x64.
+constexpr int kBigWGM = 4, kBigWGN = 2, kBigSM = 2, kBigSN = 2;
 
 // XOR key of row r (CH 16-byte chunks per row): 16 consecutive rows get distinct
 // chunk positions and rows r..r+3 of a transpose read land in different 64-byte bank
@@ -634,7 +619,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_v3(
     db.copy(b_org, (uint32_t)((BKC ? k0 : k0 * ldb) * (int64_t)sizeof(T)), bs);
   };
   auto mul = [&](const char* as, const char* bs) {
-    if constexpr (OCC == 1 && kGemmPipe) {
+    if constexpr (OCC == 1) {
       // One wave per SIMD: software pipeline.  The fragment reads of k-step ks+1 are
       // issued between the MFMAs of k-step ks (sched_barrier keeps the order), so only
       // the first k-step of a tile waits on LDS latency.
@@ -696,7 +681,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_v3(
     mul(a1, b1);
     if (!more2) break;
   }
-  if (m0 + TBM <= M && n0 + TBN <= N && kGemmLdsEpi) {
+  if (m0 + TBM <= M && n0 + TBN <= N) {
     // Full tile: each wave stages one slab of HR rows (32, or 16 when two 32-row
     // slabs per stage array do not fit) of its C tile at a time in its own LDS region
     // (the operand stages are free once every wave has passed the barrier) and writes

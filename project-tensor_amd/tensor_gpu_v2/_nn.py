@@ -456,17 +456,20 @@ class CrossEntropyLoss(Module):
         if ld.dim() != 2:
             raise ValueError(f"CrossEntropyLoss expects logits [N, C], got {tuple(ld.shape)}")
         N, C = ld.shape
-        if isinstance(targets, Tensor):
-            tg = targets.data
-        elif isinstance(targets, torch.Tensor):
-            tg = targets
+        on_device = isinstance(targets, (Tensor, torch.Tensor))
+        if on_device:
+            tg = targets.data if isinstance(targets, Tensor) else targets
+            tg = tg.to(device=ld.device, dtype=torch.int64).reshape(-1).contiguous()
+            # negative targets wrap as in the reference; targets outside [-C, C) are
+            # not checked on the device (that would need a device-to-host read)
+            tg = torch.where(tg < 0, tg + C, tg)
         else:
-            host = np.asarray(targets)
-            # the reference indexes probs[arange(N), targets]: out-of-range targets raise
-            if host.size and (host.min() < 0 or host.max() >= C):
-                raise IndexError(f"CrossEntropyLoss: target outside [0, {C})")
-            tg = L.to_device(host.astype(np.int64, copy=False), ld.device)
-        tg = tg.to(device=ld.device, dtype=torch.int64).reshape(-1).contiguous()
+            host = np.asarray(targets).astype(np.int64, copy=False).reshape(-1)
+            # the reference indexes probs[arange(N), targets] (NumPy / CuPy indexing):
+            # targets in [-C, 0) wrap, anything outside [-C, C) raises
+            if host.size and (host.min() < -C or host.max() >= C):
+                raise IndexError(f"CrossEntropyLoss: target outside [-{C}, {C})")
+            tg = L.to_device(np.where(host < 0, host + C, host), ld.device)
         if tg.numel() != N:
             raise ValueError(f"CrossEntropyLoss: {tg.numel()} targets for {N} rows")
         ldc = ld.contiguous()
@@ -527,6 +530,23 @@ class SGD:
         for p in self.params:
             if p._has_grad():
                 p.zero_grad()
+
+    def state_dict(self):
+        """Hyper-parameters and momentum velocities, the reference's keys
+        (_nn.py:1356-1364)."""
+        return {"lr": self.lr, "momentum": self.momentum, "weight_decay": self.weight_decay,
+                "nesterov": self.nesterov, "velocities": [v.cpu().numpy() for v in self.velocities]}
+
+    def load_state_dict(self, state):
+        """(_nn.py:1366-1374): missing keys keep the current values; velocities load as
+        fp32."""
+        self.lr = state.get("lr", self.lr)
+        self.momentum = state.get("momentum", self.momentum)
+        self.weight_decay = state.get("weight_decay", self.weight_decay)
+        self.nesterov = state.get("nesterov", self.nesterov)
+        if "velocities" in state:
+            self.velocities = [torch.as_tensor(np.asarray(v, dtype=np.float32), device="cuda")
+                               for v in state["velocities"]]
 
 
 class Adam:
