@@ -338,6 +338,29 @@ def _op_embedding(torch, L, g):
     return Timed("embedding_bwd", run, work, "GB/s", HBM_PEAK_GBS)
 
 
+def _op_ln_c5(torch, L, g):
+    """C5 LayerNorm backward: fp16 [8192, 1024] (one of the step's nine), dx accumulated
+    into the residual gradient as in the pre-LN block.  Algorithmic bytes: read x, dy
+    and the old dx, write dx (8 B per element), plus the fp32 row statistics."""
+    R, C = 8192, 1024
+    x = torch.randn(R, C, device="cuda", generator=g).half()
+    gam = 1 + 0.02 * torch.randn(C, device="cuda", generator=g)
+    bet = 0.02 * torch.randn(C, device="cuda", generator=g)
+    _, mean, rstd = L.layernorm_fwd(x, gam, bet, 1e-5)
+    dy = torch.randn(R, C, device="cuda", generator=g).half()
+    dx = torch.randn(R, C, device="cuda", generator=g).half()
+    dg, db = torch.empty_like(gam), torch.empty_like(bet)
+    lib, s, p = L.load(), L.stream_handle, L.ptr
+    ws = L.workspace(lib.tg_layernorm_bwd_workspace(1, R, C), "cuda")
+    for t in (x, dy, dx):
+        _need(t, R * C, "ln c5")
+
+    def run():  # the raw entry point with a prepared workspace (a ~20 us op)
+        L._check("ln", lib.tg_layernorm_bwd(1, p(x), p(mean), p(rstd), p(gam), p(dy), p(dx),
+                                            p(dg), p(db), R, C, 1, 0, p(ws), ws.numel(), s()))
+    return Timed("layernorm_bwd_c5_fp16", run, 8 * R * C + 8 * R, "GB/s", HBM_PEAK_GBS)
+
+
 def _op_tied(torch, L, g):
     """C5 tied-weight transfer: embedding.grad [32000, 1024] += head.grad.T, fp32.
     Algorithmic bytes: read both, write the source gradient (3 x 131 MB)."""
@@ -360,6 +383,7 @@ def component_ops(torch, L, only):
                 ("gemm_fc1_bwd", lambda: _op_gemm(torch, L, g)),
                 ("cross_entropy_fwd_bwd", lambda: _op_ce(torch, L, g)),
                 ("embedding_bwd", lambda: _op_embedding(torch, L, g)),
+                ("layernorm_bwd_c5_fp16", lambda: _op_ln_c5(torch, L, g)),
                 ("tied_grad_sync", lambda: _op_tied(torch, L, g)),
                 ("gpt_step", lambda: _op_gpt(torch, L, g))]
     for d in (64, 128):

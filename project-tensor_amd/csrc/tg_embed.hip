@@ -1,7 +1,10 @@
 // Embedding backward and the tied-weight gradient transfer.
 //
 // tg_embedding_bwd: grad[idx[i]] (+)= dout[i] (Embedding._backward, _nn.py:1083-1089,
-// a scatter-add).  Deterministic: the tokens are sorted by (index, position) -- 64-bit
+// a scatter-add), deterministic, in the order np.add.at applies the tokens.  Up to 8192
+// tokens: one launch of k_embed_band (each workgroup finds the tokens of its band of
+// gradient rows and writes every row once).  More tokens: the tokens are sorted by
+// (index, position) -- 64-bit
 // keys index << 32 | position, all distinct -- with a radix sort of 8192-key chunks in
 // LDS (stable, so equal indices keep their token order) and, for more tokens, merge
 // passes of the sorted chunks.  One wavefront per run of equal indices then sums the
@@ -235,6 +238,142 @@ __global__ __launch_bounds__(kBlock) void k_embed_seg(const K* __restrict__ sort
   }
 }
 
+// Up to kChunk tokens, one launch, no sort and no workspace: workgroup b owns the
+// gradient rows [b*kBandRows, (b+1)*kBandRows) and writes each of them exactly once.
+// Phase 1: wave w scans tokens [w*seg, (w+1)*seg) of the indices and keeps the ones
+// that fall in the band in LDS, in token order (ballot compaction), as
+// (row in band) << 16 | token.  The four wave lists read in wave order are therefore
+// the band's tokens in token order.  Phase 2: wave w takes band rows w, w+4, ...; for
+// each column chunk it walks the lists, and for every token of its row adds the dout
+// row in token order (the order np.add.at applies them), then writes grad (+)= sum, or
+// zeros for a row no token touches (nothing, when accumulating).
+constexpr int kBandRows = 64;
+constexpr int kBandThreads = 512;
+
+template <typename TD, typename TG, bool VEC, bool VG>
+__global__ __launch_bounds__(kBandThreads) void k_embed_band(const int64_t* __restrict__ idx, int n,
+                                                       const TD* __restrict__ dout, int64_t dim,
+                                                       int64_t V, int accumulate,
+                                                       TG* __restrict__ grad) {
+  constexpr int PER = VEC ? 16 / (int)sizeof(TD) : 4;
+  constexpr int NW = kBandThreads / 64;
+  __shared__ uint32_t list[kChunk];
+  __shared__ int cnt[NW];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t r0 = (int64_t)blockIdx.x * kBandRows;
+  const int seg = (n + NW - 1) / NW;
+  const int t0 = wave * seg, t1 = min(n, t0 + seg);
+  uint32_t* wl = list + t0;
+  const uint64_t below = (1ull << lane) - 1;
+  // all of the wave's indices are loaded at once (seg <= kChunk / NW = 64 * KPL), so
+  // the scan costs one memory round trip
+  constexpr int KPL = kChunk / NW / 64;
+  int64_t k[KPL];
+#pragma unroll
+  for (int u = 0; u < KPL; ++u) {
+    const int i = t0 + u * 64 + lane;
+    k[u] = i < t1 ? idx[i] : -1;
+  }
+  int c = 0;
+#pragma unroll
+  for (int u = 0; u < KPL; ++u) {
+    const bool hit = k[u] >= r0 && k[u] < r0 + kBandRows && k[u] < V;
+    const uint64_t m = __ballot(hit);
+    if (hit) wl[c + __popcll(m & below)] = (uint32_t)(k[u] - r0) << 16 | (uint32_t)(u * 64 + lane);
+    c += __popcll(m);
+  }
+  if (lane == 0) cnt[wave] = c;
+  __syncthreads();
+  int wc[NW];
+#pragma unroll
+  for (int w = 0; w < NW; ++w) wc[w] = cnt[w];
+  auto col = [&](int64_t c0, int e) {
+    return VEC ? c0 + (int64_t)lane * PER + e : c0 + (int64_t)e * 64 + lane;
+  };
+  for (int rl = wave; rl < kBandRows; rl += NW) {
+    const int64_t row = r0 + rl;
+    if (row >= V) break;
+    bool any = false;
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+      for (int b = 0; b < wc[w] && !any; b += 64)
+        any = __ballot(b + lane < wc[w] && (int)(list[w * seg + b + lane] >> 16) == rl) != 0;
+    if (!any && accumulate) continue;
+    TG* grow = grad + row * dim;
+    // NCH column chunks of 64 * PER per pass: a token's loads for all of them are in
+    // flight together
+    constexpr int NCH = 4;
+    for (int64_t c0 = 0; c0 < dim; c0 += NCH * 64 * PER) {
+      float acc[NCH][PER];
+#pragma unroll
+      for (int q = 0; q < NCH; ++q)
+#pragma unroll
+        for (int e = 0; e < PER; ++e) acc[q][e] = 0.f;
+      auto add = [&](int tok) {
+        const TD* drow = dout + (int64_t)tok * dim;
+        if (VEC) {
+          tg_vec16<TD> t[NCH];
+#pragma unroll
+          for (int q = 0; q < NCH; ++q)
+            if (col(c0 + q * 64 * PER, 0) < dim) t[q] = tg_load16(drow + col(c0 + q * 64 * PER, 0));
+#pragma unroll
+          for (int q = 0; q < NCH; ++q)
+            if (col(c0 + q * 64 * PER, 0) < dim)
+#pragma unroll
+              for (int e = 0; e < PER; ++e) acc[q][e] += tg_to_float(t[q].v[e]);
+        } else {
+#pragma unroll
+          for (int q = 0; q < NCH; ++q)
+#pragma unroll
+            for (int e = 0; e < PER; ++e) {
+              const int64_t cc = col(c0 + q * 64 * PER, e);
+              if (cc < dim) acc[q][e] += tg_to_float(drow[cc]);
+            }
+        }
+      };
+      if (any) {
+#pragma unroll
+        for (int w = 0; w < NW; ++w)
+          for (int b = 0; b < wc[w]; b += 64) {
+            const uint32_t e = b + lane < wc[w] ? list[w * seg + b + lane] : 0xffffffffu;
+            uint64_t m = __ballot((int)(e >> 16) == rl);
+            while (m) {  // tokens of this row in token order
+              const int j = __builtin_ctzll(m);
+              m &= m - 1;
+              add(w * seg + (int)(__shfl(e, j, 64) & 0xffffu));
+            }
+          }
+      }
+#pragma unroll
+      for (int q = 0; q < NCH; ++q) {
+        const int64_t cq = c0 + q * 64 * PER;
+        if (VG && col(cq, 0) < dim) {
+          constexpr int NG = tg_vec16<TG>::N;
+#pragma unroll
+          for (int h = 0; h < PER / NG; ++h) {
+            TG* p = grow + col(cq, h * NG);
+            tg_vec16<TG> o;
+            if (accumulate) o = tg_load16(p);
+#pragma unroll
+            for (int e = 0; e < NG; ++e)
+              o.v[e] = tg_from_float<TG>((accumulate ? tg_to_float(o.v[e]) : 0.f) +
+                                         acc[q][h * NG + e]);
+            tg_store16(p, o);
+          }
+        } else if (!VG) {
+#pragma unroll
+          for (int e = 0; e < PER; ++e) {
+            const int64_t cc = col(cq, e);
+            if (cc < dim)
+              grow[cc] =
+                  tg_from_float<TG>((accumulate ? tg_to_float(grow[cc]) : 0.f) + acc[q][e]);
+          }
+        }
+      }
+    }
+  }
+}
+
 template <typename TS, typename TD>
 __global__ __launch_bounds__(kBlock) void k_transpose_add(const TS* __restrict__ src, int64_t R,
                                                           int64_t C, TD* __restrict__ dst,
@@ -352,7 +491,8 @@ size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 // Workspace: two n-key buffers of 64-bit keys (the sorted keys and the merge passes'
 // partner); 32-bit keys use the front of each.
-size_t embed_ws(int64_t n) { return 2 * align256(n * sizeof(uint64_t)); }
+// (none up to kChunk tokens: the band kernel needs no scratch)
+size_t embed_ws(int64_t n) { return n <= kChunk ? 0 : 2 * align256(n * sizeof(uint64_t)); }
 
 int bits_for(int64_t v) {  // bits holding 0..v
   int b = 1;
@@ -363,6 +503,22 @@ int bits_for(int64_t v) {  // bits holding 0..v
 template <typename K, typename TD, typename TG>
 int embed_k(const void* dout, const int64_t* idx, int64_t n, int64_t dim, void* grad, int64_t V,
             int accumulate, char* ws, int pb, hipStream_t s) {
+  constexpr int PER = 16 / (int)sizeof(TD);
+  const bool vec = dim % PER == 0 && tg_aligned16(dout);
+  const bool vg = vec && (PER * sizeof(TG)) % 16 == 0 && (dim * sizeof(TG)) % 16 == 0 &&
+                  tg_aligned16(grad);
+  if (n <= kChunk) {
+    if (n == 0 && accumulate) return TG_OK;
+    const unsigned nb = (unsigned)((V + kBandRows - 1) / kBandRows);
+#define BAND(VE, VGE)                                                                         \
+  k_embed_band<TD, TG, VE, VGE><<<nb, kBandThreads, 0, s>>>(idx, (int)n, (const TD*)dout, dim, V, \
+                                                      accumulate, (TG*)grad)
+    if (vg) BAND(true, true);
+    else if (vec) BAND(true, false);
+    else BAND(false, false);
+#undef BAND
+    return tg_check_launch("tg_embedding_bwd");
+  }
   const int64_t total = V * dim;
   int64_t fill_blocks = (total + 8 * kSortThreads - 1) / (8 * kSortThreads);
   if (fill_blocks > (int64_t)tg_num_cus() * 2) fill_blocks = (int64_t)tg_num_cus() * 2;
@@ -387,10 +543,6 @@ int embed_k(const void* dout, const int64_t* idx, int64_t n, int64_t dim, void* 
   int cur = 0;
   for (int64_t w = kChunk; w < n; w *= 2, cur ^= 1)
     k_embed_merge<K><<<(unsigned)((n + 255) / 256), 256, 0, s>>>(buf[cur], n, w, buf[cur ^ 1]);
-  constexpr int PER = 16 / (int)sizeof(TD);
-  const bool vec = dim % PER == 0 && tg_aligned16(dout);
-  const bool vg = vec && (PER * sizeof(TG)) % 16 == 0 && (dim * sizeof(TG)) % 16 == 0 &&
-                  tg_aligned16(grad);
   const unsigned sb = (unsigned)((n + 3) / 4);
 #define SEG(VE, VGE)                                                                        \
   k_embed_seg<K, TD, TG, VE, VGE><<<sb, kBlock, 0, s>>>(buf[cur], pb, n, (const TD*)dout, dim, \
@@ -427,7 +579,7 @@ TG_EXPORT int tg_embedding_bwd(int dtype_dout, const void* dout, const int64_t* 
   TG_REQUIRE(n_tokens <= 0x7fffffff, "tg_embedding_bwd: too many tokens");
   TG_REQUIRE(grad && (n_tokens == 0 || (dout && indices)), "tg_embedding_bwd: null pointer");
   const size_t need = tg_embedding_bwd_workspace(n_tokens, num_embeddings);
-  if (n_tokens > 0 && (!workspace || workspace_bytes < need)) {
+  if (need > 0 && (!workspace || workspace_bytes < need)) {
     tg_set_error("tg_embedding_bwd: workspace of %zu bytes needed, got %zu", need,
                  workspace ? workspace_bytes : (size_t)0);
     return TG_ERR_WORKSPACE;

@@ -22,8 +22,9 @@
 //   S^T = K Q^T (lane = query), online softmax per lane, O^T += V^T P^T.
 // Backward (no atomics, two kernels):
 //   k_fa_bwd_dkdv: one workgroup = 128 keys (4 waves x 32 keys), loop over query
-//     tiles of 64: S = Q K^T (lane = key), P = exp(S*scale - lse), dP = dO V^T,
-//     dS = P*(dP - D)*scale, dV += P^T dO, dK += dS^T Q.
+//     tiles of 128: S = Q K^T (lane = key), P = exp(S*scale - lse), dP = dO V^T,
+//     dS = P*(dP - D)*scale, dV += P^T dO, dK += dS^T Q (the factor scale is applied
+//     to dK once, when it is stored).
 //   k_fa_bwd_dq: one workgroup = 128 queries, loop over key tiles of 64:
 //     S^T = K Q^T (lane = query), dP^T = V dO^T, dQ += dS K.
 //   D = rowsum(dO * O) is formed by k_fa_bwd_dq (launched first) for its queries and
@@ -102,28 +103,47 @@ struct FaLay {
 __device__ __forceinline__ int crow(int r, int h) { return ((r >> 2) << 3) + (h << 2) + (r & 3); }
 
 // ============================================================================ backward
-template <typename T>
-__device__ __forceinline__ void store_c_tile(T* __restrict__ out, int64_t ld, int64_t row0,
-                                             int64_t nrows, int col, const f32x16& acc, float mul,
-                                             bool accumulate, int h) {
-  if (row0 + 32 <= nrows) {  // uniform: every row exists, all loads in flight together
-    float prev[16];
+// Store of a wave's 32 x D accumulator tiles (rows row0.., C layout) through a wave-
+// private LDS region st of 32 x D floats: each lane writes its column's 16 values, then
+// reads back 8 consecutive values of one row and writes them with one 16-byte global
+// store (plus one 16-byte load of the old values when accumulating), so every store
+// instruction covers whole rows.  (Written straight from the C layout, the tiles need
+// 16 two-byte stores per lane and tile, each covering two 64-byte row pieces: measured
+// at about a quarter of the dK/dV kernel's time at d = 128.)  Columns of the rows with
+// bit 2 set (lane half 1) are XOR-ed with 32 so the two lane halves write different
+// banks.  out (+)= acc * mul, in fp32, then rounded to T.
+template <typename T, int D>
+__device__ __forceinline__ void store_tiles_staged(T* __restrict__ out, int64_t ld, int64_t row0,
+                                                   int64_t nrows, const f32x16 (&acc)[D / 32],
+                                                   float mul, int accumulate, int lane,
+                                                   float* st) {
+  const int h = lane >> 5, l32 = lane & 31;
+#pragma unroll
+  for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
     for (int r = 0; r < 16; ++r)
-      prev[r] = accumulate ? (float)out[(row0 + crow(r, h)) * ld + col] : 0.f;
+      st[crow(r, h) * D + ((dt * 32 + l32) ^ (h << 5))] = acc[dt][r] * mul;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  constexpr int LPR = D / 8, RPI = 64 / LPR;  // lanes per row, rows per pass
+  const int c = (lane % LPR) * 8;
 #pragma unroll
-    for (int r = 0; r < 16; ++r)
-      out[(row0 + crow(r, h)) * ld + col] = (T)(acc[r] * mul + prev[r]);
-    return;
-  }
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int64_t row = row0 + crow(r, h);
+  for (int it = 0; it < 32 / RPI; ++it) {
+    const int rr = it * RPI + lane / LPR;
+    const float* src = st + rr * D + (c ^ (rr & 4 ? 32 : 0));
+    const float4 a = *reinterpret_cast<const float4*>(src);
+    const float4 b = *reinterpret_cast<const float4*>(src + 4);
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    const int64_t row = row0 + rr;
     if (row < nrows) {
-      T* p = out + row * ld + col;
-      float v = acc[r] * mul;
-      if (accumulate) v += (float)*p;
-      *p = (T)v;
+      T* p = out + row * ld + c;
+      tg_vec16<T> o;
+      if (accumulate) o = tg_load16(p);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        o.v[e] = (T)(v[e] + (accumulate ? (float)o.v[e] : 0.f));
+      tg_store16(p, o);
     }
   }
 }
@@ -188,16 +208,20 @@ struct DmaPlan {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (TG_LDS void*)l, 16, o, 0, 0, 0);
 #endif
   }
+  // copy() issues this wave's instructions k0 <= k < k1 (all by default), so a caller
+  // can spread a tile's copy over its compute.
   __device__ __forceinline__ void copy(const T* __restrict__ g, int64_t row0, int64_t nrows,
-                                       char* lds) const {
+                                       char* lds, int k0 = 0, int k1 = NPW) const {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const T* base = g + row0 * rs;
     if (row0 + R <= nrows) {  // uniform
 #pragma unroll
-      for (int k = 0; k < NPW; ++k) dma(base, off[k], lds + (wave + k * NW) * 1024);
+      for (int k = 0; k < NPW; ++k)
+        if (k >= k0 && k < k1) dma(base, off[k], lds + (wave + k * NW) * 1024);
     } else {
 #pragma unroll
       for (int k = 0; k < NPW; ++k) {
+        if (k < k0 || k >= k1) continue;
         const int u = (wave + k * NW) * 64 + lane;
         const int r = u / CH, c = (u % CH) ^ SwzTile<D>::key(r);
         const int64_t rr = (row0 + r < nrows ? row0 + r : nrows - 1) - row0;
@@ -279,6 +303,8 @@ __device__ __forceinline__ void dkdv_sub_pipe(const char* qs, const char* dos,
   V8 qa[DK], da[DK], bv[NB], bk[NB];
 #pragma unroll
   for (int i = 0; i < PF; ++i) qa[i] = lds_a<T>(qs + o.a[i]);
+  // lse and dvs hold log2e*lse and D of the query rows: P = exp2(S*scale*log2e - la)
+  // and dS/scale = P * (dP - D) (dK takes the factor scale when it is stored).
   float la[16], db[16];
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
@@ -339,14 +365,14 @@ __device__ __forceinline__ void dkdv_sub_pipe(const char* qs, const char* dos,
 #pragma unroll
       for (int e = 0; e < EB; ++e) {
         const int r = (n - 1) * EB + e;
-        ds[r] = p[r] * fmaf(dpa[r], scale, -db[r]);
+        ds[r] = p[r] * (dpa[r] - db[r]);
       }
     TG_SB();
   }
 #pragma unroll
   for (int e = 0; e < EB; ++e) {
     const int r = (NB - 1) * EB + e;
-    ds[r] = p[r] * fmaf(dpa[r], scale, -db[r]);
+    ds[r] = p[r] * (dpa[r] - db[r]);
   }
   V8 dsa[2] = {pack8<T>(&ds[0]), pack8<T>(&ds[8])};
   TG_SB();
@@ -362,17 +388,20 @@ __device__ __forceinline__ void dkdv_sub_pipe(const char* qs, const char* dos,
 
 // The BM/32 sub-tiles of one staged query tile; kq = first key of this wave minus the
 // tile's first query.  The wave's keys are kq .. kq + 31.
-template <typename T, int D, int BM>
+// issue(t) runs before sub-tile t whether or not the sub-tile is skipped (the caller
+// spreads the next tile's DMA over the first sub-tiles with it).
+template <typename T, int D, int BM, typename F>
 __device__ __forceinline__ void dkdv_tile(const char* qs, const char* dos, const float* lse,
                                           const float* dvs, int kq, int causal, int h, int l32,
                                           const LaneOffs<D>& o,
                                           const typename Vec8<T>::type (&kf)[D / 16],
                                           const typename Vec8<T>::type (&vf)[D / 16],
                                           f32x16 (&dk)[D / 32], f32x16 (&dv)[D / 32],
-                                          float sl2, float scale) {
+                                          float sl2, float scale, F&& issue) {
   constexpr int RB = D * 2;
 #pragma unroll
   for (int t = 0; t < BM / 32; ++t) {
+    issue(t);
     // causal: a 32-query sub-tile wholly before this wave's keys contributes nothing
     if (causal && t * 32 + 31 < kq) continue;
     const char* q = qs + t * 32 * RB;
@@ -429,6 +458,14 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dkdv(
       kf[ks] = ld8(K + kc * rs + ks * 16 + h * 8);
       vf[ks] = ld8(V + kc * rs + ks * 16 + h * 8);
     }
+    // At d = 128 the kernel holds more than the 256 vector registers: K and V, used only
+    // as MFMA operands, are placed in accumulation registers (an empty asm whose "a"
+    // constraint emits no instruction), leaving the vector registers to S, dP and the
+    // values the VALU works on.
+    if (D == 128) {
+#pragma unroll
+      for (int ks = 0; ks < DK; ++ks) asm volatile("" : "+a"(kf[ks]), "+a"(vf[ks]));
+    }
   }
   f32x16 dk[DT], dv[DT];
 #pragma unroll
@@ -444,8 +481,8 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dkdv(
   plan.init(lane, wave, rs);
   // causal: queries below the first key of this block contribute nothing
   const int64_t qstart = causal ? (kblk / BM) * BM : 0;
-  // log2-scaled LSE (+inf past Sq: P = 0 for padded rows) and scale*D of one tile
-  // LSE and D of one tile's rows (+inf / 0 past Sq, so P = 0 for padded rows).  The
+  // log2e*lse and D of one tile's rows (+inf / 0 past Sq, so P = 0 for padded rows).
+  // The
   // two global loads are issued before the tile's DMA and converted only when stored
   // to LDS after the current tile's compute: vector-memory loads retire in issue order,
   // so a use right behind the DMA would wait for the whole DMA.
@@ -461,7 +498,7 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dkdv(
   auto put = [&](float* lse_s, float* dvs_s) {
     if (threadIdx.x < BM) {
       lse_s[threadIdx.x] = lok ? lv * kLog2e : INFINITY;
-      dvs_s[threadIdx.x] = lok ? dd * scale : 0.f;
+      dvs_s[threadIdx.x] = lok ? dd : 0.f;
     }
   };
   if (qstart < Sq) {
@@ -470,40 +507,45 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dkdv(
     plan.copy(dO, qstart, Sq, do0s);
     put(lse0, dvs0);
   }
+  // The next tile's copy is issued in two halves, before the first two sub-tiles of
+  // the current one: issued all at once right after the barrier, the four waves'
+  // copies queue up behind each other in the address unit while no MFMA runs.
+  constexpr int NPW = DmaPlan<T, D, BM>::NPW;
+  auto stage = [&](int64_t qn, char* qd, char* dd) {
+    return [&plan, &Q, &dO, qn, qd, dd, Sq](int t) {
+      if (t < 2 && qn < Sq) {
+        plan.copy(Q, qn, Sq, qd, t * NPW / 2, (t + 1) * NPW / 2);
+        plan.copy(dO, qn, Sq, dd, t * NPW / 2, (t + 1) * NPW / 2);
+      }
+    };
+  };
   for (int64_t q0 = qstart; q0 < Sq; q0 += 2 * BM) {
     // stage 0 holds tile q0; stage 1 is free (its last readers passed the barrier)
     dma_wait();
     __syncthreads();
     const bool more1 = q0 + BM < Sq;
-    if (more1) {
-      lsed(q0 + BM);
-      plan.copy(Q, q0 + BM, Sq, q1s);
-      plan.copy(dO, q0 + BM, Sq, do1s);
-    }
+    if (more1) lsed(q0 + BM);
     dkdv_tile<T, D, BM>(q0s, do0s, lse0, dvs0, (int)(kw - q0), causal, h, l32, o, kf, vf, dk,
-                        dv, sl2, scale);
+                        dv, sl2, scale, stage(q0 + BM, q1s, do1s));
     if (!more1) break;
     put(lse1, dvs1);
     // stage 1 holds tile q0 + BM
     dma_wait();
     __syncthreads();
     const bool more2 = q0 + 2 * BM < Sq;
-    if (more2) {
-      lsed(q0 + 2 * BM);
-      plan.copy(Q, q0 + 2 * BM, Sq, q0s);
-      plan.copy(dO, q0 + 2 * BM, Sq, do0s);
-    }
+    if (more2) lsed(q0 + 2 * BM);
     dkdv_tile<T, D, BM>(q1s, do1s, lse1, dvs1, (int)(kw - q0 - BM), causal, h, l32, o, kf, vf,
-                        dk, dv, sl2, scale);
+                        dk, dv, sl2, scale, stage(q0 + 2 * BM, q0s, do0s));
     if (!more2) break;
     put(lse0, dvs0);
   }
-  // C tiles: rows = keys of this wave, cols = d
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt) {
-    store_c_tile<T>(dK, rs, kw, Sk, dt * 32 + l32, dk[dt], 1.f, accumulate, h);
-    store_c_tile<T>(dV, rs, kw, Sk, dt * 32 + l32, dv[dt], 1.f, accumulate, h);
-  }
+  // C tiles (rows = keys of this wave, cols = d) staged through the first stage's
+  // buffers, 32 x D floats per wave, once every wave is done reading them
+  static_assert(2 * 32 * D * 4 <= TB, "two waves' staging per stage buffer");
+  __syncthreads();
+  float* st = reinterpret_cast<float*>(wave < 2 ? q0s : do0s) + (wave & 1) * 32 * D;
+  store_tiles_staged<T, D>(dK, rs, kw, Sk, dk, scale, accumulate, lane, st);  // dS's scale
+  store_tiles_staged<T, D>(dV, rs, kw, Sk, dv, 1.f, accumulate, lane, st);
 }
 
 // One 32-key x 32-query sub-tile of the dQ kernel for one wave (lane = query):
@@ -714,10 +756,13 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dq(
                       o, qf, of, acc, sl2, scale, lq, dqs);
     if (!more2) break;
   }
-  // C tiles: rows = queries of this wave, cols = d
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-    store_c_tile<T>(dQ, rs, qblk + wave * 32, Sq, dt * 32 + l32, acc[dt], 1.f, accumulate, h);
+  // C tiles (rows = queries of this wave, cols = d) staged through the stage buffers,
+  // one 32 x D float region per wave, once every wave is done reading them
+  static_assert(32 * D * 4 <= TB, "one wave's staging per stage buffer");
+  __syncthreads();
+  char* const stb = wave == 0 ? k0s : wave == 1 ? v0s : wave == 2 ? k1s : v1s;
+  store_tiles_staged<T, D>(dQ, rs, qblk + wave * 32, Sq, acc, 1.f, accumulate, lane,
+                           reinterpret_cast<float*>(stb));
 }
 
 // ---------------------------------------------------------------- forward, DMA-staged

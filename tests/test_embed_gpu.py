@@ -20,10 +20,12 @@ def L():
 
 # includes many-token, few-row and few-token, many-row cases; 32-bit sort keys (index
 # and position bits fit 32) and 64-bit ones (the last case), one sorted chunk and
-# several merged ones (n > 8192)
+# several merged ones (n > 8192); up to 8192 tokens the band kernel (no sort) runs,
+# also with thousands of tokens on one row
 @pytest.mark.parametrize("n,V,dim", [(1, 1, 1), (24, 5, 7), (8192, 32000, 64), (300, 50, 1000),
                                      (16384, 3, 12), (20000, 64, 8), (500, 70000, 4),
-                                     (9000, 1 << 20, 4)])
+                                     (9000, 1 << 20, 4), (8192, 3, 1024), (4097, 129, 130),
+                                     (8192, 64, 256)])
 def test_embedding_bwd_bit_exact_fp32(cuda, n, V, dim):
     rng = np.random.default_rng(n + V)
     idx = rng.integers(0, V, n)

@@ -163,7 +163,7 @@ def test_layernorm_fp32(cuda, shape, acc):
 
 
 @pytest.mark.parametrize("dt", F16S)
-@pytest.mark.parametrize("rows,cols,acc", [(64, 1024, False), (2309, 1024, True),
+@pytest.mark.parametrize("rows,cols,acc", [(64, 1024, False), (2309, 1024, True), (8192, 1024, True),
                                            (1029, 4096, True), (600, 8192, False)])
 def test_layernorm_half(cuda, dt, rows, cols, acc):
     rng = np.random.default_rng(4 + rows)
