@@ -522,6 +522,16 @@ struct V3Dma {
                                                16, off[k], soff, 0, 0);
 #endif
   }
+  // Instruction k of copy() alone, so a caller can spread a tile's copy over its MFMAs.
+  __device__ __forceinline__ void copy1(const T* base, uint32_t soff, char* lds, int k) const {
+#if defined(__HIP_DEVICE_COMPILE__)
+    const int wave = threadIdx.x >> 6;
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<T*>(base), (short)0, 0x7fffffff, 0x00020000);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (TG_LDS_G void*)(lds + (wave + k * NW) * 1024),
+                                             16, off[k], soff, 0, 0);
+#endif
+  }
 };
 
 // Fragment reader for one operand tile of EXT rows (m or n) and 64 k.
@@ -618,11 +628,24 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_v3(
     da.copy(a_org, (uint32_t)((AKC ? k0 : k0 * lda) * (int64_t)sizeof(T)), as);
     db.copy(b_org, (uint32_t)((BKC ? k0 : k0 * ldb) * (int64_t)sizeof(T)), bs);
   };
-  auto mul = [&](const char* as, const char* bs) {
+  // The next tile's copy, instruction q of ANPW + BNPW (A's first), issued between the
+  // MFMAs of the current tile by the pipelined path below (has_next false: nothing).
+  constexpr int ANPW = decltype(da)::NPW, BNPW = decltype(db)::NPW;
+  auto dma1 = [&](int64_t k0, char* as, char* bs, int q) {
+    if (q < ANPW) da.copy1(a_org, (uint32_t)((AKC ? k0 : k0 * lda) * (int64_t)sizeof(T)), as, q);
+    else db.copy1(b_org, (uint32_t)((BKC ? k0 : k0 * ldb) * (int64_t)sizeof(T)), bs, q - ANPW);
+  };
+  auto mul = [&](const char* as, const char* bs, bool has_next, int64_t kn, char* an, char* bn) {
     if constexpr (OCC == 1) {
       // One wave per SIMD: software pipeline.  The fragment reads of k-step ks+1 are
       // issued between the MFMAs of k-step ks (sched_barrier keeps the order), so only
-      // the first k-step of a tile waits on LDS latency.
+      // the first k-step of a tile waits on LDS latency.  The next tile's DMA goes out
+      // one instruction per two MFMAs over the first half of the tile: issued all at
+      // once after the barrier, the waves' copies queue in the address unit while no
+      // MFMA runs.
+      constexpr int NQ = ANPW + BNPW, NMF = (V3_BK / 16) * SM * SN;
+      constexpr int QSTEP = NQ * 2 <= NMF / 2 ? 2 : 1;
+      int q = 0;
       typename Vec8<T>::type fr[2][SM + SN];
       auto rd = [&](int buf, int ks, int n) {
         if (n < SM) fr[buf][n] = fa.get(as, wm, n, ks, l32);
@@ -644,6 +667,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_v3(
               rd(cur ^ 1, ks + 1, nr);
               ++nr;
             }
+            const int mf = (ks * SM + i) * SN + j;
+            if (has_next && mf % QSTEP == QSTEP - 1 && mf / QSTEP < NQ) dma1(kn, an, bn, mf / QSTEP);
             __builtin_amdgcn_sched_barrier(0);
           }
         if (ks + 1 < V3_BK / 16)
@@ -652,6 +677,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_v3(
         __builtin_amdgcn_sched_barrier(0);
       }
     } else {
+      if (has_next) dma(kn, an, bn);
 #pragma unroll
       for (int ks = 0; ks < V3_BK / 16; ++ks) {
         typename Vec8<T>::type af[SM], bf[SN];
@@ -671,14 +697,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_v3(
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     const bool more1 = k0 + V3_BK < K;
-    if (more1) dma(k0 + V3_BK, a1, b1);
-    mul(a0, b0);
+    mul(a0, b0, more1, k0 + V3_BK, a1, b1);
     if (!more1) break;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     const bool more2 = k0 + 2 * V3_BK < K;
-    if (more2) dma(k0 + 2 * V3_BK, a0, b0);
-    mul(a1, b1);
+    mul(a1, b1, more2, k0 + 2 * V3_BK, a0, b0);
     if (!more2) break;
   }
   if (m0 + TBM <= M && n0 + TBN <= N) {
@@ -782,11 +806,12 @@ int launch(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const v
   const int64_t b_span = (tb ? N * ldb : K * ldb) * (int64_t)sizeof(T);
   if (vec && M >= 64 && N >= 64 && K >= 64 && M % 8 == 0 && N % 8 == 0 && K % V3_BK == 0 &&
       a_span < (int64_t{1} << 31) && b_span < (int64_t{1} << 31)) {
-    // Block shapes (waves x per-wave tile): 2x2 waves of 128x128 (256x256, one block
-    // and one wave per SIMD, accumulators in AGPRs) when the problem has enough such
-    // tiles to fill the CUs: half the LDS fragment bytes and global tile bytes per flop
-    // of the smaller shapes.  Else 2x2 waves of 128x64 (256x128), else 2x2 waves of
-    // 64x64 (128x128, two blocks per CU).
+    // Block shapes (waves x per-wave tile): 4x2 waves of 64x128 (256x256, one block
+    // and two waves per SIMD) when the problem has enough such tiles to fill the CUs:
+    // fewer global tile bytes per flop than the smaller shapes.  (The same tile as 2x2
+    // waves of 128x128, one wave per SIMD, measured 3-8 % slower: nothing overlaps a
+    // wave's LDS waits and barrier.)  Else 4x2 waves of 64x64 (256x128), else 2x2
+    // waves of 64x64 (128x128, two blocks per CU).
     const int64_t ncu = tg_num_cus();
     const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256) * batch;
     const int64_t t128 = ((M + 255) / 256) * ((N + 127) / 128) * batch;
@@ -800,7 +825,7 @@ int launch(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const v
   } while (0)
 #define TG_G3(TA_, TB_)                                          \
   do {                                                           \
-    if (shape == 2) TG_G3_SHAPE(TA_, TB_, 2, 2, 4, 4, 1);        \
+    if (shape == 2) TG_G3_SHAPE(TA_, TB_, 4, 2, 2, 4, 1);        \
     else if (shape == 1) TG_G3_SHAPE(TA_, TB_, kBigWGM, kBigWGN, kBigSM, kBigSN, 1); \
     else TG_G3_SHAPE(TA_, TB_, 2, 2, 2, 2, 2);                   \
   } while (0)
