@@ -10,7 +10,12 @@
  *    the library keeps no reference after return.
  *  - `stream` is a hipStream_t (NULL = default stream).  Work is asynchronous
  *    on that stream; only tg_stream_sync waits.
- *  - dtype codes: 0 = fp32, 1 = fp16, 2 = bf16.
+ *  - dtype codes: 0 = fp32, 1 = fp16, 2 = bf16, 3 = fp64.  fp64 (float64 data,
+ *    which the reference keeps in float64, _core.py:173-193) is computed in double by
+ *    the activations, tg_axpby(z), tg_fill, softmax, LayerNorm, tg_reduce_rows,
+ *    tg_broadcast_mul_sum, tg_gemm (dtype_ab = dtype_c = 3), GradScaler unscale and
+ *    clipping, and by tg_axpbyz64, tg_cross_entropy_*_f64 and tg_adam_step_f64 (double
+ *    scalars); BatchNorm, embedding, FlashAttention and the transpose-add reject code 3.
  *  - `accumulate` != 0 means out += result (the reference's `grad += local`
  *    closures); 0 means out = result (out is not read).
  *  - Tensors are contiguous row-major unless leading dimensions are passed.
@@ -61,6 +66,11 @@ int tg_axpby(int dtype_x, const void* x, int dtype_y, void* y, int64_t n, float 
  * _core.py:945-966). */
 int tg_axpbyz(int dtype_x, const void* x, int dtype_y, const void* y, void* z, int64_t n,
               float alpha, float beta, void* stream);
+/* tg_axpbyz with double scalars, for fp64 operands (x or y fp64, the other fp64 or fp32;
+ * arithmetic in double, z of y's dtype).  No reference counterpart of its own: it keeps
+ * scale factors such as 1/n of a mean exact to double for float64 gradients. */
+int tg_axpbyz64(int dtype_x, const void* x, int dtype_y, const void* y, void* z, int64_t n,
+                double alpha, double beta, void* stream);
 /* Fill with a constant by a kernel (grad zeroing; graph-capture safe). */
 int tg_fill(int dtype, void* y, int64_t n, float value, void* stream);
 
@@ -71,7 +81,9 @@ int tg_softmax_fwd(int dtype, const void* x, void* y, int64_t rows, int64_t cols
 int tg_softmax_bwd(int dtype, const void* y, const void* dy, void* dx, int64_t rows,
                    int64_t cols, int accumulate, void* stream);
 /* LayerNorm forward over the last axis; saves mean and rstd = 1/sqrt(var+eps)
- * per row (fp32).  gamma/beta fp32.  (_nn.py:900-919) */
+ * per row (fp32).  gamma/beta fp32.  (_nn.py:900-919)  dtype 3 (fp64 x, y, dy, dx): mean
+ * and rstd point to double arrays; gamma/beta and dgamma/dbeta stay fp32 (the
+ * reference's module parameters are float32, _nn.py:896-897). */
 int tg_layernorm_fwd(int dtype, const void* x, const float* gamma, const float* beta, void* y,
                      float* mean, float* rstd, int64_t rows, int64_t cols, float eps,
                      void* stream);
@@ -108,7 +120,8 @@ int tg_broadcast_mul_sum(int ndim, const int64_t* shape, int dtype_a, const void
                          const int64_t* strides_out, double alpha, int accumulate,
                          void* stream);
 /* out[c] (+)= sum_r in[r][c]: Tensor._unbroadcast's leading-dimension sums
- * (_core.py:1380-1424), e.g. the Linear bias gradient. */
+ * (_core.py:1380-1424), e.g. the Linear bias gradient.  fp64 input or output: summed in
+ * double, in fixed order. */
 size_t tg_reduce_rows_workspace(int64_t rows, int64_t cols);
 int tg_reduce_rows(int dtype_in, const void* in, int dtype_out, void* out, int64_t rows,
                    int64_t cols, int accumulate, void* workspace, size_t workspace_bytes,
@@ -173,12 +186,20 @@ int tg_grad_norm(int ntensors, int dtype, void* const* grads, const int64_t* num
 /* xp.where(isfinite(g), g, 0) per tensor (_nn.py:1596). */
 int tg_zero_nonfinite(int ntensors, int dtype, void* const* grads, const int64_t* numel,
                       void* stream);
+/* tg_adam_step for float64 parameters, gradients and moments, in double throughout
+ * (the reference's Adam on float64 arrays, _nn.py:1413-1442). */
+int tg_adam_step_f64(int ntensors, double* const* params, const double* const* grads,
+                     double* const* exp_avg, double* const* exp_avg_sq,
+                     double* const* max_exp_avg_sq, const int64_t* numel, double lr,
+                     double beta1, double beta2, double eps, double weight_decay,
+                     double bias_correction1, double bias_correction2, void* stream);
 
 /* ---- dense contractions (MFMA) ------------------------------------------ */
 /* Batched row-major GEMM: C[b] = alpha * op(A[b]) @ op(B[b]) + beta * C[b],
  * op(A) is [M,K] (trans_a = 0: A[m*lda+k]; 1: A[k*lda+m]), op(B) is [K,N]
  * (trans_b = 0: B[k*ldb+n]; 1: B[n*ldb+k]); stride 0 broadcasts an operand.
- * dtype_ab in {fp32, fp16, bf16}; dtype_c is fp32 or dtype_ab.  Serves the
+ * dtype_ab in {fp32, fp16, bf16}; dtype_c is fp32 or dtype_ab; or dtype_ab = dtype_c =
+ * fp64 (fp64 matrix cores, v_mfma_f64_16x16x4f64).  Serves the
  * matmul forward and its backward dA = dC @ B^T, dB = A^T @ dC
  * (_core.py:999-1068). */
 int tg_gemm(int dtype_ab, int dtype_c, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
@@ -228,7 +249,7 @@ int tg_flash_attn_bwd_layout(int dtype, const void* q, const void* k, const void
  * _nn.py:1128-1185).  Forward: per-row log-sum-exp lse[N] and per-row loss
  * -log(p[t] + 1e-10) (label smoothing s: -sum_c w_c log(p_c + 1e-10), w = s/C +
  * (1-s) onehot); the caller reduces loss[N].  A target outside [0, C) gives a NaN
- * loss.  dtype fp32/fp16/bf16. */
+ * loss.  dtype fp32/fp16/bf16 (fp64: tg_cross_entropy_fwd_f64). */
 int tg_cross_entropy_fwd(int dtype, const void* logits, const int64_t* targets, int64_t N,
                          int64_t C, float label_smoothing, float* lse, float* loss, void* stream);
 /* Backward (_nn.py:1168-1180): grad (+)= (softmax(logits) - w) * scale, with
@@ -237,6 +258,14 @@ int tg_cross_entropy_fwd(int dtype, const void* logits, const int64_t* targets, 
 int tg_cross_entropy_bwd(int dtype, const void* logits, const int64_t* targets, const float* lse,
                          int64_t N, int64_t C, float label_smoothing, float scale, int dtype_grad,
                          void* grad, int accumulate, void* stream);
+/* The cross-entropy pair for fp64 logits, in double, with double scalars (label
+ * smoothing and the gradient scale, e.g. 1/N, are not exact in fp32); lse and loss are
+ * double and the gradient is fp64 (the reference's arithmetic on float64 logits). */
+int tg_cross_entropy_fwd_f64(const double* logits, const int64_t* targets, int64_t N, int64_t C,
+                             double label_smoothing, double* lse, double* loss, void* stream);
+int tg_cross_entropy_bwd_f64(const double* logits, const int64_t* targets, const double* lse,
+                             int64_t N, int64_t C, double label_smoothing, double scale,
+                             double* grad, int accumulate, void* stream);
 
 /* Embedding forward (Embedding.__call__, _nn.py:1076-1082): out[i, :] =
  * weight[indices[i], :] converted to dtype_out (the autocast cast of the gathered

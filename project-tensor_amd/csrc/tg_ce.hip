@@ -279,7 +279,8 @@ TG_EXPORT int tg_cross_entropy_fwd(int dtype, const void* logits, const int64_t*
     case TG_F16: return fwd_t<tg_half>(logits, targets, N, C, label_smoothing, lse, loss, s);
     case TG_BF16: return fwd_t<tg_bf16>(logits, targets, N, C, label_smoothing, lse, loss, s);
   }
-  tg_set_error("tg_cross_entropy_fwd: unsupported dtype %d", dtype);
+  tg_set_error("tg_cross_entropy_fwd: unsupported dtype %d (fp64: tg_cross_entropy_fwd_f64)",
+               dtype);
   return TG_ERR_UNSUPPORTED;
 }
 

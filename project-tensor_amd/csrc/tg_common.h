@@ -159,6 +159,35 @@ __device__ __forceinline__ void tg_st16(T* p, const tg_vec16<T>& r) {
 // Number of CUs on the current device, cached per device by tg_runtime.
 int tg_num_cus();
 
+// fp64 implementations (tg_f64.hip) behind the entry points' TG_F64 cases.
+int tg64_gemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, double alpha,
+              const double* A, int64_t lda, int64_t sa, const double* B, int64_t ldb,
+              int64_t sb, double beta, double* C, int64_t ldc, int64_t sc, int64_t batch,
+              const double* bias, hipStream_t s);
+int tg64_act_fwd(int kind, const void* x, void* y, int64_t n, hipStream_t s);
+int tg64_act_bwd(int kind, const void* x, const void* dy, void* dx, int64_t n, int acc,
+                 hipStream_t s);
+int tg64_fill(void* y, int64_t n, double v, hipStream_t s);
+int tg64_axpbyz(int dtype_x, const void* x, int dtype_y, const void* y, void* z, int64_t n,
+                double alpha, double beta, hipStream_t s);
+int tg64_softmax_fwd(const void* x, void* y, int64_t rows, int64_t cols, hipStream_t s);
+int tg64_softmax_bwd(const void* y, const void* dy, void* dx, int64_t rows, int64_t cols,
+                     int acc, hipStream_t s);
+int tg64_layernorm_fwd(const void* x, const float* gamma, const float* beta, void* y,
+                       void* mean, void* rstd, int64_t rows, int64_t cols, double eps,
+                       hipStream_t s);
+size_t tg64_layernorm_bwd_workspace(int64_t rows, int64_t cols);
+int tg64_layernorm_bwd(const void* x, const void* mean, const void* rstd, const float* gamma,
+                       const void* dy, void* dx, float* dgamma, float* dbeta, int64_t rows,
+                       int64_t cols, int acc_dx, int acc_params, void* ws, hipStream_t s);
+int tg64_reduce_rows(int dtype_in, const void* in, int dtype_out, void* out, int64_t rows,
+                     int64_t cols, int acc, void* ws, size_t ws_bytes, hipStream_t s);
+int tg64_unscale_check(int ntensors, void* const* grads, const int64_t* numel, double mul,
+                       int write, int* flags, hipStream_t s);
+int tg64_grad_norm(int ntensors, void* const* grads, const int64_t* numel, int kind, double p,
+                   int64_t chunk, double* out, int* flags, double* part, hipStream_t s);
+int tg64_zero_nonfinite(int ntensors, void* const* grads, const int64_t* numel, hipStream_t s);
+
 // Deterministic fp32 column sums: out[c] (+)= sum_{k<K} in[k*cols + c], converted to
 // dtype_out.  `scratch` must hold tg_sum_partials_scratch(K, cols, nb) bytes (may be
 // null when that is 0).  tg_sum_partials2 finishes two stacked matrices [2][K][cols]

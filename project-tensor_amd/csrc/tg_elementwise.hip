@@ -183,6 +183,7 @@ int dispatch_bwd(int dtype, const void* x, const void* dy, void* dx, int64_t n, 
     case TG_F32: return launch_act_bwd<float, OP>(x, dy, dx, n, acc, s);
     case TG_F16: return launch_act_bwd<tg_half, OP>(x, dy, dx, n, acc, s);
     case TG_BF16: return launch_act_bwd<tg_bf16, OP>(x, dy, dx, n, acc, s);
+    case TG_F64: return tg64_act_bwd(OP, x, dy, dx, n, acc, s);
   }
   tg_set_error("activation backward: unsupported dtype %d", dtype);
   return TG_ERR_UNSUPPORTED;
@@ -198,6 +199,7 @@ int dispatch_fwd(int dtype, const void* x, void* y, int64_t n, void* stream) {
     case TG_F32: return launch_act_fwd<float, OP>(x, y, n, s);
     case TG_F16: return launch_act_fwd<tg_half, OP>(x, y, n, s);
     case TG_BF16: return launch_act_fwd<tg_bf16, OP>(x, y, n, s);
+    case TG_F64: return tg64_act_fwd(OP, x, y, n, s);
   }
   tg_set_error("activation forward: unsupported dtype %d", dtype);
   return TG_ERR_UNSUPPORTED;
@@ -205,7 +207,8 @@ int dispatch_fwd(int dtype, const void* x, void* y, int64_t n, void* stream) {
 
 // ---------------------------------------------------------------------------
 // z = alpha*x + beta*y   (beta == 0: y is not read; z == y is the in-place update).
-// x and y may differ in dtype, z has y's; arithmetic is fp32.  Used for `grad += g`
+// x and y may differ in dtype, z has y's; arithmetic is fp32 (fp64 when an operand is
+// fp64).  Used for `grad += g`
 // with a dtype cast, for scaling, and for the out-of-place accumulation into a
 // gradient buffer that another node shares.
 template <typename TX, typename TY>
@@ -334,6 +337,8 @@ TG_EXPORT int tg_axpbyz(int dtype_x, const void* x, int dtype_y, const void* y, 
   TG_AXPBY_CASE(TG_BF16, tg_bf16, TG_F32, float)
   TG_AXPBY_CASE(TG_BF16, tg_bf16, TG_BF16, tg_bf16)
 #undef TG_AXPBY_CASE
+  if (dtype_x == TG_F64 || dtype_y == TG_F64)  // fp64 arithmetic (tg_f64.hip)
+    return tg64_axpbyz(dtype_x, x, dtype_y, y, z, n, alpha, beta, s);
   tg_set_error("tg_axpby: unsupported dtype pair (%d,%d)", dtype_x, dtype_y);
   return TG_ERR_UNSUPPORTED;
 }
@@ -359,6 +364,7 @@ TG_EXPORT int tg_fill(int dtype, void* y, int64_t n, float value, void* stream) 
     case TG_F32: k_fill<float><<<(unsigned)blocks, kThreads, 0, s>>>((float*)y, value, n); break;
     case TG_F16: k_fill<tg_half><<<(unsigned)blocks, kThreads, 0, s>>>((tg_half*)y, value, n); break;
     case TG_BF16: k_fill<tg_bf16><<<(unsigned)blocks, kThreads, 0, s>>>((tg_bf16*)y, value, n); break;
+    case TG_F64: return tg64_fill(y, n, value, s);
     default:
       tg_set_error("tg_fill: unsupported dtype %d", dtype);
       return TG_ERR_UNSUPPORTED;

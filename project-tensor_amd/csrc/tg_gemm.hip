@@ -898,6 +898,13 @@ int gemm_dispatch(const char* who, int dtype_ab, int dtype_c, int trans_a, int t
     TG_REQUIRE(A && B, "%s: null operand", who);
     TG_REQUIRE(lda >= (trans_a ? M : K) && ldb >= (trans_b ? K : N), "%s: bad leading dim", who);
   }
+  if (dtype_ab == TG_F64 && dtype_c == TG_F64) {
+    TG_REQUIRE(!bias, "%s: fp64 takes no fused bias", who);
+    TG_REQUIRE((M + 63) / 64 <= 65535, "%s: M too large", who);
+    return tg64_gemm(trans_a, trans_b, M, N, K, (double)alpha, (const double*)A, lda, stride_a,
+                     (const double*)B, ldb, stride_b, (double)beta, (double*)C, ldc, stride_c,
+                     batch, nullptr, s);
+  }
 #define TG_GEMM_CALL(TA, TC)                                                                  \
   return launch<TA, TC>(trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb, stride_b, \
                         beta, C, ldc, stride_c, batch, s, bias)

@@ -503,9 +503,10 @@ TG_EXPORT int tg_unscale_check(int ntensors, int dtype, void* const* grads, cons
   TG_REQUIRE(ntensors >= 0, "tg_unscale_check: negative tensor count");
   if (ntensors == 0) return TG_OK;
   TG_REQUIRE(grads && numel && flags, "tg_unscale_check: null argument");
-  TG_REQUIRE(dtype == TG_F32 || dtype == TG_F16 || dtype == TG_BF16,
+  TG_REQUIRE(dtype == TG_F32 || dtype == TG_F16 || dtype == TG_BF16 || dtype == TG_F64,
              "tg_unscale_check: unsupported dtype %d", dtype);
   hipStream_t s = tg_stream(stream);
+  if (dtype == TG_F64) return tg64_unscale_check(ntensors, grads, numel, mul, write, flags, s);
   k_zero_ints<<<1, kBlock, 0, s>>>(flags, ntensors);
   return for_each_launch(ntensors, grads, nullptr, nullptr, nullptr, nullptr, nullptr, numel,
                          [&](const MtArgs& A, int64_t nb) {
@@ -535,7 +536,7 @@ TG_EXPORT int tg_grad_norm(int ntensors, int dtype, void* const* grads, const in
   TG_REQUIRE(ntensors >= 0, "tg_grad_norm: negative tensor count");
   TG_REQUIRE(out && flags, "tg_grad_norm: null output");
   TG_REQUIRE(norm_kind >= 0 && norm_kind <= 2, "tg_grad_norm: bad norm kind %d", norm_kind);
-  TG_REQUIRE(dtype == TG_F32 || dtype == TG_F16 || dtype == TG_BF16,
+  TG_REQUIRE(dtype == TG_F32 || dtype == TG_F16 || dtype == TG_BF16 || dtype == TG_F64,
              "tg_grad_norm: unsupported dtype %d", dtype);
   hipStream_t s = tg_stream(stream);
   const int64_t nb_total = ntensors > 0 ? total_blocks(ntensors, numel) : 0;
@@ -545,6 +546,8 @@ TG_EXPORT int tg_grad_norm(int ntensors, int dtype, void* const* grads, const in
     return TG_ERR_WORKSPACE;
   }
   double* part = (double*)workspace;
+  if (dtype == TG_F64)  // one partial per kChunk elements, as the workspace counts them
+    return tg64_grad_norm(ntensors, grads, numel, norm_kind, p, kChunk, out, flags, part, s);
   if (ntensors > 0) k_zero_ints<<<1, kBlock, 0, s>>>(flags, ntensors);
   int64_t part_base = 0;
   int st = TG_OK;
@@ -576,6 +579,7 @@ TG_EXPORT int tg_zero_nonfinite(int ntensors, int dtype, void* const* grads, con
   if (ntensors == 0) return TG_OK;
   TG_REQUIRE(grads && numel, "tg_zero_nonfinite: null argument");
   hipStream_t s = tg_stream(stream);
+  if (dtype == TG_F64) return tg64_zero_nonfinite(ntensors, grads, numel, s);
   return for_each_launch(ntensors, grads, nullptr, nullptr, nullptr, nullptr, nullptr, numel,
                          [&](const MtArgs& A, int64_t nb) {
                            if (dtype == TG_F32) k_zero_nonfinite<float><<<(unsigned)nb, kBlock, 0, s>>>(A);

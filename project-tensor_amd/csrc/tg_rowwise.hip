@@ -807,6 +807,7 @@ TG_EXPORT int tg_softmax_fwd(int dtype, const void* x, void* y, int64_t rows, in
     case TG_F32: return softmax_fwd_t<float>(x, y, rows, cols, s);
     case TG_F16: return softmax_fwd_t<tg_half>(x, y, rows, cols, s);
     case TG_BF16: return softmax_fwd_t<tg_bf16>(x, y, rows, cols, s);
+    case TG_F64: return tg64_softmax_fwd(x, y, rows, cols, s);
   }
   tg_set_error("tg_softmax_fwd: unsupported dtype %d", dtype);
   return TG_ERR_UNSUPPORTED;
@@ -822,6 +823,7 @@ TG_EXPORT int tg_softmax_bwd(int dtype, const void* y, const void* dy, void* dx,
     case TG_F32: return softmax_bwd_t<float>(y, dy, dx, rows, cols, accumulate, s);
     case TG_F16: return softmax_bwd_t<tg_half>(y, dy, dx, rows, cols, accumulate, s);
     case TG_BF16: return softmax_bwd_t<tg_bf16>(y, dy, dx, rows, cols, accumulate, s);
+    case TG_F64: return tg64_softmax_bwd(y, dy, dx, rows, cols, accumulate, s);
   }
   tg_set_error("tg_softmax_bwd: unsupported dtype %d", dtype);
   return TG_ERR_UNSUPPORTED;
@@ -838,6 +840,7 @@ TG_EXPORT int tg_layernorm_fwd(int dtype, const void* x, const float* gamma, con
     case TG_F32: return ln_fwd_t<float>(x, gamma, beta, y, mean, rstd, rows, cols, eps, s);
     case TG_F16: return ln_fwd_t<tg_half>(x, gamma, beta, y, mean, rstd, rows, cols, eps, s);
     case TG_BF16: return ln_fwd_t<tg_bf16>(x, gamma, beta, y, mean, rstd, rows, cols, eps, s);
+    case TG_F64: return tg64_layernorm_fwd(x, gamma, beta, y, mean, rstd, rows, cols, eps, s);
   }
   tg_set_error("tg_layernorm_fwd: unsupported dtype %d", dtype);
   return TG_ERR_UNSUPPORTED;
@@ -845,6 +848,7 @@ TG_EXPORT int tg_layernorm_fwd(int dtype, const void* x, const float* gamma, con
 
 TG_EXPORT size_t tg_layernorm_bwd_workspace(int dtype, int64_t rows, int64_t cols) {
   if (rows <= 0 || cols <= 0) return 0;
+  if (dtype == TG_F64) return tg64_layernorm_bwd_workspace(rows, cols);
   // Alignment unknown at query time: size for the larger of the two plans.
   LnBwdPlan a = ln_bwd_plan_dt(dtype, rows, cols, true);
   LnBwdPlan b = ln_bwd_plan_dt(dtype, rows, cols, false);
@@ -860,6 +864,16 @@ TG_EXPORT int tg_layernorm_bwd(int dtype, const void* x, const float* mean, cons
   TG_REQUIRE(rows >= 0 && cols > 0, "tg_layernorm_bwd: bad shape");
   if (rows == 0) return TG_OK;
   TG_REQUIRE(x && mean && rstd && gamma && dy && dx, "tg_layernorm_bwd: null pointer");
+  if (dtype == TG_F64) {
+    const size_t need64 = tg64_layernorm_bwd_workspace(rows, cols);
+    if ((dgamma || dbeta) && (!workspace || workspace_bytes < need64)) {
+      tg_set_error("tg_layernorm_bwd: workspace of %zu bytes needed, got %zu", need64,
+                   workspace ? workspace_bytes : (size_t)0);
+      return TG_ERR_WORKSPACE;
+    }
+    return tg64_layernorm_bwd(x, mean, rstd, gamma, dy, dx, dgamma, dbeta, rows, cols,
+                              accumulate_dx, accumulate_params, workspace, tg_stream(stream));
+  }
   const bool al = tg_aligned16(x) && tg_aligned16(dy) && tg_aligned16(dx);
   LnBwdPlan p = ln_bwd_plan_dt(dtype, rows, cols, al);
   const size_t need =
@@ -953,7 +967,8 @@ TG_EXPORT int tg_layernorm_bwd_noalloc(int dtype, const void* x, const float* me
 TG_EXPORT size_t tg_reduce_rows_workspace(int64_t rows, int64_t cols) {
   if (rows <= 0 || cols <= 0) return 0;
   const int64_t ns = rr_splits(rows, cols);
-  return (size_t)(ns * cols) * sizeof(float) + tg_sum_partials_scratch(ns, cols);
+  // sized for fp64 partials (the fp64 path keeps its partial sums in double)
+  return (size_t)(ns * cols) * sizeof(double) + tg_sum_partials_scratch(ns, cols);
 }
 
 // out[c] (+)= sum_r in[r][c] for a row-major [rows, cols] input: the reduction that
@@ -968,9 +983,13 @@ TG_EXPORT int tg_reduce_rows(int dtype_in, const void* in, int dtype_out, void* 
   if (rows == 0) {
     if (accumulate) return TG_OK;
     // sum over zero rows is zero
+    if (dtype_out == TG_F64) return tg64_fill(out, cols, 0.0, s);
     return tg_sum_partials(nullptr, 0, cols, dtype_out, out, 0, nullptr, s);
   }
   TG_REQUIRE(in, "tg_reduce_rows: null input");
+  if (dtype_in == TG_F64 || dtype_out == TG_F64)  // fp64 sums in fixed order (tg_f64.hip)
+    return tg64_reduce_rows(dtype_in, in, dtype_out, out, rows, cols, accumulate, workspace,
+                            workspace_bytes, s);
   // A few fp32 rows over many columns (split-K GEMM partials): the finishing column
   // sum reads them directly, one launch instead of partials plus a copy.
   if (dtype_in == TG_F32 && rows <= 64 && cols >= 4096)

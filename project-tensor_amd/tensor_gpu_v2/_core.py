@@ -916,7 +916,7 @@ def _activation(x, kind):
 
 
 # ====================================================================== matmul
-_GEMM_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
+_GEMM_DTYPES = (torch.float32, torch.float16, torch.bfloat16, torch.float64)
 
 
 def _compute_dtype(a, b):
@@ -928,6 +928,25 @@ def _compute_dtype(a, b):
     return torch.promote_types(a.dtype, b.dtype)
 
 
+def _operand(t, cdt):
+    """A GEMM operand in compute dtype cdt, contiguous: float data through the copy
+    kernel, integer data (the reference's integer @ float promotes it) through torch."""
+    if t.dtype in L._TORCH_TO_CODE:
+        return _as(t, cdt)
+    return t.to(cdt).contiguous()
+
+
+def _wide(cdt):
+    """Accumulation (output) dtype of a GEMM computing in cdt: fp64 for fp64, else fp32."""
+    return torch.float64 if cdt == torch.float64 else torch.float32
+
+
+def _direct_out(buf_dtype, cdt):
+    """Whether a gradient buffer of buf_dtype can be the GEMM's output: the compute dtype
+    itself, or fp32 for a 16-bit compute dtype."""
+    return buf_dtype == cdt or (buf_dtype == torch.float32 and cdt != torch.float64)
+
+
 def _matmul(self, other):
     a, b = self.data, other.data
     if a.dim() == 0 or b.dim() == 0:
@@ -935,9 +954,9 @@ def _matmul(self, other):
     cdt = _compute_dtype(a, b)
     if cdt not in _GEMM_DTYPES:
         raise TypeError(f"matmul: dtype {cdt} is not supported by the MFMA GEMM "
-                        "(float32, float16, bfloat16)")
-    ac = a.to(cdt).contiguous()
-    bc = b.to(cdt).contiguous()
+                        "(float32, float16, bfloat16, float64)")
+    ac = _operand(a, cdt)
+    bc = _operand(b, cdt)
     out_t = _matmul_fwd(ac, bc)
     out = Tensor._wrap(out_t, (self, other), "@")
     if out._requires_grad:
@@ -953,6 +972,8 @@ def _weight_operand(w, wd, wt, cdt):
     (autocast) comes from the cast cache, owned by the tensor whose storage it is (the
     source of a tied weight), so the optimizer can refresh it in its update pass."""
     src = wd.t() if wt else wd
+    if cdt == torch.float64:
+        return _as(src, cdt)  # promoted: the copy kernel casts (no cast cache for fp64)
     if src.dtype == cdt or w._prev or not src.is_contiguous():
         return src.to(cdt).contiguous()
     tied = getattr(w, "_tied_source", None)
@@ -977,13 +998,17 @@ def _linear(x, w, b):
     cdt = _compute_dtype(a, wd)
     if cdt not in _GEMM_DTYPES:
         raise TypeError(f"matmul: dtype {cdt} is not supported by the MFMA GEMM "
-                        "(float32, float16, bfloat16)")
+                        "(float32, float16, bfloat16, float64)")
     K, N = wd.shape
     lead = tuple(a.shape[:-1])
-    A2 = a.to(cdt).contiguous().reshape(-1, K)
+    A2 = (_as(a, cdt) if cdt == torch.float64 else a.to(cdt).contiguous()).reshape(-1, K)
     wt = not wd.is_contiguous() and wd.t().is_contiguous()
     bc = _weight_operand(w, wd, wt, cdt)  # [N, K] if wt
-    if b is not None:
+    if b is not None and cdt == torch.float64:
+        # fp64: the product, then the bias added by the broadcast kernel (in fp64)
+        y = L.matmul2d(A2, bc, trans_b=wt)
+        L.broadcast_mul_sum(y, b.data.reshape(1, N), accumulate=True)
+    elif b is not None:
         odt = cfg.resolve_dtype(torch.promote_types(cdt, b.data.dtype))
         bias = b.data.to(torch.float32).contiguous().reshape(N)
         if odt in (torch.float32, cdt):
@@ -1003,21 +1028,21 @@ def _linear(x, w, b):
             G2 = _as(g, cdt).reshape(-1, N)
             if x._has_grad():
                 buf, acc = x._grad_target()
-                if buf.dtype in (torch.float32, cdt):
+                if _direct_out(buf.dtype, cdt):
                     L.matmul2d(G2, bc, out=buf.view(-1, K), trans_b=not wt,
                                beta=1.0 if acc else 0.0)
                 else:
-                    da = L.matmul2d(G2, bc, trans_b=not wt, out_dtype=torch.float32)
+                    da = L.matmul2d(G2, bc, trans_b=not wt, out_dtype=_wide(cdt))
                     if acc:
                         x._accumulate(da.reshape(buf.shape), True)
                     else:
                         _copy_into(buf, da.reshape(buf.shape))
             if w._has_grad():
                 buf, acc = w._grad_target()
-                if buf.dtype in (torch.float32, cdt):
+                if _direct_out(buf.dtype, cdt):
                     L.matmul2d(A2, G2, out=buf.view(K, N), trans_a=True, beta=1.0 if acc else 0.0)
                 else:
-                    dw = L.matmul2d(A2, G2, trans_a=True, out_dtype=torch.float32)
+                    dw = L.matmul2d(A2, G2, trans_a=True, out_dtype=_wide(cdt))
                     if acc:
                         w._accumulate(dw, True)
                     else:
@@ -1110,19 +1135,19 @@ def _matmul_bwd(self, other, ac, bc, out):
         if self._has_grad():
             # dA[.., m, k] = G @ B^T
             buf, acc = self._grad_target()
-            if buf.dtype in (torch.float32, cdt):
+            if _direct_out(buf.dtype, cdt):
                 L.matmul2d(G2, Bm, out=buf.view(A2.shape[0], K), trans_b=True,
                            beta=1.0 if acc else 0.0)
             else:
-                da = L.matmul2d(G2, Bm, trans_b=True, out_dtype=torch.float32)
+                da = L.matmul2d(G2, Bm, trans_b=True, out_dtype=_wide(cdt))
                 L.broadcast_mul_sum(buf, da.reshape(buf.shape), accumulate=acc)
         if other._has_grad():
             # dB[k, n] = sum over all leading rows of A^T @ G: one TN GEMM with K' = rows
             buf, acc = other._grad_target()
-            if buf.dtype in (torch.float32, cdt):
+            if _direct_out(buf.dtype, cdt):
                 L.matmul2d(A2, G2, out=buf.view(K, N), trans_a=True, beta=1.0 if acc else 0.0)
             else:
-                db = L.matmul2d(A2, G2, trans_a=True, out_dtype=torch.float32)
+                db = L.matmul2d(A2, G2, trans_a=True, out_dtype=_wide(cdt))
                 L.broadcast_mul_sum(buf, db.reshape(buf.shape), accumulate=acc)
         return
     # batched operands
@@ -1131,7 +1156,7 @@ def _matmul_bwd(self, other, ac, bc, out):
     G3 = _as(G.expand(*batch_shape, M, N), cdt).reshape(bsz, M, N)
     if self._has_grad():
         B3, sb, _ = _batch_view(Bm, batch_shape, K, N)
-        da = torch.empty(bsz, M, K, dtype=torch.float32, device=A.device)
+        da = torch.empty(bsz, M, K, dtype=_wide(cdt), device=A.device)
         L.gemm(G3, B3, da, False, True, 1.0, 0.0, M, K, N, N, N, K, M * N, sb, M * K, bsz)
         da = da.reshape(*batch_shape, M, K)
         if av:
@@ -1139,7 +1164,7 @@ def _matmul_bwd(self, other, ac, bc, out):
         self._accumulate(_unbroadcast_dev(da, tuple(lhs.shape), lhs.dtype), True)
     if other._has_grad():
         A3, sa, _ = _batch_view(A, batch_shape, M, K)
-        db = torch.empty(bsz, K, N, dtype=torch.float32, device=A.device)
+        db = torch.empty(bsz, K, N, dtype=_wide(cdt), device=A.device)
         L.gemm(A3, G3, db, True, False, 1.0, 0.0, K, N, M, K, N, N, sa, M * N, K * N, bsz)
         db = db.reshape(*batch_shape, K, N)
         if bv:

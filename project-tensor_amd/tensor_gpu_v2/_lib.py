@@ -18,10 +18,11 @@ import torch
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("TG_HIP_LIB", os.path.join(_HERE, "libtgbwd.so"))
 
-F32, F16, BF16 = 0, 1, 2
+F32, F16, BF16, F64 = 0, 1, 2, 3
 NHWC, NCHW = 0, 1
 
-_TORCH_TO_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+_TORCH_TO_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16,
+                  torch.float64: F64}
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -42,6 +43,7 @@ SIGNATURES = {
     "tg_silu_fwd": (_i32, [_i32, _vp, _vp, _i64, _vp]),
     "tg_axpby": (_i32, [_i32, _vp, _i32, _vp, _i64, _f32, _f32, _vp]),
     "tg_axpbyz": (_i32, [_i32, _vp, _i32, _vp, _vp, _i64, _f32, _f32, _vp]),
+    "tg_axpbyz64": (_i32, [_i32, _vp, _i32, _vp, _vp, _i64, _f64, _f64, _vp]),
     "tg_fill": (_i32, [_i32, _vp, _i64, _f32, _vp]),
     "tg_softmax_fwd": (_i32, [_i32, _vp, _vp, _i64, _i64, _vp]),
     "tg_softmax_bwd": (_i32, [_i32, _vp, _vp, _vp, _i64, _i64, _i32, _vp]),
@@ -63,6 +65,11 @@ SIGNATURES = {
                                 _i64, _i32, _i32, _i32, _vp, _sz, _vp]),
     "tg_adam_step": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _f64, _f64, _f64, _f64, _f64,
                             _f64, _f64, _vp]),
+    "tg_cross_entropy_fwd_f64": (_i32, [_vp, _vp, _i64, _i64, _f64, _vp, _vp, _vp]),
+    "tg_cross_entropy_bwd_f64": (_i32, [_vp, _vp, _vp, _i64, _i64, _f64, _f64, _vp, _i32,
+                                        _vp]),
+    "tg_adam_step_f64": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _f64, _f64, _f64, _f64,
+                                _f64, _f64, _f64, _vp]),
     "tg_adam_step_lowp": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _f64, _f64, _f64, _f64,
                                  _f64, _f64, _f64, _i32, _vp, _vp]),
     "tg_unscale_check": (_i32, [_i32, _i32, _vp, _vp, _f32, _i32, _vp, _vp]),
@@ -196,7 +203,7 @@ def dtype_code(t):
         return _TORCH_TO_CODE[t.dtype]
     except KeyError:
         raise TypeError(f"unsupported dtype {t.dtype} for the HIP kernels "
-                        "(float32, float16, bfloat16 are supported)") from None
+                        "(float32, float16, bfloat16, float64 are supported)") from None
 
 
 def ptr(t):
@@ -255,6 +262,11 @@ def axpby(x, y, alpha=1.0, beta=1.0):
     if x.numel() != y.numel():
         raise ValueError(f"axpby: numel mismatch {x.numel()} vs {y.numel()}")
     ensure_device(y.device.index)
+    if torch.float64 in (x.dtype, y.dtype):  # double scalars for fp64 arithmetic
+        _check("tg_axpbyz64", load().tg_axpbyz64(dtype_code(x), ptr(x), dtype_code(y), ptr(y),
+                                                 ptr(y), y.numel(), float(alpha), float(beta),
+                                                 stream_handle()))
+        return y
     _check("tg_axpby", load().tg_axpby(dtype_code(x), ptr(x), dtype_code(y), ptr(y), y.numel(),
                                        float(alpha), float(beta), stream_handle()))
     return y
@@ -271,8 +283,9 @@ def axpbyz(x, y, alpha=1.0, beta=1.0, out=None):
     elif out.dtype != y.dtype or out.numel() != y.numel() or not out.is_contiguous():
         raise ValueError("axpbyz: out must be contiguous with y's dtype and numel")
     ensure_device(y.device.index)
-    _check("tg_axpbyz", load().tg_axpbyz(dtype_code(x), ptr(x), dtype_code(y), ptr(y), ptr(out),
-                                         y.numel(), float(alpha), float(beta), stream_handle()))
+    fn = load().tg_axpbyz64 if torch.float64 in (x.dtype, y.dtype) else load().tg_axpbyz
+    _check("tg_axpbyz", fn(dtype_code(x), ptr(x), dtype_code(y), ptr(y), ptr(out), y.numel(),
+                           float(alpha), float(beta), stream_handle()))
     return out
 
 
@@ -359,14 +372,17 @@ def layernorm_fwd(x, gamma, beta, eps, y=None, mean=None, rstd=None):
     rows = x.numel() // cols
     if y is None:
         y = torch.empty_like(x)
+    # row statistics in fp32, or fp64 for fp64 input; the parameters are fp32
+    sdt = torch.float64 if x.dtype == torch.float64 else torch.float32
     if mean is None:
-        mean = torch.empty(rows, dtype=torch.float32, device=x.device)
+        mean = torch.empty(rows, dtype=sdt, device=x.device)
     if rstd is None:
-        rstd = torch.empty(rows, dtype=torch.float32, device=x.device)
-    for n, t in (("gamma", gamma), ("beta", beta), ("mean", mean), ("rstd", rstd)):
+        rstd = torch.empty(rows, dtype=sdt, device=x.device)
+    for n, t, want in (("gamma", gamma, torch.float32), ("beta", beta, torch.float32),
+                       ("mean", mean, sdt), ("rstd", rstd, sdt)):
         _dev(t, n)
-        if t.dtype != torch.float32:
-            raise TypeError(f"layernorm_fwd: {n} must be float32")
+        if t.dtype != want:
+            raise TypeError(f"layernorm_fwd: {n} must be {want}")
     ensure_device(x.device.index)
     _check("tg_layernorm_fwd", load().tg_layernorm_fwd(
         dtype_code(x), ptr(x), ptr(gamma), ptr(beta), ptr(y), ptr(mean), ptr(rstd), rows, cols,
@@ -505,13 +521,16 @@ def _adam_state(params, exp_avg, exp_avg_sq, max_exp_avg_sq):
     if st is not None and all(p.numel() == n for p, n in zip(params, st[1])):
         return st
     groups = (params, exp_avg, exp_avg_sq) + ((max_exp_avg_sq,) if max_exp_avg_sq else ())
+    pdt = params[0].dtype
+    if pdt not in (torch.float32, torch.float64):
+        raise TypeError("adam_step: fp32 or fp64 tensors required")
     for group in groups:
         if len(group) != len(params):
             raise ValueError("adam_step: param/state list lengths differ")
         for t in group:
             _dev(t, "adam operand")
-            if t.dtype != torch.float32:
-                raise TypeError("adam_step: fp32 tensors required")
+            if t.dtype != pdt:
+                raise TypeError(f"adam_step: every tensor of one step must be {pdt}")
     numels = [p.numel() for p in params]
     for p, m, v in zip(params, exp_avg, exp_avg_sq):
         if not (p.numel() == m.numel() == v.numel()):
@@ -536,16 +555,22 @@ def adam_step(params, grads, exp_avg, exp_avg_sq, max_exp_avg_sq, lr, beta1, bet
     arrs, numels, numel_arr = _adam_state(params, exp_avg, exp_avg_sq, max_exp_avg_sq)
     if len(grads) != n:
         raise ValueError("adam_step: param/grad list lengths differ")
+    pdt = params[0].dtype
     for g, k in zip(grads, numels):
         _dev(g, "adam operand")
-        if g.dtype != torch.float32:
-            raise TypeError("adam_step: fp32 tensors required")
+        if g.dtype != pdt:
+            raise TypeError(f"adam_step: gradients must be {pdt} like their params")
         if g.numel() != k:
             raise ValueError("adam_step: param/grad/state sizes differ")
     ensure_device(params[0].device.index)
     args = (arrs[0], _ptr_array(grads), arrs[1], arrs[2], arrs[3], numel_arr,
             float(lr), float(beta1), float(beta2), float(eps), float(weight_decay),
             float(bias_correction1), float(bias_correction2))
+    if pdt == torch.float64:
+        if lowp is not None and any(t is not None for t in lowp):
+            raise TypeError("adam_step: low-precision copies are for fp32 params")
+        _check("tg_adam_step_f64", load().tg_adam_step_f64(n, *args, stream_handle()))
+        return
     if lowp is not None and any(t is not None for t in lowp):
         if len(lowp) != n:
             raise ValueError("adam_step: lowp list length differs from params")
@@ -769,7 +794,8 @@ def matmul2d(a, b, out=None, trans_a=False, trans_b=False, alpha=1.0, beta=0.0, 
     if tuple(out.shape) != (M, N):
         raise ValueError(f"matmul2d: out shape {tuple(out.shape)} != {(M, N)}")
     lda, ldb = a.shape[1], b.shape[1]
-    s_ = _split_k(M, N, K, a.device) if (alpha == 1.0 and beta in (0.0, 1.0)) else 1
+    s_ = (_split_k(M, N, K, a.device)
+          if (alpha == 1.0 and beta in (0.0, 1.0) and a.dtype != torch.float64) else 1)
     if s_ > 1:
         kc = K // s_
         parts = torch.empty(s_, M, N, dtype=torch.float32, device=a.device)
@@ -853,7 +879,7 @@ def flash_attn_bwd(q, k, v, o, do, lse, dq, dk, dv, scale, causal, accumulate, l
 
 def cross_entropy_fwd(logits, targets, label_smoothing=0.0):
     """Per-row log-sum-exp and loss of logits [N, C] against int64 targets [N]:
-    returns (lse, loss), both fp32 [N]."""
+    returns (lse, loss), both fp32 [N] (fp64 for fp64 logits)."""
     _dev(logits, "logits")
     _dev(targets, "targets")
     if logits.dim() != 2 or not logits.is_contiguous():
@@ -861,9 +887,15 @@ def cross_entropy_fwd(logits, targets, label_smoothing=0.0):
     if targets.dtype != torch.int64 or targets.numel() != logits.shape[0]:
         raise ValueError("cross_entropy: targets must be int64 [N]")
     N, C = logits.shape
-    lse = torch.empty(N, dtype=torch.float32, device=logits.device)
-    loss = torch.empty(N, dtype=torch.float32, device=logits.device)
+    sdt = torch.float64 if logits.dtype == torch.float64 else torch.float32
+    lse = torch.empty(N, dtype=sdt, device=logits.device)
+    loss = torch.empty(N, dtype=sdt, device=logits.device)
     ensure_device(logits.device.index)
+    if logits.dtype == torch.float64:
+        _check("tg_cross_entropy_fwd_f64", load().tg_cross_entropy_fwd_f64(
+            ptr(logits), ptr(targets), N, C, float(label_smoothing), ptr(lse), ptr(loss),
+            stream_handle()))
+        return lse, loss
     _check("tg_cross_entropy_fwd", load().tg_cross_entropy_fwd(
         dtype_code(logits), ptr(logits), ptr(targets), N, C, float(label_smoothing), ptr(lse),
         ptr(loss), stream_handle()))
@@ -877,6 +909,13 @@ def cross_entropy_bwd(logits, targets, lse, grad, scale, accumulate, label_smoot
     if grad.shape != logits.shape or not grad.is_contiguous():
         raise ValueError("cross_entropy: grad must be contiguous with the logits' shape")
     N, C = logits.shape
+    if logits.dtype == torch.float64:
+        if grad.dtype != torch.float64 or lse.dtype != torch.float64:
+            raise TypeError("cross_entropy: fp64 logits need an fp64 gradient and lse")
+        _check("tg_cross_entropy_bwd_f64", load().tg_cross_entropy_bwd_f64(
+            ptr(logits), ptr(targets), ptr(lse), N, C, float(label_smoothing), float(scale),
+            ptr(grad), int(bool(accumulate)), stream_handle()))
+        return
     _check("tg_cross_entropy_bwd", load().tg_cross_entropy_bwd(
         dtype_code(logits), ptr(logits), ptr(targets), ptr(lse), N, C, float(label_smoothing),
         float(scale), dtype_code(grad), ptr(grad), int(bool(accumulate)), stream_handle()))

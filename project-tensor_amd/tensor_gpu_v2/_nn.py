@@ -14,7 +14,7 @@ import torch
 from . import _config as cfg
 from . import _lib as L
 from . import _lowp
-from ._core import Tensor, _linear
+from ._core import Tensor, _as, _linear
 
 
 def _targets(tensors):
@@ -583,23 +583,30 @@ class Adam:
         self.t += 1
         bc1 = 1 - self.beta1 ** self.t
         bc2 = 1 - self.beta2 ** self.t
-        ps, gs, ms, vs, vms = [], [], [], [], []
+        # one multi-tensor step per parameter dtype: fp32 (with the autocast copies) and
+        # fp64 (parameters made from float64 arrays, updated in double)
+        groups = {}
         for i, p in enumerate(self.params):
             if not p._has_grad():
                 continue
-            if p.data.dtype != torch.float32 or not p.data.is_contiguous():
-                raise TypeError("Adam: parameters must be contiguous float32 device tensors")
+            dt = p.data.dtype
+            if dt not in (torch.float32, torch.float64) or not p.data.is_contiguous():
+                raise TypeError("Adam: parameters must be contiguous float32 or float64 "
+                                "device tensors")
             g = p.grad
-            if g.dtype != torch.float32:
-                g = g.float()
+            if g.dtype != dt:
+                g = _as(g, dt)
+            ps, gs, ms, vs, vms = groups.setdefault(dt, ([], [], [], [], []))
             ps.append(p.data)
             gs.append(g)
             ms.append(self.m[i])
             vs.append(self.v[i])
             if self.amsgrad:
                 vms.append(self.v_max[i])
-        L.adam_step(ps, gs, ms, vs, vms if self.amsgrad else None, lr, self.beta1, self.beta2,
-                    self.eps, wd, bc1, bc2, lowp=_lowp.refresh_targets(ps))
+        for dt, (ps, gs, ms, vs, vms) in groups.items():
+            L.adam_step(ps, gs, ms, vs, vms if self.amsgrad else None, lr, self.beta1,
+                        self.beta2, self.eps, wd, bc1, bc2,
+                        lowp=_lowp.refresh_targets(ps) if dt == torch.float32 else None)
 
     def step(self, clip_grad_norm=None):
         if clip_grad_norm is not None:
@@ -626,13 +633,16 @@ class Adam:
             self.beta1, self.beta2 = state["betas"]
         self.eps = state.get("eps", self.eps)
         self.weight_decay = state.get("weight_decay", self.weight_decay)
+        # moments take their parameter's dtype (fp32, or fp64 for float64 parameters)
+        def _load(vals):
+            return [torch.as_tensor(np.asarray(v), device="cuda").to(p.data.dtype)
+                    for v, p in zip(vals, self.params)]
         if "m" in state:
-            self.m = [torch.as_tensor(np.asarray(m, dtype=np.float32), device="cuda") for m in state["m"]]
+            self.m = _load(state["m"])
         if "v" in state:
-            self.v = [torch.as_tensor(np.asarray(v, dtype=np.float32), device="cuda") for v in state["v"]]
+            self.v = _load(state["v"])
         if self.amsgrad and "v_max" in state:
-            self.v_max = [torch.as_tensor(np.asarray(v, dtype=np.float32), device="cuda")
-                          for v in state["v_max"]]
+            self.v_max = _load(state["v_max"])
 
 
 class AdamW(Adam):
