@@ -22,6 +22,16 @@ namespace {
 
 constexpr int kBlock = 256;
 
+// A dout element as added: fp32 for 16/32-bit dout; fp64 dout is added in double and the
+// sum rounded to fp32 at every step, as np.add.at does on a float32 array.
+__device__ __forceinline__ float tg_in(float v) { return v; }
+__device__ __forceinline__ float tg_in(tg_half v) { return (float)v; }
+__device__ __forceinline__ float tg_in(tg_bf16 v) { return (float)v; }
+__device__ __forceinline__ double tg_in(double v) { return v; }
+__device__ __forceinline__ void acc_add(float& a, float v) { a += v; }
+__device__ __forceinline__ void acc_add(float& a, double v) { a = (float)((double)a + v); }
+template <typename TD> using InT = decltype(tg_in(TD()));
+
 constexpr int kSortThreads = 1024;
 constexpr int kChunk = 8192;  // keys sorted per workgroup in LDS (two 64 KiB buffers)
 
@@ -183,37 +193,38 @@ __global__ __launch_bounds__(kBlock) void k_embed_seg(const K* __restrict__ sort
     float acc[PER];
 #pragma unroll
     for (int e = 0; e < PER; ++e) acc[e] = 0.f;
-    auto load = [&](int64_t j, float (&v)[PER]) {
+    using IT = InT<TD>;
+    auto load = [&](int64_t j, IT (&v)[PER]) {
       const TD* drow = dout + (int64_t)(sorted[j] & pmask) * dim;
       if (VEC) {
         if (col(c0, 0) < dim) {
           const tg_vec16<TD> t = tg_load16(drow + col(c0, 0));
 #pragma unroll
-          for (int e = 0; e < PER; ++e) v[e] = tg_to_float(t.v[e]);
+          for (int e = 0; e < PER; ++e) v[e] = tg_in(t.v[e]);
         } else {
 #pragma unroll
-          for (int e = 0; e < PER; ++e) v[e] = 0.f;
+          for (int e = 0; e < PER; ++e) v[e] = 0;
         }
       } else {
 #pragma unroll
-        for (int e = 0; e < PER; ++e) v[e] = col(c0, e) < dim ? tg_to_float(drow[col(c0, e)]) : 0.f;
+        for (int e = 0; e < PER; ++e) v[e] = col(c0, e) < dim ? tg_in(drow[col(c0, e)]) : (IT)0;
       }
     };
     int64_t j = i;
     for (; j + U <= end; j += U) {
-      float v[U][PER];
+      IT v[U][PER];
 #pragma unroll
       for (int u = 0; u < U; ++u) load(j + u, v[u]);
 #pragma unroll
       for (int u = 0; u < U; ++u)
 #pragma unroll
-        for (int e = 0; e < PER; ++e) acc[e] += v[u][e];
+        for (int e = 0; e < PER; ++e) acc_add(acc[e], v[u][e]);
     }
     for (; j < end; ++j) {
-      float v[PER];
+      IT v[PER];
       load(j, v);
 #pragma unroll
-      for (int e = 0; e < PER; ++e) acc[e] += v[e];
+      for (int e = 0; e < PER; ++e) acc_add(acc[e], v[e]);
     }
     if (VG && col(c0, 0) < dim) {  // PER adjacent outputs per lane as 16-byte stores
       constexpr int NG = tg_vec16<TG>::N;
@@ -320,14 +331,14 @@ __global__ __launch_bounds__(kBandThreads) void k_embed_band(const int64_t* __re
           for (int q = 0; q < NCH; ++q)
             if (col(c0 + q * 64 * PER, 0) < dim)
 #pragma unroll
-              for (int e = 0; e < PER; ++e) acc[q][e] += tg_to_float(t[q].v[e]);
+              for (int e = 0; e < PER; ++e) acc_add(acc[q][e], tg_in(t[q].v[e]));
         } else {
 #pragma unroll
           for (int q = 0; q < NCH; ++q)
 #pragma unroll
             for (int e = 0; e < PER; ++e) {
               const int64_t cc = col(c0 + q * 64 * PER, e);
-              if (cc < dim) acc[q][e] += tg_to_float(drow[cc]);
+              if (cc < dim) acc_add(acc[q][e], tg_in(drow[cc]));
             }
         }
       };
@@ -603,6 +614,7 @@ TG_EXPORT int tg_embedding_bwd(int dtype_dout, const void* dout, const int64_t* 
     case TG_F32: G(float)
     case TG_F16: G(tg_half)
     case TG_BF16: G(tg_bf16)
+    case TG_F64: G(double)  // each row rounded to fp32, then added in fp32 (np.add.at)
   }
 #undef G
   tg_set_error("tg_embedding_bwd: unsupported dtypes %d/%d", dtype_dout, dtype_grad);

@@ -234,3 +234,22 @@ def test_float64_softmax_layernorm_ce_autograd(cuda):
     assert abs(loss.item() - lt.item()) < 1e-8
     lt.backward()
     assert_close(x.grad, xt.grad.numpy(), 1e-8, "fp64 LN-softmax-CE input gradient")
+
+
+@pytest.mark.parametrize("n,V,acc", [(300, 40, False), (8192, 1000, True), (9000, 64, False)])
+def test_embedding_bwd_f64_rows_into_fp32(cuda, n, V, acc):
+    """An fp64 output gradient scattered into the fp32 embedding gradient: np.add.at on
+    a float32 array adds each float64 row in double and rounds at every step; the kernel
+    does the same, so the result is bit-exact (one launch up to 8192 tokens, the sorted
+    path beyond)."""
+    rng = np.random.default_rng(n)
+    idx = rng.integers(0, V, n)
+    idx[: n // 4] = idx[0]
+    d = rng.standard_normal((n, 24))
+    want = np.zeros((V, 24), np.float32)
+    np.add.at(want, idx, d)
+    base = rng.standard_normal((V, 24)).astype(np.float32)
+    grad = torch.tensor(base if acc else np.zeros_like(base), device="cuda")
+    L().embedding_bwd(dev(d), torch.tensor(idx, device="cuda"), grad, acc)
+    exp = (base + want) if acc else want
+    np.testing.assert_array_equal(host(grad), exp)
