@@ -213,6 +213,23 @@ int tg_gemm_bias(int dtype_ab, int dtype_c, int trans_a, int trans_b, int64_t M,
                  int64_t K, float alpha, const void* A, int64_t lda, const void* B, int64_t ldb,
                  const float* bias, void* C, int64_t ldc, void* stream);
 
+/* Weight and bias gradients of a Linear layer y = x @ w + b from one pass over the
+ * output gradient (the matmul node's dB = A^T @ dC, _core.py:1064-1068, and the
+ * broadcast-add node's unbroadcast sum of _core.py:1380-1424, as Linear.__call__ builds
+ * them, _nn.py:258-285): dW[M,N] (+)= X^T @ G and db[N] (+)= sum_k G[k,:], with X
+ * [K,M] (ldx) the layer input, G [K,N] (ldg) the output gradient, K the tokens.  db
+ * NULL: weight only.  acc_w / acc_b: add to the gradient instead of overwriting it.
+ * dtype_ab in {fp32, fp16, bf16, fp64}; dtype_w and dtype_b are fp32 or dtype_ab (fp64
+ * for fp64).  fp16/bf16 GEMMs add up the column sums of G inside the GEMM; small
+ * outputs split K, and one finishing launch reduces the weight and bias partials in
+ * a fixed order (deterministic).  workspace: tg_gemm_wgrad_workspace(dtype_ab, M, N,
+ * K, db != NULL) bytes, 16-byte aligned. */
+size_t tg_gemm_wgrad_workspace(int dtype_ab, int64_t M, int64_t N, int64_t K, int with_bias);
+int tg_gemm_wgrad(int dtype_ab, int64_t M, int64_t N, int64_t K, const void* X, int64_t ldx,
+                  const void* G, int64_t ldg, int dtype_w, void* dW, int64_t ldw, int acc_w,
+                  int dtype_b, void* db, int acc_b, void* workspace, size_t workspace_bytes,
+                  void* stream);
+
 /* ---- attention ------------------------------------------------------------ */
 /* FlashAttention forward on contiguous (B,H,S,D) tensors, saving the row
  * log-sum-exp lse[B,H,Sq] (fp32) for the backward.  causal masks col > row

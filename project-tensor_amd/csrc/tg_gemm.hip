@@ -577,13 +577,38 @@ struct V3Frag {
   }
 };
 
+// Sum of the 8 k-elements of a B fragment, added to acc in fp32 (v_dot2 with ones:
+// the products are exact, so each step is one fp32 addition of a pair).
+__device__ __forceinline__ float frag_sum(const Vec8<tg_half>::type& v, float acc) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 one = {(_Float16)1, (_Float16)1};
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) acc = __builtin_amdgcn_fdot2(h2{v[e], v[e + 1]}, one, acc, false);
+  return acc;
+}
+__device__ __forceinline__ float frag_sum(const Vec8<tg_bf16>::type& v, float acc) {
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  const b2 one = {(__bf16)1.0f, (__bf16)1.0f};
+#pragma unroll
+  for (int e = 0; e < 8; e += 2)
+    acc = __builtin_amdgcn_fdot2_f32_bf16(b2{v[e], v[e + 1]}, one, acc, false);
+  return acc;
+}
+
 // Block = WGM x WGN waves, each owning (SM*32) x (SN*32) of C.
-template <typename T, typename TC, bool TA, bool TB, int WGM, int WGN, int SM, int SN, int OCC>
+// BSUM: the column sums of op(B) over this launch's K range are written too, as fp32
+// bsum[batch][N] (the bias gradient of a Linear layer next to its weight gradient
+// dW = X^T dY, where op(B) = dY).  Every wave adds up the B fragments it multiplies
+// (one v_dot2 per pair of elements, beside the MFMAs); the waves of the first block
+// row that hold rows 0.. of C, which between them see every k of every column once,
+// store theirs.
+template <typename T, typename TC, bool TA, bool TB, int WGM, int WGN, int SM, int SN, int OCC,
+          bool BSUM = false>
 __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_v3(
     int64_t M, int64_t N, int64_t K, float alpha, const T* __restrict__ A, int64_t lda,
     int64_t sa, const T* __restrict__ B, int64_t ldb, int64_t sb, float beta,
     TC* __restrict__ C, int64_t ldc, int64_t sc,
-    const float* __restrict__ bias) {
+    const float* __restrict__ bias, float* __restrict__ bsum) {
   constexpr int NW = WGM * WGN, TBM = WGM * SM * 32, TBN = WGN * SN * 32;
   constexpr int ATILE = TBM * V3_BK * 2, BTILE = TBN * V3_BK * 2;
   __shared__ __attribute__((aligned(1024))) char a0[ATILE];
@@ -615,6 +640,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_v3(
     for (int j = 0; j < SN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  float bsums[SN];  // BSUM: this lane's partial column sums (8 k per fragment and k-step)
+#pragma unroll
+  for (int j = 0; j < SN; ++j) bsums[j] = 0.f;
   // A is [M][K] (lda) or, transposed, [K][M]; B is [K][N] or, transposed, [N][K].
   // Tile origins: k-contiguous operands start at (row m0|n0, column k0), the others
   // at (row k0, column m0|n0); the clamps at the M / N edge are per block.
@@ -658,6 +686,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_v3(
       for (int ks = 0; ks < V3_BK / 16; ++ks) {
         const int cur = ks & 1;
         int nr = 0;
+        if constexpr (BSUM) {
+#pragma unroll
+          for (int j = 0; j < SN; ++j) bsums[j] = frag_sum(fr[cur][SM + j], bsums[j]);
+        }
 #pragma unroll
         for (int i = 0; i < SM; ++i)
 #pragma unroll
@@ -685,6 +717,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_v3(
         for (int i = 0; i < SM; ++i) af[i] = fa.get(as, wm, i, ks, l32);
 #pragma unroll
         for (int j = 0; j < SN; ++j) bf[j] = fb.get(bs, wn, j, ks, l32);
+        if constexpr (BSUM) {
+#pragma unroll
+          for (int j = 0; j < SN; ++j) bsums[j] = frag_sum(bf[j], bsums[j]);
+        }
 #pragma unroll
         for (int i = 0; i < SM; ++i)
 #pragma unroll
@@ -704,6 +740,17 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_v3(
     const bool more2 = k0 + 2 * V3_BK < K;
     mul(a1, b1, more2, k0 + 2 * V3_BK, a0, b0);
     if (!more2) break;
+  }
+  if constexpr (BSUM) {
+    if (tm == 0 && wm == 0) {
+      // lanes l32 and l32 + 32 hold the two 8-element k halves of column l32
+#pragma unroll
+      for (int j = 0; j < SN; ++j) {
+        const float v = bsums[j] + __shfl_xor(bsums[j], 32);
+        const int64_t col = n0 + wn + j * 32 + l32;
+        if (lh == 0 && col < N) bsum[bz * N + col] = v;
+      }
+    }
   }
   if (m0 + TBM <= M && n0 + TBN <= N) {
     // Full tile: each wave stages one slab of HR rows (32, or 16 when two 32-row
@@ -787,10 +834,26 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_v3(
 // (256 x 128, one block per CU, two waves per SIMD) when the problem has at least
 // one such tile per CU, else 2 x 2 waves (128 x 128, two blocks per CU).
 
+// Whether a 16-bit GEMM runs on the DMA-staged kernel (k_gemm_v3).
+bool v3_ok(int elem, int ta, int tb, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+           int64_t sa, const void* B, int64_t ldb, int64_t sb) {
+  const int VE = 16 / elem;
+  const bool vec = tg_aligned16(A) && tg_aligned16(B) && lda % VE == 0 && ldb % VE == 0 &&
+                   sa % VE == 0 && sb % VE == 0;
+  // The DMA addresses each operand (one batch entry) through a 2 GiB buffer window.
+  const int64_t a_span = (ta ? K * lda : M * lda) * (int64_t)elem;
+  const int64_t b_span = (tb ? N * ldb : K * ldb) * (int64_t)elem;
+  return elem == 2 && vec && M >= 64 && N >= 64 && K >= 64 && M % 8 == 0 && N % 8 == 0 &&
+         K % V3_BK == 0 && a_span < (int64_t{1} << 31) && b_span < (int64_t{1} << 31);
+}
+
+// bsum (non-null only where v3_ok holds, with ta = 1, tb = 0): also write the column
+// sums of B over each batch entry's K range to bsum[batch][N].
 template <typename T, typename TC>
 int launch(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const void* A,
            int64_t lda, int64_t sa, const void* B, int64_t ldb, int64_t sb, float beta, void* C,
-           int64_t ldc, int64_t sc, int64_t batch, hipStream_t s, const float* bias = nullptr) {
+           int64_t ldc, int64_t sc, int64_t batch, hipStream_t s, const float* bias = nullptr,
+           float* bsum = nullptr) {
   constexpr int VE = 16 / sizeof(T);
   const bool vec = tg_aligned16(A) && tg_aligned16(B) && lda % VE == 0 && ldb % VE == 0 &&
                    sa % VE == 0 && sb % VE == 0;
@@ -800,12 +863,12 @@ int launch(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const v
   TC* c = (TC*)C;
   // v2 stages whole 16-byte vectors along every contiguous dimension: extents must be
   // multiples of 8 so no vector straddles a row end.
+  if (bsum && !(ta && !tb && v3_ok((int)sizeof(T), ta, tb, M, N, K, A, lda, sa, B, ldb, sb))) {
+    tg_set_error("tg_gemm: fused column sums need the DMA-staged 16-bit kernel");
+    return TG_ERR_UNSUPPORTED;
+  }
   if constexpr (sizeof(T) == 2) {
-  // The DMA addresses each operand (one batch entry) through a 2 GiB buffer window.
-  const int64_t a_span = (ta ? K * lda : M * lda) * (int64_t)sizeof(T);
-  const int64_t b_span = (tb ? N * ldb : K * ldb) * (int64_t)sizeof(T);
-  if (vec && M >= 64 && N >= 64 && K >= 64 && M % 8 == 0 && N % 8 == 0 && K % V3_BK == 0 &&
-      a_span < (int64_t{1} << 31) && b_span < (int64_t{1} << 31)) {
+  if (v3_ok((int)sizeof(T), ta, tb, M, N, K, A, lda, sa, B, ldb, sb)) {
     // Block shapes (waves x per-wave tile): 4x2 waves of 64x128 (256x256, one block
     // and two waves per SIMD) when the problem has enough such tiles to fill the CUs:
     // fewer global tile bytes per flop than the smaller shapes.  (The same tile as 2x2
@@ -820,8 +883,15 @@ int launch(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const v
   do {                                                                                     \
     constexpr int TBM = WGM * SM * 32, TBN = WGN * SN * 32;                                \
     dim3 g3((unsigned)((N + TBN - 1) / TBN), (unsigned)((M + TBM - 1) / TBM), (unsigned)batch); \
+    if constexpr (TA_ && !TB_) {                                                           \
+      if (bsum) {                                                                          \
+        k_gemm_v3<T, TC, TA_, TB_, WGM, WGN, SM, SN, OCC, true><<<g3, 64 * WGM * WGN, 0, s>>>( \
+            M, N, K, alpha, a, lda, sa, b, ldb, sb, beta, c, ldc, sc, bias, bsum);          \
+        break;                                                                             \
+      }                                                                                    \
+    }                                                                                      \
     k_gemm_v3<T, TC, TA_, TB_, WGM, WGN, SM, SN, OCC><<<g3, 64 * WGM * WGN, 0, s>>>(        \
-        M, N, K, alpha, a, lda, sa, b, ldb, sb, beta, c, ldc, sc, bias);                    \
+        M, N, K, alpha, a, lda, sa, b, ldb, sb, beta, c, ldc, sc, bias, nullptr);           \
   } while (0)
 #define TG_G3(TA_, TB_)                                          \
   do {                                                           \
@@ -922,6 +992,179 @@ int gemm_dispatch(const char* who, int dtype_ab, int dtype_c, int trans_a, int t
   return TG_ERR_UNSUPPORTED;
 }
 }  // namespace
+
+namespace {
+// Finishing pass of the weight-gradient entry: dW[i] (+)= sum_s parts[s][i] over the
+// M*N elements (when K was split), then db[c] (+)= sum_s bparts[s][c].  A thread owns 4
+// adjacent elements and adds the S partials in order with 4 rows of loads in flight,
+// so the result does not depend on scheduling.
+constexpr int kFinBlock = 256;
+
+template <typename TO>
+__device__ __forceinline__ void fin_store(void* out, int64_t i, const float a[4], int acc) {
+  TO* o = reinterpret_cast<TO*>(out) + i;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float v = a[j];
+    if (acc) v += tg_to_float(o[j]);
+    o[j] = tg_from_float<TO>(v);
+  }
+}
+
+__global__ __launch_bounds__(kFinBlock) void k_wgrad_finish(
+    const float* __restrict__ parts, int S, int64_t MN, void* dW, int dtw, int accw,
+    const float* __restrict__ bparts, int64_t N, void* db, int dtb, int accb) {
+  const int64_t q = (int64_t)blockIdx.x * kFinBlock + threadIdx.x;
+  const int64_t qw = MN / 4;
+  const float* in;
+  int64_t stride, i;
+  void* out;
+  int dt, acc;
+  if (q < qw) {
+    in = parts, stride = MN, i = q * 4, out = dW, dt = dtw, acc = accw;
+  } else {
+    i = (q - qw) * 4;
+    if (db == nullptr || i >= N) return;
+    in = bparts, stride = N, out = db, dt = dtb, acc = accb;
+  }
+  float a[4] = {0.f, 0.f, 0.f, 0.f};
+  int r = 0;
+  for (; r + 4 <= S; r += 4) {
+    float4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const float4*>(in + (r + u) * stride + i);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      a[0] += v[u].x;
+      a[1] += v[u].y;
+      a[2] += v[u].z;
+      a[3] += v[u].w;
+    }
+  }
+  for (; r < S; ++r) {
+    const float4 v = *reinterpret_cast<const float4*>(in + r * stride + i);
+    a[0] += v.x;
+    a[1] += v.y;
+    a[2] += v.z;
+    a[3] += v.w;
+  }
+  if (dt == TG_F32) fin_store<float>(out, i, a, acc);
+  else if (dt == TG_F16) fin_store<tg_half>(out, i, a, acc);
+  else fin_store<tg_bf16>(out, i, a, acc);
+}
+
+// K split of a weight gradient whose output has too few 128x128 tiles for two per CU
+// (qkv/out projections [1024, 1024] and FC weights [1024, 4096] over 8192 tokens), or
+// whose K is very long: returns s with K % s == 0 and (K / s) % 64 == 0, or 1.
+int64_t wgrad_split(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N % 4 != 0) return 1;  // the finish reads 4-element groups
+  const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128);
+  const int64_t cus = tg_num_cus();
+  int64_t want;
+  if (K >= 16384 && tiles < 4 * cus) want = 2;
+  else if (tiles >= 2 * cus || K < 2048) return 1;
+  else want = std::min((2 * cus + tiles - 1) / tiles, K / 1024);
+  for (int64_t s = want; s > 1; --s)
+    if (K % s == 0 && (K / s) % 64 == 0) return s;
+  return 1;
+}
+
+size_t al256(size_t n) { return (n + 255) & ~size_t{255}; }
+
+struct WgradPlan {
+  int64_t split;
+  size_t parts, bparts, red;  // byte offsets-to-be: sizes of the three workspace regions
+};
+
+WgradPlan wgrad_plan(int dtype_ab, int64_t M, int64_t N, int64_t K, bool has_b) {
+  WgradPlan p{1, 0, 0, 0};
+  if (dtype_ab != TG_F64) p.split = wgrad_split(M, N, K);
+  if (p.split > 1) p.parts = al256((size_t)(p.split * M * N) * sizeof(float));
+  if (has_b) {
+    p.bparts = al256((size_t)(p.split * N) * sizeof(float));
+    p.red = al256(tg_reduce_rows_workspace(K, N));
+  }
+  return p;
+}
+}  // namespace
+
+TG_EXPORT size_t tg_gemm_wgrad_workspace(int dtype_ab, int64_t M, int64_t N, int64_t K,
+                                         int with_bias) {
+  if (N <= 0 || M < 0 || K < 0) return 0;
+  const WgradPlan p = wgrad_plan(dtype_ab, M, N, K, with_bias != 0);
+  return p.parts + p.bparts + p.red;
+}
+
+TG_EXPORT int tg_gemm_wgrad(int dtype_ab, int64_t M, int64_t N, int64_t K, const void* X,
+                            int64_t ldx, const void* G, int64_t ldg, int dtype_w, void* dW,
+                            int64_t ldw, int acc_w, int dtype_b, void* db, int acc_b,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  TG_REQUIRE(M >= 0 && N >= 0 && K >= 0, "tg_gemm_wgrad: negative extent");
+  if (M == 0 || N == 0) {
+    if (N == 0 || db == nullptr) return TG_OK;
+    // no weight, only the bias gradient
+    return tg_reduce_rows(dtype_ab, G, dtype_b, db, K, N, acc_b, workspace, workspace_bytes,
+                          stream);
+  }
+  TG_REQUIRE(dW, "tg_gemm_wgrad: null dW");
+  TG_REQUIRE(ldw >= N && ldx >= M && ldg >= N, "tg_gemm_wgrad: bad leading dimension");
+  TG_REQUIRE(dtype_w == TG_F32 || dtype_w == dtype_ab, "tg_gemm_wgrad: dW dtype %d", dtype_w);
+  TG_REQUIRE(!db || dtype_b == TG_F32 || dtype_b == dtype_ab, "tg_gemm_wgrad: db dtype %d",
+             dtype_b);
+  TG_REQUIRE(dtype_ab != TG_F64 || (dtype_w == TG_F64 && (!db || dtype_b == TG_F64)),
+             "tg_gemm_wgrad: fp64 operands take fp64 gradients");
+  if (K > 0) TG_REQUIRE(X && G, "tg_gemm_wgrad: null operand");
+  WgradPlan p = wgrad_plan(dtype_ab, M, N, K, db != nullptr);
+  if (ldw != N) p.split = 1;  // the split finish writes a dense dW
+  TG_REQUIRE(workspace_bytes >= p.parts + p.bparts + p.red && (workspace || !p.parts),
+             "tg_gemm_wgrad: workspace of %zu bytes, need %zu", workspace_bytes,
+             p.parts + p.bparts + p.red);
+  char* ws = static_cast<char*>(workspace);
+  float* parts = reinterpret_cast<float*>(ws);
+  float* bparts = reinterpret_cast<float*>(ws + p.parts);
+  void* red = ws + p.parts + p.bparts;
+  hipStream_t s = tg_stream(stream);
+  const int64_t S = p.split, kc = K / S;
+  const float bw = acc_w ? 1.f : 0.f;
+  const bool fused = db && K > 0 && (dtype_ab == TG_F16 || dtype_ab == TG_BF16) &&
+                     v3_ok(2, 1, 0, M, N, kc, X, ldx, kc * ldx, G, ldg, kc * ldg);
+  int rc;
+  if (fused) {
+#define TG_WG(T)                                                                              \
+  if (S > 1)                                                                                  \
+    rc = launch<T, float>(1, 0, M, N, kc, 1.f, X, ldx, kc * ldx, G, ldg, kc * ldg, 0.f, parts, \
+                          N, M * N, S, s, nullptr, bparts);                                   \
+  else if (dtype_w == TG_F32)                                                                 \
+    rc = launch<T, float>(1, 0, M, N, K, 1.f, X, ldx, 0, G, ldg, 0, bw, dW, ldw, 0, 1, s,       \
+                          nullptr, bparts);                                                   \
+  else                                                                                        \
+    rc = launch<T, T>(1, 0, M, N, K, 1.f, X, ldx, 0, G, ldg, 0, bw, dW, ldw, 0, 1, s, nullptr, \
+                      bparts)
+    if (dtype_ab == TG_F16) { TG_WG(tg_half); } else { TG_WG(tg_bf16); }
+#undef TG_WG
+    if (rc != TG_OK) return rc;
+  } else if (S > 1) {
+    rc = gemm_dispatch("tg_gemm_wgrad", dtype_ab, TG_F32, 1, 0, M, N, kc, 1.f, X, ldx, kc * ldx,
+                       G, ldg, kc * ldg, 0.f, parts, N, M * N, S, nullptr, stream);
+    if (rc != TG_OK) return rc;
+  } else {
+    rc = gemm_dispatch("tg_gemm_wgrad", dtype_ab, dtype_w, 1, 0, M, N, K, 1.f, X, ldx, 0, G, ldg,
+                       0, bw, dW, ldw, 0, 1, nullptr, stream);
+    if (rc != TG_OK) return rc;
+  }
+  const int64_t MN = S > 1 ? M * N : 0;
+  const int64_t nb = fused ? N : 0;
+  if (MN + nb > 0) {
+    const int64_t groups = (MN + nb) / 4;
+    k_wgrad_finish<<<(unsigned)((groups + kFinBlock - 1) / kFinBlock), kFinBlock, 0, s>>>(
+        parts, (int)S, MN, dW, dtype_w, acc_w, bparts, N, fused ? db : nullptr, dtype_b, acc_b);
+    rc = tg_check_launch("tg_gemm_wgrad");
+    if (rc != TG_OK) return rc;
+  }
+  if (db && !fused)
+    return tg_reduce_rows(dtype_ab, G, dtype_b, db, K, N, acc_b, red, p.red, stream);
+  return TG_OK;
+}
 
 TG_EXPORT int tg_gemm(int dtype_ab, int dtype_c, int trans_a, int trans_b, int64_t M, int64_t N,
                       int64_t K, float alpha, const void* A, int64_t lda, int64_t stride_a,

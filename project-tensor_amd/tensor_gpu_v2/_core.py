@@ -1037,18 +1037,33 @@ def _linear(x, w, b):
                         x._accumulate(da.reshape(buf.shape), True)
                     else:
                         _copy_into(buf, da.reshape(buf.shape))
-            if w._has_grad():
-                buf, acc = w._grad_target()
-                if _direct_out(buf.dtype, cdt):
-                    L.matmul2d(A2, G2, out=buf.view(K, N), trans_a=True, beta=1.0 if acc else 0.0)
+            fuse = (w._has_grad() and b is not None and b._has_grad() and g.dtype == cdt
+                    and b.data.numel() == N and b.data.shape[-1] == N)
+            if fuse:
+                # dW and db from one pass over the output gradient
+                wbuf, wacc = w._grad_target()
+                bbuf, bacc = b._grad_target()
+                if _direct_out(wbuf.dtype, cdt) and _direct_out(bbuf.dtype, cdt):
+                    L.wgrad(A2, G2, wbuf.view(K, N), wacc, bbuf.view(N), bacc)
                 else:
-                    dw = L.matmul2d(A2, G2, trans_a=True, out_dtype=_wide(cdt))
-                    if acc:
-                        w._accumulate(dw, True)
-                    else:
-                        _copy_into(buf, dw)
+                    _wgrad_into(G2, wbuf, wacc)
+                    L.reduce_rows(G2, bbuf.view(N), bacc)
+                return
+            if w._has_grad():
+                _wgrad_into(G2, *w._grad_target())
             if b is not None and b._has_grad():
                 b._accumulate_unb(g)
+
+        def _wgrad_into(G2, buf, acc):
+            """w's gradient buffer (+)= A2^T @ G2."""
+            if _direct_out(buf.dtype, cdt):
+                L.matmul2d(A2, G2, out=buf.view(K, N), trans_a=True, beta=1.0 if acc else 0.0)
+            else:
+                dw = L.matmul2d(A2, G2, trans_a=True, out_dtype=_wide(cdt))
+                if acc:
+                    w._accumulate(dw, True)
+                else:
+                    _copy_into(buf, dw)
         out._backward = _backward
     return out
 

@@ -80,6 +80,9 @@ SIGNATURES = {
                        _i64, _i64, _f32, _vp, _i64, _i64, _i64, _vp]),
     "tg_gemm_bias": (_i32, [_i32, _i32, _i32, _i32, _i64, _i64, _i64, _f32, _vp, _i64, _vp, _i64,
                             _vp, _vp, _i64, _vp]),
+    "tg_gemm_wgrad_workspace": (_sz, [_i32, _i64, _i64, _i64, _i32]),
+    "tg_gemm_wgrad": (_i32, [_i32, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _i32, _vp, _i64, _i32,
+                             _i32, _vp, _i32, _vp, _sz, _vp]),
     "tg_flash_attn_fwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                  _f32, _i32, _vp]),
     "tg_flash_attn_fwd_layout": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
@@ -741,6 +744,36 @@ def gemm_bias(a, b, bias, out, trans_b=False):
         dtype_code(a), dtype_code(out), 0, int(bool(trans_b)), M, N, K, 1.0, ptr(a), K, ptr(b),
         b.shape[1], ptr(bias), ptr(out), N, stream_handle()))
     return out
+
+
+def wgrad(x, g, dw, acc_w, db=None, acc_b=False):
+    """dw (+)= x^T @ g and db (+)= g.sum(0) for x [K, M], g [K, N] contiguous (the weight
+    and bias gradients of a Linear layer over K tokens); one GEMM pass over g for both
+    with 16-bit operands."""
+    for n, t in (("x", x), ("g", g), ("dw", dw)):
+        _dev(t, n)
+    if db is not None:
+        _dev(db, "db")
+    if x.dim() != 2 or g.dim() != 2 or x.shape[0] != g.shape[0]:
+        raise ValueError(f"wgrad: x {tuple(x.shape)} and g {tuple(g.shape)} must be [K, M], [K, N]")
+    if x.dtype != g.dtype:
+        raise TypeError(f"wgrad: x and g dtypes differ ({x.dtype} vs {g.dtype})")
+    K, M = x.shape
+    N = g.shape[1]
+    if tuple(dw.shape) != (M, N) or not dw.is_contiguous():
+        raise ValueError(f"wgrad: dw must be a contiguous [{M}, {N}] buffer")
+    if db is not None and (db.numel() != N or not db.is_contiguous()):
+        raise ValueError(f"wgrad: db must be a contiguous buffer of {N} elements")
+    lib = load()
+    ensure_device(dw.device.index)
+    ws = workspace(lib.tg_gemm_wgrad_workspace(dtype_code(x), M, N, K, int(db is not None)),
+                   dw.device)
+    _check("tg_gemm_wgrad", lib.tg_gemm_wgrad(
+        dtype_code(x), M, N, K, ptr(x), M, ptr(g), N, dtype_code(dw), ptr(dw), N,
+        int(bool(acc_w)), dtype_code(db) if db is not None else 0,
+        ptr(db) if db is not None else None, int(bool(acc_b)), ptr(ws), ws.numel(),
+        stream_handle()))
+    return dw
 
 
 _CUS = {}
