@@ -176,6 +176,11 @@ int tg_adam_step_lowp(int ntensors, float* const* params, const float* const* gr
  * tensor has one. */
 int tg_unscale_check(int ntensors, int dtype, void* const* grads, const int64_t* numel, float mul,
                      int write, int* flags, void* stream);
+/* GradScaler.unscale_ with zero_nan_grads (_nn.py:1816-1829): every gradient i whose
+ * device flag flags[i] (from tg_unscale_check) is non-zero is zeroed whole, decided on
+ * the device, so the flags need no read-back before the next kernels. */
+int tg_zero_flagged(int ntensors, int dtype, void* const* grads, const int64_t* numel,
+                    const int* flags, void* stream);
 /* clip_grad_norm_ (_nn.py:1563-1626) reduction: out[0] (device double) =
  * sum g^2 (kind 0), max|g| (kind 1) or sum |g|^p (kind 2) over finite entries;
  * flags[i] |= 1 when tensor i has non-finite entries. */

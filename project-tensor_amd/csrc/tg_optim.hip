@@ -355,6 +355,27 @@ __global__ __launch_bounds__(kBlock) void k_zero_nonfinite(MtArgs A) {
   }
 }
 
+// Every tensor whose flag is set is zeroed whole (GradScaler.unscale_ clearing a
+// gradient that holds a non-finite value).  The flags are read once per block into
+// LDS; with none set every block exits after that read.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_zero_flagged(MtArgs A, const int* __restrict__ flags) {
+  __shared__ int fl[kMaxT];
+  if (threadIdx.x < A.ntensors) fl[threadIdx.x] = flags[A.fidx[threadIdx.x]];
+  __syncthreads();
+  T z;
+  if constexpr (sizeof(T) == 8) z = 0.0;
+  else z = tg_from_float<T>(0.f);
+  for (int t = 0; t < A.ntensors; ++t) {
+    if (fl[t] == 0) continue;
+    T* __restrict__ g = (T*)A.a[t];
+    const int64_t n = A.n[t];
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * kBlock)
+      g[i] = z;
+  }
+}
+
 __global__ void k_zero_ints(int* p, int n) {
   for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0;
 }
@@ -570,6 +591,27 @@ TG_EXPORT int tg_grad_norm(int ntensors, int dtype, void* const* grads, const in
   else
     k_norm_final<0><<<1, kNormFinal, 0, s>>>(part, nb_total, out);
   return tg_check_launch("tg_grad_norm final");
+}
+
+// Zero every gradient i whose device flag flags[i] is non-zero (as set by
+// tg_unscale_check), without a read-back.
+TG_EXPORT int tg_zero_flagged(int ntensors, int dtype, void* const* grads, const int64_t* numel,
+                              const int* flags, void* stream) {
+  TG_REQUIRE(ntensors >= 0, "tg_zero_flagged: negative tensor count");
+  if (ntensors == 0) return TG_OK;
+  TG_REQUIRE(grads && numel && flags, "tg_zero_flagged: null argument");
+  TG_REQUIRE(dtype == TG_F32 || dtype == TG_F16 || dtype == TG_BF16 || dtype == TG_F64,
+             "tg_zero_flagged: unsupported dtype %d", dtype);
+  hipStream_t s = tg_stream(stream);
+  const unsigned grid = (unsigned)tg_num_cus();
+  return for_each_launch(ntensors, grads, nullptr, nullptr, nullptr, nullptr, nullptr, numel,
+                         [&](const MtArgs& A, int64_t) {
+                           if (dtype == TG_F32) k_zero_flagged<float><<<grid, kBlock, 0, s>>>(A, flags);
+                           else if (dtype == TG_F16) k_zero_flagged<tg_half><<<grid, kBlock, 0, s>>>(A, flags);
+                           else if (dtype == TG_BF16) k_zero_flagged<tg_bf16><<<grid, kBlock, 0, s>>>(A, flags);
+                           else k_zero_flagged<double><<<grid, kBlock, 0, s>>>(A, flags);
+                           return tg_check_launch("tg_zero_flagged");
+                         });
 }
 
 // Replace non-finite gradient entries by zero.

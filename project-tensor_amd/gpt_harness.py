@@ -79,6 +79,10 @@ class Trainer:
                  strict_chain_rule=False):
         self.model = model
         params = model.parameters()
+        # every parameter, the tied head weight included (its gradient is transferred
+        # to the embedding each step and must start from zero): the module tree is
+        # fixed, so it is walked once here rather than per step
+        self._all = params
         # the tied head weight is a view of the embedding: optimise the source only
         self.params = [p for p in params if not _is_tied(p)]
         self.opt = tg.AdamW(self.params, lr=lr, weight_decay=weight_decay)
@@ -87,8 +91,7 @@ class Trainer:
         self.loss_fn = tg.CrossEntropyLoss(strict_chain_rule=strict_chain_rule)
 
     def step(self, ids, targets):
-        self.opt.zero_grad()
-        for p in self.model.parameters():
+        for p in self._all:
             p.zero_grad()
         with tg.autocast():
             logits = self.model(ids)

@@ -76,6 +76,7 @@ SIGNATURES = {
     "tg_grad_norm_workspace": (_sz, [_i32, _vp]),
     "tg_grad_norm": (_i32, [_i32, _i32, _vp, _vp, _i32, _f32, _vp, _vp, _vp, _sz, _vp]),
     "tg_zero_nonfinite": (_i32, [_i32, _i32, _vp, _vp, _vp]),
+    "tg_zero_flagged": (_i32, [_i32, _i32, _vp, _vp, _vp, _vp]),
     "tg_gemm": (_i32, [_i32, _i32, _i32, _i32, _i64, _i64, _i64, _f32, _vp, _i64, _i64, _vp,
                        _i64, _i64, _f32, _vp, _i64, _i64, _i64, _vp]),
     "tg_gemm_bias": (_i32, [_i32, _i32, _i32, _i32, _i64, _i64, _i64, _f32, _vp, _i64, _vp, _i64,
@@ -552,9 +553,18 @@ def adam_step(params, grads, exp_avg, exp_avg_sq, max_exp_avg_sq, lr, beta1, bet
     """Multi-tensor Adam/AdamW step.  `lowp`, if given, is a list parallel to `params`
     of None or a contiguous fp16/bf16 tensor of the param's size (one dtype for the
     list) that receives the updated param rounded to that dtype in the same pass."""
+    adam_prepare(params, grads, exp_avg, exp_avg_sq, max_exp_avg_sq, lowp)(
+        lr, beta1, beta2, eps, weight_decay, bias_correction1, bias_correction2)
+
+
+def adam_prepare(params, grads, exp_avg, exp_avg_sq, max_exp_avg_sq, lowp=None):
+    """The checks and pointer arrays of adam_step for these buffers, done now; returns
+    launch(lr, beta1, beta2, eps, weight_decay, bias_correction1, bias_correction2),
+    which only enqueues the kernel.  An optimizer prepares while the device is still
+    busy and launches after the last host read-back of the step."""
     n = len(params)
     if n == 0:
-        return
+        return lambda *a: None
     arrs, numels, numel_arr = _adam_state(params, exp_avg, exp_avg_sq, max_exp_avg_sq)
     if len(grads) != n:
         raise ValueError("adam_step: param/grad list lengths differ")
@@ -565,16 +575,15 @@ def adam_step(params, grads, exp_avg, exp_avg_sq, max_exp_avg_sq, lr, beta1, bet
             raise TypeError(f"adam_step: gradients must be {pdt} like their params")
         if g.numel() != k:
             raise ValueError("adam_step: param/grad/state sizes differ")
-    ensure_device(params[0].device.index)
-    args = (arrs[0], _ptr_array(grads), arrs[1], arrs[2], arrs[3], numel_arr,
-            float(lr), float(beta1), float(beta2), float(eps), float(weight_decay),
-            float(bias_correction1), float(bias_correction2))
+    dev = params[0].device.index
+    garr = _ptr_array(grads)
+    keep = (list(grads),)  # the pointer array's buffers stay alive with the launcher
+    lib = load()
     if pdt == torch.float64:
         if lowp is not None and any(t is not None for t in lowp):
             raise TypeError("adam_step: low-precision copies are for fp32 params")
-        _check("tg_adam_step_f64", load().tg_adam_step_f64(n, *args, stream_handle()))
-        return
-    if lowp is not None and any(t is not None for t in lowp):
+        fn, extra, name = lib.tg_adam_step_f64, (), "tg_adam_step_f64"
+    elif lowp is not None and any(t is not None for t in lowp):
         if len(lowp) != n:
             raise ValueError("adam_step: lowp list length differs from params")
         lp = [t for t in lowp if t is not None]
@@ -588,10 +597,20 @@ def adam_step(params, grads, exp_avg, exp_avg_sq, max_exp_avg_sq, lr, beta1, bet
             if t.numel() != p.numel() or not t.is_contiguous():
                 raise ValueError("adam_step: low-precision copy must be contiguous and of its "
                                  "param's size")
-        _check("tg_adam_step_lowp", load().tg_adam_step_lowp(
-            n, *args, dtype_code(lp[0]), _ptr_array(lowp), stream_handle()))
-        return
-    _check("tg_adam_step", load().tg_adam_step(n, *args, stream_handle()))
+        fn, extra, name = lib.tg_adam_step_lowp, (dtype_code(lp[0]), _ptr_array(lowp)), \
+            "tg_adam_step_lowp"
+        keep = keep + (list(lowp),)
+    else:
+        fn, extra, name = lib.tg_adam_step, (), "tg_adam_step"
+
+    def launch(lr, beta1, beta2, eps, weight_decay, bias_correction1, bias_correction2):
+        ensure_device(dev)
+        _check(name, fn(n, arrs[0], garr, arrs[1], arrs[2], arrs[3], numel_arr, float(lr),
+                        float(beta1), float(beta2), float(eps), float(weight_decay),
+                        float(bias_correction1), float(bias_correction2), *extra,
+                        stream_handle()))
+        return keep
+    return launch
 
 
 def _group_by_dtype(ts):
@@ -648,6 +667,54 @@ def unscale_check(grads, mul, write=True, readback=True):
             out[i] = host[off + j]
         off += len(idx)
     return out
+
+
+def unscale_deferred(grads, mul):
+    """GradScaler.unscale_ without a synchronisation: grads *= mul, every tensor that
+    held or now holds a non-finite value zeroed on the device, and the per-tensor
+    flags copied to host memory behind an event.  Returns resolve(), which waits for
+    that copy and returns the flags (host list of ints, as unscale_check's) — at no
+    cost once the stream has been synchronised for another read-back."""
+    n = len(grads)
+    if n == 0:
+        return lambda: []
+    for t in grads:
+        _dev(t, "grad")
+    dev = grads[0].device
+    ensure_device(dev.index)
+    # a fresh device buffer per call (not the shared scratch): a later call must not
+    # overwrite flags that are still being copied out
+    flags = torch.empty(n, dtype=torch.int32, device=dev)
+    lib = load()
+    groups = _group_by_dtype(grads)
+    off = 0
+    for dt, idx in groups.items():
+        sub = [grads[i] for i in idx]
+        fl = flags[off: off + len(sub)]
+        off += len(sub)
+        gp, ne = _ptr_array(sub), _numel_array(sub)
+        _check("tg_unscale_check", lib.tg_unscale_check(
+            len(sub), dtype_code(sub[0]), gp, ne, float(mul), 1, ptr(fl), stream_handle()))
+        _check("tg_zero_flagged", lib.tg_zero_flagged(
+            len(sub), dtype_code(sub[0]), gp, ne, ptr(fl), stream_handle()))
+    host = torch.empty(n, dtype=torch.int32, pin_memory=True)
+    host.copy_(flags, non_blocking=True)
+    flags_keep = [flags]  # held until the copy is known to be done
+    ev = torch.cuda.Event()
+    ev.record()
+
+    def resolve():
+        ev.synchronize()
+        del flags_keep[:]
+        h = host.tolist()
+        out = [0] * n
+        o = 0
+        for dt, idx in groups.items():
+            for j, i in enumerate(idx):
+                out[i] = h[o + j]
+            o += len(idx)
+        return out
+    return resolve
 
 
 def grad_norm(grads, norm_kind, p=2.0):

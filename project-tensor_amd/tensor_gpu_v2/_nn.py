@@ -579,23 +579,31 @@ class Adam:
             L.scale_(grads, max_norm / (total + 1e-6))
         return total
 
-    def _apply(self, lr, wd):
-        self.t += 1
-        bc1 = 1 - self.beta1 ** self.t
-        bc2 = 1 - self.beta2 ** self.t
-        # one multi-tensor step per parameter dtype: fp32 (with the autocast copies) and
-        # fp64 (parameters made from float64 arrays, updated in double)
+    def _plan(self):
+        """Launchers of the step for the current gradient buffers: one multi-tensor
+        launch per parameter dtype, fp32 (with the autocast copies) and fp64
+        (parameters made from float64 arrays, updated in double), with every check and
+        pointer array done here.  Returns (gradient buffers, lowp generation,
+        launchers), or gradient buffers None when a gradient was converted to its
+        parameter's dtype (the launcher then holds a copy that an in-place change of
+        the gradient would not reach, so the plan is only good for an immediate
+        launch); a plan is reused while its buffers and generation are unchanged."""
         groups = {}
+        gbufs = []
+        copied = False
         for i, p in enumerate(self.params):
             if not p._has_grad():
+                gbufs.append(None)
                 continue
             dt = p.data.dtype
             if dt not in (torch.float32, torch.float64) or not p.data.is_contiguous():
                 raise TypeError("Adam: parameters must be contiguous float32 or float64 "
                                 "device tensors")
             g = p.grad
+            gbufs.append(p._g)
             if g.dtype != dt:
                 g = _as(g, dt)
+                copied = True
             ps, gs, ms, vs, vms = groups.setdefault(dt, ([], [], [], [], []))
             ps.append(p.data)
             gs.append(g)
@@ -603,10 +611,34 @@ class Adam:
             vs.append(self.v[i])
             if self.amsgrad:
                 vms.append(self.v_max[i])
-        for dt, (ps, gs, ms, vs, vms) in groups.items():
-            L.adam_step(ps, gs, ms, vs, vms if self.amsgrad else None, lr, self.beta1,
-                        self.beta2, self.eps, wd, bc1, bc2,
-                        lowp=_lowp.refresh_targets(ps) if dt == torch.float32 else None)
+        launchers = [
+            L.adam_prepare(ps, gs, ms, vs, vms if self.amsgrad else None,
+                           lowp=_lowp.refresh_targets(ps) if dt == torch.float32 else None)
+            for dt, (ps, gs, ms, vs, vms) in groups.items()]
+        return (None if copied else gbufs), _lowp._GEN[0], launchers
+
+    def _prepare(self):
+        """Plan the next step now (GradScaler.unscale_ calls this while the device is
+        still busy with the backward), so the step after the last read-back only
+        launches."""
+        self._planned = self._plan()
+
+    def _apply(self, lr, wd):
+        self.t += 1
+        bc1 = 1 - self.beta1 ** self.t
+        bc2 = 1 - self.beta2 ** self.t
+        plan = getattr(self, "_planned", None)
+        self._planned = None
+        if plan is not None:
+            gbufs, gen, _ = plan
+            if gbufs is None or gen != _lowp._GEN[0] or len(gbufs) != len(self.params) or any(
+                    b is not (p._g if p._has_grad() else None)
+                    for b, p in zip(gbufs, self.params)):
+                plan = None
+        if plan is None:
+            plan = self._plan()
+        for launch in plan[2]:
+            launch(lr, self.beta1, self.beta2, self.eps, wd, bc1, bc2)
 
     def step(self, clip_grad_norm=None):
         if clip_grad_norm is not None:
@@ -694,8 +726,11 @@ def clip_grad_value_(parameters, clip_value):
 # ============================================================================ GradScaler
 class GradScaler:
     """Dynamic loss scaling (_nn.py:1713-1912).  unscale_ is one multi-tensor
-    kernel pass (scale + non-finite flags) and one flag read-back instead of the
-    reference's per-parameter host checks; the scale state machine is unchanged."""
+    kernel pass (scale + non-finite flags) instead of the reference's per-parameter
+    host checks; with zero_nan_grads the flagged gradients are zeroed on the device and
+    the flags are read back only when found_inf is first needed (step, update), which
+    after clip_grad_norm_'s own read-back costs no further synchronisation.  The scale
+    state machine is unchanged."""
 
     def __init__(self, init_scale=65536.0, growth_factor=2.0, backoff_factor=0.5,
                  growth_interval=2000, min_scale=1.0, max_scale=2 ** 24, enabled=True):
@@ -713,10 +748,23 @@ class GradScaler:
         self.max_scale = max_scale
         self.enabled = enabled
         self._growth_tracker = 0
+        self._pending = None
         self._found_inf = False
         self._overflow_count = 0
         self._step_count = 0
         self._consecutive_successes = 0
+
+    @property
+    def _found_inf(self):
+        if self._pending is not None:
+            resolve, self._pending = self._pending, None
+            self._found_inf_v = any(f != 0 for f in resolve())
+        return self._found_inf_v
+
+    @_found_inf.setter
+    def _found_inf(self, value):
+        self._pending = None
+        self._found_inf_v = bool(value)
 
     def scale(self, loss):
         if not self.enabled:
@@ -732,20 +780,19 @@ class GradScaler:
         self._found_inf = False
         params = [p for p in optimizer.params if p._has_grad()]
         grads = [p.grad for p in params]
-        if grads:
-            if zero_nan_grads:
-                flags = L.unscale_check(grads, inv, write=True)
-                bad = [g for g, f in zip(grads, flags) if f]
-            else:
-                pre = L.unscale_check(grads, 1.0, write=False)
-                clean = [g for g, f in zip(grads, pre) if not (f & 1)]
-                post = L.unscale_check(clean, inv, write=True) if clean else []
-                bad = [1] * sum(1 for f in pre if f & 1) + [1 for f in post if f]
-            if bad:
+        if grads and zero_nan_grads:
+            # flagged gradients are zeroed on the device; found_inf is read lazily
+            self._pending = L.unscale_deferred(grads, inv)
+            prep = getattr(optimizer, "_prepare", None)
+            if prep is not None:
+                prep()
+        elif grads:
+            # pre-existing non-finite gradients are left as they are (not unscaled)
+            pre = L.unscale_check(grads, 1.0, write=False)
+            clean = [g for g, f in zip(grads, pre) if not (f & 1)]
+            post = L.unscale_check(clean, inv, write=True) if clean else []
+            if any(f & 1 for f in pre) or any(post):
                 self._found_inf = True
-                if zero_nan_grads:
-                    for g in bad:
-                        L.fill(g, 0.0)
         optimizer._is_unscaled = True
 
     def step(self, optimizer, clip_grad_norm=None):

@@ -342,6 +342,69 @@ def test_gradscaler_overflow_and_growth(tg):
     assert s3.get_scale() == 1.0
 
 
+def test_gradscaler_zeroes_only_flagged_tensors(tg):
+    """unscale_ with zero_nan_grads (the reference's per-parameter loop,
+    _nn.py:1816-1829): a gradient holding a NaN or Inf is zeroed whole, the others are
+    unscaled bit-exact; fp32 and fp64 parameters; found_inf read after the fact."""
+    rng = np.random.default_rng(4)
+    vals = [rng.standard_normal(n).astype(dt) * 100
+            for n, dt in ((7, np.float32), (3000, np.float32), (5000, np.float32),
+                          (9, np.float64), (4100, np.float64))]
+    vals[1][1234] = np.inf
+    vals[4][7] = np.nan
+    ps = [tg.Tensor(np.zeros_like(v)) for v in vals]
+    for p, v in zip(ps, vals):
+        p.grad = v
+    opt = tg.SGD(ps, lr=0.1)
+    sc = tg.GradScaler(init_scale=4096.0)
+    sc.unscale_(opt)
+    for i in (0, 2, 3):
+        inv = vals[i].dtype.type(1.0 / 4096.0)
+        assert np.array_equal(ps[i].grad.cpu().numpy(), vals[i] * inv), i
+    for i in (1, 4):
+        assert not np.any(ps[i].grad.cpu().numpy()), i
+    assert sc._found_inf
+    sc.update()
+    assert sc.get_scale() == 2048.0
+    for p, v in zip(ps, vals):
+        p.grad = np.nan_to_num(v, posinf=1.0, nan=1.0)
+    opt._is_unscaled = False
+    sc.unscale_(opt)
+    assert not sc._found_inf
+
+
+def test_adamw_step_planned_at_unscale(tg):
+    """GradScaler.unscale_ plans the AdamW launch before clip_grad_norm_ rescales the
+    gradients in place; the step must see the clipped values, and a gradient replaced
+    after unscale_ must be used instead of the planned buffer.  Reference: the AdamW
+    update of _nn.py:1413-1442 in float64 NumPy on the same gradients."""
+    rng = np.random.default_rng(8)
+    shapes = [(64, 32), (32,), (1000,)]
+    w0 = [rng.standard_normal(s).astype(np.float32) for s in shapes]
+    g0 = [rng.standard_normal(s).astype(np.float32) * 50 for s in shapes]
+    ps = [tg.Tensor(w.copy()) for w in w0]
+    opt = tg.AdamW(ps, lr=1e-2, weight_decay=0.1)
+    sc = tg.GradScaler(init_scale=4.0)
+    for p, g in zip(ps, g0):
+        p.grad = g * np.float32(4.0)
+    sc.unscale_(opt)
+    norm = tg.clip_grad_norm_(ps, 1.0)
+    grads = [p.grad.double().cpu().numpy() for p in ps]  # unscaled and clipped
+    assert norm > 1.0 and abs(np.sqrt(sum((g * g).sum() for g in grads)) - 1.0) < 1e-4
+    replaced = rng.standard_normal(shapes[2]).astype(np.float32)
+    ps[2].grad = replaced  # a new buffer after the plan
+    grads[2] = replaced.astype(np.float64)
+    sc.step(opt)
+    sc.update()
+    for w, g, p in zip(w0, grads, ps):
+        w = w.astype(np.float64)
+        m = 0.1 * g
+        v = 0.001 * g * g
+        upd = (m / 0.1) / (np.sqrt(v / 0.001) + 1e-8)
+        ref = w - 1e-2 * 0.1 * w - 1e-2 * upd
+        assert_close(p.data, ref, 1e-5, "AdamW planned step")
+
+
 def test_gradscaler_unscale_bit_exact(tg):
     rng = np.random.default_rng(11)
     vals = [rng.standard_normal(n).astype(np.float32) * 100 for n in (5, 1000, 4097)]
