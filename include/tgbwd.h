@@ -95,6 +95,16 @@ int tg_layernorm_bwd(int dtype, const void* x, const float* mean, const float* r
                      const float* gamma, const void* dy, void* dx, float* dgamma, float* dbeta,
                      int64_t rows, int64_t cols, int accumulate_dx, int accumulate_params,
                      void* workspace, size_t workspace_bytes, void* stream);
+/* tg_layernorm_bwd writing dx = (LayerNorm dx) + dx_add, where dx_add may be another
+ * buffer than dx: the input's gradient is shared with another node (the residual
+ * add's pass-through, _core.py:941-968, then the LayerNorm closure's parent.grad +=),
+ * so the sum goes to the input's own new buffer in the same pass, with no copy first.
+ * dx_add == dx is tg_layernorm_bwd with accumulate_dx. */
+int tg_layernorm_bwd_add(int dtype, const void* x, const float* mean, const float* rstd,
+                         const float* gamma, const void* dy, const void* dx_add, void* dx,
+                         float* dgamma, float* dbeta, int64_t rows, int64_t cols,
+                         int accumulate_params, void* workspace, size_t workspace_bytes,
+                         void* stream);
 /* tg_layernorm_bwd without a workspace argument and without any allocation: the
  * partial sums live in a fixed device array of the library (one per GPU, held until
  * the process ends; tg_layernorm_bwd_noalloc_max_scratch() bytes).  No counterpart in

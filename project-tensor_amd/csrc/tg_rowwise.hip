@@ -379,11 +379,14 @@ __global__ __launch_bounds__(kBlock) void k_ln_fwd_loop(const T* __restrict__ x,
 //   dgamma partial = sum_rows dy*xhat, dbeta partial = sum_rows dy
 // Block b walks rows b, b+nblocks, ...; its threads own fixed columns, so the
 // dgamma/dbeta partials stay in registers and are written once per block to
-// part[b][0:cols] and part[nblocks + b][0:cols].
+// part[b][0:cols] and part[nblocks + b][0:cols].  ACC: dx = (that) + dxin, where dxin
+// is dx itself (accumulate in place) or another buffer (a gradient shared with another
+// node, summed into this node's own buffer without copying it first); each element of
+// dxin is read by the thread that writes that element of dx, before the write.
 template <typename T, int TPR, int VPT, bool ACC, bool NT>
 __global__ __launch_bounds__(kBlock) void k_ln_bwd_reg(
     const T* __restrict__ x, const float* __restrict__ mean, const float* __restrict__ rstd,
-    const float* __restrict__ gamma, const T* __restrict__ dy, T* __restrict__ dx,
+    const float* __restrict__ gamma, const T* __restrict__ dy, T* dx, const T* dxin,
     float* __restrict__ part, int64_t rows, int cols) {
   constexpr int V = tg_vec16<T>::N;
   constexpr int G = kBlock / TPR;
@@ -426,7 +429,7 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_reg(
         if (vi < nv) {
           b.x[k] = tg_ld16<NT>(x + off + vi * V);
           b.y[k] = tg_ld16<NT>(dy + off + vi * V);
-          if (kPreO) b.o[k] = tg_ld16<NT>(dx + off + vi * V);
+          if (kPreO) b.o[k] = tg_ld16<NT>(dxin + off + vi * V);
         }
       }
       b.mu = mean[row];
@@ -470,7 +473,7 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_reg(
         const int vi = t + k * TPR;
         if (vi < nv) {
           tg_vec16<T> o;
-          if (ACC && !kPreO) o = tg_ld16<NT>(dx + off + vi * V);
+          if (ACC && !kPreO) o = tg_ld16<NT>(dxin + off + vi * V);
 #pragma unroll
           for (int j = 0; j < V; ++j) {
             float r = rs * (dyv[k][j] * gam[k][j] - mg - xh[k][j] * mgx);
@@ -550,7 +553,7 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_reg(
 template <typename T, bool ACC>
 __global__ __launch_bounds__(kBlock) void k_ln_bwd_dx_loop(
     const T* __restrict__ x, const float* __restrict__ mean, const float* __restrict__ rstd,
-    const float* __restrict__ gamma, const T* __restrict__ dy, T* __restrict__ dx, int64_t rows,
+    const float* __restrict__ gamma, const T* __restrict__ dy, T* dx, const T* dxin, int64_t rows,
     int64_t cols) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -568,7 +571,7 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_dx_loop(
   for (int64_t c = lane; c < cols; c += 64) {
     const float xh = (tg_to_float(x[off + c]) - mu) * rs;
     float r = rs * (tg_to_float(dy[off + c]) * gamma[c] - mg - xh * mgx);
-    if (ACC) r += tg_to_float(dx[off + c]);
+    if (ACC) r += tg_to_float(dxin[off + c]);
     dx[off + c] = tg_from_float<T>(r);
   }
 }
@@ -753,13 +756,15 @@ LnBwdPlan ln_bwd_plan_dt(int dtype, int64_t rows, int64_t cols, bool aligned) {
 
 template <typename T>
 int ln_bwd_t(const void* x, const float* mean, const float* rstd, const float* gamma,
-             const void* dy, void* dx, float* dgamma, float* dbeta, int64_t rows, int64_t cols,
+             const void* dy, void* dx, const void* dxin, float* dgamma, float* dbeta,
+             int64_t rows, int64_t cols,
              int acc_dx, int acc_params, float* part, const LnBwdPlan& p, hipStream_t s) {
   if (p.reg) {
     const unsigned blocks = (unsigned)p.nparts;
     const int tpr = p.tpr, vpt = p.vpt;
     const bool nt = (int64_t)sizeof(T) * rows * cols >= kNtBytes;
-#define LNARGS (const T*)x, mean, rstd, gamma, (const T*)dy, (T*)dx, part, rows, (int)cols
+#define LNARGS \
+  (const T*)x, mean, rstd, gamma, (const T*)dy, (T*)dx, (const T*)dxin, part, rows, (int)cols
     if (acc_dx) {
 #define L(TPR, VPT)                                                                           \
   if (nt) k_ln_bwd_reg<T, TPR, VPT, true, true><<<blocks, kBlock, 0, s>>>(LNARGS); \
@@ -778,10 +783,12 @@ int ln_bwd_t(const void* x, const float* mean, const float* rstd, const float* g
     const unsigned blocks = (unsigned)((rows + 3) / 4);
     if (acc_dx)
       k_ln_bwd_dx_loop<T, true><<<blocks, kBlock, 0, s>>>((const T*)x, mean, rstd, gamma,
-                                                          (const T*)dy, (T*)dx, rows, cols);
+                                                          (const T*)dy, (T*)dx, (const T*)dxin,
+                                                          rows, cols);
     else
       k_ln_bwd_dx_loop<T, false><<<blocks, kBlock, 0, s>>>((const T*)x, mean, rstd, gamma,
-                                                           (const T*)dy, (T*)dx, rows, cols);
+                                                           (const T*)dy, (T*)dx, (const T*)dxin,
+                                                           rows, cols);
     dim3 grid((unsigned)((cols + kBlock - 1) / kBlock), (unsigned)p.nparts);
     k_ln_bwd_param_loop<T><<<grid, kBlock, 0, s>>>((const T*)x, mean, rstd, (const T*)dy, part,
                                                    rows, cols);
@@ -856,48 +863,82 @@ TG_EXPORT size_t tg_layernorm_bwd_workspace(int dtype, int64_t rows, int64_t col
   return (size_t)(2 * np * cols) * sizeof(float) + tg_sum_partials_scratch(np, cols, 2);
 }
 
+namespace {
+// dx = LayerNorm dx (+ dxin when dxin is non-null; dxin may be dx itself).
+int ln_bwd_entry(const char* who, int dtype, const void* x, const float* mean, const float* rstd,
+                 const float* gamma, const void* dy, void* dx, const void* dxin, float* dgamma,
+                 float* dbeta, int64_t rows, int64_t cols, int accumulate_params,
+                 void* workspace, size_t workspace_bytes, void* stream) {
+  TG_REQUIRE(rows >= 0 && cols > 0, "%s: bad shape", who);
+  if (rows == 0) return TG_OK;
+  TG_REQUIRE(x && mean && rstd && gamma && dy && dx, "%s: null pointer", who);
+  hipStream_t s = tg_stream(stream);
+  if (dtype == TG_F64) {
+    const size_t need64 = tg64_layernorm_bwd_workspace(rows, cols);
+    if ((dgamma || dbeta) && (!workspace || workspace_bytes < need64)) {
+      tg_set_error("%s: workspace of %zu bytes needed, got %zu", who, need64,
+                   workspace ? workspace_bytes : (size_t)0);
+      return TG_ERR_WORKSPACE;
+    }
+    if (dxin && dxin != dx) {
+      // the fp64 kernels accumulate in place: start dx from dxin
+      const hipError_t e = hipMemcpyAsync(dx, dxin, (size_t)(rows * cols) * sizeof(double),
+                                          hipMemcpyDeviceToDevice, s);
+      if (e != hipSuccess) {
+        tg_set_error("%s: hipMemcpyAsync: %s", who, hipGetErrorString(e));
+        return TG_ERR_HIP;
+      }
+    }
+    return tg64_layernorm_bwd(x, mean, rstd, gamma, dy, dx, dgamma, dbeta, rows, cols,
+                              dxin != nullptr, accumulate_params, workspace, s);
+  }
+  const bool al = tg_aligned16(x) && tg_aligned16(dy) && tg_aligned16(dx) &&
+                  (!dxin || tg_aligned16(dxin));
+  LnBwdPlan p = ln_bwd_plan_dt(dtype, rows, cols, al);
+  const size_t need =
+      (size_t)(2 * p.nparts * cols) * sizeof(float) + tg_sum_partials_scratch(p.nparts, cols, 2);
+  if (!workspace || workspace_bytes < need) {
+    tg_set_error("%s: workspace of %zu bytes needed, got %zu", who, need,
+                 workspace ? workspace_bytes : (size_t)0);
+    return TG_ERR_WORKSPACE;
+  }
+  float* part = (float*)workspace;
+  const int acc = dxin != nullptr;
+  switch (dtype) {
+    case TG_F32:
+      return ln_bwd_t<float>(x, mean, rstd, gamma, dy, dx, dxin, dgamma, dbeta, rows, cols, acc,
+                             accumulate_params, part, p, s);
+    case TG_F16:
+      return ln_bwd_t<tg_half>(x, mean, rstd, gamma, dy, dx, dxin, dgamma, dbeta, rows, cols,
+                               acc, accumulate_params, part, p, s);
+    case TG_BF16:
+      return ln_bwd_t<tg_bf16>(x, mean, rstd, gamma, dy, dx, dxin, dgamma, dbeta, rows, cols,
+                               acc, accumulate_params, part, p, s);
+  }
+  tg_set_error("%s: unsupported dtype %d", who, dtype);
+  return TG_ERR_UNSUPPORTED;
+}
+}  // namespace
+
 TG_EXPORT int tg_layernorm_bwd(int dtype, const void* x, const float* mean, const float* rstd,
                                const float* gamma, const void* dy, void* dx, float* dgamma,
                                float* dbeta, int64_t rows, int64_t cols, int accumulate_dx,
                                int accumulate_params, void* workspace, size_t workspace_bytes,
                                void* stream) {
-  TG_REQUIRE(rows >= 0 && cols > 0, "tg_layernorm_bwd: bad shape");
-  if (rows == 0) return TG_OK;
-  TG_REQUIRE(x && mean && rstd && gamma && dy && dx, "tg_layernorm_bwd: null pointer");
-  if (dtype == TG_F64) {
-    const size_t need64 = tg64_layernorm_bwd_workspace(rows, cols);
-    if ((dgamma || dbeta) && (!workspace || workspace_bytes < need64)) {
-      tg_set_error("tg_layernorm_bwd: workspace of %zu bytes needed, got %zu", need64,
-                   workspace ? workspace_bytes : (size_t)0);
-      return TG_ERR_WORKSPACE;
-    }
-    return tg64_layernorm_bwd(x, mean, rstd, gamma, dy, dx, dgamma, dbeta, rows, cols,
-                              accumulate_dx, accumulate_params, workspace, tg_stream(stream));
-  }
-  const bool al = tg_aligned16(x) && tg_aligned16(dy) && tg_aligned16(dx);
-  LnBwdPlan p = ln_bwd_plan_dt(dtype, rows, cols, al);
-  const size_t need =
-      (size_t)(2 * p.nparts * cols) * sizeof(float) + tg_sum_partials_scratch(p.nparts, cols, 2);
-  if (!workspace || workspace_bytes < need) {
-    tg_set_error("tg_layernorm_bwd: workspace of %zu bytes needed, got %zu", need,
-                 workspace ? workspace_bytes : (size_t)0);
-    return TG_ERR_WORKSPACE;
-  }
-  hipStream_t s = tg_stream(stream);
-  float* part = (float*)workspace;
-  switch (dtype) {
-    case TG_F32:
-      return ln_bwd_t<float>(x, mean, rstd, gamma, dy, dx, dgamma, dbeta, rows, cols,
-                             accumulate_dx, accumulate_params, part, p, s);
-    case TG_F16:
-      return ln_bwd_t<tg_half>(x, mean, rstd, gamma, dy, dx, dgamma, dbeta, rows, cols,
-                               accumulate_dx, accumulate_params, part, p, s);
-    case TG_BF16:
-      return ln_bwd_t<tg_bf16>(x, mean, rstd, gamma, dy, dx, dgamma, dbeta, rows, cols,
-                               accumulate_dx, accumulate_params, part, p, s);
-  }
-  tg_set_error("tg_layernorm_bwd: unsupported dtype %d", dtype);
-  return TG_ERR_UNSUPPORTED;
+  return ln_bwd_entry("tg_layernorm_bwd", dtype, x, mean, rstd, gamma, dy, dx,
+                      accumulate_dx ? dx : nullptr, dgamma, dbeta, rows, cols,
+                      accumulate_params, workspace, workspace_bytes, stream);
+}
+
+TG_EXPORT int tg_layernorm_bwd_add(int dtype, const void* x, const float* mean,
+                                   const float* rstd, const float* gamma, const void* dy,
+                                   const void* dx_add, void* dx, float* dgamma, float* dbeta,
+                                   int64_t rows, int64_t cols, int accumulate_params,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+  TG_REQUIRE(dx_add || rows == 0, "tg_layernorm_bwd_add: null dx_add");
+  return ln_bwd_entry("tg_layernorm_bwd_add", dtype, x, mean, rstd, gamma, dy, dx, dx_add,
+                      dgamma, dbeta, rows, cols, accumulate_params, workspace, workspace_bytes,
+                      stream);
 }
 
 // ---- LayerNorm backward without a caller workspace -------------------------

@@ -197,6 +197,20 @@ class Tensor:
             self._privatize()
         return self._g, True
 
+    def _grad_target_add(self):
+        """(buffer, source) for a kernel that writes buffer = its result + source:
+        source None means no prior gradient (overwrite).  A gradient shared with
+        another node is not copied first: the kernel reads it as the source and writes
+        this tensor's own new buffer; otherwise source is the buffer itself."""
+        if (not self._gz and self._gsh and self._g.is_contiguous()
+                and self._g.dtype == self.data.dtype and self._g.shape == self.data.shape):
+            src = self._g
+            self._g = self._new_buf()
+            self._gsh = False
+            return self._g, src
+        buf, acc = self._grad_target()
+        return buf, (buf if acc else None)
+
     def _share_grad(self, donor, g):
         """First gradient of this node is `g`, a read-only view of donor's gradient
         buffer (the reshape/view/transpose/add pass-through).  Adopted without a copy,

@@ -51,6 +51,8 @@ SIGNATURES = {
     "tg_layernorm_bwd_workspace": (_sz, [_i32, _i64, _i64]),
     "tg_layernorm_bwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
                                 _i32, _i32, _vp, _sz, _vp]),
+    "tg_layernorm_bwd_add": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
+                                    _i64, _i32, _vp, _sz, _vp]),
     "tg_layernorm_bwd_noalloc_max_scratch": (_sz, []),
     "tg_layernorm_bwd_noalloc": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
                                         _i64, _i32, _i32, _vp]),
@@ -395,11 +397,16 @@ def layernorm_fwd(x, gamma, beta, eps, y=None, mean=None, rstd=None):
 
 
 def layernorm_bwd(x, mean, rstd, gamma, dy, dx, dgamma, dbeta, accumulate_dx,
-                  accumulate_params):
+                  accumulate_params, dx_add=None):
+    """dx (+)= LayerNorm input gradient; with dx_add (another buffer of dx's shape),
+    dx = gradient + dx_add instead (accumulate_dx is then ignored)."""
     for n, t in (("x", x), ("dy", dy), ("dx", dx), ("mean", mean), ("rstd", rstd),
                  ("gamma", gamma)):
         _dev(t, n)
     _same("layernorm_bwd", x, dy, dx)
+    if dx_add is not None:
+        _dev(dx_add, "dx_add")
+        _same("layernorm_bwd", x, dx_add)
     cols = gamma.numel()
     rows = x.numel() // cols
     lib = load()
@@ -407,6 +414,12 @@ def layernorm_bwd(x, mean, rstd, gamma, dy, dx, dgamma, dbeta, accumulate_dx,
     code = dtype_code(x)
     nbytes = lib.tg_layernorm_bwd_workspace(code, rows, cols)
     ws = workspace(nbytes, x.device)
+    if dx_add is not None:
+        _check("tg_layernorm_bwd_add", lib.tg_layernorm_bwd_add(
+            code, ptr(x), ptr(mean), ptr(rstd), ptr(gamma), ptr(dy), ptr(dx_add), ptr(dx),
+            ptr(dgamma), ptr(dbeta), rows, cols, int(bool(accumulate_params)), ptr(ws),
+            ws.numel(), stream_handle()))
+        return dx
     _check("tg_layernorm_bwd", lib.tg_layernorm_bwd(
         code, ptr(x), ptr(mean), ptr(rstd), ptr(gamma), ptr(dy), ptr(dx), ptr(dgamma),
         ptr(dbeta), rows, cols, int(bool(accumulate_dx)), int(bool(accumulate_params)), ptr(ws),

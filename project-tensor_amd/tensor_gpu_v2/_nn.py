@@ -240,8 +240,12 @@ class LayerNorm(Module):
                 if dg is not None and dg.dtype != torch.float32 or db is not None and db.dtype != torch.float32:
                     raise TypeError("LayerNorm parameters must be float32")
                 if x._has_grad():
-                    dx, accx = x._grad_target()
-                    L.layernorm_bwd(xd, mean, rstd, g32, dy, dx, dg, db, accx, accp)
+                    dx, src = x._grad_target_add()
+                    if src is None or src is dx:
+                        L.layernorm_bwd(xd, mean, rstd, g32, dy, dx, dg, db, src is dx, accp)
+                    else:  # x's gradient is shared: the sum goes to x's own buffer
+                        L.layernorm_bwd(xd, mean, rstd, g32, dy, dx, dg, db, True, accp,
+                                        dx_add=src)
                 else:
                     L.layernorm_bwd(xd, mean, rstd, g32, dy, torch.empty_like(xd), dg, db,
                                     False, accp)

@@ -520,3 +520,28 @@ def test_matmul2d_k_split(cuda, M, N, K, beta):
     want = x.double().t() @ y.double() + (out.double() if beta else 0.0)
     L().matmul2d(x, y, out, trans_a=True, beta=beta)
     assert_close(out, want.cpu().numpy(), RTOL_F32_MM, "k-split matmul")
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16, torch.bfloat16, torch.float64])
+@pytest.mark.parametrize("rows,cols", [(512, 1024), (300, 1000), (65, 7)])
+def test_layernorm_bwd_add_matches_in_place(cuda, dt, rows, cols):
+    """tg_layernorm_bwd_add (dx = LayerNorm dx + dx_add from another buffer) is
+    bit-identical to accumulating in place into a copy of dx_add, on the register
+    kernels (cols 1024, 1000) and the generic ones (7), and leaves dx_add untouched."""
+    g = torch.Generator(device="cuda").manual_seed(rows + cols)
+    x = torch.randn(rows, cols, device="cuda", generator=g).to(dt)
+    dy = torch.randn(rows, cols, device="cuda", generator=g).to(dt)
+    gam = torch.randn(cols, device="cuda", generator=g)
+    bet = torch.randn(cols, device="cuda", generator=g)
+    _, mean, rstd = L().layernorm_fwd(x, gam, bet, 1e-5)
+    add = torch.randn(rows, cols, device="cuda", generator=g).to(dt)
+    add0 = add.clone()
+    ref = add.clone()
+    dg1, db1 = torch.zeros(cols, device="cuda"), torch.zeros(cols, device="cuda")
+    dg2, db2 = torch.zeros(cols, device="cuda"), torch.zeros(cols, device="cuda")
+    L().layernorm_bwd(x, mean, rstd, gam, dy, ref, dg1, db1, True, False)
+    out = torch.full_like(add, float("nan"))
+    L().layernorm_bwd(x, mean, rstd, gam, dy, out, dg2, db2, True, False, dx_add=add)
+    assert torch.equal(out, ref)
+    assert torch.equal(add, add0)
+    assert torch.equal(dg1, dg2) and torch.equal(db1, db2)
