@@ -766,56 +766,84 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dq(
 }
 
 // ---------------------------------------------------------------- forward, DMA-staged
-// One 32-key sub-tile of the forward for one wave (lane = query).  S^T = K Q^T (keys on
-// the accumulator rows), online softmax per lane, O^T += V^T P^T with V^T read by
-// transpose reads and P^T taken straight from the accumulator registers.  O^T is only
-// rescaled when some lane's running maximum rose by more than kLazy (log2 units): P is
-// then at most 2^kLazy against the stale maximum, O and l use the same maximum, and
-// the result is exact.
+// One 32-key sub-tile of the forward for one wave (lane = query), in two halves:
+// fwd_s forms S^T = K Q^T (keys on the accumulator rows); fwd_pv runs the online
+// softmax per lane and O^T += V^T P^T with V^T read by transpose reads and P^T taken
+// straight from the accumulator registers.  The caller issues fwd_s of sub-tile j + 1
+// before fwd_pv of sub-tile j, so the softmax's vector ALU work overlaps those MFMAs.
+// O^T is only rescaled when some lane's running maximum rose by more than kLazy (log2
+// units): P is then at most 2^kLazy against the stale maximum, O and l use the same
+// maximum, and the result is exact.
 constexpr float kLazy = 8.f;
-template <typename T, int D, bool MASK>
-__device__ __forceinline__ void fwd_sub(const char* ks, const char* vs, const LaneOffs<D>& o,
-                                        const typename Vec8<T>::type (&qf)[D / 16],
-                                        f32x16 (&acc)[D / 32], float sl2, float& m, float& l,
-                                        int thr) {
+template <typename T, int D>
+__device__ __forceinline__ f32x16 fwd_s(const char* ks, const LaneOffs<D>& o,
+                                        const typename Vec8<T>::type (&qf)[D / 16]) {
   using V8 = typename Vec8<T>::type;
-  constexpr int DK = D / 16, DT = D / 32, RB = D * 2, PF = 4, NB = 2 * DT;
-  auto tr = [&](int n) {
-    const char* b = vs + (n / DT) * 16 * RB;
-    return lds_tr<T>(b + o.t[0][n % DT], b + o.t[1][n % DT]);
-  };
-  V8 ka[DK], bt[NB];
+  constexpr int DK = D / 16, PF = 4;
+  V8 ka[DK];
 #pragma unroll
   for (int i = 0; i < PF; ++i) ka[i] = lds_a<T>(ks + o.a[i]);
   f32x16 sa;
 #pragma unroll
   for (int r = 0; r < 16; ++r) sa[r] = 0.f;
   TG_SB();
-  int nt = 0;
 #pragma unroll
   for (int k = 0; k < DK; ++k) {
     sa = mfma(ka[k], qf[k], sa);
     if (k + PF < DK) ka[k + PF] = lds_a<T>(ks + o.a[k + PF]);
-    else if (nt < NB) { bt[nt] = tr(nt); ++nt; }
     TG_SB();
   }
-  while (nt < NB) { bt[nt] = tr(nt); ++nt; }
-  // scores in log2 units, masked keys at -inf; this lane's 16 keys, then the other half
+  return sa;
+}
+
+// Running maximum m starts at kMInit, finite, so exp2(x - m) needs no guard: until a
+// lane sees a finite score, m stays kMInit and every (masked, -inf) score gives 0; the
+// first finite maximum is more than kLazy above kMInit and replaces it.
+constexpr float kMInit = -1e30f;
+
+// max / sum of x over lanes l and l ^ 32, in every lane, with one v_permlane32_swap
+// (x swapped with itself: one result holds lane l's value, the other lane l ^ 32's)
+// instead of an LDS permute.
+__device__ __forceinline__ float xhalf_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  const float a = __uint_as_float(r[0]), b = __uint_as_float(r[1]);
+  return a > b ? a : b;
+}
+__device__ __forceinline__ float xhalf_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                                  false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+template <typename T, int D, bool MASK>
+__device__ __forceinline__ void fwd_pv(const f32x16& sa, const char* vs, const LaneOffs<D>& o,
+                                       f32x16 (&acc)[D / 32], float sl2, float& m, float& l,
+                                       int thr) {
+  using V8 = typename Vec8<T>::type;
+  constexpr int DT = D / 32, RB = D * 2, NB = 2 * DT;
+  V8 bt[NB];
+#pragma unroll
+  for (int n = 0; n < NB; ++n) {
+    const char* b = vs + (n / DT) * 16 * RB;
+    bt[n] = lds_tr<T>(b + o.t[0][n % DT], b + o.t[1][n % DT]);
+  }
+  // raw scores (masked keys at -inf); their maximum is scaled once (sl2 > 0, so the
+  // maximum of the scaled scores is the scaled maximum), and each exponent argument is
+  // one fused multiply-add
   float x[16];
   float mloc = -INFINITY;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    float v = sa[r] * sl2;
+    float v = sa[r];
     if (MASK) v = (8 * (r >> 2) + (r & 3) > thr) ? -INFINITY : v;
     x[r] = v;
     mloc = fmaxf(mloc, v);
   }
-  mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-  // lazy rescale (uniform branch): only when some lane's maximum rose by > kLazy
+  mloc = xhalf_max(mloc) * sl2;
   const bool grow = mloc > m + kLazy;
   if (__any(grow)) {
     const float mn = fmaxf(m, mloc);
-    const float alpha = (m == -INFINITY) ? 0.f : fexp2(m - mn);
+    const float alpha = fexp2(m - mn);
     l *= alpha;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
@@ -826,11 +854,11 @@ __device__ __forceinline__ void fwd_sub(const char* ks, const char* vs, const La
   float p[16], ls = 0.f;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    const float e = (m == -INFINITY) ? 0.f : fexp2(x[r] - m);
+    const float e = fexp2(fmaf(x[r], sl2, -m));
     p[r] = e;
     ls += e;
   }
-  l += ls + __shfl_xor(ls, 32, 64);
+  l += xhalf_sum(ls);
 #pragma unroll
   for (int sg = 0; sg < 2; ++sg) {
     const V8 pb = pack8<T>(&p[8 * sg]);
@@ -876,7 +904,7 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_fwd2(
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[dt][r] = 0.f;
-  float m = -INFINITY, l = 0.f;
+  float m = kMInit, l = 0.f;
   LaneOffs<D> o;
   o.init(lane);
   DmaPlan<T, D, BN> plan;
@@ -887,14 +915,25 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_fwd2(
   // minus k0
   auto tile_fn = [&](const char* ks_, const char* vs_, int64_t k0) {
     const int qk = (int)(qblk - k0) + wave * 32;
+    // active sub-tiles: a prefix [0, na) (keys past Sk, or wholly after this wave's
+    // queries under causal masking, are skipped)
+    int na = BN / 32;
+    const int64_t nk = (Sk - k0 + 31) / 32;
+    if (nk < na) na = (int)nk;
+    if (causal) {
+      const int nc = qk + 31 >= 0 ? (qk + 31) / 32 + 1 : 0;
+      if (nc < na) na = nc;
+    }
+    if (na <= 0) return;
+    f32x16 sa = fwd_s<T, D>(ks_, o, qf);
 #pragma unroll
     for (int kt = 0; kt < BN / 32; ++kt) {
+      if (kt >= na) break;
+      f32x16 sn;
+      if (kt + 1 < na) sn = fwd_s<T, D>(ks_ + (kt + 1) * 32 * RB, o, qf);
       const int64_t kb0 = k0 + kt * 32;
-      if (kb0 >= Sk) break;
-      if (causal && kt * 32 > qk + 31) continue;  // wholly after this wave's queries
       const bool diag = causal && kt * 32 + 31 > qk;
       const bool edge = kb0 + 32 > Sk;
-      const char* kk = ks_ + kt * 32 * RB;
       const char* vv = vs_ + kt * 32 * RB;
       if (diag || edge) {
         int thr = 1 << 30;
@@ -903,10 +942,11 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_fwd2(
           const int kb = (int)(Sk - kb0) - 4 * h - 1;
           thr = kb < thr ? kb : thr;
         }
-        fwd_sub<T, D, true>(kk, vv, o, qf, acc, sl2, m, l, thr);
+        fwd_pv<T, D, true>(sa, vv, o, acc, sl2, m, l, thr);
       } else {
-        fwd_sub<T, D, false>(kk, vv, o, qf, acc, sl2, m, l, 0);
+        fwd_pv<T, D, false>(sa, vv, o, acc, sl2, m, l, 0);
       }
+      if (kt + 1 < na) sa = sn;
     }
   };
   if (kend > 0) {
@@ -945,7 +985,7 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_fwd2(
         *reinterpret_cast<uint2*>(O + q * rs + dt * 32 + g * 8 + h * 4) =
             *reinterpret_cast<const uint2*>(w);
       }
-    if (h == 0) LSE[q] = (m + log2f(l)) / kLog2e;
+    if (h == 0) LSE[q] = l > 0.f ? (m + log2f(l)) / kLog2e : -INFINITY;
   }
 }
 
