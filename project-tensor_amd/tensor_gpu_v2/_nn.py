@@ -663,6 +663,7 @@ class Adam:
         return st
 
     def load_state_dict(self, state):
+        self._planned = None  # a planned launch holds the moment buffers replaced below
         self.lr = state.get("lr", self.lr)
         self.t = state.get("t", self.t)
         if "betas" in state:

@@ -405,6 +405,30 @@ def test_adamw_step_planned_at_unscale(tg):
         assert_close(p.data, ref, 1e-5, "AdamW planned step")
 
 
+def test_adamw_plan_dropped_by_load_state_dict(tg):
+    """A state loaded between unscale_ (which plans the launch) and step replaces the
+    moment buffers: the step must update the loaded moments, not the planned ones.
+    Reference: the AdamW recurrence of _nn.py:1413-1442 in float64 NumPy."""
+    rng = np.random.default_rng(12)
+    w0 = rng.standard_normal(300).astype(np.float32)
+    g0 = rng.standard_normal(300).astype(np.float32)
+    m0 = rng.standard_normal(300).astype(np.float32) * 0.1
+    v0 = np.abs(rng.standard_normal(300)).astype(np.float32) * 0.01
+    p = tg.Tensor(w0.copy())
+    opt = tg.AdamW([p], lr=1e-2, weight_decay=0.1)
+    sc = tg.GradScaler(init_scale=2.0)
+    p.grad = g0 * np.float32(2.0)
+    sc.unscale_(opt)
+    opt.load_state_dict({"t": 3, "m": [m0], "v": [v0]})
+    sc.step(opt)
+    g, w = g0.astype(np.float64), w0.astype(np.float64)
+    m = 0.9 * m0 + 0.1 * g
+    v = 0.999 * v0 + 0.001 * g * g
+    ref = w - 1e-2 * 0.1 * w - 1e-2 * (m / (1 - 0.9 ** 4)) / (np.sqrt(v / (1 - 0.999 ** 4)) + 1e-8)
+    assert_close(p.data, ref, 1e-5, "AdamW after load_state_dict")
+    assert_close(opt.m[0], m, 1e-6, "loaded first moment updated")
+
+
 def test_gradscaler_unscale_bit_exact(tg):
     rng = np.random.default_rng(11)
     vals = [rng.standard_normal(n).astype(np.float32) * 100 for n in (5, 1000, 4097)]
