@@ -137,7 +137,7 @@ int tg_reduce_rows(int dtype_in, const void* in, int dtype_out, void* out, int64
                    int64_t cols, int accumulate, void* workspace, size_t workspace_bytes,
                    void* stream);
 
-/* ---- batch norm (+ReLU), fp32 ----------------------------------------- */
+/* ---- batch norm (+ReLU), fp32 (fp64 forms below) ------------------------- */
 /* layout: 0 = NHWC ([N*H*W, C]), 1 = NCHW.  HW = H*W. */
 size_t tg_batchnorm_workspace(int layout, int64_t N, int64_t C, int64_t HW);
 /* Training forward of FusedBatchNormReLU / BatchNorm2D (_nn.py:794-810, :701-714):
@@ -156,6 +156,29 @@ int tg_batchnorm_bwd(int layout, const float* x, const float* mean, const float*
                      float* dgamma, float* dbeta, int64_t N, int64_t C, int64_t HW, int relu,
                      int accumulate_dx, int accumulate_params, void* workspace,
                      size_t workspace_bytes, void* stream);
+/* Training forward on float64 data (_nn.py:794-810 on float64 arrays): batch mean/var
+ * (two passes), rstd, the running EMA in double (either running pointer may be NULL),
+ * y = [relu](gamma*xhat + beta) in double; gamma/beta are the fp32 parameters. */
+int tg_batchnorm_fwd_train_f64(int layout, const double* x, const float* gamma,
+                               const float* beta, double* y, double* mean, double* rstd,
+                               double* var, double* running_mean, double* running_var,
+                               double momentum, int64_t N, int64_t C, int64_t HW, double eps,
+                               int relu, void* stream);
+/* Backward with the reference's own formula against given per-channel statistics
+ * (mean, rstd in double): dout = dy*[out > 0], dgamma (+)= sum dout*xhat, dbeta (+)=
+ * sum dout, dx (+)= dout*gamma*rstd + dvar*(2/m)*xc + dmean/m with
+ * dvar = -0.5*rstd^3*sum(dout*gamma*xc), dmean = -rstd*sum(dout*gamma) +
+ * dvar*(-2/m)*sum(xc) (_nn.py:812-833, :720-736).  Serves float64 data (dtype 3) and
+ * the eval-mode BatchNorm2D backward on the running statistics (dtype 0 or 3), where
+ * sum(xc) != 0.  Sums in double; the fp32 parameter gradients are rounded once.
+ * Workspace: tg_batchnorm_stats_workspace(C) bytes. */
+size_t tg_batchnorm_stats_workspace(int64_t C);
+int tg_batchnorm_bwd_stats(int dtype, int layout, const void* x, const double* mean,
+                           const double* rstd, const float* gamma, const float* beta,
+                           const void* dy, void* dx, float* dgamma, float* dbeta, int64_t N,
+                           int64_t C, int64_t HW, int relu, int accumulate_dx,
+                           int accumulate_params, void* workspace, size_t workspace_bytes,
+                           void* stream);
 
 /* ---- optimizers and gradient hygiene (multi-tensor, host pointer lists) --- */
 /* Adam / AdamW step over `ntensors` fp32 tensors (_nn.py:1413-1442, FusedAdam
@@ -276,6 +299,23 @@ int tg_flash_attn_bwd_layout(int dtype, const void* q, const void* k, const void
                              void* dk, void* dv, int64_t B, int64_t H, int64_t Sq, int64_t Sk,
                              int64_t D, float scale, int causal, int accumulate, int layout,
                              void* workspace, size_t workspace_bytes, void* stream);
+/* FlashAttention on float64 data (the reference runs flash_attention in the input's
+ * dtype, _core.py:1716-1867): the scores of a chunk of heads are materialised in the
+ * workspace (as the reference materialises them per query block), the products run on
+ * the fp64 matrix cores, softmax and lse (natural log, double, [B,H,Sq]) in double;
+ * the backward recomputes P from lse and uses the reference's row term
+ * dS = P*(dP - rowsum(P*dP))*scale.  layout as for the _layout forms; o is not read by
+ * the backward.  Workspace: tg_flash_attn_f64_workspace bytes (at most 512 MiB). */
+size_t tg_flash_attn_f64_workspace(int64_t B, int64_t H, int64_t Sq, int64_t Sk);
+int tg_flash_attn_fwd_f64(const double* q, const double* k, const double* v, double* o,
+                          double* lse, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
+                          double scale, int causal, int layout, void* workspace,
+                          size_t workspace_bytes, void* stream);
+int tg_flash_attn_bwd_f64(const double* q, const double* k, const double* v, const double* o,
+                          const double* dout, const double* lse, double* dq, double* dk,
+                          double* dv, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
+                          double scale, int causal, int layout, int accumulate,
+                          void* workspace, size_t workspace_bytes, void* stream);
 
 /* Cross-entropy over logits [N, C] with int64 targets (CrossEntropyLoss,
  * _nn.py:1128-1185).  Forward: per-row log-sum-exp lse[N] and per-row loss

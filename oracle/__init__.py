@@ -18,6 +18,8 @@ How each function is pinned (tests/test_oracle.py):
   layernorm_fwd/bwd             torch.nn.functional.layer_norm autograd float64
   batchnorm_relu_fwd/bwd        torch batch_norm(training) + relu autograd float64
                                 (the reference's BatchNorm2D oracle pattern)
+  batchnorm_eval_fwd            eval mode with the running statistics set to the
+                                batch's own equals the torch-pinned training path
   flash_attention_fwd/bwd       naive float64 softmax(QK^T s + mask) V autograd,
                                 causal and non-causal, 3-D and 4-D inputs
   matmul_bwd / unbroadcast      torch autograd float64 over the reference test's

@@ -9,7 +9,8 @@ import numpy as np
 __all__ = [
     "gelu_fwd", "gelu_bwd", "silu_fwd", "silu_bwd", "softmax_fwd", "softmax_bwd",
     "layernorm_fwd", "layernorm_bwd", "batchnorm_relu_fwd", "batchnorm_relu_bwd",
-    "batchnorm_relu_fwd_nhwc", "batchnorm_relu_bwd_nhwc", "unbroadcast", "matmul_bwd",
+    "batchnorm_eval_fwd", "batchnorm_relu_fwd_nhwc", "batchnorm_relu_bwd_nhwc", "unbroadcast",
+    "matmul_bwd",
     "flash_attention_fwd", "flash_attention_bwd", "adam_step", "GradScalerRef",
     "clip_grad_norm", "cross_entropy_fwd", "cross_entropy_bwd", "embedding_bwd",
     "mlp_step",
@@ -114,6 +115,19 @@ def batchnorm_relu_bwd(dy, gamma, cache, relu=True):
     dmean = dmean + dvar * (-2.0 / m) * xc.sum(axis=(0, 2, 3), keepdims=True)
     dx = dxn * std_inv + dvar * (2.0 / m) * xc + dmean / m
     return dx, dgamma, dbeta
+
+
+def batchnorm_eval_fwd(x, gamma, beta, running_mean, running_var, eps=1e-5):
+    """BatchNorm2D forward in eval mode on NCHW (_nn.py:706-718): the running statistics
+    take the place of the batch ones.  The reference keeps the backward of
+    _nn.py:720-736, so the returned cache feeds batchnorm_relu_bwd(..., relu=False)
+    unchanged (with m = N*H*W and sum(xc) no longer zero)."""
+    N, C, H, W = x.shape
+    std_inv = 1.0 / np.sqrt(running_var.reshape(1, C, 1, 1) + eps)
+    xc = x - running_mean.reshape(1, C, 1, 1)
+    xn = xc * std_inv
+    out = gamma.reshape(1, C, 1, 1) * xn + beta.reshape(1, C, 1, 1)
+    return out, (xn, xc, std_inv, N * H * W, out, running_mean, running_var)
 
 
 def batchnorm_relu_fwd_nhwc(x, gamma, beta, eps=1e-5, relu=True):

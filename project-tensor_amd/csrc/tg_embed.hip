@@ -410,6 +410,33 @@ __global__ __launch_bounds__(kBlock) void k_transpose_add(const TS* __restrict__
   }
 }
 
+// The same in double, for gradients where either side is float64 (the reference's
+// source.grad += param.grad.T adds in the wider dtype and casts to the destination's).
+template <typename TS, typename TD>
+__global__ __launch_bounds__(kBlock) void k_transpose_add_d(const TS* __restrict__ src, int64_t R,
+                                                            int64_t C, TD* __restrict__ dst,
+                                                            double alpha) {
+  __shared__ double tile[64][65];
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;  // 64 x 4
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int rr = ty + 4 * k;
+    const int64_t r = r0 + rr, c = c0 + tx;
+    tile[rr][tx] = (r < R && c < C) ? (double)src[r * C + c] : 0.0;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int cc = ty + 4 * k;
+    const int64_t c = c0 + cc, r = r0 + tx;  // dst[c][r]
+    if (c < C && r < R) {
+      TD* p = dst + c * R + r;
+      *p = (TD)((double)*p + alpha * tile[tx][cc]);
+    }
+  }
+}
+
 // fp32 transpose-add over whole 64 x 64 tiles (R and C multiples of 64, 16-byte
 // aligned rows): 16-byte loads of src rows and 16-byte read-modify-writes of dst
 // rows, all non-temporal (each element is touched once).
@@ -660,6 +687,19 @@ TG_EXPORT int tg_transpose_add(int dtype_src, const void* src, int64_t rows, int
       cols / 64 <= 65535 && tg_aligned16(src) && tg_aligned16(dst)) {
     const dim3 gt((unsigned)(rows / 64), (unsigned)(cols / 64));
     k_transpose_add_v4<<<gt, kBlock, 0, s>>>((const float*)src, rows, cols, (float*)dst, alpha);
+    return tg_check_launch("tg_transpose_add");
+  }
+  if (dtype_src == TG_F64 || dtype_dst == TG_F64) {
+#define D2(TS, TD) \
+  k_transpose_add_d<TS, TD><<<grid, kBlock, 0, s>>>((const TS*)src, rows, cols, (TD*)dst, (double)alpha)
+    if (dtype_src == TG_F64 && dtype_dst == TG_F64) D2(double, double);
+    else if (dtype_src == TG_F64 && dtype_dst == TG_F32) D2(double, float);
+    else if (dtype_src == TG_F32 && dtype_dst == TG_F64) D2(float, double);
+    else {
+      tg_set_error("tg_transpose_add: unsupported dtypes %d/%d", dtype_src, dtype_dst);
+      return TG_ERR_UNSUPPORTED;
+    }
+#undef D2
     return tg_check_launch("tg_transpose_add");
   }
 #define T2(TS)                                                                                  \

@@ -464,6 +464,192 @@ __global__ void k64_zero_ints(int* p, int n) {
   for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0;
 }
 
+// ---------------------------------------------------------------- attention
+// fp64 FlashAttention (flash_attention on float64 data, _core.py:1686-1870, which runs in
+// the input dtype): scores of a chunk of heads are materialised in a workspace (the
+// reference materialises them per 64-query block) and the products run as batched fp64
+// GEMMs.  Row softmax of S (one wavefront per row of a [rows = heads * Sq, Sk] chunk),
+// P written over S; query i keeps keys j <= i under causal masking (the reference's
+// -1e9 fill gives those keys exactly zero weight in double).  lse = m + log(sum).
+__global__ __launch_bounds__(kT) void k64_fa_softmax(double* __restrict__ S,
+                                                     double* __restrict__ lse, int64_t rows,
+                                                     int64_t Sq, int64_t Sk, int causal) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const int64_t i = r % Sq;
+  double* row = S + r * Sk;
+  const int64_t kend = causal ? (i + 1 < Sk ? i + 1 : Sk) : Sk;
+  double m = -INFINITY;
+  for (int64_t c = lane; c < kend; c += 64) m = fmax(m, row[c]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = fmax(m, __shfl_xor(m, off, 64));
+  double s = 0.0;
+  for (int64_t c = lane; c < kend; c += 64) s += exp(row[c] - m);
+  s = tg_wave_sum_d(s);
+  for (int64_t c = lane; c < Sk; c += 64) row[c] = c < kend ? exp(row[c] - m) / s : 0.0;
+  if (lane == 0) lse[r] = m + log(s);
+}
+
+// P = exp(S - lse) (masked keys 0), in place, for the backward.
+__global__ __launch_bounds__(kT) void k64_fa_p(double* __restrict__ S,
+                                               const double* __restrict__ lse, int64_t rows,
+                                               int64_t Sq, int64_t Sk, int causal) {
+  const int64_t n = rows * Sk;
+  for (int64_t e = (int64_t)blockIdx.x * kT + threadIdx.x; e < n; e += (int64_t)gridDim.x * kT) {
+    const int64_t r = e / Sk, c = e % Sk;
+    S[e] = (causal && c > r % Sq) ? 0.0 : exp(S[e] - lse[r]);
+  }
+}
+
+// dS = P * (dP - rowsum(P * dP)) * scale, written over dP (the reference's row term,
+// _core.py:1818-1847).
+__global__ __launch_bounds__(kT) void k64_fa_ds(const double* __restrict__ P,
+                                                double* __restrict__ dP, int64_t rows,
+                                                int64_t Sk, double scale) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const double* pr = P + r * Sk;
+  double* dr = dP + r * Sk;
+  double t = 0.0;
+  for (int64_t c = lane; c < Sk; c += 64) t += pr[c] * dr[c];
+  t = tg_wave_sum_d(t);
+  for (int64_t c = lane; c < Sk; c += 64) dr[c] = pr[c] * (dr[c] - t) * scale;
+}
+
+// ---------------------------------------------------------------- batch norm
+// fp64 BatchNorm(+ReLU) training forward/backward (FusedBatchNormReLU / BatchNorm2D on
+// float64 data, _nn.py:794-833, :701-736), following the reference's formulas in
+// double; gamma/beta are the module's fp32 parameters.  One workgroup per channel
+// reduces over the m = N*HW elements of the channel (layout 0: [m, C]; 1: NCHW).
+__device__ __forceinline__ int64_t bn_at(int layout, int64_t j, int64_t c, int64_t C,
+                                         int64_t HW) {
+  return layout == 0 ? j * C + c : ((j / HW) * C + c) * HW + j % HW;
+}
+
+__device__ __forceinline__ double block_sum_d(double v, double* red) {
+  v = tg_wave_sum_d(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  double t = 0.0;
+#pragma unroll
+  for (int w = 0; w < kT / 64; ++w) t += red[w];
+  return t;
+}
+
+// mean, var (population, two passes as xp.var), rstd = 1/sqrt(var + eps), running EMA
+__global__ __launch_bounds__(kT) void k64_bn_stats(int layout, const double* __restrict__ x,
+                                                   int64_t C, int64_t HW, int64_t m, double eps,
+                                                   double momentum, double* __restrict__ mean,
+                                                   double* __restrict__ var,
+                                                   double* __restrict__ rstd,
+                                                   double* __restrict__ rmean,
+                                                   double* __restrict__ rvar) {
+  __shared__ double red[kT / 64];
+  const int64_t c = blockIdx.x;
+  double s = 0.0;
+  for (int64_t j = threadIdx.x; j < m; j += kT) s += x[bn_at(layout, j, c, C, HW)];
+  const double mu = block_sum_d(s, red) / (double)m;
+  double q = 0.0;
+  for (int64_t j = threadIdx.x; j < m; j += kT) {
+    const double d = x[bn_at(layout, j, c, C, HW)] - mu;
+    q += d * d;
+  }
+  const double v = block_sum_d(q, red) / (double)m;
+  if (threadIdx.x == 0) {
+    mean[c] = mu;
+    if (var) var[c] = v;
+    rstd[c] = 1.0 / sqrt(v + eps);
+    if (rmean) rmean[c] = (1.0 - momentum) * rmean[c] + momentum * mu;
+    if (rvar) rvar[c] = (1.0 - momentum) * rvar[c] + momentum * v;
+  }
+}
+
+// y = [relu](gamma * ((x - mean) * rstd) + beta)
+__global__ __launch_bounds__(kT) void k64_bn_apply(int layout, const double* __restrict__ x,
+                                                   const float* __restrict__ gamma,
+                                                   const float* __restrict__ beta,
+                                                   const double* __restrict__ mean,
+                                                   const double* __restrict__ rstd,
+                                                   double* __restrict__ y, int64_t n, int64_t C,
+                                                   int64_t HW, int relu) {
+  for (int64_t e = (int64_t)blockIdx.x * kT + threadIdx.x; e < n; e += (int64_t)gridDim.x * kT) {
+    const int64_t c = layout == 0 ? e % C : (e / HW) % C;
+    double v = (double)gamma[c] * ((x[e] - mean[c]) * rstd[c]) + (double)beta[c];
+    y[e] = relu ? fmax(v, 0.0) : v;
+  }
+}
+
+// Backward per channel (_nn.py:812-833, :720-736), for float64 data and for the
+// eval-mode BatchNorm2D backward (which the reference runs with the same formula on the
+// running statistics): T is the data type, every sum is in double.
+// dout = dy*[out > 0]; dgamma += sum dout*xn,
+// dbeta += sum dout (rounded into the fp32 gradients as the reference's in-place add on
+// float32 arrays does); coefficients of dx = dxn*rstd + dvar*(2/m)*xc + dmean/m with
+// dxn = dout*gamma, dvar = sum(dxn*xc)*(-0.5)*rstd^3,
+// dmean = sum(dxn*(-rstd)) + dvar*(-2/m)*sum(xc).
+template <typename T>
+__global__ __launch_bounds__(kT) void k64_bn_bwd_sums(
+    int layout, const T* __restrict__ x, const double* __restrict__ mean,
+    const double* __restrict__ rstd, const float* __restrict__ gamma,
+    const float* __restrict__ beta, const T* __restrict__ dy, int64_t C, int64_t HW,
+    int64_t m, int relu, float* __restrict__ dgamma, float* __restrict__ dbeta, int acc_params,
+    double* __restrict__ coef) {
+  __shared__ double red[kT / 64];
+  const int64_t c = blockIdx.x;
+  const double mu = mean[c], rs = rstd[c], g = (double)gamma[c], b = (double)beta[c];
+  double s_dxn = 0.0, s_dn = 0.0, s_d = 0.0, s_dxc = 0.0, s_xc = 0.0;
+  for (int64_t j = threadIdx.x; j < m; j += kT) {
+    const int64_t e = bn_at(layout, j, c, C, HW);
+    const double xc = (double)x[e] - mu, xn = xc * rs;
+    double d = (double)dy[e];
+    if (relu && !(g * xn + b > 0.0)) d = 0.0;
+    s_dn += d * xn;
+    s_d += d;
+    s_dxc += d * g * xc;
+    s_dxn += d * g * (-rs);
+    s_xc += xc;
+  }
+  s_dn = block_sum_d(s_dn, red);
+  s_d = block_sum_d(s_d, red);
+  s_dxc = block_sum_d(s_dxc, red);
+  s_dxn = block_sum_d(s_dxn, red);
+  s_xc = block_sum_d(s_xc, red);
+  if (threadIdx.x == 0) {
+    if (dgamma) dgamma[c] = (float)(acc_params ? (double)dgamma[c] + s_dn : s_dn);
+    if (dbeta) dbeta[c] = (float)(acc_params ? (double)dbeta[c] + s_d : s_d);
+    const double dvar = s_dxc * -0.5 * (rs * rs * rs);
+    const double dmean = s_dxn + dvar * (-2.0 / (double)m) * s_xc;
+    coef[3 * c] = dvar * (2.0 / (double)m);
+    coef[3 * c + 1] = dmean / (double)m;
+    coef[3 * c + 2] = 0.0;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kT) void k64_bn_bwd_dx(int layout, const T* __restrict__ x,
+                                                    const double* __restrict__ mean,
+                                                    const double* __restrict__ rstd,
+                                                    const float* __restrict__ gamma,
+                                                    const float* __restrict__ beta,
+                                                    const T* __restrict__ dy,
+                                                    const double* __restrict__ coef,
+                                                    T* __restrict__ dx, int64_t n,
+                                                    int64_t C, int64_t HW, int relu, int acc) {
+  for (int64_t e = (int64_t)blockIdx.x * kT + threadIdx.x; e < n; e += (int64_t)gridDim.x * kT) {
+    const int64_t c = layout == 0 ? e % C : (e / HW) % C;
+    const double rs = rstd[c], g = (double)gamma[c];
+    const double xc = (double)x[e] - mean[c];
+    double d = (double)dy[e];
+    if (relu && !(g * (xc * rs) + (double)beta[c] > 0.0)) d = 0.0;
+    const double v = d * g * rs + coef[3 * c] * xc + coef[3 * c + 1];
+    dx[e] = (T)(acc ? (double)dx[e] + v : v);
+  }
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------- internal entry points
@@ -702,4 +888,212 @@ TG_EXPORT int tg_cross_entropy_bwd_f64(const double* logits, const int64_t* targ
                                                         label_smoothing, scale, grad,
                                                         accumulate);
   return tg_check_launch("tg_cross_entropy_bwd_f64");
+}
+
+// ---------------------------------------------------------------- fp64 attention entries
+namespace {
+constexpr int64_t kFa64Budget = (int64_t)256 << 20;  // bytes of scores per chunk buffer
+
+int64_t fa64_heads_per_chunk(int64_t H, int64_t Sq, int64_t Sk) {
+  const int64_t per = Sq * Sk * (int64_t)sizeof(double);
+  int64_t hc = per > 0 ? kFa64Budget / per : H;
+  if (hc < 1) hc = 1;
+  return hc < H ? hc : H;
+}
+
+struct Fa64Geo {
+  int64_t H, Sq, Sk, D;
+  int layout;
+  int64_t rs() const { return layout ? H * D : D; }
+  int64_t hstride(int64_t S) const { return layout ? D : S * D; }
+  int64_t head(int64_t b, int64_t h, int64_t S) const {
+    return layout ? (b * S * H + h) * D : (b * H + h) * S * D;
+  }
+};
+
+int fa64_check(const char* who, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
+               int layout) {
+  TG_REQUIRE(B >= 0 && H >= 0 && Sq >= 0 && Sk >= 0 && D > 0, "%s: bad shape", who);
+  TG_REQUIRE(layout == 0 || layout == 1, "%s: layout %d", who, layout);
+  TG_REQUIRE(H <= 65535 && (Sq + 63) / 64 <= 65535 && (Sk + 63) / 64 <= 65535,
+             "%s: shape too large for the fp64 path", who);
+  return TG_OK;
+}
+}  // namespace
+
+TG_EXPORT size_t tg_flash_attn_f64_workspace(int64_t B, int64_t H, int64_t Sq, int64_t Sk) {
+  if (B <= 0 || H <= 0 || Sq <= 0 || Sk <= 0) return 0;
+  return (size_t)(2 * fa64_heads_per_chunk(H, Sq, Sk) * Sq * Sk) * sizeof(double);
+}
+
+TG_EXPORT int tg_flash_attn_fwd_f64(const double* q, const double* k, const double* v,
+                                    double* o, double* lse, int64_t B, int64_t H, int64_t Sq,
+                                    int64_t Sk, int64_t D, double scale, int causal, int layout,
+                                    void* workspace, size_t workspace_bytes, void* stream) {
+  int st = fa64_check("tg_flash_attn_fwd_f64", B, H, Sq, Sk, D, layout);
+  if (st) return st;
+  if (B == 0 || H == 0 || Sq == 0) return TG_OK;
+  TG_REQUIRE(q && k && v && o && lse, "tg_flash_attn_fwd_f64: null pointer");
+  hipStream_t s = tg_stream(stream);
+  const Fa64Geo g{H, Sq, Sk, D, layout};
+  if (Sk == 0) {  // no keys: zero output, log-sum-exp -inf
+    for (int64_t b = 0; b < B; ++b)
+      for (int64_t h = 0; h < H; ++h) {
+        st = tg64_gemm(0, 0, Sq, D, 0, 1.0, nullptr, 1, 0, nullptr, 1, 0, 0.0,
+                       o + g.head(b, h, Sq), g.rs(), 0, 1, nullptr, s);
+        if (st) return st;
+      }
+    return tg64_fill(lse, B * H * Sq, -INFINITY, s);
+  }
+  const size_t need = tg_flash_attn_f64_workspace(B, H, Sq, Sk);
+  TG_REQUIRE(workspace && workspace_bytes >= need,
+             "tg_flash_attn_fwd_f64: workspace of %zu bytes needed", need);
+  double* S = (double*)workspace;
+  const int64_t hc = fa64_heads_per_chunk(H, Sq, Sk);
+  for (int64_t b = 0; b < B; ++b)
+    for (int64_t h0 = 0; h0 < H; h0 += hc) {
+      const int64_t n = hc < H - h0 ? hc : H - h0;
+      const int64_t oq = g.head(b, h0, Sq), ok = g.head(b, h0, Sk);
+      st = tg64_gemm(0, 1, Sq, Sk, D, scale, q + oq, g.rs(), g.hstride(Sq), k + ok, g.rs(),
+                     g.hstride(Sk), 0.0, S, Sk, Sq * Sk, n, nullptr, s);
+      if (st) return st;
+      k64_fa_softmax<<<(unsigned)((n * Sq + 3) / 4), kT, 0, s>>>(S, lse + (b * H + h0) * Sq,
+                                                                 n * Sq, Sq, Sk, causal);
+      st = tg_check_launch("tg_flash_attn_fwd_f64");
+      if (st) return st;
+      st = tg64_gemm(0, 0, Sq, D, Sk, 1.0, S, Sk, Sq * Sk, v + ok, g.rs(), g.hstride(Sk), 0.0,
+                     o + oq, g.rs(), g.hstride(Sq), n, nullptr, s);
+      if (st) return st;
+    }
+  return TG_OK;
+}
+
+TG_EXPORT int tg_flash_attn_bwd_f64(const double* q, const double* k, const double* v,
+                                    const double* o, const double* dout, const double* lse,
+                                    double* dq, double* dk, double* dv, int64_t B, int64_t H,
+                                    int64_t Sq, int64_t Sk, int64_t D, double scale, int causal,
+                                    int layout, int accumulate, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+  (void)o;  // the row term is rowsum(P * dP), as the reference forms it
+  int st = fa64_check("tg_flash_attn_bwd_f64", B, H, Sq, Sk, D, layout);
+  if (st) return st;
+  if (B == 0 || H == 0 || (Sq == 0 && Sk == 0)) return TG_OK;
+  TG_REQUIRE(q && k && v && dout && lse && dq && dk && dv,
+             "tg_flash_attn_bwd_f64: null pointer");
+  hipStream_t s = tg_stream(stream);
+  const Fa64Geo g{H, Sq, Sk, D, layout};
+  const double beta = accumulate ? 1.0 : 0.0;
+  if (Sq == 0 || Sk == 0) {  // empty product: dq (Sk == 0) or dk, dv (Sq == 0) are zero
+    for (int64_t b = 0; b < B; ++b)
+      for (int64_t h = 0; h < H; ++h) {
+        if (Sq > 0)
+          st = tg64_gemm(0, 0, Sq, D, 0, 1.0, nullptr, 1, 0, nullptr, 1, 0, beta,
+                         dq + g.head(b, h, Sq), g.rs(), 0, 1, nullptr, s);
+        if (!st && Sk > 0)
+          st = tg64_gemm(0, 0, Sk, D, 0, 1.0, nullptr, 1, 0, nullptr, 1, 0, beta,
+                         dk + g.head(b, h, Sk), g.rs(), 0, 1, nullptr, s);
+        if (!st && Sk > 0)
+          st = tg64_gemm(0, 0, Sk, D, 0, 1.0, nullptr, 1, 0, nullptr, 1, 0, beta,
+                         dv + g.head(b, h, Sk), g.rs(), 0, 1, nullptr, s);
+        if (st) return st;
+      }
+    return TG_OK;
+  }
+  const size_t need = tg_flash_attn_f64_workspace(B, H, Sq, Sk);
+  TG_REQUIRE(workspace && workspace_bytes >= need,
+             "tg_flash_attn_bwd_f64: workspace of %zu bytes needed", need);
+  const int64_t hc = fa64_heads_per_chunk(H, Sq, Sk);
+  double* P = (double*)workspace;
+  double* dP = P + hc * Sq * Sk;
+  const int64_t rs = g.rs(), hq = g.hstride(Sq), hk = g.hstride(Sk), ss = Sq * Sk;
+  for (int64_t b = 0; b < B; ++b)
+    for (int64_t h0 = 0; h0 < H; h0 += hc) {
+      const int64_t n = hc < H - h0 ? hc : H - h0;
+      const int64_t oq = g.head(b, h0, Sq), ok = g.head(b, h0, Sk);
+      // P = exp(scale Q K^T - lse)
+      st = tg64_gemm(0, 1, Sq, Sk, D, scale, q + oq, rs, hq, k + ok, rs, hk, 0.0, P, Sk, ss, n,
+                     nullptr, s);
+      if (st) return st;
+      const int64_t e = n * ss;
+      k64_fa_p<<<(unsigned)grid_for(e, kT * 4), kT, 0, s>>>(P, lse + (b * H + h0) * Sq, n * Sq,
+                                                          Sq, Sk, causal);
+      if ((st = tg_check_launch("tg_flash_attn_bwd_f64"))) return st;
+      // dV (+)= P^T dO;  dP = dO V^T;  dS over dP;  dQ (+)= dS K;  dK (+)= dS^T Q
+      st = tg64_gemm(1, 0, Sk, D, Sq, 1.0, P, Sk, ss, dout + oq, rs, hq, beta, dv + ok, rs, hk,
+                     n, nullptr, s);
+      if (!st)
+        st = tg64_gemm(0, 1, Sq, Sk, D, 1.0, dout + oq, rs, hq, v + ok, rs, hk, 0.0, dP, Sk, ss,
+                       n, nullptr, s);
+      if (st) return st;
+      k64_fa_ds<<<(unsigned)((n * Sq + 3) / 4), kT, 0, s>>>(P, dP, n * Sq, Sk, scale);
+      if ((st = tg_check_launch("tg_flash_attn_bwd_f64"))) return st;
+      st = tg64_gemm(0, 0, Sq, D, Sk, 1.0, dP, Sk, ss, k + ok, rs, hk, beta, dq + oq, rs, hq, n,
+                     nullptr, s);
+      if (!st)
+        st = tg64_gemm(1, 0, Sk, D, Sq, 1.0, dP, Sk, ss, q + oq, rs, hq, beta, dk + ok, rs, hk,
+                       n, nullptr, s);
+      if (st) return st;
+    }
+  return TG_OK;
+}
+
+// ---------------------------------------------------------------- batch norm entries
+TG_EXPORT size_t tg_batchnorm_stats_workspace(int64_t C) {
+  return C > 0 ? (size_t)(3 * C) * sizeof(double) : 0;
+}
+
+TG_EXPORT int tg_batchnorm_fwd_train_f64(int layout, const double* x, const float* gamma,
+                                         const float* beta, double* y, double* mean,
+                                         double* rstd, double* var, double* running_mean,
+                                         double* running_var, double momentum, int64_t N,
+                                         int64_t C, int64_t HW, double eps, int relu,
+                                         void* stream) {
+  TG_REQUIRE(layout == 0 || layout == 1, "tg_batchnorm_fwd_train_f64: layout %d", layout);
+  TG_REQUIRE(N >= 0 && C >= 0 && HW >= 0, "tg_batchnorm_fwd_train_f64: negative shape");
+  const int64_t m = N * HW;
+  if (C == 0) return TG_OK;
+  TG_REQUIRE(m > 0, "tg_batchnorm_fwd_train_f64: no elements per channel");
+  TG_REQUIRE(C <= 0x7fffffff, "tg_batchnorm_fwd_train_f64: too many channels");
+  TG_REQUIRE(x && gamma && beta && y && mean && rstd, "tg_batchnorm_fwd_train_f64: null pointer");
+  hipStream_t s = tg_stream(stream);
+  k64_bn_stats<<<(unsigned)C, kT, 0, s>>>(layout, x, C, HW, m, eps, momentum, mean, var, rstd,
+                                          running_mean, running_var);
+  int st = tg_check_launch("tg_batchnorm_fwd_train_f64");
+  if (st) return st;
+  const int64_t n = m * C;
+  k64_bn_apply<<<(unsigned)grid_for(n, kT * 4), kT, 0, s>>>(layout, x, gamma, beta, mean, rstd, y,
+                                                            n, C, HW, relu);
+  return tg_check_launch("tg_batchnorm_fwd_train_f64");
+}
+
+TG_EXPORT int tg_batchnorm_bwd_stats(int dtype, int layout, const void* x, const double* mean,
+                                     const double* rstd, const float* gamma, const float* beta,
+                                     const void* dy, void* dx, float* dgamma, float* dbeta,
+                                     int64_t N, int64_t C, int64_t HW, int relu,
+                                     int accumulate_dx, int accumulate_params, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  TG_REQUIRE(layout == 0 || layout == 1, "tg_batchnorm_bwd_stats: layout %d", layout);
+  TG_REQUIRE(dtype == TG_F32 || dtype == TG_F64, "tg_batchnorm_bwd_stats: dtype %d", dtype);
+  TG_REQUIRE(N >= 0 && C >= 0 && HW >= 0, "tg_batchnorm_bwd_stats: negative shape");
+  const int64_t m = N * HW;
+  if (C == 0) return TG_OK;
+  TG_REQUIRE(m > 0, "tg_batchnorm_bwd_stats: no elements per channel");
+  TG_REQUIRE(C <= 0x7fffffff, "tg_batchnorm_bwd_stats: too many channels");
+  TG_REQUIRE(x && mean && rstd && gamma && beta && dy && dx, "tg_batchnorm_bwd_stats: null pointer");
+  TG_REQUIRE(workspace && workspace_bytes >= tg_batchnorm_stats_workspace(C),
+             "tg_batchnorm_bwd_stats: workspace of %zu bytes needed",
+             tg_batchnorm_stats_workspace(C));
+  hipStream_t s = tg_stream(stream);
+  double* coef = (double*)workspace;
+  const int64_t n = m * C;
+#define BN(T)                                                                                   \
+  k64_bn_bwd_sums<T><<<(unsigned)C, kT, 0, s>>>(layout, (const T*)x, mean, rstd, gamma, beta,   \
+                                                (const T*)dy, C, HW, m, relu, dgamma, dbeta,    \
+                                                accumulate_params, coef);                       \
+  k64_bn_bwd_dx<T><<<(unsigned)grid_for(n, kT * 4), kT, 0, s>>>(                                \
+      layout, (const T*)x, mean, rstd, gamma, beta, (const T*)dy, coef, (T*)dx, n, C, HW, relu,  \
+      accumulate_dx)
+  if (dtype == TG_F64) { BN(double); } else { BN(float); }
+#undef BN
+  return tg_check_launch("tg_batchnorm_bwd_stats");
 }

@@ -1219,7 +1219,7 @@ def flash_attention(query, key, value, block_size=64, is_causal=False, scale=Non
     D = q4.shape[-1]
     scale = scale or D ** -0.5
     dt = q4.dtype
-    if dt not in (torch.float16, torch.bfloat16, torch.float32):
+    if dt not in (torch.float16, torch.bfloat16, torch.float32, torch.float64):
         raise TypeError(f"flash_attention: unsupported dtype {dt}")
     q4c, k4c, v4c = q4, k4.to(dt), v4.to(dt)
     # (B, S, H, D) memory (the head split of a projection, viewed as (B, H, S, D)) is read

@@ -94,6 +94,16 @@ SIGNATURES = {
                                         _i64, _i64, _i64, _i64, _f32, _i32, _i32, _i32, _vp, _sz,
                                         _vp]),
     "tg_flash_attn_bwd_workspace": (_sz, [_i64, _i64, _i64, _i64, _i64]),
+    "tg_flash_attn_f64_workspace": (_sz, [_i64, _i64, _i64, _i64]),
+    "tg_flash_attn_fwd_f64": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f64,
+                                     _i32, _i32, _vp, _sz, _vp]),
+    "tg_flash_attn_bwd_f64": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
+                                     _i64, _i64, _i64, _f64, _i32, _i32, _i32, _vp, _sz, _vp]),
+    "tg_batchnorm_stats_workspace": (_sz, [_i64]),
+    "tg_batchnorm_fwd_train_f64": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                          _f64, _i64, _i64, _i64, _f64, _i32, _vp]),
+    "tg_batchnorm_bwd_stats": (_i32, [_i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                      _i64, _i64, _i64, _i32, _i32, _i32, _vp, _sz, _vp]),
     "tg_flash_attn_bwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
                                  _i64, _i64, _i64, _f32, _i32, _i32, _vp, _sz, _vp]),
     "tg_cross_entropy_fwd": (_i32, [_i32, _vp, _vp, _i64, _i64, _f32, _vp, _vp, _vp]),
@@ -491,6 +501,49 @@ def batchnorm_fwd_train(x, gamma, beta, eps, momentum, running_mean, running_var
         ptr(running_mean), ptr(running_var), float(momentum), N, C, HW, float(eps),
         int(bool(relu)), ptr(ws), ws.numel(), stream_handle()))
     return y, mean, rstd, var
+
+
+def batchnorm_fwd_train_f64(x, gamma, beta, eps, momentum, running_mean, running_var, relu,
+                            layout=NHWC):
+    """fp64 training forward: y (fp64) and the batch mean, rstd, var (fp64, [C]); the
+    running statistics (fp64 buffers, or None) take the EMA update in double."""
+    _dev(x, "x")
+    if x.dtype != torch.float64:
+        raise TypeError("batchnorm_fwd_train_f64: x must be float64")
+    for n, t in (("running_mean", running_mean), ("running_var", running_var)):
+        if t is not None and (t.dtype != torch.float64 or not t.is_contiguous()):
+            raise TypeError(f"batchnorm_fwd_train_f64: {n} must be a contiguous float64 buffer")
+    N, C, HW = _bn_shape(x, layout)
+    y = torch.empty_like(x)
+    mean = torch.empty(C, dtype=torch.float64, device=x.device)
+    rstd, var = torch.empty_like(mean), torch.empty_like(mean)
+    ensure_device(x.device.index)
+    _check("tg_batchnorm_fwd_train_f64", load().tg_batchnorm_fwd_train_f64(
+        layout, ptr(x), ptr(gamma), ptr(beta), ptr(y), ptr(mean), ptr(rstd), ptr(var),
+        ptr(running_mean), ptr(running_var), float(momentum), N, C, HW, float(eps),
+        int(bool(relu)), stream_handle()))
+    return y, mean, rstd, var
+
+
+def batchnorm_bwd_stats(x, mean, rstd, gamma, beta, dy, dx, dgamma, dbeta, relu,
+                        accumulate_dx, accumulate_params, layout=NHWC):
+    """BatchNorm backward with the reference's full formula against given per-channel
+    statistics (fp64 mean and rstd [C]): the fp64 path, and the eval-mode BatchNorm2D
+    backward on the running statistics.  x, dy, dx fp32 or fp64."""
+    for n, t in (("x", x), ("dy", dy), ("dx", dx), ("mean", mean), ("rstd", rstd)):
+        _dev(t, n)
+    _same("batchnorm_bwd_stats", x, dy, dx)
+    if mean.dtype != torch.float64 or rstd.dtype != torch.float64:
+        raise TypeError("batchnorm_bwd_stats: mean and rstd must be float64")
+    N, C, HW = _bn_shape(x, layout)
+    lib = load()
+    ensure_device(x.device.index)
+    ws = workspace(lib.tg_batchnorm_stats_workspace(C), x.device)
+    _check("tg_batchnorm_bwd_stats", lib.tg_batchnorm_bwd_stats(
+        dtype_code(x), layout, ptr(x), ptr(mean), ptr(rstd), ptr(gamma), ptr(beta), ptr(dy),
+        ptr(dx), ptr(dgamma), ptr(dbeta), N, C, HW, int(bool(relu)), int(bool(accumulate_dx)),
+        int(bool(accumulate_params)), ptr(ws), ws.numel(), stream_handle()))
+    return dx
 
 
 def batchnorm_bwd(x, mean, rstd, gamma, beta, dy, dx, dgamma, dbeta, relu, accumulate_dx,
@@ -966,8 +1019,18 @@ def flash_attn_fwd(q, k, v, scale, causal, layout=0):
     if k.shape != (B, H, Sk, D) or v.shape != (B, H, Sk, D):
         raise ValueError(f"flash_attn: k/v shape mismatch {tuple(k.shape)} {tuple(v.shape)}")
     o = fa_empty(B, H, Sq, D, q.dtype, q.device, layout)
-    lse = torch.empty(B, H, Sq, dtype=torch.float32, device=q.device)
     ensure_device(q.device.index)
+    if q.dtype == torch.float64:
+        # fp64: scores of a chunk of heads materialised in a workspace, fp64 GEMMs, lse in
+        # double
+        lse = torch.empty(B, H, Sq, dtype=torch.float64, device=q.device)
+        lib = load()
+        ws = workspace(lib.tg_flash_attn_f64_workspace(B, H, Sq, Sk), q.device)
+        _check("tg_flash_attn_fwd_f64", lib.tg_flash_attn_fwd_f64(
+            ptr(q), ptr(k), ptr(v), ptr(o), ptr(lse), B, H, Sq, Sk, D, float(scale),
+            int(bool(causal)), int(layout), ptr(ws), ws.numel(), stream_handle()))
+        return o, lse
+    lse = torch.empty(B, H, Sq, dtype=torch.float32, device=q.device)
     _check("tg_flash_attn_fwd", load().tg_flash_attn_fwd_layout(
         dtype_code(q), ptr(q), ptr(k), ptr(v), ptr(o), ptr(lse), B, H, Sq, Sk, D, float(scale),
         int(bool(causal)), int(layout), stream_handle()))
@@ -983,6 +1046,15 @@ def flash_attn_bwd(q, k, v, o, do, lse, dq, dk, dv, scale, causal, accumulate, l
     Sk = k.shape[2]
     lib = load()
     ensure_device(q.device.index)
+    if q.dtype == torch.float64:
+        if lse.dtype != torch.float64:
+            raise TypeError("flash_attn_bwd: fp64 inputs need the fp64 lse of the forward")
+        ws = workspace(lib.tg_flash_attn_f64_workspace(B, H, Sq, Sk), q.device)
+        _check("tg_flash_attn_bwd_f64", lib.tg_flash_attn_bwd_f64(
+            ptr(q), ptr(k), ptr(v), ptr(o), ptr(do), ptr(lse), ptr(dq), ptr(dk), ptr(dv), B, H,
+            Sq, Sk, D, float(scale), int(bool(causal)), int(layout), int(bool(accumulate)),
+            ptr(ws), ws.numel(), stream_handle()))
+        return
     ws = workspace(lib.tg_flash_attn_bwd_workspace(B, H, Sq, Sk, D), q.device)
     _check("tg_flash_attn_bwd", lib.tg_flash_attn_bwd_layout(
         dtype_code(q), ptr(q), ptr(k), ptr(v), ptr(o), ptr(do), ptr(lse), ptr(dq), ptr(dk),

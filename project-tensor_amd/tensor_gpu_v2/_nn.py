@@ -282,7 +282,8 @@ class _BatchNormBase(Module):
         if x.ndim != 4:
             raise ValueError(f"{type(self).__name__} expects a 4-D input, got {x.shape}")
         xd = x.data.contiguous()
-        if xd.dtype != torch.float32:
+        fp64 = xd.dtype == torch.float64
+        if not fp64 and xd.dtype != torch.float32:
             xd = xd.float()
         C = xd.shape[3] if self.data_format == "NHWC" else xd.shape[1]
         if C != self.num_features:
@@ -291,41 +292,92 @@ class _BatchNormBase(Module):
         g32 = gamma.data.float().contiguous()
         b32 = beta.data.float().contiguous()
         if not self._training:
-            return self._eval_forward(xd, g32, b32)
-        y, mean, rstd, var = L.batchnorm_fwd_train(
-            xd, g32, b32, self.eps, self.momentum, self.running_mean, self.running_var,
-            self._relu, self._layout())
+            return self._eval_forward(x, xd, g32, b32)
+        relu, layout = self._relu, self._layout()
+        if fp64:
+            # float64 data is computed in double (_nn.py:794-833 on float64 arrays); the
+            # reference's running-stat update promotes its float32 buffers to float64
+            self.running_mean = self.running_mean.to(torch.float64).contiguous()
+            self.running_var = self.running_var.to(torch.float64).contiguous()
+            y, mean, rstd, var = L.batchnorm_fwd_train_f64(
+                xd, g32, b32, self.eps, self.momentum, self.running_mean, self.running_var,
+                relu, layout)
+        else:
+            rm, rv = self.running_mean, self.running_var
+            wide = rm.dtype != torch.float32  # float64 after an earlier float64 batch
+            if wide:
+                rm, rv = rm.float(), rv.float()
+            y, mean, rstd, var = L.batchnorm_fwd_train(xd, g32, b32, self.eps, self.momentum,
+                                                       rm, rv, relu, layout)
+            if wide:
+                self.running_mean.copy_(rm)
+                self.running_var.copy_(rv)
         out = Tensor._wrap(y, (x, gamma, beta), type(self).__name__)
         self._cache = (mean, rstd)
-        relu, layout = self._relu, self._layout()
 
         if out._requires_grad:
             def _backward():
                 dy = out._grad_out()
-                if dy.dtype != torch.float32 or not dy.is_contiguous():
-                    dy = dy.float().contiguous()
+                if dy.dtype != xd.dtype or not dy.is_contiguous():
+                    dy = dy.to(xd.dtype).contiguous()
                 (dg, db), accp = _targets([gamma, beta])
-                if x._has_grad() and x.data.dtype == torch.float32:
+                direct = x._has_grad() and x.data.dtype == xd.dtype
+                if direct:
                     dx, accx = x._grad_target()
+                else:
+                    dx, accx = torch.empty_like(xd), False
+                if fp64:
+                    L.batchnorm_bwd_stats(xd, mean, rstd, g32, b32, dy, dx, dg, db, relu, accx,
+                                          accp, layout)
+                else:
                     L.batchnorm_bwd(xd, mean, rstd, g32, b32, dy, dx, dg, db, relu, accx, accp,
                                     layout)
-                else:
-                    dx = L.batchnorm_bwd(xd, mean, rstd, g32, b32, dy, torch.empty_like(xd), dg,
-                                         db, relu, False, accp, layout)
-                    if x._has_grad():
-                        x._accumulate(dx, True)
+                if x._has_grad() and not direct:
+                    x._accumulate(dx, True)
             out._backward = _backward
         return out
 
-    def _eval_forward(self, xd, g32, b32):
-        inv = 1.0 / torch.sqrt(self.running_var + self.eps)
-        scale = g32 * inv
-        shift = b32 - g32 * self.running_mean * inv
+    def _eval_forward(self, x, xd, g32, b32):
         shp = (1, 1, 1, -1) if self.data_format == "NHWC" else (1, -1, 1, 1)
-        y = xd * scale.reshape(shp) + shift.reshape(shp)
+        rm, rv = self.running_mean, self.running_var
         if self._relu:
-            y = torch.clamp_min(y, 0)
-        return Tensor(y, requires_grad=False)
+            # FusedBatchNormReLU inference (_nn.py:780-787, :857-862): fp32 scale and shift
+            # folded from the running statistics, no graph
+            inv = 1.0 / torch.sqrt(rv + self.eps)
+            scale = (g32 * inv).to(torch.float32)
+            shift = (b32 - g32 * rm * inv).to(torch.float32)
+            y = torch.clamp_min(xd * scale.reshape(shp) + shift.reshape(shp), 0)
+            return Tensor(y, requires_grad=False)
+        # BatchNorm2D in eval mode (_nn.py:706-745) normalises with the running statistics
+        # and keeps its backward, the training formula applied to those statistics
+        inv = 1.0 / torch.sqrt(rv + self.eps)
+        y = g32.to(xd.dtype).reshape(shp) * ((xd - rm.reshape(shp)) * inv.reshape(shp)) \
+            + b32.to(xd.dtype).reshape(shp)
+        y = y.to(torch.promote_types(xd.dtype, rm.dtype))
+        gamma, beta = self.gamma, self.beta
+        out = Tensor._wrap(y, (x, gamma, beta), type(self).__name__)
+        if out._requires_grad:
+            # std_inv in the running statistics' own dtype, as the reference forms it
+            mean64 = rm.to(torch.float64).contiguous()
+            rstd64 = inv.to(torch.float64).contiguous()
+            layout = self._layout()
+
+            def _backward():
+                dy = out._grad_out()
+                if dy.dtype != xd.dtype or not dy.is_contiguous():
+                    dy = dy.to(xd.dtype).contiguous()
+                (dg, db), accp = _targets([gamma, beta])
+                direct = x._has_grad() and x.data.dtype == xd.dtype
+                if direct:
+                    dx, accx = x._grad_target()
+                else:
+                    dx, accx = torch.empty_like(xd), False
+                L.batchnorm_bwd_stats(xd, mean64, rstd64, g32, b32, dy, dx, dg, db, False, accx,
+                                      accp, layout)
+                if x._has_grad() and not direct:
+                    x._accumulate(dx, True)
+            out._backward = _backward
+        return out
 
     def parameters(self):
         return [self.gamma, self.beta]

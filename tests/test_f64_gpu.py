@@ -253,3 +253,152 @@ def test_embedding_bwd_f64_rows_into_fp32(cuda, n, V, acc):
     L().embedding_bwd(dev(d), torch.tensor(idx, device="cuda"), grad, acc)
     exp = (base + want) if acc else want
     np.testing.assert_array_equal(host(grad), exp)
+
+
+@pytest.mark.parametrize("B,H,Sq,Sk,D,causal,layout", [
+    (2, 3, 70, 70, 40, False, 0), (2, 3, 70, 70, 40, True, 0),
+    (1, 2, 33, 65, 16, True, 0),   # fewer queries than keys
+    (1, 2, 65, 33, 24, True, 0),   # more queries than keys
+    (2, 4, 48, 48, 32, True, 1),   # (B, S, H, D) memory, the head split of a projection
+    (1, 1, 300, 257, 8, False, 0),
+])
+def test_flash_attention_f64(cuda, B, H, Sq, Sk, D, causal, layout):
+    """fp64 forward (o, natural-log lse) and backward (the reference's row term
+    rowsum(P*dP)) against the float64 oracle; accumulate adds to existing gradients."""
+    rng = np.random.default_rng(B * 100 + Sq + Sk + D + causal)
+    q = rng.standard_normal((B, H, Sq, D))
+    k = rng.standard_normal((B, H, Sk, D))
+    v = rng.standard_normal((B, H, Sk, D))
+    do = rng.standard_normal((B, H, Sq, D))
+    scale = D ** -0.5
+    o_ref, lse_ref = O.flash_attention_fwd(q, k, v, causal, scale)
+    dq_ref, dk_ref, dv_ref = O.flash_attention_bwd(q, k, v, do, causal, scale)
+
+    def put(a):  # layout 1: (B, S, H, D) memory viewed as (B, H, S, D)
+        t = dev(a)
+        return t.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3) if layout else t
+
+    qt, kt, vt, dot = put(q), put(k), put(v), put(do)
+    o, lse = L().flash_attn_fwd(qt, kt, vt, scale, causal, layout)
+    assert o.dtype == torch.float64 and lse.dtype == torch.float64
+    assert_close(o, o_ref, RTOL_F64, "fp64 attention o")
+    assert_close(lse, lse_ref, RTOL_F64, "fp64 attention lse")
+    grads = [L().fa_empty(B, H, s, D, torch.float64, qt.device, layout) for s in (Sq, Sk, Sk)]
+    for g in grads:
+        g.fill_(0.5)
+    L().flash_attn_bwd(qt, kt, vt, o, dot, lse, *grads, scale, causal, True, layout)
+    for g, ref, n in zip(grads, (dq_ref, dk_ref, dv_ref), ("dq", "dk", "dv")):
+        assert_close(g, ref + 0.5, 1e-10, f"fp64 attention {n}")
+
+
+def test_flash_attention_f64_autograd_3d(cuda):
+    """tg.flash_attention on float64 (B, L, D) tensors: values and gradients stay
+    float64 and match the oracle."""
+    import tensor_gpu_v2 as tg
+    rng = np.random.default_rng(9)
+    q, k, v = (rng.standard_normal((3, 50, 24)) for _ in range(3))
+    g = rng.standard_normal((3, 50, 24))
+    Q, K, V = tg.Tensor(q), tg.Tensor(k), tg.Tensor(v)
+    out = tg.flash_attention(Q, K, V, is_causal=True)
+    assert out.data.dtype == torch.float64
+    out.backward(tg.Tensor(g))
+    o_ref, _ = O.flash_attention_fwd(q, k, v, True)
+    assert_close(out.data, o_ref, RTOL_F64, "o")
+    for t, ref in zip((Q, K, V), O.flash_attention_bwd(q, k, v, g, True)):
+        assert t.grad.dtype == torch.float64
+        assert_close(t.grad, ref, 1e-10, "3-D fp64 attention grad")
+
+
+@pytest.mark.parametrize("fmt", ["NCHW", "NHWC"])
+@pytest.mark.parametrize("relu", [True, False])
+def test_batchnorm_f64_module(cuda, fmt, relu):
+    """FusedBatchNormReLU / BatchNorm2D on float64 data: output, batch statistics in the
+    running-stat update (float64 buffers, as the reference's update promotes them), dx in
+    double, dgamma/dbeta rounded into the fp32 parameter gradients — against the
+    oracle's float64 training forward/backward."""
+    import tensor_gpu_v2 as tg
+    rng = np.random.default_rng(11 + relu)
+    N, C, Hh, W = 4, 6, 5, 7
+    x_nchw = rng.standard_normal((N, C, Hh, W)) * 1.5 + 0.3
+    dy_nchw = rng.standard_normal((N, C, Hh, W))
+    mod = (tg.FusedBatchNormReLU if relu else tg.BatchNorm2D)(C, data_format=fmt)
+    g = (1 + 0.1 * rng.standard_normal(C)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(C)).astype(np.float32)
+    mod.gamma.data.copy_(torch.tensor(g))
+    mod.beta.data.copy_(torch.tensor(b))
+    to = (lambda a: a.transpose(0, 2, 3, 1).copy()) if fmt == "NHWC" else (lambda a: a)
+    x = tg.Tensor(to(x_nchw))
+    y = mod(x)
+    assert y.data.dtype == torch.float64
+    y.backward(tg.Tensor(to(dy_nchw)))
+    y_ref, cache = O.batchnorm_relu_fwd(x_nchw, g.astype(np.float64), b.astype(np.float64),
+                                        1e-5, relu)
+    dx_ref, dg_ref, db_ref = O.batchnorm_relu_bwd(dy_nchw, g.astype(np.float64), cache, relu)
+    assert_close(y.data, to(y_ref), RTOL_F64, "fp64 BN output")
+    assert x.grad.dtype == torch.float64
+    assert_close(x.grad, to(dx_ref), 1e-10, "fp64 BN dx")
+    assert mod.gamma.grad.dtype == torch.float32
+    assert_close(mod.gamma.grad, dg_ref, 1e-6, "BN dgamma (fp32 buffer)")
+    assert_close(mod.beta.grad, db_ref, 1e-6, "BN dbeta (fp32 buffer)")
+    assert mod.running_mean.dtype == torch.float64
+    assert_close(mod.running_mean, 0.1 * cache[5], RTOL_F64, "running mean")
+    assert_close(mod.running_var, 0.9 + 0.1 * cache[6], RTOL_F64, "running var")
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+@pytest.mark.parametrize("fmt", ["NCHW", "NHWC"])
+def test_batchnorm2d_eval_mode_gradient(cuda, dt, fmt):
+    """BatchNorm2D in eval mode normalises with the running statistics and still
+    differentiates, with the training formula applied to those statistics (reference
+    _nn.py:706-736): against the oracle's eval forward and its backward on that cache."""
+    import tensor_gpu_v2 as tg
+    rng = np.random.default_rng(21)
+    N, C, Hh, W = 3, 5, 4, 6
+    x_nchw = (rng.standard_normal((N, C, Hh, W)) * 2).astype(dt)
+    dy_nchw = rng.standard_normal((N, C, Hh, W)).astype(dt)
+    rm = (0.5 * rng.standard_normal(C)).astype(np.float32)
+    rv = (0.5 + rng.random(C)).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(C)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(C)).astype(np.float32)
+    mod = tg.BatchNorm2D(C, data_format=fmt)
+    mod.gamma.data.copy_(torch.tensor(g))
+    mod.beta.data.copy_(torch.tensor(b))
+    mod.running_mean.copy_(torch.tensor(rm))
+    mod.running_var.copy_(torch.tensor(rv))
+    mod.eval()
+    to = (lambda a: a.transpose(0, 2, 3, 1).copy()) if fmt == "NHWC" else (lambda a: a)
+    x = tg.Tensor(to(x_nchw))
+    y = mod(x)
+    y.backward(tg.Tensor(to(dy_nchw)))
+    # the reference's parameters and running statistics are float32 arrays: std_inv is
+    # formed in float32 and meets the data's dtype after that (NumPy promotion), so the
+    # oracle gets them as float32 too
+    y_ref, cache = O.batchnorm_eval_fwd(x_nchw, g, b, rm, rv, 1e-5)
+    dx_ref, dg_ref, db_ref = O.batchnorm_relu_bwd(dy_nchw, g, cache, False)
+    tol = RTOL_F64 if dt == np.float64 else RTOL_F32
+    assert_close(y.data, to(y_ref), tol, "eval BN output")
+    # dx: every sum in double here; the reference rounds std_inv**3 in float32, so
+    # the float64 result agrees to float32 rounding of that factor (1e-6)
+    assert_close(x.grad, to(dx_ref), 1e-6 if dt == np.float64 else RTOL_F32, "eval BN dx")
+    assert_close(mod.gamma.grad, dg_ref, 1e-6, "eval BN dgamma")
+    assert_close(mod.beta.grad, db_ref, 1e-6, "eval BN dbeta")
+
+
+@pytest.mark.parametrize("R,C", [(64, 128), (70, 33)])
+def test_transpose_add_f64(cuda, R, C):
+    """sync_tied_gradients' source.grad += param.grad.T (_training.py:264-284) with a
+    float64 side: added in double, cast once to the destination (bit-exact with NumPy)."""
+    rng = np.random.default_rng(R + C)
+    src = rng.standard_normal((R, C))
+    d64 = rng.standard_normal((C, R))
+    out = dev(d64)
+    L().transpose_add(dev(src), out)
+    assert np.array_equal(host(out), d64 + src.T)
+    d32 = rng.standard_normal((C, R)).astype(np.float32)
+    out32 = torch.tensor(d32, device="cuda")
+    L().transpose_add(dev(src), out32)
+    assert np.array_equal(out32.cpu().numpy(), (d32.astype(np.float64) + src.T).astype(np.float32))
+    s32 = rng.standard_normal((R, C)).astype(np.float32)
+    out = dev(d64)
+    L().transpose_add(torch.tensor(s32, device="cuda"), out)
+    assert np.array_equal(host(out), d64 + s32.astype(np.float64).T)

@@ -101,6 +101,29 @@ def test_batchnorm_relu_vs_torch(relu):
     close(db, bt.grad.numpy())
 
 
+def test_batchnorm_eval_with_batch_stats_equals_training():
+    """Pins batchnorm_eval_fwd's cache: with the running statistics set to the batch's
+    own mean and (population) variance, the eval-mode forward and the reference's
+    backward on that cache equal the training-mode ones, which torch pins above."""
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((3, 4, 5, 2)) * 2 + 0.5
+    g = 1 + 0.1 * rng.standard_normal(4)
+    b = 0.1 * rng.standard_normal(4)
+    dy = rng.standard_normal(x.shape)
+    yt, ct = O.batchnorm_relu_fwd(x, g, b, 1e-5, relu=False)
+    ye, ce = O.batchnorm_eval_fwd(x, g, b, x.mean(axis=(0, 2, 3)), x.var(axis=(0, 2, 3)), 1e-5)
+    close(ye, yt, 1e-12)
+    for a, e in zip(O.batchnorm_relu_bwd(dy, g, ce, relu=False),
+                    O.batchnorm_relu_bwd(dy, g, ct, relu=False)):
+        close(a, e, 1e-12)
+    # with other running statistics the dvar / dmean terms no longer vanish: dx differs
+    # from the plain chain rule gamma * rstd * dy of the eval forward
+    _, c2 = O.batchnorm_eval_fwd(x, g, b, np.zeros(4), np.ones(4), 1e-5)
+    dx2, _, _ = O.batchnorm_relu_bwd(dy, g, c2, relu=False)
+    plain = dy * (g / np.sqrt(1 + 1e-5)).reshape(1, 4, 1, 1)
+    assert np.abs(dx2 - plain).max() > 1e-3
+
+
 def test_batchnorm_nhwc_is_transposed_nchw():
     rng = np.random.default_rng(4)
     x = rng.standard_normal((2, 3, 4, 8))  # NHWC, C = 8
