@@ -358,7 +358,9 @@ int tg_embedding_bwd(int dtype_dout, const void* dout, const int64_t* indices, i
                      int64_t dim, int dtype_grad, void* grad, int64_t num_embeddings,
                      int accumulate, void* workspace, size_t workspace_bytes, void* stream);
 /* dst[c][r] += alpha * src[r][c] for src [rows, cols] (sync_tied_gradients,
- * _training.py:264-284: source.grad += param.grad.T). */
+ * _training.py:264-284: source.grad += param.grad.T).  fp32/fp16/bf16 in fp32; when
+ * either side is fp64 (fp64/fp64, fp64 into fp32, fp32 into fp64) in double, rounded
+ * once to the destination. */
 int tg_transpose_add(int dtype_src, const void* src, int64_t rows, int64_t cols, int dtype_dst,
                      void* dst, float alpha, void* stream);
 
