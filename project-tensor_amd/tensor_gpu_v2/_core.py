@@ -820,16 +820,24 @@ def _unique(children):
 
 def _scalar_like(v, ref):
     """Python scalars / arrays as device tensors.  Float scalars adopt the reference
-    tensor's dtype (NumPy 2 weak-scalar promotion keeps fp32 op fp32)."""
+    tensor's dtype (NumPy 2 weak-scalar promotion keeps fp32 op fp32).  A scalar is
+    made on the device by a fill kernel and an array goes through the pinned staging
+    copy: a pageable host-to-device copy (torch.tensor(v, device=...)) would block the
+    host until the device queue drains, e.g. in every GradScaler.scale(loss)."""
     if isinstance(v, torch.Tensor):
         return v
     if isinstance(v, (bool, int, float)):
         dt = ref.dtype if ref.is_floating_point() or isinstance(v, int) else torch.float32
         if isinstance(v, float) and not ref.is_floating_point():
             dt = torch.float32
-        return torch.tensor(v, dtype=dt, device="cuda")
-    arr = np.asarray(v)
-    return torch.as_tensor(arr, device="cuda")
+        # made in a wide dtype, then cast: a value outside dt's range becomes inf (or
+        # wraps) as the weak-scalar cast does (65536.0 as fp16 is inf), where a fill in
+        # dt itself would raise
+        wide = torch.float64 if dt.is_floating_point else torch.int64
+        if dt == torch.bool:
+            wide = torch.bool
+        return torch.full((), v, dtype=wide, device="cuda").to(dt)
+    return L.to_device(np.asarray(v))
 
 
 def _basic_index(idx):
@@ -843,9 +851,9 @@ def _index_to_torch(idx):
     if isinstance(idx, Tensor):
         return idx.data.long() if not idx.data.dtype == torch.bool else idx.data
     if isinstance(idx, np.ndarray):
-        return torch.as_tensor(idx, device="cuda")
+        return L.to_device(idx)
     if isinstance(idx, list):
-        return torch.as_tensor(np.asarray(idx), device="cuda")
+        return L.to_device(np.asarray(idx))
     return idx
 
 
@@ -1274,11 +1282,11 @@ def scaled_dot_product_attention(query, key, value, attn_mask=None, dropout_p=0.
     scores = (query @ key.transpose(0, 1, 3, 2)) * scale
     if is_causal:
         m = torch.triu(torch.ones(Lq, S, dtype=torch.bool, device="cuda"), diagonal=1)
-        scores.data = torch.where(m, torch.tensor(-1e9, dtype=scores.data.dtype, device="cuda"),
-                                  scores.data)
+        scores.data = torch.where(m, torch.full((), -1e9, dtype=scores.data.dtype,
+                                                device="cuda"), scores.data)
     if attn_mask is not None:
-        am = attn_mask.data if isinstance(attn_mask, Tensor) else torch.as_tensor(
-            np.asarray(attn_mask), device="cuda")
+        am = attn_mask.data if isinstance(attn_mask, Tensor) else L.to_device(
+            np.asarray(attn_mask))
         scores.data = scores.data + am.to(scores.data.dtype)
     attn = scores.softmax(axis=-1)
     if dropout_p > 0 and cfg._grad_enabled:
