@@ -267,6 +267,24 @@ int tg_gemm_wgrad(int dtype_ab, int64_t M, int64_t N, int64_t K, const void* X, 
                   const void* G, int64_t ldg, int dtype_w, void* dW, int64_t ldw, int acc_w,
                   int dtype_b, void* db, int acc_b, void* workspace, size_t workspace_bytes,
                   void* stream);
+/* n weight (+ bias) gradients of the same shape, tg_gemm_wgrad for each member g:
+ * dW[g] (+)= X[g]^T @ G[g], db[g] (+)= column sums of G[g] (db NULL or db[g] NULL: no
+ * bias; acc_w / acc_b NULL: overwrite all).  X, G, dW, db, acc_w and acc_b are host
+ * arrays of n entries.  The reference runs these products one node at a time in its
+ * backward sweep (the matmul node of _core.py:1064-1068 for each Linear, _nn.py:258-285);
+ * gathered, the equal-shaped layers' products (e.g. the q/k/v/o projections of every
+ * block) become one launch of whole-K tiles, without the K split and finishing pass
+ * that a lone small-output product needs.  fp16/bf16 groups whose tiles fill the CUs
+ * take the grouped kernel; other members run through tg_gemm_wgrad one after another.
+ * Every member's gradient buffers must be distinct.  workspace:
+ * tg_gemm_wgrad_group_workspace(dtype_ab, n, M, N, K, any db[g] != NULL) bytes. */
+size_t tg_gemm_wgrad_group_workspace(int dtype_ab, int n, int64_t M, int64_t N, int64_t K,
+                                     int with_bias);
+int tg_gemm_wgrad_group(int dtype_ab, int n, int64_t M, int64_t N, int64_t K,
+                        const void* const* X, int64_t ldx, const void* const* G, int64_t ldg,
+                        int dtype_w, void* const* dW, int64_t ldw, const int* acc_w,
+                        int dtype_b, void* const* db, const int* acc_b, void* workspace,
+                        size_t workspace_bytes, void* stream);
 
 /* ---- attention ------------------------------------------------------------ */
 /* FlashAttention forward on contiguous (B,H,S,D) tensors, saving the row

@@ -602,13 +602,16 @@ __device__ __forceinline__ float frag_sum(const Vec8<tg_bf16>::type& v, float ac
 // (one v_dot2 per pair of elements, beside the MFMAs); the waves of the first block
 // row that hold rows 0.. of C, which between them see every k of every column once,
 // store theirs.
+// One block's C tile of a DMA-staged GEMM (A, B, C already at their batch entry).
+// BSUM: the blocks of the first tile row also sum B's columns over the whole K range
+// and store the sums to bsum (fp32) or, with bsum null, to dbo (dtype dbt, added to
+// its contents when dbacc; dbo null: nowhere).
 template <typename T, typename TC, bool TA, bool TB, int WGM, int WGN, int SM, int SN, int OCC,
-          bool BSUM = false>
-__global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_v3(
+          bool BSUM>
+__device__ __forceinline__ void v3_tile(
     int64_t M, int64_t N, int64_t K, float alpha, const T* __restrict__ A, int64_t lda,
-    int64_t sa, const T* __restrict__ B, int64_t ldb, int64_t sb, float beta,
-    TC* __restrict__ C, int64_t ldc, int64_t sc,
-    const float* __restrict__ bias, float* __restrict__ bsum) {
+    const T* __restrict__ B, int64_t ldb, float beta, TC* __restrict__ C, int64_t ldc,
+    const float* __restrict__ bias, float* __restrict__ bsum, void* dbo, int dbt, bool dbacc) {
   constexpr int NW = WGM * WGN, TBM = WGM * SM * 32, TBN = WGN * SN * 32;
   constexpr int ATILE = TBM * V3_BK * 2, BTILE = TBN * V3_BK * 2;
   __shared__ __attribute__((aligned(1024))) char a0[ATILE];
@@ -621,10 +624,6 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_v3(
   int64_t lin = (int64_t)blockIdx.y * gx + blockIdx.x;
   if (T_ % 8 == 0) lin = (lin % 8) * (T_ / 8) + lin / 8;  // XCD-contiguous bands
   const int64_t tm = lin / gx, tn = lin % gx;
-  const int64_t bz = blockIdx.z;
-  A += bz * sa;
-  B += bz * sb;
-  C += bz * sc;
   const int64_t m0 = tm * TBM, n0 = tn * TBN;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = (wave / WGN) * SM * 32, wn = (wave % WGN) * SN * 32;
@@ -748,7 +747,17 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_v3(
       for (int j = 0; j < SN; ++j) {
         const float v = bsums[j] + __shfl_xor(bsums[j], 32);
         const int64_t col = n0 + wn + j * 32 + l32;
-        if (lh == 0 && col < N) bsum[bz * N + col] = v;
+        if (lh == 0 && col < N) {
+          if (bsum) bsum[col] = v;
+          else if (dbo == nullptr) {
+          } else if (dbt == TG_F32) {
+            float* d = static_cast<float*>(dbo) + col;
+            *d = v + (dbacc ? *d : 0.f);
+          } else {
+            T* d = static_cast<T*>(dbo) + col;
+            *d = tg_from_float<T>(v + (dbacc ? tg_to_float(*d) : 0.f));
+          }
+        }
       }
     }
   }
@@ -828,6 +837,43 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_v3(
         }
       }
     }
+}
+
+template <typename T, typename TC, bool TA, bool TB, int WGM, int WGN, int SM, int SN, int OCC,
+          bool BSUM = false>
+__global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_v3(
+    int64_t M, int64_t N, int64_t K, float alpha, const T* __restrict__ A, int64_t lda,
+    int64_t sa, const T* __restrict__ B, int64_t ldb, int64_t sb, float beta,
+    TC* __restrict__ C, int64_t ldc, int64_t sc,
+    const float* __restrict__ bias, float* __restrict__ bsum) {
+  const int64_t bz = blockIdx.z;
+  v3_tile<T, TC, TA, TB, WGM, WGN, SM, SN, OCC, BSUM>(
+      M, N, K, alpha, A + bz * sa, lda, B + bz * sb, ldb, beta, C + bz * sc, ldc, bias,
+      BSUM ? bsum + bz * N : nullptr, nullptr, 0, false);
+}
+
+// A group of same-shape GEMMs C_g (+)= A_g^T B_g with their own operands (weight
+// gradients of several layers), member g = blockIdx.z, passed by value.
+constexpr int kGroupMax = 32;
+template <typename T, typename TC>
+struct V3Group {
+  const T* A[kGroupMax];
+  const T* B[kGroupMax];
+  TC* C[kGroupMax];
+  void* db[kGroupMax];  // null: no column sums for this member
+  float beta[kGroupMax];
+  unsigned dbacc;       // bit g: add member g's column sums to db's contents
+};
+
+template <typename T, typename TC, int WGM, int WGN, int SM, int SN, bool BSUM>
+__global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_v3g(
+    int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
+    const V3Group<T, TC> g, int dbt) {
+  // (one v3_tile instance per kernel: each holds its own static LDS stages)
+  const int bz = blockIdx.z;
+  v3_tile<T, TC, true, false, WGM, WGN, SM, SN, 1, BSUM>(
+      M, N, K, 1.f, g.A[bz], lda, g.B[bz], ldb, g.beta[bz], g.C[bz], ldc, nullptr, nullptr,
+      g.db[bz], dbt, (g.dbacc >> bz) & 1u);
 }
 
 // Block shapes of the DMA-staged kernel (waves of 64 x 64 of C): 4 x 2 waves
@@ -1163,6 +1209,104 @@ TG_EXPORT int tg_gemm_wgrad(int dtype_ab, int64_t M, int64_t N, int64_t K, const
   }
   if (db && !fused)
     return tg_reduce_rows(dtype_ab, G, dtype_b, db, K, N, acc_b, red, p.red, stream);
+  return TG_OK;
+}
+
+namespace {
+// One launch of k_gemm_v3g over members [g0, g0 + n) (n <= kGroupMax, every member
+// passing v3_ok): 256x256 blocks (shape 2) or 256x128 blocks (shape 1), whole K per block.
+template <typename T, typename TC>
+int wgrad_group_launch(int shape, int g0, int n, int64_t M, int64_t N, int64_t K,
+                       const void* const* X, int64_t ldx, const void* const* G, int64_t ldg,
+                       void* const* dW, int64_t ldw, const int* acc_w, int dtype_b,
+                       void* const* db, const int* acc_b, hipStream_t s) {
+  V3Group<T, TC> grp{};
+  bool any_b = false;
+  for (int i = 0; i < n; ++i) {
+    grp.A[i] = static_cast<const T*>(X[g0 + i]);
+    grp.B[i] = static_cast<const T*>(G[g0 + i]);
+    grp.C[i] = static_cast<TC*>(dW[g0 + i]);
+    grp.beta[i] = acc_w && acc_w[g0 + i] ? 1.f : 0.f;
+    grp.db[i] = db ? db[g0 + i] : nullptr;
+    if (grp.db[i]) {
+      any_b = true;
+      if (acc_b && acc_b[g0 + i]) grp.dbacc |= 1u << i;
+    }
+  }
+#define TG_GG(WGM, WGN, SM, SN)                                                                \
+  do {                                                                                         \
+    constexpr int TBM = WGM * SM * 32, TBN = WGN * SN * 32;                                    \
+    dim3 g3((unsigned)((N + TBN - 1) / TBN), (unsigned)((M + TBM - 1) / TBM), (unsigned)n);    \
+    if (any_b)                                                                                 \
+      k_gemm_v3g<T, TC, WGM, WGN, SM, SN, true><<<g3, 64 * WGM * WGN, 0, s>>>(                 \
+          M, N, K, ldx, ldg, ldw, grp, dtype_b);                                               \
+    else                                                                                       \
+      k_gemm_v3g<T, TC, WGM, WGN, SM, SN, false><<<g3, 64 * WGM * WGN, 0, s>>>(                \
+          M, N, K, ldx, ldg, ldw, grp, dtype_b);                                               \
+  } while (0)
+  if (shape == 2) TG_GG(4, 2, 2, 4);
+  else TG_GG(kBigWGM, kBigWGN, kBigSM, kBigSN);
+#undef TG_GG
+  return tg_check_launch("tg_gemm_wgrad_group");
+}
+}  // namespace
+
+TG_EXPORT size_t tg_gemm_wgrad_group_workspace(int dtype_ab, int n, int64_t M, int64_t N,
+                                               int64_t K, int with_bias) {
+  // members that cannot be grouped run one by one through tg_gemm_wgrad, in stream
+  // order over the same workspace
+  return n > 0 ? tg_gemm_wgrad_workspace(dtype_ab, M, N, K, with_bias) : 0;
+}
+
+TG_EXPORT int tg_gemm_wgrad_group(int dtype_ab, int n, int64_t M, int64_t N, int64_t K,
+                                  const void* const* X, int64_t ldx, const void* const* G,
+                                  int64_t ldg, int dtype_w, void* const* dW, int64_t ldw,
+                                  const int* acc_w, int dtype_b, void* const* db,
+                                  const int* acc_b, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  TG_REQUIRE(n >= 0 && M >= 0 && N >= 0 && K >= 0, "tg_gemm_wgrad_group: negative extent");
+  if (n == 0) return TG_OK;
+  TG_REQUIRE(X && G && dW, "tg_gemm_wgrad_group: null pointer array");
+  bool with_b = false;
+  for (int i = 0; i < n && db; ++i) with_b = with_b || db[i] != nullptr;
+  const size_t need = tg_gemm_wgrad_group_workspace(dtype_ab, n, M, N, K, with_b);
+  TG_REQUIRE(workspace_bytes >= need, "tg_gemm_wgrad_group: workspace of %zu bytes, need %zu",
+             workspace_bytes, need);
+  hipStream_t s = tg_stream(stream);
+  const int64_t ncu = tg_num_cus();
+  const bool lowp = dtype_ab == TG_F16 || dtype_ab == TG_BF16;
+  bool grouped = lowp && M > 0 && N > 0 && K > 0 && ldw >= N &&
+                 (dtype_w == TG_F32 || dtype_w == dtype_ab) &&
+                 (!with_b || dtype_b == TG_F32 || dtype_b == dtype_ab);
+  for (int i = 0; i < n && grouped; ++i)
+    grouped = dW[i] && v3_ok(2, 1, 0, M, N, K, X[i], ldx, 0, G[i], ldg, 0);
+  int g0 = 0;
+  while (grouped && g0 < n) {
+    const int cnt = (int)std::min<int64_t>(n - g0, kGroupMax);
+    const int64_t t256 = cnt * ((M + 255) / 256) * ((N + 255) / 256);
+    const int64_t t128 = cnt * ((M + 255) / 256) * ((N + 127) / 128);
+    // whole-K blocks only where the members' tiles fill the CUs; else the K split
+    const int shape = t256 >= kHugeTiles * ncu / 4 ? 2 : (t128 >= ncu ? 1 : 0);
+    if (shape == 0) break;
+    int rc;
+#define TG_WGG(T, TC)                                                                   \
+  rc = wgrad_group_launch<T, TC>(shape, g0, cnt, M, N, K, X, ldx, G, ldg, dW, ldw, acc_w, \
+                                 dtype_b, with_b ? db : nullptr, acc_b, s)
+    if (dtype_ab == TG_F16) {
+      if (dtype_w == TG_F32) TG_WGG(tg_half, float); else TG_WGG(tg_half, tg_half);
+    } else {
+      if (dtype_w == TG_F32) TG_WGG(tg_bf16, float); else TG_WGG(tg_bf16, tg_bf16);
+    }
+#undef TG_WGG
+    if (rc != TG_OK) return rc;
+    g0 += cnt;
+  }
+  for (; g0 < n; ++g0) {
+    const int rc = tg_gemm_wgrad(dtype_ab, M, N, K, X[g0], ldx, G[g0], ldg, dtype_w, dW[g0], ldw,
+                                 acc_w ? acc_w[g0] : 0, dtype_b, db ? db[g0] : nullptr,
+                                 acc_b ? acc_b[g0] : 0, workspace, workspace_bytes, stream);
+    if (rc != TG_OK) return rc;
+  }
   return TG_OK;
 }
 

@@ -27,6 +27,56 @@ def _noop():
     return None
 
 
+# ------------------------------------------------------- deferred weight gradients
+# During Tensor.backward() a 16-bit Linear layer's weight (and bias) gradient is queued
+# instead of computed at once; the queue is flushed before backward() returns, with the
+# equal-shaped products of all layers run as one grouped launch (L.wgrad_group).  Each
+# queued parameter leaf has already claimed its gradient buffer; any other access to
+# that gradient first flushes the queue, so the order of accumulation is unchanged.
+_WG_QUEUE = []       # (A2, G2, wbuf, wacc, bbuf, bacc) in sweep order
+_WG_TARGETS = {}     # id -> Tensor whose gradient a queued record writes
+_WG_STATE = [0, 0]   # [backward nesting depth, bytes of operands the queue keeps alive]
+_WG_MAX_BYTES = 4 << 30  # flush early once the queue keeps this much alive
+
+
+def _wgrad_defer(A2, G2, w, wbuf, wacc, b=None, bbuf=None, bacc=False):
+    _WG_QUEUE.append((A2, G2, wbuf, wacc, bbuf, bacc))
+    _WG_TARGETS[id(w)] = w
+    if b is not None:
+        _WG_TARGETS[id(b)] = b
+    _WG_STATE[1] += A2.numel() * A2.element_size() + G2.numel() * G2.element_size()
+    if _WG_STATE[1] > _WG_MAX_BYTES:
+        _wgrad_flush()
+
+
+def _wgrad_flush():
+    """Run the queued weight-gradient products: records of one shape and dtype set as
+    one grouped call, in the order their groups first appear."""
+    if not _WG_QUEUE:
+        return
+    recs = list(_WG_QUEUE)
+    _WG_QUEUE.clear()
+    _WG_TARGETS.clear()
+    _WG_STATE[1] = 0
+    groups = {}
+    for r in recs:
+        A2, G2, wbuf, _, bbuf, _ = r
+        key = (tuple(A2.shape), G2.shape[1], A2.dtype, wbuf.dtype,
+               None if bbuf is None else bbuf.dtype)
+        groups.setdefault(key, []).append(r)
+    for (a_shape, N, _, _, _), rs in groups.items():
+        K = a_shape[1]
+        if len(rs) == 1:
+            A2, G2, wbuf, wacc, bbuf, bacc = rs[0]
+            L.wgrad(A2, G2, wbuf.view(K, N), wacc, None if bbuf is None else bbuf.view(N), bacc)
+        else:
+            has_b = rs[0][4] is not None
+            L.wgrad_group([r[0] for r in rs], [r[1] for r in rs],
+                          [r[2].view(K, N) for r in rs], [r[3] for r in rs],
+                          [r[4].view(N) for r in rs] if has_b else None,
+                          [r[5] for r in rs] if has_b else None)
+
+
 def _to_device_tensor(data, dtype):
     """Convert array-likes / torch tensors to a device tensor of `dtype` (or the
     inferred dtype when None).  Returns (tensor, inferred_dtype)."""
@@ -145,6 +195,8 @@ class Tensor:
 
     @property
     def grad(self):
+        if _WG_TARGETS and id(self) in _WG_TARGETS:
+            _wgrad_flush()
         if self._gz:
             self._g = self._new_buf(0)
             self._gz = False
@@ -154,6 +206,8 @@ class Tensor:
 
     @grad.setter
     def grad(self, value):
+        if _WG_TARGETS and id(self) in _WG_TARGETS:
+            _wgrad_flush()
         self._gz = False
         self._gsh = False
         if value is None:
@@ -175,6 +229,8 @@ class Tensor:
     def _grad_out(self):
         """Gradient flowing into this node's closure (zeros if nothing arrived).
         Read-only: it may be shared with other nodes."""
+        if _WG_TARGETS and id(self) in _WG_TARGETS:
+            _wgrad_flush()
         if self._gz:
             return self._new_buf(0)
         return self._g
@@ -182,6 +238,8 @@ class Tensor:
     def _privatize(self):
         """Give this node its own contiguous copy of a gradient buffer it shares (or
         holds with strides)."""
+        if _WG_TARGETS and id(self) in _WG_TARGETS:
+            _wgrad_flush()
         buf = self._new_buf()
         _copy_into(buf, self._g)
         self._g = buf
@@ -189,6 +247,8 @@ class Tensor:
 
     def _grad_target(self):
         """(buffer, accumulate) for a kernel that adds this tensor's gradient."""
+        if _WG_TARGETS and id(self) in _WG_TARGETS:
+            _wgrad_flush()
         if self._gz:
             self._g = self._new_buf()
             self._gz = False
@@ -202,6 +262,8 @@ class Tensor:
         source None means no prior gradient (overwrite).  A gradient shared with
         another node is not copied first: the kernel reads it as the source and writes
         this tensor's own new buffer; otherwise source is the buffer itself."""
+        if _WG_TARGETS and id(self) in _WG_TARGETS:
+            _wgrad_flush()
         if (not self._gz and self._gsh and self._g.is_contiguous()
                 and self._g.dtype == self.data.dtype and self._g.shape == self.data.shape):
             src = self._g
@@ -218,6 +280,8 @@ class Tensor:
         both nodes are marked shared, so the first in-place write to either one
         copies (out of place for an accumulation, which moves no more bytes than the
         in-place one would)."""
+        if _WG_TARGETS and id(self) in _WG_TARGETS:
+            _wgrad_flush()
         if not self._gz or g.dtype != self.data.dtype or not (g.is_contiguous() or _dense(g)):
             self._accumulate(g)
             return
@@ -243,6 +307,8 @@ class Tensor:
 
     def _accumulate(self, g, owned=False):
         """self.grad += g (g: torch tensor broadcast-compatible in shape, any float dtype)."""
+        if _WG_TARGETS and id(self) in _WG_TARGETS:
+            _wgrad_flush()
         if not self._has_grad():
             return
         if g.shape != self.data.shape:
@@ -338,6 +404,8 @@ class Tensor:
                       dtype=np.float32)
 
     def zero_grad(self):
+        if _WG_TARGETS and id(self) in _WG_TARGETS:
+            _wgrad_flush()
         if self._has_grad():
             self._g = None
             self._gz = True
@@ -749,7 +817,8 @@ class Tensor:
         """Reverse-mode sweep (_core.py:1426-1461): topological order over the
         recorded graph (iterative DFS), seed with `gradient` (added to any existing
         grad) or ones when the grad is absent or all zero, then run each closure once
-        in reverse order and drop it."""
+        in reverse order and drop it.  Weight gradients of 16-bit Linear layers queued
+        during the sweep are computed, grouped by shape, before it returns."""
         topo = []
         visited = set()
         stack = [(self, False)]
@@ -789,9 +858,15 @@ class Tensor:
             self._g = self._new_buf(1)
             self._gz = False
             self._gsh = False
-        for v in reversed(topo):
-            v._backward()
-            v._backward = _noop
+        _WG_STATE[0] += 1
+        try:
+            for v in reversed(topo):
+                v._backward()
+                v._backward = _noop
+        finally:
+            _WG_STATE[0] -= 1
+            if _WG_STATE[0] == 0:
+                _wgrad_flush()
 
 
 # ====================================================================== helpers
@@ -1061,18 +1136,28 @@ def _linear(x, w, b):
                         _copy_into(buf, da.reshape(buf.shape))
             fuse = (w._has_grad() and b is not None and b._has_grad() and g.dtype == cdt
                     and b.data.numel() == N and b.data.shape[-1] == N)
+            # 16-bit products into leaf parameters wait for the end of the sweep
+            defer = (_WG_STATE[0] > 0 and cdt in (torch.float16, torch.bfloat16)
+                     and not w._prev and (b is None or not b._prev))
             if fuse:
                 # dW and db from one pass over the output gradient
                 wbuf, wacc = w._grad_target()
                 bbuf, bacc = b._grad_target()
                 if _direct_out(wbuf.dtype, cdt) and _direct_out(bbuf.dtype, cdt):
-                    L.wgrad(A2, G2, wbuf.view(K, N), wacc, bbuf.view(N), bacc)
+                    if defer:
+                        _wgrad_defer(A2, G2, w, wbuf, wacc, b, bbuf, bacc)
+                    else:
+                        L.wgrad(A2, G2, wbuf.view(K, N), wacc, bbuf.view(N), bacc)
                 else:
                     _wgrad_into(G2, wbuf, wacc)
                     L.reduce_rows(G2, bbuf.view(N), bacc)
                 return
             if w._has_grad():
-                _wgrad_into(G2, *w._grad_target())
+                wbuf, wacc = w._grad_target()
+                if defer and _direct_out(wbuf.dtype, cdt):
+                    _wgrad_defer(A2, G2, w, wbuf, wacc)
+                else:
+                    _wgrad_into(G2, wbuf, wacc)
             if b is not None and b._has_grad():
                 b._accumulate_unb(g)
 

@@ -86,6 +86,9 @@ SIGNATURES = {
     "tg_gemm_wgrad_workspace": (_sz, [_i32, _i64, _i64, _i64, _i32]),
     "tg_gemm_wgrad": (_i32, [_i32, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _i32, _vp, _i64, _i32,
                              _i32, _vp, _i32, _vp, _sz, _vp]),
+    "tg_gemm_wgrad_group_workspace": (_sz, [_i32, _i32, _i64, _i64, _i64, _i32]),
+    "tg_gemm_wgrad_group": (_i32, [_i32, _i32, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _i32,
+                                   _vp, _i64, _vp, _i32, _vp, _vp, _vp, _sz, _vp]),
     "tg_flash_attn_fwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                  _f32, _i32, _vp]),
     "tg_flash_attn_fwd_layout": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
@@ -893,6 +896,8 @@ def wgrad(x, g, dw, acc_w, db=None, acc_b=False):
         raise TypeError(f"wgrad: x and g dtypes differ ({x.dtype} vs {g.dtype})")
     K, M = x.shape
     N = g.shape[1]
+    if not (x.is_contiguous() and g.is_contiguous()):
+        raise ValueError("wgrad: x and g must be contiguous")
     if tuple(dw.shape) != (M, N) or not dw.is_contiguous():
         raise ValueError(f"wgrad: dw must be a contiguous [{M}, {N}] buffer")
     if db is not None and (db.numel() != N or not db.is_contiguous()):
@@ -908,6 +913,64 @@ def wgrad(x, g, dw, acc_w, db=None, acc_b=False):
         stream_handle()))
     return dw
 
+
+
+def wgrad_group(xs, gs, dws, acc_ws, dbs=None, acc_bs=None):
+    """wgrad for n members of one shape at once: dws[i] (+)= xs[i]^T @ gs[i] and
+    dbs[i] (+)= gs[i].sum(0) (dbs None, or an entry None: no bias).  Equal-shaped 16-bit
+    members whose tiles fill the CUs run as one launch; the gradient buffers must be
+    distinct."""
+    n = len(xs)
+    if not (len(gs) == len(dws) == len(acc_ws) == n):
+        raise ValueError("wgrad_group: xs, gs, dws and acc_ws differ in length")
+    if n == 0:
+        return
+    dbs = list(dbs) if dbs is not None else [None] * n
+    acc_bs = list(acc_bs) if acc_bs is not None else [False] * n
+    if len(dbs) != n or len(acc_bs) != n:
+        raise ValueError("wgrad_group: dbs and acc_bs must have one entry per member")
+    x0, g0 = xs[0], gs[0]
+    if x0.dim() != 2 or g0.dim() != 2 or x0.shape[0] != g0.shape[0]:
+        raise ValueError(f"wgrad_group: x {tuple(x0.shape)} and g {tuple(g0.shape)} must be "
+                         "[K, M], [K, N]")
+    K, M = x0.shape
+    N = g0.shape[1]
+    dbt = next((d.dtype for d in dbs if d is not None), None)
+    seen = set()
+    for x, g, dw, db in zip(xs, gs, dws, dbs):
+        for nm, t in (("x", x), ("g", g), ("dw", dw)):
+            _dev(t, nm)
+        if tuple(x.shape) != (K, M) or tuple(g.shape) != (K, N):
+            raise ValueError("wgrad_group: members differ in shape")
+        if x.dtype != x0.dtype or g.dtype != x0.dtype or dw.dtype != dws[0].dtype:
+            raise TypeError("wgrad_group: members differ in dtype")
+        if not (x.is_contiguous() and g.is_contiguous()):
+            raise ValueError("wgrad_group: x and g must be contiguous")
+        if tuple(dw.shape) != (M, N) or not dw.is_contiguous():
+            raise ValueError(f"wgrad_group: dw must be a contiguous [{M}, {N}] buffer")
+        targets = [dw]
+        if db is not None:
+            _dev(db, "db")
+            if db.numel() != N or not db.is_contiguous() or db.dtype != dbt:
+                raise ValueError(f"wgrad_group: db must be a contiguous {dbt} buffer of {N} "
+                                 "elements")
+            targets.append(db)
+        for t in targets:
+            if t.data_ptr() in seen:
+                raise ValueError("wgrad_group: two members write one gradient buffer")
+            seen.add(t.data_ptr())
+    lib = load()
+    dev = dws[0].device
+    ensure_device(dev.index)
+    with_b = dbt is not None
+    ws = workspace(lib.tg_gemm_wgrad_group_workspace(dtype_code(x0), n, M, N, K, int(with_b)),
+                   dev)
+    accw = (ctypes.c_int * n)(*[int(bool(a)) for a in acc_ws])
+    accb = (ctypes.c_int * n)(*[int(bool(a)) for a in acc_bs])
+    _check("tg_gemm_wgrad_group", lib.tg_gemm_wgrad_group(
+        dtype_code(x0), n, M, N, K, _ptr_array(xs), M, _ptr_array(gs), N, dtype_code(dws[0]),
+        _ptr_array(dws), N, accw, _TORCH_TO_CODE[dbt] if with_b else 0,
+        _ptr_array(dbs) if with_b else None, accb, ptr(ws), ws.numel(), stream_handle()))
 
 _CUS = {}
 

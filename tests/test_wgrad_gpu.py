@@ -136,3 +136,109 @@ def test_linear_autocast_accumulated(cuda):
     gy = 2.0 * yh                        # d(sum y^2)/dy, formed in fp16 by the engine
     assert_close(lin.w.grad, 2 * (xs.T @ gy).numpy(), RTOL_F16, "Linear dW")
     assert_close(lin.b.grad, 2 * gy.sum(0).numpy(), RTOL_F16, "Linear db")
+
+
+# ---------------------------------------------------------------- grouped members
+def _group_case(n, M, N, K, dt, wdt, bdt, seed, bias=(), acc=()):
+    """n members with their own operands; bias / acc: member indices with a bias
+    gradient / accumulating into existing gradients."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    xs = [torch.randn(K, M, device="cuda", generator=g).to(dt) for _ in range(n)]
+    gs = [torch.randn(K, N, device="cuda", generator=g).to(dt) for _ in range(n)]
+    w0 = [torch.randn(M, N, device="cuda", generator=g).to(wdt) for _ in range(n)]
+    b0 = [torch.randn(N, device="cuda", generator=g).to(bdt) for _ in range(n)]
+    dws = [w.clone() for w in w0]
+    dbs = [b.clone() if i in bias else None for i, b in enumerate(b0)]
+    accs = [i in acc for i in range(n)]
+    L().wgrad_group(xs, gs, dws, accs, dbs if bias else None, accs if bias else None)
+    for i in range(n):
+        ref_w = xs[i].double().T @ gs[i].double() + (w0[i].double() if accs[i] else 0.0)
+        rtol = RTOL_F32_MM if wdt == torch.float32 else _tol(wdt)
+        assert_close(dws[i], ref_w, rtol, f"dW member {i} of {n} ({M}x{N}x{K} {dt})")
+        if i in bias:
+            ref_b = gs[i].double().sum(0) + (b0[i].double() if accs[i] else 0.0)
+            assert_close(dbs[i], ref_b, RTOL_F32 if bdt == torch.float32 else _tol(bdt),
+                         f"db member {i}")
+
+
+@pytest.mark.parametrize("n,M,N,K", [
+    (16, 1024, 1024, 8192),  # q/k/v/o projections of four blocks: 256x256 whole-K tiles
+    (4, 1024, 4096, 8192),   # FC weights of four blocks
+    (6, 1024, 1024, 2048),   # 256x128 tiles
+    (3, 256, 256, 1024),     # too few tiles: one by one (K split)
+])
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_wgrad_group(cuda, n, M, N, K, dt):
+    _group_case(n, M, N, K, dt, torch.float32, torch.float32, n + M + K,
+                bias=set(range(n)), acc={i for i in range(n) if i % 2})
+
+
+def test_wgrad_group_mixed_bias_lowp_outputs(cuda):
+    """Members without a bias beside members with one; gradients in the operands'
+    16-bit dtype."""
+    for dt in (torch.float16, torch.bfloat16):
+        _group_case(8, 1024, 1024, 4096, dt, dt, dt, 3, bias={0, 3, 5}, acc={1, 3, 4})
+
+
+def test_wgrad_group_chunks(cuda):
+    """40 members: a first launch of 32, the remaining 8 (too few tiles) one by one;
+    and a group without any bias."""
+    _group_case(40, 512, 512, 256, torch.float16, torch.float32, torch.float32, 7,
+                bias=set(range(0, 40, 3)), acc=set(range(0, 40, 2)))
+    _group_case(5, 1024, 2048, 1024, torch.bfloat16, torch.float32, torch.float32, 8)
+
+
+def test_wgrad_group_ragged_and_rejects(cuda):
+    """Ragged edge tiles (M, N not multiples of the tile) and the checks of the
+    wrapper: duplicate gradient buffers and unequal shapes."""
+    _group_case(12, 1000, 776, 2048, torch.float16, torch.float32, torch.float32, 11,
+                bias=set(range(12)), acc={2})
+    x = torch.randn(64, 64, device="cuda").half()
+    dw = torch.empty(64, 64, device="cuda")
+    with pytest.raises(ValueError):
+        L().wgrad_group([x, x], [x, x], [dw, dw], [False, False])
+    with pytest.raises(ValueError):
+        L().wgrad_group([x, x[:32]], [x, x[:32]], [dw, torch.empty_like(dw)], [False, False])
+
+
+def _mlp_grads(defer, seed=4):
+    """Gradients of a stack of equal Linear layers (one applied twice) under fp16
+    autocast over two backward passes; defer False turns the queue off by setting its
+    byte limit to zero."""
+    import numpy as np
+    import tensor_gpu_v2 as tg
+    from tensor_gpu_v2 import _core
+    rng = np.random.default_rng(seed)
+    d = 1024
+    # ten layers over 8192 tokens: the sweep queues nine products (layer 1's second
+    # use to layer 2; grouped) until layer 1's first use flushes them, then two (one by one)
+    layers = [tg.Linear(d, d) for _ in range(10)]
+    for lin in layers:
+        lin.w.data = tg.Tensor(rng.standard_normal((d, d)).astype(np.float32) * 0.04).data
+        lin.b.data = tg.Tensor(rng.standard_normal(d).astype(np.float32) * 0.1).data
+    xs = [rng.standard_normal((8, 1024, d)).astype(np.float32) for _ in range(2)]
+    saved = _core._WG_MAX_BYTES
+    _core._WG_MAX_BYTES = saved if defer else -1
+    try:
+        for x_np in xs:
+            h = tg.Tensor(x_np)
+            with tg.autocast():
+                for lin in layers + [layers[1]]:  # layer 1 twice: its gradient accumulates
+                    h = lin(h).relu()
+                loss = (h * h).mean()
+            loss.backward()
+            assert not _core._WG_QUEUE and not _core._WG_TARGETS
+    finally:
+        _core._WG_MAX_BYTES = saved
+    return [(lin.w.grad.clone(), lin.b.grad.clone()) for lin in layers]
+
+
+def test_linear_deferred_weight_gradients(cuda):
+    """The engine's queued, grouped weight gradients against the same network with
+    every product run at once (queue limit zero): same tolerance as one GEMM against
+    another (the products sum K in a different order)."""
+    a = _mlp_grads(True)
+    b = _mlp_grads(False)
+    for i, ((wa, ba), (wb, bb)) in enumerate(zip(a, b)):
+        assert_close(wa, wb.double(), RTOL_F16, f"layer {i} dW")
+        assert_close(ba, bb.double(), RTOL_F16, f"layer {i} db")
