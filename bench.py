@@ -229,6 +229,23 @@ def _op_unscale(torch, L, g):
     return Timed("unscale_check", run, 8 * sum(sizes), "GB/s", HBM_PEAK_GBS)
 
 
+def _op_unscale_norm(torch, L, g):
+    """GradScaler unscale check + the clip's L2 norm in one read-only pass over 83.2M
+    fp32 grads (the unscale itself left pending for AdamW): 4 B/param."""
+    lib, s, p = L.load(), L.stream_handle, L.ptr
+    sizes = [NPARAM // 48] * 48
+    gs = [torch.randn(n, device="cuda", generator=g) for n in sizes]
+    flags = torch.empty(len(gs), dtype=torch.int32, device="cuda")
+    out = torch.empty(1, dtype=torch.float64, device="cuda")
+    arr, num = L._ptr_array(gs), L._numel_array(gs)
+    ws = L.workspace(lib.tg_unscale_norm_workspace(len(gs), num), "cuda")
+
+    def run():
+        L._check("unscale_norm", lib.tg_unscale_norm(len(gs), 0, arr, num, 1.0 / 65536,
+                                                     p(flags), p(out), p(ws), ws.numel(), s()))
+    return Timed("unscale_norm", run, 4 * sum(sizes), "GB/s", HBM_PEAK_GBS)
+
+
 def _op_gemm(torch, L, g):
     """C5 FC1 backward (8192 tokens, 1024 -> 4096), fp16 in, fp32 accumulate:
     dA = dC W^T and dW = A^T dC, 4*M*N*K flops."""
@@ -380,6 +397,7 @@ def component_ops(torch, L, only):
                 ("bn_relu_bwd_nhwc", lambda: _op_bn(torch, L, g)),
                 ("adamw_step", lambda: _op_adam(torch, L, g)),
                 ("unscale_check", lambda: _op_unscale(torch, L, g)),
+                ("unscale_norm", lambda: _op_unscale_norm(torch, L, g)),
                 ("gemm_fc1_bwd", lambda: _op_gemm(torch, L, g)),
                 ("cross_entropy_fwd_bwd", lambda: _op_ce(torch, L, g)),
                 ("embedding_bwd", lambda: _op_embedding(torch, L, g)),

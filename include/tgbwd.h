@@ -204,6 +204,18 @@ int tg_adam_step_lowp(int ntensors, float* const* params, const float* const* gr
                       double beta1, double beta2, double eps, double weight_decay,
                       double bias_correction1, double bias_correction2, int lowp_dtype,
                       void* const* lowp, void* stream);
+/* tg_adam_step / tg_adam_step_lowp (lowp NULL: no copies) reading each gradient as
+ * (g * grad_mul1) * grad_mul2 in fp32: the values an in-place unscale by grad_mul1
+ * (GradScaler.unscale_, _nn.py:1795-1833) followed by an in-place clip scaling by
+ * grad_mul2 (clip_grad_norm_, _nn.py:1620-1624) would leave, so the gradients can stay
+ * loss-scaled in memory until the optimizer reads them.  No reference counterpart of its
+ * own; the update is tg_adam_step's. */
+int tg_adam_step_scaled(int ntensors, float* const* params, const float* const* grads,
+                        float* const* exp_avg, float* const* exp_avg_sq,
+                        float* const* max_exp_avg_sq, const int64_t* numel, double lr,
+                        double beta1, double beta2, double eps, double weight_decay,
+                        double bias_correction1, double bias_correction2, float grad_mul1,
+                        float grad_mul2, int lowp_dtype, void* const* lowp, void* stream);
 /* GradScaler.unscale_ (_nn.py:1795-1833): g *= mul (if write); flags[i] (device,
  * cleared first) |= 1 if tensor i had a non-finite value, |= 2 if the scaled
  * tensor has one. */
@@ -221,6 +233,16 @@ size_t tg_grad_norm_workspace(int ntensors, const int64_t* numel);
 int tg_grad_norm(int ntensors, int dtype, void* const* grads, const int64_t* numel, int norm_kind,
                  float p, double* out, int* flags, void* workspace, size_t workspace_bytes,
                  void* stream);
+/* GradScaler.unscale_ (_nn.py:1795-1833) and clip_grad_norm_'s L2 reduction
+ * (_nn.py:1588-1612) in one read-only pass: flags[i] as tg_unscale_check's, and out[0]
+ * (device double) = the sum of squares the gradients would have after
+ * tg_unscale_check(mul, write = 1) and tg_zero_flagged, bit for bit (tg_grad_norm's
+ * chunks and order; a flagged tensor counts zero).  fp32, fp16 and bf16 gradients.
+ * Workspace: tg_unscale_norm_workspace(ntensors, numel) bytes. */
+size_t tg_unscale_norm_workspace(int ntensors, const int64_t* numel);
+int tg_unscale_norm(int ntensors, int dtype, void* const* grads, const int64_t* numel,
+                    float mul, int* flags, double* out, void* workspace,
+                    size_t workspace_bytes, void* stream);
 /* xp.where(isfinite(g), g, 0) per tensor (_nn.py:1596). */
 int tg_zero_nonfinite(int ntensors, int dtype, void* const* grads, const int64_t* numel,
                       void* stream);

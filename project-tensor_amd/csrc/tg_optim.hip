@@ -122,8 +122,10 @@ __device__ __forceinline__ bool al16(const void* p) {
 // The divisions by the bias corrections are multiplications by their reciprocals
 // (formed in double on the host) and the last one a reciprocal of the denominator:
 // each differs from the division by at most one rounding.
+// gm1, gm2: the gradient is read as (g * gm1) * gm2, two fp32 roundings, the values
+// that scaling the gradient in place by gm1 and then by gm2 would leave (1, 1: g).
 struct AdamConsts {
-  float lr, b1, omb1, b2, omb2, eps, lrwd, ibc1, ibc2;
+  float lr, b1, omb1, b2, omb2, eps, lrwd, ibc1, ibc2, gm1, gm2;
   int decay;
 };
 
@@ -167,7 +169,7 @@ __device__ __forceinline__ void adam_chunk(float* __restrict__ p, const float* _
   for (int i = 0; i < E; ++i) {
     float pp = P[i];
     if (K.decay) pp -= K.lrwd * pp;
-    const float gg = G[i];
+    const float gg = (G[i] * K.gm1) * K.gm2;
     const float mm = K.b1 * Mv[i] + K.omb1 * gg;
     const float vv = K.b2 * Vv[i] + K.omb2 * (gg * gg);
     const float mh = mm * K.ibc1;
@@ -292,15 +294,75 @@ __global__ __launch_bounds__(kBlock) void k_norm_partial(MtArgs A, float p, doub
   }
 }
 
+// GradScaler.unscale_ followed by the squared gradient norm, read-only: flags as
+// k_scale_check's (bit 0: g non-finite, bit 1: g*mul rounded through T non-finite)
+// and the per-block partial sum of (g*mul)^2 over finite entries, with k_norm_partial's
+// chunking and order (the value it would give after the in-place unscale); tidx[b]
+// is the caller's index of block b's tensor, for the masked final reduction.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_unscale_norm_partial(MtArgs A, float mul,
+                                                                 double* part, int* tidx,
+                                                                 int64_t part_base, int* flags) {
+  const int t = find_tensor(A, blockIdx.x);
+  const int64_t n = A.n[t];
+  const int64_t start = (blockIdx.x - A.first_block[t]) * kChunk;
+  const int64_t end = start + kChunk < n ? start + kChunk : n;
+  const T* g = (const T*)A.a[t];
+  float x[kEPT];
+  if (start + kChunk <= n && al16(g)) load_chunk<T, true, kEPT, true>(g, start, end, x);
+  else load_chunk<T, false>(g, start, end, x);  // out-of-range entries read as 0
+  double acc = 0.0;
+  int f = 0;
+  using M = ChunkMap<T>;
+#pragma unroll
+  for (int i = 0; i < kEPT; ++i) {
+    if (M::at(start, i / M::PER) + i % M::PER >= end) continue;  // padding of a tail chunk
+    if (!isfinite(x[i])) f |= 1;
+    const float y = tg_to_float(tg_from_float<T>(x[i] * mul));
+    if (!isfinite(y)) {
+      f |= 2;
+      continue;
+    }
+    const float ay = fabsf(y);
+    acc += (double)ay * (double)ay;
+  }
+  __shared__ double red[4];
+  acc = tg_wave_sum_d(acc);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) f |= __shfl_xor(f, off, 64);
+  if ((threadIdx.x & 63) == 0) {
+    red[threadIdx.x >> 6] = acc;
+    if (f) atomicOr(flags + A.fidx[t], f);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    part[part_base + blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
+    tidx[part_base + blockIdx.x] = A.fidx[t];
+  }
+}
+
 // Deterministic single-block reduction of the partials: 1024 threads, each with
 // kNF independent accumulators over a fixed stride (kNF loads in flight instead of
 // one dependent chain), then a fixed-order tree.
 constexpr int kNormFinal = 1024;
 constexpr int kNF = 8;
+// With tidx (k_unscale_norm_partial): a partial whose tensor is flagged counts as 0,
+// the value it has once unscale_ has zeroed that tensor.  The flags of up to kFlagLds
+// tensors are staged in LDS first, so the mask is not a second dependent global load.
+constexpr int kFlagLds = 8192;
 template <int KIND>
 __global__ __launch_bounds__(kNormFinal) void k_norm_final(const double* part, int64_t n,
-                                                           double* out) {
+                                                           double* out,
+                                                           const int* tidx = nullptr,
+                                                           const int* flags = nullptr,
+                                                           int ntensors = 0) {
   auto comb = [](double a, double b) { return KIND == 1 ? fmax(a, b) : a + b; };
+  __shared__ int fl[kFlagLds];
+  const bool lds = tidx && ntensors <= kFlagLds;
+  if (lds) {
+    for (int i = threadIdx.x; i < ntensors; i += kNormFinal) fl[i] = flags[i];
+    __syncthreads();
+  }
   double acc[kNF];
 #pragma unroll
   for (int u = 0; u < kNF; ++u) acc[u] = 0.0;
@@ -308,7 +370,10 @@ __global__ __launch_bounds__(kNormFinal) void k_norm_final(const double* part, i
 #pragma unroll
     for (int u = 0; u < kNF; ++u) {
       const int64_t i = i0 + (int64_t)u * kNormFinal;
-      if (i < n) acc[u] = comb(acc[u], part[i]);
+      if (i < n) {
+        const bool masked = tidx && (lds ? fl[tidx[i]] : flags[tidx[i]]);
+        acc[u] = comb(acc[u], masked ? 0.0 : part[i]);
+      }
     }
   }
 #pragma unroll
@@ -442,7 +507,8 @@ int adam_step_impl(const char* who, int ntensors, float* const* params,
                    const float* const* grads, float* const* exp_avg, float* const* exp_avg_sq,
                    float* const* max_exp_avg_sq, const int64_t* numel, double lr, double beta1,
                    double beta2, double eps, double weight_decay, double bias_correction1,
-                   double bias_correction2, int lowp_dtype, void* const* lowp, void* stream) {
+                   double bias_correction2, float gm1, float gm2, int lowp_dtype,
+                   void* const* lowp, void* stream) {
   TG_REQUIRE(ntensors >= 0, "%s: negative tensor count", who);
   if (ntensors == 0) return TG_OK;
   TG_REQUIRE(params && grads && exp_avg && exp_avg_sq && numel, "%s: null list", who);
@@ -473,6 +539,8 @@ int adam_step_impl(const char* who, int ntensors, float* const* params,
   K.decay = weight_decay != 0.0;
   K.ibc1 = (float)(1.0 / bias_correction1);
   K.ibc2 = (float)(1.0 / bias_correction2);
+  K.gm1 = gm1;
+  K.gm2 = gm2;
   return for_each_launch(
       ntensors, (void* const*)params, (void* const*)grads, (void* const*)exp_avg,
       (void* const*)exp_avg_sq, (void* const*)max_exp_avg_sq, lowp, numel,
@@ -498,7 +566,7 @@ TG_EXPORT int tg_adam_step(int ntensors, float* const* params, const float* cons
                            double bias_correction1, double bias_correction2, void* stream) {
   return adam_step_impl("tg_adam_step", ntensors, params, grads, exp_avg, exp_avg_sq,
                         max_exp_avg_sq, numel, lr, beta1, beta2, eps, weight_decay,
-                        bias_correction1, bias_correction2, 0, nullptr, stream);
+                        bias_correction1, bias_correction2, 1.f, 1.f, 0, nullptr, stream);
 }
 
 // tg_adam_step that also writes each updated parameter, rounded to `lowp_dtype`
@@ -513,7 +581,23 @@ TG_EXPORT int tg_adam_step_lowp(int ntensors, float* const* params, const float*
   TG_REQUIRE(lowp, "tg_adam_step_lowp: null copy list");
   return adam_step_impl("tg_adam_step_lowp", ntensors, params, grads, exp_avg, exp_avg_sq,
                         max_exp_avg_sq, numel, lr, beta1, beta2, eps, weight_decay,
-                        bias_correction1, bias_correction2, lowp_dtype, lowp, stream);
+                        bias_correction1, bias_correction2, 1.f, 1.f, lowp_dtype, lowp, stream);
+}
+
+// tg_adam_step(_lowp) reading each gradient as (g * grad_mul1) * grad_mul2: the gradients
+// still hold the loss-scaled values, and the unscale factor and the clip factor are
+// applied here, in the order and with the roundings of two in-place scalings.
+TG_EXPORT int tg_adam_step_scaled(int ntensors, float* const* params, const float* const* grads,
+                                  float* const* exp_avg, float* const* exp_avg_sq,
+                                  float* const* max_exp_avg_sq, const int64_t* numel,
+                                  double lr, double beta1, double beta2, double eps,
+                                  double weight_decay, double bias_correction1,
+                                  double bias_correction2, float grad_mul1, float grad_mul2,
+                                  int lowp_dtype, void* const* lowp, void* stream) {
+  return adam_step_impl("tg_adam_step_scaled", ntensors, params, grads, exp_avg, exp_avg_sq,
+                        max_exp_avg_sq, numel, lr, beta1, beta2, eps, weight_decay,
+                        bias_correction1, bias_correction2, grad_mul1, grad_mul2, lowp_dtype,
+                        lowp, stream);
 }
 
 // Multiply every gradient by `mul` (when write != 0) and report non-finite values:
@@ -591,6 +675,53 @@ TG_EXPORT int tg_grad_norm(int ntensors, int dtype, void* const* grads, const in
   else
     k_norm_final<0><<<1, kNormFinal, 0, s>>>(part, nb_total, out);
   return tg_check_launch("tg_grad_norm final");
+}
+
+TG_EXPORT size_t tg_unscale_norm_workspace(int ntensors, const int64_t* numel) {
+  if (ntensors <= 0 || !numel) return 2 * sizeof(double);
+  const int64_t b = total_blocks(ntensors, numel);
+  return (size_t)(b > 0 ? b : 1) * (sizeof(double) + sizeof(int)) + sizeof(double);
+}
+
+// Read-only form of GradScaler.unscale_ plus clip_grad_norm_'s reduction: flags[i]
+// (cleared here) as tg_unscale_check's, and out[0] = the squared L2 norm the gradients
+// would have after tg_unscale_check(mul, write) and tg_zero_flagged, bit for bit (the
+// same chunks and order as tg_grad_norm, flagged tensors counting zero).  fp32, fp16,
+// bf16.
+TG_EXPORT int tg_unscale_norm(int ntensors, int dtype, void* const* grads, const int64_t* numel,
+                              float mul, int* flags, double* out, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  TG_REQUIRE(ntensors >= 0, "tg_unscale_norm: negative tensor count");
+  TG_REQUIRE(out && flags, "tg_unscale_norm: null output");
+  TG_REQUIRE(dtype == TG_F32 || dtype == TG_F16 || dtype == TG_BF16,
+             "tg_unscale_norm: unsupported dtype %d", dtype);
+  TG_REQUIRE(ntensors == 0 || (grads && numel), "tg_unscale_norm: null argument");
+  hipStream_t s = tg_stream(stream);
+  const int64_t nb_total = ntensors > 0 ? total_blocks(ntensors, numel) : 0;
+  const size_t need = tg_unscale_norm_workspace(ntensors, numel);
+  if (!workspace || workspace_bytes < need) {
+    tg_set_error("tg_unscale_norm: workspace of %zu bytes needed", need);
+    return TG_ERR_WORKSPACE;
+  }
+  double* part = (double*)workspace;
+  int* tidx = (int*)(part + (nb_total > 0 ? nb_total : 1));
+  if (ntensors > 0) k_zero_ints<<<1, kBlock, 0, s>>>(flags, ntensors);
+  int64_t part_base = 0;
+  int st = TG_OK;
+  if (ntensors > 0)
+    st = for_each_launch(ntensors, grads, nullptr, nullptr, nullptr, nullptr, nullptr, numel,
+                         [&](const MtArgs& A, int64_t nb) {
+#define L(T) k_unscale_norm_partial<T><<<(unsigned)nb, kBlock, 0, s>>>(A, mul, part, tidx, part_base, flags)
+                           if (dtype == TG_F32) L(float);
+                           else if (dtype == TG_F16) L(tg_half);
+                           else L(tg_bf16);
+#undef L
+                           part_base += nb;
+                           return tg_check_launch("tg_unscale_norm");
+                         });
+  if (st) return st;
+  k_norm_final<0><<<1, kNormFinal, 0, s>>>(part, nb_total, out, tidx, flags, ntensors);
+  return tg_check_launch("tg_unscale_norm final");
 }
 
 // Zero every gradient i whose device flag flags[i] is non-zero (as set by

@@ -39,6 +39,39 @@ _WG_STATE = [0, 0]   # [backward nesting depth, bytes of operands the queue keep
 _WG_MAX_BYTES = 4 << 30  # flush early once the queue keeps this much alive
 
 
+# ------------------------------------------------------- pending gradient scalings
+# GradScaler.unscale_ and clip_grad_norm_ may leave their factor pending on a parameter's
+# gradient instead of rewriting it: _GSCALE[id(t)] = (t, (f1, f2, ...)) means the
+# gradient is its buffer scaled in place by f1, then by f2, ... (one fp32 rounding each).
+# The optimizer applies the factors as it reads the buffers; any other access to the
+# gradient applies them first (_settle), so every value read is the rewritten one.
+_GSCALE = {}
+
+
+def _grad_scale_pending(t, factor):
+    """Record one more pending in-place scaling of t's gradient buffer by factor."""
+    e = _GSCALE.get(id(t))
+    _GSCALE[id(t)] = (t, (e[1] if e is not None else ()) + (float(factor),))
+
+
+def _grad_factors(t):
+    """Pending scaling factors of t's gradient (empty tuple: none)."""
+    e = _GSCALE.get(id(t))
+    return e[1] if e is not None else ()
+
+
+def _settle(t, drop=False):
+    """Before an access to t's gradient: run the queued weight-gradient products if
+    one writes it, then apply its pending scalings (drop: discard them, the buffer is
+    being replaced or cleared)."""
+    if _WG_TARGETS and id(t) in _WG_TARGETS:
+        _wgrad_flush()
+    e = _GSCALE.pop(id(t), None)
+    if e is not None and not drop and t._g is not None:
+        for f in e[1]:
+            L.scale_([t._g], f)
+
+
 def _wgrad_defer(A2, G2, w, wbuf, wacc, b=None, bbuf=None, bacc=False):
     _WG_QUEUE.append((A2, G2, wbuf, wacc, bbuf, bacc))
     _WG_TARGETS[id(w)] = w
@@ -195,8 +228,8 @@ class Tensor:
 
     @property
     def grad(self):
-        if _WG_TARGETS and id(self) in _WG_TARGETS:
-            _wgrad_flush()
+        if _WG_TARGETS or _GSCALE:
+            _settle(self)
         if self._gz:
             self._g = self._new_buf(0)
             self._gz = False
@@ -206,8 +239,8 @@ class Tensor:
 
     @grad.setter
     def grad(self, value):
-        if _WG_TARGETS and id(self) in _WG_TARGETS:
-            _wgrad_flush()
+        if _WG_TARGETS or _GSCALE:
+            _settle(self, drop=True)
         self._gz = False
         self._gsh = False
         if value is None:
@@ -229,8 +262,8 @@ class Tensor:
     def _grad_out(self):
         """Gradient flowing into this node's closure (zeros if nothing arrived).
         Read-only: it may be shared with other nodes."""
-        if _WG_TARGETS and id(self) in _WG_TARGETS:
-            _wgrad_flush()
+        if _WG_TARGETS or _GSCALE:
+            _settle(self)
         if self._gz:
             return self._new_buf(0)
         return self._g
@@ -238,8 +271,8 @@ class Tensor:
     def _privatize(self):
         """Give this node its own contiguous copy of a gradient buffer it shares (or
         holds with strides)."""
-        if _WG_TARGETS and id(self) in _WG_TARGETS:
-            _wgrad_flush()
+        if _WG_TARGETS or _GSCALE:
+            _settle(self)
         buf = self._new_buf()
         _copy_into(buf, self._g)
         self._g = buf
@@ -247,8 +280,8 @@ class Tensor:
 
     def _grad_target(self):
         """(buffer, accumulate) for a kernel that adds this tensor's gradient."""
-        if _WG_TARGETS and id(self) in _WG_TARGETS:
-            _wgrad_flush()
+        if _WG_TARGETS or _GSCALE:
+            _settle(self)
         if self._gz:
             self._g = self._new_buf()
             self._gz = False
@@ -262,8 +295,8 @@ class Tensor:
         source None means no prior gradient (overwrite).  A gradient shared with
         another node is not copied first: the kernel reads it as the source and writes
         this tensor's own new buffer; otherwise source is the buffer itself."""
-        if _WG_TARGETS and id(self) in _WG_TARGETS:
-            _wgrad_flush()
+        if _WG_TARGETS or _GSCALE:
+            _settle(self)
         if (not self._gz and self._gsh and self._g.is_contiguous()
                 and self._g.dtype == self.data.dtype and self._g.shape == self.data.shape):
             src = self._g
@@ -280,8 +313,8 @@ class Tensor:
         both nodes are marked shared, so the first in-place write to either one
         copies (out of place for an accumulation, which moves no more bytes than the
         in-place one would)."""
-        if _WG_TARGETS and id(self) in _WG_TARGETS:
-            _wgrad_flush()
+        if _WG_TARGETS or _GSCALE:
+            _settle(self)
         if not self._gz or g.dtype != self.data.dtype or not (g.is_contiguous() or _dense(g)):
             self._accumulate(g)
             return
@@ -307,8 +340,8 @@ class Tensor:
 
     def _accumulate(self, g, owned=False):
         """self.grad += g (g: torch tensor broadcast-compatible in shape, any float dtype)."""
-        if _WG_TARGETS and id(self) in _WG_TARGETS:
-            _wgrad_flush()
+        if _WG_TARGETS or _GSCALE:
+            _settle(self)
         if not self._has_grad():
             return
         if g.shape != self.data.shape:
@@ -404,8 +437,8 @@ class Tensor:
                       dtype=np.float32)
 
     def zero_grad(self):
-        if _WG_TARGETS and id(self) in _WG_TARGETS:
-            _wgrad_flush()
+        if _WG_TARGETS or _GSCALE:
+            _settle(self, drop=True)
         if self._has_grad():
             self._g = None
             self._gz = True

@@ -74,7 +74,11 @@ SIGNATURES = {
                                 _f64, _f64, _f64, _vp]),
     "tg_adam_step_lowp": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _f64, _f64, _f64, _f64,
                                  _f64, _f64, _f64, _i32, _vp, _vp]),
+    "tg_adam_step_scaled": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _f64, _f64, _f64, _f64,
+                                   _f64, _f64, _f64, _f32, _f32, _i32, _vp, _vp]),
     "tg_unscale_check": (_i32, [_i32, _i32, _vp, _vp, _f32, _i32, _vp, _vp]),
+    "tg_unscale_norm_workspace": (_sz, [_i32, _vp]),
+    "tg_unscale_norm": (_i32, [_i32, _i32, _vp, _vp, _f32, _vp, _vp, _vp, _sz, _vp]),
     "tg_grad_norm_workspace": (_sz, [_i32, _vp]),
     "tg_grad_norm": (_i32, [_i32, _i32, _vp, _vp, _i32, _f32, _vp, _vp, _vp, _sz, _vp]),
     "tg_zero_nonfinite": (_i32, [_i32, _i32, _vp, _vp, _vp]),
@@ -628,9 +632,11 @@ def adam_step(params, grads, exp_avg, exp_avg_sq, max_exp_avg_sq, lr, beta1, bet
 
 def adam_prepare(params, grads, exp_avg, exp_avg_sq, max_exp_avg_sq, lowp=None):
     """The checks and pointer arrays of adam_step for these buffers, done now; returns
-    launch(lr, beta1, beta2, eps, weight_decay, bias_correction1, bias_correction2),
-    which only enqueues the kernel.  An optimizer prepares while the device is still
-    busy and launches after the last host read-back of the step."""
+    launch(lr, beta1, beta2, eps, weight_decay, bias_correction1, bias_correction2,
+    gmul=(1.0, 1.0)), which only enqueues the kernel.  An optimizer prepares while the
+    device is still busy and launches after the last host read-back of the step.  gmul
+    (fp32 params): the gradients are read as (g * gmul[0]) * gmul[1] (scalings still
+    pending on them)."""
     n = len(params)
     if n == 0:
         return lambda *a: None
@@ -671,12 +677,21 @@ def adam_prepare(params, grads, exp_avg, exp_avg_sq, max_exp_avg_sq, lowp=None):
         keep = keep + (list(lowp),)
     else:
         fn, extra, name = lib.tg_adam_step, (), "tg_adam_step"
+    scaled_extra = extra if extra else (0, None)
 
-    def launch(lr, beta1, beta2, eps, weight_decay, bias_correction1, bias_correction2):
+    def launch(lr, beta1, beta2, eps, weight_decay, bias_correction1, bias_correction2,
+               gmul=(1.0, 1.0)):
         ensure_device(dev)
-        _check(name, fn(n, arrs[0], garr, arrs[1], arrs[2], arrs[3], numel_arr, float(lr),
-                        float(beta1), float(beta2), float(eps), float(weight_decay),
-                        float(bias_correction1), float(bias_correction2), *extra,
+        hyper = (float(lr), float(beta1), float(beta2), float(eps), float(weight_decay),
+                 float(bias_correction1), float(bias_correction2))
+        if tuple(gmul) != (1.0, 1.0):
+            if pdt != torch.float32:
+                raise TypeError("adam_step: gradient multipliers are for fp32 params")
+            _check("tg_adam_step_scaled", lib.tg_adam_step_scaled(
+                n, arrs[0], garr, arrs[1], arrs[2], arrs[3], numel_arr, *hyper,
+                float(gmul[0]), float(gmul[1]), *scaled_extra, stream_handle()))
+            return keep
+        _check(name, fn(n, arrs[0], garr, arrs[1], arrs[2], arrs[3], numel_arr, *hyper, *extra,
                         stream_handle()))
         return keep
     return launch
@@ -783,6 +798,67 @@ def unscale_deferred(grads, mul):
                 out[i] = h[o + j]
             o += len(idx)
         return out
+    return resolve
+
+
+def unscale_norm_deferred(grads, mul):
+    """unscale_deferred without writing the scaled values: the gradients keep their
+    contents (the caller applies `mul` later), every tensor that holds or would hold a
+    non-finite value is zeroed on the device, and the squared L2 norm the unscaled,
+    zeroed gradients would have is formed in the same pass (bit for bit the value
+    grad_norm(kind 0) would return after unscale_deferred).  fp32/fp16/bf16 only.
+    Returns resolve() -> (flags, sum of squares), which waits for one asynchronous
+    device-to-host copy."""
+    n = len(grads)
+    if n == 0:
+        return lambda: ([], 0.0)
+    for t in grads:
+        _dev(t, "grad")
+        if t.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+            raise TypeError(f"unscale_norm_deferred: unsupported dtype {t.dtype}")
+    dev = grads[0].device
+    ensure_device(dev.index)
+    lib = load()
+    groups = list(_group_by_dtype(grads).items())
+    ng = len(groups)
+    # per call: the flags and group sums (fresh, a later call must not overwrite them
+    # while they are being copied out)
+    buf = torch.empty(8 * ng + 4 * n, dtype=torch.uint8, device=dev)
+    vals = buf[: 8 * ng].view(torch.float64)
+    fls = buf[8 * ng:].view(torch.int32)
+    off = 0
+    for gi, (dt, idx) in enumerate(groups):
+        sub = [grads[i] for i in idx]
+        gp, ne = _ptr_array(sub), _numel_array(sub)
+        fl = fls[off: off + len(sub)]
+        off += len(sub)
+        nb = lib.tg_unscale_norm_workspace(len(sub), ne)
+        ws = _scratch(("unscalenorm", gi), nb, dev)
+        _check("tg_unscale_norm", lib.tg_unscale_norm(
+            len(sub), dtype_code(sub[0]), gp, ne, float(mul), ptr(fl), ptr(vals[gi:gi + 1]),
+            ptr(ws), ws.numel(), stream_handle()))
+        _check("tg_zero_flagged", lib.tg_zero_flagged(
+            len(sub), dtype_code(sub[0]), gp, ne, ptr(fl), stream_handle()))
+    host = torch.empty(buf.numel(), dtype=torch.uint8, pin_memory=True)
+    host.copy_(buf, non_blocking=True)
+    keep = [buf]
+    ev = torch.cuda.Event()
+    ev.record()
+
+    def resolve():
+        ev.synchronize()
+        del keep[:]
+        hv = host[: 8 * ng].view(torch.float64).tolist()
+        hf = host[8 * ng:].view(torch.int32).tolist()
+        out = [0] * n
+        total = 0.0
+        o = 0
+        for gi, (dt, idx) in enumerate(groups):
+            total += float(hv[gi])
+            for j, i in enumerate(idx):
+                out[i] = hf[o + j]
+            o += len(idx)
+        return out, total
     return resolve
 
 

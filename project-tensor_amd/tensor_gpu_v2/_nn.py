@@ -13,7 +13,7 @@ import torch
 
 from . import _config as cfg
 from . import _lib as L
-from . import _lowp
+from . import _core, _lowp
 from ._core import Tensor, _as, _linear
 
 
@@ -655,7 +655,12 @@ class Adam:
             if dt not in (torch.float32, torch.float64) or not p.data.is_contiguous():
                 raise TypeError("Adam: parameters must be contiguous float32 or float64 "
                                 "device tensors")
-            g = p.grad
+            # a gradient with scalings pending is read as it is stored (the launch
+            # applies them), unless it needs converting
+            if _core._grad_factors(p) and p._g.dtype == dt:
+                g = p._g
+            else:
+                g = p.grad
             gbufs.append(p._g)
             if g.dtype != dt:
                 g = _as(g, dt)
@@ -668,8 +673,8 @@ class Adam:
             if self.amsgrad:
                 vms.append(self.v_max[i])
         launchers = [
-            L.adam_prepare(ps, gs, ms, vs, vms if self.amsgrad else None,
-                           lowp=_lowp.refresh_targets(ps) if dt == torch.float32 else None)
+            (dt, L.adam_prepare(ps, gs, ms, vs, vms if self.amsgrad else None,
+                                lowp=_lowp.refresh_targets(ps) if dt == torch.float32 else None))
             for dt, (ps, gs, ms, vs, vms) in groups.items()]
         return (None if copied else gbufs), _lowp._GEN[0], launchers
 
@@ -693,8 +698,22 @@ class Adam:
                 plan = None
         if plan is None:
             plan = self._plan()
-        for launch in plan[2]:
-            launch(lr, self.beta1, self.beta2, self.eps, wd, bc1, bc2)
+        # Scalings pending on the gradients (unscale, clip) go into the launch when every
+        # fp32 gradient carries the same one or two; otherwise they are applied first.
+        live = [p for p in self.params if p._has_grad()]
+        fac = {_core._grad_factors(p) for p in live if p.data.dtype == torch.float32}
+        gmul = (1.0, 1.0)
+        if len(fac) == 1 and 0 < len(next(iter(fac))) <= 2:
+            f = next(iter(fac))
+            gmul = (f[0], f[1] if len(f) > 1 else 1.0)
+        else:
+            fac = set()
+        for p in live:
+            if _core._grad_factors(p) and not (fac and p.data.dtype == torch.float32):
+                _core._settle(p)  # in place: the planned pointers stay valid
+        for dt, launch in plan[2]:
+            launch(lr, self.beta1, self.beta2, self.eps, wd, bc1, bc2,
+                   gmul=gmul if dt == torch.float32 else (1.0, 1.0))
 
     def step(self, clip_grad_norm=None):
         if clip_grad_norm is not None:
@@ -742,13 +761,52 @@ class AdamW(Adam):
 
 
 # ============================================================================ clipping
+class _UnscaledNorm:
+    """The squared L2 norm GradScaler.unscale_ formed for `params` while leaving the
+    unscale pending; good for clip_grad_norm_ as long as every one of those gradients
+    still holds the same buffer with only that scaling pending (any other access
+    applies the scaling and ends the match)."""
+
+    def __init__(self, params, inv, resolve):
+        self.params = list(params)
+        self.bufs = [p._g for p in params]
+        self.factors = (float(inv),)
+        self.resolve = resolve
+
+    def matches(self, params):
+        if len(params) != len(self.params):
+            return False
+        for p, q, b in zip(params, self.params, self.bufs):
+            if p is not q or p._g is not b or _core._grad_factors(p) != self.factors:
+                return False
+        return True
+
+
+_NORM_CACHE = [None]
+
+
 def clip_grad_norm_(parameters, max_norm, norm_type=2.0, error_if_nonfinite=False):
     """Global-norm clip (_nn.py:1563-1626): non-finite entries are zeroed (warning)
     or raise; the norm is one multi-tensor reduction; grads are rescaled by
-    max_norm/(norm+1e-6) when that is < 1.  Returns the pre-clip norm."""
+    max_norm/(norm+1e-6) when that is < 1.  Returns the pre-clip norm.  Right after
+    GradScaler.unscale_ over the same parameters, the norm that unscale_ formed is used
+    and the rescale is left pending on the gradients like the unscale (the optimizer
+    applies both as it reads them)."""
     params = [p for p in parameters if p._has_grad()]
     if not params:
         return 0.0
+    cache, _NORM_CACHE[0] = _NORM_CACHE[0], None
+    if norm_type == 2.0 and cache is not None and cache.matches(params):
+        # flagged gradients were zeroed by unscale_: nothing non-finite is left
+        value = cache.resolve()[1]
+        total = value ** (1.0 / 2.0)
+        if total == 0.0:
+            return 0.0
+        coef = max_norm / (total + 1e-6)
+        if coef < 1.0:
+            for p in params:
+                _core._grad_scale_pending(p, coef)
+        return total
     grads = [p.grad for p in params]
     if norm_type == float("inf"):
         kind, pw = 1, 1.0
@@ -837,7 +895,21 @@ class GradScaler:
         self._found_inf = False
         params = [p for p in optimizer.params if p._has_grad()]
         grads = [p.grad for p in params]
-        if grads and zero_nan_grads:
+        if grads and zero_nan_grads and all(
+                g.dtype in (torch.float32, torch.float16, torch.bfloat16) for g in grads):
+            # One read-only pass: flags, the zeroing of flagged gradients, and the norm
+            # clip_grad_norm_ would compute next.  The unscale itself stays pending on
+            # the gradients (applied by the optimizer as it reads them, or by any other
+            # access first); found_inf is read lazily.
+            resolve = L.unscale_norm_deferred(grads, inv)
+            for p in params:
+                _core._grad_scale_pending(p, inv)
+            _NORM_CACHE[0] = _UnscaledNorm(params, inv, resolve)
+            self._pending = lambda: resolve()[0]
+            prep = getattr(optimizer, "_prepare", None)
+            if prep is not None:
+                prep()
+        elif grads and zero_nan_grads:
             # flagged gradients are zeroed on the device; found_inf is read lazily
             self._pending = L.unscale_deferred(grads, inv)
             prep = getattr(optimizer, "_prepare", None)
