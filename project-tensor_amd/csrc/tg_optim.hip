@@ -18,6 +18,10 @@ constexpr int kBlock = 256;
 constexpr int kMaxT = 56;  // tensors per launch: 68 B each in the kernel argument block (< 4 KiB)
 constexpr int kEPT = 16;                     // elements per thread (grad kernels)
 constexpr int64_t kChunk = kBlock * kEPT;    // elements per workgroup
+// Norm reductions: each workgroup covers kNormSub consecutive chunks (all loads issued
+// first), so the single-block final reduction has half the partials.
+constexpr int kNormSub = 2;
+constexpr int64_t kNormChunk = kNormSub * kChunk;
 // Adam streams four inputs and three outputs: two 16-byte vectors per operand and
 // thread in 64-thread workgroups, with non-temporal loads and stores (measured 0.73 of
 // peak; one vector per thread 0.69, four 0.67, 256-thread workgroups 0.66).
@@ -246,33 +250,56 @@ __global__ __launch_bounds__(kBlock) void k_scale_check(MtArgs A, float mul, int
   if ((threadIdx.x & 63) == 0 && f) atomicOr(flags + A.fidx[t], f);
 }
 
-// Per-block partial of the gradient norm over finite entries.
+// The kNormSub chunks of a norm workgroup from element `base` of a tensor of n
+// elements, every load issued before any is used (entries past n read as 0).
+template <typename T>
+__device__ __forceinline__ void load_norm_chunks(const T* __restrict__ g, int64_t base,
+                                                 int64_t n, float (&x)[kNormSub][kEPT]) {
+#pragma unroll
+  for (int c = 0; c < kNormSub; ++c) {
+    const int64_t start = base + c * kChunk;
+    const int64_t end = start + kChunk < n ? start + kChunk : n;
+    if (start + kChunk <= n && al16(g)) {
+      load_chunk<T, true, kEPT, true>(g, start, end, x[c]);
+    } else if (start < n) {
+      load_chunk<T, false>(g, start, end, x[c]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kEPT; ++i) x[c][i] = 0.f;
+    }
+  }
+}
+
+// Per-block partial of the gradient norm over finite entries (kNormChunk elements).
 // KIND 0: sum g^2, 1: max |g|, 2: sum |g|^p.  Non-finite entries set flags bit 1.
 template <typename T, int KIND>
 __global__ __launch_bounds__(kBlock) void k_norm_partial(MtArgs A, float p, double* part,
                                                          int64_t part_base, int* flags) {
   const int t = find_tensor(A, blockIdx.x);
   const int64_t n = A.n[t];
-  const int64_t start = (blockIdx.x - A.first_block[t]) * kChunk;
-  const int64_t end = start + kChunk < n ? start + kChunk : n;
+  const int64_t base = (blockIdx.x - A.first_block[t]) * kNormChunk;
   const T* g = (const T*)A.a[t];
-  float x[kEPT];
-  if (start + kChunk <= n && al16(g)) load_chunk<T, true, kEPT, true>(g, start, end, x);
-  else load_chunk<T, false>(g, start, end, x);  // out-of-range entries read as 0
+  float x[kNormSub][kEPT];
+  load_norm_chunks<T>(g, base, n, x);
   double acc = 0.0;
   int f = 0;
   using M = ChunkMap<T>;
 #pragma unroll
-  for (int i = 0; i < kEPT; ++i) {
-    if (M::at(start, i / M::PER) + i % M::PER >= end) continue;  // padding of a tail chunk
-    if (!isfinite(x[i])) {
-      f = 1;
-      continue;
+  for (int c = 0; c < kNormSub; ++c) {
+    const int64_t start = base + c * kChunk;
+    const int64_t end = start + kChunk < n ? start + kChunk : n;
+#pragma unroll
+    for (int i = 0; i < kEPT; ++i) {
+      if (M::at(start, i / M::PER) + i % M::PER >= end) continue;  // past the tensor's end
+      if (!isfinite(x[c][i])) {
+        f = 1;
+        continue;
+      }
+      const float ax = fabsf(x[c][i]);
+      if (KIND == 0) acc += (double)ax * (double)ax;
+      else if (KIND == 1) acc = fmax(acc, (double)ax);
+      else acc += pow((double)ax, (double)p);
     }
-    const float ax = fabsf(x[i]);
-    if (KIND == 0) acc += (double)ax * (double)ax;
-    else if (KIND == 1) acc = fmax(acc, (double)ax);
-    else acc += pow((double)ax, (double)p);
   }
   __shared__ double red[4];
   if (KIND == 1) {
@@ -299,45 +326,52 @@ __global__ __launch_bounds__(kBlock) void k_norm_partial(MtArgs A, float p, doub
 // and the per-block partial sum of (g*mul)^2 over finite entries, with k_norm_partial's
 // chunking and order (the value it would give after the in-place unscale); tidx[b]
 // is the caller's index of block b's tensor, for the masked final reduction.
-template <typename T>
+template <typename T, bool BFLAG>
 __global__ __launch_bounds__(kBlock) void k_unscale_norm_partial(MtArgs A, float mul,
                                                                  double* part, int* tidx,
-                                                                 int64_t part_base, int* flags) {
+                                                                 int64_t part_base, int* flags,
+                                                                 int* bflag) {
   const int t = find_tensor(A, blockIdx.x);
   const int64_t n = A.n[t];
-  const int64_t start = (blockIdx.x - A.first_block[t]) * kChunk;
-  const int64_t end = start + kChunk < n ? start + kChunk : n;
+  const int64_t base = (blockIdx.x - A.first_block[t]) * kNormChunk;
   const T* g = (const T*)A.a[t];
-  float x[kEPT];
-  if (start + kChunk <= n && al16(g)) load_chunk<T, true, kEPT, true>(g, start, end, x);
-  else load_chunk<T, false>(g, start, end, x);  // out-of-range entries read as 0
+  float x[kNormSub][kEPT];
+  load_norm_chunks<T>(g, base, n, x);
   double acc = 0.0;
   int f = 0;
   using M = ChunkMap<T>;
 #pragma unroll
-  for (int i = 0; i < kEPT; ++i) {
-    if (M::at(start, i / M::PER) + i % M::PER >= end) continue;  // padding of a tail chunk
-    if (!isfinite(x[i])) f |= 1;
-    const float y = tg_to_float(tg_from_float<T>(x[i] * mul));
-    if (!isfinite(y)) {
-      f |= 2;
-      continue;
+  for (int c = 0; c < kNormSub; ++c) {
+    const int64_t start = base + c * kChunk;
+    const int64_t end = start + kChunk < n ? start + kChunk : n;
+#pragma unroll
+    for (int i = 0; i < kEPT; ++i) {
+      if (M::at(start, i / M::PER) + i % M::PER >= end) continue;  // past the tensor's end
+      if (!isfinite(x[c][i])) f |= 1;
+      const float y = tg_to_float(tg_from_float<T>(x[c][i] * mul));
+      if (!isfinite(y)) {
+        f |= 2;
+        continue;
+      }
+      const float ay = fabsf(y);
+      acc += (double)ay * (double)ay;
     }
-    const float ay = fabsf(y);
-    acc += (double)ay * (double)ay;
   }
   __shared__ double red[4];
+  __shared__ int redf[4];
   acc = tg_wave_sum_d(acc);
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) f |= __shfl_xor(f, off, 64);
   if ((threadIdx.x & 63) == 0) {
     red[threadIdx.x >> 6] = acc;
-    if (f) atomicOr(flags + A.fidx[t], f);
+    redf[threadIdx.x >> 6] = f;
+    if (!BFLAG && f) atomicOr(flags + A.fidx[t], f);
   }
   __syncthreads();
   if (threadIdx.x == 0) {
     part[part_base + blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
     tidx[part_base + blockIdx.x] = A.fidx[t];
+    if (BFLAG) bflag[part_base + blockIdx.x] = (redf[0] | redf[1]) | (redf[2] | redf[3]);
   }
 }
 
@@ -348,46 +382,80 @@ constexpr int kNormFinal = 1024;
 constexpr int kNF = 8;
 // With tidx (k_unscale_norm_partial): a partial whose tensor is flagged counts as 0,
 // the value it has once unscale_ has zeroed that tensor.  The flags of up to kFlagLds
-// tensors are staged in LDS first, so the mask is not a second dependent global load.
+// tensors live in LDS, so the mask is not a second dependent global load; with bflag
+// (per-block flags of the partial kernel) they are also formed here, OR-ed per tensor
+// in LDS and written to flags[] (no clearing launch, no global atomics).  Each thread
+// sums kNF strided partials per round with every load issued first, the kNF sums are
+// combined in a fixed tree, then within the wavefront (xor butterfly) and across the
+// 16 wavefronts in order: deterministic.
 constexpr int kFlagLds = 8192;
 template <int KIND>
 __global__ __launch_bounds__(kNormFinal) void k_norm_final(const double* part, int64_t n,
                                                            double* out,
                                                            const int* tidx = nullptr,
-                                                           const int* flags = nullptr,
-                                                           int ntensors = 0) {
+                                                           int* flags = nullptr,
+                                                           int ntensors = 0,
+                                                           const int* bflag = nullptr) {
   auto comb = [](double a, double b) { return KIND == 1 ? fmax(a, b) : a + b; };
   __shared__ int fl[kFlagLds];
+  __shared__ double red[kNormFinal / 64];
   const bool lds = tidx && ntensors <= kFlagLds;
   if (lds) {
-    for (int i = threadIdx.x; i < ntensors; i += kNormFinal) fl[i] = flags[i];
-    __syncthreads();
+    if (bflag) {
+      for (int i = threadIdx.x; i < ntensors; i += kNormFinal) fl[i] = 0;
+      __syncthreads();
+      for (int64_t b0 = threadIdx.x; b0 < n; b0 += (int64_t)kNormFinal * kNF) {
+        int f[kNF];
+#pragma unroll
+        for (int u = 0; u < kNF; ++u) {
+          const int64_t b = b0 + (int64_t)u * kNormFinal;
+          f[u] = b < n ? bflag[b] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < kNF; ++u)
+          if (f[u]) atomicOr(&fl[tidx[b0 + (int64_t)u * kNormFinal]], f[u]);
+      }
+      __syncthreads();
+      for (int i = threadIdx.x; i < ntensors; i += kNormFinal) flags[i] = fl[i];
+    } else {
+      for (int i = threadIdx.x; i < ntensors; i += kNormFinal) fl[i] = flags[i];
+      __syncthreads();
+    }
   }
   double acc[kNF];
 #pragma unroll
   for (int u = 0; u < kNF; ++u) acc[u] = 0.0;
   for (int64_t i0 = threadIdx.x; i0 < n; i0 += (int64_t)kNormFinal * kNF) {
+    double v[kNF];
+    int ti[kNF];
 #pragma unroll
     for (int u = 0; u < kNF; ++u) {
       const int64_t i = i0 + (int64_t)u * kNormFinal;
-      if (i < n) {
-        const bool masked = tidx && (lds ? fl[tidx[i]] : flags[tidx[i]]);
-        acc[u] = comb(acc[u], masked ? 0.0 : part[i]);
-      }
+      const bool ok = i < n;
+      v[u] = ok ? part[i] : 0.0;
+      ti[u] = (tidx && ok) ? tidx[i] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < kNF; ++u) {
+      const bool masked = ti[u] >= 0 && (lds ? fl[ti[u]] : flags[ti[u]]);
+      acc[u] = comb(acc[u], masked ? 0.0 : v[u]);
     }
   }
 #pragma unroll
   for (int w = kNF / 2; w >= 1; w /= 2)
 #pragma unroll
     for (int u = 0; u < w; ++u) acc[u] = comb(acc[u], acc[u + w]);
-  __shared__ double red[kNormFinal];
-  red[threadIdx.x] = acc[0];
+  double a = acc[0];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) a = comb(a, __shfl_xor(a, off, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = a;
   __syncthreads();
-  for (int s = kNormFinal / 2; s > 0; s >>= 1) {
-    if (threadIdx.x < s) red[threadIdx.x] = comb(red[threadIdx.x], red[threadIdx.x + s]);
-    __syncthreads();
+  if (threadIdx.x == 0) {
+    double r = red[0];
+#pragma unroll
+    for (int w = 1; w < kNormFinal / 64; ++w) r = comb(r, red[w]);
+    out[0] = r;
   }
-  if (threadIdx.x == 0) out[0] = red[0];
 }
 
 // Non-finite entries become zero; a 16-byte vector is written back only if it held one.
@@ -492,10 +560,10 @@ int for_each_launch(int ntensors, void* const* a, void* const* b, void* const* c
   return flush();
 }
 
-int64_t total_blocks(int ntensors, const int64_t* numel) {
+int64_t total_blocks(int ntensors, const int64_t* numel, int64_t chunk = kChunk) {
   int64_t b = 0;
   for (int i = 0; i < ntensors; ++i)
-    if (numel[i] > 0) b += (numel[i] + kChunk - 1) / kChunk;
+    if (numel[i] > 0) b += (numel[i] + chunk - 1) / chunk;
   return b;
 }
 
@@ -654,6 +722,8 @@ TG_EXPORT int tg_grad_norm(int ntensors, int dtype, void* const* grads, const in
   if (dtype == TG_F64)  // one partial per kChunk elements, as the workspace counts them
     return tg64_grad_norm(ntensors, grads, numel, norm_kind, p, kChunk, out, flags, part, s);
   if (ntensors > 0) k_zero_ints<<<1, kBlock, 0, s>>>(flags, ntensors);
+  // (the workspace counts kChunk partials, at least the kNormChunk ones used here)
+  const int64_t nparts = ntensors > 0 ? total_blocks(ntensors, numel, kNormChunk) : 0;
   int64_t part_base = 0;
   int st = TG_OK;
   if (ntensors > 0)
@@ -668,19 +738,20 @@ TG_EXPORT int tg_grad_norm(int ntensors, int dtype, void* const* grads, const in
 #undef L
                            part_base += nb;
                            return tg_check_launch("tg_grad_norm");
-                         });
+                         },
+                         kNormChunk);
   if (st) return st;
   if (norm_kind == 1)
-    k_norm_final<1><<<1, kNormFinal, 0, s>>>(part, nb_total, out);
+    k_norm_final<1><<<1, kNormFinal, 0, s>>>(part, nparts, out);
   else
-    k_norm_final<0><<<1, kNormFinal, 0, s>>>(part, nb_total, out);
+    k_norm_final<0><<<1, kNormFinal, 0, s>>>(part, nparts, out);
   return tg_check_launch("tg_grad_norm final");
 }
 
 TG_EXPORT size_t tg_unscale_norm_workspace(int ntensors, const int64_t* numel) {
   if (ntensors <= 0 || !numel) return 2 * sizeof(double);
-  const int64_t b = total_blocks(ntensors, numel);
-  return (size_t)(b > 0 ? b : 1) * (sizeof(double) + sizeof(int)) + sizeof(double);
+  const int64_t b = total_blocks(ntensors, numel, kNormChunk);
+  return (size_t)(b > 0 ? b : 1) * (sizeof(double) + 2 * sizeof(int)) + sizeof(double);
 }
 
 // Read-only form of GradScaler.unscale_ plus clip_grad_norm_'s reduction: flags[i]
@@ -697,7 +768,7 @@ TG_EXPORT int tg_unscale_norm(int ntensors, int dtype, void* const* grads, const
              "tg_unscale_norm: unsupported dtype %d", dtype);
   TG_REQUIRE(ntensors == 0 || (grads && numel), "tg_unscale_norm: null argument");
   hipStream_t s = tg_stream(stream);
-  const int64_t nb_total = ntensors > 0 ? total_blocks(ntensors, numel) : 0;
+  const int64_t nb_total = ntensors > 0 ? total_blocks(ntensors, numel, kNormChunk) : 0;
   const size_t need = tg_unscale_norm_workspace(ntensors, numel);
   if (!workspace || workspace_bytes < need) {
     tg_set_error("tg_unscale_norm: workspace of %zu bytes needed", need);
@@ -705,22 +776,30 @@ TG_EXPORT int tg_unscale_norm(int ntensors, int dtype, void* const* grads, const
   }
   double* part = (double*)workspace;
   int* tidx = (int*)(part + (nb_total > 0 ? nb_total : 1));
-  if (ntensors > 0) k_zero_ints<<<1, kBlock, 0, s>>>(flags, ntensors);
+  int* bflag = tidx + (nb_total > 0 ? nb_total : 1);
+  // up to kFlagLds tensors: per-block flags OR-ed by the final kernel; beyond that,
+  // cleared flags and per-wavefront atomics
+  const bool bf = ntensors <= kFlagLds;
+  if (ntensors > 0 && !bf) k_zero_ints<<<1, kBlock, 0, s>>>(flags, ntensors);
   int64_t part_base = 0;
   int st = TG_OK;
   if (ntensors > 0)
     st = for_each_launch(ntensors, grads, nullptr, nullptr, nullptr, nullptr, nullptr, numel,
                          [&](const MtArgs& A, int64_t nb) {
-#define L(T) k_unscale_norm_partial<T><<<(unsigned)nb, kBlock, 0, s>>>(A, mul, part, tidx, part_base, flags)
-                           if (dtype == TG_F32) L(float);
-                           else if (dtype == TG_F16) L(tg_half);
-                           else L(tg_bf16);
+#define L(T, B) k_unscale_norm_partial<T, B><<<(unsigned)nb, kBlock, 0, s>>>(A, mul, part, tidx, part_base, flags, bflag)
+#define LB(T) if (bf) L(T, true); else L(T, false)
+                           if (dtype == TG_F32) LB(float);
+                           else if (dtype == TG_F16) LB(tg_half);
+                           else LB(tg_bf16);
+#undef LB
 #undef L
                            part_base += nb;
                            return tg_check_launch("tg_unscale_norm");
-                         });
+                         },
+                         kNormChunk);
   if (st) return st;
-  k_norm_final<0><<<1, kNormFinal, 0, s>>>(part, nb_total, out, tidx, flags, ntensors);
+  k_norm_final<0><<<1, kNormFinal, 0, s>>>(part, nb_total, out, tidx, flags, ntensors,
+                                           bf ? bflag : nullptr);
   return tg_check_launch("tg_unscale_norm final");
 }
 
