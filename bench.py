@@ -339,6 +339,19 @@ def _op_ce(torch, L, g):
     return Timed("cross_entropy_fwd_bwd", run, 3 * 2 * N * C, "GB/s", HBM_PEAK_GBS)
 
 
+def _op_ce_one_pass(torch, L, g):
+    """The same cross-entropy as the engine runs it when a backward follows (its gradient
+    does not depend on the upstream one): statistics, losses and the fp16 gradient from
+    one read of the logits.  Algorithmic bytes: 2 x 524 MB."""
+    N, C = 8192, 32000
+    x = (torch.randn(N, C, device="cuda", generator=g) * 2).half()
+    y = torch.randint(0, C, (N,), device="cuda", generator=g)
+
+    def run():
+        L.cross_entropy_fwd_grad(x, y, 1.0 / N)
+    return Timed("cross_entropy_one_pass", run, 2 * 2 * N * C, "GB/s", HBM_PEAK_GBS)
+
+
 def _op_embedding(torch, L, g):
     """C5 embedding backward: fp32 output gradient [8192, 1024] scattered into a fresh
     [32000, 1024] fp32 gradient (deterministic sorted scatter-add; untouched rows
@@ -400,6 +413,7 @@ def component_ops(torch, L, only):
                 ("unscale_norm", lambda: _op_unscale_norm(torch, L, g)),
                 ("gemm_fc1_bwd", lambda: _op_gemm(torch, L, g)),
                 ("cross_entropy_fwd_bwd", lambda: _op_ce(torch, L, g)),
+                ("cross_entropy_one_pass", lambda: _op_ce_one_pass(torch, L, g)),
                 ("embedding_bwd", lambda: _op_embedding(torch, L, g)),
                 ("layernorm_bwd_c5_fp16", lambda: _op_ln_c5(torch, L, g)),
                 ("tied_grad_sync", lambda: _op_tied(torch, L, g)),

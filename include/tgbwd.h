@@ -364,6 +364,17 @@ int tg_flash_attn_bwd_f64(const double* q, const double* k, const double* v, con
  * loss.  dtype fp32/fp16/bf16 (fp64: tg_cross_entropy_fwd_f64). */
 int tg_cross_entropy_fwd(int dtype, const void* logits, const int64_t* targets, int64_t N,
                          int64_t C, float label_smoothing, float* lse, float* loss, void* stream);
+/* tg_cross_entropy_fwd (label smoothing 0) and the gradient grad = (softmax - onehot) *
+ * scale in the logits' dtype, from one read of the logits (each row held in registers;
+ * C at most tg_cross_entropy_fwd_grad_max_classes(dtype), a multiple of 16 bytes' worth
+ * of elements, 16-byte aligned logits and grad).  Bit for bit tg_cross_entropy_fwd
+ * followed by tg_cross_entropy_bwd(accumulate = 0).  The reference's backward does not
+ * use the loss's upstream gradient (_nn.py:1168-1180), so the gradient is known at the
+ * forward (_nn.py:1128-1185) and the backward only hands it to the logits. */
+int tg_cross_entropy_fwd_grad_max_classes(int dtype);
+int tg_cross_entropy_fwd_grad(int dtype, const void* logits, const int64_t* targets, int64_t N,
+                              int64_t C, float* lse, float* loss, float scale, void* grad,
+                              void* stream);
 /* Backward (_nn.py:1168-1180): grad (+)= (softmax(logits) - w) * scale, with
  * scale = 1/N for the mean reduction and no upstream-gradient factor, as in the
  * reference.  grad has dtype dtype_grad. */

@@ -218,6 +218,77 @@ __global__ __launch_bounds__(kBlock) void k_ce_bwd(const T* __restrict__ X,
   }
 }
 
+// Forward and gradient in one pass (no label smoothing; the gradient does not depend on
+// the loss's upstream gradient): the row stays in registers, kFgVec 16-byte vectors per
+// thread at vector indices tid + k*kBlock, which the statistics visit in the steps of
+// row_stats (4 vectors at a time), so the log-sum-exp, the loss and the gradient are
+// bit for bit those of k_ce_fwd followed by k_ce_bwd.  Reads the logits once instead of
+// twice.
+constexpr int kFgVec = 16;
+template <typename T, bool NTS>
+__global__ __launch_bounds__(kBlock) void k_ce_fwd_grad(const T* __restrict__ X,
+                                                        const int64_t* __restrict__ tgt,
+                                                        int64_t C, float* __restrict__ lse_out,
+                                                        float* __restrict__ loss_out, float scale,
+                                                        T* __restrict__ G) {
+  constexpr int V = tg_vec16<T>::N, U = 4;
+  const int64_t row = blockIdx.x;
+  const T* x = X + row * C;
+  T* g = G + row * C;
+  const int nv = (int)(C / V);
+  tg_vec16<T> v[kFgVec];
+#pragma unroll
+  for (int k = 0; k < kFgVec; ++k) {
+    const int i = threadIdx.x + k * kBlock;
+    if (i < nv) v[k] = tg_load16(x + (int64_t)i * V);
+    else
+#pragma unroll
+      for (int j = 0; j < V; ++j) v[k].v[j] = tg_from_float<T>(-INFINITY);
+  }
+  float m = -INFINITY, s = 0.f;
+#pragma unroll
+  for (int k0 = 0; k0 < kFgVec; k0 += U) {
+    if (threadIdx.x + k0 * kBlock >= nv) break;  // row_stats stops at the same step
+    tg_vec16<T> w[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) w[u] = v[k0 + u];
+    const float vm = vec_max<T, U>(w) * kLog2e;
+    const float mn = fmaxf(m, vm);
+    const float mref = mn == -INFINITY ? 0.f : mn;
+    s *= fexp2(m - mref);
+    m = mn;
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int j = 0; j < V; ++j) s += fexp2(fmaf(tg_to_float(w[u].v[j]), kLog2e, -mref));
+  }
+  const float lse = block_lse(m, s);
+  const int64_t t = tgt[row];
+  const bool valid = t >= 0 && t < C;
+  if (threadIdx.x == 0) {
+    lse_out[row] = lse;
+    loss_out[row] = valid ? -logf(expf(tg_to_float(x[t]) - lse) + 1e-10f) : NAN;
+  }
+  const float l2 = lse * kLog2e;
+#pragma unroll
+  for (int k = 0; k < kFgVec; ++k) {
+    const int i = threadIdx.x + k * kBlock;
+    if (i < nv) {
+      tg_vec16<T> o;
+#pragma unroll
+      for (int j = 0; j < V; ++j) {
+        // p*scale rounded, then the target's -scale: the two roundings of k_ce_bwd (not
+        // contracted into one fused multiply-add)
+#pragma clang fp contract(off)
+        float r = fexp2(fmaf(tg_to_float(v[k].v[j]), kLog2e, -l2)) * scale;
+        if (valid && (int64_t)i * V + j == t) r -= scale;
+        o.v[j] = tg_from_float<T>(r);
+      }
+      tg_st16<NTS>(g + (int64_t)i * V, o);
+    }
+  }
+}
+
 template <typename T>
 int fwd_t(const void* x, const int64_t* tg, int64_t N, int64_t C, float smooth, float* lse,
           float* loss, hipStream_t s) {
@@ -282,6 +353,45 @@ TG_EXPORT int tg_cross_entropy_fwd(int dtype, const void* logits, const int64_t*
   tg_set_error("tg_cross_entropy_fwd: unsupported dtype %d (fp64: tg_cross_entropy_fwd_f64)",
                dtype);
   return TG_ERR_UNSUPPORTED;
+}
+
+TG_EXPORT int tg_cross_entropy_fwd_grad_max_classes(int dtype) {
+  switch (dtype) {
+    case TG_F32: return kFgVec * kBlock * tg_vec16<float>::N;
+    case TG_F16:
+    case TG_BF16: return kFgVec * kBlock * tg_vec16<tg_half>::N;
+  }
+  return 0;
+}
+
+TG_EXPORT int tg_cross_entropy_fwd_grad(int dtype, const void* logits, const int64_t* targets,
+                                        int64_t N, int64_t C, float* lse, float* loss,
+                                        float scale, void* grad, void* stream) {
+  int st = check(N, C, 0.f, "tg_cross_entropy_fwd_grad");
+  if (st) return st;
+  if (N == 0) return TG_OK;
+  TG_REQUIRE(logits && targets && lse && loss && grad, "tg_cross_entropy_fwd_grad: null pointer");
+  TG_REQUIRE(dtype == TG_F32 || dtype == TG_F16 || dtype == TG_BF16,
+             "tg_cross_entropy_fwd_grad: unsupported dtype %d", dtype);
+  const int V = dtype == TG_F32 ? 4 : 8;
+  TG_REQUIRE(C % V == 0 && C <= tg_cross_entropy_fwd_grad_max_classes(dtype) &&
+                 tg_aligned16(logits) && tg_aligned16(grad),
+             "tg_cross_entropy_fwd_grad: needs 16-byte aligned rows of at most %d classes, "
+             "a multiple of %d (C = %lld)",
+             tg_cross_entropy_fwd_grad_max_classes(dtype), V, (long long)C);
+  hipStream_t s = tg_stream(stream);
+  const int64_t esz = dtype == TG_F32 ? 4 : 2;
+  const bool nts = esz * N * C >= (128ll << 20);
+#define L(T)                                                                                  \
+  if (nts) k_ce_fwd_grad<T, true><<<(unsigned)N, kBlock, 0, s>>>((const T*)logits, targets, C, \
+                                                                 lse, loss, scale, (T*)grad); \
+  else k_ce_fwd_grad<T, false><<<(unsigned)N, kBlock, 0, s>>>((const T*)logits, targets, C,   \
+                                                              lse, loss, scale, (T*)grad)
+  if (dtype == TG_F32) L(float);
+  else if (dtype == TG_F16) L(tg_half);
+  else L(tg_bf16);
+#undef L
+  return tg_check_launch("tg_cross_entropy_fwd_grad");
 }
 
 TG_EXPORT int tg_cross_entropy_bwd(int dtype, const void* logits, const int64_t* targets,

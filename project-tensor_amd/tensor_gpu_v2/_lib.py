@@ -114,6 +114,8 @@ SIGNATURES = {
     "tg_flash_attn_bwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64,
                                  _i64, _i64, _i64, _f32, _i32, _i32, _vp, _sz, _vp]),
     "tg_cross_entropy_fwd": (_i32, [_i32, _vp, _vp, _i64, _i64, _f32, _vp, _vp, _vp]),
+    "tg_cross_entropy_fwd_grad_max_classes": (_i32, [_i32]),
+    "tg_cross_entropy_fwd_grad": (_i32, [_i32, _vp, _vp, _i64, _i64, _vp, _vp, _f32, _vp, _vp]),
     "tg_embedding_bwd_workspace": (_sz, [_i64, _i64]),
     "tg_embedding_fwd": (_i32, [_i32, _vp, _vp, _i64, _i64, _i64, _i32, _vp, _vp]),
     "tg_embedding_bwd": (_i32, [_i32, _vp, _vp, _i64, _i64, _i32, _vp, _i64, _i32, _vp, _sz, _vp]),
@@ -1224,6 +1226,40 @@ def cross_entropy_fwd(logits, targets, label_smoothing=0.0):
         dtype_code(logits), ptr(logits), ptr(targets), N, C, float(label_smoothing), ptr(lse),
         ptr(loss), stream_handle()))
     return lse, loss
+
+
+def cross_entropy_fwd_grad_ok(logits):
+    """Whether cross_entropy_fwd_grad takes these logits (fp32/fp16/bf16, 16-byte
+    aligned rows of at most the kernel's register-resident width)."""
+    if logits.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        return False
+    if logits.dim() != 2 or not logits.is_contiguous() or logits.data_ptr() % 16:
+        return False
+    C = logits.shape[1]
+    v = 16 // logits.element_size()
+    return C % v == 0 and C <= load().tg_cross_entropy_fwd_grad_max_classes(dtype_code(logits))
+
+
+def cross_entropy_fwd_grad(logits, targets, scale):
+    """cross_entropy_fwd (no label smoothing) and the gradient (softmax - onehot) * scale
+    in the logits' dtype, from one read of the logits: returns (lse, loss, grad), bit for
+    bit cross_entropy_fwd's results and what cross_entropy_bwd would write."""
+    _dev(logits, "logits")
+    _dev(targets, "targets")
+    if not cross_entropy_fwd_grad_ok(logits):
+        raise ValueError("cross_entropy_fwd_grad: logits not supported (see "
+                         "cross_entropy_fwd_grad_ok)")
+    if targets.dtype != torch.int64 or targets.numel() != logits.shape[0]:
+        raise ValueError("cross_entropy: targets must be int64 [N]")
+    N, C = logits.shape
+    lse = torch.empty(N, dtype=torch.float32, device=logits.device)
+    loss = torch.empty(N, dtype=torch.float32, device=logits.device)
+    grad = torch.empty_like(logits)
+    ensure_device(logits.device.index)
+    _check("tg_cross_entropy_fwd_grad", load().tg_cross_entropy_fwd_grad(
+        dtype_code(logits), ptr(logits), ptr(targets), N, C, ptr(lse), ptr(loss), float(scale),
+        ptr(grad), stream_handle()))
+    return lse, loss, grad
 
 
 def cross_entropy_bwd(logits, targets, lse, grad, scale, accumulate, label_smoothing=0.0):

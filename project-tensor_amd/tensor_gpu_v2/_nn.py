@@ -529,22 +529,35 @@ class CrossEntropyLoss(Module):
         if tg.numel() != N:
             raise ValueError(f"CrossEntropyLoss: {tg.numel()} targets for {N} rows")
         ldc = ld.contiguous()
-        lse, loss = L.cross_entropy_fwd(ldc, tg, self.label_smoothing)
+        strict = self.strict_chain_rule
+        scale = 1.0 / N if self.reduction == "mean" else 1.0
+        smoothing = self.label_smoothing
+        # The gradient does not depend on the upstream one (the reference's rule): when
+        # a backward may follow, it is formed here, from the same read of the logits.
+        pre = (not strict and smoothing == 0 and cfg._grad_enabled and logits._requires_grad
+               and L.cross_entropy_fwd_grad_ok(ldc))
+        grad = None
+        if pre:
+            lse, loss, grad = L.cross_entropy_fwd_grad(ldc, tg, scale)
+        else:
+            lse, loss = L.cross_entropy_fwd(ldc, tg, self.label_smoothing)
         if self.reduction == "mean":
             lv = loss.mean()
         elif self.reduction == "sum":
             lv = loss.sum()
         else:
             lv = loss
-        strict = self.strict_chain_rule
         out = Tensor._wrap(lv.to(ld.dtype), (logits,), "CrossEntropy")
         if strict:
             out.data = lv  # fp32, past the autocast cast of _wrap
-        scale = 1.0 / N if self.reduction == "mean" else 1.0
-        smoothing = self.label_smoothing
         if out._requires_grad:
             def _backward():
                 if not logits._has_grad():
+                    return
+                if grad is not None:
+                    # formed by the forward: adopted as the logits' gradient buffer
+                    # when it has none yet, else added
+                    logits._accumulate(grad.reshape(ld.shape), owned=True)
                     return
                 sc = scale * float(out._grad_out().reshape(-1)[0]) if strict else scale
                 buf, acc = logits._grad_target()

@@ -91,3 +91,48 @@ def test_ce_target_range(cuda):
     lse, loss = L().cross_entropy_fwd(x.data, torch.tensor([0, 5], device="cuda"))
     out = loss.cpu().numpy()
     assert np.isfinite(out[0]) and np.isnan(out[1])
+
+
+@pytest.mark.parametrize("N,C", [(32, 16), (7, 4096), (64, 32000), (5, 32768), (9, 8)])
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16, torch.bfloat16])
+def test_ce_fwd_grad_equals_fwd_then_bwd(cuda, N, C, dt):
+    """tg_cross_entropy_fwd_grad (one read of the logits) against tg_cross_entropy_fwd
+    followed by tg_cross_entropy_bwd: bit-identical lse, loss and gradient, also for an
+    out-of-range target (NaN loss, no target term); the oracle pins the pair."""
+    if not L().cross_entropy_fwd_grad_ok(torch.empty(1, C, dtype=dt, device="cuda")):
+        assert dt == torch.float32 and C > 16384
+        return
+    g = torch.Generator(device="cuda").manual_seed(N + C)
+    x = (torch.randn(N, C, device="cuda", generator=g) * 3).to(dt)
+    y = torch.randint(0, C, (N,), device="cuda", generator=g)
+    y[N // 2] = C  # outside [0, C)
+    lse, loss = L().cross_entropy_fwd(x, y)
+    ref = torch.empty_like(x)
+    L().cross_entropy_bwd(x, y, lse, ref, 1.0 / N, False)
+    lse2, loss2, grad = L().cross_entropy_fwd_grad(x, y, 1.0 / N)
+    assert torch.equal(lse2, lse)
+    assert torch.equal(torch.nan_to_num(loss2, nan=-7.0), torch.nan_to_num(loss, nan=-7.0))
+    assert torch.isnan(loss2[N // 2])
+    assert torch.equal(grad, ref)
+
+
+def test_ce_module_gradient_formed_in_forward(cuda):
+    """CrossEntropyLoss with a backward to follow takes the one-pass kernel: the logits'
+    gradient (adopted from the forward, then accumulated on a second backward) equals
+    the two-pass path's (under no_grad-free eval it is not formed at all)."""
+    import tensor_gpu_v2 as tg
+    rng = np.random.default_rng(3)
+    x_np = (rng.standard_normal((64, 4096)) * 2).astype(np.float32)
+    y_np = rng.integers(0, 4096, 64)
+    grads = []
+    for smoothing in (0.0, 1e-12):  # any smoothing takes the two-pass path
+        x = tg.Tensor(x_np)
+        ce = tg.CrossEntropyLoss(label_smoothing=smoothing)
+        for _ in range(2):
+            ce(x, y_np).backward()
+        grads.append(x.grad.clone())
+    assert_close(grads[0], f64(grads[1]), 1e-6, "one-pass vs two-pass CE gradient")
+    x = tg.Tensor(x_np)
+    with tg.no_grad():
+        loss = tg.CrossEntropyLoss()(x, y_np)
+    assert loss.data.numel() == 1
