@@ -240,7 +240,7 @@ __global__ __launch_bounds__(kBlock) void k_ce_fwd_grad(const T* __restrict__ X,
 #pragma unroll
   for (int k = 0; k < kFgVec; ++k) {
     const int i = threadIdx.x + k * kBlock;
-    if (i < nv) v[k] = tg_load16(x + (int64_t)i * V);
+    if (i < nv) v[k] = tg_ld16<NTS>(x + (int64_t)i * V);  // read once: non-temporal when large
     else
 #pragma unroll
       for (int j = 0; j < V; ++j) v[k].v[j] = tg_from_float<T>(-INFINITY);
