@@ -252,6 +252,67 @@ __global__ __launch_bounds__(kThreads) void k_gemm(int64_t M, int64_t N, int64_t
 }
 
 // ---------------------------------------------------------------------------
+// Small fp32 outputs (the generic kernel's 128 x 128 tiles leave most CUs idle and, for
+// a few rows, compute mostly padding): one 32 x 32 output tile per workgroup, its four
+// wavefronts each taking a quarter of K with the fp32 MFMA's fragments read straight
+// from global memory (no operand is shared between wavefronts), then the four partial
+// tiles added in LDS in a fixed order (deterministic).  Of every 8 k, lane half h
+// multiplies k + 4h .. k + 4h + 3 in four MFMAs (the same pairing for A and B).
+template <typename TC, bool TA, bool TB>
+__global__ __launch_bounds__(kThreads) void k_gemm_f32_small(
+    int64_t M, int64_t N, int64_t K, float alpha, const float* __restrict__ A, int64_t lda,
+    int64_t sa, const float* __restrict__ B, int64_t ldb, int64_t sb, float beta,
+    TC* __restrict__ C, int64_t ldc, int64_t sc, const float* __restrict__ bias) {
+  const int64_t bz = blockIdx.z;
+  A += bz * sa;
+  B += bz * sb;
+  C += bz * sc;
+  const int64_t m0 = (int64_t)blockIdx.y * 32, n0 = (int64_t)blockIdx.x * 32;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l32 = lane & 31, h = lane >> 5;
+  const int64_t row = m0 + l32, col = n0 + l32;
+  const int64_t per = ((K + 31) / 32) * 8;  // k per wavefront, a multiple of 8
+  const int64_t kb = wave * per;
+  const int64_t ke = kb + per < K ? kb + per : K;
+  const bool rok = row < M, cok = col < N;
+  f32x16 acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+#pragma unroll 4
+  for (int64_t k0 = kb; k0 < ke; k0 += 8) {
+    float a[4], b[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t k = k0 + 4 * h + j;
+      const bool kok = k < ke;
+      a[j] = (rok && kok) ? (TA ? A[k * lda + row] : A[row * lda + k]) : 0.f;
+      b[j] = (cok && kok) ? (TB ? B[col * ldb + k] : B[k * ldb + col]) : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[j], b[j], acc, 0, 0, 0);
+  }
+  __shared__ float red[3][16][64];
+  if (wave > 0) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) red[wave - 1][r][lane] = acc[r];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const float v = ((acc[r] + red[0][r][lane]) + red[1][r][lane]) + red[2][r][lane];
+    const int64_t i = m0 + (r >> 2) * 8 + h * 4 + (r & 3);
+    if (i < M && cok) {
+      float o = alpha * v;
+      if (bias) o += bias[col];
+      TC* pc = C + i * ldc + col;
+      if (beta != 0.f) o += beta * tg_to_float(*pc);
+      *pc = tg_from_float<TC>(o);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Pipelined kernel for fp16/bf16: block tile 128 x BN x 64 (BN = 128 or 64),
 // 4 wavefronts in a 2 x 2 grid, each owning a 64 x BN/2 sub-tile of MFMA 32x32
 // tiles; LDS double-buffered so the next k-tile's global loads overlap the
@@ -975,6 +1036,20 @@ int launch(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const v
 #undef TG_G2
     return tg_check_launch("tg_gemm");
   }
+  }
+  if constexpr (sizeof(T) == 4) {
+    // fewer 128 x 128 tiles than a quarter of the CUs: 32 x 32 tiles, K in four
+    if ((int64_t)grid.x * grid.y * grid.z * 4 < (int64_t)tg_num_cus() && K >= 64) {
+      dim3 gs((unsigned)((N + 31) / 32), (unsigned)((M + 31) / 32), (unsigned)batch);
+#define TG_GS(TA_, TB_) \
+  k_gemm_f32_small<TC, TA_, TB_><<<gs, kThreads, 0, s>>>(M, N, K, alpha, a, lda, sa, b, ldb, sb, beta, c, ldc, sc, bias)
+      if (!ta && !tb) TG_GS(false, false);
+      else if (!ta && tb) TG_GS(false, true);
+      else if (ta && !tb) TG_GS(true, false);
+      else TG_GS(true, true);
+#undef TG_GS
+      return tg_check_launch("tg_gemm");
+    }
   }
 #define TG_G(TA_, TB_, V_) \
   k_gemm<T, TC, TA_, TB_, V_><<<grid, kThreads, 0, s>>>(M, N, K, alpha, a, lda, sa, b, ldb, sb, beta, c, ldc, sc, bias)
