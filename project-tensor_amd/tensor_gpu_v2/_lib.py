@@ -329,6 +329,32 @@ def _i64_array(vals):
     return (ctypes.c_int64 * max(len(vals), 1))(*vals)
 
 
+def _bcast_space(shapes):
+    """NumPy broadcast of the shapes (right-aligned), as torch.broadcast_shapes."""
+    nd = max(len(sh) for sh in shapes)
+    space = [1] * nd
+    for sh in shapes:
+        off = nd - len(sh)
+        for i, n in enumerate(sh):
+            cur = space[off + i]
+            if n != cur:
+                if cur == 1:
+                    space[off + i] = n
+                elif n != 1:
+                    raise RuntimeError(f"shapes {shapes} are not broadcastable")
+    return tuple(space)
+
+
+def _bcast_strides(t, space):
+    """Strides of t viewed expanded to space (0 on broadcast axes), as
+    t.expand(space).stride()."""
+    off = len(space) - t.dim()
+    st = [0] * len(space)
+    for i, (n, s_) in enumerate(zip(t.shape, t.stride())):
+        st[off + i] = s_ if n == space[off + i] else 0
+    return st
+
+
 def broadcast_mul_sum(out, a, b=None, alpha=1.0, accumulate=False):
     """out (+)= alpha * a * b, with a and b broadcast (NumPy rules) to the index space
     broadcast(a, b, out) and the result summed over every axis where out has extent 1
@@ -342,15 +368,15 @@ def broadcast_mul_sum(out, a, b=None, alpha=1.0, accumulate=False):
         if t.dtype not in _BCAST_CODE:
             raise TypeError(f"broadcast_mul_sum: unsupported dtype {t.dtype} for {n}")
     shapes = [tuple(a.shape), tuple(out.shape)] + ([tuple(b.shape)] if b is not None else [])
-    space = torch.broadcast_shapes(*shapes)
+    space = _bcast_space(shapes)
     if len(out.shape) > len(space):
         raise ValueError(f"broadcast_mul_sum: out {tuple(out.shape)} has more axes than {space}")
     for size, stride in zip(out.shape, out.stride()):
         if size > 1 and stride == 0:
             raise ValueError("broadcast_mul_sum: out overlaps itself (a zero stride)")
-    sa = a.expand(space).stride()
-    so = out.expand(space).stride()
-    sb = b.expand(space).stride() if b is not None else ()
+    sa = _bcast_strides(a, space)
+    so = _bcast_strides(out, space)
+    sb = _bcast_strides(b, space) if b is not None else ()
     nd = len(space)
     ensure_device(out.device.index)
     _check("tg_broadcast_mul_sum", load().tg_broadcast_mul_sum(
