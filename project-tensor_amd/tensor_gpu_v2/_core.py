@@ -15,6 +15,8 @@ the reference's `parent.grad += local` with one read pass fewer.  Reading
 `.grad` materialises the zeros, so observable behaviour matches.
 """
 
+import weakref
+
 import numpy as np
 import torch
 
@@ -44,14 +46,25 @@ _WG_MAX_BYTES = 4 << 30  # flush early once the queue keeps this much alive
 # gradient instead of rewriting it: _GSCALE[id(t)] = (t, (f1, f2, ...)) means the
 # gradient is its buffer scaled in place by f1, then by f2, ... (one fp32 rounding each).
 # The optimizer applies the factors as it reads the buffers; any other access to the
-# gradient applies them first (_settle), so every value read is the rewritten one.
+# gradient applies them first (_settle), so every value read is the rewritten one.  The
+# tensor is held weakly: an entry leaves with its tensor (no model is kept alive by it,
+# and a later object reusing the id never inherits its factors).
 _GSCALE = {}
 
 
 def _grad_scale_pending(t, factor):
     """Record one more pending in-place scaling of t's gradient buffer by factor."""
-    e = _GSCALE.get(id(t))
-    _GSCALE[id(t)] = (t, (e[1] if e is not None else ()) + (float(factor),))
+    k = id(t)
+    e = _GSCALE.get(k)
+    if e is not None:
+        _GSCALE[k] = (e[0], e[1] + (float(factor),))
+        return
+
+    def _gone(ref, k=k):
+        cur = _GSCALE.get(k)
+        if cur is not None and cur[0] is ref:
+            del _GSCALE[k]
+    _GSCALE[k] = (weakref.ref(t, _gone), (float(factor),))
 
 
 def _grad_factors(t):

@@ -7,6 +7,7 @@ GradScaler — run their gradient math in libtgbwd's HIP kernels.
 import math
 import types
 import warnings
+import weakref
 
 import numpy as np
 import torch
@@ -781,8 +782,9 @@ class _UnscaledNorm:
     applies the scaling and ends the match)."""
 
     def __init__(self, params, inv, resolve):
-        self.params = list(params)
-        self.bufs = [p._g for p in params]
+        # weak: the cache must not keep a discarded model or a cleared gradient alive
+        self.params = [weakref.ref(p) for p in params]
+        self.bufs = [weakref.ref(p._g) for p in params]
         self.factors = (float(inv),)
         self.resolve = resolve
 
@@ -790,7 +792,7 @@ class _UnscaledNorm:
         if len(params) != len(self.params):
             return False
         for p, q, b in zip(params, self.params, self.bufs):
-            if p is not q or p._g is not b or _core._grad_factors(p) != self.factors:
+            if p is not q() or p._g is not b() or _core._grad_factors(p) != self.factors:
                 return False
         return True
 

@@ -188,3 +188,45 @@ def test_clip_on_other_parameters_falls_back(tg):
     assert abs(n - ref) <= 1e-6 * ref
     for p, r in zip(params, raw):
         assert torch.equal(p.grad, r * (1.0 / 2 ** 8))
+
+
+def test_pending_scalings_dropped_by_zero_grad_and_replacement(tg):
+    """zero_grad() discards a gradient's pending factors (nothing is computed for a
+    buffer being cleared), a replaced gradient (p.grad = ...) reads as given, and an
+    untouched one reads as scaled."""
+    from tensor_gpu_v2 import _core
+    params, loss_fn = _mlp(tg, 14)
+    opt = tg.AdamW(params, lr=1e-2)
+    sc = tg.GradScaler(init_scale=2.0 ** 6)
+    with tg.autocast():
+        loss = loss_fn()
+    sc.scale(loss).backward()
+    raw = [p.grad.clone() for p in params]
+    sc.unscale_(opt)
+    assert all(_core._grad_factors(p) == (2.0 ** -6,) for p in params)
+    params[0].zero_grad()
+    assert id(params[0]) not in _core._GSCALE
+    assert not torch.any(params[0].grad != 0)
+    new = torch.full_like(raw[1], 3.0)
+    params[1].grad = new
+    assert id(params[1]) not in _core._GSCALE and torch.equal(params[1].grad, new)
+    assert torch.equal(params[2].grad, raw[2] * (2.0 ** -6))
+    assert id(params[2]) not in _core._GSCALE  # applied by the read
+    assert _core._grad_factors(params[3]) == (2.0 ** -6,)
+    for p in params:
+        p.zero_grad()
+    assert not any(id(p) in _core._GSCALE for p in params)
+
+
+def test_pending_scaling_entry_leaves_with_its_tensor(tg):
+    """A parameter dropped while a scaling is pending takes its entry with it."""
+    import gc
+    from tensor_gpu_v2 import _core
+    p = tg.Tensor(np.ones(10, np.float32))
+    p.grad = np.ones(10, np.float32)
+    _core._grad_scale_pending(p, 0.5)
+    k = id(p)
+    assert k in _core._GSCALE
+    del p
+    gc.collect()
+    assert k not in _core._GSCALE

@@ -242,3 +242,34 @@ def test_linear_deferred_weight_gradients(cuda):
     for i, ((wa, ba), (wb, bb)) in enumerate(zip(a, b)):
         assert_close(wa, wb.double(), RTOL_F16, f"layer {i} dW")
         assert_close(ba, bb.double(), RTOL_F16, f"layer {i} db")
+
+
+def test_deferred_weight_gradients_flushed_when_backward_raises(cuda):
+    """A node that raises during the sweep: the weight gradients queued before it are
+    still computed (backward's finally), the queue and its bookkeeping are empty, and
+    a later backward runs normally."""
+    import numpy as np
+    import tensor_gpu_v2 as tg
+    from tensor_gpu_v2 import _core
+    rng = np.random.default_rng(41)
+    l1, l2 = tg.Linear(256, 256), tg.Linear(256, 256)
+    x = tg.Tensor(rng.standard_normal((512, 256)).astype(np.float32))
+    with tg.autocast():
+        h = l1(x)
+        y = l2(h.relu())
+        loss = (y * y).mean()
+
+    def boom():
+        raise RuntimeError("injected")
+    h._backward = boom  # l2's weight gradient is queued before h's node runs
+    with pytest.raises(RuntimeError, match="injected"):
+        loss.backward()
+    assert not _core._WG_QUEUE and not _core._WG_TARGETS and _core._WG_STATE == [0, 0]
+    g2 = l2.w.grad.double()
+    assert torch.isfinite(g2).all() and float(g2.abs().sum()) > 0
+    for p in (l1.w, l1.b, l2.w, l2.b):
+        p.zero_grad()
+    with tg.autocast():
+        loss2 = (l2(l1(x).relu()) ** 2).mean()
+    loss2.backward()
+    assert torch.isfinite(l1.w.grad).all() and float(l1.w.grad.abs().sum()) > 0
