@@ -100,7 +100,7 @@ def traffic(fetch_dir, write_dir, calib_bytes):
           f"for {calib_bytes:.0f} B each way -> fetch scale {fs:.4f}, write scale {ws:.4f}")
     for k in sorted(f):
         name = k[5:] if k.startswith("void ") else k
-        if k in w and (name.startswith("k_") or k == cal[0]):
+        if k in w and (name.startswith("k_") or "_GLOBAL__N_" in name or k == cal[0]):
             fb, wb = f[k] * 1024.0 * fs, w[k] * 1024.0 * ws
             print(f"traffic {name.replace(' ', '')} {fb + wb:.0f} # fetch {fb:.0f} write {wb:.0f}")
 
