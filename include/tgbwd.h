@@ -52,6 +52,40 @@ int tg_gelu_bwd(int dtype, const void* x, const void* dy, void* dx, int64_t n, i
  * and the xp path (_core.py:1237-1243). */
 int tg_silu_bwd(int dtype, const void* x, const void* dy, void* dx, int64_t n, int accumulate,
                 void* stream);
+/* dx (+)= f'(a) * dy for the other pointwise ops, in the reference closure's order
+ * (float/double data in their own precision, fp16/bf16 in fp32 rounded once).
+ * op: 0 ReLU, a = y: (y > 0) * dy             (_core.py:1149-1157)
+ *     1 LeakyReLU, a = x: (x >= 0 ? 1 : param) * dy (_core.py:1159-1170)
+ *     2 sigmoid, a = y: y * (1 - y) * dy       (_core.py:1262-1272)
+ *     3 tanh, a = y: (1 - y*y) * dy            (_core.py:1274-1282)
+ *     4 exp, a = y: y * dy
+ *     5 log, a = x: dy / x
+ *     6 power x ** param, a = x: (param * x ** (param - 1)) * dy (_core.py:973-981;
+ *       a / b runs as a * b ** -1, _core.py:993-995); x ** e uses 1, sqrt, x, x*x and
+ *       1/x for e = 0, 0.5, 1, 2, -1 as NumPy's power does, pow otherwise
+ *     7 Swish x * sigmoid(param * x), a = x: (s + param*x*s*(1 - s)) * dy with
+ *       s = 1 / (1 + exp(-param*x))               (_core.py:1248-1260) */
+int tg_unary_bwd(int dtype, int op, const void* a, const void* dy, void* dx, int64_t n,
+                 double param, int accumulate, void* stream);
+/* log_softmax backward over the last axis of [rows, cols]:
+ * dx (+)= dy - exp(y) * sum_row(dy) (_core.py:1301-1314). */
+int tg_log_softmax_bwd(int dtype, const void* y, const void* dy, void* dx, int64_t rows,
+                       int64_t cols, int accumulate, void* stream);
+/* max backward with x viewed as [rows, cols] (reduced axes last), r [rows] the
+ * maxima, g [rows] their upstream gradient: dx (+)= (x == r) * g / count(x == r) per
+ * row (_core.py:1115-1132; min is -max(-x), :1134-1135). */
+int tg_max_bwd(int dtype, const void* x, const void* r, const void* g, void* dx, int64_t rows,
+               int64_t cols, int accumulate, void* stream);
+/* Scatter-add of an integer-array / mask __getitem__ (_core.py:918-929, whose
+ * _scatter_add is NumPy's add.at on the CPU path, :890-916): for each of nseg
+ * distinct flat indices target[s], grad[target[s]] += (sum of src[order[j]] for j in
+ * [start[s], start[s+1]), added in j order with the dtype's rounding at every step).
+ * order is a stable sort of the selected elements by flat index (int64 [n]), start
+ * is int64 [nseg + 1], src holds the upstream gradient of the selected elements
+ * (contiguous, grad's dtype).  Deterministic: one thread owns each target. */
+int tg_index_add_sorted(int dtype, void* grad, int64_t nseg, const int64_t* target,
+                        const int64_t* start, const int64_t* order, const void* src,
+                        void* stream);
 /* Forward kernels feeding the above: gelu_forward (_core.py:479-491),
  * silu_forward (_core.py:510-520). */
 int tg_gelu_fwd(int dtype, const void* x, void* y, int64_t n, void* stream);
@@ -345,7 +379,9 @@ int tg_flash_attn_bwd_layout(int dtype, const void* q, const void* k, const void
  * the fp64 matrix cores, softmax and lse (natural log, double, [B,H,Sq]) in double;
  * the backward recomputes P from lse and uses the reference's row term
  * dS = P*(dP - rowsum(P*dP))*scale.  layout as for the _layout forms; o is not read by
- * the backward.  Workspace: tg_flash_attn_f64_workspace bytes (at most 512 MiB). */
+ * the backward.  Workspace: tg_flash_attn_f64_workspace bytes: 2*hc*Sq*Sk doubles for a chunk of hc
+ * heads sized to about 512 MiB, but never less than one head's 2*Sq*Sk doubles (e.g.
+ * 4 GiB at Sq = Sk = 16384). */
 size_t tg_flash_attn_f64_workspace(int64_t B, int64_t H, int64_t Sq, int64_t Sk);
 int tg_flash_attn_fwd_f64(const double* q, const double* k, const double* v, double* o,
                           double* lse, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,

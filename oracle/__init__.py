@@ -32,6 +32,15 @@ How each function is pinned (tests/test_oracle.py):
   cross_entropy_fwd/bwd         torch.nn.functional.cross_entropy autograd
                                 float64 (mean reduction), upstream grad ignored
   embedding_bwd                 np.add.at closed form with repeated indices
+  relu/leaky_relu/swish/sigmoid/tanh/exp/log/pow_bwd
+                                torch autograd float64 of the same op, central
+                                finite differences, and the kinks (relu at 0 -> 0,
+                                leaky at 0 -> 1) by closed form
+  log_softmax_fwd/bwd           torch.log_softmax autograd float64, any axis
+  max_bwd                       torch.amax autograd float64 (ties share the
+                                gradient evenly), axis None / int / keepdims
+  getitem_bwd                   torch index backward (index_put accumulate),
+                                integer arrays with repeats and boolean masks
 No function is left unpinned.
 """
 from .ref_ops import *  # noqa: F401,F403

@@ -13,7 +13,9 @@ __all__ = [
     "matmul_bwd",
     "flash_attention_fwd", "flash_attention_bwd", "adam_step", "GradScalerRef",
     "clip_grad_norm", "cross_entropy_fwd", "cross_entropy_bwd", "embedding_bwd",
-    "mlp_step",
+    "mlp_step", "relu_bwd", "leaky_relu_bwd", "swish_bwd", "sigmoid_bwd", "tanh_bwd",
+    "exp_bwd", "log_bwd", "pow_bwd", "log_softmax_fwd", "log_softmax_bwd", "max_bwd",
+    "getitem_bwd",
 ]
 
 _C0 = 0.7978845608028654  # sqrt(2/pi)
@@ -45,6 +47,79 @@ def silu_bwd(x, dy):
     """dx = dy * s * (1 + x*(1-s)), s = sigmoid(x) (_core.py:522-533, :1237-1243)."""
     s = 1 / (1 + np.exp(-x))
     return dy * (s * (1 + x * (1 - s)))
+
+
+# ---------------------------------------------------------------- other pointwise ops
+def relu_bwd(y, dy):
+    """(out > 0) * g with y = relu(x) (_core.py:1149-1157)."""
+    return (y > 0) * dy
+
+
+def leaky_relu_bwd(x, dy, slope=0.01):
+    """where(x >= 0, 1, slope) * g (_core.py:1159-1170)."""
+    return np.where(x >= 0, 1.0, slope) * dy
+
+
+def swish_bwd(x, dy, beta=1.0):
+    """(s + beta*x*s*(1 - s)) * g, s = 1/(1 + exp(-beta*x)) (_core.py:1248-1260)."""
+    s = 1 / (1 + np.exp(-beta * x))
+    return (s + beta * x * s * (1 - s)) * dy
+
+
+def sigmoid_bwd(y, dy):
+    """out * (1 - out) * g (_core.py:1262-1272)."""
+    return y * (1 - y) * dy
+
+
+def tanh_bwd(y, dy):
+    """(1 - out**2) * g (_core.py:1274-1282)."""
+    return (1 - y ** 2) * dy
+
+
+def exp_bwd(y, dy):
+    """out * g: d/dx exp(x) = exp(x)."""
+    return y * dy
+
+
+def log_bwd(x, dy):
+    """g / x: d/dx log(x) = 1/x."""
+    return dy / x
+
+
+def pow_bwd(x, dy, p):
+    """(p * x**(p - 1)) * g (_core.py:973-981); a / b is a * b**-1 (_core.py:993-995)."""
+    return (p * x ** (p - 1)) * dy
+
+
+def log_softmax_fwd(x, axis=-1):
+    """shifted - log(sum(exp(shifted))) (_core.py:1301-1307)."""
+    sh = x - x.max(axis=axis, keepdims=True)
+    return sh - np.log(np.exp(sh).sum(axis=axis, keepdims=True))
+
+
+def log_softmax_bwd(y, dy, axis=-1):
+    """g - exp(out) * sum(g) (_core.py:1309-1312)."""
+    return dy - np.exp(y) * dy.sum(axis=axis, keepdims=True)
+
+
+def max_bwd(x, dy, axis=None, keepdims=False):
+    """mask * broadcast(g) / count(mask) over the reduced axes (_core.py:1115-1132)."""
+    r = x.max(axis=axis, keepdims=keepdims)
+    if axis is None:
+        mask = x == r
+    else:
+        mask = x == (r if keepdims else np.expand_dims(r, axis))
+    count = mask.sum(axis=axis, keepdims=True)
+    g = np.expand_dims(dy, axis) if (not keepdims and axis is not None) else dy
+    return mask * np.broadcast_to(g, x.shape) / count
+
+
+def getitem_bwd(shape, idx, dy, dtype=np.float64):
+    """zeros; add.at(zeros, idx, g) (_core.py:918-929; the CPU path's _scatter_add is
+    np.add.at, :890-916): repeated indices accumulate in index order."""
+    grad = np.zeros(shape, dtype=dtype)
+    np.add.at(grad, idx, dy)
+    return grad
 
 
 # ---------------------------------------------------------------- softmax

@@ -6,6 +6,9 @@ launches:
         python3 project-tensor_amd/prof_backward.py
     python3 project-tensor_amd/prof_summary.py ranges <dir>
 
+Arguments select the configurations (default C1 C5); "closures" runs one backward
+per op of the pointwise / log_softmax / max / advanced-index closures.
+
 Phases (range names): "<cfg>.forward", "<cfg>.backward" (seed through the last
 gradient closure; for C5 also sync_tied_gradients), "<cfg>.optimizer" (unscale,
 clip, optimizer step).  The device is synchronised at both ends of every range, so
@@ -80,6 +83,33 @@ def c5(tag):
             tr.scaler.update()
 
 
+def closures(tag):
+    """One backward phase per op whose closure runs on tg_unary_bwd,
+    tg_log_softmax_bwd, tg_max_bwd or tg_index_add_sorted (fp32 [256, 1024] input;
+    each loss is a .sum() so the seed and the sum's backward fill are the other
+    kernels in the phase)."""
+    rng = np.random.default_rng(0)
+    xv = (np.abs(rng.standard_normal((256, 1024))) + 0.1).astype(np.float32)
+    bv = (np.abs(rng.standard_normal((256, 1024))) + 0.5).astype(np.float32)
+    idx = rng.integers(0, 256, 4096)
+    ops = {
+        "relu": lambda x, b: x.relu(), "leaky_relu": lambda x, b: x.leaky_relu(0.1),
+        "swish": lambda x, b: x.swish(1.5), "sigmoid": lambda x, b: x.sigmoid(),
+        "tanh": lambda x, b: x.tanh(), "exp": lambda x, b: x.exp(),
+        "log": lambda x, b: x.log(), "pow": lambda x, b: x ** 3.0,
+        "truediv": lambda x, b: x / b, "log_softmax": lambda x, b: x.log_softmax(-1),
+        "max": lambda x, b: x.max(axis=1), "min": lambda x, b: x.min(axis=0),
+        "getitem_array": lambda x, b: x[idx], "getitem_mask": lambda x, b: x[xv > 1.0],
+    }
+    for name, f in ops.items():
+        for ranged in (False, True):
+            x = tg.Tensor(xv)
+            b = tg.Tensor(bv)
+            loss = f(x, b).sum()
+            with (_phase(f"{tag}.{name}.backward") if ranged else _null()):
+                loss.backward()
+
+
 class _null:
     def __enter__(self):
         return None
@@ -90,8 +120,13 @@ class _null:
 
 def main():
     _lib.ensure_device(0)
-    c1("C1")
-    c5("C5")
+    which = sys.argv[1:] or ["C1", "C5"]
+    if "C1" in which:
+        c1("C1")
+    if "C5" in which:
+        c5("C5")
+    if "closures" in which:
+        closures("closures")
     torch.cuda.synchronize()
     print("prof_backward: done", flush=True)
 

@@ -512,10 +512,9 @@ class Tensor:
         assert isinstance(other, (int, float)), "only supporting int/float powers"
         out = self._out(self.data ** other, (self,), f"**{other}")
         if out._requires_grad:
-            def _backward():
-                if self._has_grad():
-                    self._accumulate((other * self.data ** (other - 1)) * out._grad_out(), True)
-            out._backward = _backward
+            # (other * x ** (other - 1)) * g (_core.py:973-981) on tg_unary_bwd; a / b
+            # reaches here as a * b ** -1 (_core.py:993-995)
+            out._backward = _unary_backward(self, out, "pow", False, float(other))
         return out
 
     def __neg__(self):
@@ -593,15 +592,33 @@ class Tensor:
         out = self._out(r, (self,), "max")
         if out._requires_grad:
             def _backward():
+                # mask * g / count(mask) over the reduced axes (_core.py:1115-1132) on
+                # tg_max_bwd: x is viewed as [kept, reduced] (the reduced axes moved
+                # last by the strided copy kernel when they are not already last)
                 if not self._has_grad():
                     return
-                od = r if (keepdims or axis is None) else r.unsqueeze(axis)
-                mask = (self.data == od).to(self.data.dtype)
-                cnt = mask.sum() if axis is None else mask.sum(dim=axis, keepdim=True)
-                g = out._grad_out()
-                if not keepdims and axis is not None:
-                    g = g.unsqueeze(axis)
-                self._accumulate(mask * g.expand(self.data.shape) / cnt, True)
+                dt = self.data.dtype
+                shape = tuple(self.data.shape)
+                nd = len(shape)
+                if axis is None:
+                    red = tuple(range(nd))
+                else:
+                    red = tuple(sorted(a % nd for a in ((axis,) if isinstance(axis, int)
+                                                        else axis)))
+                perm = [d for d in range(nd) if d not in red] + list(red)
+                outer = int(np.prod([shape[d] for d in perm[:nd - len(red)]]))
+                nred = int(np.prod([shape[d] for d in red]))
+                ident = perm == list(range(nd))
+                x2 = _as(self.data if ident else self.data.permute(perm), dt).reshape(outer, nred)
+                r2 = _as(r, dt).reshape(outer)
+                g2 = _as(out._grad_out(), dt).reshape(outer)
+                if ident:
+                    buf, acc = self._grad_target()
+                    L.max_bwd(x2, r2, g2, buf.reshape(outer, nred), acc)
+                else:
+                    dx2 = L.max_bwd(x2, r2, g2, torch.empty_like(x2), False)
+                    inv = [perm.index(d) for d in range(nd)]
+                    self._accumulate(dx2.reshape([shape[d] for d in perm]).permute(inv), True)
             out._backward = _backward
         return out
 
@@ -625,22 +642,15 @@ class Tensor:
 
     def relu(self):
         out = self._out(torch.clamp_min(self.data, 0), (self,), "ReLU")
-        if out._requires_grad:
-            def _backward():
-                if self._has_grad():
-                    self._accumulate((out.data > 0).to(self.data.dtype) * out._grad_out(), True)
-            out._backward = _backward
+        if out._requires_grad:  # (y > 0) * g (_core.py:1149-1157)
+            out._backward = _unary_backward(self, out, "relu", True)
         return out
 
     def leaky_relu(self, negative_slope=0.01):
         out = self._out(torch.where(self.data >= 0, self.data, negative_slope * self.data),
                         (self,), "LeakyReLU")
-        if out._requires_grad:
-            def _backward():
-                if self._has_grad():
-                    m = torch.where(self.data >= 0, 1.0, negative_slope).to(self.data.dtype)
-                    self._accumulate(m * out._grad_out(), True)
-            out._backward = _backward
+        if out._requires_grad:  # where(x >= 0, 1, slope) * g (_core.py:1159-1170)
+            out._backward = _unary_backward(self, out, "leaky_relu", False, float(negative_slope))
         return out
 
     def swish(self, beta=1.0):
@@ -648,48 +658,32 @@ class Tensor:
             return self.silu()
         s = torch.sigmoid(beta * self.data)
         out = self._out(self.data * s, (self,), "Swish")
-        if out._requires_grad:
-            def _backward():
-                if self._has_grad():
-                    sv = torch.sigmoid(beta * self.data)
-                    self._accumulate((sv + beta * self.data * sv * (1 - sv)) * out._grad_out(), True)
-            out._backward = _backward
+        if out._requires_grad:  # (s + beta*x*s*(1 - s)) * g (_core.py:1248-1260)
+            out._backward = _unary_backward(self, out, "swish", False, float(beta))
         return out
 
     def sigmoid(self):
         out = self._out(torch.sigmoid(self.data), (self,), "sigmoid")
-        if out._requires_grad:
-            def _backward():
-                if self._has_grad():
-                    self._accumulate(out.data * (1 - out.data) * out._grad_out(), True)
-            out._backward = _backward
+        if out._requires_grad:  # y * (1 - y) * g (_core.py:1262-1272)
+            out._backward = _unary_backward(self, out, "sigmoid", True)
         return out
 
     def tanh(self):
         out = self._out(torch.tanh(self.data), (self,), "tanh")
-        if out._requires_grad:
-            def _backward():
-                if self._has_grad():
-                    self._accumulate((1 - out.data ** 2) * out._grad_out(), True)
-            out._backward = _backward
+        if out._requires_grad:  # (1 - y**2) * g (_core.py:1274-1282)
+            out._backward = _unary_backward(self, out, "tanh", True)
         return out
 
     def exp(self):
         out = self._out(torch.exp(self.data), (self,), "exp")
-        if out._requires_grad:
-            def _backward():
-                if self._has_grad():
-                    self._accumulate(out.data * out._grad_out(), True)
-            out._backward = _backward
+        if out._requires_grad:  # y * g
+            out._backward = _unary_backward(self, out, "exp", True)
         return out
 
     def log(self):
         out = self._out(torch.log(self.data), (self,), "log")
-        if out._requires_grad:
-            def _backward():
-                if self._has_grad():
-                    self._accumulate(out._grad_out() / self.data, True)
-            out._backward = _backward
+        if out._requires_grad:  # g / x
+            out._backward = _unary_backward(self, out, "log", False)
         return out
 
     def softmax(self, axis=-1):
@@ -724,11 +718,26 @@ class Tensor:
         r = torch.log_softmax(self.data.float(), dim=axis).to(self.data.dtype)
         out = self._out(r, (self,), "log_softmax")
         if out._requires_grad:
+            nd = self.data.dim()
+            ax = axis % nd if nd else 0
+            moved = nd > 0 and ax != nd - 1
+
             def _backward():
-                if self._has_grad():
-                    g = out._grad_out()
-                    sm = torch.exp(out.data)
-                    self._accumulate(g - sm * g.sum(dim=axis, keepdim=True), True)
+                # g - exp(y) * sum(g, axis) (_core.py:1301-1314) on tg_log_softmax_bwd;
+                # other axes are moved last around the kernel
+                if not self._has_grad():
+                    return
+                dt = self.data.dtype
+                yy = out.data.movedim(ax, -1) if moved else out.data
+                g = out._grad_out()
+                yy = _as(yy, dt)
+                g = _as(g.movedim(ax, -1) if moved else g, dt)
+                if moved:
+                    dx = L.log_softmax_bwd(yy, g, torch.empty_like(yy), False)
+                    self._accumulate(dx.movedim(-1, ax), True)
+                else:
+                    buf, acc = self._grad_target()
+                    L.log_softmax_bwd(yy, g, buf, acc)
             out._backward = _backward
         return out
 
@@ -818,6 +827,13 @@ class Tensor:
         idx_t = _index_to_torch(idx)
         out = self._out(self.data[idx_t], (self,), "getitem")
         if out._requires_grad:
+            basic = _basic_index(idx_t)
+            if not basic:
+                # integer-array / mask indexing: the flat source index of every selected
+                # element, stably sorted, with the segment of each distinct target; the
+                # backward's scatter-add then needs no index arithmetic
+                seg = _scatter_segments(self.data, idx_t)
+
             def _backward():
                 if not self._has_grad():
                     return
@@ -825,14 +841,12 @@ class Tensor:
                 buf, acc = self._grad_target()
                 if not acc:
                     _fill(buf, 0.0)
-                if _basic_index(idx_t):
+                if basic:
                     # a view of the gradient buffer: one strided add into it
                     L.broadcast_mul_sum(buf[idx_t], g, accumulate=True)
-                else:  # integer-array / mask indexing: torch's indexing backward
-                    leaf = torch.zeros_like(self.data, requires_grad=True)
-                    with torch.enable_grad():
-                        leaf[idx_t].backward(_as(g, leaf.dtype))
-                    L.broadcast_mul_sum(buf, leaf.grad, accumulate=True)
+                else:
+                    # grad += add.at(zeros, idx, g) (_core.py:918-929) in add.at's order
+                    L.index_add_sorted(buf, *seg, _as(g, buf.dtype).reshape(-1))
             out._backward = _backward
         return out
 
@@ -886,6 +900,10 @@ class Tensor:
                 g = torch.as_tensor(np.asarray(g))
             if g.device.type != "cuda":
                 g = g.to(device="cuda")
+            # the reference takes xp.asarray(gradient, dtype=self.dtype): an integer or
+            # differently-typed seed is cast to the tensor's dtype first
+            if g.dtype != self.data.dtype:
+                g = g.to(dtype=self.data.dtype)
             if not self._has_grad():
                 self._g = self._new_buf()
                 _copy_into(self._g, g)
@@ -951,12 +969,18 @@ def _scalar_like(v, ref):
         dt = ref.dtype if ref.is_floating_point() or isinstance(v, int) else torch.float32
         if isinstance(v, float) and not ref.is_floating_point():
             dt = torch.float32
-        # made in a wide dtype, then cast: a value outside dt's range becomes inf (or
-        # wraps) as the weak-scalar cast does (65536.0 as fp16 is inf), where a fill in
-        # dt itself would raise
+        # made in a wide dtype, then cast: a float outside dt's range becomes inf as the
+        # weak-scalar cast does (65536.0 as fp16 is inf), where a fill in dt itself
+        # would raise; an out-of-range int raises (checked below)
         wide = torch.float64 if dt.is_floating_point else torch.int64
         if dt == torch.bool:
             wide = torch.bool
+        elif isinstance(v, int) and not isinstance(v, bool) and not dt.is_floating_point:
+            # NumPy 2's weak-scalar rule: a Python int outside the integer dtype's range
+            # raises instead of wrapping
+            info = torch.iinfo(dt)
+            if v < info.min or v > info.max:
+                raise OverflowError(f"Python integer {v} out of bounds for {dt}")
         return torch.full((), v, dtype=wide, device="cuda").to(dt)
     return L.to_device(np.asarray(v))
 
@@ -1021,6 +1045,32 @@ def _as(t, dtype):
     out = torch.empty(t.shape, dtype=dtype, device=t.device)
     _copy_into(out, t)
     return out
+
+
+def _unary_backward(x, out, op, use_y, param=0.0):
+    """Closure for out = op(x): x.grad (+)= op'(.) * out.grad on tg_unary_bwd, with
+    the op's input (use_y False) or output (True) as the kernel's operand."""
+    def _backward():
+        if not x._has_grad():
+            return
+        dt = x.data.dtype
+        a = _as(out.data if use_y else x.data, dt)
+        g = _as(out._grad_out(), dt)
+        buf, acc = x._grad_target()
+        L.unary_bwd(op, a, g, buf, acc, param)
+    return _backward
+
+
+def _scatter_segments(data, idx_t):
+    """(targets, starts, order) of an advanced index into `data`: the flat indices the
+    selected elements come from, grouped by target in a stable sort (so each group
+    keeps the selection order NumPy's add.at adds in)."""
+    lin = torch.arange(data.numel(), device=data.device).reshape(data.shape)[idx_t].reshape(-1)
+    srt, order = torch.sort(lin, stable=True)
+    targets, counts = torch.unique_consecutive(srt, return_counts=True)
+    starts = torch.zeros(targets.numel() + 1, dtype=torch.int64, device=data.device)
+    torch.cumsum(counts, 0, out=starts[1:])
+    return targets.contiguous(), starts, order.contiguous()
 
 
 def _fill(buf, value):

@@ -40,6 +40,10 @@ SIGNATURES = {
     "tg_gelu_bwd": (_i32, [_i32, _vp, _vp, _vp, _i64, _i32, _vp]),
     "tg_silu_bwd": (_i32, [_i32, _vp, _vp, _vp, _i64, _i32, _vp]),
     "tg_gelu_fwd": (_i32, [_i32, _vp, _vp, _i64, _vp]),
+    "tg_unary_bwd": (_i32, [_i32, _i32, _vp, _vp, _vp, _i64, _f64, _i32, _vp]),
+    "tg_log_softmax_bwd": (_i32, [_i32, _vp, _vp, _vp, _i64, _i64, _i32, _vp]),
+    "tg_index_add_sorted": (_i32, [_i32, _vp, _i64, _vp, _vp, _vp, _vp, _vp]),
+    "tg_max_bwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _vp]),
     "tg_silu_fwd": (_i32, [_i32, _vp, _vp, _i64, _vp]),
     "tg_axpby": (_i32, [_i32, _vp, _i32, _vp, _i64, _f32, _f32, _vp]),
     "tg_axpbyz": (_i32, [_i32, _vp, _i32, _vp, _vp, _i64, _f32, _f32, _vp]),
@@ -267,6 +271,73 @@ def act_bwd(kind, x, dy, dx, accumulate):
     _check(f"tg_{kind}_bwd", fn(dtype_code(x), ptr(x), ptr(dy), ptr(dx), x.numel(),
                                 int(bool(accumulate)), stream_handle()))
     return dx
+
+
+UNARY_OPS = {"relu": 0, "leaky_relu": 1, "sigmoid": 2, "tanh": 3, "exp": 4, "log": 5,
+             "pow": 6, "swish": 7}
+
+
+def unary_bwd(op, a, dy, dx, accumulate, param=0.0):
+    """dx (+)= f'(a) * dy (tg_unary_bwd); a is the op's input x or output y as
+    include/tgbwd.h lists per op; param is the LeakyReLU slope or the exponent."""
+    for n, t in (("a", a), ("dy", dy), ("dx", dx)):
+        _dev(t, n)
+    _same(f"{op}_bwd", a, dy, dx)
+    ensure_device(a.device.index)
+    _check("tg_unary_bwd", load().tg_unary_bwd(dtype_code(a), UNARY_OPS[op], ptr(a), ptr(dy),
+                                               ptr(dx), a.numel(), float(param),
+                                               int(bool(accumulate)), stream_handle()))
+    return dx
+
+
+def log_softmax_bwd(y, dy, dx, accumulate):
+    """dx (+)= dy - exp(y) * sum_row(dy) over the last axis (tg_log_softmax_bwd)."""
+    for n, t in (("y", y), ("dy", dy), ("dx", dx)):
+        _dev(t, n)
+    _same("log_softmax_bwd", y, dy, dx)
+    rows, cols = _rows_cols(y)
+    ensure_device(y.device.index)
+    _check("tg_log_softmax_bwd",
+           load().tg_log_softmax_bwd(dtype_code(y), ptr(y), ptr(dy), ptr(dx), rows, cols,
+                                     int(bool(accumulate)), stream_handle()))
+    return dx
+
+
+def max_bwd(x, r, g, dx, accumulate):
+    """dx (+)= (x == r) * g / count per row of x [rows, cols] (tg_max_bwd); r and g
+    hold one value per row."""
+    for n, t in (("x", x), ("r", r), ("g", g), ("dx", dx)):
+        _dev(t, n)
+    _same("max_bwd", x, dx)
+    _same("max_bwd", r, g)
+    rows, cols = _rows_cols(x)
+    if r.numel() != rows or r.dtype != x.dtype:
+        raise ValueError("max_bwd: one maximum per row of x's dtype expected")
+    ensure_device(x.device.index)
+    _check("tg_max_bwd", load().tg_max_bwd(dtype_code(x), ptr(x), ptr(r), ptr(g), ptr(dx), rows,
+                                           cols, int(bool(accumulate)), stream_handle()))
+    return dx
+
+
+def index_add_sorted(grad, target, start, order, src):
+    """grad.flat[target[s]] += in-order sum of src.flat[order[start[s]:start[s+1]]]
+    (tg_index_add_sorted): the scatter-add of an advanced-index __getitem__."""
+    _dev(grad, "grad")
+    _dev(src, "src")
+    for n, t in (("target", target), ("start", start), ("order", order)):
+        _dev(t, n)
+        if t.dtype != torch.int64:
+            raise TypeError(f"index_add_sorted: {n} must be int64")
+    if src.dtype != grad.dtype:
+        raise ValueError("index_add_sorted: src and grad dtypes differ")
+    nseg = target.numel()
+    if start.numel() != nseg + 1 or order.numel() != src.numel():
+        raise ValueError("index_add_sorted: inconsistent segment arrays")
+    ensure_device(grad.device.index)
+    _check("tg_index_add_sorted",
+           load().tg_index_add_sorted(dtype_code(grad), ptr(grad), nseg, ptr(target),
+                                      ptr(start), ptr(order), ptr(src), stream_handle()))
+    return grad
 
 
 def act_fwd(kind, x, y=None):

@@ -500,13 +500,20 @@ class CrossEntropyLoss(Module):
     65504, and so would its upstream gradient) and reads the upstream gradient back to
     the host once per backward."""
 
-    def __init__(self, reduction="mean", label_smoothing=0.0, strict_chain_rule=False):
+    def __init__(self, reduction="mean", label_smoothing=0.0, strict_chain_rule=False,
+                 grad_in_forward=True):
         super().__init__()
         if strict_chain_rule and reduction not in ("mean", "sum"):
             raise ValueError("strict_chain_rule needs reduction 'mean' or 'sum'")
         self.reduction = reduction
         self.label_smoothing = label_smoothing
         self.strict_chain_rule = bool(strict_chain_rule)
+        # One-pass mode (default): when grad mode is on and the logits require grad, the
+        # forward also writes the logits' gradient (one more logits-sized write, and a
+        # logits-sized buffer held by the loss graph until its backward runs or the
+        # graph is dropped: 512 MiB at [8192, 32000] fp16).  False keeps the
+        # reference's order: the gradient is formed only inside backward.
+        self.grad_in_forward = bool(grad_in_forward)
 
     def __call__(self, logits, targets):
         ld = logits.data
@@ -535,8 +542,8 @@ class CrossEntropyLoss(Module):
         smoothing = self.label_smoothing
         # The gradient does not depend on the upstream one (the reference's rule): when
         # a backward may follow, it is formed here, from the same read of the logits.
-        pre = (not strict and smoothing == 0 and cfg._grad_enabled and logits._requires_grad
-               and L.cross_entropy_fwd_grad_ok(ldc))
+        pre = (self.grad_in_forward and not strict and smoothing == 0 and cfg._grad_enabled
+               and logits._requires_grad and L.cross_entropy_fwd_grad_ok(ldc))
         grad = None
         if pre:
             lse, loss, grad = L.cross_entropy_fwd_grad(ldc, tg, scale)

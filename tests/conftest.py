@@ -65,3 +65,9 @@ def cuda():
     from tensor_gpu_v2 import _lib
     _lib.ensure_device(0)
     return torch.device("cuda", 0)
+
+
+@pytest.fixture
+def tg(cuda):
+    import tensor_gpu_v2
+    return tensor_gpu_v2

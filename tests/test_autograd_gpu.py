@@ -147,6 +147,25 @@ def test_backward_seed_semantics(tg):
     assert np.allclose(x.grad.cpu().numpy(), [4, 6, 8])
 
 
+def test_backward_integer_seed_is_cast(tg):
+    """An integer seed (Python int, int array, int tensor) is cast to the tensor's
+    dtype first, as xp.asarray(gradient, dtype=self.dtype) does in the reference
+    (_core.py:1447-1454): fresh grad and accumulation into an existing one."""
+    for seed in (2, np.array([2, 2, 2], np.int64), torch.tensor([2, 2, 2], dtype=torch.int32)):
+        x = tg.Tensor(np.array([1.0, 2.0, 3.0], np.float32))
+        y = x * 3.0
+        y.backward(seed)
+        assert y.grad.dtype == torch.float32
+        assert np.allclose(x.grad.cpu().numpy(), [6, 6, 6])
+        y.backward(seed)  # existing grad: the cast seed is added
+        assert np.allclose(y.grad.cpu().numpy(), [4, 4, 4])
+    h = tg.Tensor(np.array([1.0, -1.0], np.float16))
+    z = h * 2.0
+    z.backward(np.array([1, 3], np.int64))
+    assert z.grad.dtype == torch.float16
+    assert np.allclose(h.grad.float().cpu().numpy(), [2, 6])
+
+
 # ------------------------------------------------------------------ modules
 @pytest.mark.parametrize("shape", [(4, 6, 64), (16, 1024), (3, 100)])
 def test_layernorm_module(tg, shape):

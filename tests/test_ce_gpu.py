@@ -136,3 +136,21 @@ def test_ce_module_gradient_formed_in_forward(cuda):
     with tg.no_grad():
         loss = tg.CrossEntropyLoss()(x, y_np)
     assert loss.data.numel() == 1
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16])
+def test_ce_grad_in_forward_switch(cuda, tg, dt):
+    """CrossEntropyLoss(grad_in_forward=False) forms the gradient only inside
+    backward (the reference's order) and gives the same loss and gradient bit for bit
+    as the default one-pass mode."""
+    rng = np.random.default_rng(3)
+    x_np = (3 * rng.standard_normal((64, 3000))).astype(np.float32)
+    y_np = rng.integers(0, 3000, 64)
+    out = []
+    for gf in (True, False):
+        x = tg.Tensor(torch.as_tensor(x_np).to(dt).cuda())
+        loss = tg.CrossEntropyLoss(grad_in_forward=gf)(x, y_np)
+        loss.backward()
+        out.append((loss.data.float().cpu(), x.grad.float().cpu()))
+    assert torch.equal(out[0][0], out[1][0])
+    assert torch.equal(out[0][1], out[1][1])

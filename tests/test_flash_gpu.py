@@ -105,6 +105,30 @@ def test_flash_accumulate(cuda):
         assert_close(b, 2 * f64(a), RTOL_F16, "accumulate doubles")
 
 
+def assert_close_rows(actual, expected, rtol, what):
+    """assert_close with the absolute term taken from the larger of the tensor's rms
+    and the element's own row's rms (a row = one query or key of one head).  Each
+    gradient row is its own reduction over up to S products whose fp16 roundings (dS
+    and P enter the products as fp16, as in every fp16 FlashAttention backward) scale
+    with that row's terms: under causal masking the first keys collect ~S large terms
+    that cancel to a small result, so their error budget is the row's magnitude, not
+    the head's average.  Never stricter than assert_close, looser only on rows whose
+    own rms exceeds the tensor's."""
+    a = actual.detach().double()
+    e = expected.detach().double().to(a.device)
+    assert a.shape == e.shape, what
+    assert bool(torch.isfinite(a).all()), f"{what}: non-finite values"
+    scale = torch.maximum(e.pow(2).mean().sqrt(), e.pow(2).mean(-1, keepdim=True).sqrt())
+    err = (a - e).abs()
+    lim = rtol * e.abs() + rtol * scale
+    bad = err > lim
+    if bool(bad.any()):
+        i = tuple(int(v) for v in torch.nonzero((err - lim) == (err - lim).max())[0])
+        raise AssertionError(f"{what}: {int(bad.sum())}/{a.numel()} elements outside "
+                             f"rtol={rtol} (worst at {i}: got {float(a[i])!r}, want "
+                             f"{float(e[i])!r}, bound {float(lim[i]):.3e})")
+
+
 def _head_invariants(q, k, v, o, do, dq, dk, dv):
     """Per-head identities of attention's gradients, in float64 on the device, for
     every (b, h) at once.  With P's rows summing to 1 and dS = P*(dP - rowsum):
@@ -133,10 +157,12 @@ def _head_invariants(q, k, v, o, do, dq, dk, dv):
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("causal", [False, True])
 def test_flash_full_size_all_heads(cuda, D, causal):
-    """C4 shape B=8, H=16, S=2048.  All 128 (b, h) heads are checked through the
-    per-head identities; six heads spread over the dispatch's head groups (groups of
-    8 heads per XCD range: first, last of group 0, first of group 1, both sides of
-    the middle, last) are checked element by element against the oracle."""
+    """C4 shape B=8, H=16, S=2048.  All 128 (b, h) heads are checked element by
+    element against float64 torch autograd of softmax(Q K^T s + mask) V (run on the
+    device, one batch of 16 heads at a time; rtol 1e-2 with the row-scaled absolute
+    term of assert_close_rows) and through the per-head identities at the fp16 bar; six heads spread over the dispatch's head groups (groups of 8 heads
+    per XCD range: first, last of group 0, first of group 1, both sides of the
+    middle, last) are also checked against the NumPy oracle."""
     B, H, S = 8, 16, 2048
     print(f"C4 full size D={D} causal={causal}", flush=True)
     q, k, v, do = (rnd((B, H, S, D), torch.float16, 10 + s) for s in range(4))
@@ -144,7 +170,21 @@ def test_flash_full_size_all_heads(cuda, D, causal):
     inv = _head_invariants(q, k, v, o, do, dq, dk, dv)
     print("identity errors:", {n: f"{x:.2e}" for n, x in inv.items()}, flush=True)
     for n, x in inv.items():
-        assert x < 2e-2, f"{n}: {x:.3e}"
+        assert x < RTOL_F16, f"{n}: {x:.3e}"
+    scale = D ** -0.5
+    for b in range(B):
+        qd, kd, vd = (t[b].double().requires_grad_() for t in (q, k, v))
+        sc = qd @ kd.transpose(-1, -2) * scale
+        if causal:
+            sc = sc.masked_fill(torch.ones(S, S, dtype=torch.bool, device=sc.device).triu(1),
+                                float("-inf"))
+        od = torch.softmax(sc, -1) @ vd
+        od.backward(do[b].double())
+        assert_close_rows(o[b], od.detach(), RTOL_F16, f"O batch {b}")
+        assert_close_rows(dq[b], qd.grad, RTOL_F16, f"dQ batch {b}")
+        assert_close_rows(dk[b], kd.grad, RTOL_F16, f"dK batch {b}")
+        assert_close_rows(dv[b], vd.grad, RTOL_F16, f"dV batch {b}")
+        del qd, kd, vd, sc, od
     for flat in (0, 7, 8, 63, 64, 127):
         b, hh = divmod(flat, H)
         sl = (slice(b, b + 1), slice(hh, hh + 1))
@@ -245,6 +285,7 @@ def test_flash_many_heads_chunked(cuda):
         assert_close(o[sl], oo, RTOL_F32_MM, f"O b={b}")
         rq, rk, rv = O.flash_attention_bwd(f64(q[sl]), f64(k[sl]), f64(v[sl]), f64(do[sl]), False)
         assert_close(dq[sl], rq, RTOL_F32_MM, f"dQ b={b}")
+        assert_close(dk[sl], rk, RTOL_F32_MM, f"dK b={b}")
         assert_close(dv[sl], rv, RTOL_F32_MM, f"dV b={b}")
 
 

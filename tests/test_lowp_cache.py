@@ -175,3 +175,17 @@ def test_cross_entropy_strict_chain_rule_needs_scalar_loss():
         tg.CrossEntropyLoss(reduction="none", strict_chain_rule=True)
     assert tg.CrossEntropyLoss(strict_chain_rule=True).strict_chain_rule
     assert not tg.CrossEntropyLoss().strict_chain_rule
+
+
+def test_scalar_like_int_out_of_range_raises():
+    """A Python int outside an integer tensor's dtype raises OverflowError, as NumPy 2's
+    weak-scalar rule does, instead of wrapping (checked before any device work)."""
+    import torch
+    from tensor_gpu_v2._core import _scalar_like
+    ref = torch.zeros(2, dtype=torch.int32)
+    with pytest.raises(OverflowError, match="out of bounds"):
+        _scalar_like(2 ** 40, ref)
+    with pytest.raises(OverflowError, match="out of bounds"):
+        _scalar_like(-(2 ** 31) - 1, ref)
+    with pytest.raises(OverflowError):
+        _scalar_like(300, torch.zeros(2, dtype=torch.uint8))

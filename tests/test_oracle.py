@@ -342,3 +342,91 @@ def test_mlp_step_vs_torch():
     opt.step()
     for name, t in zip(("w1", "b1", "w2", "b2"), ts):
         close(r[name], t.detach().numpy(), 1e-9)
+
+
+# ------------------------------------------------------------------ other pointwise ops
+_UNARY = {
+    # name: (torch forward, oracle backward taking (x, y, dy), domain)
+    "relu": (torch.relu, lambda x, y, dy: O.relu_bwd(y, dy), "any"),
+    "leaky_relu": (lambda t: torch.nn.functional.leaky_relu(t, 0.2),
+                   lambda x, y, dy: O.leaky_relu_bwd(x, dy, 0.2), "any"),
+    "swish": (lambda t: t * torch.sigmoid(1.7 * t), lambda x, y, dy: O.swish_bwd(x, dy, 1.7), "any"),
+    "sigmoid": (torch.sigmoid, lambda x, y, dy: O.sigmoid_bwd(y, dy), "any"),
+    "tanh": (torch.tanh, lambda x, y, dy: O.tanh_bwd(y, dy), "any"),
+    "exp": (torch.exp, lambda x, y, dy: O.exp_bwd(y, dy), "any"),
+    "log": (torch.log, lambda x, y, dy: O.log_bwd(x, dy), "pos"),
+    "pow3": (lambda t: t ** 3, lambda x, y, dy: O.pow_bwd(x, dy, 3), "any"),
+    "pow-1": (lambda t: t ** -1, lambda x, y, dy: O.pow_bwd(x, dy, -1), "pos"),
+    "pow0.5": (lambda t: t ** 0.5, lambda x, y, dy: O.pow_bwd(x, dy, 0.5), "pos"),
+    "pow2.7": (lambda t: t ** 2.7, lambda x, y, dy: O.pow_bwd(x, dy, 2.7), "pos"),
+}
+
+
+@pytest.mark.parametrize("name", sorted(_UNARY))
+def test_unary_bwd_vs_torch_and_finite_differences(name):
+    fwd, bwd, dom = _UNARY[name]
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal(3000) * 2
+    if dom == "pos":
+        x = np.abs(x) + 0.1
+    x[np.abs(x) < 1e-3] = 0.5  # keep finite differences away from the kinks
+    dy = rng.standard_normal(3000)
+    xt = tt(x)
+    y = fwd(xt)
+    y.backward(torch.tensor(dy))
+    got = bwd(x, y.detach().numpy(), dy)
+    close(got, xt.grad.numpy(), 1e-12)
+    h = 1e-6
+    with torch.no_grad():
+        fd = (fwd(tt(x + h, False)) - fwd(tt(x - h, False))).numpy() / (2 * h) * dy
+    close(got, fd, 1e-6)
+
+
+def test_unary_bwd_kinks_and_quotient():
+    # relu at 0: (out > 0) is False -> 0; leaky at 0: x >= 0 -> 1 (the reference's
+    # choices at the kinks, which differ from torch's leaky_relu at exactly 0)
+    close(O.relu_bwd(np.array([0.0, 2.0, -1.0]), np.ones(3)), [0.0, 1.0, 0.0])
+    close(O.leaky_relu_bwd(np.array([0.0, -2.0]), np.ones(2), 0.1), [1.0, 0.1])
+    # a / b = a * b ** -1: d/db = -a / b^2
+    b = np.array([2.0, -4.0])
+    close(O.pow_bwd(b, np.array([3.0, 3.0]), -1), [-0.75, -0.1875])
+
+
+@pytest.mark.parametrize("axis", [-1, 0, 1])
+def test_log_softmax_vs_torch(axis):
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((13, 7, 33)) * 3
+    dy = rng.standard_normal((13, 7, 33))
+    xt = tt(x)
+    y = torch.log_softmax(xt, axis)
+    y.backward(torch.tensor(dy))
+    yo = O.log_softmax_fwd(x, axis)
+    close(yo, y.detach().numpy())
+    close(O.log_softmax_bwd(yo, dy, axis), xt.grad.numpy())
+
+
+@pytest.mark.parametrize("axis,keepdims", [(None, False), (0, False), (1, True), (-1, False),
+                                           ((0, 2), False)])
+def test_max_bwd_vs_torch_with_ties(axis, keepdims):
+    rng = np.random.default_rng(9)
+    x = rng.integers(0, 4, (6, 5, 7)).astype(np.float64)  # many ties
+    xt = tt(x)
+    r = torch.amax(xt) if axis is None else torch.amax(xt, dim=axis, keepdim=keepdims)
+    dy = rng.standard_normal(tuple(r.shape))
+    r.backward(torch.tensor(dy))
+    close(O.max_bwd(x, dy, axis, keepdims), xt.grad.numpy())
+
+
+def test_getitem_bwd_vs_torch_repeats_and_masks():
+    rng = np.random.default_rng(10)
+    x = rng.standard_normal((9, 4))
+    for idx in (np.array([3, 1, 3, 3, 0]), (np.array([0, 2, 2]), np.array([1, 3, 1])),
+                x > 0.3, (slice(None), np.array([2, 2, 0]))):
+        xt = tt(x)
+        sel = xt[tuple(torch.as_tensor(i) if isinstance(i, np.ndarray) else i
+                       for i in idx) if isinstance(idx, tuple) else torch.as_tensor(idx)]
+        dy = rng.standard_normal(tuple(sel.shape))
+        sel.backward(torch.tensor(dy))
+        close(O.getitem_bwd(x.shape, idx, dy), xt.grad.numpy())
+    # add.at with a repeated index: the closed form
+    close(O.getitem_bwd((3,), np.array([1, 1, 1]), np.array([1.0, 2.0, 4.0])), [0, 7, 0])
