@@ -403,6 +403,26 @@ def _op_tied(torch, L, g):
     return Timed("tied_grad_sync", run, 3 * V * dim * 4, "GB/s", HBM_PEAK_GBS)
 
 
+def _copy_floors(torch, L, nbytes):
+    """Same-box floors of a memory-bound op: a plain copy moving the op's algorithmic
+    byte count (half read, half written) in one launch, by libtgbwd's tg_axpby with
+    beta 0 (read x, write y, 16-byte vectors) and by a device-to-device hipMemcpy
+    (ROCm's blit kernel, through torch's copy_).  At the component sizes a launch's
+    ramp-up and drain are a visible share of its time, so the faster of the two is
+    the ceiling a single kernel of that size reaches on this box, not 8 TB/s."""
+    n = max(1, nbytes // 8)
+    x = torch.ones(n, device="cuda")
+    y = torch.empty_like(x)
+
+    def axpby():
+        L.axpby(x, y, 1.0, 0.0)
+
+    def memcpy():
+        y.copy_(x)
+    return [Timed("copy_axpby", axpby, n * 8, "GB/s", HBM_PEAK_GBS),
+            Timed("copy_memcpy", memcpy, n * 8, "GB/s", HBM_PEAK_GBS)]
+
+
 def component_ops(torch, L, only):
     """Other configurations, each built in its own scope on HBM-resident inputs."""
     g = torch.Generator(device="cuda").manual_seed(1)
@@ -733,6 +753,19 @@ def main():
                 op.run(True)
             torch.cuda.synchronize()
             comps[op.name] = op.summary()
+            if op.unit == "GB/s":
+                best = None
+                for fl in _copy_floors(torch, L, op.work):
+                    for _ in range(max(1, a.warmup)):
+                        fl.run(False)
+                    for _ in range(max(3, a.steps // 2) + 1):
+                        fl.run(True)
+                    torch.cuda.synchronize()
+                    if best is None or fl.avg_ms() < best[0]:
+                        best = (fl.avg_ms(), fl.name)
+                comps[op.name]["copy_floor_ms"] = round(best[0], 5)
+                comps[op.name]["copy_floor_kernel"] = best[1]
+                comps[op.name]["frac_of_copy_floor"] = round(best[0] / comps[op.name]["ms"], 4)
             del op
             torch.cuda.empty_cache()
 

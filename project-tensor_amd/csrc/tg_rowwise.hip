@@ -418,6 +418,8 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_reg(
     float mu, rs;
   };
   constexpr bool kPreO = ACC && VPT <= 4;  // wider rows load the old dx late (no spill)
+  // rows in flight per group: 2 where the registers allow (measured: 3 and 4 are slower
+  // on the fp16 [8192, 1024] shape, 4 by a fifth)
   constexpr int kDepth = (ACC ? VPT <= 2 : VPT <= 4) ? 2 : 1;
   auto fetch = [&](int64_t it, RowBuf& b) {
     const int64_t row = it * stride + (int64_t)blockIdx.x * G + grp;
@@ -485,26 +487,20 @@ __global__ __launch_bounds__(kBlock) void k_ln_bwd_reg(
       }
     }
   };
-  RowBuf ra, cur;
-  if (iters > 0) fetch(0, ra);
-  if constexpr (kDepth == 2) {
-    RowBuf rb;
-    if (iters > 1) fetch(1, rb);
-    for (int64_t it = 0; it < iters; it += 2) {
-      cur = ra;
-      if (it + 2 < iters) fetch(it + 2, ra);
-      body(it, cur);
-      if (it + 1 < iters) {  // uniform across the block, as iters is
-        cur = rb;
-        if (it + 3 < iters) fetch(it + 3, rb);
-        body(it + 1, cur);
+  // kDepth row buffers in a ring (the loop is unrolled by kDepth, so each buffer's
+  // registers are fixed): row it + kDepth is fetched as row it is processed
+  RowBuf ring[kDepth], cur;
+#pragma unroll
+  for (int j = 0; j < kDepth; ++j)
+    if (j < iters) fetch(j, ring[j]);
+  for (int64_t it = 0; it < iters; it += kDepth) {
+#pragma unroll
+    for (int j = 0; j < kDepth; ++j) {
+      if (it + j < iters) {  // uniform across the block, as iters is
+        cur = ring[j];
+        if (it + j + kDepth < iters) fetch(it + j + kDepth, ring[j]);
+        body(it + j, cur);
       }
-    }
-  } else {
-    for (int64_t it = 0; it < iters; ++it) {
-      cur = ra;
-      if (it + 1 < iters) fetch(it + 1, ra);
-      body(it, cur);
     }
   }
   // Combine the G row groups of this block, then write the block partial.
