@@ -393,6 +393,24 @@ int tg_flash_attn_bwd_f64(const double* q, const double* k, const double* v, con
                           double scale, int causal, int layout, int accumulate,
                           void* workspace, size_t workspace_bytes, void* stream);
 
+/* A Linear layer's GEMM with a fused epilogue (fp16 / bf16 on the DMA-staged kernel;
+ * other shapes, layouts or alignments return -3 and the caller runs the separate
+ * kernels).  The product is rounded to the dtype exactly as tg_gemm stores it, then
+ *   epi 1, GELU backward: C (+)= round(A B^T) * gelu'(X), A [M,K], B [N,K], X [M,N] the
+ *     GELU input (ldx).  The input gradient of a Linear layer fed by a GELU with the
+ *     GELU's backward applied (matmul bwd _core.py:1060 followed by the gelu closure
+ *     _core.py:1185-1206); beta 0 overwrites C, 1 adds.
+ *   epi 2, GELU forward: C = round(A B + bias), X = round(gelu(C)), B [K,N]: a Linear
+ *     layer's forward (_nn.py:258-285) followed by gelu (_core.py:1172-1197), both
+ *     outputs written.
+ *   epi 3, residual: C = round(A B + bias) + X, B [K,N]: x + Linear(..) (__add__,
+ *     _core.py:941-951, after _nn.py:258-285).
+ * bias is fp32 [N] or null (null for epi 1).  Each result equals the separate kernels'
+ * (tg_gemm / tg_gemm_bias, then tg_gelu_bwd / tg_gelu_fwd / the add) bit for bit. */
+int tg_gemm_epilogue(int dtype, int epi, int64_t M, int64_t N, int64_t K, const void* A,
+                     int64_t lda, const void* B, int64_t ldb, const float* bias, void* X,
+                     int64_t ldx, float beta, void* C, int64_t ldc, void* stream);
+
 /* Cross-entropy over logits [N, C] with int64 targets (CrossEntropyLoss,
  * _nn.py:1128-1185).  Forward: per-row log-sum-exp lse[N] and per-row loss
  * -log(p[t] + 1e-10) (label smoothing s: -sum_c w_c log(p_c + 1e-10), w = s/C +

@@ -65,6 +65,45 @@ template <> __device__ __forceinline__ float tg_from_float<float>(float v) { ret
 template <> __device__ __forceinline__ tg_half tg_from_float<tg_half>(float v) { return (tg_half)v; }
 template <> __device__ __forceinline__ tg_bf16 tg_from_float<tg_bf16>(float v) { return (tg_bf16)v; }
 
+// v materialised as an fp32 value: the compiler cannot merge the operation that made
+// it with a following conversion (e.g. an FMA and the fp32 -> fp16 rounding into one
+// single-rounding mixed-precision instruction), so kernels that compute the same value
+// and then round it round identically.
+__device__ __forceinline__ float tg_f32(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// tanh-approx GELU derivative, reference formula (_core.py:493-507):
+//   u = c0*(x + c1*x^3), t = tanh(u)
+//   g = 0.5*(1+t) + 0.5*x*(1-t^2)*c0*(1+3*c1*x^2)
+// tanh is evaluated from e = exp(-2|u|) in (0,1] so that neither (1+t) nor
+// (1-t^2) = sech^2(u) loses precision to cancellation.
+// Both functions evaluate without FMA contraction, so every kernel that inlines them
+// (the activation kernels and the GEMM epilogues) computes the same values.
+__device__ __forceinline__ float tg_gelu_grad(float x) {
+#pragma clang fp contract(off)
+  const float c0 = 0.7978845608028654f, c1 = 0.044715f;
+  const float x2 = x * x;
+  const float u = c0 * (x + c1 * x2 * x);
+  const float e = __expf(-2.0f * fabsf(u));
+  const float r = __builtin_amdgcn_rcpf(1.0f + e);  // 1 ulp, e in (0, 1]
+  const float onept = (u >= 0.f) ? 1.0f + (1.0f - e) * r : 2.0f * e * r;  // 1 + tanh(u)
+  const float sech2 = 4.0f * e * r * r;                                   // 1 - tanh(u)^2
+  const float du = c0 * (1.0f + 3.0f * c1 * x2);
+  return 0.5f * onept + 0.5f * x * sech2 * du;
+}
+
+__device__ __forceinline__ float tg_gelu_fwd(float x) {
+#pragma clang fp contract(off)
+  const float c0 = 0.7978845608028654f, c1 = 0.044715f;
+  const float u = c0 * (x + c1 * x * x * x);
+  const float e = __expf(-2.0f * fabsf(u));
+  const float r = __builtin_amdgcn_rcpf(1.0f + e);  // 1 ulp, e in (0, 1]
+  const float onept = (u >= 0.f) ? 1.0f + (1.0f - e) * r : 2.0f * e * r;
+  return tg_f32(0.5f * x * onept);
+}
+
 // Sum across the 64 lanes of a wavefront (butterfly, every lane gets the total).
 __device__ __forceinline__ float tg_wave_sum(float v) {
 #pragma unroll

@@ -15,31 +15,10 @@ constexpr int kActThreads = 128;
 
 enum { OP_GELU = 0, OP_SILU = 1 };
 
-// tanh-approx GELU derivative, reference formula (_core.py:493-507):
-//   u = c0*(x + c1*x^3), t = tanh(u)
-//   g = 0.5*(1+t) + 0.5*x*(1-t^2)*c0*(1+3*c1*x^2)
-// tanh is evaluated from e = exp(-2|u|) in (0,1] so that neither (1+t) nor
-// (1-t^2) = sech^2(u) loses precision to cancellation.
-__device__ __forceinline__ float gelu_grad(float x) {
-  const float c0 = 0.7978845608028654f, c1 = 0.044715f;
-  const float x2 = x * x;
-  const float u = c0 * (x + c1 * x2 * x);
-  const float e = __expf(-2.0f * fabsf(u));
-  const float r = __builtin_amdgcn_rcpf(1.0f + e);  // 1 ulp, e in (0, 1]
-  const float onept = (u >= 0.f) ? 1.0f + (1.0f - e) * r : 2.0f * e * r;  // 1 + tanh(u)
-  const float sech2 = 4.0f * e * r * r;                                   // 1 - tanh(u)^2
-  const float du = c0 * (1.0f + 3.0f * c1 * x2);
-  return 0.5f * onept + 0.5f * x * sech2 * du;
-}
-
-__device__ __forceinline__ float gelu_fwd(float x) {
-  const float c0 = 0.7978845608028654f, c1 = 0.044715f;
-  const float u = c0 * (x + c1 * x * x * x);
-  const float e = __expf(-2.0f * fabsf(u));
-  const float r = __builtin_amdgcn_rcpf(1.0f + e);  // 1 ulp, e in (0, 1]
-  const float onept = (u >= 0.f) ? 1.0f + (1.0f - e) * r : 2.0f * e * r;
-  return 0.5f * x * onept;
-}
+// GELU value and derivative: tg_gelu_grad / tg_gelu_fwd (tg_common.h, shared with the
+// GEMM epilogues so fused and separate passes give identical values).
+__device__ __forceinline__ float gelu_grad(float x) { return tg_gelu_grad(x); }
+__device__ __forceinline__ float gelu_fwd(float x) { return tg_gelu_fwd(x); }
 
 // SiLU derivative, reference formula (_core.py:522-533): s*(1 + x*(1-s)),
 // s = sigmoid(x).  1-s is formed as e*s with e = exp(-x) (no cancellation).
@@ -92,8 +71,10 @@ __global__ __launch_bounds__(kActThreads) void k_act_bwd(const T* __restrict__ x
       tg_vec16<T> r;
 #pragma unroll
       for (int j = 0; j < V; ++j) {
-        float g = tg_to_float(gv[u].v[j]) * act_grad<OP>(tg_to_float(xv[u].v[j]));
-        if (ACC) g += tg_to_float(ov[u].v[j]);
+        // accumulation as one explicit FMA, rounded to fp32 then to T (the GEMM epilogue
+        // that fuses this derivative rounds the same way)
+        const float d = tg_to_float(gv[u].v[j]), a = act_grad<OP>(tg_to_float(xv[u].v[j]));
+        const float g = tg_f32(ACC ? fmaf(d, a, tg_to_float(ov[u].v[j])) : d * a);
         r.v[j] = tg_from_float<T>(g);
       }
       tg_st16<NT>(dx + i * V, r);
@@ -102,8 +83,8 @@ __global__ __launch_bounds__(kActThreads) void k_act_bwd(const T* __restrict__ x
   // scalar tail (fewer than V elements), handled by the first block
   if (blockIdx.x == 0) {
     for (int64_t i = nvec * V + threadIdx.x; i < n; i += kActThreads) {
-      float g = tg_to_float(dy[i]) * act_grad<OP>(tg_to_float(x[i]));
-      if (ACC) g += tg_to_float(dx[i]);
+      const float d = tg_to_float(dy[i]), a = act_grad<OP>(tg_to_float(x[i]));
+      const float g = tg_f32(ACC ? fmaf(d, a, tg_to_float(dx[i])) : d * a);
       dx[i] = tg_from_float<T>(g);
     }
   }

@@ -667,12 +667,32 @@ __device__ __forceinline__ float frag_sum(const Vec8<tg_bf16>::type& v, float ac
 // BSUM: the blocks of the first tile row also sum B's columns over the whole K range
 // and store the sums to bsum (fp32) or, with bsum null, to dbo (dtype dbt, added to
 // its contents when dbacc; dbo null: nowhere).
+// EPI (epilogue fused on the stored values, which are first rounded to TC exactly as a
+// plain GEMM stores them, so each fused result equals the separate kernel's bit for bit):
+//   EPI_NONE      C (+)= alpha*AB (+ bias)
+//   EPI_GELU_BWD  C (+)= round(alpha*AB) * gelu'(X)   (X: the GELU input, [M, N], ldx)
+//   EPI_GELU_FWD  C = round(alpha*AB + bias), X = round(gelu(C))  (X written)
+//   EPI_RESIDUAL  C = round(alpha*AB + bias) + X      (X: the residual, read)
+enum { EPI_NONE = 0, EPI_GELU_BWD = 1, EPI_GELU_FWD = 2, EPI_RESIDUAL = 3 };
+// v = the product rounded to TC; c = the old C value (added when beta != 0).  GELU
+// backward accumulates with one explicit FMA, as tg_gelu_bwd's accumulate mode does.
+template <int EPI>
+__device__ __forceinline__ float epi_val(float v, float x, float beta, float c) {
+  if (EPI == EPI_GELU_BWD) {
+    const float g = tg_gelu_grad(x);
+    return tg_f32(beta != 0.f ? fmaf(v, g, beta * c) : v * g);
+  }
+  if (EPI == EPI_RESIDUAL) return v + x;
+  return v;
+}
+
 template <typename T, typename TC, bool TA, bool TB, int WGM, int WGN, int SM, int SN, int OCC,
-          bool BSUM>
+          bool BSUM, int EPI = EPI_NONE>
 __device__ __forceinline__ void v3_tile(
     int64_t M, int64_t N, int64_t K, float alpha, const T* __restrict__ A, int64_t lda,
     const T* __restrict__ B, int64_t ldb, float beta, TC* __restrict__ C, int64_t ldc,
-    const float* __restrict__ bias, float* __restrict__ bsum, void* dbo, int dbt, bool dbacc) {
+    const float* __restrict__ bias, float* __restrict__ bsum, void* dbo, int dbt, bool dbacc,
+    TC* __restrict__ X = nullptr, int64_t ldx = 0) {
   constexpr int NW = WGM * WGN, TBM = WGM * SM * 32, TBN = WGN * SN * 32;
   constexpr int ATILE = TBM * V3_BK * 2, BTILE = TBN * V3_BK * 2;
   __shared__ __attribute__((aligned(1024))) char a0[ATILE];
@@ -841,10 +861,23 @@ __device__ __forceinline__ void v3_tile(
     float bv[SN];  // bias of this lane's column in each 32-column tile
 #pragma unroll
     for (int j = 0; j < SN; ++j) bv[j] = bias ? bias[n0 + wn + j * 32 + l32] : 0.f;
+    constexpr int NQ = HR * CPR / 64;  // 16-byte chunks per lane and slab
 #pragma unroll
     for (int i = 0; i < SM; ++i) {
 #pragma unroll
       for (int half = 0; half < 32 / HR; ++half) {
+        // the epilogue operand's chunks of this slab, all loads issued before the slab
+        // is staged, so their latency overlaps the staging instead of each store
+        uint4 xq[EPI == EPI_GELU_BWD || EPI == EPI_RESIDUAL ? NQ : 1];
+        if constexpr (EPI == EPI_GELU_BWD || EPI == EPI_RESIDUAL) {
+#pragma unroll
+          for (int q = 0; q < NQ; ++q) {
+            const int u = q * 64 + lane, row = u / CPR, ch = u % CPR;
+            xq[q] = *reinterpret_cast<const uint4*>(
+                X + (m0 + wm + i * 32 + half * HR + row) * ldx + n0 + wn +
+                ch * (16 / (int)sizeof(TC)));
+          }
+        }
         // accumulator registers r in [half*16*HR/32, ...): rows half*HR .. half*HR+HR-1
 #pragma unroll
         for (int j = 0; j < SN; ++j)
@@ -858,12 +891,35 @@ __device__ __forceinline__ void v3_tile(
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's slab is written
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
-        for (int q = 0; q < HR * CPR / 64; ++q) {
+        for (int q = 0; q < NQ; ++q) {
           const int u = q * 64 + lane, row = u / CPR, ch = u % CPR;
           const uint4 v = *reinterpret_cast<const uint4*>(slab + row * RS + ch * 16);
-          TC* pc = C + (m0 + wm + i * 32 + half * HR + row) * ldc + n0 + wn +
-                   ch * (16 / (int)sizeof(TC));
-          if (beta != 0.f) {
+          const int64_t grow = m0 + wm + i * 32 + half * HR + row;
+          const int64_t gcol = n0 + wn + ch * (16 / (int)sizeof(TC));
+          TC* pc = C + grow * ldc + gcol;
+          if constexpr (EPI != EPI_NONE) {
+            tg_vec16<TC> o;
+            *reinterpret_cast<uint4*>(&o) = v;
+            if constexpr (EPI == EPI_GELU_FWD) {
+              *reinterpret_cast<uint4*>(pc) = v;
+              tg_vec16<TC> a;
+#pragma unroll
+              for (int e = 0; e < tg_vec16<TC>::N; ++e)
+                a.v[e] = tg_from_float<TC>(tg_gelu_fwd(tg_to_float(o.v[e])));
+              tg_store16(X + grow * ldx + gcol, a);
+            } else {
+              tg_vec16<TC> xv;
+              *reinterpret_cast<uint4*>(&xv) = xq[q];
+              tg_vec16<TC> c;
+              if (beta != 0.f) c = tg_load16(pc);
+#pragma unroll
+              for (int e = 0; e < tg_vec16<TC>::N; ++e) {
+                o.v[e] = tg_from_float<TC>(epi_val<EPI>(tg_to_float(o.v[e]), tg_to_float(xv.v[e]),
+                                                        beta, beta != 0.f ? tg_to_float(c.v[e]) : 0.f));
+              }
+              tg_store16(pc, o);
+            }
+          } else if (beta != 0.f) {
             tg_vec16<TC> o, c = tg_load16(pc);
             *reinterpret_cast<uint4*>(&o) = v;
 #pragma unroll
@@ -893,6 +949,17 @@ __device__ __forceinline__ void v3_tile(
           float v = alpha * acc[i][j][r];
           if (bias) v += bias[col];
           TC* pc = C + row * ldc + col;
+          if constexpr (EPI == EPI_GELU_FWD) {
+            const TC h = tg_from_float<TC>(v);
+            *pc = h;
+            X[row * ldx + col] = tg_from_float<TC>(tg_gelu_fwd(tg_to_float(h)));
+            continue;
+          } else if constexpr (EPI != EPI_NONE) {
+            *pc = tg_from_float<TC>(epi_val<EPI>(tg_to_float(tg_from_float<TC>(v)),
+                                                 tg_to_float(X[row * ldx + col]), beta,
+                                                 beta != 0.f ? tg_to_float(*pc) : 0.f));
+            continue;
+          }
           if (beta != 0.f) v += beta * tg_to_float(*pc);
           *pc = tg_from_float<TC>(v);
         }
@@ -911,6 +978,20 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_v3(
   v3_tile<T, TC, TA, TB, WGM, WGN, SM, SN, OCC, BSUM>(
       M, N, K, alpha, A + bz * sa, lda, B + bz * sb, ldb, beta, C + bz * sc, ldc, bias,
       BSUM ? bsum + bz * N : nullptr, nullptr, 0, false);
+}
+
+// k_gemm_v3 (one batch entry) with a fused epilogue operand X (EPI_* above).
+// (alpha stays a run-time argument, 1 in every call, so the stored product is formed by
+// the same instructions as k_gemm_v3's: a constant 1 would let the compiler replace
+// the single-rounding fp32->fp16 multiply-add of alpha*acc + bias by an add and a
+// conversion, which round twice)
+template <typename T, bool TA, bool TB, int WGM, int WGN, int SM, int SN, int OCC, int EPI>
+__global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_v3e(
+    int64_t M, int64_t N, int64_t K, float alpha, const T* __restrict__ A, int64_t lda,
+    const T* __restrict__ B, int64_t ldb, float beta, T* __restrict__ C, int64_t ldc,
+    const float* __restrict__ bias, T* __restrict__ X, int64_t ldx) {
+  v3_tile<T, T, TA, TB, WGM, WGN, SM, SN, OCC, false, EPI>(
+      M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, bias, nullptr, nullptr, 0, false, X, ldx);
 }
 
 // A group of same-shape GEMMs C_g (+)= A_g^T B_g with their own operands (weight
@@ -1066,6 +1147,48 @@ int launch(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const v
   }
 #undef TG_G
   return tg_check_launch("tg_gemm");
+}
+
+// The fused-epilogue GEMMs on the DMA-staged kernel: GELU backward as C (+)= ...
+// (A [M,K], op(B) = B^T with B [N,K]: a Linear layer's input gradient G W^T), GELU
+// forward and residual as C = A B + bias (B [K,N]: a Linear layer's forward).  Other
+// layouts or shapes return TG_ERR_UNSUPPORTED (the caller runs the separate kernels).
+template <typename T>
+int launch_epi(int epi, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+               const void* B, int64_t ldb, float beta, void* C, int64_t ldc, const float* bias,
+               void* X, int64_t ldx, hipStream_t s) {
+  const int tb = epi == EPI_GELU_BWD;
+  const int VE = 16 / (int)sizeof(T);
+  if (!v3_ok((int)sizeof(T), 0, tb, M, N, K, A, lda, 0, B, ldb, 0) || !tg_aligned16(C) ||
+      !tg_aligned16(X) || ldc % VE || ldx % VE || (epi == EPI_GELU_BWD && bias)) {
+    tg_set_error("tg_gemm_epilogue: shape or alignment outside the fused kernel");
+    return TG_ERR_UNSUPPORTED;
+  }
+  const int64_t ncu = tg_num_cus();
+  const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
+  const int64_t t128 = ((M + 255) / 256) * ((N + 127) / 128);
+  const int shape = t256 >= kHugeTiles * ncu / 4 ? 2 : (t128 >= ncu ? 1 : 0);
+  const T* a = (const T*)A;
+  const T* b = (const T*)B;
+#define TG_GE(TB_, E, WGM, WGN, SM, SN, OCC)                                                   \
+  do {                                                                                       \
+    constexpr int TBM = WGM * SM * 32, TBN = WGN * SN * 32;                                  \
+    dim3 g((unsigned)((N + TBN - 1) / TBN), (unsigned)((M + TBM - 1) / TBM), 1);             \
+    k_gemm_v3e<T, false, TB_, WGM, WGN, SM, SN, OCC, E><<<g, 64 * WGM * WGN, 0, s>>>(          \
+        M, N, K, 1.f, a, lda, b, ldb, beta, (T*)C, ldc, bias, (T*)X, ldx);                     \
+  } while (0)
+#define TG_GES(TB_, E)                                                          \
+  do {                                                                          \
+    if (shape == 2) TG_GE(TB_, E, 4, 2, 2, 4, 1);                              \
+    else if (shape == 1) TG_GE(TB_, E, kBigWGM, kBigWGN, kBigSM, kBigSN, 1);  \
+    else TG_GE(TB_, E, 2, 2, 2, 2, 2);                                         \
+  } while (0)
+  if (epi == EPI_GELU_BWD) TG_GES(true, EPI_GELU_BWD);
+  else if (epi == EPI_GELU_FWD) TG_GES(false, EPI_GELU_FWD);
+  else TG_GES(false, EPI_RESIDUAL);
+#undef TG_GES
+#undef TG_GE
+  return tg_check_launch("tg_gemm_epilogue");
 }
 
 }  // namespace
@@ -1400,4 +1523,24 @@ TG_EXPORT int tg_gemm_bias(int dtype_ab, int dtype_c, int trans_a, int trans_b, 
   TG_REQUIRE(bias, "tg_gemm_bias: null bias");
   return gemm_dispatch("tg_gemm_bias", dtype_ab, dtype_c, trans_a, trans_b, M, N, K, alpha, A,
                        lda, 0, B, ldb, 0, 0.f, C, ldc, 0, 1, bias, stream);
+}
+
+TG_EXPORT int tg_gemm_epilogue(int dtype, int epi, int64_t M, int64_t N, int64_t K,
+                               const void* A, int64_t lda, const void* B, int64_t ldb,
+                               const float* bias, void* X, int64_t ldx, float beta, void* C,
+                               int64_t ldc, void* stream) {
+  TG_REQUIRE(M >= 0 && N >= 0 && K >= 0, "tg_gemm_epilogue: negative extent");
+  TG_REQUIRE(epi >= EPI_GELU_BWD && epi <= EPI_RESIDUAL, "tg_gemm_epilogue: unknown epilogue %d",
+             epi);
+  if (M == 0 || N == 0) return TG_OK;
+  TG_REQUIRE(A && B && C && X, "tg_gemm_epilogue: null pointer");
+  TG_REQUIRE(ldc >= N && ldx >= N, "tg_gemm_epilogue: ldc / ldx below N");
+  TG_REQUIRE(epi == EPI_GELU_BWD || beta == 0.f, "tg_gemm_epilogue: beta only with GELU bwd");
+  hipStream_t s = tg_stream(stream);
+  if (dtype == TG_F16)
+    return launch_epi<tg_half>(epi, M, N, K, A, lda, B, ldb, beta, C, ldc, bias, X, ldx, s);
+  if (dtype == TG_BF16)
+    return launch_epi<tg_bf16>(epi, M, N, K, A, lda, B, ldb, beta, C, ldc, bias, X, ldx, s);
+  tg_set_error("tg_gemm_epilogue: dtype %d has no fused kernel (fp16 / bf16 only)", dtype);
+  return TG_ERR_UNSUPPORTED;
 }

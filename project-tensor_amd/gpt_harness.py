@@ -2,7 +2,9 @@
 
 Pre-LayerNorm decoder: tied token embedding, per layer LN -> Q/K/V/O Linear with
 causal FlashAttention -> residual, LN -> Linear(d, 4d) -> GELU -> Linear(4d, d) ->
-residual; final LN; logits = h @ E^T; CrossEntropyLoss.  One step runs the forward
+residual; final LN; logits = h @ E^T; CrossEntropyLoss.  The residual adds and the
+GELU run in the adjacent Linear GEMMs' epilogues (Linear's residual= / activation=
+options: the same graph and values as the separate ops).  One step runs the forward
 under fp16 autocast, GradScaler.scale(loss).backward(), sync_tied_gradients,
 unscale_, clip_grad_norm_(1.0), GradScaler.step(AdamW) and update().
 
@@ -46,9 +48,11 @@ class Block(tg.Module):
             return t.reshape(B, T, H, hd).transpose(0, 2, 1, 3)
         att = tg.flash_attention(split(self.q(a)), split(self.k(a)), split(self.v(a)),
                                  is_causal=True)
-        h = h + self.o(att.transpose(0, 2, 1, 3).reshape(B, T, C))
+        # h + o(att) and fc2(gelu(fc1(m))) + h with the add and the GELU in the GEMMs'
+        # epilogues (Linear's keyword options; the same ops, values and gradients)
+        h = self.o(att.transpose(0, 2, 1, 3).reshape(B, T, C), residual=h)
         m = self.ln2(h)
-        return h + self.fc2(self.fc1(m).gelu())
+        return self.fc2(self.fc1(m, activation="gelu"), residual=h)
 
 
 class GPT(tg.Module):

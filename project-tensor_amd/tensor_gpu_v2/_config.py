@@ -15,6 +15,11 @@ _default_dtype = np.dtype(np.float32)
 _mixed_precision = False
 _grad_enabled = True
 _active_autocast_dtype = None  # numpy/torch dtype while autocast is active
+# A GELU output consumed by exactly one Linear layer: the Linear's backward applies the
+# GELU derivative in its input-gradient GEMM and the GELU output's own gradient is not
+# formed (reading .grad of that intermediate then gives zeros).  False keeps the
+# reference's materialised intermediate gradient (two kernels, same values).
+fuse_gelu_backward = True
 
 _NP_TO_TORCH = {
     np.dtype(np.float32): torch.float32,

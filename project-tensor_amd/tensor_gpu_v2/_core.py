@@ -148,7 +148,7 @@ class Tensor:
 
     __slots__ = ("data", "_g", "_gz", "_gsh", "_backward", "_prev", "_op", "label", "_device",
                  "_requires_grad", "_is_view", "_base", "_grad_fn", "__weakref__",
-                 "_tied_source", "_tied_transpose")
+                 "_tied_source", "_tied_transpose", "_nuse", "_act")
 
     def __init__(self, data, _children=(), _op="", label="", device=None, requires_grad=True,
                  dtype=None):
@@ -169,6 +169,10 @@ class Tensor:
         self._gsh = False  # _g may alias another node's gradient (copy-on-write)
         self._backward = _noop
         self._prev = _unique(_children)
+        self._nuse = 0  # graph nodes recorded with this tensor as an operand
+        self._act = None  # GELU output: (input tensor, its contiguous data)
+        for c in self._prev:
+            c._nuse += 1
         self._op = _op
         self.label = label
         self._device = device
@@ -191,6 +195,10 @@ class Tensor:
         out._gsh = False
         out._backward = _noop
         out._prev = _unique(children) if rg else ()
+        out._nuse = 0
+        out._act = None
+        for c in out._prev:
+            c._nuse += 1
         out._op = op
         out.label = ""
         out._device = "cuda"
@@ -476,7 +484,11 @@ class Tensor:
     # ------------------------------------------------------------ arithmetic
     def __add__(self, other):
         other = self._other(other)
-        out = self._out(self.data + other.data, (self, other), "+")
+        return self._add_node(other, self.data + other.data)
+
+    def _add_node(self, other, data):
+        """The node of self + other with its sum already computed (data)."""
+        out = self._out(data, (self, other), "+")
         if out._requires_grad:
             def _backward():
                 g = out._grad_out()
@@ -1094,8 +1106,16 @@ def _activation(x, kind):
     if xd.dtype not in L._TORCH_TO_CODE:
         raise TypeError(f"{kind}: unsupported dtype {xd.dtype}")
     xc = xd.contiguous()
-    y = L.act_fwd(kind, xc)
+    return _activation_node(x, kind, xc, L.act_fwd(kind, xc))
+
+
+def _activation_node(x, kind, xc, y):
+    """The graph node of y = act(x) (xc: x's contiguous data): its closure adds
+    dy * act'(x) to x's gradient.  A GELU output also records (x, xc), so a Linear
+    layer that is its only consumer can apply the derivative in its own backward."""
     out = Tensor._wrap(y, (x,), "GELU" if kind == "gelu" else "SiLU")
+    if kind == "gelu" and out._requires_grad:
+        out._act = (x, xc)
     if out._requires_grad:
         def _backward():
             if not x._has_grad():
@@ -1178,16 +1198,12 @@ def _weight_operand(w, wd, wt, cdt):
     return _lowp.cast(src, cdt)
 
 
-def _linear(x, w, b):
-    """y = x @ w + b for a 2-D weight as one GEMM with the bias added in its epilogue
-    (Linear.__call__, _nn.py:258-285, which builds a matmul node and a broadcast-add
-    node; the gradients are those of the pair: dx = g @ w^T, dw = x^T @ g, db = g
-    summed over the leading axes).  A weight that is the transpose of a contiguous
-    tensor (a tied head) is cast without transposing and used through op(B) = B^T."""
+def _linear_operands(x, w):
+    """(A2 [rows, K] in the compute dtype, B operand, wt, cdt, K, N, lead) of
+    x @ w for a 2-D weight, or None when x @ w is not a plain 2-D-weight product."""
     a, wd = x.data, w.data
     if a.dim() < 2 or wd.dim() != 2 or a.shape[-1] != wd.shape[0]:
-        out = x @ w
-        return out + b if b is not None else out
+        return None
     cdt = _compute_dtype(a, wd)
     if cdt not in _GEMM_DTYPES:
         raise TypeError(f"matmul: dtype {cdt} is not supported by the MFMA GEMM "
@@ -1197,6 +1213,21 @@ def _linear(x, w, b):
     A2 = (_as(a, cdt) if cdt == torch.float64 else a.to(cdt).contiguous()).reshape(-1, K)
     wt = not wd.is_contiguous() and wd.t().is_contiguous()
     bc = _weight_operand(w, wd, wt, cdt)  # [N, K] if wt
+    return A2, bc, wt, cdt, K, N, lead
+
+
+def _linear(x, w, b):
+    """y = x @ w + b for a 2-D weight as one GEMM with the bias added in its epilogue
+    (Linear.__call__, _nn.py:258-285, which builds a matmul node and a broadcast-add
+    node; the gradients are those of the pair: dx = g @ w^T, dw = x^T @ g, db = g
+    summed over the leading axes).  A weight that is the transpose of a contiguous
+    tensor (a tied head) is cast without transposing and used through op(B) = B^T."""
+    ops = _linear_operands(x, w)
+    if ops is None:
+        out = x @ w
+        return out + b if b is not None else out
+    A2, bc, wt, cdt, K, N, lead = ops
+    a = x.data
     if b is not None and cdt == torch.float64:
         # fp64: the product, then the bias added by the broadcast kernel (in fp64)
         y = L.matmul2d(A2, bc, trans_b=wt)
@@ -1213,23 +1244,78 @@ def _linear(x, w, b):
             y = y.to(odt)
     else:
         y = L.matmul2d(A2, bc, trans_b=wt)
+    return _linear_node(x, w, b, A2, bc, wt, cdt, K, N, y.reshape(*lead, N))
+
+
+def _fused_out_dtype(cdt, b):
+    """The output dtype of a fused-epilogue Linear: cdt when the plain path would also
+    produce cdt (16-bit operands whose bias promotion resolves back to cdt), else None."""
+    if cdt not in (torch.float16, torch.bfloat16):
+        return None
+    if b is None:
+        return cdt
+    return cdt if cfg.resolve_dtype(torch.promote_types(cdt, b.data.dtype)) == cdt else None
+
+
+def _linear_gelu(x, w, b):
+    """gelu(x @ w + b) with the GELU applied in the GEMM's epilogue (tg_gemm_epilogue,
+    both the pre-activation and the activation written; bit-identical to the Linear
+    then gelu nodes, which it builds).  Falls back to the two kernels where the fused
+    kernel does not serve the shape."""
+    ops = _linear_operands(x, w)
+    if ops is not None:
+        A2, bc, wt, cdt, K, N, lead = ops
+        if not wt and _fused_out_dtype(cdt, b) is not None:
+            h = torch.empty(A2.shape[0], N, dtype=cdt, device=A2.device)
+            act = torch.empty_like(h)
+            bias = None if b is None else b.data.to(torch.float32).contiguous().reshape(N)
+            if L.gemm_epilogue("gelu_fwd", A2, bc, act, h, bias):
+                hn = _linear_node(x, w, b, A2, bc, wt, cdt, K, N, h.reshape(*lead, N))
+                return _activation_node(hn, "gelu", h.reshape(*lead, N), act.reshape(*lead, N))
+    return _linear(x, w, b).gelu()
+
+
+def _linear_residual(x, w, b, r):
+    """r + (x @ w + b) with the residual added in the GEMM's epilogue
+    (tg_gemm_epilogue; bit-identical to the Linear then add nodes, which it builds:
+    the Linear node keeps the sum's buffer as its data, which its backward never
+    reads).  Falls back to the two kernels where the fused kernel does not serve the
+    shape or r does not match the output."""
+    ops = _linear_operands(x, w)
+    if ops is not None and isinstance(r, Tensor):
+        A2, bc, wt, cdt, K, N, lead = ops
+        rd = r.data
+        if (not wt and _fused_out_dtype(cdt, b) is not None and rd.dtype == cdt
+                and tuple(rd.shape) == lead + (N,) and rd.is_contiguous()):
+            out = torch.empty(A2.shape[0], N, dtype=cdt, device=A2.device)
+            bias = None if b is None else b.data.to(torch.float32).contiguous().reshape(N)
+            if L.gemm_epilogue("residual", A2, bc, rd.reshape(-1, N), out, bias):
+                o = out.reshape(*lead, N)
+                y = _linear_node(x, w, b, A2, bc, wt, cdt, K, N, o)
+                return r._add_node(y, o)
+    return r + _linear(x, w, b)
+
+
+def _linear_node(x, w, b, A2, bc, wt, cdt, K, N, y):
+    """The graph node of y = x @ w + b (A2, bc: the GEMM operands the forward used)."""
     children = (x, w) if b is None else (x, w, b)
-    out = Tensor._wrap(y.reshape(*lead, N), children, "linear")
+    out = Tensor._wrap(y, children, "linear")
     if out._requires_grad:
         def _backward():
             g = out._grad_out()
             G2 = _as(g, cdt).reshape(-1, N)
             if x._has_grad():
-                buf, acc = x._grad_target()
-                if _direct_out(buf.dtype, cdt):
-                    L.matmul2d(G2, bc, out=buf.view(-1, K), trans_b=not wt,
-                               beta=1.0 if acc else 0.0)
-                else:
-                    da = L.matmul2d(G2, bc, trans_b=not wt, out_dtype=_wide(cdt))
-                    if acc:
-                        x._accumulate(da.reshape(buf.shape), True)
+                if not _gelu_input_grad(x, G2, bc, wt, cdt):
+                    buf, acc = x._grad_target()
+                    if _direct_out(buf.dtype, cdt):
+                        L.matmul2d(G2, bc, out=buf.view(-1, K), trans_b=not wt,
+                                   beta=1.0 if acc else 0.0)
                     else:
-                        _copy_into(buf, da.reshape(buf.shape))
+                        da = L.matmul2d(G2, bc, trans_b=not wt, out_dtype=_wide(cdt))
+                        if acc:
+                            x._accumulate(da.reshape(buf.shape), True)
+                        else:
+                            _copy_into(buf, da.reshape(buf.shape))
             fuse = (w._has_grad() and b is not None and b._has_grad() and g.dtype == cdt
                     and b.data.numel() == N and b.data.shape[-1] == N)
             # 16-bit products into leaf parameters wait for the end of the sweep
@@ -1269,6 +1355,34 @@ def _linear(x, w, b):
                     _copy_into(buf, dw)
         out._backward = _backward
     return out
+
+
+def _gelu_input_grad(x, G2, bc, wt, cdt):
+    """When x is a GELU output whose only consumer is this Linear layer, x's gradient is
+    exactly G2 @ w^T: the GELU's input gradient is formed from it in the GEMM's
+    epilogue (tg_gemm_epilogue "gelu_bwd", bit-identical to the two kernels) and the
+    GELU node's own closure is retired, so x's gradient buffer is never formed.
+    Returns False (nothing done) when the pattern or the fused kernel does not apply."""
+    act = x._act
+    if act is None or x._nuse != 1 or wt or not cfg.fuse_gelu_backward:
+        return False
+    src, xc = act
+    if xc.dtype != cdt or not x._gz:  # x must not hold a gradient from elsewhere
+        return False
+    if not src._has_grad():
+        x._backward = _noop
+        return True
+    if src.data.dtype != cdt or cdt not in (torch.float16, torch.bfloat16):
+        return False
+    buf, acc = src._grad_target()
+    M = G2.shape[0]
+    x2, b2 = xc.reshape(M, -1), buf.view(M, -1)
+    if not L.gemm_epilogue("gelu_bwd", G2, bc, x2, b2, beta=1.0 if acc else 0.0):
+        # the fused kernel does not serve this shape: the same two kernels the separate
+        # closures would run (the GELU input's buffer is already claimed)
+        L.act_bwd("gelu", x2, L.matmul2d(G2, bc, trans_b=True), b2, acc)
+    x._backward = _noop
+    return True
 
 
 def _batch_view(x, batch_shape, m, n):

@@ -44,6 +44,8 @@ SIGNATURES = {
     "tg_log_softmax_bwd": (_i32, [_i32, _vp, _vp, _vp, _i64, _i64, _i32, _vp]),
     "tg_index_add_sorted": (_i32, [_i32, _vp, _i64, _vp, _vp, _vp, _vp, _vp]),
     "tg_max_bwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _i64, _i64, _i32, _vp]),
+    "tg_gemm_epilogue": (_i32, [_i32, _i32, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _vp,
+                                _i64, _f32, _vp, _i64, _vp]),
     "tg_silu_fwd": (_i32, [_i32, _vp, _vp, _i64, _vp]),
     "tg_axpby": (_i32, [_i32, _vp, _i32, _vp, _i64, _f32, _f32, _vp]),
     "tg_axpbyz": (_i32, [_i32, _vp, _i32, _vp, _vp, _i64, _f32, _f32, _vp]),
@@ -301,6 +303,44 @@ def log_softmax_bwd(y, dy, dx, accumulate):
            load().tg_log_softmax_bwd(dtype_code(y), ptr(y), ptr(dy), ptr(dx), rows, cols,
                                      int(bool(accumulate)), stream_handle()))
     return dx
+
+
+GEMM_EPI = {"gelu_bwd": 1, "gelu_fwd": 2, "residual": 3}
+
+
+def gemm_epilogue(epi, a, b, x, out, bias=None, beta=0.0):
+    """A Linear layer's GEMM with a fused epilogue (tg_gemm_epilogue): "gelu_bwd"
+    out (+)= (a @ b.T) * gelu'(x); "gelu_fwd" out = a @ b + bias and x = gelu(out);
+    "residual" out = a @ b + bias + x.  a [M, K]; b [N, K] for gelu_bwd, else [K, N];
+    x and out [M, N]; all fp16 or all bf16, contiguous.  Returns False (nothing run)
+    when the fused kernel does not serve the shape or layout."""
+    for n, t in (("a", a), ("b", b), ("x", x), ("out", out)):
+        _dev(t, n)
+    dt = a.dtype
+    if dt not in (torch.float16, torch.bfloat16) or any(t.dtype != dt for t in (b, x, out)):
+        return False
+    M, K = a.shape
+    N = b.shape[0] if epi == "gelu_bwd" else b.shape[1]
+    if (b.shape[1] if epi == "gelu_bwd" else b.shape[0]) != K or tuple(x.shape) != (M, N) \
+            or tuple(out.shape) != (M, N):
+        raise ValueError(f"gemm_epilogue: shapes {tuple(a.shape)} {tuple(b.shape)} "
+                         f"{tuple(x.shape)} {tuple(out.shape)}")
+    if bias is not None:
+        _dev(bias, "bias")
+        if bias.dtype != torch.float32 or bias.numel() != N:
+            raise ValueError("gemm_epilogue: bias must be fp32 [N]")
+    if _split_k(M, N, K, a.device) > 1:
+        # the plain product would run K-split (another summation order): not fused, so
+        # a fused result always equals the separate kernels' bit for bit
+        return False
+    ensure_device(a.device.index)
+    st = load().tg_gemm_epilogue(dtype_code(a), GEMM_EPI[epi], M, N, K, ptr(a), K, ptr(b),
+                                 b.shape[1], ptr(bias), ptr(x), N, float(beta), ptr(out), N,
+                                 stream_handle())
+    if st == -3:
+        return False
+    _check("tg_gemm_epilogue", st)
+    return True
 
 
 def max_bwd(x, r, g, dx, accumulate):

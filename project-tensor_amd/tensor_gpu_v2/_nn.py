@@ -15,7 +15,7 @@ import torch
 from . import _config as cfg
 from . import _lib as L
 from . import _core, _lowp
-from ._core import Tensor, _as, _linear
+from ._core import Tensor, _as, _linear, _linear_gelu, _linear_residual
 
 
 def _targets(tensors):
@@ -188,10 +188,23 @@ class Linear(Module):
         self.use_bias = bias
         self.b = Tensor(np.zeros(nout, dtype=np.float32), dtype=np.float32) if bias else None
 
-    def __call__(self, x):
-        # one GEMM with the bias in its epilogue (same values and gradients as
-        # x @ w followed by + b)
-        return _linear(x, self.w, self.b if self.use_bias else None)
+    def __call__(self, x, *, activation=None, residual=None):
+        """x @ w + b as one GEMM with the bias in its epilogue (same values and
+        gradients as x @ w followed by + b).  Keyword options, not in the reference
+        (which composes the ops): activation="gelu" returns gelu(x @ w + b) and
+        residual=r returns r + (x @ w + b), each with the extra op applied in the same
+        GEMM's epilogue where the fused kernel serves the shape (fp16 / bf16), values
+        and graph identical to the separate ops."""
+        b = self.b if self.use_bias else None
+        if activation is not None and residual is not None:
+            raise ValueError("Linear: activation and residual cannot be combined")
+        if activation is not None:
+            if activation != "gelu":
+                raise ValueError(f"Linear: unsupported activation {activation!r}")
+            return _linear_gelu(x, self.w, b)
+        if residual is not None:
+            return _linear_residual(x, self.w, b, residual)
+        return _linear(x, self.w, b)
 
     def parameters(self):
         return [self.w, self.b] if self.use_bias else [self.w]
