@@ -341,6 +341,19 @@ int tg_gemm_wgrad_group(int dtype_ab, int n, int64_t M, int64_t N, int64_t K,
                         int dtype_w, void* const* dW, int64_t ldw, const int* acc_w,
                         int dtype_b, void* const* db, const int* acc_b, void* workspace,
                         size_t workspace_bytes, void* stream);
+/* tg_gemm_wgrad_group over members of one input shape X[g]: (K, M) whose outputs
+ * differ in width: G[g] is (K, N[g]) with row stride ldg[g], dW[g] (M, N[g]) with row
+ * stride ldw[g] (N, ldg, ldw: host arrays of n entries).  The members' output tiles
+ * form one launch, so layers of one input width (e.g. a fused Q/K/V projection, N =
+ * 3d, and the output projection, N = d) fill the CUs together.  workspace:
+ * tg_gemm_wgrad_group_n_workspace bytes. */
+size_t tg_gemm_wgrad_group_n_workspace(int dtype_ab, int n, int64_t M, const int64_t* N,
+                                       int64_t K, int with_bias);
+int tg_gemm_wgrad_group_n(int dtype_ab, int n, int64_t M, const int64_t* N, int64_t K,
+                          const void* const* X, int64_t ldx, const void* const* G,
+                          const int64_t* ldg, int dtype_w, void* const* dW, const int64_t* ldw,
+                          const int* acc_w, int dtype_b, void* const* db, const int* acc_b,
+                          void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- attention ------------------------------------------------------------ */
 /* FlashAttention forward on contiguous (B,H,S,D) tensors, saving the row
@@ -373,6 +386,21 @@ int tg_flash_attn_bwd_layout(int dtype, const void* q, const void* k, const void
                              void* dk, void* dv, int64_t B, int64_t H, int64_t Sq, int64_t Sk,
                              int64_t D, float scale, int causal, int accumulate, int layout,
                              void* workspace, size_t workspace_bytes, void* stream);
+/* Self-attention on one packed projection qkv of (B,S,3,H,D) memory: the output of a
+ * fused Q/K/V Linear(d, 3*H*D) whose columns hold the query, key and value heads in that
+ * order (the reference's MultiHeadAttention module projects x by w_q, w_k, w_v and splits
+ * the heads by reshape + transpose copies, _training.py:1885-1904; _core.py:1873-1913 is
+ * the functional form).  q, k and v are read in place (rows 3*H*D elements apart); o and
+ * dout are (B,S,H,D) (the merged-head input of the output projection, with no copy); the
+ * backward writes (or adds, accumulate != 0) dq, dk and dv into the matching columns of
+ * dqkv, also (B,S,3,H,D).  lse (B,H,S) fp32; workspace as tg_flash_attn_bwd_workspace(B,
+ * H, S, S, D).  Same dtypes and head dims as the calls above. */
+int tg_flash_attn_fwd_qkv(int dtype, const void* qkv, void* o, float* lse, int64_t B, int64_t H,
+                          int64_t S, int64_t D, float scale, int causal, void* stream);
+int tg_flash_attn_bwd_qkv(int dtype, const void* qkv, const void* o, const void* dout,
+                          const float* lse, void* dqkv, int64_t B, int64_t H, int64_t S,
+                          int64_t D, float scale, int causal, int accumulate, void* workspace,
+                          size_t workspace_bytes, void* stream);
 /* FlashAttention on float64 data (the reference runs flash_attention in the input's
  * dtype, _core.py:1716-1867): the scores of a chunk of heads are materialised in the
  * workspace (as the reference materialises them per query block), the products run on

@@ -86,17 +86,27 @@ __device__ __forceinline__ void fa_block(int64_t& tile, int64_t& head, int G) {
 }
 
 // Layout of Q/K/V/O/dO/dQ/dK/dV.  Logical [B, H, S, D]; in memory either
-// contiguous [B, H, S, D] (bshd = 0) or contiguous [B, S, H, D] (bshd = 1: the head
-// split of a [B, S, H*D] projection, used without a transposing copy).  Rows of one
-// head are rs = D or H*D elements apart.  LSE and D stay [B, H, S].
+// contiguous [B, H, S, D] (bshd = 0: rows D elements apart) or [B, S, H, D] rows with
+// head h at column h*D (bshd = 1: the head split of a projection, used without a
+// transposing copy).  Under bshd the rows of Q/K/V/dQ/dK/dV are rsa elements apart and
+// those of O/dO rso: H*D each for separate [B, S, H*D] tensors, rsa = 3*H*D for Q, K
+// and V read from (and dQ, dK, dV written into) one packed [B, S, 3, H, D] projection.
+// LSE and D stay [B, H, S].
 struct FaLay {
   int64_t H;
   int bshd;
-  int G;  // heads per dispatch group (fa_block)
-  __device__ __forceinline__ int64_t head(int64_t bh, int64_t S, int D) const {
-    return bshd ? ((bh / H) * S * H + (bh % H)) * D : bh * S * D;
+  int G;    // heads per dispatch group (fa_block)
+  int rsa;  // row stride of Q, K, V, dQ, dK, dV
+  int rso;  // row stride of O, dO
+  __device__ __forceinline__ int64_t head(int64_t bh, int64_t S, int D, int rs) const {
+    return bshd ? (bh / H) * S * rs + (bh % H) * D : bh * S * D;
   }
-  __device__ __forceinline__ int rs(int D) const { return bshd ? (int)(H * D) : D; }
+  __device__ __forceinline__ int64_t ha(int64_t bh, int64_t S, int D) const {
+    return head(bh, S, D, rsa);
+  }
+  __device__ __forceinline__ int64_t ho(int64_t bh, int64_t S, int D) const {
+    return head(bh, S, D, rso);
+  }
 };
 
 // Row index (within a 32-row C tile) of accumulator register r for lane half h.
@@ -433,15 +443,15 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dkdv(
   __shared__ __attribute__((aligned(16))) float lse0[BM], dvs0[BM], lse1[BM], dvs1[BM];
   int64_t tile, bh;
   fa_block(tile, bh, lay.G);
-  Q += lay.head(bh, Sq, D);
-  dO += lay.head(bh, Sq, D);
-  K += lay.head(bh, Sk, D);
-  V += lay.head(bh, Sk, D);
-  dK += lay.head(bh, Sk, D);
-  dV += lay.head(bh, Sk, D);
+  Q += lay.ha(bh, Sq, D);
+  dO += lay.ho(bh, Sq, D);
+  K += lay.ha(bh, Sk, D);
+  V += lay.ha(bh, Sk, D);
+  dK += lay.ha(bh, Sk, D);
+  dV += lay.ha(bh, Sk, D);
   LSE += bh * Sq;
   Dv += bh * Sq;
-  const int rs = lay.rs(D);
+  const int rs = lay.rsa, ro = lay.rso;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int h = lane >> 5, l32 = lane & 31;
   const int64_t kblk = tile * 128;
@@ -477,8 +487,9 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dkdv(
     }
   LaneOffs<D> o;
   o.init(lane);
-  DmaPlan<T, D, BM> plan;
+  DmaPlan<T, D, BM> plan, plano;  // Q and dO tiles
   plan.init(lane, wave, rs);
+  plano.init(lane, wave, ro);
   // causal: queries below the first key of this block contribute nothing
   const int64_t qstart = causal ? (kblk / BM) * BM : 0;
   // log2e*lse and D of one tile's rows (+inf / 0 past Sq, so P = 0 for padded rows).
@@ -504,7 +515,7 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dkdv(
   if (qstart < Sq) {
     lsed(qstart);
     plan.copy(Q, qstart, Sq, q0s);
-    plan.copy(dO, qstart, Sq, do0s);
+    plano.copy(dO, qstart, Sq, do0s);
     put(lse0, dvs0);
   }
   // The next tile's copy is issued in two halves, before the first two sub-tiles of
@@ -512,10 +523,10 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dkdv(
   // copies queue up behind each other in the address unit while no MFMA runs.
   constexpr int NPW = DmaPlan<T, D, BM>::NPW;
   auto stage = [&](int64_t qn, char* qd, char* dd) {
-    return [&plan, &Q, &dO, qn, qd, dd, Sq](int t) {
+    return [&plan, &plano, &Q, &dO, qn, qd, dd, Sq](int t) {
       if (t < 2 && qn < Sq) {
         plan.copy(Q, qn, Sq, qd, t * NPW / 2, (t + 1) * NPW / 2);
-        plan.copy(dO, qn, Sq, dd, t * NPW / 2, (t + 1) * NPW / 2);
+        plano.copy(dO, qn, Sq, dd, t * NPW / 2, (t + 1) * NPW / 2);
       }
     };
   };
@@ -682,15 +693,15 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dq(
   __shared__ __attribute__((aligned(1024))) char v1s[TB];
   int64_t tile, bh;
   fa_block(tile, bh, lay.G);
-  Q += lay.head(bh, Sq, D);
-  O += lay.head(bh, Sq, D);
-  dO += lay.head(bh, Sq, D);
-  dQ += lay.head(bh, Sq, D);
-  K += lay.head(bh, Sk, D);
-  V += lay.head(bh, Sk, D);
+  Q += lay.ha(bh, Sq, D);
+  O += lay.ho(bh, Sq, D);
+  dO += lay.ho(bh, Sq, D);
+  dQ += lay.ha(bh, Sq, D);
+  K += lay.ha(bh, Sk, D);
+  V += lay.ha(bh, Sk, D);
   LSE += bh * Sq;
   Dv += bh * Sq;
-  const int rs = lay.rs(D);
+  const int rs = lay.rsa, ro = lay.rso;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int h = lane >> 5, l32 = lane & 31;
   // causal: the last query blocks carry the most keys, so they are dispatched first
@@ -704,7 +715,7 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dq(
 #pragma unroll
   for (int ks = 0; ks < DK; ++ks) {
     qf[ks] = ld8(Q + qc * rs + ks * 16 + h * 8);
-    of[ks] = ld8(dO + qc * rs + ks * 16 + h * 8);
+    of[ks] = ld8(dO + qc * ro + ks * 16 + h * 8);
   }
   const float lq = LSE[qc] * kLog2e;
   // D = rowsum(dO * O) of this lane's query: the two lane halves hold the two halves of
@@ -712,7 +723,7 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_bwd_dq(
   float dsum = 0.f;
 #pragma unroll
   for (int ks = 0; ks < DK; ++ks) {
-    const typename Vec8<T>::type ov = ld8(O + qc * rs + ks * 16 + h * 8);
+    const typename Vec8<T>::type ov = ld8(O + qc * ro + ks * 16 + h * 8);
 #pragma unroll
     for (int e = 0; e < 8; ++e) dsum += (float)ov[e] * (float)of[ks][e];
   }
@@ -881,12 +892,12 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_fwd2(
   __shared__ __attribute__((aligned(1024))) char v1s[TB];
   int64_t tile, bh;
   fa_block(tile, bh, lay.G);
-  Q += lay.head(bh, Sq, D);
-  O += lay.head(bh, Sq, D);
-  K += lay.head(bh, Sk, D);
-  V += lay.head(bh, Sk, D);
+  Q += lay.ha(bh, Sq, D);
+  O += lay.ho(bh, Sq, D);
+  K += lay.ha(bh, Sk, D);
+  V += lay.ha(bh, Sk, D);
   LSE += bh * Sq;
-  const int rs = lay.rs(D);
+  const int rs = lay.rsa, ro = lay.rso;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int h = lane >> 5, l32 = lane & 31;
   // causal: the last query blocks carry the most keys, so they are dispatched first
@@ -982,7 +993,7 @@ __global__ __launch_bounds__(kThreads, OCC) void k_fa_fwd2(
         T w[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) w[i] = (T)(acc[dt][g * 4 + i] * inv);
-        *reinterpret_cast<uint2*>(O + q * rs + dt * 32 + g * 8 + h * 4) =
+        *reinterpret_cast<uint2*>(O + q * ro + dt * 32 + g * 8 + h * 4) =
             *reinterpret_cast<const uint2*>(w);
       }
     if (h == 0) LSE[q] = l > 0.f ? (m + log2f(l)) / kLog2e : -INFINITY;
@@ -1123,12 +1134,12 @@ __global__ __launch_bounds__(kThreads) void k_fa_fwd_gen(const T* __restrict__ Q
   __shared__ __attribute__((aligned(16))) float Vs[32 * LD];
   int64_t tile, bh;
   fa_block(tile, bh, lay.G);
-  Q += lay.head(bh, Sq, D);
-  O += lay.head(bh, Sq, D);
-  K += lay.head(bh, Sk, D);
-  V += lay.head(bh, Sk, D);
+  Q += lay.ha(bh, Sq, D);
+  O += lay.ho(bh, Sq, D);
+  K += lay.ha(bh, Sk, D);
+  V += lay.ha(bh, Sk, D);
   LSE += bh * Sq;
-  const int rs = lay.rs(D);
+  const int rs = lay.rsa, ro = lay.rso;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int h = lane >> 5, l32 = lane & 31;
   const int64_t qb = causal ? (int64_t)gridDim.x - 1 - tile : tile;
@@ -1185,7 +1196,7 @@ __global__ __launch_bounds__(kThreads) void k_fa_fwd_gen(const T* __restrict__ Q
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int d = 32 * db + crow(r, h);
-        if (d < D) O[q * rs + d] = (T)(acc[db][r] * inv);
+        if (d < D) O[q * ro + d] = (T)(acc[db][r] * inv);
       }
     if (h == 0) LSE[q] = l > 0.f ? (m + log2f(l)) / kLog2e : -INFINITY;
   }
@@ -1205,15 +1216,15 @@ __global__ __launch_bounds__(kThreads) void k_fa_bwd_dq_gen(
   __shared__ __attribute__((aligned(16))) float Vs[32 * LD];
   int64_t tile, bh;
   fa_block(tile, bh, lay.G);
-  Q += lay.head(bh, Sq, D);
-  O += lay.head(bh, Sq, D);
-  dO += lay.head(bh, Sq, D);
-  dQ += lay.head(bh, Sq, D);
-  K += lay.head(bh, Sk, D);
-  V += lay.head(bh, Sk, D);
+  Q += lay.ha(bh, Sq, D);
+  O += lay.ho(bh, Sq, D);
+  dO += lay.ho(bh, Sq, D);
+  dQ += lay.ha(bh, Sq, D);
+  K += lay.ha(bh, Sk, D);
+  V += lay.ha(bh, Sk, D);
   LSE += bh * Sq;
   Dv += bh * Sq;
-  const int rs = lay.rs(D);
+  const int rs = lay.rsa, ro = lay.rso;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int h = lane >> 5, l32 = lane & 31;
   const int d0 = blockIdx.z * DO;
@@ -1222,14 +1233,14 @@ __global__ __launch_bounds__(kThreads) void k_fa_bwd_dq_gen(
   const bool qv = q < Sq;
   float qr[NS], dor[NS];
   load_kap<T, DP>(Q, q, rs, D, qv, h, qr);
-  load_kap<T, DP>(dO, q, rs, D, qv, h, dor);
+  load_kap<T, DP>(dO, q, ro, D, qv, h, dor);
   float dsum = 0.f;
 #pragma unroll
   for (int t = 0; t < DP / 8; ++t)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int d = 8 * t + 4 * h + e;
-      if (qv && d < D) dsum += gld(O, q * rs + d) * dor[4 * t + e];
+      if (qv && d < D) dsum += gld(O, q * ro + d) * dor[4 * t + e];
     }
   dsum += __shfl_xor(dsum, 32, 64);
   if (qv && h == 0 && blockIdx.z == 0) Dv[q] = dsum;
@@ -1286,15 +1297,15 @@ __global__ __launch_bounds__(kThreads) void k_fa_bwd_dkdv_gen(
   __shared__ float ls[32], ds[32];
   int64_t tile, bh;
   fa_block(tile, bh, lay.G);
-  Q += lay.head(bh, Sq, D);
-  dO += lay.head(bh, Sq, D);
-  K += lay.head(bh, Sk, D);
-  V += lay.head(bh, Sk, D);
-  dK += lay.head(bh, Sk, D);
-  dV += lay.head(bh, Sk, D);
+  Q += lay.ha(bh, Sq, D);
+  dO += lay.ho(bh, Sq, D);
+  K += lay.ha(bh, Sk, D);
+  V += lay.ha(bh, Sk, D);
+  dK += lay.ha(bh, Sk, D);
+  dV += lay.ha(bh, Sk, D);
   LSE += bh * Sq;
   Dv += bh * Sq;
-  const int rs = lay.rs(D);
+  const int rs = lay.rsa, ro = lay.rso;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int h = lane >> 5, l32 = lane & 31;
   const int d0 = blockIdx.z * DO;
@@ -1315,7 +1326,7 @@ __global__ __launch_bounds__(kThreads) void k_fa_bwd_dkdv_gen(
   for (int64_t q0 = qstart; q0 < Sq; q0 += 32) {
     __syncthreads();
     stage32<T, DP>(Q, q0, Sq, rs, D, Qs);
-    stage32<T, DP>(dO, q0, Sq, rs, D, dOs);
+    stage32<T, DP>(dO, q0, Sq, ro, D, dOs);
     if (threadIdx.x < 32) {
       const int64_t qq = q0 + threadIdx.x;
       ls[threadIdx.x] = qq < Sq ? LSE[qq] * kLog2e : 0.f;
@@ -1466,12 +1477,33 @@ const char* off(const void* p, int64_t elems, int esz) {
   return (const char*)p + elems * esz;
 }
 
+// Layouts: 0 = [B, H, S, D], 1 = [B, S, H, D] (separate tensors), 2 = Q, K and V (and
+// dQ, dK, dV) interleaved in one [B, S, 3, H, D] buffer, O and dO [B, S, H, D].
+int check_layout(int layout, int64_t Sq, int64_t Sk, const char* who) {
+  TG_REQUIRE(layout == 0 || layout == 1 || layout == 2,
+             "%s: layout must be 0 (BHSD), 1 (BSHD) or 2 (packed QKV)", who);
+  TG_REQUIRE(layout != 2 || Sq == Sk, "%s: packed QKV needs Sq == Sk", who);
+  return TG_OK;
+}
+
+FaLay fa_lay(int layout, int64_t H, int64_t D, int G) {
+  const int hd = (int)(H * D);
+  return FaLay{H, layout != 0, G, layout == 0 ? (int)D : layout == 1 ? hd : 3 * hd,
+               layout == 0 ? (int)D : hd};
+}
+
+// Element offset of batch b0 in a Q/K/V-family tensor of S rows.
+int64_t fa_in_off(int layout, int64_t b0, int64_t H, int64_t S, int64_t D) {
+  return (layout == 2 ? 3 : 1) * b0 * H * S * D;
+}
+
 int fa_fwd(int dtype, const void* q, const void* k, const void* v, void* o, float* lse,
            int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D, float scale, int causal,
            int layout, void* stream, const char* who) {
   int st = check_fa(dtype, B, H, Sq, Sk, D, who);
   if (st) return st;
-  TG_REQUIRE(layout == 0 || layout == 1, "%s: layout must be 0 (BHSD) or 1 (BSHD)", who);
+  st = check_layout(layout, Sq, Sk, who);
+  if (st) return st;
   TG_REQUIRE(q && k && v && o && lse, "%s: null pointer", who);
   hipStream_t s = tg_stream(stream);
   const bool fast = fa_fast(dtype, D, {q, k, v, o});
@@ -1479,11 +1511,11 @@ int fa_fwd(int dtype, const void* q, const void* k, const void* v, void* o, floa
   const int64_t nb = fa_batch_chunk(B, H);
   for (int64_t b0 = 0; b0 < B; b0 += nb) {
     const int64_t bn = B - b0 < nb ? B - b0 : nb, BH = bn * H;
-    const int64_t qo = b0 * H * Sq * D, ko = b0 * H * Sk * D;
+    const int64_t qo = fa_in_off(layout, b0, H, Sq, D), ko = fa_in_off(layout, b0, H, Sk, D);
     const void *qc = off(q, qo, es), *kc = off(k, ko, es), *vc = off(v, ko, es);
-    void* oc = (void*)off(o, qo, es);
+    void* oc = (void*)off(o, b0 * H * Sq * D, es);
     float* lc = lse + b0 * H * Sq;
-    const FaLay lay{H, layout, fa_group(BH, causal, 1)};
+    const FaLay lay = fa_lay(layout, H, D, fa_group(BH, causal, 1));
     const int Di = (int)D;
     if (fast) {
       if (dtype == TG_F16)
@@ -1510,7 +1542,8 @@ int fa_bwd(int dtype, const void* q, const void* k, const void* v, const void* o
            int layout, void* workspace, size_t workspace_bytes, void* stream, const char* who) {
   int st = check_fa(dtype, B, H, Sq, Sk, D, who);
   if (st) return st;
-  TG_REQUIRE(layout == 0 || layout == 1, "%s: layout must be 0 (BHSD) or 1 (BSHD)", who);
+  st = check_layout(layout, Sq, Sk, who);
+  if (st) return st;
   TG_REQUIRE(q && k && v && o && dout && lse && dq && dk && dv, "%s: null pointer", who);
   const size_t need = (size_t)(B * H * Sq) * sizeof(float);
   if (!workspace || workspace_bytes < need) {
@@ -1523,15 +1556,16 @@ int fa_bwd(int dtype, const void* q, const void* k, const void* v, const void* o
   const int64_t nb = fa_batch_chunk(B, H);
   for (int64_t b0 = 0; b0 < B; b0 += nb) {
     const int64_t bn = B - b0 < nb ? B - b0 : nb, BH = bn * H;
-    const int64_t qo = b0 * H * Sq * D, ko = b0 * H * Sk * D;
+    const int64_t qo = fa_in_off(layout, b0, H, Sq, D), ko = fa_in_off(layout, b0, H, Sk, D);
+    const int64_t oo = b0 * H * Sq * D;
     const void *qc = off(q, qo, es), *kc = off(k, ko, es), *vc = off(v, ko, es);
-    const void *oc = off(o, qo, es), *gc = off(dout, qo, es);
+    const void *oc = off(o, oo, es), *gc = off(dout, oo, es);
     void* dqc = (void*)off(dq, qo, es);
     void* dkc = (void*)off(dk, ko, es);
     void* dvc = (void*)off(dv, ko, es);
     const float* lc = lse + b0 * H * Sq;
     float* dvec = (float*)workspace + b0 * H * Sq;
-    const FaLay lay{H, layout, fa_group(BH, causal, 0)};
+    const FaLay lay = fa_lay(layout, H, D, fa_group(BH, causal, 0));
     const int Di = (int)D;
     if (fast) {
       if (dtype == TG_F16)
@@ -1571,6 +1605,8 @@ TG_EXPORT int tg_flash_attn_fwd_layout(int dtype, const void* q, const void* k, 
                                        void* o, float* lse, int64_t B, int64_t H, int64_t Sq,
                                        int64_t Sk, int64_t D, float scale, int causal, int layout,
                                        void* stream) {
+  TG_REQUIRE(layout == 0 || layout == 1,
+             "tg_flash_attn_fwd_layout: layout must be 0 (BHSD) or 1 (BSHD)");
   return fa_fwd(dtype, q, k, v, o, lse, B, H, Sq, Sk, D, scale, causal, layout, stream,
                 "tg_flash_attn_fwd_layout");
 }
@@ -1598,7 +1634,30 @@ TG_EXPORT int tg_flash_attn_bwd_layout(int dtype, const void* q, const void* k, 
                                        int64_t Sq, int64_t Sk, int64_t D, float scale, int causal,
                                        int accumulate, int layout, void* workspace,
                                        size_t workspace_bytes, void* stream) {
+  TG_REQUIRE(layout == 0 || layout == 1,
+             "tg_flash_attn_bwd_layout: layout must be 0 (BHSD) or 1 (BSHD)");
   return fa_bwd(dtype, q, k, v, o, dout, lse, dq, dk, dv, B, H, Sq, Sk, D, scale, causal,
                 accumulate, layout, workspace, workspace_bytes, stream,
                 "tg_flash_attn_bwd_layout");
+}
+
+TG_EXPORT int tg_flash_attn_fwd_qkv(int dtype, const void* qkv, void* o, float* lse, int64_t B,
+                                    int64_t H, int64_t S, int64_t D, float scale, int causal,
+                                    void* stream) {
+  TG_REQUIRE(qkv, "tg_flash_attn_fwd_qkv: null pointer");
+  const int es = tg_dtype_size(dtype);
+  return fa_fwd(dtype, qkv, off(qkv, H * D, es), off(qkv, 2 * H * D, es), o, lse, B, H, S, S,
+                D, scale, causal, 2, stream, "tg_flash_attn_fwd_qkv");
+}
+
+TG_EXPORT int tg_flash_attn_bwd_qkv(int dtype, const void* qkv, const void* o, const void* dout,
+                                    const float* lse, void* dqkv, int64_t B, int64_t H, int64_t S,
+                                    int64_t D, float scale, int causal, int accumulate,
+                                    void* workspace, size_t workspace_bytes, void* stream) {
+  TG_REQUIRE(qkv && dqkv, "tg_flash_attn_bwd_qkv: null pointer");
+  const int es = tg_dtype_size(dtype);
+  return fa_bwd(dtype, qkv, off(qkv, H * D, es), off(qkv, 2 * H * D, es), o, dout, lse, dqkv,
+                (void*)off(dqkv, H * D, es), (void*)off(dqkv, 2 * H * D, es), B, H, S, S, D,
+                scale, causal, accumulate, 2, workspace, workspace_bytes, stream,
+                "tg_flash_attn_bwd_qkv");
 }

@@ -13,6 +13,9 @@
 // is multiplied.  Accumulation is fp32; the epilogue applies alpha/beta and converts.
 #include "tg_common.h"
 
+#include <algorithm>
+#include <vector>
+
 namespace {
 
 constexpr int kThreads = 256;
@@ -686,13 +689,15 @@ __device__ __forceinline__ float epi_val(float v, float x, float beta, float c) 
   return v;
 }
 
+// EXT: the caller names the tile (row tile xtm, column tile xtn); otherwise it follows
+// from the block index, XCD-banded.
 template <typename T, typename TC, bool TA, bool TB, int WGM, int WGN, int SM, int SN, int OCC,
-          bool BSUM, int EPI = EPI_NONE>
+          bool BSUM, int EPI = EPI_NONE, bool EXT = false>
 __device__ __forceinline__ void v3_tile(
     int64_t M, int64_t N, int64_t K, float alpha, const T* __restrict__ A, int64_t lda,
     const T* __restrict__ B, int64_t ldb, float beta, TC* __restrict__ C, int64_t ldc,
     const float* __restrict__ bias, float* __restrict__ bsum, void* dbo, int dbt, bool dbacc,
-    TC* __restrict__ X = nullptr, int64_t ldx = 0) {
+    TC* __restrict__ X = nullptr, int64_t ldx = 0, int64_t xtm = 0, int64_t xtn = 0) {
   constexpr int NW = WGM * WGN, TBM = WGM * SM * 32, TBN = WGN * SN * 32;
   constexpr int ATILE = TBM * V3_BK * 2, BTILE = TBN * V3_BK * 2;
   __shared__ __attribute__((aligned(1024))) char a0[ATILE];
@@ -700,11 +705,15 @@ __device__ __forceinline__ void v3_tile(
   __shared__ __attribute__((aligned(1024))) char a1[ATILE];
   __shared__ __attribute__((aligned(1024))) char b1[BTILE];
   constexpr bool AKC = !TA, BKC = TB;
-  const int64_t gx = gridDim.x, gy = gridDim.y;
-  const int64_t T_ = gx * gy;
-  int64_t lin = (int64_t)blockIdx.y * gx + blockIdx.x;
-  if (T_ % 8 == 0) lin = (lin % 8) * (T_ / 8) + lin / 8;  // XCD-contiguous bands
-  const int64_t tm = lin / gx, tn = lin % gx;
+  int64_t tm = xtm, tn = xtn;
+  if constexpr (!EXT) {
+    const int64_t gx = gridDim.x, gy = gridDim.y;
+    const int64_t T_ = gx * gy;
+    int64_t lin = (int64_t)blockIdx.y * gx + blockIdx.x;
+    if (T_ % 8 == 0) lin = (lin % 8) * (T_ / 8) + lin / 8;  // XCD-contiguous bands
+    tm = lin / gx;
+    tn = lin % gx;
+  }
   const int64_t m0 = tm * TBM, n0 = tn * TBN;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = (wave / WGN) * SM * 32, wn = (wave % WGN) * SN * 32;
@@ -994,8 +1003,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void k_gemm_v3e(
       M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, bias, nullptr, nullptr, 0, false, X, ldx);
 }
 
-// A group of same-shape GEMMs C_g (+)= A_g^T B_g with their own operands (weight
-// gradients of several layers), member g = blockIdx.z, passed by value.
+// A group of GEMMs C_g (+)= A_g^T B_g (weight gradients of several layers) with their
+// own operands, a common M and K and each its own N and row strides of B_g and C_g,
+// passed by value.  The members' output tiles form one list: member g owns
+// tiles [tiles[g], tiles[g+1]), row-major over its tile grid.
 constexpr int kGroupMax = 32;
 template <typename T, typename TC>
 struct V3Group {
@@ -1003,19 +1014,30 @@ struct V3Group {
   const T* B[kGroupMax];
   TC* C[kGroupMax];
   void* db[kGroupMax];  // null: no column sums for this member
+  int64_t N[kGroupMax], ldb[kGroupMax], ldc[kGroupMax];
   float beta[kGroupMax];
+  int tiles[kGroupMax + 1];
+  int n;
   unsigned dbacc;       // bit g: add member g's column sums to db's contents
 };
 
 template <typename T, typename TC, int WGM, int WGN, int SM, int SN, bool BSUM>
 __global__ __launch_bounds__(64 * WGM * WGN, 1) void k_gemm_v3g(
-    int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
-    const V3Group<T, TC> g, int dbt) {
+    int64_t M, int64_t K, int64_t lda, const V3Group<T, TC> g, int dbt) {
+  constexpr int TBN = WGN * SN * 32;
+  // XCD-contiguous bands over the whole list (consecutive tiles share operand rows)
+  const int T_ = g.tiles[g.n];
+  int lin = (int)blockIdx.x;
+  if (T_ % 8 == 0) lin = (lin % 8) * (T_ / 8) + lin / 8;
+  int bz = 0;
+  while (bz + 1 < g.n && g.tiles[bz + 1] <= lin) ++bz;
+  const int loc = lin - g.tiles[bz];
+  const int64_t N = g.N[bz], gx = (N + TBN - 1) / TBN;
   // (one v3_tile instance per kernel: each holds its own static LDS stages)
-  const int bz = blockIdx.z;
-  v3_tile<T, TC, true, false, WGM, WGN, SM, SN, 1, BSUM>(
-      M, N, K, 1.f, g.A[bz], lda, g.B[bz], ldb, g.beta[bz], g.C[bz], ldc, nullptr, nullptr,
-      g.db[bz], dbt, (g.dbacc >> bz) & 1u);
+  v3_tile<T, TC, true, false, WGM, WGN, SM, SN, 1, BSUM, EPI_NONE, true>(
+      M, N, K, 1.f, g.A[bz], lda, g.B[bz], g.ldb[bz], g.beta[bz], g.C[bz], g.ldc[bz], nullptr,
+      nullptr,
+      g.db[bz], dbt, (g.dbacc >> bz) & 1u, nullptr, 0, loc / gx, loc % gx);
 }
 
 // Block shapes of the DMA-staged kernel (waves of 64 x 64 of C): 4 x 2 waves
@@ -1411,48 +1433,129 @@ TG_EXPORT int tg_gemm_wgrad(int dtype_ab, int64_t M, int64_t N, int64_t K, const
 }
 
 namespace {
-// One launch of k_gemm_v3g over members [g0, g0 + n) (n <= kGroupMax, every member
-// passing v3_ok): 256x256 blocks (shape 2) or 256x128 blocks (shape 1), whole K per block.
+// One launch of k_gemm_v3g over members idx[0..n) (n <= kGroupMax, every member passing
+// v3_ok): 256x256 blocks (shape 2) or 256x128 blocks (shape 1), whole K per block.
 template <typename T, typename TC>
-int wgrad_group_launch(int shape, int g0, int n, int64_t M, int64_t N, int64_t K,
-                       const void* const* X, int64_t ldx, const void* const* G, int64_t ldg,
-                       void* const* dW, int64_t ldw, const int* acc_w, int dtype_b,
-                       void* const* db, const int* acc_b, hipStream_t s) {
+int wgrad_group_launch(int shape, const int* idx, int n, int64_t M, const int64_t* N,
+                       int64_t K, const void* const* X, int64_t ldx, const void* const* G,
+                       const int64_t* ldg, void* const* dW, const int64_t* ldw,
+                       const int* acc_w, int dtype_b, void* const* db, const int* acc_b,
+                       hipStream_t s) {
   V3Group<T, TC> grp{};
   bool any_b = false;
+  grp.n = n;
+  const int tbn = shape == 2 ? 2 * 4 * 32 : kBigWGN * kBigSN * 32;
+  const int tbm = shape == 2 ? 4 * 2 * 32 : kBigWGM * kBigSM * 32;
+  const int64_t gy = (M + tbm - 1) / tbm;
   for (int i = 0; i < n; ++i) {
-    grp.A[i] = static_cast<const T*>(X[g0 + i]);
-    grp.B[i] = static_cast<const T*>(G[g0 + i]);
-    grp.C[i] = static_cast<TC*>(dW[g0 + i]);
-    grp.beta[i] = acc_w && acc_w[g0 + i] ? 1.f : 0.f;
-    grp.db[i] = db ? db[g0 + i] : nullptr;
+    const int m = idx[i];
+    grp.A[i] = static_cast<const T*>(X[m]);
+    grp.B[i] = static_cast<const T*>(G[m]);
+    grp.C[i] = static_cast<TC*>(dW[m]);
+    grp.N[i] = N[m];
+    grp.ldb[i] = ldg[m];
+    grp.ldc[i] = ldw[m];
+    grp.beta[i] = acc_w && acc_w[m] ? 1.f : 0.f;
+    grp.db[i] = db ? db[m] : nullptr;
+    grp.tiles[i + 1] = grp.tiles[i] + (int)(gy * ((N[m] + tbn - 1) / tbn));
     if (grp.db[i]) {
       any_b = true;
-      if (acc_b && acc_b[g0 + i]) grp.dbacc |= 1u << i;
+      if (acc_b && acc_b[m]) grp.dbacc |= 1u << i;
     }
   }
 #define TG_GG(WGM, WGN, SM, SN)                                                                \
   do {                                                                                         \
-    constexpr int TBM = WGM * SM * 32, TBN = WGN * SN * 32;                                    \
-    dim3 g3((unsigned)((N + TBN - 1) / TBN), (unsigned)((M + TBM - 1) / TBM), (unsigned)n);    \
+    static_assert(WGM * SM * 32 > 0 && WGN * SN * 32 > 0, "tile");                            \
+    dim3 g3((unsigned)grp.tiles[n]);                                                           \
     if (any_b)                                                                                 \
-      k_gemm_v3g<T, TC, WGM, WGN, SM, SN, true><<<g3, 64 * WGM * WGN, 0, s>>>(                 \
-          M, N, K, ldx, ldg, ldw, grp, dtype_b);                                               \
+      k_gemm_v3g<T, TC, WGM, WGN, SM, SN, true><<<g3, 64 * WGM * WGN, 0, s>>>(M, K, ldx, grp,   \
+                                                                            dtype_b);          \
     else                                                                                       \
-      k_gemm_v3g<T, TC, WGM, WGN, SM, SN, false><<<g3, 64 * WGM * WGN, 0, s>>>(                \
-          M, N, K, ldx, ldg, ldw, grp, dtype_b);                                               \
+      k_gemm_v3g<T, TC, WGM, WGN, SM, SN, false><<<g3, 64 * WGM * WGN, 0, s>>>(M, K, ldx, grp,  \
+                                                                             dtype_b);         \
   } while (0)
   if (shape == 2) TG_GG(4, 2, 2, 4);
   else TG_GG(kBigWGM, kBigWGN, kBigSM, kBigSN);
 #undef TG_GG
   return tg_check_launch("tg_gemm_wgrad_group");
 }
+
+size_t wgrad_group_ws(int dtype_ab, int n, int64_t M, const int64_t* N, int64_t K,
+                      int with_bias) {
+  // members that cannot be grouped run one by one through tg_gemm_wgrad, in stream
+  // order over the same workspace
+  size_t w = 0;
+  for (int i = 0; i < n; ++i) w = std::max(w, tg_gemm_wgrad_workspace(dtype_ab, M, N[i], K, with_bias));
+  return w;
+}
+
+int wgrad_group_impl(const char* who, int dtype_ab, int n, int64_t M, const int64_t* N,
+                     int64_t K, const void* const* X, int64_t ldx, const void* const* G,
+                     const int64_t* ldg, int dtype_w, void* const* dW, const int64_t* ldw,
+                     const int* acc_w, int dtype_b, void* const* db, const int* acc_b,
+                     void* workspace, size_t workspace_bytes, void* stream) {
+  TG_REQUIRE(n >= 0 && M >= 0 && K >= 0, "%s: negative extent", who);
+  if (n == 0) return TG_OK;
+  TG_REQUIRE(X && G && dW && N && ldg && ldw, "%s: null pointer array", who);
+  bool with_b = false;
+  for (int i = 0; i < n; ++i) {
+    TG_REQUIRE(N[i] >= 0, "%s: negative extent", who);
+    with_b = with_b || (db && db[i] != nullptr);
+  }
+  const size_t need = wgrad_group_ws(dtype_ab, n, M, N, K, with_b);
+  TG_REQUIRE(workspace_bytes >= need, "%s: workspace of %zu bytes, need %zu", who,
+             workspace_bytes, need);
+  hipStream_t s = tg_stream(stream);
+  const int64_t ncu = tg_num_cus();
+  const bool lowp = dtype_ab == TG_F16 || dtype_ab == TG_BF16;
+  const bool kinds = lowp && M > 0 && K > 0 && (dtype_w == TG_F32 || dtype_w == dtype_ab) &&
+                     (!with_b || dtype_b == TG_F32 || dtype_b == dtype_ab);
+  // members the grouped kernel takes, in order; the rest run one by one
+  int ok[kGroupMax];
+  int g0 = 0;
+  std::vector<char> done(n, 0);
+  while (kinds && g0 < n) {
+    int cnt = 0;
+    int64_t t256 = 0, t128 = 0;
+    int g = g0;
+    for (; g < n && cnt < kGroupMax; ++g) {
+      if (!(dW[g] && N[g] > 0 && ldw[g] >= N[g] &&
+            v3_ok(2, 1, 0, M, N[g], K, X[g], ldx, 0, G[g], ldg[g], 0)))
+        continue;
+      ok[cnt++] = g;
+      t256 += ((M + 255) / 256) * ((N[g] + 255) / 256);
+      t128 += ((M + 255) / 256) * ((N[g] + 127) / 128);
+    }
+    g0 = g;
+    // whole-K blocks only where the members' tiles fill the CUs; else the K split
+    const int shape = t256 >= kHugeTiles * ncu / 4 ? 2 : (t128 >= ncu ? 1 : 0);
+    if (cnt == 0 || shape == 0 || t128 > INT32_MAX) continue;
+    int rc;
+#define TG_WGG(T, TC)                                                                     \
+  rc = wgrad_group_launch<T, TC>(shape, ok, cnt, M, N, K, X, ldx, G, ldg, dW, ldw, acc_w, \
+                                 dtype_b, with_b ? db : nullptr, acc_b, s)
+    if (dtype_ab == TG_F16) {
+      if (dtype_w == TG_F32) TG_WGG(tg_half, float); else TG_WGG(tg_half, tg_half);
+    } else {
+      if (dtype_w == TG_F32) TG_WGG(tg_bf16, float); else TG_WGG(tg_bf16, tg_bf16);
+    }
+#undef TG_WGG
+    if (rc != TG_OK) return rc;
+    for (int i = 0; i < cnt; ++i) done[ok[i]] = 1;
+  }
+  for (int g = 0; g < n; ++g) {
+    if (done[g]) continue;
+    const int rc = tg_gemm_wgrad(dtype_ab, M, N[g], K, X[g], ldx, G[g], ldg[g], dtype_w, dW[g],
+                                 ldw[g], acc_w ? acc_w[g] : 0, dtype_b, db ? db[g] : nullptr,
+                                 acc_b ? acc_b[g] : 0, workspace, workspace_bytes, stream);
+    if (rc != TG_OK) return rc;
+  }
+  return TG_OK;
+}
 }  // namespace
 
 TG_EXPORT size_t tg_gemm_wgrad_group_workspace(int dtype_ab, int n, int64_t M, int64_t N,
                                                int64_t K, int with_bias) {
-  // members that cannot be grouped run one by one through tg_gemm_wgrad, in stream
-  // order over the same workspace
   return n > 0 ? tg_gemm_wgrad_workspace(dtype_ab, M, N, K, with_bias) : 0;
 }
 
@@ -1462,50 +1565,27 @@ TG_EXPORT int tg_gemm_wgrad_group(int dtype_ab, int n, int64_t M, int64_t N, int
                                   const int* acc_w, int dtype_b, void* const* db,
                                   const int* acc_b, void* workspace, size_t workspace_bytes,
                                   void* stream) {
-  TG_REQUIRE(n >= 0 && M >= 0 && N >= 0 && K >= 0, "tg_gemm_wgrad_group: negative extent");
-  if (n == 0) return TG_OK;
-  TG_REQUIRE(X && G && dW, "tg_gemm_wgrad_group: null pointer array");
-  bool with_b = false;
-  for (int i = 0; i < n && db; ++i) with_b = with_b || db[i] != nullptr;
-  const size_t need = tg_gemm_wgrad_group_workspace(dtype_ab, n, M, N, K, with_b);
-  TG_REQUIRE(workspace_bytes >= need, "tg_gemm_wgrad_group: workspace of %zu bytes, need %zu",
-             workspace_bytes, need);
-  hipStream_t s = tg_stream(stream);
-  const int64_t ncu = tg_num_cus();
-  const bool lowp = dtype_ab == TG_F16 || dtype_ab == TG_BF16;
-  bool grouped = lowp && M > 0 && N > 0 && K > 0 && ldw >= N &&
-                 (dtype_w == TG_F32 || dtype_w == dtype_ab) &&
-                 (!with_b || dtype_b == TG_F32 || dtype_b == dtype_ab);
-  for (int i = 0; i < n && grouped; ++i)
-    grouped = dW[i] && v3_ok(2, 1, 0, M, N, K, X[i], ldx, 0, G[i], ldg, 0);
-  int g0 = 0;
-  while (grouped && g0 < n) {
-    const int cnt = (int)std::min<int64_t>(n - g0, kGroupMax);
-    const int64_t t256 = cnt * ((M + 255) / 256) * ((N + 255) / 256);
-    const int64_t t128 = cnt * ((M + 255) / 256) * ((N + 127) / 128);
-    // whole-K blocks only where the members' tiles fill the CUs; else the K split
-    const int shape = t256 >= kHugeTiles * ncu / 4 ? 2 : (t128 >= ncu ? 1 : 0);
-    if (shape == 0) break;
-    int rc;
-#define TG_WGG(T, TC)                                                                   \
-  rc = wgrad_group_launch<T, TC>(shape, g0, cnt, M, N, K, X, ldx, G, ldg, dW, ldw, acc_w, \
-                                 dtype_b, with_b ? db : nullptr, acc_b, s)
-    if (dtype_ab == TG_F16) {
-      if (dtype_w == TG_F32) TG_WGG(tg_half, float); else TG_WGG(tg_half, tg_half);
-    } else {
-      if (dtype_w == TG_F32) TG_WGG(tg_bf16, float); else TG_WGG(tg_bf16, tg_bf16);
-    }
-#undef TG_WGG
-    if (rc != TG_OK) return rc;
-    g0 += cnt;
-  }
-  for (; g0 < n; ++g0) {
-    const int rc = tg_gemm_wgrad(dtype_ab, M, N, K, X[g0], ldx, G[g0], ldg, dtype_w, dW[g0], ldw,
-                                 acc_w ? acc_w[g0] : 0, dtype_b, db ? db[g0] : nullptr,
-                                 acc_b ? acc_b[g0] : 0, workspace, workspace_bytes, stream);
-    if (rc != TG_OK) return rc;
-  }
-  return TG_OK;
+  TG_REQUIRE(n >= 0, "tg_gemm_wgrad_group: negative extent");
+  const std::vector<int64_t> Ns(n, N), lg(n, ldg), lw(n, ldw);
+  return wgrad_group_impl("tg_gemm_wgrad_group", dtype_ab, n, M, Ns.data(), K, X, ldx, G,
+                          lg.data(), dtype_w, dW, lw.data(), acc_w, dtype_b, db, acc_b,
+                          workspace, workspace_bytes, stream);
+}
+
+TG_EXPORT size_t tg_gemm_wgrad_group_n_workspace(int dtype_ab, int n, int64_t M,
+                                                 const int64_t* N, int64_t K, int with_bias) {
+  return n > 0 && N ? wgrad_group_ws(dtype_ab, n, M, N, K, with_bias) : 0;
+}
+
+TG_EXPORT int tg_gemm_wgrad_group_n(int dtype_ab, int n, int64_t M, const int64_t* N, int64_t K,
+                                    const void* const* X, int64_t ldx, const void* const* G,
+                                    const int64_t* ldg, int dtype_w, void* const* dW,
+                                    const int64_t* ldw, const int* acc_w, int dtype_b,
+                                    void* const* db, const int* acc_b, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+  return wgrad_group_impl("tg_gemm_wgrad_group_n", dtype_ab, n, M, N, K, X, ldx, G, ldg,
+                          dtype_w, dW, ldw, acc_w, dtype_b, db, acc_b, workspace,
+                          workspace_bytes, stream);
 }
 
 TG_EXPORT int tg_gemm(int dtype_ab, int dtype_c, int trans_a, int trans_b, int64_t M, int64_t N,

@@ -1,8 +1,9 @@
 """GPT-style training step composed from the tensor_gpu_v2 API.
 
-Pre-LayerNorm decoder: tied token embedding, per layer LN -> Q/K/V/O Linear with
-causal FlashAttention -> residual, LN -> Linear(d, 4d) -> GELU -> Linear(4d, d) ->
-residual; final LN; logits = h @ E^T; CrossEntropyLoss.  The residual adds and the
+Pre-LayerNorm decoder: tied token embedding, per layer LN -> one Q/K/V Linear(d, 3d)
+-> causal FlashAttention on the packed projection (flash_attention_qkv: q, k and v
+read in place, the heads merged on output) -> O Linear -> residual, LN ->
+Linear(d, 4d) -> GELU -> Linear(4d, d) -> residual; final LN; logits = h @ E^T; CrossEntropyLoss.  The residual adds and the
 GELU run in the adjacent Linear GEMMs' epilogues (Linear's residual= / activation=
 options: the same graph and values as the separate ops).  One step runs the forward
 under fp16 autocast, GradScaler.scale(loss).backward(), sync_tied_gradients,
@@ -10,7 +11,7 @@ unscale_, clip_grad_norm_(1.0), GradScaler.step(AdamW) and update().
 
 The reference has no GPT model class on the gradient path; this harness builds the
 configuration from the same public primitives a reference user would combine
-(Embedding, Linear, LayerNorm, flash_attention, CrossEntropyLoss, weight_tie,
+(Embedding, Linear, LayerNorm, flash_attention(_qkv), CrossEntropyLoss, weight_tie,
 sync_tied_gradients, AdamW, GradScaler, clip_grad_norm_).
 """
 import gc
@@ -30,27 +31,18 @@ class Block(tg.Module):
         self.d, self.heads = d, heads
         self.ln1 = tg.LayerNorm(d)
         self.ln2 = tg.LayerNorm(d)
-        self.q = tg.Linear(d, d)
-        self.k = tg.Linear(d, d)
-        self.v = tg.Linear(d, d)
+        self.qkv = tg.Linear(d, 3 * d)  # columns: query heads | key heads | value heads
         self.o = tg.Linear(d, d)
         self.fc1 = tg.Linear(d, 4 * d)
         self.fc2 = tg.Linear(4 * d, d)
-        for lin in (self.q, self.k, self.v, self.o, self.fc1, self.fc2):
+        for lin in (self.qkv, self.o, self.fc1, self.fc2):
             lin.w.data = tg.Tensor(_normal(lin.w.shape, 0.02, rng), requires_grad=False).data
 
     def __call__(self, h):
-        B, T, C = h.shape
-        H, hd = self.heads, C // self.heads
-        a = self.ln1(h)
-
-        def split(t):
-            return t.reshape(B, T, H, hd).transpose(0, 2, 1, 3)
-        att = tg.flash_attention(split(self.q(a)), split(self.k(a)), split(self.v(a)),
-                                 is_causal=True)
+        att = tg.flash_attention_qkv(self.qkv(self.ln1(h)), self.heads, is_causal=True)
         # h + o(att) and fc2(gelu(fc1(m))) + h with the add and the GELU in the GEMMs'
         # epilogues (Linear's keyword options; the same ops, values and gradients)
-        h = self.o(att.transpose(0, 2, 1, 3).reshape(B, T, C), residual=h)
+        h = self.o(att, residual=h)
         m = self.ln2(h)
         return self.fc2(self.fc1(m, activation="gelu"), residual=h)
 

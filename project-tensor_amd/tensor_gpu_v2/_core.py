@@ -96,8 +96,9 @@ def _wgrad_defer(A2, G2, w, wbuf, wacc, b=None, bbuf=None, bacc=False):
 
 
 def _wgrad_flush():
-    """Run the queued weight-gradient products: records of one shape and dtype set as
-    one grouped call, in the order their groups first appear."""
+    """Run the queued weight-gradient products: records of one input shape [K, M] and
+    dtype set (any output width N) as one grouped call, in the order their groups first
+    appear."""
     if not _WG_QUEUE:
         return
     recs = list(_WG_QUEUE)
@@ -107,19 +108,19 @@ def _wgrad_flush():
     groups = {}
     for r in recs:
         A2, G2, wbuf, _, bbuf, _ = r
-        key = (tuple(A2.shape), G2.shape[1], A2.dtype, wbuf.dtype,
-               None if bbuf is None else bbuf.dtype)
+        key = (tuple(A2.shape), A2.dtype, wbuf.dtype, None if bbuf is None else bbuf.dtype)
         groups.setdefault(key, []).append(r)
-    for (a_shape, N, _, _, _), rs in groups.items():
+    for (a_shape, _, _, _), rs in groups.items():
         K = a_shape[1]
         if len(rs) == 1:
             A2, G2, wbuf, wacc, bbuf, bacc = rs[0]
+            N = G2.shape[1]
             L.wgrad(A2, G2, wbuf.view(K, N), wacc, None if bbuf is None else bbuf.view(N), bacc)
         else:
             has_b = rs[0][4] is not None
             L.wgrad_group([r[0] for r in rs], [r[1] for r in rs],
-                          [r[2].view(K, N) for r in rs], [r[3] for r in rs],
-                          [r[4].view(N) for r in rs] if has_b else None,
+                          [r[2].view(K, r[1].shape[1]) for r in rs], [r[3] for r in rs],
+                          [r[4].view(r[1].shape[1]) for r in rs] if has_b else None,
                           [r[5] for r in rs] if has_b else None)
 
 
@@ -1557,6 +1558,56 @@ def flash_attention(query, key, value, block_size=64, is_causal=False, scale=Non
                 key._accumulate(dk.reshape(key.data.shape), True)
             if value._has_grad():
                 value._accumulate(dv.reshape(value.data.shape), True)
+        out._backward = _backward
+    return out
+
+
+def flash_attention_qkv(qkv, num_heads, is_causal=False, scale=None):
+    """Self-attention on one packed projection: qkv (B, S, 3*H*D) holds the query heads in
+    columns [0, HD), the keys in [HD, 2HD) and the values in [2HD, 3HD) (the output of
+    one Linear(d, 3d) in place of the reference module's three projections w_q, w_k,
+    w_v, _training.py:1885-1904).  Returns the merged heads (B, S, H*D): the values of
+    flash_attention on the head splits of the three column blocks followed by the
+    merge-heads transpose (_training.py:1894-1913), from the same kernels reading q, k
+    and v in place, with no split or merge copy.  The backward writes dq, dk and dv
+    straight into qkv's gradient columns.  fp16, bf16 and fp32; float64 runs through
+    flash_attention on copies of the head splits."""
+    x = qkv.data
+    if x.dim() != 3 or x.shape[2] % (3 * num_heads):
+        raise ValueError(f"flash_attention_qkv: qkv must be (B, S, 3*H*D) with H = "
+                         f"{num_heads}, got {tuple(x.shape)}")
+    B, S, C3 = x.shape
+    C = C3 // 3
+    D = C // num_heads
+    scale = scale or D ** -0.5
+    if x.dtype == torch.float64:
+        def heads(t):
+            return t.reshape(B, S, num_heads, D).transpose(0, 2, 1, 3)
+        q, k, v = (heads(qkv[:, :, i * C:(i + 1) * C]) for i in range(3))
+        o = flash_attention(q, k, v, is_causal=is_causal, scale=scale)
+        return o.transpose(0, 2, 1, 3).reshape(B, S, C)
+    if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise TypeError(f"flash_attention_qkv: unsupported dtype {x.dtype}")
+    dt = x.dtype
+    xc = x.contiguous()
+    o, lse = L.flash_attn_fwd_qkv(xc, num_heads, scale, is_causal)
+    out = Tensor._wrap(o, (qkv,), "FlashAttention")
+    if out._requires_grad:
+        def _backward():
+            if not qkv._has_grad():
+                return
+            g = out._grad_out()
+            if g.dtype != dt or not g.is_contiguous():
+                gl = torch.empty(B, S, C, dtype=dt, device=xc.device)
+                _copy_into(gl, g)
+                g = gl
+            buf, acc = qkv._grad_target()
+            if buf.dtype == dt:
+                L.flash_attn_bwd_qkv(xc, o, g, lse, buf, num_heads, scale, is_causal, acc)
+            else:
+                d = torch.empty_like(xc)
+                L.flash_attn_bwd_qkv(xc, o, g, lse, d, num_heads, scale, is_causal, False)
+                L.broadcast_mul_sum(buf, d, accumulate=acc)
         out._backward = _backward
     return out
 

@@ -97,6 +97,9 @@ SIGNATURES = {
     "tg_gemm_wgrad": (_i32, [_i32, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _i32, _vp, _i64, _i32,
                              _i32, _vp, _i32, _vp, _sz, _vp]),
     "tg_gemm_wgrad_group_workspace": (_sz, [_i32, _i32, _i64, _i64, _i64, _i32]),
+    "tg_gemm_wgrad_group_n_workspace": (_sz, [_i32, _i32, _i64, _vp, _i64, _i32]),
+    "tg_gemm_wgrad_group_n": (_i32, [_i32, _i32, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i32,
+                                     _vp, _vp, _vp, _i32, _vp, _vp, _vp, _sz, _vp]),
     "tg_gemm_wgrad_group": (_i32, [_i32, _i32, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _i32,
                                    _vp, _i64, _vp, _i32, _vp, _vp, _vp, _sz, _vp]),
     "tg_flash_attn_fwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
@@ -106,6 +109,10 @@ SIGNATURES = {
     "tg_flash_attn_bwd_layout": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
                                         _i64, _i64, _i64, _i64, _f32, _i32, _i32, _i32, _vp, _sz,
                                         _vp]),
+    "tg_flash_attn_fwd_qkv": (_i32, [_i32, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _i32,
+                                     _vp]),
+    "tg_flash_attn_bwd_qkv": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32,
+                                     _i32, _i32, _vp, _sz, _vp]),
     "tg_flash_attn_bwd_workspace": (_sz, [_i64, _i64, _i64, _i64, _i64]),
     "tg_flash_attn_f64_workspace": (_sz, [_i64, _i64, _i64, _i64]),
     "tg_flash_attn_fwd_f64": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _f64,
@@ -1131,10 +1138,10 @@ def wgrad(x, g, dw, acc_w, db=None, acc_b=False):
 
 
 def wgrad_group(xs, gs, dws, acc_ws, dbs=None, acc_bs=None):
-    """wgrad for n members of one shape at once: dws[i] (+)= xs[i]^T @ gs[i] and
-    dbs[i] (+)= gs[i].sum(0) (dbs None, or an entry None: no bias).  Equal-shaped 16-bit
-    members whose tiles fill the CUs run as one launch; the gradient buffers must be
-    distinct."""
+    """wgrad for n members at once: dws[i] (+)= xs[i]^T @ gs[i] and dbs[i] (+)=
+    gs[i].sum(0) (dbs None, or an entry None: no bias).  The members share xs' shape
+    [K, M]; each gs[i] is [K, N_i] with its own N_i.  16-bit members whose tiles together
+    fill the CUs run as one launch; the gradient buffers must be distinct."""
     n = len(xs)
     if not (len(gs) == len(dws) == len(acc_ws) == n):
         raise ValueError("wgrad_group: xs, gs, dws and acc_ws differ in length")
@@ -1149,14 +1156,16 @@ def wgrad_group(xs, gs, dws, acc_ws, dbs=None, acc_bs=None):
         raise ValueError(f"wgrad_group: x {tuple(x0.shape)} and g {tuple(g0.shape)} must be "
                          "[K, M], [K, N]")
     K, M = x0.shape
-    N = g0.shape[1]
     dbt = next((d.dtype for d in dbs if d is not None), None)
     seen = set()
+    Ns = []
     for x, g, dw, db in zip(xs, gs, dws, dbs):
         for nm, t in (("x", x), ("g", g), ("dw", dw)):
             _dev(t, nm)
-        if tuple(x.shape) != (K, M) or tuple(g.shape) != (K, N):
-            raise ValueError("wgrad_group: members differ in shape")
+        if tuple(x.shape) != (K, M) or g.dim() != 2 or g.shape[0] != K:
+            raise ValueError("wgrad_group: members differ in K or M")
+        N = g.shape[1]
+        Ns.append(N)
         if x.dtype != x0.dtype or g.dtype != x0.dtype or dw.dtype != dws[0].dtype:
             raise TypeError("wgrad_group: members differ in dtype")
         if not (x.is_contiguous() and g.is_contiguous()):
@@ -1178,13 +1187,23 @@ def wgrad_group(xs, gs, dws, acc_ws, dbs=None, acc_bs=None):
     dev = dws[0].device
     ensure_device(dev.index)
     with_b = dbt is not None
-    ws = workspace(lib.tg_gemm_wgrad_group_workspace(dtype_code(x0), n, M, N, K, int(with_b)),
-                   dev)
     accw = (ctypes.c_int * n)(*[int(bool(a)) for a in acc_ws])
     accb = (ctypes.c_int * n)(*[int(bool(a)) for a in acc_bs])
-    _check("tg_gemm_wgrad_group", lib.tg_gemm_wgrad_group(
-        dtype_code(x0), n, M, N, K, _ptr_array(xs), M, _ptr_array(gs), N, dtype_code(dws[0]),
-        _ptr_array(dws), N, accw, _TORCH_TO_CODE[dbt] if with_b else 0,
+    if len(set(Ns)) == 1:
+        N = Ns[0]
+        ws = workspace(lib.tg_gemm_wgrad_group_workspace(dtype_code(x0), n, M, N, K,
+                                                         int(with_b)), dev)
+        _check("tg_gemm_wgrad_group", lib.tg_gemm_wgrad_group(
+            dtype_code(x0), n, M, N, K, _ptr_array(xs), M, _ptr_array(gs), N,
+            dtype_code(dws[0]), _ptr_array(dws), N, accw, _TORCH_TO_CODE[dbt] if with_b else 0,
+            _ptr_array(dbs) if with_b else None, accb, ptr(ws), ws.numel(), stream_handle()))
+        return
+    na = (ctypes.c_int64 * n)(*Ns)
+    ws = workspace(lib.tg_gemm_wgrad_group_n_workspace(dtype_code(x0), n, M, na, K,
+                                                       int(with_b)), dev)
+    _check("tg_gemm_wgrad_group_n", lib.tg_gemm_wgrad_group_n(
+        dtype_code(x0), n, M, na, K, _ptr_array(xs), M, _ptr_array(gs), na, dtype_code(dws[0]),
+        _ptr_array(dws), na, accw, _TORCH_TO_CODE[dbt] if with_b else 0,
         _ptr_array(dbs) if with_b else None, accb, ptr(ws), ws.numel(), stream_handle()))
 
 _CUS = {}
@@ -1338,6 +1357,54 @@ def flash_attn_bwd(q, k, v, o, do, lse, dq, dk, dv, scale, causal, accumulate, l
         dtype_code(q), ptr(q), ptr(k), ptr(v), ptr(o), ptr(do), ptr(lse), ptr(dq), ptr(dk),
         ptr(dv), B, H, Sq, Sk, D, float(scale), int(bool(causal)), int(bool(accumulate)),
         int(layout), ptr(ws), ws.numel(), stream_handle()))
+
+
+def _qkv_dev(qkv, heads):
+    if not isinstance(qkv, torch.Tensor) or not qkv.is_cuda:
+        raise TypeError("qkv must be a torch device tensor")
+    if qkv.dim() != 3 or qkv.shape[2] % (3 * heads) or not qkv.is_contiguous():
+        raise ValueError(f"qkv must be a contiguous (B, S, 3*H*D) tensor with H = {heads}, "
+                         f"got {tuple(qkv.shape)}")
+    B, S, C3 = qkv.shape
+    return B, S, C3 // (3 * heads)
+
+
+def flash_attn_fwd_qkv(qkv, heads, scale, causal):
+    """o, lse = self-attention of the packed projection qkv (B, S, 3*H*D): columns
+    [0, HD) hold the query heads, [HD, 2HD) the keys, [2HD, 3HD) the values, head h at
+    h*D within each.  o is (B, S, H*D) (heads merged), lse (B, H, S) fp32."""
+    B, S, D = _qkv_dev(qkv, heads)
+    if qkv.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise TypeError(f"flash_attn_fwd_qkv: unsupported dtype {qkv.dtype}")
+    o = torch.empty(B, S, heads * D, dtype=qkv.dtype, device=qkv.device)
+    lse = torch.empty(B, heads, S, dtype=torch.float32, device=qkv.device)
+    ensure_device(qkv.device.index)
+    _check("tg_flash_attn_fwd_qkv", load().tg_flash_attn_fwd_qkv(
+        dtype_code(qkv), ptr(qkv), ptr(o), ptr(lse), B, heads, S, D, float(scale),
+        int(bool(causal)), stream_handle()))
+    return o, lse
+
+
+def flash_attn_bwd_qkv(qkv, o, do, lse, dqkv, heads, scale, causal, accumulate):
+    """dqkv (+)= the gradient of flash_attn_fwd_qkv: dq, dk, dv in qkv's column order."""
+    B, S, D = _qkv_dev(qkv, heads)
+    _qkv_dev(dqkv, heads)
+    for n, t in (("o", o), ("do", do)):
+        if not t.is_cuda or tuple(t.shape) != (B, S, heads * D) or not t.is_contiguous():
+            raise ValueError(f"{n} must be a contiguous ({B}, {S}, {heads * D}) device tensor")
+    for n, t in (("o", o), ("do", do), ("dqkv", dqkv)):
+        if t.dtype != qkv.dtype:
+            raise TypeError(f"flash_attn_bwd_qkv: {n} dtype {t.dtype} != {qkv.dtype}")
+    if tuple(dqkv.shape) != tuple(qkv.shape):
+        raise ValueError("flash_attn_bwd_qkv: dqkv shape differs from qkv")
+    _dev(lse, "lse")
+    lib = load()
+    ensure_device(qkv.device.index)
+    ws = workspace(lib.tg_flash_attn_bwd_workspace(B, heads, S, S, D), qkv.device)
+    _check("tg_flash_attn_bwd_qkv", lib.tg_flash_attn_bwd_qkv(
+        dtype_code(qkv), ptr(qkv), ptr(o), ptr(do), ptr(lse), ptr(dqkv), B, heads, S, D,
+        float(scale), int(bool(causal)), int(bool(accumulate)), ptr(ws), ws.numel(),
+        stream_handle()))
 
 
 def cross_entropy_fwd(logits, targets, label_smoothing=0.0):

@@ -140,13 +140,14 @@ def test_linear_autocast_accumulated(cuda):
 
 # ---------------------------------------------------------------- grouped members
 def _group_case(n, M, N, K, dt, wdt, bdt, seed, bias=(), acc=()):
-    """n members with their own operands; bias / acc: member indices with a bias
-    gradient / accumulating into existing gradients."""
+    """n members with their own operands; N: one width or a list of n; bias / acc:
+    member indices with a bias gradient / accumulating into existing gradients."""
     g = torch.Generator(device="cuda").manual_seed(seed)
+    Ns = list(N) if isinstance(N, (list, tuple)) else [N] * n
     xs = [torch.randn(K, M, device="cuda", generator=g).to(dt) for _ in range(n)]
-    gs = [torch.randn(K, N, device="cuda", generator=g).to(dt) for _ in range(n)]
-    w0 = [torch.randn(M, N, device="cuda", generator=g).to(wdt) for _ in range(n)]
-    b0 = [torch.randn(N, device="cuda", generator=g).to(bdt) for _ in range(n)]
+    gs = [torch.randn(K, Ns[i], device="cuda", generator=g).to(dt) for i in range(n)]
+    w0 = [torch.randn(M, Ns[i], device="cuda", generator=g).to(wdt) for i in range(n)]
+    b0 = [torch.randn(Ns[i], device="cuda", generator=g).to(bdt) for i in range(n)]
     dws = [w.clone() for w in w0]
     dbs = [b.clone() if i in bias else None for i, b in enumerate(b0)]
     accs = [i in acc for i in range(n)]
@@ -199,6 +200,17 @@ def test_wgrad_group_ragged_and_rejects(cuda):
         L().wgrad_group([x, x], [x, x], [dw, dw], [False, False])
     with pytest.raises(ValueError):
         L().wgrad_group([x, x[:32]], [x, x[:32]], [dw, torch.empty_like(dw)], [False, False])
+
+
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_wgrad_group_mixed_widths(cuda, dt):
+    """Members of one input shape with different output widths in one launch: the
+    packed Q/K/V (N = 3d) and output (N = d) projections of four blocks; and a mix in
+    which unaligned or small members run one by one beside the grouped ones."""
+    _group_case(8, 1024, [3072] * 4 + [1024] * 4, 8192, dt, torch.float32, torch.float32, 21,
+                bias=set(range(8)), acc={1, 6})
+    _group_case(6, 512, [1536, 100, 512, 776, 2048, 64], 2048, dt, torch.float32,
+                torch.float32, 22, bias={0, 1, 3}, acc={3, 4})
 
 
 def _mlp_grads(defer, seed=4):
