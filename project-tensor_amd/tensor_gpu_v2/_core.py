@@ -67,6 +67,20 @@ def _grad_scale_pending(t, factor):
     _GSCALE[k] = (weakref.ref(t, _gone), (float(factor),))
 
 
+def _grad_scale_pending_many(ts, factor):
+    """_grad_scale_pending for each of ts with one factor (the common case, tensors that
+    already carry an entry, handled inline)."""
+    f = (float(factor),)
+    get = _GSCALE.get
+    for t in ts:
+        k = id(t)
+        e = get(k)
+        if e is not None:
+            _GSCALE[k] = (e[0], e[1] + f)
+        else:
+            _grad_scale_pending(t, f[0])
+
+
 def _grad_factors(t):
     """Pending scaling factors of t's gradient (empty tuple: none)."""
     e = _GSCALE.get(id(t))

@@ -5,6 +5,7 @@ LayerNorm, BatchNorm2D / FusedBatchNormReLU, Adam/AdamW, clip_grad_norm_,
 GradScaler — run their gradient math in libtgbwd's HIP kernels.
 """
 import math
+import operator
 import types
 import warnings
 import weakref
@@ -724,26 +725,31 @@ class Adam:
         bc2 = 1 - self.beta2 ** self.t
         plan = getattr(self, "_planned", None)
         self._planned = None
+        params = self.params
+        live = [p for p in params if p._gz or p._g is not None]
         if plan is not None:
             gbufs, gen, _ = plan
-            if gbufs is None or gen != _lowp._GEN[0] or len(gbufs) != len(self.params) or any(
-                    b is not (p._g if p._has_grad() else None)
-                    for b, p in zip(gbufs, self.params)):
+            if (gbufs is None or gen != _lowp._GEN[0] or len(gbufs) != len(params)
+                    or not all(map(operator.is_, gbufs,
+                                   [p._g if (p._gz or p._g is not None) else None
+                                    for p in params]))):
                 plan = None
         if plan is None:
             plan = self._plan()
         # Scalings pending on the gradients (unscale, clip) go into the launch when every
         # fp32 gradient carries the same one or two; otherwise they are applied first.
-        live = [p for p in self.params if p._has_grad()]
-        fac = {_core._grad_factors(p) for p in live if p.data.dtype == torch.float32}
+        get = _core._GSCALE.get
+        ents = [get(id(p)) for p in live]
+        f32 = [p.data.dtype == torch.float32 for p in live]
+        fac = {(e[1] if e is not None else ()) for e, is32 in zip(ents, f32) if is32}
         gmul = (1.0, 1.0)
         if len(fac) == 1 and 0 < len(next(iter(fac))) <= 2:
             f = next(iter(fac))
             gmul = (f[0], f[1] if len(f) > 1 else 1.0)
         else:
             fac = set()
-        for p in live:
-            if _core._grad_factors(p) and not (fac and p.data.dtype == torch.float32):
+        for p, e, is32 in zip(live, ents, f32):
+            if e is not None and not (fac and is32):
                 _core._settle(p)  # in place: the planned pointers stay valid
         for dt, launch in plan[2]:
             launch(lr, self.beta1, self.beta2, self.eps, wd, bc1, bc2,
@@ -839,8 +845,7 @@ def clip_grad_norm_(parameters, max_norm, norm_type=2.0, error_if_nonfinite=Fals
             return 0.0
         coef = max_norm / (total + 1e-6)
         if coef < 1.0:
-            for p in params:
-                _core._grad_scale_pending(p, coef)
+            _core._grad_scale_pending_many(params, coef)
         return total
     grads = [p.grad for p in params]
     if norm_type == float("inf"):
