@@ -290,7 +290,8 @@ def _op_gpt(torch, L, g):
     from gpt_harness import GPT, Trainer, synthetic_batch
     model = GPT()
     tr = Trainer(model)
-    ids, targets = synthetic_batch()
+    # the synthetic batch is resident in HBM, like every other workload's inputs
+    ids, targets = (L.to_device(a) for a in synthetic_batch())
     nparam = sum(p.size for p in tr.params)
     B, T, H, hd, layers = 8, 1024, 16, 64, 4
     flops = 6 * nparam * B * T + layers * 14 * B * H * T * T * hd // 2

@@ -442,8 +442,10 @@ int tg_gemm_epilogue(int dtype, int epi, int64_t M, int64_t N, int64_t K, const 
 /* Cross-entropy over logits [N, C] with int64 targets (CrossEntropyLoss,
  * _nn.py:1128-1185).  Forward: per-row log-sum-exp lse[N] and per-row loss
  * -log(p[t] + 1e-10) (label smoothing s: -sum_c w_c log(p_c + 1e-10), w = s/C +
- * (1-s) onehot); the caller reduces loss[N].  A target outside [0, C) gives a NaN
- * loss.  dtype fp32/fp16/bf16 (fp64: tg_cross_entropy_fwd_f64). */
+ * (1-s) onehot); the caller reduces loss[N].  A target in [-C, 0) counts from the end
+ * (the reference indexes with NumPy); one outside [-C, C) gives a NaN loss.  This holds
+ * for every cross-entropy entry point.  dtype fp32/fp16/bf16 (fp64:
+ * tg_cross_entropy_fwd_f64). */
 int tg_cross_entropy_fwd(int dtype, const void* logits, const int64_t* targets, int64_t N,
                          int64_t C, float label_smoothing, float* lse, float* loss, void* stream);
 /* tg_cross_entropy_fwd (label smoothing 0) and the gradient grad = (softmax - onehot) *

@@ -10,12 +10,15 @@
 // stores the row's log-sum-exp for the backward, which streams the row once more
 // (rows in reverse launch order) and writes the gradient.  Arithmetic is fp32; the
 // gradient is rounded to its storage dtype once (for fp16 logits, (p - w)/N below
-// fp16's range rounds to zero as in the reference's fp16 arithmetic).  A target
-// outside [0, C) yields a NaN loss and an all-(p*scale) gradient row instead of an
-// out-of-bounds access.
+// fp16's range rounds to zero as in the reference's fp16 arithmetic).  A target in
+// [-C, 0) counts from the end (the reference's NumPy indexing); one outside [-C, C)
+// yields a NaN loss and an all-(p*scale) gradient row instead of an out-of-bounds
+// access.
 #include "tg_common.h"
 
 namespace {
+
+__device__ __forceinline__ int64_t wrap_target(int64_t t, int64_t C) { return t < 0 ? t + C : t; }
 
 // 512-thread workgroups (one row each): measured 5 % faster than 256 for the one-pass
 // and the two-pass forms at [8192, 32000] fp16 (half the serial work per thread).
@@ -130,7 +133,7 @@ __global__ __launch_bounds__(kBlock) void k_ce_fwd(const T* __restrict__ X,
   float m, s;
   row_stats<T, VEC>(x, C, m, s);
   const float lse = block_lse(m, s);
-  const int64_t t = tgt[row];
+  const int64_t t = wrap_target(tgt[row], C);
   const bool valid = t >= 0 && t < C;
   float sum_log = 0.f;
   if (smooth > 0.f) {
@@ -165,7 +168,7 @@ __global__ __launch_bounds__(kBlock) void k_ce_bwd(const T* __restrict__ X,
   const T* x = X + row * C;
   TG* g = G + row * C;
   const float l2 = lse_in[row] * kLog2e;
-  const int64_t t = tgt[row];
+  const int64_t t = wrap_target(tgt[row], C);
   const float wu = smooth / (float)C;  // weight of every class
   const float wt = 1.f - smooth;       // extra weight of the target
   const float wus = wu * scale, wts = wt * scale;
@@ -265,7 +268,7 @@ __global__ __launch_bounds__(kBlock) void k_ce_fwd_grad(const T* __restrict__ X,
       for (int j = 0; j < V; ++j) s += fexp2(fmaf(tg_to_float(w[u].v[j]), kLog2e, -mref));
   }
   const float lse = block_lse(m, s);
-  const int64_t t = tgt[row];
+  const int64_t t = wrap_target(tgt[row], C);
   const bool valid = t >= 0 && t < C;
   if (threadIdx.x == 0) {
     lse_out[row] = lse;

@@ -349,7 +349,7 @@ __global__ __launch_bounds__(kT) void k64_ce_fwd(const double* __restrict__ X,
     sum_log = block_reduce_d(sum_log, false);
   }
   if (threadIdx.x == 0) {
-    const int64_t t = tgt[row];
+    const int64_t t = tgt[row] < 0 ? tgt[row] + C : tgt[row];  // [-C, 0) wraps
     double loss = NAN;
     if (t >= 0 && t < C) {
       const double lpt = log(exp(x[t] - lse) + 1e-10);
@@ -369,7 +369,7 @@ __global__ __launch_bounds__(kT) void k64_ce_bwd(const double* __restrict__ X,
   const double* x = X + row * C;
   double* g = G + row * C;
   const double lse = lse_in[row];
-  const int64_t t = tgt[row];
+  const int64_t t = tgt[row] < 0 ? tgt[row] + C : tgt[row];  // [-C, 0) wraps
   const double wu = smooth / (double)C, wt = 1.0 - smooth;
   for (int64_t i = threadIdx.x; i < C; i += kT) {
     const double w = wu + (i == t ? wt : 0.0);

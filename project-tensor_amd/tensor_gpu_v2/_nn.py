@@ -538,16 +538,16 @@ class CrossEntropyLoss(Module):
         if on_device:
             tg = targets.data if isinstance(targets, Tensor) else targets
             tg = tg.to(device=ld.device, dtype=torch.int64).reshape(-1).contiguous()
-            # negative targets wrap as in the reference; targets outside [-C, C) are
-            # not checked on the device (that would need a device-to-host read)
-            tg = torch.where(tg < 0, tg + C, tg)
+            # negative targets wrap as in the reference (in the kernels); targets
+            # outside [-C, C) are not checked on the device (that would need a
+            # device-to-host read): their loss is NaN
         else:
             host = np.asarray(targets).astype(np.int64, copy=False).reshape(-1)
             # the reference indexes probs[arange(N), targets] (NumPy / CuPy indexing):
             # targets in [-C, 0) wrap, anything outside [-C, C) raises
             if host.size and (host.min() < -C or host.max() >= C):
                 raise IndexError(f"CrossEntropyLoss: target outside [-{C}, {C})")
-            tg = L.to_device(np.where(host < 0, host + C, host), ld.device)
+            tg = L.to_device(host, ld.device)  # negative targets wrap in the kernels
         if tg.numel() != N:
             raise ValueError(f"CrossEntropyLoss: {tg.numel()} targets for {N} rows")
         ldc = ld.contiguous()

@@ -93,6 +93,34 @@ def test_ce_target_range(cuda):
     assert np.isfinite(out[0]) and np.isnan(out[1])
 
 
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16, torch.float64])
+def test_ce_negative_targets_wrap(cuda, tg, dt):
+    """Targets in [-C, 0) count from the end (NumPy indexing, as in the reference) in
+    every kernel: host and device targets give the wrapped targets' loss and gradient
+    bit for bit, through the one-pass, the two-pass and the fp64 paths."""
+    rng = np.random.default_rng(5)
+    N, C = 16, 40
+    xv = rng.standard_normal((N, C)) * 2
+    yw = rng.integers(0, C, N)
+    yn = np.where(np.arange(N) % 2 == 0, yw - C, yw)  # half of them negative
+    npdt = {torch.float32: np.float32, torch.float16: np.float16, torch.float64: np.float64}[dt]
+    out = {}
+    for name, y in (("wrapped", yw), ("host", yn), ("device", torch.as_tensor(yn).cuda())):
+        for gif in (True, False):
+            x = tg.Tensor(xv.astype(npdt), requires_grad=True)
+            loss = tg.CrossEntropyLoss(grad_in_forward=gif)(x, y)
+            loss.backward()
+            out[(name, gif)] = (loss.data.double().cpu(), x.grad.double().cpu())
+    for k, (l, g) in out.items():
+        assert torch.equal(l, out[("wrapped", k[1])][0]), k
+        assert torch.equal(g, out[("wrapped", k[1])][1]), k
+    # below -C: NaN on the device path
+    lse, loss = L().cross_entropy_fwd(torch.zeros(2, 3, device="cuda"),
+                                      torch.tensor([-3, -4], device="cuda"))
+    o = loss.cpu().numpy()
+    assert np.isfinite(o[0]) and np.isnan(o[1])
+
+
 @pytest.mark.parametrize("N,C", [(32, 16), (7, 4096), (64, 32000), (5, 32768), (9, 8)])
 @pytest.mark.parametrize("dt", [torch.float32, torch.float16, torch.bfloat16])
 def test_ce_fwd_grad_equals_fwd_then_bwd(cuda, N, C, dt):
