@@ -486,8 +486,9 @@ int tg_embedding_fwd(int dtype_w, const void* weight, const int64_t* indices, in
  * dout[i] for n_tokens rows of dim elements, grad [num_embeddings, dim].
  * Deterministic: each index's rows are summed in their original order (np.add.at's
  * order); up to 8192 tokens in one launch that writes every gradient row once, more
- * through a stable sort of the indices.  Indices outside [0, num_embeddings) are
- * skipped.  Workspace from tg_embedding_bwd_workspace (0 bytes up to 8192 tokens). */
+ * through a stable sort of the indices.  Indices in [-num_embeddings, 0) count from
+ * the end (the reference's NumPy indexing); indices outside [-num_embeddings,
+ * num_embeddings) are skipped.  Workspace from tg_embedding_bwd_workspace (0 bytes up to 8192 tokens). */
 size_t tg_embedding_bwd_workspace(int64_t n_tokens, int64_t num_embeddings);
 int tg_embedding_bwd(int dtype_dout, const void* dout, const int64_t* indices, int64_t n_tokens,
                      int64_t dim, int dtype_grad, void* grad, int64_t num_embeddings,

@@ -12,7 +12,8 @@
 // the order np.add.at uses, so fp32 results match it exactly.  When not accumulating,
 // every gradient row is zeroed first; for up to 8192 tokens that fill runs in the same
 // launch as the sort (one workgroup sorts, the others write zeros), so the sort's
-// latency hides behind the fill.  Indices outside [0, V) are skipped.
+// latency hides behind the fill.  Indices in [-V, 0) count from the end (NumPy
+// indexing, as the reference's forward gathers); indices outside [-V, V) are skipped.
 //
 // tg_transpose_add: dst[c][r] += alpha * src[r][c] through 64x64 LDS tiles
 // (sync_tied_gradients, _training.py:264-284: source.grad += param.grad.T).
@@ -33,13 +34,15 @@ __device__ __forceinline__ void acc_add(float& a, double v) { a = (float)((doubl
 template <typename TD> using InT = decltype(tg_in(TD()));
 
 constexpr int kSortThreads = 1024;
+
+__device__ __forceinline__ int64_t wrap_index(int64_t k, int64_t V) { return k < 0 ? k + V : k; }
 constexpr int kChunk = 8192;  // keys sorted per workgroup in LDS (two 64 KiB buffers)
 
 // Sort keys: index << pb | position, with pb position bits (32 in 64-bit keys; in
 // 32-bit keys, used when the index and position bits fit, the fewest that hold n - 1).
 template <typename K>
 __device__ __forceinline__ K sort_key(const int64_t* idx, int64_t i, int64_t V, int pb) {
-  const int64_t k = idx[i];
+  const int64_t k = wrap_index(idx[i], V);
   const K key = (k >= 0 && k < V) ? (K)k : (K)V;  // V: skipped
   return key << pb | (K)i;
 }
@@ -283,7 +286,7 @@ __global__ __launch_bounds__(kBandThreads) void k_embed_band(const int64_t* __re
 #pragma unroll
   for (int u = 0; u < KPL; ++u) {
     const int i = t0 + u * 64 + lane;
-    k[u] = i < t1 ? idx[i] : -1;
+    k[u] = i < t1 ? wrap_index(idx[i], V) : -1;
   }
   int c = 0;
 #pragma unroll

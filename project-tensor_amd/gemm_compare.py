@@ -21,12 +21,15 @@ from tensor_gpu_v2 import _lib as L  # noqa: E402
 
 # (name, M, N, K, trans_a, trans_b, out dtype)
 SHAPES = [
-    ("qkvo fwd 8192x1024x1024", 8192, 1024, 1024, False, False, torch.float16),
+    ("o fwd 8192x1024x1024", 8192, 1024, 1024, False, False, torch.float16),
+    ("qkv fwd 8192x3072x1024", 8192, 3072, 1024, False, False, torch.float16),
+    ("qkv dA 8192x1024x3072 (NT)", 8192, 1024, 3072, False, True, torch.float16),
     ("fc1 fwd 8192x4096x1024", 8192, 4096, 1024, False, False, torch.float16),
     ("fc2 fwd 8192x1024x4096", 8192, 1024, 4096, False, False, torch.float16),
     ("head fwd 8192x32000x1024", 8192, 32000, 1024, False, True, torch.float16),
     ("fc1 dA 8192x1024x4096 (NT)", 8192, 1024, 4096, False, True, torch.float16),
-    ("qkvo dW 1024x1024x8192 (TN)", 1024, 1024, 8192, True, False, torch.float32),
+    ("o dW 1024x1024x8192 (TN)", 1024, 1024, 8192, True, False, torch.float32),
+    ("qkv dW 1024x3072x8192 (TN)", 1024, 3072, 8192, True, False, torch.float32),
     ("fc1 dW 1024x4096x8192 (TN)", 1024, 4096, 8192, True, False, torch.float32),
     ("head dA 8192x1024x32000", 8192, 1024, 32000, False, False, torch.float16),
     ("square 8192x8192x8192", 8192, 8192, 8192, False, False, torch.float16),

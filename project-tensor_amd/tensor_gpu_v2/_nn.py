@@ -469,7 +469,7 @@ class Embedding(Module):
         rows = L.embedding_fwd(w, idx, cfg.resolve_dtype(w.dtype))
         out = Tensor._wrap(rows, (weight,), "Embedding")
         dim = self.embedding_dim
-        flat = torch.where(idx < 0, idx + V, idx).reshape(-1)
+        flat = idx.reshape(-1)  # negative indices wrap in the backward kernels too
         if out._requires_grad:
             def _backward():
                 if not weight._has_grad():

@@ -43,13 +43,14 @@ def test_embedding_bwd_half_accumulate_and_bounds(cuda, n, V):
     rng = np.random.default_rng(9)
     dim = 33
     idx = rng.integers(0, V, n)
-    idx[5], idx[6] = -1, V  # out of range: skipped
+    idx[5], idx[6] = -V - 1, V  # out of range: skipped
+    idx[7], idx[8] = -1, -V  # count from the end (rows V-1 and 0)
     d = rng.standard_normal((n, dim)).astype(np.float16)
     base = rng.standard_normal((V, dim)).astype(np.float32)
     grad = torch.tensor(base, device="cuda")
     L().embedding_bwd(torch.tensor(d, device="cuda"), torch.tensor(idx, device="cuda"), grad, True)
-    ok = (idx >= 0) & (idx < V)
-    want = base.astype(np.float64) + O.embedding_bwd(idx[ok], d[ok].astype(np.float64), V)
+    ok = (idx >= -V) & (idx < V)
+    want = base.astype(np.float64) + O.embedding_bwd(idx[ok] % V, d[ok].astype(np.float64), V)
     assert_close(grad, want, RTOL_F32, "accumulated fp16 rows")
 
 
@@ -70,17 +71,18 @@ def test_embedding_module(cuda):
 
 @pytest.mark.parametrize("acc", [False, True])
 def test_embedding_bwd_out_of_range_power_of_two_rows(cuda, acc):
-    """Indices -1 and V with V a power of two share their low bits with the valid keys
-    V-1 and 0; they must still be skipped, and rows V-1 and 0 summed exactly once."""
+    """Indices -V-1 and V with V a power of two share their low bits with the valid keys
+    V-1 and 0; they must still be skipped, and rows V-1 and 0 summed exactly once (-1
+    counts from the end: row V-1, in token order with the other 63s)."""
     V, dim = 64, 24
     rng = np.random.default_rng(21)
-    idx = np.array([63, -1, 0, 64, 63, -1, 0, 64, 5] * 7)
+    idx = np.array([63, -65, 0, 64, 63, -1, 0, 64, 5] * 7)
     d = rng.standard_normal((idx.size, dim)).astype(np.float32)
     base = rng.standard_normal((V, dim)).astype(np.float32)
     grad = torch.tensor(base, device="cuda")
     L().embedding_bwd(torch.tensor(d, device="cuda"), torch.tensor(idx, device="cuda"), grad, acc)
-    ok = (idx >= 0) & (idx < V)
-    want = O.embedding_bwd(idx[ok], d[ok], V)
+    ok = (idx >= -V) & (idx < V)
+    want = O.embedding_bwd(idx[ok] % V, d[ok], V)
     if acc:
         want = base + want.astype(np.float32)
     assert np.array_equal(grad.cpu().numpy(), want.astype(np.float32))
