@@ -139,6 +139,22 @@ int tg_layernorm_bwd_add(int dtype, const void* x, const float* mean, const floa
                          float* dgamma, float* dbeta, int64_t rows, int64_t cols,
                          int accumulate_params, void* workspace, size_t workspace_bytes,
                          void* stream);
+/* With dgamma and dbeta both NULL, tg_layernorm_bwd(_add) leaves the dgamma and dbeta
+ * partials in the workspace's first 2*K*cols floats (K rows each, dgamma's first) for a
+ * later finish; tg_layernorm_bwd_partials gives K for that call's shape and pointers,
+ * or -1 where the partials cannot be finished by tg_sum_partials2_group (fp64, or a
+ * partial count it does not cover).  During Tensor.backward() the LayerNorm closures
+ * (_nn.py:921-942) leave their partials this way and the parameter gradients are
+ * finished together when the sweep ends. */
+int64_t tg_layernorm_bwd_partials(int dtype, const void* x, const void* dy, const void* dx,
+                                  const void* dx_add, int64_t rows, int64_t cols);
+/* n finishes in one launch: out0[i] (+)= column sums of parts[i][0:K[i]][0:cols[i]] and
+ * out1[i] (+)= those of parts[i][K[i]:2K[i]] (fp32; acc[i] non-zero: add to the
+ * outputs; acc NULL: overwrite), each equal to finishing member i on its own.  Host
+ * arrays of n entries; an output may be NULL (skipped). */
+int tg_sum_partials2_group(int n, const float* const* parts, const int64_t* K,
+                           const int64_t* cols, float* const* out0, float* const* out1,
+                           const int* acc, void* stream);
 /* tg_layernorm_bwd without a workspace argument and without any allocation: the
  * partial sums live in a fixed device array of the library (one per GPU, held until
  * the process ends; tg_layernorm_bwd_noalloc_max_scratch() bytes).  No counterpart in

@@ -233,6 +233,9 @@ int tg64_zero_nonfinite(int ntensors, void* const* grads, const int64_t* numel, 
 // into out0 and out1 in one launch (a null output is skipped).  Defined in
 // tg_reduce.hip.
 size_t tg_sum_partials_scratch(int64_t K, int64_t cols, int nb = 1);
+// Whether tg_sum_partials2_group finishes K partial rows of `cols` columns (its members
+// must be finished by the same arithmetic as tg_sum_partials2 would use).
+bool tg_sum_partials_groupable(int64_t K, int64_t cols);
 int tg_sum_partials(const float* in, int64_t K, int64_t cols, int dtype_out, void* out, int acc,
                     float* scratch, hipStream_t s);
 int tg_sum_partials2(const float* in, int64_t K, int64_t cols, int dtype_out, void* out0,

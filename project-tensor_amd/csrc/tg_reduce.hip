@@ -165,7 +165,64 @@ int sum_partials(const float* in, int64_t K, int64_t cols, int dtype_out, Outs o
   return tg_check_launch("sum of partials");
 }
 
+// Several finishes of two stacked partial matrices (dgamma, dbeta) in one launch:
+// member m = blockIdx.z, with its own rows K, columns and outputs; the per-column
+// arithmetic is k_colsum's final pass (the members' K within kDirect), so each output
+// equals that member finished on its own.
+constexpr int kGroupMax = 32;
+struct ColsumGroup {
+  const float* in[kGroupMax];
+  int64_t K[kGroupMax], cols[kGroupMax];
+  float* out[kGroupMax][2];
+  unsigned acc;  // bit m: add member m's sums to its outputs
+};
+
+__global__ __launch_bounds__(kBlock) void k_colsum_group(const ColsumGroup g) {
+  const int m = blockIdx.z, b = blockIdx.y;
+  const int64_t cols = g.cols[m], K = g.K[m];
+  float* out = g.out[m][b];
+  if (out == nullptr || (int64_t)blockIdx.x * 64 >= cols) return;  // uniform per block
+  const float* in = g.in[m] + (int64_t)b * K * cols;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t c = (int64_t)blockIdx.x * 64 + lane;
+  float acc[kU];
+#pragma unroll
+  for (int u = 0; u < kU; ++u) acc[u] = 0.f;
+  if (c < cols) {
+    int64_t r = wave;
+    for (; r + (kU - 1) * kWaves < K; r += kU * kWaves) {
+#pragma unroll
+      for (int u = 0; u < kU; ++u) acc[u] += in[(r + u * kWaves) * cols + c];
+    }
+#pragma unroll
+    for (int u = 0; u < kU - 1; ++u)
+      if (r + u * kWaves < K) acc[u] += in[(r + u * kWaves) * cols + c];
+  }
+#pragma unroll
+  for (int w = kU / 2; w >= 1; w /= 2)
+#pragma unroll
+    for (int u = 0; u < w; ++u) acc[u] += acc[u + w];
+  __shared__ float red[kWaves][64];
+  red[wave][lane] = acc[0];
+  __syncthreads();
+  if (wave == 0 && c < cols) {
+    float v[kWaves];
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) v[w] = red[w][lane];
+#pragma unroll
+    for (int w = kWaves / 2; w >= 1; w /= 2)
+#pragma unroll
+      for (int u = 0; u < w; ++u) v[u] += v[u + w];
+    float sv = v[0];
+    if ((g.acc >> m) & 1u) sv += out[c];
+    out[c] = sv;
+  }
+}
 }  // namespace
+
+bool tg_sum_partials_groupable(int64_t K, int64_t cols) {
+  return K >= 1 && K <= kDirect && !(K <= kNarrowK && cols >= 4096);
+}
 
 size_t tg_sum_partials_scratch(int64_t K, int64_t cols, int nb) {
   if (K <= kDirect) return 0;
@@ -182,4 +239,38 @@ int tg_sum_partials2(const float* in, int64_t K, int64_t cols, int dtype_out, vo
                      void* out1, int acc, float* scratch, hipStream_t s) {
   Outs o{{out0, out1}};
   return sum_partials(in, K, cols, dtype_out, o, 2, acc, scratch, s);
+}
+
+TG_EXPORT int tg_sum_partials2_group(int n, const float* const* parts, const int64_t* K,
+                                     const int64_t* cols, float* const* out0,
+                                     float* const* out1, const int* acc, void* stream) {
+  TG_REQUIRE(n >= 0, "tg_sum_partials2_group: negative count");
+  if (n == 0) return TG_OK;
+  TG_REQUIRE(parts && K && cols && out0 && out1, "tg_sum_partials2_group: null pointer array");
+  for (int i = 0; i < n; ++i) {
+    TG_REQUIRE(parts[i] && cols[i] > 0 && tg_sum_partials_groupable(K[i], cols[i]),
+               "tg_sum_partials2_group: member %d: K = %lld rows of %lld columns not covered "
+               "(1 <= K <= %lld, and not K <= %lld with 4096 or more columns)", i,
+               (long long)K[i], (long long)cols[i], (long long)kDirect, (long long)kNarrowK);
+  }
+  hipStream_t s = tg_stream(stream);
+  for (int g0 = 0; g0 < n; g0 += kGroupMax) {
+    const int cnt = n - g0 < kGroupMax ? n - g0 : kGroupMax;
+    ColsumGroup grp{};
+    int64_t maxc = 0;
+    for (int i = 0; i < cnt; ++i) {
+      grp.in[i] = parts[g0 + i];
+      grp.K[i] = K[g0 + i];
+      grp.cols[i] = cols[g0 + i];
+      grp.out[i][0] = out0[g0 + i];
+      grp.out[i][1] = out1[g0 + i];
+      if (acc && acc[g0 + i]) grp.acc |= 1u << i;
+      maxc = cols[g0 + i] > maxc ? cols[g0 + i] : maxc;
+    }
+    dim3 grid((unsigned)((maxc + 63) / 64), 2, (unsigned)cnt);
+    k_colsum_group<<<grid, kBlock, 0, s>>>(grp);
+    const int st = tg_check_launch("tg_sum_partials2_group");
+    if (st) return st;
+  }
+  return TG_OK;
 }

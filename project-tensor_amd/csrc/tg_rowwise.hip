@@ -926,6 +926,17 @@ TG_EXPORT int tg_layernorm_bwd(int dtype, const void* x, const float* mean, cons
                       accumulate_params, workspace, workspace_bytes, stream);
 }
 
+TG_EXPORT int64_t tg_layernorm_bwd_partials(int dtype, const void* x, const void* dy,
+                                            const void* dx, const void* dx_add, int64_t rows,
+                                            int64_t cols) {
+  if (rows <= 0 || cols <= 0 || dtype == TG_F64) return -1;
+  if (dtype != TG_F32 && dtype != TG_F16 && dtype != TG_BF16) return -1;
+  const bool al = tg_aligned16(x) && tg_aligned16(dy) && tg_aligned16(dx) &&
+                  (!dx_add || tg_aligned16(dx_add));
+  const LnBwdPlan p = ln_bwd_plan_dt(dtype, rows, cols, al);
+  return tg_sum_partials_groupable(p.nparts, cols) ? p.nparts : -1;
+}
+
 TG_EXPORT int tg_layernorm_bwd_add(int dtype, const void* x, const float* mean,
                                    const float* rstd, const float* gamma, const void* dy,
                                    const void* dx_add, void* dx, float* dgamma, float* dbeta,

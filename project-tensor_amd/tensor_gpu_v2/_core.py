@@ -36,6 +36,7 @@ def _noop():
 # queued parameter leaf has already claimed its gradient buffer; any other access to
 # that gradient first flushes the queue, so the order of accumulation is unchanged.
 _WG_QUEUE = []       # (A2, G2, wbuf, wacc, bbuf, bacc) in sweep order
+_LN_QUEUE = []       # LayerNorm parameter gradients: (partials, dgamma buf, dbeta buf, acc)
 _WG_TARGETS = {}     # id -> Tensor whose gradient a queued record writes
 _WG_STATE = [0, 0]   # [backward nesting depth, bytes of operands the queue keeps alive]
 _WG_MAX_BYTES = 4 << 30  # flush early once the queue keeps this much alive
@@ -109,16 +110,33 @@ def _wgrad_defer(A2, G2, w, wbuf, wacc, b=None, bbuf=None, bacc=False):
         _wgrad_flush()
 
 
+def _ln_defer(partials, gamma, dg, beta, db, acc):
+    """Queue the finish of a LayerNorm's parameter gradients (dg/db: the claimed
+    gradient buffers, either may be None) from its partial sums."""
+    _LN_QUEUE.append((partials, dg, db, acc))
+    for p, b in ((gamma, dg), (beta, db)):
+        if b is not None:
+            _WG_TARGETS[id(p)] = p
+    _WG_STATE[1] += partials.numel() * 4
+    if _WG_STATE[1] > _WG_MAX_BYTES:
+        _wgrad_flush()
+
+
 def _wgrad_flush():
     """Run the queued weight-gradient products: records of one input shape [K, M] and
     dtype set (any output width N) as one grouped call, in the order their groups first
-    appear."""
-    if not _WG_QUEUE:
+    appear; and the queued LayerNorm parameter-gradient finishes, all in one launch."""
+    if not _WG_QUEUE and not _LN_QUEUE:
         return
     recs = list(_WG_QUEUE)
+    lns = list(_LN_QUEUE)
     _WG_QUEUE.clear()
+    _LN_QUEUE.clear()
     _WG_TARGETS.clear()
     _WG_STATE[1] = 0
+    if lns:
+        L.sum_partials2_group([r[0] for r in lns], [r[1] for r in lns], [r[2] for r in lns],
+                              [r[3] for r in lns])
     groups = {}
     for r in recs:
         A2, G2, wbuf, _, bbuf, _ = r

@@ -130,6 +130,8 @@ SIGNATURES = {
     "tg_cross_entropy_fwd_grad_max_classes": (_i32, [_i32]),
     "tg_cross_entropy_fwd_grad": (_i32, [_i32, _vp, _vp, _i64, _i64, _vp, _vp, _f32, _vp, _vp]),
     "tg_embedding_bwd_workspace": (_sz, [_i64, _i64]),
+    "tg_layernorm_bwd_partials": (_i64, [_i32, _vp, _vp, _vp, _vp, _i64, _i64]),
+    "tg_sum_partials2_group": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "tg_embedding_fwd": (_i32, [_i32, _vp, _vp, _i64, _i64, _i64, _i32, _vp, _vp]),
     "tg_embedding_bwd": (_i32, [_i32, _vp, _vp, _i64, _i64, _i32, _vp, _i64, _i32, _vp, _sz, _vp]),
     "tg_transpose_add": (_i32, [_i32, _vp, _i64, _i64, _i32, _vp, _f32, _vp]),
@@ -588,6 +590,68 @@ def layernorm_bwd(x, mean, rstd, gamma, dy, dx, dgamma, dbeta, accumulate_dx,
         ptr(dbeta), rows, cols, int(bool(accumulate_dx)), int(bool(accumulate_params)), ptr(ws),
         ws.numel(), stream_handle()))
     return dx
+
+
+def layernorm_bwd_partials(x, mean, rstd, gamma, dy, dx, accumulate_dx, dx_add=None):
+    """layernorm_bwd for dx only, leaving the dgamma/dbeta partial rows for a later
+    sum_partials2_group: returns (partials, K), partials a [2, K, cols] fp32 tensor
+    (dgamma's rows first), or None (nothing done) where that finish does not cover the
+    shape; the caller then runs layernorm_bwd."""
+    if x.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        return None
+    for n, t in (("x", x), ("dy", dy), ("dx", dx), ("mean", mean), ("rstd", rstd),
+                 ("gamma", gamma)):
+        _dev(t, n)
+    _same("layernorm_bwd", x, dy, dx)
+    if dx_add is not None:
+        _dev(dx_add, "dx_add")
+        _same("layernorm_bwd", x, dx_add)
+    cols = gamma.numel()
+    rows = x.numel() // cols
+    lib = load()
+    code = dtype_code(x)
+    K = lib.tg_layernorm_bwd_partials(code, ptr(x), ptr(dy), ptr(dx),
+                                      ptr(dx_add) if dx_add is not None else None, rows, cols)
+    if K <= 0:
+        return None
+    ensure_device(x.device.index)
+    nbytes = lib.tg_layernorm_bwd_workspace(code, rows, cols)
+    ws = torch.empty(max(int(nbytes), 8 * K * cols) // 4 + 1, dtype=torch.float32,
+                     device=x.device)
+    if dx_add is not None:
+        _check("tg_layernorm_bwd_add", lib.tg_layernorm_bwd_add(
+            code, ptr(x), ptr(mean), ptr(rstd), ptr(gamma), ptr(dy), ptr(dx_add), ptr(dx),
+            None, None, rows, cols, 0, ptr(ws), ws.numel() * 4, stream_handle()))
+    else:
+        _check("tg_layernorm_bwd", lib.tg_layernorm_bwd(
+            code, ptr(x), ptr(mean), ptr(rstd), ptr(gamma), ptr(dy), ptr(dx), None, None,
+            rows, cols, int(bool(accumulate_dx)), 0, ptr(ws), ws.numel() * 4,
+            stream_handle()))
+    return ws[: 2 * K * cols].view(2, K, cols), K
+
+
+def sum_partials2_group(parts, dgs, dbs, accs):
+    """dgs[i] (+)= parts[i][0].sum(0) and dbs[i] (+)= parts[i][1].sum(0) for the
+    [2, K, cols] partials of layernorm_bwd_partials, all in one launch (accs[i]: add);
+    fp32 outputs, an output may be None."""
+    n = len(parts)
+    if n == 0:
+        return
+    for t, d, b in zip(parts, dgs, dbs):
+        _dev(t, "partials")
+        if t.dtype != torch.float32 or t.dim() != 3 or t.shape[0] != 2 or not t.is_contiguous():
+            raise ValueError("sum_partials2_group: partials must be contiguous [2, K, cols] fp32")
+        for o in (d, b):
+            if o is not None and (o.dtype != torch.float32 or o.numel() != t.shape[2]
+                                  or not o.is_contiguous()):
+                raise ValueError("sum_partials2_group: outputs must be contiguous fp32 of "
+                                 "cols elements")
+    Ks = (ctypes.c_int64 * n)(*[t.shape[1] for t in parts])
+    cs = (ctypes.c_int64 * n)(*[t.shape[2] for t in parts])
+    acc = (ctypes.c_int * n)(*[int(bool(a)) for a in accs])
+    ensure_device(parts[0].device.index)
+    _check("tg_sum_partials2_group", load().tg_sum_partials2_group(
+        n, _ptr_array(parts), Ks, cs, _ptr_array(dgs), _ptr_array(dbs), acc, stream_handle()))
 
 
 def layernorm_bwd_noalloc(x, mean, rstd, gamma, dy, dx, dgamma, dbeta, accumulate_dx,

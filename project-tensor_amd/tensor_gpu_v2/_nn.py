@@ -256,14 +256,22 @@ class LayerNorm(Module):
                     raise TypeError("LayerNorm parameters must be float32")
                 if x._has_grad():
                     dx, src = x._grad_target_add()
-                    if src is None or src is dx:
-                        L.layernorm_bwd(xd, mean, rstd, g32, dy, dx, dg, db, src is dx, accp)
-                    else:  # x's gradient is shared: the sum goes to x's own buffer
-                        L.layernorm_bwd(xd, mean, rstd, g32, dy, dx, dg, db, True, accp,
-                                        dx_add=src)
+                    acc_dx = src is not None
+                    add = src if src is not None and src is not dx else None
                 else:
-                    L.layernorm_bwd(xd, mean, rstd, g32, dy, torch.empty_like(xd), dg, db,
-                                    False, accp)
+                    dx, acc_dx, add = torch.empty_like(xd), False, None
+                # inside backward(), the parameter gradients' finishing sums are queued
+                # and run with the other layers' in one launch when the sweep ends
+                part = None
+                if _core._WG_STATE[0] > 0 and (dg is not None or db is not None):
+                    part = L.layernorm_bwd_partials(xd, mean, rstd, g32, dy, dx, acc_dx,
+                                                    dx_add=add)
+                if part is not None:
+                    _core._ln_defer(part[0], gamma, dg, beta, db, accp)
+                elif add is not None:  # x's gradient is shared: the sum goes to x's own buffer
+                    L.layernorm_bwd(xd, mean, rstd, g32, dy, dx, dg, db, True, accp, dx_add=add)
+                else:
+                    L.layernorm_bwd(xd, mean, rstd, g32, dy, dx, dg, db, acc_dx, accp)
             out._backward = _backward
         return out
 
