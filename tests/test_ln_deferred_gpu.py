@@ -8,7 +8,7 @@ import torch
 pytestmark = pytest.mark.gpu
 
 
-def _grads(tg, deferred, dt, twice, seed=0):
+def _grads(tg, deferred, dt, twice, seed=0, shared=False):
     from tensor_gpu_v2 import _lib as L
     rng = np.random.default_rng(seed)
     orig = L.layernorm_bwd_partials
@@ -17,6 +17,8 @@ def _grads(tg, deferred, dt, twice, seed=0):
     try:
         d = 256
         lns = [tg.LayerNorm(d) for _ in range(3)]
+        # shared: the first module is applied again as the third (one gamma, two nodes)
+        uses = [lns[0], lns[1], lns[0]] if shared else lns
         for ln in lns:
             ln.gamma.data = torch.as_tensor(1 + 0.1 * rng.standard_normal(d).astype(np.float32)).cuda()
             ln.beta.data = torch.as_tensor(0.1 * rng.standard_normal(d).astype(np.float32)).cuda()
@@ -25,11 +27,12 @@ def _grads(tg, deferred, dt, twice, seed=0):
             with tg.autocast(enabled=dt != torch.float32):
                 h = x * 1.0
                 # the residual stream's gradient is shared with each LayerNorm input
-                for ln in lns:
+                for ln in uses:
                     h = h + ln(h) * 0.5
                 loss = (h * h).mean()
             loss.backward()
-        out = [p.grad.clone() for ln in lns for p in (ln.gamma, ln.beta)] + [x.grad.clone()]
+        out = [p.grad.clone() for ln in dict.fromkeys(uses) for p in (ln.gamma, ln.beta)]
+        out.append(x.grad.clone())
     finally:
         L.layernorm_bwd_partials = orig
     return out
@@ -40,6 +43,17 @@ def _grads(tg, deferred, dt, twice, seed=0):
 def test_deferred_ln_param_grads_equal_immediate(cuda, tg, dt, twice):
     a = _grads(tg, True, dt, twice)
     b = _grads(tg, False, dt, twice)
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16])
+def test_deferred_ln_shared_module(cuda, tg, dt):
+    """A LayerNorm applied twice in one graph: the second node to run finds its gamma's
+    finish queued, which runs first, so the two contributions add in the immediate
+    order."""
+    a = _grads(tg, True, dt, False, shared=True)
+    b = _grads(tg, False, dt, False, shared=True)
     for u, v in zip(a, b):
         assert torch.equal(u, v)
 
