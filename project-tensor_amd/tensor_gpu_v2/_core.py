@@ -536,6 +536,9 @@ class Tensor:
         return self + other
 
     def __mul__(self, other):
+        if (type(other) is float or (type(other) is int and -(1 << 53) <= other <= 1 << 53)) \
+                and self.data.is_floating_point():
+            return self._scalar_mul(other)
         other = self._other(other)
         out = self._out(self.data * other.data, (self, other), "*")
         if out._requires_grad:
@@ -547,6 +550,22 @@ class Tensor:
                         _check_unbroadcast(tuple(g.shape), tuple(t.data.shape))
                         buf, acc = t._grad_target()
                         L.broadcast_mul_sum(buf, g, u.data, accumulate=acc)
+            out._backward = _backward
+        return out
+
+    def _scalar_mul(self, v):
+        """self * v for a Python scalar v and a floating tensor: v rounded to the
+        tensor's dtype (the NumPy 2 weak-scalar rule, as the device scalar of the
+        general path is), one multiply, and g * v in the backward; the same values as
+        the general path, with no scalar tensor made on the device."""
+        vr = _round_scalar(v, self.data.dtype)
+        out = self._out(self.data * vr, (self,), "*")
+        if out._requires_grad:
+            def _backward():
+                if self._has_grad():
+                    g = out._grad_out()
+                    buf, acc = self._grad_target()
+                    L.broadcast_mul_sum(buf, g, alpha=vr, accumulate=acc)
             out._backward = _backward
         return out
 
@@ -1002,6 +1021,27 @@ def _unique(children):
     return tuple(out)
 
 
+_ROUNDED = {}
+
+
+def _round_scalar(v, dt):
+    """The Python number v as a value of floating dtype dt (a Python float): through
+    float64, with the conversion a device cast from float64 applies (for the 16-bit
+    types through float32, as torch's casts do; out of range: inf)."""
+    if dt == torch.float64:
+        return float(v)
+    if dt == torch.float32:
+        with np.errstate(over="ignore"):
+            return float(np.float32(float(v)))
+    key = (float(v), dt)
+    r = _ROUNDED.get(key)
+    if r is None:
+        if len(_ROUNDED) > 4096:
+            _ROUNDED.clear()
+        r = _ROUNDED[key] = torch.tensor(float(v), dtype=torch.float64).to(dt).item()
+    return r
+
+
 def _scalar_like(v, ref):
     """Python scalars / arrays as device tensors.  Float scalars adopt the reference
     tensor's dtype (NumPy 2 weak-scalar promotion keeps fp32 op fp32).  A scalar is
@@ -1243,7 +1283,10 @@ def _linear_operands(x, w):
                         "(float32, float16, bfloat16, float64)")
     K, N = wd.shape
     lead = tuple(a.shape[:-1])
-    A2 = (_as(a, cdt) if cdt == torch.float64 else a.to(cdt).contiguous()).reshape(-1, K)
+    if a.dtype == cdt and a.is_contiguous():
+        A2 = a.view(-1, K)
+    else:
+        A2 = (_as(a, cdt) if cdt == torch.float64 else a.to(cdt).contiguous()).reshape(-1, K)
     wt = not wd.is_contiguous() and wd.t().is_contiguous()
     bc = _weight_operand(w, wd, wt, cdt)  # [N, K] if wt
     return A2, bc, wt, cdt, K, N, lead
@@ -1266,8 +1309,16 @@ def _linear(x, w, b):
         y = L.matmul2d(A2, bc, trans_b=wt)
         L.broadcast_mul_sum(y, b.data.reshape(1, N), accumulate=True)
     elif b is not None:
-        odt = cfg.resolve_dtype(torch.promote_types(cdt, b.data.dtype))
-        bias = b.data.to(torch.float32).contiguous().reshape(N)
+        bd = b.data
+        odt = cfg.resolve_dtype(torch.promote_types(cdt, bd.dtype))
+        if odt in (torch.float32, cdt) and bd.dtype == torch.float32 and bd.dim() == 1 \
+                and bd.numel() == N and bd.is_contiguous():
+            # the operands are built here (contiguous, checked shapes): launch directly
+            L.ensure_device(A2.get_device())
+            y = torch.empty(A2.shape[0], N, dtype=odt, device=a.device)
+            L._gemm_bias_launch(A2, bc, bd, y, wt)
+            return _linear_node(x, w, b, A2, bc, wt, cdt, K, N, y.reshape(*lead, N))
+        bias = bd.to(torch.float32).contiguous().reshape(N)
         if odt in (torch.float32, cdt):
             y = torch.empty(A2.shape[0], N, dtype=odt, device=a.device)
             L.gemm_bias(A2, bc, bias, y, trans_b=wt)
@@ -1361,6 +1412,9 @@ def _linear_node(x, w, b, A2, bc, wt, cdt, K, N, y):
                 if _direct_out(wbuf.dtype, cdt) and _direct_out(bbuf.dtype, cdt):
                     if defer:
                         _wgrad_defer(A2, G2, w, wbuf, wacc, b, bbuf, bacc)
+                    elif A2.is_contiguous() and G2.is_contiguous():
+                        # operands built by this node: launch without re-checking
+                        L._wgrad_launch(A2, G2, wbuf.view(K, N), wacc, bbuf.view(N), bacc)
                     else:
                         L.wgrad(A2, G2, wbuf.view(K, N), wacc, bbuf.view(N), bacc)
                 else:

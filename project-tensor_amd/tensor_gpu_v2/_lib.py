@@ -195,11 +195,12 @@ if hasattr(torch._C, "_cuda_getCurrentRawStream") and hasattr(torch._C, "_cuda_g
     _cur_dev = torch._C._cuda_getDevice
 
     def stream_handle():
-        """The current HIP stream of the current device (torch's current stream)."""
-        return ctypes.c_void_p(_raw_stream(_cur_dev()))
+        """The current HIP stream of the current device (torch's current stream), as
+        the integer handle a c_void_p argument takes."""
+        return _raw_stream(_cur_dev())
 else:
     def stream_handle():
-        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        return torch.cuda.current_stream().cuda_stream
 
 
 # Host-to-device copies of NumPy inputs (token ids, targets, data batches) go through a
@@ -247,7 +248,8 @@ def dtype_code(t):
 
 
 def ptr(t):
-    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+    # a c_void_p argument takes the integer address (None: NULL)
+    return t.data_ptr() if t is not None else None
 
 
 def _dev(t, name):
@@ -475,6 +477,34 @@ def _bcast_strides(t, space):
     return st
 
 
+_BCAST_PLANS = {}
+
+
+def _bcast_plan(out, a, b):
+    """(nd, space, strides of a, b, out) as ctypes int64 arrays for broadcast_mul_sum,
+    cached by the operands' shapes and strides (training loops repeat them)."""
+    key = (a.shape, a.stride(), out.shape, out.stride(),
+           None if b is None else (b.shape, b.stride()))
+    plan = _BCAST_PLANS.get(key)
+    if plan is not None:
+        return plan
+    shapes = [tuple(a.shape), tuple(out.shape)] + ([tuple(b.shape)] if b is not None else [])
+    space = _bcast_space(shapes)
+    if len(out.shape) > len(space):
+        raise ValueError(f"broadcast_mul_sum: out {tuple(out.shape)} has more axes than {space}")
+    for size, stride in zip(out.shape, out.stride()):
+        if size > 1 and stride == 0:
+            raise ValueError("broadcast_mul_sum: out overlaps itself (a zero stride)")
+    nd = len(space)
+    plan = (nd, _i64_array(space), _i64_array(_bcast_strides(a, space)),
+            _i64_array(_bcast_strides(b, space)) if (b is not None and nd) else None,
+            _i64_array(_bcast_strides(out, space)))
+    if len(_BCAST_PLANS) > 4096:
+        _BCAST_PLANS.clear()
+    _BCAST_PLANS[key] = plan
+    return plan
+
+
 def broadcast_mul_sum(out, a, b=None, alpha=1.0, accumulate=False):
     """out (+)= alpha * a * b, with a and b broadcast (NumPy rules) to the index space
     broadcast(a, b, out) and the result summed over every axis where out has extent 1
@@ -487,22 +517,12 @@ def broadcast_mul_sum(out, a, b=None, alpha=1.0, accumulate=False):
             raise TypeError(f"broadcast_mul_sum: {n} must be a torch device tensor")
         if t.dtype not in _BCAST_CODE:
             raise TypeError(f"broadcast_mul_sum: unsupported dtype {t.dtype} for {n}")
-    shapes = [tuple(a.shape), tuple(out.shape)] + ([tuple(b.shape)] if b is not None else [])
-    space = _bcast_space(shapes)
-    if len(out.shape) > len(space):
-        raise ValueError(f"broadcast_mul_sum: out {tuple(out.shape)} has more axes than {space}")
-    for size, stride in zip(out.shape, out.stride()):
-        if size > 1 and stride == 0:
-            raise ValueError("broadcast_mul_sum: out overlaps itself (a zero stride)")
-    sa = _bcast_strides(a, space)
-    so = _bcast_strides(out, space)
-    sb = _bcast_strides(b, space) if b is not None else ()
-    nd = len(space)
-    ensure_device(out.device.index)
-    _check("tg_broadcast_mul_sum", load().tg_broadcast_mul_sum(
-        nd, _i64_array(space), _BCAST_CODE[a.dtype], ptr(a), _i64_array(sa),
-        _BCAST_CODE[b.dtype] if b is not None else 0, ptr(b), _i64_array(sb) if nd else None,
-        _BCAST_CODE[out.dtype], ptr(out), _i64_array(so), float(alpha), int(bool(accumulate)),
+    nd, space, sa, sb, so = _bcast_plan(out, a, b)
+    ensure_device(out.get_device())
+    _check("tg_broadcast_mul_sum", (_lib or load()).tg_broadcast_mul_sum(
+        nd, space, _BCAST_CODE[a.dtype], a.data_ptr(), sa,
+        _BCAST_CODE[b.dtype] if b is not None else 0, b.data_ptr() if b is not None else None,
+        sb, _BCAST_CODE[out.dtype], out.data_ptr(), so, float(alpha), int(bool(accumulate)),
         stream_handle()))
     return out
 
@@ -921,7 +941,7 @@ _SCRATCH = {}
 
 
 def _scratch(key, nbytes, device):
-    k = (key, device, stream_handle().value)  # per stream: calls on one stream are ordered
+    k = (key, device, stream_handle())  # per stream: calls on one stream are ordered
     t = _SCRATCH.get(k)
     if t is None or t.numel() < nbytes:
         t = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
@@ -1171,9 +1191,19 @@ def gemm_bias(a, b, bias, out, trans_b=False):
     if a.dtype != b.dtype or out.dtype not in (torch.float32, a.dtype):
         raise TypeError(f"gemm_bias: dtypes a={a.dtype} b={b.dtype} out={out.dtype}")
     ensure_device(out.device.index)
-    _check("tg_gemm_bias", load().tg_gemm_bias(
-        dtype_code(a), dtype_code(out), 0, int(bool(trans_b)), M, N, K, 1.0, ptr(a), K, ptr(b),
-        b.shape[1], ptr(bias), ptr(out), N, stream_handle()))
+    return _gemm_bias_launch(a, b, bias, out, trans_b)
+
+
+def _gemm_bias_launch(a, b, bias, out, trans_b):
+    """gemm_bias without the argument checks, for callers that built the operands
+    themselves (contiguous a [M, K], b [K, N] or [N, K], fp32 bias [N], out [M, N] on
+    an initialised device)."""
+    M, K = a.shape
+    N = out.shape[1]
+    _check("tg_gemm_bias", (_lib or load()).tg_gemm_bias(
+        _TORCH_TO_CODE[a.dtype], _TORCH_TO_CODE[out.dtype], 0, 1 if trans_b else 0, M, N, K,
+        1.0, a.data_ptr(), K, b.data_ptr(), b.shape[1], bias.data_ptr(), out.data_ptr(), N,
+        stream_handle()))
     return out
 
 
@@ -1208,6 +1238,26 @@ def wgrad(x, g, dw, acc_w, db=None, acc_b=False):
         stream_handle()))
     return dw
 
+
+
+def _wgrad_launch(x, g, dw, acc_w, db, acc_b):
+    """wgrad without the argument checks, for callers that built the operands
+    themselves (contiguous x [K, M] and g [K, N], dw [M, N] and db [N] contiguous, one
+    device); the workspace is this stream's reusable scratch (calls on one stream run in
+    order, and the workspace is consumed within the call)."""
+    K, M = x.shape
+    N = g.shape[1]
+    lib = _lib or load()
+    code = _TORCH_TO_CODE[x.dtype]
+    has_b = db is not None
+    ws = _scratch("wgrad", lib.tg_gemm_wgrad_workspace(code, M, N, K, 1 if has_b else 0),
+                  x.device)
+    _check("tg_gemm_wgrad", lib.tg_gemm_wgrad(
+        code, M, N, K, x.data_ptr(), M, g.data_ptr(), N, _TORCH_TO_CODE[dw.dtype],
+        dw.data_ptr(), N, 1 if acc_w else 0, _TORCH_TO_CODE[db.dtype] if has_b else 0,
+        db.data_ptr() if has_b else None, 1 if acc_b else 0, ws.data_ptr(), ws.numel(),
+        stream_handle()))
+    return dw
 
 
 def wgrad_group(xs, gs, dws, acc_ws, dbs=None, acc_bs=None):
