@@ -160,9 +160,10 @@ def test_flash_full_size_all_heads(cuda, D, causal):
     """C4 shape B=8, H=16, S=2048.  All 128 (b, h) heads are checked element by
     element against float64 torch autograd of softmax(Q K^T s + mask) V (run on the
     device, one batch of 16 heads at a time; rtol 1e-2 with the row-scaled absolute
-    term of assert_close_rows) and through the per-head identities at the fp16 bar; six heads spread over the dispatch's head groups (groups of 8 heads
-    per XCD range: first, last of group 0, first of group 1, both sides of the
-    middle, last) are also checked against the NumPy oracle."""
+    term of assert_close_rows) and through the per-head identities at the fp16 bar;
+    six heads spread over the dispatch's head groups (groups of 8 heads per XCD range:
+    first, last of group 0, first of group 1, both sides of the middle, last) are also
+    checked against the NumPy oracle."""
     B, H, S = 8, 16, 2048
     print(f"C4 full size D={D} causal={causal}", flush=True)
     q, k, v, do = (rnd((B, H, S, D), torch.float16, 10 + s) for s in range(4))
