@@ -24,7 +24,7 @@ def _grads(tg, deferred, dt, twice, seed=0, shared=False):
             ln.beta.data = torch.as_tensor(0.1 * rng.standard_normal(d).astype(np.float32)).cuda()
         x = tg.Tensor(rng.standard_normal((64, 32, d)).astype(np.float32))
         for _ in range(2 if twice else 1):
-            with tg.autocast(enabled=dt != torch.float32):
+            with tg.autocast(enabled=dt != torch.float32, dtype=dt):
                 h = x * 1.0
                 # the residual stream's gradient is shared with each LayerNorm input
                 for ln in uses:
@@ -38,7 +38,7 @@ def _grads(tg, deferred, dt, twice, seed=0, shared=False):
     return out
 
 
-@pytest.mark.parametrize("dt", [torch.float32, torch.float16])
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("twice", [False, True])
 def test_deferred_ln_param_grads_equal_immediate(cuda, tg, dt, twice):
     a = _grads(tg, True, dt, twice)
