@@ -54,3 +54,27 @@ def test_error_path_without_gpu_work():
     assert lib.tg_gemm(0, 0, 0, 0, -1, 1, 1, 1.0, None, 1, 0, None, 1, 0, 0.0, None, 1, 0, 1,
                        None) == -1
     assert lib.tg_version() >= 10000
+
+
+def test_every_entry_point_rejects_invalid_arguments():
+    """Every status-returning entry point refuses NULL pointers (sizes 1) and negative
+    sizes (pointers NULL) with a nonzero status and a message, before any device work
+    (so this runs without a GPU).  Capability queries (int results that are counts) are
+    not status functions and are left out."""
+    import ctypes
+    from tensor_gpu_v2 import _lib
+    lib = _lib.load()
+    skip = {"tg_init", "tg_stream_sync", "tg_cross_entropy_fwd_grad_max_classes"}
+    ints = (ctypes.c_int64, ctypes.c_int, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_int32)
+    checked = 0
+    for name, (res, args) in sorted(_lib.SIGNATURES.items()):
+        if res is not ctypes.c_int or name in skip:
+            continue
+        for size in (-1, 1):
+            vals = [size if a in ints else 1.0 if a in (ctypes.c_float, ctypes.c_double)
+                    else None for a in args]
+            st = getattr(lib, name)(*vals)
+            assert st != 0, f"{name} accepted {'negative sizes' if size < 0 else 'NULL pointers'}"
+            assert lib.tg_last_error(), name
+            checked += 1
+    assert checked >= 100
