@@ -545,3 +545,25 @@ def test_layernorm_bwd_add_matches_in_place(cuda, dt, rows, cols):
     assert torch.equal(out, ref)
     assert torch.equal(add, add0)
     assert torch.equal(dg1, dg2) and torch.equal(db1, db2)
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 200, 128), (129, 257, 64), (64, 72, 40), (520, 136, 192)])
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16, torch.bfloat16])
+def test_gemm_padded_leading_dims(cuda, M, N, K, ta, tb, dt):
+    """A, B and C as sub-blocks of wider buffers (leading dimensions larger than the
+    logical width, kept 16-byte multiples so the DMA-staged path stays eligible): the
+    product equals the one of the compact copies, and C's padding is left untouched."""
+    pa, pb, pc = 64, 8, 16
+    rng = np.random.default_rng(M + 7 * N + 13 * K)
+    ra, ca = (K, M) if ta else (M, K)
+    rb, cb = (N, K) if tb else (K, N)
+    A = dev(rng.standard_normal((ra, ca + pa)), dt)
+    B = dev(rng.standard_normal((rb, cb + pb)), dt)
+    C = dev(rng.standard_normal((M, N + pc)))
+    C0 = C.clone()
+    L().gemm(A, B, C, ta, tb, 1.5, 0.5, M, N, K, ca + pa, cb + pb, N + pc)
+    a, b = f64(A[:, :ca]), f64(B[:, :cb])
+    ref = 1.5 * ((a.T if ta else a) @ (b.T if tb else b)) + 0.5 * f64(C0[:, :N])
+    assert_close(C[:, :N], ref, RTOL_F32_MM, f"gemm padded {dt} {M}x{N}x{K} ta={ta} tb={tb}")
+    assert torch.equal(C[:, N:], C0[:, N:])
