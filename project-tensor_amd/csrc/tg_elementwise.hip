@@ -80,9 +80,12 @@ __global__ __launch_bounds__(kActThreads) void k_act_bwd(const T* __restrict__ x
       tg_st16<NT>(dx + i * V, r);
     }
   }
-  // scalar tail (fewer than V elements), handled by the first block
-  if (blockIdx.x == 0) {
-    for (int64_t i = nvec * V + threadIdx.x; i < n; i += kActThreads) {
+  // scalar part: the tail of fewer than V elements, or every element when an operand is
+  // not 16-byte aligned (nvec == 0); grid-stride over all blocks
+  {
+    const int64_t stride = (int64_t)gridDim.x * kActThreads;
+    for (int64_t i = nvec * V + (int64_t)blockIdx.x * kActThreads + threadIdx.x; i < n;
+         i += stride) {
       const float d = tg_to_float(dy[i]), a = act_grad<OP>(tg_to_float(x[i]));
       const float g = tg_f32(ACC ? fmaf(d, a, tg_to_float(dx[i])) : d * a);
       dx[i] = tg_from_float<T>(g);
@@ -112,10 +115,28 @@ __global__ __launch_bounds__(kActThreads) void k_act_fwd(const T* __restrict__ x
       tg_st16<NT>(y + i * V, r);
     }
   }
-  if (blockIdx.x == 0) {
-    for (int64_t i = nvec * V + threadIdx.x; i < n; i += kActThreads)
+  {
+    const int64_t stride = (int64_t)gridDim.x * kActThreads;
+    for (int64_t i = nvec * V + (int64_t)blockIdx.x * kActThreads + threadIdx.x; i < n;
+         i += stride)
       y[i] = tg_from_float<T>(act_fwd<OP>(tg_to_float(x[i])));
   }
+}
+
+// Grid size: one block per kActThreads*unroll vectors; misaligned operands run the
+// scalar loop grid-stride over a capped grid.  -1 when the grid would exceed the
+// 2^32 work-items a dispatch can hold.
+int64_t act_blocks(bool vec, int64_t nvec, int64_t n, int unroll) {
+  int64_t blocks;
+  if (vec) {
+    blocks = (nvec + kActThreads * unroll - 1) / (kActThreads * unroll);
+  } else {
+    blocks = (n + kActThreads - 1) / kActThreads;
+    const int64_t cap = (int64_t)tg_num_cus() * 16;
+    if (blocks > cap) blocks = cap;
+  }
+  if (blocks < 1) blocks = 1;
+  return blocks * kActThreads > 0xffffffffll ? -1 : blocks;
 }
 
 template <typename T, int OP>
@@ -123,9 +144,8 @@ int launch_act_bwd(const void* x, const void* dy, void* dx, int64_t n, int acc, 
   constexpr int V = tg_vec16<T>::N;
   const bool vec = tg_aligned16(x) && tg_aligned16(dy) && tg_aligned16(dx);
   const int64_t nvec = vec ? n / V : 0;
-  int64_t blocks = (nvec + kActThreads * kUnrollBwd - 1) / (kActThreads * kUnrollBwd);
-  if (blocks < 1) blocks = 1;
-  if (blocks > 0x7fffffff) {
+  const int64_t blocks = act_blocks(vec, nvec, n, kUnrollBwd);
+  if (blocks < 0) {
     tg_set_error("activation backward: n=%lld too large", (long long)n);
     return TG_ERR_INVALID;
   }
@@ -144,8 +164,11 @@ int launch_act_fwd(const void* x, void* y, int64_t n, hipStream_t s) {
   constexpr int V = tg_vec16<T>::N;
   const bool vec = tg_aligned16(x) && tg_aligned16(y);
   const int64_t nvec = vec ? n / V : 0;
-  int64_t blocks = (nvec + kActThreads * kUnrollFwd - 1) / (kActThreads * kUnrollFwd);
-  if (blocks < 1) blocks = 1;
+  const int64_t blocks = act_blocks(vec, nvec, n, kUnrollFwd);
+  if (blocks < 0) {
+    tg_set_error("activation forward: n=%lld too large", (long long)n);
+    return TG_ERR_INVALID;
+  }
   if ((int64_t)sizeof(T) * n >= kNtBytes)
     k_act_fwd<T, OP, true><<<(unsigned)blocks, kActThreads, 0, s>>>((const T*)x, (T*)y, nvec, n);
   else

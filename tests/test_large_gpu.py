@@ -1,0 +1,141 @@
+"""Operands past 2^31 elements: the streaming and row kernels index with 64-bit offsets,
+so windows at the start, across the 2^31 boundary and at the end of one large call must
+match the oracle and the same kernel run on that window alone.  Misaligned operands at
+a few million elements take the scalar loop spread over the whole grid and must equal
+the aligned vector path bit for bit.  GPU only; about 16 GiB of device memory."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from conftest import RTOL_F16, RTOL_F32, assert_close
+
+pytestmark = pytest.mark.gpu
+
+BIG = (1 << 31) + 4099  # not a multiple of the 8-element vector: exercises the tail too
+WIN = 1 << 16
+
+
+def L():
+    from tensor_gpu_v2 import _lib
+    return _lib
+
+
+def f64(t):
+    return t.detach().double().cpu().numpy()
+
+
+def windows(n, w):
+    """Starts of windows at the beginning, across 2^31 and covering the last element."""
+    return [0, (1 << 31) - w // 2, n - w]
+
+
+@pytest.fixture
+def free_after():
+    yield
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("kind", ["gelu", "silu"])
+def test_act_past_2e31(cuda, free_after, kind):
+    gen = torch.Generator(device="cuda").manual_seed(17)
+    x = torch.randn(BIG, dtype=torch.float16, device="cuda", generator=gen) * 3
+    dy = torch.randn(BIG, dtype=torch.float16, device="cuda", generator=gen)
+    dx = torch.empty_like(x)
+    L().act_bwd(kind, x, dy, dx, False)
+    y = L().act_fwd(kind, x)
+    fwd = O.gelu_fwd if kind == "gelu" else O.silu_fwd
+    bwd = O.gelu_bwd if kind == "gelu" else O.silu_bwd
+    for s in windows(BIG, WIN):
+        xs, ds = x[s:s + WIN].clone(), dy[s:s + WIN].clone()
+        got_b, got_f = dx[s:s + WIN], y[s:s + WIN]
+        assert_close(got_b, bwd(f64(xs), f64(ds)), RTOL_F16, f"{kind} bwd window {s}")
+        assert_close(got_f, fwd(f64(xs)), RTOL_F16, f"{kind} fwd window {s}")
+        small = torch.empty_like(xs)
+        L().act_bwd(kind, xs, ds, small, False)
+        assert torch.equal(small, got_b), f"{kind} bwd window {s} differs from a small call"
+        assert torch.equal(L().act_fwd(kind, xs), got_f), f"{kind} fwd window {s}"
+    # accumulate into the same buffer: dx += dy * act'(x), checked on the last window
+    s = BIG - WIN
+    before = dx[s:].float().clone()
+    L().act_bwd(kind, x, dy, dx, True)
+    ref = bwd(f64(x[s:]), f64(dy[s:])) + before.double().cpu().numpy()
+    assert_close(dx[s:], ref, RTOL_F16, f"{kind} accumulate tail")
+
+
+def test_axpby_past_2e31(cuda, free_after):
+    gen = torch.Generator(device="cuda").manual_seed(18)
+    x = torch.randn(BIG, dtype=torch.float16, device="cuda", generator=gen)
+    y = torch.randn(BIG, dtype=torch.float16, device="cuda", generator=gen)
+    y0 = {s: y[s:s + WIN].clone() for s in windows(BIG, WIN)}
+    L().axpby(x, y, 0.5, -2.0)
+    for s, ys in y0.items():
+        want = 0.5 * f64(x[s:s + WIN]) - 2.0 * f64(ys)
+        assert_close(y[s:s + WIN], want, RTOL_F16, f"axpby window {s}")
+        small = ys.clone()
+        L().axpby(x[s:s + WIN].clone(), small, 0.5, -2.0)
+        assert torch.equal(small, y[s:s + WIN]), f"axpby window {s} differs from a small call"
+
+
+def test_layernorm_past_2e31(cuda, free_after):
+    """rows * cols > 2^31 (fp16): per-row outputs on row windows against the oracle, and
+    dgamma / dbeta (sums over every row) against an fp32 sum in row chunks."""
+    cols = 1024
+    rows = (1 << 21) + 5
+    gen = torch.Generator(device="cuda").manual_seed(19)
+    x = torch.randn(rows, cols, dtype=torch.float16, device="cuda", generator=gen)
+    dy = torch.randn(rows, cols, dtype=torch.float16, device="cuda", generator=gen)
+    rng = np.random.default_rng(19)
+    g = torch.as_tensor(1 + 0.02 * rng.standard_normal(cols), dtype=torch.float32).cuda()
+    b = torch.as_tensor(0.02 * rng.standard_normal(cols), dtype=torch.float32).cuda()
+    y, mean, rstd = L().layernorm_fwd(x, g, b, 1e-5)
+    dx = torch.empty_like(x)
+    dg, db = torch.empty_like(g), torch.empty_like(b)
+    L().layernorm_bwd(x, mean, rstd, g, dy, dx, dg, db, False, False)
+    w = 64
+    for r in windows(rows, w):
+        yr, xh, _, var = O.layernorm_fwd(f64(x[r:r + w]), f64(g), f64(b), 1e-5)
+        dxr, _, _ = O.layernorm_bwd(xh, var, f64(g), f64(dy[r:r + w]), 1e-5)
+        assert_close(y[r:r + w], yr, RTOL_F16, f"ln y rows {r}")
+        assert_close(dx[r:r + w], dxr, RTOL_F16, f"ln dx rows {r}")
+    sg = torch.zeros(cols, dtype=torch.float64, device="cuda")
+    sb = torch.zeros(cols, dtype=torch.float64, device="cuda")
+    step = 1 << 16
+    for r in range(0, rows, step):
+        xc = x[r:r + step].float()
+        xh = (xc - mean[r:r + step, None]) * rstd[r:r + step, None]
+        dc = dy[r:r + step].float()
+        sg += (dc * xh).sum(0, dtype=torch.float64)
+        sb += dc.sum(0, dtype=torch.float64)
+    assert_close(dg, sg.cpu().numpy(), RTOL_F32 * 10, "ln dgamma")
+    assert_close(db, sb.cpu().numpy(), RTOL_F32 * 10, "ln dbeta")
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16])
+@pytest.mark.parametrize("kind", ["gelu", "silu"])
+def test_act_misaligned_large_equals_aligned(cuda, dt, kind):
+    """Every operand 2 or 4 bytes off 16-byte alignment runs the scalar loop over a grid
+    of many blocks; its results equal the vector path's bit for bit."""
+    n = 3_000_017
+    gen = torch.Generator(device="cuda").manual_seed(20)
+    x = (torch.randn(n, device="cuda", generator=gen) * 3).to(dt)
+    dy = torch.randn(n, device="cuda", generator=gen).to(dt)
+    base = torch.randn(n, device="cuda", generator=gen).to(dt)
+
+    def off(t):
+        buf = torch.empty(n + 8, dtype=dt, device="cuda")
+        v = buf[1:1 + n]
+        v.copy_(t)
+        return v
+
+    for acc in (False, True):
+        want = base.clone()
+        L().act_bwd(kind, x, dy, want, acc)
+        got = off(base)
+        L().act_bwd(kind, off(x), off(dy), got, acc)
+        assert torch.equal(got, want), f"{kind} bwd acc={acc}"
+    want = L().act_fwd(kind, x)
+    got = off(torch.zeros_like(x))
+    L().act_fwd(kind, off(x), got)
+    assert torch.equal(got, want), f"{kind} fwd"
