@@ -701,6 +701,23 @@ def calibration_copy(torch):
     del src, dst
 
 
+WARM_MS = 50.0
+
+
+def _warm(torch, op, calls):
+    """Untimed runs of op: at least `calls` of them and at least WARM_MS of wall time.
+    The GPU clock ramps up over the first tens of milliseconds of work after an idle
+    gap (a 0.5 ms FlashAttention backward runs ~15 % slower in its first ten calls), so
+    a fixed small count would time part of the ramp."""
+    n, t0 = 0, time.perf_counter()
+    while n < max(1, calls) or (time.perf_counter() - t0) * 1e3 < WARM_MS:
+        op.run(False)
+        n += 1
+        if n % 4 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+
+
 def main():
     a = _args()
     if a.gpus != 1:
@@ -747,9 +764,7 @@ def main():
     if not a.no_components:
         only = set(x for x in a.only.split(",") if x)
         for op in component_ops(torch, L, only):
-            for _ in range(max(1, a.warmup)):
-                op.run(False)
-            torch.cuda.synchronize()
+            _warm(torch, op, a.warmup)
             for _ in range(max(3, a.steps // 2) + 1):
                 op.run(True)
             torch.cuda.synchronize()
@@ -757,8 +772,7 @@ def main():
             if op.unit == "GB/s":
                 best = None
                 for fl in _copy_floors(torch, L, op.work):
-                    for _ in range(max(1, a.warmup)):
-                        fl.run(False)
+                    _warm(torch, fl, a.warmup)
                     for _ in range(max(3, a.steps // 2) + 1):
                         fl.run(True)
                     torch.cuda.synchronize()
