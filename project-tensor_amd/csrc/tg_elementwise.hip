@@ -210,9 +210,18 @@ int dispatch_fwd(int dtype, const void* x, void* y, int64_t n, void* stream) {
 }
 
 // ---------------------------------------------------------------------------
+// v rounded to T; for fp16/bf16 through tg_f32, so that the rounding is never merged
+// with the multiply before it into one single-rounding instruction in one code path
+// (the scalar tail, say) and not in another (the vector body).
+template <typename T>
+__device__ __forceinline__ T tg_round(float v) {
+  return tg_from_float<T>(sizeof(T) == 2 ? tg_f32(v) : v);
+}
+
+// ---------------------------------------------------------------------------
 // z = alpha*x + beta*y   (beta == 0: y is not read; z == y is the in-place update).
 // x and y may differ in dtype, z has y's; arithmetic is fp32 (fp64 when an operand is
-// fp64).  Used for `grad += g`
+// fp64), as fma(beta, y, alpha*x) in every code path.  Used for `grad += g`
 // with a dtype cast, for scaling, and for the out-of-place accumulation into a
 // gradient buffer that another node shares.
 template <typename TX, typename TY>
@@ -221,8 +230,8 @@ __global__ __launch_bounds__(kThreads) void k_axpby(const TX* __restrict__ x, co
   const int64_t stride = (int64_t)gridDim.x * kThreads;
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += stride) {
     float v = alpha * tg_to_float(x[i]);
-    if (beta != 0.f) v += beta * tg_to_float(y[i]);
-    z[i] = tg_from_float<TY>(v);
+    if (beta != 0.f) v = fmaf(beta, tg_to_float(y[i]), v);
+    z[i] = tg_round<TY>(v);
   }
 }
 
@@ -244,7 +253,7 @@ __device__ __forceinline__ void st8f(T* p, const float (&f)[8]) {
   for (int h = 0; h < 8 / V; ++h) {
     tg_vec16<T> v;
 #pragma unroll
-    for (int j = 0; j < V; ++j) v.v[j] = tg_from_float<T>(f[h * V + j]);
+    for (int j = 0; j < V; ++j) v.v[j] = tg_round<T>(f[h * V + j]);
     tg_store16(p + h * V, v);
   }
 }
@@ -260,14 +269,14 @@ __global__ __launch_bounds__(kThreads) void k_axpby8(const TX* __restrict__ x, c
     ld8f(x + i * 8, a);
     if (READ_Y) ld8f(y + i * 8, b);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) a[j] = READ_Y ? alpha * a[j] + beta * b[j] : alpha * a[j];
+    for (int j = 0; j < 8; ++j) a[j] = READ_Y ? fmaf(beta, b[j], alpha * a[j]) : alpha * a[j];
     st8f(z + i * 8, a);
   }
   if (blockIdx.x == 0) {
     for (int64_t i = n8 * 8 + threadIdx.x; i < n; i += kThreads) {
       float v = alpha * tg_to_float(x[i]);
-      if (READ_Y) v += beta * tg_to_float(y[i]);
-      z[i] = tg_from_float<TY>(v);
+      if (READ_Y) v = fmaf(beta, tg_to_float(y[i]), v);
+      z[i] = tg_round<TY>(v);
     }
   }
 }

@@ -40,8 +40,12 @@ template <typename T> __device__ __forceinline__ typename Acc<T>::type up(T v) {
   return (typename Acc<T>::type)tg_to_float(v);
 }
 template <> __device__ __forceinline__ double up<double>(double v) { return v; }
+// fp16/bf16: the fp32 value is materialised first (tg_f32), so the rounding to T cannot
+// be merged with the operation before it into one single-rounding mixed-precision
+// instruction in one code path and not in another (the vector body and the scalar loop
+// then round every element alike).
 template <typename T> __device__ __forceinline__ T down(typename Acc<T>::type v) {
-  return tg_from_float<T>(v);
+  return tg_from_float<T>(sizeof(T) == 2 ? tg_f32(v) : v);
 }
 template <> __device__ __forceinline__ double down<double>(double v) { return v; }
 
@@ -84,7 +88,9 @@ __device__ __forceinline__ C ugrad(C a, C g, C p, C pm1, int ek) {
   }
 }
 
-// One 16-byte vector per operand and thread; a scalar tail in block 0.
+// One 16-byte vector per operand and thread; then a scalar loop, grid-stride over all
+// blocks, for the tail of fewer than V elements or, when an operand is not 16-byte
+// aligned (nvec == 0), for every element.
 template <typename T, int OP, bool ACC>
 __global__ __launch_bounds__(kThreads) void k_unary_bwd(const T* __restrict__ a,
                                                         const T* __restrict__ dy,
@@ -107,43 +113,50 @@ __global__ __launch_bounds__(kThreads) void k_unary_bwd(const T* __restrict__ a,
     }
     tg_store16(dx + i * V, r);
   }
-  if (blockIdx.x == 0) {
-    for (int64_t k = nvec * V + threadIdx.x; k < n; k += kThreads) {
-      C v = ugrad<OP, C>(up<T>(a[k]), up<T>(dy[k]), pc, pm1, ek);
-      if (ACC) v = up<T>(dx[k]) + v;
-      dx[k] = down<T>(v);
-    }
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  for (int64_t k = nvec * V + i; k < n; k += stride) {
+    C v = ugrad<OP, C>(up<T>(a[k]), up<T>(dy[k]), pc, pm1, ek);
+    if (ACC) v = up<T>(dx[k]) + v;
+    dx[k] = down<T>(v);
   }
 }
 
 template <typename T, int OP>
-void launch_unary(const void* a, const void* dy, void* dx, int64_t n, double p, int ek, int acc,
-                  hipStream_t s) {
+int launch_unary(const void* a, const void* dy, void* dx, int64_t n, double p, int ek, int acc,
+                 hipStream_t s) {
   constexpr int V = tg_vec16<T>::N;
   const bool vec = tg_aligned16(a) && tg_aligned16(dy) && tg_aligned16(dx);
   const int64_t nvec = vec ? n / V : 0;
-  int64_t blocks = (nvec + kThreads - 1) / kThreads;
+  // one block per kThreads vectors; misaligned operands: the scalar loop over a capped
+  // grid
+  int64_t blocks = vec ? (nvec + kThreads - 1) / kThreads : (n + kThreads - 1) / kThreads;
+  if (!vec && blocks > (int64_t)tg_num_cus() * 16) blocks = (int64_t)tg_num_cus() * 16;
   if (blocks < 1) blocks = 1;
+  if (blocks * kThreads > 0xffffffffll) {  // a dispatch holds at most 2^32 work-items
+    tg_set_error("tg_unary_bwd: n=%lld too large", (long long)n);
+    return TG_ERR_INVALID;
+  }
   if (acc)
     k_unary_bwd<T, OP, true><<<(unsigned)blocks, kThreads, 0, s>>>(
         (const T*)a, (const T*)dy, (T*)dx, nvec, n, p, ek);
   else
     k_unary_bwd<T, OP, false><<<(unsigned)blocks, kThreads, 0, s>>>(
         (const T*)a, (const T*)dy, (T*)dx, nvec, n, p, ek);
+  return TG_OK;
 }
 
 template <typename T>
-void unary_t(int op, const void* a, const void* dy, void* dx, int64_t n, double p, int ek,
-             int acc, hipStream_t s) {
+int unary_t(int op, const void* a, const void* dy, void* dx, int64_t n, double p, int ek,
+            int acc, hipStream_t s) {
   switch (op) {
-    case U_RELU: launch_unary<T, U_RELU>(a, dy, dx, n, p, ek, acc, s); break;
-    case U_LEAKY: launch_unary<T, U_LEAKY>(a, dy, dx, n, p, ek, acc, s); break;
-    case U_SIGMOID: launch_unary<T, U_SIGMOID>(a, dy, dx, n, p, ek, acc, s); break;
-    case U_TANH: launch_unary<T, U_TANH>(a, dy, dx, n, p, ek, acc, s); break;
-    case U_EXP: launch_unary<T, U_EXP>(a, dy, dx, n, p, ek, acc, s); break;
-    case U_LOG: launch_unary<T, U_LOG>(a, dy, dx, n, p, ek, acc, s); break;
-    case U_SWISH: launch_unary<T, U_SWISH>(a, dy, dx, n, p, ek, acc, s); break;
-    default: launch_unary<T, U_POW>(a, dy, dx, n, p, ek, acc, s); break;
+    case U_RELU: return launch_unary<T, U_RELU>(a, dy, dx, n, p, ek, acc, s);
+    case U_LEAKY: return launch_unary<T, U_LEAKY>(a, dy, dx, n, p, ek, acc, s);
+    case U_SIGMOID: return launch_unary<T, U_SIGMOID>(a, dy, dx, n, p, ek, acc, s);
+    case U_TANH: return launch_unary<T, U_TANH>(a, dy, dx, n, p, ek, acc, s);
+    case U_EXP: return launch_unary<T, U_EXP>(a, dy, dx, n, p, ek, acc, s);
+    case U_LOG: return launch_unary<T, U_LOG>(a, dy, dx, n, p, ek, acc, s);
+    case U_SWISH: return launch_unary<T, U_SWISH>(a, dy, dx, n, p, ek, acc, s);
+    default: return launch_unary<T, U_POW>(a, dy, dx, n, p, ek, acc, s);
   }
 }
 
@@ -298,15 +311,17 @@ TG_EXPORT int tg_unary_bwd(int dtype, int op, const void* a, const void* dy, voi
   // exponent p - 1 of the power rule, by its exact form
   const double e = param - 1.0;
   const int ek = e == 0.0 ? 0 : e == 1.0 ? 1 : e == 2.0 ? 2 : e == 0.5 ? 3 : e == -1.0 ? 4 : 5;
+  int st;
   switch (dtype) {
-    case TG_F32: unary_t<float>(op, a, dy, dx, n, param, ek, accumulate, s); break;
-    case TG_F16: unary_t<tg_half>(op, a, dy, dx, n, param, ek, accumulate, s); break;
-    case TG_BF16: unary_t<tg_bf16>(op, a, dy, dx, n, param, ek, accumulate, s); break;
-    case TG_F64: unary_t<double>(op, a, dy, dx, n, param, ek, accumulate, s); break;
+    case TG_F32: st = unary_t<float>(op, a, dy, dx, n, param, ek, accumulate, s); break;
+    case TG_F16: st = unary_t<tg_half>(op, a, dy, dx, n, param, ek, accumulate, s); break;
+    case TG_BF16: st = unary_t<tg_bf16>(op, a, dy, dx, n, param, ek, accumulate, s); break;
+    case TG_F64: st = unary_t<double>(op, a, dy, dx, n, param, ek, accumulate, s); break;
     default:
       tg_set_error("tg_unary_bwd: unsupported dtype %d", dtype);
       return TG_ERR_UNSUPPORTED;
   }
+  if (st != TG_OK) return st;
   return tg_check_launch("tg_unary_bwd");
 }
 

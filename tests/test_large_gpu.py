@@ -139,3 +139,57 @@ def test_act_misaligned_large_equals_aligned(cuda, dt, kind):
     got = off(torch.zeros_like(x))
     L().act_fwd(kind, off(x), got)
     assert torch.equal(got, want), f"{kind} fwd"
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16, torch.float64])
+@pytest.mark.parametrize("op,param", [("relu", 0.0), ("leaky_relu", 0.01), ("sigmoid", 0.0),
+                                      ("tanh", 0.0), ("exp", 0.0), ("log", 0.0), ("swish", 1.0),
+                                      ("pow", 3.0)])
+def test_unary_misaligned_large_equals_aligned(cuda, dt, op, param):
+    """tg_unary_bwd with every operand off 16-byte alignment (the scalar loop over a grid
+    of many blocks) equals the aligned vector path bit for bit, plain and accumulating."""
+    n = 1_500_007
+    gen = torch.Generator(device="cuda").manual_seed(21)
+    a = torch.rand(n, device="cuda", generator=gen).to(dt) + 0.5  # log and pow need a > 0
+    dy = torch.randn(n, device="cuda", generator=gen).to(dt)
+    base = torch.randn(n, device="cuda", generator=gen).to(dt)
+
+    def off(t):
+        buf = torch.empty(n + 8, dtype=dt, device="cuda")
+        v = buf[1:1 + n]
+        v.copy_(t)
+        return v
+
+    for acc in (False, True):
+        want = base.clone()
+        L().unary_bwd(op, a, dy, want, acc, param)
+        got = off(base)
+        L().unary_bwd(op, off(a), off(dy), got, acc, param)
+        assert torch.equal(got, want), f"{op} {dt} acc={acc}"
+
+
+@pytest.mark.parametrize("dx_,dy_", [(torch.float32, torch.float16), (torch.float16, torch.float16),
+                                     (torch.float32, torch.bfloat16), (torch.float16, torch.float32)])
+@pytest.mark.parametrize("beta", [0.0, 0.75])
+def test_axpby_paths_round_alike(cuda, dx_, dy_, beta):
+    """tg_axpbyz: the 8-wide vector body, its scalar tail and the misaligned kernel give
+    the same bits for the same elements."""
+    n = 1_000_003  # 3 tail elements
+    gen = torch.Generator(device="cuda").manual_seed(22)
+    x = torch.randn(n, device="cuda", generator=gen).to(dx_)
+    y = torch.randn(n, device="cuda", generator=gen).to(dy_)
+    want = L().axpbyz(x, y, 1.3, beta)
+
+    def off(t):
+        buf = torch.empty(n + 8, dtype=t.dtype, device="cuda")
+        v = buf[1:1 + n]
+        v.copy_(t)
+        return v
+
+    got = L().axpbyz(off(x), off(y), 1.3, beta, out=off(torch.zeros_like(y)))
+    assert torch.equal(got, want)
+    # the last 16 elements (3 of them the aligned call's scalar tail) as a call of their
+    # own, where all 16 run through the vector body
+    k = n - 16
+    part = L().axpbyz(x[k:].clone(), y[k:].clone(), 1.3, beta)
+    assert torch.equal(part, want[k:])
