@@ -1050,9 +1050,11 @@ bool v3_ok(int elem, int ta, int tb, int64_t M, int64_t N, int64_t K, const void
   const int VE = 16 / elem;
   const bool vec = tg_aligned16(A) && tg_aligned16(B) && lda % VE == 0 && ldb % VE == 0 &&
                    sa % VE == 0 && sb % VE == 0;
-  // The DMA addresses each operand (one batch entry) through a 2 GiB buffer window.
-  const int64_t a_span = (ta ? K * lda : M * lda) * (int64_t)elem;
-  const int64_t b_span = (tb ? N * ldb : K * ldb) * (int64_t)elem;
+  // The DMA addresses each operand through a 2 GiB buffer window that starts at the
+  // block's origin: a k-contiguous operand (A, or B given as [N, K]) spans at most 256
+  // of its rows plus K elements from there, an m/n-contiguous one all K of its rows.
+  const int64_t a_span = (ta ? K * lda : 256 * lda + K) * (int64_t)elem;
+  const int64_t b_span = (tb ? 256 * ldb + K : K * ldb) * (int64_t)elem;
   return elem == 2 && vec && M >= 64 && N >= 64 && K >= 64 && M % 8 == 0 && N % 8 == 0 &&
          K % V3_BK == 0 && a_span < (int64_t{1} << 31) && b_span < (int64_t{1} << 31);
 }

@@ -193,3 +193,31 @@ def test_axpby_paths_round_alike(cuda, dx_, dy_, beta):
     k = n - 16
     part = L().axpbyz(x[k:].clone(), y[k:].clone(), 1.3, beta)
     assert torch.equal(part, want[k:])
+
+
+@pytest.mark.parametrize("trans_b", [False, True])
+def test_gemm_row_major_operand_past_2gib(cuda, free_after, trans_b):
+    """An fp16 A of 1,050,000 x 1024 (2.15 GB, past the 2 GiB a buffer window covers)
+    still runs on the DMA-staged kernel: each block's window starts at its own rows.
+    Row windows at the start, across byte 2^31 and at the end against float64, and bit
+    for bit against the same rows computed as a small call."""
+    import time
+    M, K, N = 1_050_000, 1024, 256
+    gen = torch.Generator(device="cuda").manual_seed(23)
+    a = torch.randn(M, K, dtype=torch.float16, device="cuda", generator=gen)
+    b = torch.randn((N, K) if trans_b else (K, N), dtype=torch.float16, device="cuda",
+                    generator=gen) * 0.05
+    c = L().matmul2d(a, b, trans_b=trans_b)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    L().matmul2d(a, b, out=c, trans_b=trans_b)
+    torch.cuda.synchronize()
+    print(f"[{M}x{N}x{K}] {2 * M * N * K / (time.perf_counter() - t0) / 1e12:.0f} TFLOP/s",
+          flush=True)
+    bd = b.double().t() if trans_b else b.double()
+    w = 256
+    for r in [0, (1 << 20) - w // 2, M - w]:  # row 2^20 starts at byte 2^31
+        assert_close(c[r:r + w], (a[r:r + w].double() @ bd).cpu().numpy(), RTOL_F16,
+                     f"rows {r}")
+        small = L().matmul2d(a[r:r + w].clone(), b, trans_b=trans_b)
+        assert torch.equal(small, c[r:r + w]), f"rows {r} differ from a small call"
