@@ -221,3 +221,32 @@ def test_gemm_row_major_operand_past_2gib(cuda, free_after, trans_b):
                      f"rows {r}")
         small = L().matmul2d(a[r:r + w].clone(), b, trans_b=trans_b)
         assert torch.equal(small, c[r:r + w]), f"rows {r} differ from a small call"
+
+
+def test_flash_attention_past_2e31(cuda, free_after):
+    """B*H*S*D = 2^31 + 3*2048 (fp16, 2^21 + 3 heads of 16 x 64; ~34 GB for Q, K, V, O,
+    dO, dQ, dK, dV): batches at the start, across element 2^31 and at the end against
+    the float64 oracle and bit for bit against the same batches as a small call, causal
+    and not."""
+    B, H, S, D = (1 << 20) + 3, 2, 16, 64
+    gen = torch.Generator(device="cuda").manual_seed(24)
+    q, k, v, do = (torch.randn(B, H, S, D, dtype=torch.float16, device="cuda",
+                               generator=gen) for _ in range(4))
+    dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+    for causal in (False, True):
+        o, lse = L().flash_attn_fwd(q, k, v, D ** -0.5, causal)
+        L().flash_attn_bwd(q, k, v, o, do, lse, dq, dk, dv, D ** -0.5, causal, False)
+        for b in [0, 1 << 20, B - 1]:  # batch 2^20 starts at element 2^31
+            sl = slice(b, b + 1)
+            qs, ks, vs, ds = (t[sl].clone() for t in (q, k, v, do))
+            os_, ls = L().flash_attn_fwd(qs, ks, vs, D ** -0.5, causal)
+            assert torch.equal(os_, o[sl]) and torch.equal(ls, lse[sl]), f"fwd batch {b}"
+            g = [torch.empty_like(qs) for _ in range(3)]
+            L().flash_attn_bwd(qs, ks, vs, os_, ds, ls, *g, D ** -0.5, causal, False)
+            for got, big, n in zip(g, (dq, dk, dv), ("dq", "dk", "dv")):
+                assert torch.equal(got, big[sl]), f"{n} batch {b} causal={causal}"
+            oo, _ = O.flash_attention_fwd(f64(qs), f64(ks), f64(vs), causal)
+            assert_close(o[sl], oo, RTOL_F16, f"O batch {b}")
+            rq, rk, rv = O.flash_attention_bwd(f64(qs), f64(ks), f64(vs), f64(ds), causal)
+            for got, want, n in ((dq, rq, "dq"), (dk, rk, "dk"), (dv, rv, "dv")):
+                assert_close(got[sl], want, RTOL_F16, f"{n} batch {b} causal={causal}")
