@@ -19,6 +19,9 @@
  *  - `accumulate` != 0 means out += result (the reference's `grad += local`
  *    closures); 0 means out = result (out is not read).
  *  - Tensors are contiguous row-major unless leading dimensions are passed.
+ *  - Element counts and offsets are 64-bit throughout; an elementwise call whose
+ *    launch would exceed the 2^32 work-items of one dispatch (n >= 2^35 fp16 elements
+ *    for the activations and tg_unary_bwd) returns -1 instead of launching.
  *
  * Each entry cites the reference code it replaces (paths are relative to the
  * reference repository root).
