@@ -20,8 +20,9 @@
  *    closures); 0 means out = result (out is not read).
  *  - Tensors are contiguous row-major unless leading dimensions are passed.
  *  - Element counts and offsets are 64-bit throughout; an elementwise call whose
- *    launch would exceed the 2^32 work-items of one dispatch (n >= 2^35 fp16 elements
- *    for the activations and tg_unary_bwd) returns -1 instead of launching.
+ *    launch would exceed the 2^32 work-items of one dispatch (the activations and
+ *    tg_unary_bwd: more than 2^32 16-byte vectors, i.e. 2^35 fp16 or 2^34 fp32
+ *    elements) returns -1 instead of launching.
  *
  * Each entry cites the reference code it replaces (paths are relative to the
  * reference repository root).
