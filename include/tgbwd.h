@@ -164,7 +164,10 @@ int tg_sum_partials2_group(int n, const float* const* parts, const int64_t* K,
  * the process ends; tg_layernorm_bwd_noalloc_max_scratch() bytes).  No counterpart in
  * the reference: it is for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops).  Shapes whose partials exceed the scratch
- * return -1 with a message.  Calls that overlap on one GPU share the scratch and race. */
+ * return -1 with a message.  Calls that overlap on one GPU share the scratch and race:
+ * calls on one stream are ordered by it; callers using several streams order their
+ * calls themselves (an event, as under graph capture, where a library-side wait on
+ * another stream's event is not allowed). */
 size_t tg_layernorm_bwd_noalloc_max_scratch(void);
 int tg_layernorm_bwd_noalloc(int dtype, const void* x, const float* mean, const float* rstd,
                              const float* gamma, const void* dy, void* dx, float* dgamma,
